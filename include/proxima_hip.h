@@ -1,0 +1,128 @@
+/*
+ * libproxima_hip: the MI355X (gfx950) data-parallel nearest-neighbour hot
+ * path of Liona-orph/proxima behind a plain C ABI.
+ *
+ * The reference's drop-in boundary is the `VectorIndex` trait
+ * (crates/proxima-index/src/index.rs:154-205): insert / remove / search /
+ * contains / len / stats. Each index type below exports exactly that surface
+ * as `pxg_<index>_*` functions on an opaque handle, plus a batched search
+ * that the single-query trait method is a batch of one of, and a
+ * device-pointer search for callers whose queries are already in HBM.
+ *
+ * Conventions
+ *   - Every function returns a pxg_status (0 = ok). The message and the
+ *     structured fields of the last error on the calling thread are available
+ *     from pxg_last_error_message() / pxg_last_error_detail(). No C++
+ *     exception crosses this boundary.
+ *   - Host pointers unless the name ends in _device. Output buffers are
+ *     caller-allocated: ids[nq*k], dist[nq*k], count[nq].
+ *   - Vectors are validated (length implicit in dim; every component finite)
+ *     and, for the cosine metric, normalised with the reference's
+ *     normalize_in_place (distance.rs:508-517) before they reach the device.
+ *   - Results are ranking scores (index.rs:136-149): squared L2, 1 - dot for
+ *     prepared cosine, -dot for inner product; nearest first, ties broken by
+ *     id, at most k per query; `count` says how many.
+ *   - search on one handle is re-entrant from many host threads; insert,
+ *     remove, train and load are exclusive (the trait takes &mut self).
+ */
+#ifndef PROXIMA_HIP_H
+#define PROXIMA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes: one per ProximaError variant (crates/proxima-core/src/error.rs:37-160). */
+typedef enum pxg_status {
+  PXG_OK = 0,
+  PXG_ERR_DIMENSION_MISMATCH = 1, /* detail a = expected, b = actual */
+  PXG_ERR_UNKNOWN_ID = 2,         /* detail a = id */
+  PXG_ERR_DUPLICATE_ID = 3,       /* detail a = id */
+  PXG_ERR_CAPACITY = 4,           /* detail a = limit */
+  PXG_ERR_NON_FINITE = 5,         /* detail a = component index, b = vector index in the batch, value */
+  PXG_ERR_CORRUPTION = 6,
+  PXG_ERR_CONFIGURATION = 7,      /* detail a = offending value */
+  PXG_ERR_INTERNAL = 8            /* device or runtime failure */
+} pxg_status;
+
+/* Metric: crates/proxima-core/src/distance.rs:90-118 (declaration order). */
+typedef enum pxg_metric {
+  PXG_EUCLIDEAN = 0,
+  PXG_COSINE = 1,
+  PXG_INNER_PRODUCT = 2,
+  PXG_MANHATTAN = 3
+} pxg_metric;
+
+/* IndexStats: crates/proxima-index/src/index.rs:68-130 (nodes_per_layer is
+ * [len] for every index here, so it is not a separate field). */
+typedef struct pxg_index_stats {
+  uint64_t len;
+  uint64_t deleted;
+  uint32_t dim;
+  int32_t metric;
+  uint64_t layers;
+  uint64_t edges;
+  uint64_t vector_bytes; /* device bytes of the full-precision store */
+  uint64_t graph_bytes;  /* device bytes of codes, lists, codebooks */
+} pxg_index_stats;
+
+/* Thread-local description of the last error on this thread ("" if none). */
+const char* pxg_last_error_message(void);
+/* Structured fields of the last error; returns its status. Any pointer may be NULL. */
+int pxg_last_error_detail(uint64_t* a, uint64_t* b, float* value);
+/* Library version string. */
+const char* pxg_version(void);
+/* Number of visible devices (0 when none); never fails. */
+int pxg_device_count(void);
+
+/* ------------------------------------------------------------------------ */
+/* Flat (exact) index: replaces FlatIndex, crates/proxima-index/src/flat.rs:68-236. */
+typedef struct pxg_flat pxg_flat;
+
+/* FlatIndex::new / with_capacity (flat.rs:72-84) over VectorSpace::new (space.rs:71-92). */
+int pxg_flat_create(uint32_t dim, int metric, uint64_t capacity, pxg_flat** out);
+void pxg_flat_destroy(pxg_flat* index);
+/* VectorIndex::insert (flat.rs:139-143) for a batch of n vectors, all-or-nothing:
+ * nothing is inserted if any vector is non-finite or any id is a duplicate
+ * (of a live id or of another id in the batch). out_slots may be NULL. */
+int pxg_flat_insert(pxg_flat* index, const uint64_t* ids, const float* vectors, uint64_t n, uint32_t* out_slots);
+/* VectorIndex::remove (flat.rs:145-151): frees the slot for LIFO reuse. */
+int pxg_flat_remove(pxg_flat* index, uint64_t id);
+/* VectorIndex::contains / len / stats (flat.rs:171-193). */
+int pxg_flat_contains(const pxg_flat* index, uint64_t id);
+uint64_t pxg_flat_len(const pxg_flat* index);
+int pxg_flat_stats(const pxg_flat* index, pxg_index_stats* out);
+/* FlatIndex::vector (flat.rs:104-106): the stored, prepared vector. */
+int pxg_flat_get_vector(const pxg_flat* index, uint64_t id, float* out);
+/* Slot table for building per-slot accept masks: slot_count() slots; ids[s]
+ * and live[s] (0 for a free slot). Either pointer may be NULL. */
+uint64_t pxg_flat_slot_count(const pxg_flat* index);
+int pxg_flat_slots(const pxg_flat* index, uint64_t* ids, uint8_t* live);
+/* VectorIndex::search (flat.rs:153-169) over nq queries (row-major nq x dim).
+ * accept: NULL (AcceptAll) or one byte per slot (nonzero = the filter accepts
+ * that slot), evaluated by the caller exactly as Filter::accepts would be. */
+int pxg_flat_search(const pxg_flat* index, const float* queries, uint64_t nq, uint64_t k, const uint8_t* accept,
+                    uint64_t* out_ids, float* out_dist, uint32_t* out_count);
+/* Same, with every pointer in device memory and work ordered on `stream`
+ * (a hipStream_t; NULL = the library's own). Queries are validated and
+ * prepared on the device; a non-finite query fails the call. Returns after
+ * the results are complete. */
+int pxg_flat_search_device(const pxg_flat* index, const float* d_queries, uint64_t nq, uint64_t k,
+                           const uint8_t* d_accept, uint64_t* d_out_ids, float* d_out_dist, uint32_t* d_out_count,
+                           void* stream);
+/* Search statistics of the last search on this thread: queries whose MFMA
+ * candidate set could not be proven to contain the exact top-k and were
+ * rescanned exactly. */
+uint64_t pxg_flat_last_fallbacks(void);
+/* Search path selection (no reference counterpart; for tests and tuning):
+ * 0 = automatic, 1 = MFMA candidates + exact rescoring whenever the metric
+ * and k allow it, 2 = exact VALU scan only. Results are identical. */
+int pxg_flat_set_search_mode(pxg_flat* index, int mode);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PROXIMA_HIP_H */

@@ -1,0 +1,385 @@
+"""proxima_amd: the MI355X hot path of Liona-orph/proxima.
+
+A host-side mirror of the reference's index API (crates/proxima-index:
+`VectorIndex`, `FlatIndex`, `IvfPqIndex`, `recall_at_k`; crates/proxima-core:
+`Metric`, `VectorSpace`, `SearchResult`, `ProximaError`) over the C ABI of
+libproxima_hip.so. Every search, train and encode runs in the HIP library on
+the GPU; this module only marshals arguments, evaluates filters into per-slot
+accept masks, and keeps metadata (which never reaches the device).
+"""
+import ctypes as C
+from collections import namedtuple
+
+import numpy as np
+
+from ._capi import IndexStats as _IndexStatsC
+from ._capi import lib as _lib
+
+__all__ = [
+    "Metric", "VectorSpace", "SearchResult", "IndexStats", "ProximaError", "DimensionMismatch", "UnknownId",
+    "DuplicateId", "Capacity", "NonFinite", "Corruption", "Configuration", "Internal", "FlatIndex", "check_k",
+]
+
+
+# --- Metric: distance.rs:90-118 ----------------------------------------------------
+class Metric:
+    EUCLIDEAN = 0
+    COSINE = 1
+    INNER_PRODUCT = 2
+    MANHATTAN = 3
+    ALL = (0, 1, 2, 3)
+    _NAMES = {0: "euclidean", 1: "cosine", 2: "inner_product", 3: "manhattan"}
+
+    @staticmethod
+    def name(m):
+        return Metric._NAMES[m]
+
+    @staticmethod
+    def from_name(name):  # distance.rs:193-201
+        for k, v in Metric._NAMES.items():
+            if v == name:
+                return k
+        return None
+
+    @staticmethod
+    def to_true_distance(m, score):  # distance.rs:167-173
+        if m == Metric.EUCLIDEAN:
+            return float(np.sqrt(np.float32(score)))
+        if m == Metric.INNER_PRODUCT:
+            return -score
+        return score
+
+
+# --- ProximaError: error.rs:37-160 --------------------------------------------------
+class ProximaError(Exception):
+    status = None
+
+    def __init__(self, message, a=0, b=0, value=0.0):
+        super().__init__(message)
+        self.a, self.b, self.value = a, b, value
+
+
+class DimensionMismatch(ProximaError):
+    status = 1
+
+    @property
+    def expected(self):
+        return self.a
+
+    @property
+    def actual(self):
+        return self.b
+
+
+class UnknownId(ProximaError):
+    status = 2
+
+    @property
+    def id(self):
+        return self.a
+
+
+class DuplicateId(ProximaError):
+    status = 3
+
+    @property
+    def id(self):
+        return self.a
+
+
+class Capacity(ProximaError):
+    status = 4
+
+
+class NonFinite(ProximaError):
+    status = 5
+
+    @property
+    def index(self):
+        return self.a
+
+
+class Corruption(ProximaError):
+    status = 6
+
+
+class Configuration(ProximaError):
+    status = 7
+
+    def __init__(self, message, a=0, b=0, value=0.0, parameter=None):
+        super().__init__(message, a, b, value)
+        self.parameter = parameter
+
+
+class Internal(ProximaError):
+    status = 8
+
+
+_BY_STATUS = {c.status: c for c in (DimensionMismatch, UnknownId, DuplicateId, Capacity, NonFinite, Corruption,
+                                    Configuration, Internal)}
+
+
+def _check(status):
+    if status == 0:
+        return
+    a, b, v = C.c_uint64(), C.c_uint64(), C.c_float()
+    _lib.pxg_last_error_detail(C.byref(a), C.byref(b), C.byref(v))
+    msg = _lib.pxg_last_error_message().decode()
+    cls = _BY_STATUS.get(status, Internal)
+    err = cls(msg, a.value, b.value, v.value)
+    if cls is Configuration:
+        err.parameter = msg.split("invalid configuration: ")[-1].split(" =")[0] if "=" in msg else None
+    raise err
+
+
+def _config(parameter, value, reason):
+    e = Configuration(f"invalid configuration: {parameter} = {value} ({reason})", value if isinstance(value, int)
+                      else 0, parameter=parameter)
+    return e
+
+
+def check_k(k):  # index.rs:212-224
+    if k > (1 << 24):
+        raise _config("k", k, "exceeds the 16777216 result ceiling")
+
+
+# --- VectorSpace: space.rs:53-162 ----------------------------------------------------
+class VectorSpace:
+    MAX_DIM = 1 << 20
+
+    def __init__(self, dim, metric):
+        if dim < 1:
+            raise _config("dim", dim, "must be at least 1; a 0-dimensional space makes all distances equal")
+        if dim > self.MAX_DIM:
+            raise _config("dim", dim, "exceeds the 1048576 dimension ceiling")
+        if metric not in Metric.ALL:
+            raise _config("metric", metric, "unknown metric")
+        self.dim = dim
+        self.metric = metric
+
+    def validate(self, vector):  # space.rs:104-121
+        v = np.asarray(vector, dtype=np.float32).reshape(-1)
+        if v.size != self.dim:
+            raise DimensionMismatch(
+                f"dimension mismatch: index holds {self.dim}-dimensional vectors, got {v.size}", self.dim, v.size)
+        bad = np.flatnonzero(~np.isfinite(v))
+        if bad.size:
+            i = int(bad[0])
+            raise NonFinite(f"vector component {i} is not finite ({v[i]})", i, 0, float(v[i]))
+        return v
+
+    def __str__(self):
+        return f"{self.dim}d/{Metric.name(self.metric)}"
+
+    def __eq__(self, other):
+        return isinstance(other, VectorSpace) and (self.dim, self.metric) == (other.dim, other.metric)
+
+
+SearchResult = namedtuple("SearchResult", ["id", "distance"])  # topk.rs:33-40
+
+
+class IndexStats(namedtuple("IndexStats", ["len", "deleted", "dim", "metric", "layers", "nodes_per_layer", "edges",
+                                           "vector_bytes", "graph_bytes"])):
+    """index.rs:68-130."""
+
+    def mean_degree(self):
+        return 0.0 if self.len + self.deleted == 0 else self.edges / (self.len + self.deleted)
+
+    def total_bytes(self):
+        return self.vector_bytes + self.graph_bytes
+
+    def bytes_per_vector(self):
+        return 0.0 if self.len == 0 else self.total_bytes() / self.len
+
+
+def _stats_from_c(s):
+    return IndexStats(s.len, s.deleted, s.dim, s.metric, s.layers, [s.len], s.edges, s.vector_bytes, s.graph_bytes)
+
+
+def _ptr(a):
+    return None if a is None else C.c_void_p(a.ctypes.data)
+
+
+def _rows(vectors, dim):
+    v = np.ascontiguousarray(vectors, dtype=np.float32)
+    if v.ndim == 1:
+        if v.size % dim != 0 or (v.size != dim and v.size == 0):
+            raise DimensionMismatch(
+                f"dimension mismatch: index holds {dim}-dimensional vectors, got {v.size}", dim, v.size)
+        v = v.reshape(-1, dim)
+    if v.shape[-1] != dim:
+        raise DimensionMismatch(
+            f"dimension mismatch: index holds {dim}-dimensional vectors, got {v.shape[-1]}", dim, v.shape[-1])
+    return np.ascontiguousarray(v.reshape(-1, dim))
+
+
+def _device_ptr(t):
+    """Device address of a torch CUDA/HIP tensor (must be contiguous)."""
+    if not t.is_contiguous():
+        raise ValueError("device tensors must be contiguous")
+    return C.c_void_p(t.data_ptr())
+
+
+# --- the VectorIndex trait surface shared by every index ------------------------------
+class _IndexBase:
+    """VectorIndex (index.rs:154-205): insert / remove / search / contains / len /
+    stats, the provided upsert and search_all, plus search_batch."""
+
+    def upsert(self, id, vector, metadata=None):  # index.rs:194-199
+        if self.contains(id):
+            self.remove(id)
+        self.insert(id, vector, metadata)
+
+    def search_all(self, query, k):  # index.rs:202-204
+        return self.search(query, k, None)
+
+    def is_empty(self):
+        return len(self) == 0
+
+    def search(self, query, k, filter=None):
+        ids, dists, counts = self.search_batch(np.asarray(query, dtype=np.float32).reshape(1, -1), k, filter)
+        return [SearchResult(int(ids[0, i]), float(dists[0, i])) for i in range(int(counts[0]))]
+
+    # metadata stays on the host; filters see it
+    def metadata(self, id):
+        if not self.contains(id):
+            return None
+        return self._meta.get(id, {})
+
+    def set_metadata(self, id, metadata):
+        if not self.contains(id):
+            raise UnknownId(f"unknown vector id {id}", id)
+        self._meta[id] = dict(metadata or {})
+
+    def _accept_mask(self, filter, slot_ids, live):
+        """Evaluate Filter::accepts over live slots (index.rs:27-35) into one byte per slot."""
+        if filter is None:
+            return None
+        acc = np.zeros(slot_ids.size, np.uint8)
+        for s in np.flatnonzero(live):
+            i = int(slot_ids[s])
+            acc[s] = 1 if filter(i, self._meta.get(i, {})) else 0
+        return acc
+
+
+# --- FlatIndex: flat.rs:68-236 ------------------------------------------------------------
+class FlatIndex(_IndexBase):
+    """Exact search over a device-resident slot-major store (GPU FlatIndex)."""
+
+    def __init__(self, space, capacity=0):
+        self.space = space
+        h = C.c_void_p()
+        _check(_lib.pxg_flat_create(space.dim, space.metric, capacity, C.byref(h)))
+        self._h = h
+        self._meta = {}
+
+    @classmethod
+    def with_capacity(cls, space, capacity):
+        return cls(space, capacity)
+
+    @classmethod
+    def from_array(cls, space, data):  # TryFrom<(&VectorSpace, &[f32])>, flat.rs:215-236
+        data = np.asarray(data, dtype=np.float32).reshape(-1)
+        if data.size % space.dim != 0:
+            raise _config("data", data.size, "must be a multiple of the space dimension")
+        n = data.size // space.dim
+        idx = cls(space, n)
+        if n:
+            idx.insert_batch(np.arange(n, dtype=np.uint64), data.reshape(n, space.dim))
+        return idx
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            _lib.pxg_flat_destroy(h)
+            self._h = None
+
+    # -- mutation (exclusive) --
+    def insert(self, id, vector, metadata=None):
+        v = np.asarray(vector, dtype=np.float32).reshape(-1)
+        if v.size != self.space.dim:
+            raise DimensionMismatch(
+                f"dimension mismatch: index holds {self.space.dim}-dimensional vectors, got {v.size}",
+                self.space.dim, v.size)
+        self.insert_batch(np.array([id], np.uint64), v.reshape(1, -1))
+        if metadata:
+            self._meta[int(id)] = dict(metadata)
+
+    def insert_batch(self, ids, vectors):
+        ids = np.ascontiguousarray(ids, dtype=np.uint64).reshape(-1)
+        v = _rows(vectors, self.space.dim)
+        if v.shape[0] != ids.size:
+            raise ValueError("ids and vectors disagree on the batch size")
+        slots = np.zeros(ids.size, np.uint32)
+        _check(_lib.pxg_flat_insert(self._h, _ptr(ids), _ptr(v), ids.size, _ptr(slots)))
+        return slots
+
+    def remove(self, id):
+        _check(_lib.pxg_flat_remove(self._h, int(id)))
+        self._meta.pop(int(id), None)
+
+    # -- queries --
+    def contains(self, id):
+        return bool(_lib.pxg_flat_contains(self._h, int(id)))
+
+    def __len__(self):
+        return int(_lib.pxg_flat_len(self._h))
+
+    def stats(self):
+        s = _IndexStatsC()
+        _check(_lib.pxg_flat_stats(self._h, C.byref(s)))
+        return _stats_from_c(s)
+
+    def vector(self, id):
+        out = np.zeros(self.space.dim, np.float32)
+        try:
+            _check(_lib.pxg_flat_get_vector(self._h, int(id), _ptr(out)))
+        except UnknownId:
+            return None
+        return out
+
+    def slots(self):
+        n = int(_lib.pxg_flat_slot_count(self._h))
+        ids = np.zeros(max(n, 1), np.uint64)
+        live = np.zeros(max(n, 1), np.uint8)
+        _check(_lib.pxg_flat_slots(self._h, _ptr(ids), _ptr(live)))
+        return ids[:n], live[:n]
+
+    def ids(self):
+        """Live ids in slot order (flat.rs:118-120)."""
+        ids, live = self.slots()
+        return [int(i) for i in ids[live.astype(bool)]]
+
+    def set_search_mode(self, mode):
+        _check(_lib.pxg_flat_set_search_mode(self._h, mode))
+
+    def search_batch(self, queries, k, filter=None):
+        """Batched VectorIndex::search: returns (ids[nq,k], dists[nq,k], counts[nq])."""
+        check_k(k)
+        q = _rows(queries, self.space.dim)
+        nq = q.shape[0]
+        acc = None
+        if filter is not None:
+            sid, live = self.slots()
+            acc = self._accept_mask(filter, sid, live)
+        kk = max(k, 1)
+        oi = np.zeros((nq, kk), np.uint64)
+        od = np.zeros((nq, kk), np.float32)
+        oc = np.zeros(max(nq, 1), np.uint32)
+        _check(_lib.pxg_flat_search(self._h, _ptr(q), nq, k, _ptr(acc), _ptr(oi), _ptr(od), _ptr(oc)))
+        return oi[:, :k] if k else oi[:, :0], od[:, :k] if k else od[:, :0], oc[:nq]
+
+    def search_device(self, queries, k, out_ids, out_dist, out_count, accept=None, stream=None):
+        """Device-pointer search: torch tensors on the GPU (queries f32 [nq, dim],
+        out_ids int64 [nq, k], out_dist f32 [nq, k], out_count int32 [nq])."""
+        _check(_lib.pxg_flat_search_device(
+            self._h, _device_ptr(queries), queries.shape[0], k, None if accept is None else _device_ptr(accept),
+            _device_ptr(out_ids), _device_ptr(out_dist), _device_ptr(out_count),
+            None if stream is None else C.c_void_p(stream)))
+
+    @staticmethod
+    def last_fallbacks():
+        return int(_lib.pxg_flat_last_fallbacks())
+
+    def exact_ids(self, query, k, filter=None):  # flat.rs:201-212
+        return [r.id for r in self.search(query, k, filter)]

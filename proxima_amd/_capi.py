@@ -1,0 +1,96 @@
+"""ctypes binding of libproxima_hip.so (the C ABI in include/proxima_hip.h).
+
+The shared library is the product: there is no fallback. If it is missing or
+fails to load, importing proxima_amd raises.
+"""
+import ctypes as C
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libproxima_hip.so")
+
+_vp = C.c_void_p
+_u64 = C.c_uint64
+_u32 = C.c_uint32
+_i32 = C.c_int
+_f32 = C.c_float
+_f64 = C.c_double
+_P = C.POINTER
+
+
+class IndexStats(C.Structure):
+    _fields_ = [
+        ("len", _u64),
+        ("deleted", _u64),
+        ("dim", _u32),
+        ("metric", C.c_int32),
+        ("layers", _u64),
+        ("edges", _u64),
+        ("vector_bytes", _u64),
+        ("graph_bytes", _u64),
+    ]
+
+
+class IvfPqConfigC(C.Structure):
+    _fields_ = [
+        ("nlist", _u64),
+        ("subspaces", _u64),
+        ("nprobe", _u64),
+        ("rerank", _u64),
+        ("seed", _u64),
+        ("max_iterations", _u64),
+        ("training_sample", _u64),
+        ("train_threshold", _u64),
+        ("retain_vectors", _i32),
+    ]
+
+
+class TrainingReportC(C.Structure):
+    _fields_ = [
+        ("sampled", _u64),
+        ("coarse_inertia", _f64),
+        ("coarse_iterations", _u64),
+        ("residual_inertia", _f64),
+        ("populated_lists", _u64),
+        ("largest_list", _u64),
+    ]
+
+
+# name -> (restype, argtypes); every entry must exist in the library.
+SIGNATURES = {
+    "pxg_last_error_message": (C.c_char_p, []),
+    "pxg_last_error_detail": (_i32, [_P(_u64), _P(_u64), _P(_f32)]),
+    "pxg_version": (C.c_char_p, []),
+    "pxg_device_count": (_i32, []),
+    # flat
+    "pxg_flat_create": (_i32, [_u32, _i32, _u64, _P(_vp)]),
+    "pxg_flat_destroy": (None, [_vp]),
+    "pxg_flat_insert": (_i32, [_vp, _vp, _vp, _u64, _vp]),
+    "pxg_flat_remove": (_i32, [_vp, _u64]),
+    "pxg_flat_contains": (_i32, [_vp, _u64]),
+    "pxg_flat_len": (_u64, [_vp]),
+    "pxg_flat_stats": (_i32, [_vp, _P(IndexStats)]),
+    "pxg_flat_get_vector": (_i32, [_vp, _u64, _vp]),
+    "pxg_flat_slot_count": (_u64, [_vp]),
+    "pxg_flat_slots": (_i32, [_vp, _vp, _vp]),
+    "pxg_flat_search": (_i32, [_vp, _vp, _u64, _u64, _vp, _vp, _vp, _vp]),
+    "pxg_flat_search_device": (_i32, [_vp, _vp, _u64, _u64, _vp, _vp, _vp, _vp, _vp]),
+    "pxg_flat_last_fallbacks": (_u64, []),
+    "pxg_flat_set_search_mode": (_i32, [_vp, _i32]),
+}
+
+
+def load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it with `python -m proxima_amd.build` "
+            "(hipcc, gfx950). There is no CPU fallback.")
+    lib = C.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = load()

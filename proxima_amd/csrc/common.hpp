@@ -1,0 +1,201 @@
+// Host-side plumbing shared by every index in libproxima_hip: status codes,
+// the thread-local last-error record, HIP error checks and RAII device
+// buffers. No C++ exception crosses the C ABI: every entry point runs its
+// body through pxg::guard(), which maps exceptions to status codes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/proxima_hip.h"
+
+namespace pxg {
+
+// The error the C ABI reports, with the fields ProximaError carries
+// (error.rs:37-160) so the caller can rebuild the variant exactly.
+struct Error {
+  int status;
+  std::string message;
+  uint64_t a = 0, b = 0;  // expected/actual, index, id or limit, per variant
+  float value = 0.0f;
+};
+
+struct Raise {
+  Error e;
+};
+
+void set_last_error(const Error& e);
+void clear_last_error();
+
+[[noreturn]] inline void raise(int status, std::string msg, uint64_t a = 0, uint64_t b = 0, float v = 0.0f) {
+  throw Raise{Error{status, std::move(msg), a, b, v}};
+}
+[[noreturn]] inline void config_error(const char* parameter, uint64_t value, const char* reason) {
+  raise(PXG_ERR_CONFIGURATION,
+        std::string("invalid configuration: ") + parameter + " = " + std::to_string(value) + " (" + reason + ")", value);
+}
+[[noreturn]] inline void internal_error(const char* location, const std::string& detail) {
+  raise(PXG_ERR_INTERNAL, std::string("internal invariant violated in ") + location + ": " + detail);
+}
+
+#define PXG_HIP(call)                                                                         \
+  do {                                                                                        \
+    hipError_t e_ = (call);                                                                   \
+    if (e_ != hipSuccess) {                                                                   \
+      if (e_ == hipErrorOutOfMemory || e_ == hipErrorMemoryAllocation)                        \
+        ::pxg::raise(PXG_ERR_CAPACITY, std::string("capacity exceeded: device memory limit (") + \
+                                           hipGetErrorString(e_) + ")");                       \
+      ::pxg::internal_error(#call, hipGetErrorString(e_));                                    \
+    }                                                                                         \
+  } while (0)
+
+template <class F>
+int guard(F&& f) {
+  try {
+    f();
+    clear_last_error();
+    return PXG_OK;
+  } catch (const Raise& r) {
+    set_last_error(r.e);
+    return r.e.status;
+  } catch (const std::bad_alloc&) {
+    set_last_error(Error{PXG_ERR_CAPACITY, "capacity exceeded: host memory"});
+    return PXG_ERR_CAPACITY;
+  } catch (const std::exception& ex) {
+    set_last_error(Error{PXG_ERR_INTERNAL, std::string("internal invariant violated: ") + ex.what()});
+    return PXG_ERR_INTERNAL;
+  } catch (...) {
+    set_last_error(Error{PXG_ERR_INTERNAL, "internal invariant violated: unknown exception"});
+    return PXG_ERR_INTERNAL;
+  }
+}
+
+// Owning device allocation.
+template <class T>
+struct DevBuf {
+  T* p = nullptr;
+  size_t n = 0;
+  DevBuf() = default;
+  explicit DevBuf(size_t count) { alloc(count); }
+  DevBuf(const DevBuf&) = delete;
+  DevBuf& operator=(const DevBuf&) = delete;
+  DevBuf(DevBuf&& o) noexcept : p(o.p), n(o.n) { o.p = nullptr; o.n = 0; }
+  DevBuf& operator=(DevBuf&& o) noexcept {
+    if (this != &o) { release(); p = o.p; n = o.n; o.p = nullptr; o.n = 0; }
+    return *this;
+  }
+  ~DevBuf() { release(); }
+  void alloc(size_t count) {
+    release();
+    if (count) PXG_HIP(hipMalloc(&p, count * sizeof(T)));
+    n = count;
+  }
+  // Grow to at least `count`, keeping the first `keep` elements.
+  void grow(size_t count, size_t keep, hipStream_t s) {
+    if (count <= n) return;
+    T* q = nullptr;
+    PXG_HIP(hipMalloc(&q, count * sizeof(T)));
+    if (keep && p) PXG_HIP(hipMemcpyAsync(q, p, keep * sizeof(T), hipMemcpyDeviceToDevice, s));
+    PXG_HIP(hipStreamSynchronize(s));
+    release();
+    p = q;
+    n = count;
+  }
+  // Ensure capacity without preserving contents.
+  void reserve(size_t count) {
+    if (count > n) alloc(count);
+  }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    n = 0;
+  }
+  size_t bytes() const { return n * sizeof(T); }
+};
+
+// LIFO slot allocator: id.rs:137-229 (most recently released slot first).
+struct SlotAllocator {
+  uint32_t next = 0;
+  std::vector<uint32_t> free;
+  uint32_t allocate() {
+    if (!free.empty()) {
+      uint32_t s = free.back();
+      free.pop_back();
+      return s;
+    }
+    if (next == UINT32_MAX)
+      raise(PXG_ERR_CAPACITY, "capacity exceeded: slot allocator limit is 4294967295", UINT32_MAX);
+    return next++;
+  }
+  void release(uint32_t s) { free.push_back(s); }
+  size_t high_water() const { return next; }
+  void clear() { next = 0; free.clear(); }
+};
+
+// Per-call execution context: a stream plus scratch memory. Searches on one
+// handle may run concurrently from many host threads; each takes its own
+// context from the pool, so no two calls share a stream or scratch.
+struct Ctx {
+  hipStream_t stream = nullptr;
+  std::unordered_map<int, DevBuf<unsigned char>> scratch;  // keyed by purpose
+  std::vector<unsigned char> host;                         // pinned-free host staging
+  unsigned char* get(int key, size_t bytes) {
+    auto& b = scratch[key];
+    if (b.n < bytes) b.alloc(bytes + bytes / 8 + 256);
+    return b.p;
+  }
+  ~Ctx() {
+    scratch.clear();
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+};
+
+struct CtxPool {
+  std::mutex mu;
+  std::vector<Ctx*> idle;
+  std::vector<Ctx*> all;
+  Ctx* acquire() {
+    std::lock_guard<std::mutex> lk(mu);
+    if (!idle.empty()) {
+      Ctx* c = idle.back();
+      idle.pop_back();
+      return c;
+    }
+    Ctx* c = new Ctx();
+    PXG_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+    all.push_back(c);
+    return c;
+  }
+  void release(Ctx* c) {
+    std::lock_guard<std::mutex> lk(mu);
+    idle.push_back(c);
+  }
+  ~CtxPool() {
+    for (Ctx* c : all) delete c;
+  }
+};
+
+struct CtxLease {
+  CtxPool& pool;
+  Ctx* c;
+  explicit CtxLease(CtxPool& p) : pool(p), c(p.acquire()) {}
+  ~CtxLease() { pool.release(c); }
+  Ctx* operator->() { return c; }
+};
+
+// VectorSpace::validate / prepare on the host (space.rs:104-138). Returns -1
+// or the index of the first non-finite component. Cosine normalisation is the
+// reference's: n = sqrt(8-lane dot(v, v)); if n > 0 and finite, v *= 1/n.
+long long validate_prepare(int metric, const float* in, uint32_t dim, float* out);
+float host_dot_unrolled(const float* a, const float* b, uint32_t n);
+
+void check_k(uint64_t k);  // index.rs:212-224
+
+}  // namespace pxg

@@ -1,0 +1,198 @@
+// Device helpers shared by the kernels: the total order on f32 scores, the
+// reference's exact 8-lane distance arithmetic, a register bitonic sort across
+// one 64-wide wavefront, and a block radix select over 64-bit keys.
+//
+// Everything that must match the reference bit for bit is built with
+// -ffp-contract=off (no FMA contraction), so `acc += d * d` rounds twice
+// exactly as the Rust source does.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace pxg {
+
+constexpr int WAVE = 64;
+constexpr uint64_t KEY_MAX = ~0ull;
+
+// f32::total_cmp order as an unsigned key (topk.rs:63-67 orders by it).
+__host__ __device__ inline uint32_t ord_key(float f) {
+  uint32_t b = __builtin_bit_cast(uint32_t, f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__host__ __device__ inline float key_float(uint32_t k) {
+  uint32_t b = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
+  return __builtin_bit_cast(float, b);
+}
+
+// 64-bit shuffle across the wave.
+__device__ inline uint64_t shfl_xor64(uint64_t v, int mask) {
+  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+  lo = __shfl_xor(lo, mask, WAVE);
+  hi = __shfl_xor(hi, mask, WAVE);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// ----------------------------------------------------------------------------
+// Exact distances in the reference's arithmetic.
+//
+// squared_euclidean_unrolled / dot_unrolled / manhattan_unrolled
+// (distance.rs:267-372): eight lane accumulators over chunks_exact(8), the
+// pairwise reduce of distance.rs:534-538, then + a sequential tail.
+//
+// dist_group8: eight consecutive threads (group lane g = 0..7) cooperate on
+// one pair; thread g owns accumulator g. Every thread of the group returns
+// the same value.
+// ----------------------------------------------------------------------------
+template <int METRIC>
+__device__ inline float lane_term(float a, float b) {
+  if constexpr (METRIC == 0) {
+    float d = a - b;
+    return d * d;
+  } else if constexpr (METRIC == 3) {
+    return fabsf(a - b);
+  } else {
+    return a * b;
+  }
+}
+
+template <int METRIC>
+__device__ inline float dist_group8(const float* __restrict__ a, const float* __restrict__ b, int dim, int g) {
+  float acc = 0.0f;
+  const int chunks = dim >> 3;
+  for (int c = 0; c < chunks; ++c) acc += lane_term<METRIC>(a[c * 8 + g], b[c * 8 + g]);
+  // ((0+1)+(2+3))+((4+5)+(6+7)): f32 addition is commutative, so the xor
+  // partner order gives the same bits on every lane of the group.
+  acc = acc + __shfl_xor(acc, 1, WAVE);
+  acc = acc + __shfl_xor(acc, 2, WAVE);
+  acc = acc + __shfl_xor(acc, 4, WAVE);
+  float tail = 0.0f;
+  for (int i = chunks * 8; i < dim; ++i) tail += lane_term<METRIC>(a[i], b[i]);
+  float r = acc + tail;
+  if constexpr (METRIC == 1) return 1.0f - r;   // cosine_normalized, distance.rs:400-402
+  if constexpr (METRIC == 2) return -r;         // inner_product, distance.rs:291-293
+  return r;
+}
+
+// One thread computes the whole distance (same arithmetic as dist_group8).
+template <int METRIC>
+__device__ inline float dist_thread(const float* __restrict__ a, const float* __restrict__ b, int dim) {
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  const int chunks = dim >> 3;
+  for (int c = 0; c < chunks; ++c) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] += lane_term<METRIC>(a[c * 8 + j], b[c * 8 + j]);
+  }
+  float tail = 0.0f;
+  for (int i = chunks * 8; i < dim; ++i) tail += lane_term<METRIC>(a[i], b[i]);
+  float r = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+  r = r + tail;
+  if constexpr (METRIC == 1) return 1.0f - r;
+  if constexpr (METRIC == 2) return -r;
+  return r;
+}
+
+__device__ inline float dist_group8_rt(int metric, const float* a, const float* b, int dim, int g) {
+  switch (metric) {
+    case 0: return dist_group8<0>(a, b, dim, g);
+    case 1: return dist_group8<1>(a, b, dim, g);
+    case 2: return dist_group8<2>(a, b, dim, g);
+    default: return dist_group8<3>(a, b, dim, g);
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Bitonic sort (ascending) of 64*E unsigned 64-bit keys held in registers by
+// one wavefront; lane L holds elements L*E .. L*E+E-1.
+// ----------------------------------------------------------------------------
+template <int E>
+__device__ inline void wave_bitonic_sort(uint64_t (&k)[E], int lane) {
+  constexpr int N = WAVE * E;
+#pragma unroll
+  for (int size = 2; size <= N; size <<= 1) {
+#pragma unroll
+    for (int j = size >> 1; j > 0; j >>= 1) {
+      if (j >= E) {
+        const int lm = j / E;
+        const bool lower = (lane & lm) == 0;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const int i = lane * E + e;
+          const bool asc = (i & size) == 0;
+          uint64_t p = shfl_xor64(k[e], lm);
+          uint64_t mn = k[e] < p ? k[e] : p;
+          uint64_t mx = k[e] < p ? p : k[e];
+          k[e] = (lower == asc) ? mn : mx;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          if ((e & j) == 0) {
+            const int i = lane * E + e;
+            const bool asc = (i & size) == 0;
+            uint64_t x = k[e], y = k[e | j];
+            bool sw = asc ? (y < x) : (x < y);
+            k[e] = sw ? y : x;
+            k[e | j] = sw ? x : y;
+          }
+        }
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Block radix select: the K-th smallest (1-based) of n unique 64-bit keys
+// read through `get(i)`. All threads of the block call it; returns the pivot
+// in every thread. `hist` is 256 ints of shared memory, `sh` 4 u64 of shared.
+// Keys equal to KEY_MAX are padding and never selected; the caller clamps K
+// to the number of real keys.
+// ----------------------------------------------------------------------------
+template <class Get>
+__device__ inline uint64_t block_radix_select(Get get, int n, int K, int* hist, uint64_t* sh) {
+  uint64_t prefix = 0, mask = 0;
+  int remaining = K;
+  for (int pass = 0; pass < 8; ++pass) {
+    const int shift = 56 - 8 * pass;
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) hist[i] = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+      uint64_t x = get(i);
+      if ((x & mask) == prefix) atomicAdd(&hist[(x >> shift) & 255], 1);
+    }
+    __syncthreads();
+    if (threadIdx.x < WAVE) {
+      // exclusive scan over 256 bins by one wave: 4 bins per lane
+      const int lane = threadIdx.x;
+      int c0 = hist[lane * 4], c1 = hist[lane * 4 + 1], c2 = hist[lane * 4 + 2], c3 = hist[lane * 4 + 3];
+      int s = c0 + c1 + c2 + c3;
+      int incl = s;
+      for (int o = 1; o < WAVE; o <<= 1) {
+        int t = __shfl_up(incl, o, WAVE);
+        if (lane >= o) incl += t;
+      }
+      int excl = incl - s;
+      // the digit d with excl(d) < remaining <= excl(d) + count(d)
+      int e0 = excl, e1 = e0 + c0, e2 = e1 + c1, e3 = e2 + c2;
+      int d = -1, before = 0;
+      if (remaining > e0 && remaining <= e1) { d = lane * 4; before = e0; }
+      else if (remaining > e1 && remaining <= e2) { d = lane * 4 + 1; before = e1; }
+      else if (remaining > e2 && remaining <= e3) { d = lane * 4 + 2; before = e2; }
+      else if (remaining > e3 && remaining <= e3 + c3) { d = lane * 4 + 3; before = e3; }
+      if (d >= 0) {
+        sh[0] = (uint64_t)d;
+        sh[1] = (uint64_t)before;
+      }
+    }
+    __syncthreads();
+    const uint64_t d = sh[0];
+    remaining -= (int)sh[1];
+    prefix |= d << shift;
+    mask |= 255ull << shift;
+    __syncthreads();
+  }
+  return prefix;
+}
+
+}  // namespace pxg

@@ -1,0 +1,887 @@
+// Exact flat search on MI355X: FlatIndex (crates/proxima-index/src/flat.rs).
+//
+// Search pipeline for a batch of nq prepared queries against N slots:
+//
+//  1. flat_prep_queries   validate + (cosine) normalise each query on the
+//                         device, pad rows to `ld`, and compute the bias and
+//                         norm terms of the MFMA epilogue.
+//  2. flat_mfma_candidates  FP32-MFMA (v_mfma_f32_32x32x2f32) tiled GEMM of
+//                         the query block against database tiles staged in
+//                         LDS, fused with a per-query top-k' filter: scores
+//                         below the running threshold are appended to a
+//                         per-(query, split) buffer that a wave-level bitonic
+//                         sort compacts back to k' whenever it fills. The
+//                         N x nq score matrix never reaches HBM.
+//  3. flat_merge_rescore  per query: radix-select the k' best approximate
+//                         keys over all splits, rescore those k' exactly with
+//                         the reference's 8-lane arithmetic, sort by
+//                         (total_cmp(distance), id) and keep k. A query whose
+//                         k-th exact distance is not below the k'-th
+//                         approximate one minus the MFMA error bound is
+//                         flagged.
+//  4. flat_exact_candidates + flat_merge_exact   exact VALU scan for flagged
+//                         queries (and the whole batch for Manhattan, small
+//                         problems, or when forced). Distances are the
+//                         reference's bit for bit and ordering is exact, so
+//                         results equal the reference's FlatIndex::search.
+//
+// Ordering key everywhere: (ord_key(distance) << 32) | id_rank, where
+// id_rank is the rank of the slot's id among live ids. Sorting that key is
+// sorting by (total_cmp(distance), id), which is SearchResult's order
+// (topk.rs:63-67).
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <mutex>
+#include <numeric>
+#include <shared_mutex>
+
+#include "common.hpp"
+#include "device.hpp"
+
+namespace pxg {
+
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+constexpr int FB_M = 128;   // queries per workgroup tile
+constexpr int FB_N = 128;   // slots per workgroup tile
+constexpr int FB_K = 32;    // k-slice staged in LDS
+constexpr int FB_LDR = FB_K + 4;
+constexpr int MARGIN = 32;  // k' = k + MARGIN
+constexpr int EXACT_CH = 1024;
+constexpr int FAST_KMAX = 256;
+
+// ---------------------------------------------------------------------------
+// 1. query preparation
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void flat_prep_queries(const float* __restrict__ raw, int dim, int ld, int metric,
+                                                        int do_prepare, float* __restrict__ Qp,
+                                                        float* __restrict__ qb, float* __restrict__ qn,
+                                                        unsigned long long* __restrict__ bad) {
+  const int q = blockIdx.x;
+  const int lane = threadIdx.x;
+  const float* v = raw + (size_t)q * dim;
+  float* out = Qp + (size_t)q * ld;
+  __shared__ float s_inv;
+  // validate: first non-finite component (space.rs:104-121)
+  for (int i = lane; i < dim; i += 64) {
+    if (!isfinite(v[i])) atomicMin(bad, ((unsigned long long)q << 32) | (unsigned)i);
+  }
+  if (lane < 8) {
+    float d = dist_group8<2>(v, v, dim, lane);  // = -dot_unrolled(v, v)
+    if (lane == 0) {
+      float dot = -d;
+      float inv = 1.0f;
+      if (do_prepare && metric == 1) {
+        float n = sqrtf(dot);
+        inv = (n > 0.0f && isfinite(n)) ? 1.0f / n : 1.0f;
+        s_inv = (n > 0.0f && isfinite(n)) ? inv : 0.0f;  // 0 marks "leave untouched"
+      } else {
+        s_inv = 0.0f;
+      }
+    }
+  }
+  __syncthreads();
+  const float inv = s_inv;
+  for (int i = lane; i < ld; i += 64) {
+    float x = i < dim ? v[i] : 0.0f;
+    if (inv != 0.0f) x = x * inv;
+    out[i] = x;
+  }
+  __syncthreads();
+  if (lane < 8) {
+    float d = -dist_group8<2>(out, out, dim, lane);
+    if (lane == 0) {
+      qn[q] = sqrtf(d);
+      qb[q] = metric == 0 ? d : (metric == 1 ? 1.0f : 0.0f);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2. MFMA distance GEMM fused with a per-query top-k' filter
+// ---------------------------------------------------------------------------
+template <int CAP>
+__device__ inline void compact_row(uint64_t* __restrict__ base, int c, int Kp, int lane, uint64_t* thr_row,
+                                   int* cnt_row, bool final_pass) {
+  constexpr int E = CAP / WAVE;
+  uint64_t kk[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int idx = lane * E + e;
+    kk[e] = idx < c ? base[idx] : KEY_MAX;
+  }
+  wave_bitonic_sort<E>(kk, lane);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int idx = lane * E + e;
+    if (idx < Kp) base[idx] = kk[e];
+    if (idx == Kp - 1 && !final_pass) *thr_row = kk[e];
+  }
+  if (lane == 0 && !final_pass) *cnt_row = Kp;
+}
+
+template <int CAP>
+__global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
+    const float* __restrict__ Q, int nq, const float* __restrict__ X, int N, int ld,
+    const float* __restrict__ qb, const float* __restrict__ xb, float scale, const uint8_t* __restrict__ live,
+    const uint8_t* __restrict__ accept, int S, int QB, int per_split, int Kp, uint64_t* __restrict__ cand) {
+  __shared__ float sQ[2][FB_M * FB_LDR];
+  __shared__ float sX[2][FB_N * FB_LDR];
+  __shared__ uint64_t thr[FB_M];
+  __shared__ int cnt[FB_M];
+  __shared__ float sqb[FB_M];
+
+  // XCD-aware mapping: consecutive workgroup ids are dealt round-robin over
+  // the 8 XCDs, so give each XCD a contiguous range of (split, query block)
+  // work; the QB workgroups sharing one split's database tiles then run on
+  // the same XCD at the same time and share its L2.
+  const int total = QB * S;
+  const int per_xcd = (total + 7) / 8;
+  const int g = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  if (g >= total) return;
+  const int qblk = g % QB, split = g / QB;
+  const int q0 = qblk * FB_M;
+  const int s_begin = split * per_split;
+  const int s_end = min(N, s_begin + per_split);
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int h = lane >> 5, r = lane & 31;
+  const int wm = (wid >> 1) * 64, wn = (wid & 1) * 64;
+
+  for (int i = tid; i < FB_M; i += 256) {
+    thr[i] = KEY_MAX;
+    cnt[i] = 0;
+    sqb[i] = (q0 + i < nq) ? qb[q0 + i] : 0.0f;
+  }
+  __syncthreads();
+
+  const int lr = tid >> 3, lc = (tid & 7) * 4;  // global->LDS copy: row, column
+  const int nK = (ld + FB_K - 1) / FB_K;
+
+  for (int n0 = s_begin; n0 < s_end; n0 += FB_N) {
+    f16v acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+    float4 rq[4], rx[4];
+    auto gload = [&](int k0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = lr + 32 * i;
+        const int kc = k0 + lc;
+        const int q = q0 + row, x = n0 + row;
+        rq[i] = (q < nq && kc < ld) ? *reinterpret_cast<const float4*>(Q + (size_t)q * ld + kc)
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+        rx[i] = (x < s_end && kc < ld) ? *reinterpret_cast<const float4*>(X + (size_t)x * ld + kc)
+                                       : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = lr + 32 * i;
+        *reinterpret_cast<float4*>(&sQ[buf][row * FB_LDR + lc]) = rq[i];
+        *reinterpret_cast<float4*>(&sX[buf][row * FB_LDR + lc]) = rx[i];
+      }
+    };
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < nK; ++kt) {
+      const int cur = kt & 1;
+      if (kt + 1 < nK) gload((kt + 1) * FB_K);
+      // Lane (h, r) feeds k = h*16 + kk of row r: the MFMA pairs A and B by
+      // lane half, so any fixed permutation of k within the slice is a
+      // valid dot product; this one lets each lane read 16 contiguous floats.
+      const float* a0p = &sQ[cur][(wm + r) * FB_LDR + h * 16];
+      const float* a1p = &sQ[cur][(wm + 32 + r) * FB_LDR + h * 16];
+      const float* b0p = &sX[cur][(wn + r) * FB_LDR + h * 16];
+      const float* b1p = &sX[cur][(wn + 32 + r) * FB_LDR + h * 16];
+#pragma unroll
+      for (int k4 = 0; k4 < 4; ++k4) {
+        const float4 a0 = *reinterpret_cast<const float4*>(a0p + k4 * 4);
+        const float4 a1 = *reinterpret_cast<const float4*>(a1p + k4 * 4);
+        const float4 b0 = *reinterpret_cast<const float4*>(b0p + k4 * 4);
+        const float4 b1 = *reinterpret_cast<const float4*>(b1p + k4 * 4);
+        const float av0[4] = {a0.x, a0.y, a0.z, a0.w}, av1[4] = {a1.x, a1.y, a1.z, a1.w};
+        const float bv0[4] = {b0.x, b0.y, b0.z, b0.w}, bv1[4] = {b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(av0[t], bv0[t], acc[0][0], 0, 0, 0);
+          acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(av0[t], bv1[t], acc[0][1], 0, 0, 0);
+          acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(av1[t], bv0[t], acc[1][0], 0, 0, 0);
+          acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(av1[t], bv1[t], acc[1][1], 0, 0, 0);
+        }
+      }
+      if (kt + 1 < nK) lstore(cur ^ 1);
+      __syncthreads();
+    }
+
+    // Epilogue: approximate score, threshold filter, append.
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int slot = n0 + wn + j * 32 + r;
+      const bool ok = slot < s_end && live[slot] && (accept == nullptr || accept[slot]);
+      const float xbv = ok ? xb[slot] : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = wm + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+          if (ok && q0 + row < nq) {
+            const float a = (sqb[row] + xbv) - scale * acc[i][j][v];
+            const uint64_t key = ((uint64_t)ord_key(a) << 32) | (uint32_t)slot;
+            if (key < thr[row]) {
+              const int pos = atomicAdd(&cnt[row], 1);
+              cand[((size_t)(q0 + row) * S + split) * CAP + pos] = key;
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+    for (int row = wid; row < FB_M; row += 4) {
+      const int c = cnt[row];
+      if (c > CAP - FB_N)
+        compact_row<CAP>(cand + ((size_t)(q0 + row) * S + split) * CAP, c, Kp, lane, &thr[row], &cnt[row], false);
+    }
+    __syncthreads();
+  }
+  // Final: every row leaves exactly Kp sorted keys (KEY_MAX padded).
+  for (int row = wid; row < FB_M; row += 4) {
+    if (q0 + row >= nq) continue;
+    compact_row<CAP>(cand + ((size_t)(q0 + row) * S + split) * CAP, cnt[row], Kp, lane, &thr[row], &cnt[row], true);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// shared-memory bitonic sort (ascending) of n = power-of-two keys
+// ---------------------------------------------------------------------------
+__device__ inline void block_bitonic_sort(uint64_t* keys, int n) {
+  for (int size = 2; size <= n; size <<= 1) {
+    for (int j = size >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < (n >> 1); i += blockDim.x) {
+        const int idx = ((i / j) * 2 * j) + (i % j);
+        const bool asc = (idx & size) == 0;
+        const uint64_t a = keys[idx], b = keys[idx + j];
+        if ((a > b) == asc) {
+          keys[idx] = b;
+          keys[idx + j] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 3. merge + exact rescore (approximate candidates)
+// ---------------------------------------------------------------------------
+constexpr int MERGE_MAXP = 512;
+
+__global__ __launch_bounds__(256) void flat_merge_rescore(
+    const uint64_t* __restrict__ cand, int S, int CAP, int Kp, int k, const float* __restrict__ Qp, int ld, int dim,
+    int metric, const float* __restrict__ X, const uint32_t* __restrict__ rank, const uint32_t* __restrict__ rank_slot,
+    const uint64_t* __restrict__ ids, const float* __restrict__ qn, float maxnorm, float eps_c,
+    uint64_t* __restrict__ out_ids, float* __restrict__ out_d, uint32_t* __restrict__ out_count,
+    int* __restrict__ flag_list, int* __restrict__ flag_count) {
+  const int q = blockIdx.x;
+  __shared__ int hist[256];
+  __shared__ uint64_t sh[4];
+  __shared__ uint64_t sel[MERGE_MAXP];
+  __shared__ int n_sel;
+  __shared__ int n_valid;
+  const uint64_t* base = cand + (size_t)q * S * CAP;
+  const int n = S * Kp;
+  auto get = [&](int i) -> uint64_t { return base[(size_t)(i / Kp) * CAP + (i % Kp)]; };
+
+  if (threadIdx.x == 0) {
+    n_valid = 0;
+    n_sel = 0;
+  }
+  __syncthreads();
+  int local = 0;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) local += get(i) != KEY_MAX;
+  atomicAdd(&n_valid, local);
+  __syncthreads();
+  const int valid = n_valid;
+  const int ksel = min(Kp, valid);
+  if (ksel == 0) {
+    if (threadIdx.x == 0) out_count[q] = 0;
+    return;
+  }
+  const uint64_t pivot = block_radix_select(get, n, ksel, hist, sh);
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const uint64_t x = get(i);
+    if (x <= pivot && x != KEY_MAX) {
+      const int p = atomicAdd(&n_sel, 1);
+      sel[p] = x;
+    }
+  }
+  __syncthreads();
+  // rescore: 8 threads per candidate
+  const int g = threadIdx.x & 7, grp = threadIdx.x >> 3;
+  const float* qv = Qp + (size_t)q * ld;
+  for (int c = grp; c < ksel; c += 32) {
+    const uint32_t slot = (uint32_t)sel[c];
+    const float d = dist_group8_rt(metric, qv, X + (size_t)slot * ld, dim, g);
+    if (g == 0) sel[c] = ((uint64_t)ord_key(d) << 32) | rank[slot];
+  }
+  __syncthreads();
+  int P = 1;
+  while (P < ksel) P <<= 1;
+  for (int i = ksel + threadIdx.x; i < P; i += blockDim.x) sel[i] = KEY_MAX;
+  __syncthreads();
+  block_bitonic_sort(sel, P);
+  const int kout = min(k, ksel);
+  for (int i = threadIdx.x; i < kout; i += blockDim.x) {
+    const uint64_t key = sel[i];
+    const uint32_t slot = rank_slot[(uint32_t)key];
+    out_ids[(size_t)q * k + i] = ids[slot];
+    out_d[(size_t)q * k + i] = key_float((uint32_t)(key >> 32));
+  }
+  if (threadIdx.x == 0) {
+    out_count[q] = kout;
+    if (valid >= Kp) {
+      // Every candidate outside the selection has approx >= approx(pivot),
+      // hence exact >= approx(pivot) - eps. The k-th exact distance must be
+      // strictly below that for the selection to contain the exact top-k.
+      const float ak = key_float((uint32_t)(pivot >> 32));
+      const float dk = key_float((uint32_t)(sel[kout - 1] >> 32));
+      const float qnv = qn[q];
+      float eps;
+      if (metric == 0) {
+        const float s = qnv + maxnorm;
+        eps = eps_c * (float)dim * 5.9604645e-08f * s * s;
+      } else {
+        eps = eps_c * (float)dim * 5.9604645e-08f * qnv * maxnorm + 2.4e-7f;
+      }
+      eps += 1e-30f;
+      if (!(dk < ak - eps)) {
+        const int p = atomicAdd(flag_count, 1);
+        flag_list[p] = q;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 4. exact VALU scan for a list of queries
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void flat_exact_candidates(
+    const int* __restrict__ qlist, const int* __restrict__ qcount, int nchunks, const float* __restrict__ Qp, int ld,
+    int dim, int metric, const float* __restrict__ X, int N, const uint8_t* __restrict__ live,
+    const uint8_t* __restrict__ accept, const uint32_t* __restrict__ rank, int k, uint64_t* __restrict__ ecand) {
+  __shared__ uint64_t keys[EXACT_CH];
+  const int total = (*qcount) * nchunks;
+  const int g = threadIdx.x & 7, grp = threadIdx.x >> 3;
+  const int kk = min(k, EXACT_CH);
+  for (int w = blockIdx.x; w < total; w += gridDim.x) {
+    const int f = w / nchunks, c = w % nchunks;
+    const int q = qlist[f];
+    const float* qv = Qp + (size_t)q * ld;
+    const int base = c * EXACT_CH;
+    for (int s = grp; s < EXACT_CH; s += 32) {
+      const int slot = base + s;
+      uint64_t key = KEY_MAX;
+      if (slot < N && live[slot] && (accept == nullptr || accept[slot])) {
+        const float d = dist_group8_rt(metric, qv, X + (size_t)slot * ld, dim, g);
+        key = ((uint64_t)ord_key(d) << 32) | rank[slot];
+      }
+      if (g == 0) keys[s] = key;
+    }
+    __syncthreads();
+    block_bitonic_sort(keys, EXACT_CH);
+    uint64_t* out = ecand + ((size_t)f * nchunks + c) * kk;
+    for (int i = threadIdx.x; i < kk; i += blockDim.x) out[i] = keys[i];
+    __syncthreads();
+  }
+}
+
+constexpr int EXACT_MERGE_MAXK = 1024;
+
+__global__ __launch_bounds__(256) void flat_merge_exact(const int* __restrict__ qlist, const int* __restrict__ qcount,
+                                                        const uint64_t* __restrict__ ecand, int nchunks, int k,
+                                                        const uint32_t* __restrict__ rank_slot,
+                                                        const uint64_t* __restrict__ ids,
+                                                        uint64_t* __restrict__ out_ids, float* __restrict__ out_d,
+                                                        uint32_t* __restrict__ out_count) {
+  const int f = blockIdx.x;
+  if (f >= *qcount) return;
+  const int q = qlist[f];
+  __shared__ int hist[256];
+  __shared__ uint64_t sh[4];
+  __shared__ uint64_t sel[EXACT_MERGE_MAXK];
+  __shared__ int n_sel, n_valid;
+  const int kk = min(k, EXACT_CH);
+  const uint64_t* base = ecand + (size_t)f * nchunks * kk;
+  const int n = nchunks * kk;
+  auto get = [&](int i) -> uint64_t { return base[i]; };
+  if (threadIdx.x == 0) {
+    n_sel = 0;
+    n_valid = 0;
+  }
+  __syncthreads();
+  int local = 0;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) local += base[i] != KEY_MAX;
+  atomicAdd(&n_valid, local);
+  __syncthreads();
+  const int ksel = min(k, n_valid);
+  if (ksel == 0) {
+    if (threadIdx.x == 0) out_count[q] = 0;
+    return;
+  }
+  const uint64_t pivot = block_radix_select(get, n, ksel, hist, sh);
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const uint64_t x = base[i];
+    if (x <= pivot && x != KEY_MAX) sel[atomicAdd(&n_sel, 1)] = x;
+  }
+  __syncthreads();
+  int P = 1;
+  while (P < ksel) P <<= 1;
+  for (int i = ksel + threadIdx.x; i < P; i += blockDim.x) sel[i] = KEY_MAX;
+  __syncthreads();
+  block_bitonic_sort(sel, P);
+  for (int i = threadIdx.x; i < ksel; i += blockDim.x) {
+    const uint64_t key = sel[i];
+    out_ids[(size_t)q * k + i] = ids[rank_slot[(uint32_t)key]];
+    out_d[(size_t)q * k + i] = key_float((uint32_t)(key >> 32));
+  }
+  if (threadIdx.x == 0) out_count[q] = ksel;
+}
+
+__global__ void iota_kernel(int* a, int n, int* count) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) a[i] = i;
+  if (i == 0) *count = n;
+}
+
+// Scatter staged rows into their slots (insert path).
+__global__ void flat_scatter_rows(const float* __restrict__ staged, const uint32_t* __restrict__ slots,
+                                  const float* __restrict__ bias, const uint64_t* __restrict__ sid, int n, int ld,
+                                  float* __restrict__ X, float* __restrict__ xb, uint8_t* __restrict__ live,
+                                  uint64_t* __restrict__ ids) {
+  const int i = blockIdx.x;
+  if (i >= n) return;
+  const uint32_t s = slots[i];
+  for (int c = threadIdx.x; c < ld; c += blockDim.x) X[(size_t)s * ld + c] = staged[(size_t)i * ld + c];
+  if (threadIdx.x == 0) {
+    xb[s] = bias[i];
+    live[s] = 1;
+    ids[s] = sid[i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+struct FlatIndex {
+  uint32_t dim = 0, ld = 0;
+  int metric = 0;
+  int mode = 0;  // 0 auto, 1 force MFMA candidates, 2 force exact scan
+
+  // host mirror of the slot table (storage.rs:100-115)
+  std::vector<uint64_t> ids;
+  std::vector<uint8_t> live;
+  std::unordered_map<uint64_t, uint32_t> by_id;
+  SlotAllocator slots;
+  float maxnorm = 0.0f;
+
+  // device state
+  size_t cap = 0;
+  DevBuf<float> X;         // cap * ld, prepared vectors, zero padded
+  DevBuf<float> xb;        // cap: |x|^2 for L2, 0 otherwise
+  DevBuf<uint8_t> d_live;  // cap
+  DevBuf<uint64_t> d_ids;  // cap
+  DevBuf<uint32_t> d_rank;       // cap
+  DevBuf<uint32_t> d_rank_slot;  // len
+  bool rank_dirty = true;
+  std::mutex rank_mu;
+
+  mutable std::shared_mutex mu;
+  CtxPool pool;
+  hipStream_t stream = nullptr;
+
+  ~FlatIndex() {
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+
+  void ensure_capacity(size_t need) {
+    if (need <= cap) return;
+    size_t nc = std::max<size_t>(need, std::max<size_t>(cap * 2, 1024));
+    const size_t hw = slots.high_water();
+    X.grow(nc * ld, hw * ld, stream);
+    xb.grow(nc, hw, stream);
+    d_live.grow(nc, hw, stream);
+    d_ids.grow(nc, hw, stream);
+    d_rank.grow(nc, hw, stream);
+    // zero the new tail of the liveness map
+    PXG_HIP(hipMemsetAsync(d_live.p + hw, 0, nc - hw, stream));
+    PXG_HIP(hipStreamSynchronize(stream));
+    cap = nc;
+  }
+
+  void rebuild_ranks(hipStream_t s) {
+    std::lock_guard<std::mutex> lk(rank_mu);
+    if (!rank_dirty) return;
+    std::vector<std::pair<uint64_t, uint32_t>> v;
+    v.reserve(by_id.size());
+    for (size_t s2 = 0; s2 < ids.size(); ++s2)
+      if (live[s2]) v.emplace_back(ids[s2], (uint32_t)s2);
+    std::sort(v.begin(), v.end());
+    std::vector<uint32_t> rs(v.size()), rk(std::max<size_t>(ids.size(), 1), 0);
+    for (size_t r = 0; r < v.size(); ++r) {
+      rs[r] = v[r].second;
+      rk[v[r].second] = (uint32_t)r;
+    }
+    d_rank_slot.reserve(std::max<size_t>(rs.size(), 1));
+    if (!rs.empty()) PXG_HIP(hipMemcpyAsync(d_rank_slot.p, rs.data(), rs.size() * 4, hipMemcpyHostToDevice, s));
+    if (!ids.empty()) PXG_HIP(hipMemcpyAsync(d_rank.p, rk.data(), ids.size() * 4, hipMemcpyHostToDevice, s));
+    PXG_HIP(hipStreamSynchronize(s));
+    rank_dirty = false;
+  }
+
+  void insert(const uint64_t* in_ids, const float* vecs, uint64_t n, uint32_t* out_slots) {
+    // Validate everything first: all-or-nothing.
+    std::vector<float> prepared((size_t)n * ld, 0.0f);
+    std::vector<float> bias(n);
+    float newmax = maxnorm;
+    for (uint64_t i = 0; i < n; ++i) {
+      long long bad = validate_prepare(metric, vecs + i * dim, dim, prepared.data() + i * ld);
+      if (bad >= 0)
+        raise(PXG_ERR_NON_FINITE,
+              "vector component " + std::to_string(bad) + " is not finite (" + std::to_string(vecs[i * dim + bad]) + ")",
+              (uint64_t)bad, i, vecs[i * dim + bad]);
+      const float* p = prepared.data() + i * ld;
+      float n2 = host_dot_unrolled(p, p, dim);
+      bias[i] = metric == PXG_EUCLIDEAN ? n2 : 0.0f;
+      float nr = std::sqrt(n2);
+      if (!(nr <= newmax)) newmax = std::isnan(nr) ? INFINITY : nr;
+    }
+    {
+      std::unordered_map<uint64_t, int> seen;
+      for (uint64_t i = 0; i < n; ++i) {
+        if (by_id.count(in_ids[i]) || !seen.emplace(in_ids[i], 1).second)
+          raise(PXG_ERR_DUPLICATE_ID, "duplicate vector id " + std::to_string(in_ids[i]), in_ids[i]);
+      }
+    }
+    if (by_id.size() + n > (size_t)UINT32_MAX - 1)
+      raise(PXG_ERR_CAPACITY, "capacity exceeded: slot allocator limit is 4294967295", UINT32_MAX);
+    std::vector<uint32_t> sl(n);
+    // Allocate in order, exactly as repeated VectorStore::insert would.
+    for (uint64_t i = 0; i < n; ++i) sl[i] = slots.allocate();
+    const size_t hw = slots.high_water();
+    ensure_capacity(hw);
+    if (ids.size() < hw) {
+      ids.resize(hw, 0);
+      live.resize(hw, 0);
+    }
+    for (uint64_t i = 0; i < n; ++i) {
+      ids[sl[i]] = in_ids[i];
+      live[sl[i]] = 1;
+      by_id[in_ids[i]] = sl[i];
+      if (out_slots) out_slots[i] = sl[i];
+    }
+    maxnorm = newmax;
+    // stage and scatter in chunks of <= 64 MiB of rows
+    const size_t rows_per = std::max<size_t>(1, (64u << 20) / ((size_t)ld * 4));
+    DevBuf<float> st_rows(std::min<size_t>(rows_per, n) * ld);
+    DevBuf<uint32_t> st_slots(std::min<size_t>(rows_per, n));
+    DevBuf<float> st_bias(std::min<size_t>(rows_per, n));
+    DevBuf<uint64_t> st_ids(std::min<size_t>(rows_per, n));
+    for (size_t a = 0; a < n; a += rows_per) {
+      const size_t m = std::min<size_t>(rows_per, n - a);
+      PXG_HIP(hipMemcpyAsync(st_rows.p, prepared.data() + a * ld, m * ld * 4, hipMemcpyHostToDevice, stream));
+      PXG_HIP(hipMemcpyAsync(st_slots.p, sl.data() + a, m * 4, hipMemcpyHostToDevice, stream));
+      PXG_HIP(hipMemcpyAsync(st_bias.p, bias.data() + a, m * 4, hipMemcpyHostToDevice, stream));
+      PXG_HIP(hipMemcpyAsync(st_ids.p, in_ids + a, m * 8, hipMemcpyHostToDevice, stream));
+      hipLaunchKernelGGL(flat_scatter_rows, dim3((unsigned)m), dim3(256), 0, stream, st_rows.p, st_slots.p,
+                         st_bias.p, st_ids.p, (int)m, (int)ld, X.p, xb.p, d_live.p, d_ids.p);
+      PXG_HIP(hipGetLastError());
+      PXG_HIP(hipStreamSynchronize(stream));
+    }
+    rank_dirty = true;
+  }
+
+  void remove(uint64_t id) {
+    auto it = by_id.find(id);
+    if (it == by_id.end()) raise(PXG_ERR_UNKNOWN_ID, "unknown vector id " + std::to_string(id), id);
+    const uint32_t s = it->second;
+    by_id.erase(it);
+    live[s] = 0;
+    slots.release(s);
+    PXG_HIP(hipMemsetAsync(d_live.p + s, 0, 1, stream));
+    PXG_HIP(hipStreamSynchronize(stream));
+    rank_dirty = true;
+  }
+
+  // Run the search pipeline on prepared-or-raw device queries.
+  void search_device(const float* d_raw, bool do_prepare, uint64_t nq, uint64_t k, const uint8_t* d_accept,
+                     uint64_t* d_oid, float* d_od, uint32_t* d_oc, Ctx* ctx, hipStream_t s, uint64_t* fallbacks) {
+    check_k(k);
+    *fallbacks = 0;
+    const size_t N = slots.high_water();
+    if (nq == 0) return;
+    if (k == 0 || by_id.empty()) {
+      PXG_HIP(hipMemsetAsync(d_oc, 0, nq * 4, s));
+      PXG_HIP(hipStreamSynchronize(s));
+      return;
+    }
+    if (k > EXACT_MERGE_MAXK)
+      config_error("k", k, "the GPU flat search supports k up to 1024 per query");
+    rebuild_ranks(s);
+
+    // 1. prepare queries
+    float* Qp = (float*)ctx->get(1, nq * ld * 4);
+    float* qb = (float*)ctx->get(2, nq * 4);
+    float* qn = (float*)ctx->get(3, nq * 4);
+    unsigned long long* bad = (unsigned long long*)ctx->get(4, 8 + 8);
+    int* flag_count = (int*)(bad + 1);
+    PXG_HIP(hipMemsetAsync(bad, 0xFF, 8, s));
+    PXG_HIP(hipMemsetAsync(flag_count, 0, 4, s));
+    hipLaunchKernelGGL(flat_prep_queries, dim3((unsigned)nq), dim3(64), 0, s, d_raw, (int)dim, (int)ld, metric,
+                       do_prepare ? 1 : 0, Qp, qb, qn, bad);
+    PXG_HIP(hipGetLastError());
+
+    int* flag_list = (int*)ctx->get(5, nq * 4);
+    // Manhattan has no inner-product form and k beyond FAST_KMAX exceeds the
+    // candidate buffers: both take the exact scan, as do small problems.
+    const bool exact_all = mode == 2 || metric == PXG_MANHATTAN || k > FAST_KMAX ||
+                           (mode == 0 && (N < 4096 || (double)N * (double)nq < 4.0e6));
+    if (!exact_all) {
+      const int Kp = (int)std::min<uint64_t>(k + MARGIN, (uint64_t)FAST_KMAX + MARGIN);
+      const int CAP = (Kp + FB_N) <= 256 ? 256 : 512;
+      const int QB = (int)((nq + FB_M - 1) / FB_M);
+      const int tiles = (int)((N + FB_N - 1) / FB_N);
+      int S = std::max(1, std::min(512 / QB, std::max(1, tiles / 4)));
+      const int tiles_per = (tiles + S - 1) / S;
+      const int per_split = tiles_per * FB_N;
+      S = (int)((N + per_split - 1) / per_split);
+      uint64_t* cand = (uint64_t*)ctx->get(6, (size_t)nq * S * CAP * 8);
+      const int total = QB * S;
+      const int grid = ((total + 7) / 8) * 8;
+      const float scale = metric == PXG_EUCLIDEAN ? 2.0f : 1.0f;
+      if (CAP == 256)
+        hipLaunchKernelGGL(flat_mfma_candidates<256>, dim3(grid), dim3(256), 0, s, Qp, (int)nq, X.p, (int)N, (int)ld,
+                           qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, Kp, cand);
+      else
+        hipLaunchKernelGGL(flat_mfma_candidates<512>, dim3(grid), dim3(256), 0, s, Qp, (int)nq, X.p, (int)N, (int)ld,
+                           qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, Kp, cand);
+      PXG_HIP(hipGetLastError());
+      hipLaunchKernelGGL(flat_merge_rescore, dim3((unsigned)nq), dim3(256), 0, s, cand, S, CAP, Kp, (int)k, Qp,
+                         (int)ld, (int)dim, metric, X.p, d_rank.p, d_rank_slot.p, d_ids.p, qn, maxnorm, 4.0f, d_oid,
+                         d_od, d_oc, flag_list, flag_count);
+      PXG_HIP(hipGetLastError());
+    } else {
+      hipLaunchKernelGGL(iota_kernel, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s, flag_list, (int)nq,
+                         flag_count);
+      PXG_HIP(hipGetLastError());
+    }
+    // exact scan for flagged queries (all of them on the exact path)
+    int nflag = 0;
+    PXG_HIP(hipMemcpyAsync(&nflag, flag_count, 4, hipMemcpyDeviceToHost, s));
+    unsigned long long badv = 0;
+    PXG_HIP(hipMemcpyAsync(&badv, bad, 8, hipMemcpyDeviceToHost, s));
+    PXG_HIP(hipStreamSynchronize(s));
+    if (badv != ~0ull) {
+      const uint32_t qi = (uint32_t)(badv >> 32), comp = (uint32_t)badv;
+      raise(PXG_ERR_NON_FINITE, "vector component " + std::to_string(comp) + " is not finite (query " +
+                                    std::to_string(qi) + ")",
+            comp, qi, NAN);
+    }
+    if (nflag > 0) {
+      const int nchunks = (int)((N + EXACT_CH - 1) / EXACT_CH);
+      const int kk = (int)std::min<uint64_t>(k, EXACT_CH);
+      uint64_t* ecand = (uint64_t*)ctx->get(7, (size_t)nflag * nchunks * kk * 8);
+      const int grid = std::min(nflag * nchunks, 4096);
+      hipLaunchKernelGGL(flat_exact_candidates, dim3(grid), dim3(256), 0, s, flag_list, flag_count, nchunks, Qp,
+                         (int)ld, (int)dim, metric, X.p, (int)N, d_live.p, d_accept, d_rank.p, (int)k, ecand);
+      PXG_HIP(hipGetLastError());
+      hipLaunchKernelGGL(flat_merge_exact, dim3((unsigned)nflag), dim3(256), 0, s, flag_list, flag_count, ecand,
+                         nchunks, (int)k, d_rank_slot.p, d_ids.p, d_oid, d_od, d_oc);
+      PXG_HIP(hipGetLastError());
+      PXG_HIP(hipStreamSynchronize(s));
+      *fallbacks = exact_all ? 0 : (uint64_t)nflag;
+    }
+  }
+};
+
+thread_local uint64_t g_last_fallbacks = 0;
+
+}  // namespace pxg
+
+using pxg::FlatIndex;
+
+struct pxg_flat {
+  FlatIndex impl;
+};
+
+extern "C" {
+
+int pxg_flat_create(uint32_t dim, int metric, uint64_t capacity, pxg_flat** out) {
+  return pxg::guard([&] {
+    if (!out) pxg::config_error("out", 0, "must not be NULL");
+    if (dim < 1) pxg::config_error("dim", dim, "must be at least 1; a 0-dimensional space makes all distances equal");
+    if (dim > (1u << 20)) pxg::config_error("dim", dim, "exceeds the 1048576 dimension ceiling");
+    if (metric < 0 || metric > 3) pxg::config_error("metric", (uint64_t)metric, "unknown metric");
+    auto* h = new pxg_flat();
+    FlatIndex& f = h->impl;
+    f.dim = dim;
+    f.ld = (dim + 3) & ~3u;
+    f.metric = metric;
+    try {
+      PXG_HIP(hipStreamCreateWithFlags(&f.stream, hipStreamNonBlocking));
+      if (capacity) f.ensure_capacity(capacity);
+    } catch (...) {
+      delete h;
+      throw;
+    }
+    *out = h;
+  });
+}
+
+void pxg_flat_destroy(pxg_flat* index) { delete index; }
+
+int pxg_flat_insert(pxg_flat* index, const uint64_t* ids, const float* vectors, uint64_t n, uint32_t* out_slots) {
+  return pxg::guard([&] {
+    if (n == 0) return;
+    std::unique_lock<std::shared_mutex> lk(index->impl.mu);
+    index->impl.insert(ids, vectors, n, out_slots);
+  });
+}
+
+int pxg_flat_remove(pxg_flat* index, uint64_t id) {
+  return pxg::guard([&] {
+    std::unique_lock<std::shared_mutex> lk(index->impl.mu);
+    index->impl.remove(id);
+  });
+}
+
+int pxg_flat_contains(const pxg_flat* index, uint64_t id) {
+  std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+  return index->impl.by_id.count(id) ? 1 : 0;
+}
+
+uint64_t pxg_flat_len(const pxg_flat* index) {
+  std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+  return index->impl.by_id.size();
+}
+
+int pxg_flat_stats(const pxg_flat* index, pxg_index_stats* out) {
+  return pxg::guard([&] {
+    std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+    const FlatIndex& f = index->impl;
+    out->len = f.by_id.size();
+    out->deleted = 0;  // slots are freed on delete: no tombstones
+    out->dim = f.dim;
+    out->metric = f.metric;
+    out->layers = 1;
+    out->edges = 0;
+    out->vector_bytes = f.X.bytes();
+    out->graph_bytes = 0;
+  });
+}
+
+int pxg_flat_get_vector(const pxg_flat* index, uint64_t id, float* out) {
+  return pxg::guard([&] {
+    std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+    const FlatIndex& f = index->impl;
+    auto it = f.by_id.find(id);
+    if (it == f.by_id.end()) pxg::raise(PXG_ERR_UNKNOWN_ID, "unknown vector id " + std::to_string(id), id);
+    PXG_HIP(hipMemcpy(out, f.X.p + (size_t)it->second * f.ld, f.dim * 4, hipMemcpyDeviceToHost));
+  });
+}
+
+uint64_t pxg_flat_slot_count(const pxg_flat* index) {
+  std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+  return index->impl.slots.high_water();
+}
+
+int pxg_flat_slots(const pxg_flat* index, uint64_t* ids, uint8_t* live) {
+  return pxg::guard([&] {
+    std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+    const FlatIndex& f = index->impl;
+    const size_t hw = f.slots.high_water();
+    for (size_t s = 0; s < hw; ++s) {
+      if (ids) ids[s] = f.live[s] ? f.ids[s] : 0;
+      if (live) live[s] = f.live[s];
+    }
+  });
+}
+
+int pxg_flat_search(const pxg_flat* index, const float* queries, uint64_t nq, uint64_t k, const uint8_t* accept,
+                    uint64_t* out_ids, float* out_dist, uint32_t* out_count) {
+  return pxg::guard([&] {
+    pxg::check_k(k);
+    FlatIndex& f = const_cast<FlatIndex&>(index->impl);
+    std::shared_lock<std::shared_mutex> lk(f.mu);
+    if (nq == 0) return;
+    // validate + prepare on the host (space.rs:130-138)
+    std::vector<float> prep((size_t)nq * f.dim);
+    for (uint64_t i = 0; i < nq; ++i) {
+      long long bad = pxg::validate_prepare(f.metric, queries + i * f.dim, f.dim, prep.data() + i * f.dim);
+      if (bad >= 0)
+        pxg::raise(PXG_ERR_NON_FINITE,
+                   "vector component " + std::to_string(bad) + " is not finite (" +
+                       std::to_string(queries[i * f.dim + bad]) + ")",
+                   (uint64_t)bad, i, queries[i * f.dim + bad]);
+    }
+    if (k == 0 || f.by_id.empty()) {
+      for (uint64_t i = 0; i < nq; ++i) out_count[i] = 0;
+      return;
+    }
+    pxg::CtxLease ctx(f.pool);
+    hipStream_t s = ctx->stream;
+    const size_t N = f.slots.high_water();
+    float* d_q = (float*)ctx->get(20, prep.size() * 4);
+    uint8_t* d_acc = nullptr;
+    if (accept) {
+      d_acc = ctx->get(21, N);
+      PXG_HIP(hipMemcpyAsync(d_acc, accept, N, hipMemcpyHostToDevice, s));
+    }
+    uint64_t* d_oid = (uint64_t*)ctx->get(22, nq * k * 8);
+    float* d_od = (float*)ctx->get(23, nq * k * 4);
+    uint32_t* d_oc = (uint32_t*)ctx->get(24, nq * 4);
+    PXG_HIP(hipMemcpyAsync(d_q, prep.data(), prep.size() * 4, hipMemcpyHostToDevice, s));
+    uint64_t fb = 0;
+    f.search_device(d_q, false, nq, k, d_acc, d_oid, d_od, d_oc, ctx.c, s, &fb);
+    PXG_HIP(hipMemcpyAsync(out_ids, d_oid, nq * k * 8, hipMemcpyDeviceToHost, s));
+    PXG_HIP(hipMemcpyAsync(out_dist, d_od, nq * k * 4, hipMemcpyDeviceToHost, s));
+    PXG_HIP(hipMemcpyAsync(out_count, d_oc, nq * 4, hipMemcpyDeviceToHost, s));
+    PXG_HIP(hipStreamSynchronize(s));
+    pxg::g_last_fallbacks = fb;
+  });
+}
+
+int pxg_flat_search_device(const pxg_flat* index, const float* d_queries, uint64_t nq, uint64_t k,
+                           const uint8_t* d_accept, uint64_t* d_out_ids, float* d_out_dist, uint32_t* d_out_count,
+                           void* stream) {
+  return pxg::guard([&] {
+    FlatIndex& f = const_cast<FlatIndex&>(index->impl);
+    std::shared_lock<std::shared_mutex> lk(f.mu);
+    pxg::CtxLease ctx(f.pool);
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    uint64_t fb = 0;
+    f.search_device(d_queries, true, nq, k, d_accept, d_out_ids, d_out_dist, d_out_count, ctx.c, s, &fb);
+    PXG_HIP(hipStreamSynchronize(s));
+    pxg::g_last_fallbacks = fb;
+  });
+}
+
+uint64_t pxg_flat_last_fallbacks(void) { return pxg::g_last_fallbacks; }
+
+int pxg_flat_set_search_mode(pxg_flat* index, int mode) {
+  return pxg::guard([&] {
+    if (mode < 0 || mode > 2) pxg::config_error("mode", (uint64_t)mode, "0 = auto, 1 = MFMA candidates, 2 = exact scan");
+    std::unique_lock<std::shared_mutex> lk(index->impl.mu);
+    index->impl.mode = mode;
+  });
+}
+
+}  // extern "C"

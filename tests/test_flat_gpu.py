@@ -1,0 +1,283 @@
+"""GPU FlatIndex: the reference's flat.rs tests, parity with the oracle (ids and
+distances bit-exact) on both device paths (MFMA candidates + exact rescoring,
+and the exact VALU scan), the BASELINE configs at parity-test sizes, the
+device-pointer entry point, and concurrent searches on one handle."""
+import threading
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+MODES = (1, 2)  # 1 = MFMA candidates + exact rescoring, 2 = exact scan
+
+
+def oracle_search(px, data, ids, metric, queries, k, accept=None, live=None, threads=8):
+    pd = orc.prepare_rows(metric, data)
+    pq = orc.prepare_rows(metric, queries)
+    return orc.flat_search(pd, ids, metric, pq, k, live=live, accept=accept, threads=threads)
+
+
+def assert_same(got, want):
+    gi, gd, gc = got
+    wi, wd, wc = want
+    assert np.array_equal(gc, wc), (gc, wc)
+    for q in range(gc.size):
+        c = int(gc[q])
+        assert np.array_equal(gi[q, :c], wi[q, :c]), (q, gi[q, :c], wi[q, :c])
+        # bit-exact distances (exact rescoring in the reference's arithmetic)
+        assert np.array_equal(gd[q, :c].view(np.uint32), wd[q, :c].view(np.uint32)), (q, gd[q, :c], wd[q, :c])
+
+
+def make_index(px, data, metric, ids=None, mode=0):
+    space = px.VectorSpace(data.shape[1], metric)
+    idx = px.FlatIndex(space, data.shape[0])
+    ids = np.arange(data.shape[0], dtype=np.uint64) if ids is None else ids
+    idx.insert_batch(ids, data)
+    idx.set_search_mode(mode)
+    return idx
+
+
+# --- flat.rs:253-419 -------------------------------------------------------------
+def test_round_trip(gpu):
+    px = gpu
+    idx = px.FlatIndex(px.VectorSpace(2, px.Metric.EUCLIDEAN))
+    idx.insert(1, [3.0, 4.0])
+    assert idx.contains(1)
+    assert list(idx.vector(1)) == [3.0, 4.0]
+    assert idx.search_all([3.0, 4.0], 1)[0].distance == 0.0
+    idx.remove(1)
+    assert not idx.contains(1) and idx.is_empty()
+
+
+def test_empty_k_zero_and_k_larger(gpu):
+    px = gpu
+    idx = px.FlatIndex(px.VectorSpace(3, px.Metric.EUCLIDEAN))
+    assert idx.search_all([1.0, 2.0, 3.0], 10) == []
+    idx1 = px.FlatIndex(px.VectorSpace(1, px.Metric.EUCLIDEAN))
+    for i in range(3):
+        idx1.insert(i, [float(i)])
+    assert len(idx1.search_all([0.0], 100)) == 3
+    assert idx1.search_all([0.0], 0) == []
+
+
+def test_identical_vectors_tie_break_on_id(gpu):
+    px = gpu
+    for mode in MODES:
+        idx = px.FlatIndex(px.VectorSpace(2, px.Metric.EUCLIDEAN))
+        idx.set_search_mode(mode)
+        for i in [9, 4, 7, 1]:
+            idx.insert(i, [1.0, 1.0])
+        assert [h.id for h in idx.search_all([1.0, 1.0], 3)] == [1, 4, 7]
+
+
+def test_duplicate_insert_and_upsert(gpu):
+    px = gpu
+    idx = px.FlatIndex(px.VectorSpace(1, px.Metric.EUCLIDEAN))
+    idx.insert(1, [0.0])
+    with pytest.raises(px.DuplicateId):
+        idx.insert(1, [1.0])
+    idx.upsert(1, [1.0])
+    assert list(idx.vector(1)) == [1.0] and len(idx) == 1
+    with pytest.raises(px.DuplicateId):
+        idx.insert_batch(np.array([5, 5], np.uint64), np.zeros((2, 1), np.float32))
+    assert len(idx) == 1  # all-or-nothing
+
+
+def test_cosine_normalised_on_the_way_in(gpu):
+    px = gpu
+    idx = px.FlatIndex(px.VectorSpace(2, px.Metric.COSINE))
+    idx.insert(1, [3.0, 4.0])
+    v = idx.vector(1)
+    assert abs(v[0] - 0.6) < 1e-6 and abs(v[1] - 0.8) < 1e-6
+    a = idx.search_all([30.0, 40.0], 1)[0].distance
+    b = idx.search_all([0.3, 0.4], 1)[0].distance
+    assert abs(a - b) < 1e-6
+
+
+def test_filter_runs_during_scan(gpu):
+    px = gpu
+    for mode in MODES:
+        idx = px.FlatIndex(px.VectorSpace(1, px.Metric.EUCLIDEAN))
+        idx.set_search_mode(mode)
+        for i in range(100):
+            idx.insert(i, [float(i)], {"keep": i % 10 == 0})
+        hits = idx.search([0.0], 5, lambda _id, m: m.get("keep") is True)
+        assert [h.id for h in hits] == [0, 10, 20, 30, 40]
+
+
+def test_dimension_mismatch_and_non_finite(gpu):
+    px = gpu
+    idx = px.FlatIndex(px.VectorSpace(3, px.Metric.EUCLIDEAN))
+    with pytest.raises(px.DimensionMismatch):
+        idx.insert(1, [1.0])
+    with pytest.raises(px.DimensionMismatch):
+        idx.search_all([1.0, 2.0], 1)
+    with pytest.raises(px.NonFinite) as e:
+        idx.insert(2, [1.0, float("nan"), 0.0])
+    assert e.value.index == 1
+    idx.insert(3, [1.0, 2.0, 3.0])
+    with pytest.raises(px.NonFinite):
+        idx.search_all([float("inf"), 0.0, 0.0], 1)
+
+
+def test_stats_and_slot_recycling(gpu):
+    px = gpu
+    idx = px.FlatIndex(px.VectorSpace(4, px.Metric.EUCLIDEAN))
+    for i in range(8):
+        idx.insert(i, [float(i)] * 4)
+    idx.remove(3)
+    st = idx.stats()
+    assert st.len == 7 and st.deleted == 0 and st.graph_bytes == 0 and st.layers == 1
+    assert st.vector_bytes >= 8 * 4 * 4
+    idx2 = px.FlatIndex(px.VectorSpace(2, px.Metric.EUCLIDEAN))
+    for i in range(4):
+        idx2.insert(i, [float(i)] * 2)
+    before = idx2.stats().vector_bytes
+    for rnd in range(200):
+        idx2.remove(rnd % 4)
+        idx2.insert(rnd % 4, [float(rnd)] * 2)
+    assert idx2.stats().vector_bytes == before
+    with pytest.raises(px.UnknownId):
+        idx2.remove(99)
+
+
+def test_from_array(gpu):
+    px = gpu
+    space = px.VectorSpace(2, px.Metric.EUCLIDEAN)
+    idx = px.FlatIndex.from_array(space, [0.0, 0.0, 1.0, 1.0, 2.0, 2.0])
+    assert len(idx) == 3 and idx.search_all([2.0, 2.0], 1)[0].id == 2
+    with pytest.raises(px.Configuration):
+        px.FlatIndex.from_array(space, [0.0, 0.0, 1.0])
+
+
+# --- parity with the oracle ---------------------------------------------------------
+@pytest.mark.parametrize("metric", [0, 1, 2, 3])
+@pytest.mark.parametrize("mode", MODES)
+def test_parity_random_shapes(gpu, metric, mode):
+    px = gpu
+    rng = np.random.default_rng(100 + metric * 7 + mode)
+    for (n, dim, nq, k) in [(1, 3, 1, 5), (37, 5, 3, 4), (300, 24, 17, 10), (1000, 131, 40, 33), (5000, 64, 130, 100),
+                            (2500, 8, 3, 256)]:
+        data = rng.standard_normal((n, dim)).astype(np.float32)
+        q = rng.standard_normal((nq, dim)).astype(np.float32)
+        ids = rng.permutation(n * 3)[:n].astype(np.uint64)
+        idx = make_index(px, data, metric, ids, mode)
+        assert_same(idx.search_batch(q, k), oracle_search(px, data, ids, metric, q, k))
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_parity_with_holes_ties_and_filter(gpu, mode):
+    px = gpu
+    rng = np.random.default_rng(7)
+    n, dim = 3000, 16
+    data = rng.integers(-3, 4, (n, dim)).astype(np.float32)  # many exact ties
+    ids = rng.permutation(n).astype(np.uint64)
+    idx = make_index(px, data, 0, ids, mode)
+    gone = rng.choice(n, 500, replace=False)
+    for i in gone:
+        idx.remove(int(ids[i]))
+    live = np.ones(n, np.uint8)
+    live[gone] = 0
+    q = rng.integers(-3, 4, (50, dim)).astype(np.float32)
+    assert_same(idx.search_batch(q, 20), oracle_search(px, data, ids, 0, q, 20, live=live))
+    keep = lambda i, _m: i % 3 == 0  # noqa: E731
+    acc = np.array([int(ids[s]) % 3 == 0 for s in range(n)], np.uint8)
+    assert_same(idx.search_batch(q, 20, keep), oracle_search(px, data, ids, 0, q, 20, live=live, accept=acc))
+    # reinsert into recycled slots (LIFO) and search again
+    new_ids = np.arange(10_000, 10_200, dtype=np.uint64)
+    new = rng.integers(-3, 4, (200, dim)).astype(np.float32)
+    slots = idx.insert_batch(new_ids, new)
+    data2, ids2, live2 = data.copy(), ids.copy(), live.copy()
+    for s, i, v in zip(slots, new_ids, new):
+        data2[s], ids2[s], live2[s] = v, i, 1
+    assert_same(idx.search_batch(q, 20), oracle_search(px, data2, ids2, 0, q, 20, live=live2))
+
+
+def _mixture(rng, n, dim, clusters, sigma, nq):
+    centres = rng.standard_normal((clusters, dim)).astype(np.float32)
+    data = centres[np.arange(n) % clusters] + sigma * rng.standard_normal((n, dim)).astype(np.float32)
+    qc = rng.integers(0, clusters, nq)
+    q = centres[qc] + sigma * rng.standard_normal((nq, dim)).astype(np.float32)
+    return data.astype(np.float32), q.astype(np.float32)
+
+
+def test_config1_l2_100k_x128_k10_full(gpu):
+    """FlatIndex exact search, Euclidean, k=10: 100k x 128, 100 clusters
+    sigma 0.15, 1000 queries in one batch; full parity with the oracle."""
+    px = gpu
+    rng = np.random.default_rng(0x9E3779B9)
+    data, q = _mixture(rng, 100_000, 128, 100, 0.15, 1000)
+    idx = make_index(px, data, px.Metric.EUCLIDEAN)
+    got = idx.search_batch(q, 10)
+    assert px.FlatIndex.last_fallbacks() == 0
+    assert_same(got, oracle_search(px, data, np.arange(100_000), 0, q, 10, threads=16))
+
+
+def test_config2_cosine_k100_subset(gpu):
+    """FlatIndex cosine, k=100 (and k=10): 768-d unit vectors from 256 offsets;
+    200k-row slice of the 1M corpus and 64 queries, full parity."""
+    px = gpu
+    rng = np.random.default_rng(2)
+    n, dim = 200_000, 768
+    offs = rng.standard_normal((256, dim)).astype(np.float32)
+    data = rng.standard_normal((n, dim)).astype(np.float32) + offs[np.arange(n) % 256]
+    q = rng.standard_normal((64, dim)).astype(np.float32) + offs[rng.integers(0, 256, 64)]
+    idx = make_index(px, data, px.Metric.COSINE)
+    for k in (100, 10):
+        got = idx.search_batch(q, k)
+        assert_same(got, oracle_search(px, data, np.arange(n), 1, q, k, threads=16))
+
+
+def test_device_entry_point_matches_host_path(gpu):
+    import torch
+    px = gpu
+    rng = np.random.default_rng(11)
+    data = rng.standard_normal((20_000, 96)).astype(np.float32)
+    q = (rng.standard_normal((300, 96)) * 3).astype(np.float32)
+    for metric in (0, 1, 2):
+        idx = make_index(px, data, metric)
+        hi, hd, hc = idx.search_batch(q, 10)
+        dq = torch.from_numpy(q).cuda()
+        oi = torch.zeros((300, 10), dtype=torch.int64, device="cuda")
+        od = torch.zeros((300, 10), dtype=torch.float32, device="cuda")
+        oc = torch.zeros(300, dtype=torch.int32, device="cuda")
+        idx.search_device(dq, 10, oi, od, oc)
+        torch.cuda.synchronize()
+        assert np.array_equal(oc.cpu().numpy().astype(np.uint32), hc)
+        assert np.array_equal(oi.cpu().numpy().view(np.uint64), hi)
+        assert np.array_equal(od.cpu().numpy().view(np.uint32), hd.view(np.uint32))
+    bad = torch.from_numpy(q).cuda()
+    bad[5, 7] = float("nan")
+    with pytest.raises(px.NonFinite):
+        idx.search_device(bad, 10, oi, od, oc)
+
+
+def test_concurrent_searches_on_one_handle(gpu):
+    px = gpu
+    rng = np.random.default_rng(12)
+    data = rng.standard_normal((30_000, 64)).astype(np.float32)
+    idx = make_index(px, data, 0)
+    qs = [rng.standard_normal((64, 64)).astype(np.float32) for _ in range(8)]
+    want = [idx.search_batch(q, 10) for q in qs]
+    got = [None] * 8
+    errs = []
+
+    def run(i):
+        try:
+            for _ in range(3):
+                got[i] = idx.search_batch(qs[i], 10)
+        except Exception as e:  # pragma: no cover
+            errs.append(e)
+
+    th = [threading.Thread(target=run, args=(i,)) for i in range(8)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    assert not errs
+    for g, w in zip(got, want):
+        for a, b in zip(g, w):
+            assert np.array_equal(a, b)
