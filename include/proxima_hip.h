@@ -78,6 +78,20 @@ const char* pxg_version(void);
 /* Number of visible devices (0 when none); never fails. */
 int pxg_device_count(void);
 
+/* Device timings of the last search/train call on the calling thread, in
+ * milliseconds, measured with hipEvents on the stream the kernels ran on.
+ * Recorded only while profiling is enabled (it adds event records, no
+ * extra synchronisation). No reference counterpart: measurement hook. */
+typedef struct pxg_timings {
+  float prep_ms;       /* query validation / preparation */
+  float candidates_ms; /* dominant kernel: MFMA candidate GEMM, ADC scan, ... */
+  float merge_ms;      /* merge, exact rescoring, final ordering */
+  float fallback_ms;   /* exact rescans of unproven queries (0 if none) */
+  float total_ms;      /* first to last recorded event */
+} pxg_timings;
+void pxg_set_profiling(int enabled);
+int pxg_last_timings(pxg_timings* out);
+
 /* ------------------------------------------------------------------------ */
 /* Flat (exact) index: replaces FlatIndex, crates/proxima-index/src/flat.rs:68-236. */
 typedef struct pxg_flat pxg_flat;
@@ -89,6 +103,11 @@ void pxg_flat_destroy(pxg_flat* index);
  * nothing is inserted if any vector is non-finite or any id is a duplicate
  * (of a live id or of another id in the batch). out_slots may be NULL. */
 int pxg_flat_insert(pxg_flat* index, const uint64_t* ids, const float* vectors, uint64_t n, uint32_t* out_slots);
+/* Same, with the vectors already in device memory (row-major n x dim); ids
+ * and out_slots stay on the host. Validation and preparation run on the
+ * device with the same arithmetic; still all-or-nothing. */
+int pxg_flat_insert_device(pxg_flat* index, const uint64_t* ids, const float* d_vectors, uint64_t n,
+                           uint32_t* out_slots);
 /* VectorIndex::remove (flat.rs:145-151): frees the slot for LIFO reuse. */
 int pxg_flat_remove(pxg_flat* index, uint64_t id);
 /* VectorIndex::contains / len / stats (flat.rs:171-193). */

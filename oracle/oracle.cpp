@@ -607,6 +607,30 @@ long long orc_prepare(int metric, const float* in, size_t n, float* out) {
   return -1;
 }
 
+// prepare() over n rows with `threads` host threads. Returns -1, or the
+// first row holding a non-finite component.
+long long orc_prepare_batch(int metric, const float* in, size_t n, size_t dim, float* out, int threads) {
+  std::vector<long long> bad(std::max(threads, 1), -1);
+  auto work = [&](int t, size_t a, size_t b) {
+    for (size_t i = a; i < b; ++i) {
+      long long r = orc_prepare(metric, in + i * dim, dim, out + i * dim);
+      if (r >= 0 && bad[t] < 0) bad[t] = (long long)i;
+    }
+  };
+  threads = std::max(threads, 1);
+  std::vector<std::thread> pool;
+  size_t per = (n + threads - 1) / threads;
+  for (int t = 0; t < threads; ++t) {
+    size_t a = t * per, b = std::min(n, a + per);
+    if (a >= b) break;
+    pool.emplace_back(work, t, a, b);
+  }
+  for (auto& th : pool) th.join();
+  for (long long b : bad)
+    if (b >= 0) return b;
+  return -1;
+}
+
 // Push (ids[i], d[i]) in order through a TopK(k); write into_sorted_vec.
 size_t orc_topk(const uint64_t* ids, const float* d, size_t n, size_t k, uint64_t* out_ids, float* out_d) {
   TopK top(k);

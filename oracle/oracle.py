@@ -48,6 +48,7 @@ def _load():
         "orc_normalize_in_place": (C.c_float, [_f32p, _sz]),
         "orc_prepare": (C.c_longlong, [C.c_int, _f32p, _sz, _f32p]),
         "orc_topk": (_sz, [_u64p, _f32p, _sz, _sz, _u64p, _f32p]),
+        "orc_prepare_batch": (C.c_longlong, [C.c_int, _f32p, _sz, _sz, _f32p, C.c_int]),
         "orc_flat_search": (None, [_f32p, _u8p, _u64p, _sz, _sz, C.c_int, _f32p, _sz, _sz, C.c_void_p,
                                    C.c_int, _u64p, _f32p, _u32p]),
         "orc_sq_train": (C.c_longlong, [_f32p, _sz, _sz, C.c_int, _f32p, _f32p, _f32p]),
@@ -163,13 +164,12 @@ def prepare(metric, v):
     return out, bad
 
 
-def prepare_rows(metric, x):
+def prepare_rows(metric, x, threads=8):
     x = f32(x)
+    n, dim = x.shape
     out = np.empty_like(x)
-    for i in range(x.shape[0]):
-        o, bad = prepare(metric, x[i])
-        assert bad < 0
-        out[i] = o
+    bad = lib.orc_prepare_batch(metric, x, n, dim, out, threads)
+    assert bad < 0, f"row {bad} is not finite"
     return out
 
 

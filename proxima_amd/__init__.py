@@ -13,12 +13,26 @@ from collections import namedtuple
 import numpy as np
 
 from ._capi import IndexStats as _IndexStatsC
+from ._capi import Timings as _TimingsC
 from ._capi import lib as _lib
 
 __all__ = [
     "Metric", "VectorSpace", "SearchResult", "IndexStats", "ProximaError", "DimensionMismatch", "UnknownId",
     "DuplicateId", "Capacity", "NonFinite", "Corruption", "Configuration", "Internal", "FlatIndex", "check_k",
+    "set_profiling", "last_timings",
 ]
+
+
+def set_profiling(enabled):
+    """Record per-stage device timings (hipEvents) for subsequent calls."""
+    _lib.pxg_set_profiling(1 if enabled else 0)
+
+
+def last_timings():
+    """Stage timings (ms) of the last search/train on this thread."""
+    t = _TimingsC()
+    _lib.pxg_last_timings(C.byref(t))
+    return {f: getattr(t, f) for f, _ in t._fields_}
 
 
 # --- Metric: distance.rs:90-118 ----------------------------------------------------
@@ -312,6 +326,16 @@ class FlatIndex(_IndexBase):
             raise ValueError("ids and vectors disagree on the batch size")
         slots = np.zeros(ids.size, np.uint32)
         _check(_lib.pxg_flat_insert(self._h, _ptr(ids), _ptr(v), ids.size, _ptr(slots)))
+        return slots
+
+    def insert_device(self, ids, vectors):
+        """Bulk insert from a contiguous GPU tensor [n, dim] (ids on the host)."""
+        ids = np.ascontiguousarray(ids, dtype=np.uint64).reshape(-1)
+        if vectors.shape[-1] != self.space.dim or vectors.shape[0] != ids.size:
+            raise DimensionMismatch("dimension mismatch: device batch does not match the index", self.space.dim,
+                                    vectors.shape[-1])
+        slots = np.zeros(ids.size, np.uint32)
+        _check(_lib.pxg_flat_insert_device(self._h, _ptr(ids), _device_ptr(vectors), ids.size, _ptr(slots)))
         return slots
 
     def remove(self, id):

@@ -31,6 +31,16 @@ class IndexStats(C.Structure):
     ]
 
 
+class Timings(C.Structure):
+    _fields_ = [
+        ("prep_ms", _f32),
+        ("candidates_ms", _f32),
+        ("merge_ms", _f32),
+        ("fallback_ms", _f32),
+        ("total_ms", _f32),
+    ]
+
+
 class IvfPqConfigC(C.Structure):
     _fields_ = [
         ("nlist", _u64),
@@ -62,10 +72,13 @@ SIGNATURES = {
     "pxg_last_error_detail": (_i32, [_P(_u64), _P(_u64), _P(_f32)]),
     "pxg_version": (C.c_char_p, []),
     "pxg_device_count": (_i32, []),
+    "pxg_set_profiling": (None, [_i32]),
+    "pxg_last_timings": (_i32, [_P(Timings)]),
     # flat
     "pxg_flat_create": (_i32, [_u32, _i32, _u64, _P(_vp)]),
     "pxg_flat_destroy": (None, [_vp]),
     "pxg_flat_insert": (_i32, [_vp, _vp, _vp, _u64, _vp]),
+    "pxg_flat_insert_device": (_i32, [_vp, _vp, _vp, _u64, _vp]),
     "pxg_flat_remove": (_i32, [_vp, _u64]),
     "pxg_flat_contains": (_i32, [_vp, _u64]),
     "pxg_flat_len": (_u64, [_vp]),

@@ -1,4 +1,5 @@
 // Error plumbing and host-side preparation shared by every index.
+#include <atomic>
 #include <cmath>
 
 #include "common.hpp"
@@ -8,6 +9,11 @@ namespace pxg {
 namespace {
 thread_local Error g_last{PXG_OK, ""};
 }
+
+std::atomic<int> g_profiling{0};
+thread_local pxg_timings g_timings{0, 0, 0, 0, 0};
+bool profiling_enabled() { return g_profiling.load(std::memory_order_relaxed) != 0; }
+void set_last_timings(const pxg_timings& t) { g_timings = t; }
 
 void set_last_error(const Error& e) { g_last = e; }
 void clear_last_error() { g_last = Error{PXG_OK, ""}; }
@@ -58,6 +64,13 @@ int pxg_last_error_detail(uint64_t* a, uint64_t* b, float* value) {
 }
 
 const char* pxg_version(void) { return "proxima-hip 0.1.0 (gfx950)"; }
+
+void pxg_set_profiling(int enabled) { pxg::g_profiling.store(enabled ? 1 : 0); }
+
+int pxg_last_timings(pxg_timings* out) {
+  if (out) *out = pxg::g_timings;
+  return PXG_OK;
+}
 
 int pxg_device_count(void) {
   int n = 0;

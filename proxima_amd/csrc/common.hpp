@@ -198,4 +198,42 @@ float host_dot_unrolled(const float* a, const float* b, uint32_t n);
 
 void check_k(uint64_t k);  // index.rs:212-224
 
+// Stage timings (pxg_set_profiling / pxg_last_timings). A Timer records
+// hipEvents on one stream; read() runs after the stream has synchronised.
+bool profiling_enabled();
+void set_last_timings(const pxg_timings& t);
+
+struct Timer {
+  bool on;
+  hipStream_t s;
+  hipEvent_t ev[8] = {};
+  int n = 0;
+  int stage_of[8] = {};
+  Timer(hipStream_t stream) : on(profiling_enabled()), s(stream) {}
+  // mark the start of `stage` (0 prep, 1 candidates, 2 merge, 3 fallback, 4 end)
+  void mark(int stage) {
+    if (!on || n >= 8) return;
+    if (hipEventCreate(&ev[n]) != hipSuccess) { on = false; return; }
+    (void)hipEventRecord(ev[n], s);
+    stage_of[n++] = stage;
+  }
+  void finish() {
+    if (!on) return;
+    mark(4);
+    (void)hipEventSynchronize(ev[n - 1]);
+    pxg_timings t{0, 0, 0, 0, 0};
+    float* slot[4] = {&t.prep_ms, &t.candidates_ms, &t.merge_ms, &t.fallback_ms};
+    for (int i = 0; i + 1 < n; ++i) {
+      float ms = 0;
+      (void)hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
+      if (stage_of[i] < 4) *slot[stage_of[i]] += ms;
+    }
+    (void)hipEventElapsedTime(&t.total_ms, ev[0], ev[n - 1]);
+    set_last_timings(t);
+  }
+  ~Timer() {
+    for (int i = 0; i < n; ++i) (void)hipEventDestroy(ev[i]);
+  }
+};
+
 }  // namespace pxg

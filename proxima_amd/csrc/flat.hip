@@ -637,6 +637,8 @@ struct FlatIndex {
       config_error("k", k, "the GPU flat search supports k up to 1024 per query");
     rebuild_ranks(s);
 
+    Timer tm(s);
+    tm.mark(0);
     // 1. prepare queries
     float* Qp = (float*)ctx->get(1, nq * ld * 4);
     float* qb = (float*)ctx->get(2, nq * 4);
@@ -665,6 +667,7 @@ struct FlatIndex {
       S = (int)((N + per_split - 1) / per_split);
       uint64_t* cand = (uint64_t*)ctx->get(6, (size_t)nq * S * CAP * 8);
       const int total = QB * S;
+      tm.mark(1);
       const int grid = ((total + 7) / 8) * 8;
       const float scale = metric == PXG_EUCLIDEAN ? 2.0f : 1.0f;
       if (CAP == 256)
@@ -674,6 +677,7 @@ struct FlatIndex {
         hipLaunchKernelGGL(flat_mfma_candidates<512>, dim3(grid), dim3(256), 0, s, Qp, (int)nq, X.p, (int)N, (int)ld,
                            qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, Kp, cand);
       PXG_HIP(hipGetLastError());
+      tm.mark(2);
       hipLaunchKernelGGL(flat_merge_rescore, dim3((unsigned)nq), dim3(256), 0, s, cand, S, CAP, Kp, (int)k, Qp,
                          (int)ld, (int)dim, metric, X.p, d_rank.p, d_rank_slot.p, d_ids.p, qn, maxnorm, 4.0f, d_oid,
                          d_od, d_oc, flag_list, flag_count);
@@ -700,15 +704,94 @@ struct FlatIndex {
       const int kk = (int)std::min<uint64_t>(k, EXACT_CH);
       uint64_t* ecand = (uint64_t*)ctx->get(7, (size_t)nflag * nchunks * kk * 8);
       const int grid = std::min(nflag * nchunks, 4096);
+      tm.mark(exact_all ? 1 : 3);
       hipLaunchKernelGGL(flat_exact_candidates, dim3(grid), dim3(256), 0, s, flag_list, flag_count, nchunks, Qp,
                          (int)ld, (int)dim, metric, X.p, (int)N, d_live.p, d_accept, d_rank.p, (int)k, ecand);
       PXG_HIP(hipGetLastError());
+      if (exact_all) tm.mark(2);
       hipLaunchKernelGGL(flat_merge_exact, dim3((unsigned)nflag), dim3(256), 0, s, flag_list, flag_count, ecand,
                          nchunks, (int)k, d_rank_slot.p, d_ids.p, d_oid, d_od, d_oc);
       PXG_HIP(hipGetLastError());
       PXG_HIP(hipStreamSynchronize(s));
       *fallbacks = exact_all ? 0 : (uint64_t)nflag;
     }
+    tm.finish();
+  }
+
+  // Insert from device memory: validate + prepare on the device, then the
+  // same slot allocation and scatter as insert().
+  void insert_device(const uint64_t* in_ids, const float* d_vecs, uint64_t n, uint32_t* out_slots) {
+    {
+      std::unordered_map<uint64_t, int> seen;
+      for (uint64_t i = 0; i < n; ++i)
+        if (by_id.count(in_ids[i]) || !seen.emplace(in_ids[i], 1).second)
+          raise(PXG_ERR_DUPLICATE_ID, "duplicate vector id " + std::to_string(in_ids[i]), in_ids[i]);
+    }
+    if (by_id.size() + n > (size_t)UINT32_MAX - 1)
+      raise(PXG_ERR_CAPACITY, "capacity exceeded: slot allocator limit is 4294967295", UINT32_MAX);
+    const size_t rows_per = std::max<size_t>(1, (256u << 20) / ((size_t)ld * 4));
+    const size_t chunk = std::min<size_t>(rows_per, n);
+    DevBuf<float> st_rows(chunk * ld);
+    DevBuf<float> st_b(chunk), st_n(chunk);
+    DevBuf<unsigned long long> bad(1);
+    // pass 1: validate every row before touching any state (all-or-nothing)
+    std::vector<float> norms(n);
+    for (size_t a = 0; a < n; a += chunk) {
+      const size_t m = std::min<size_t>(chunk, n - a);
+      PXG_HIP(hipMemsetAsync(bad.p, 0xFF, 8, stream));
+      hipLaunchKernelGGL(flat_prep_queries, dim3((unsigned)m), dim3(64), 0, stream, d_vecs + a * dim, (int)dim,
+                         (int)ld, metric, 1, st_rows.p, st_b.p, st_n.p, bad.p);
+      PXG_HIP(hipGetLastError());
+      unsigned long long bv = 0;
+      PXG_HIP(hipMemcpyAsync(&bv, bad.p, 8, hipMemcpyDeviceToHost, stream));
+      PXG_HIP(hipMemcpyAsync(norms.data() + a, st_n.p, m * 4, hipMemcpyDeviceToHost, stream));
+      PXG_HIP(hipStreamSynchronize(stream));
+      if (bv != ~0ull) {
+        const uint64_t row = a + (bv >> 32), comp = (uint32_t)bv;
+        raise(PXG_ERR_NON_FINITE, "vector component " + std::to_string(comp) + " is not finite (vector " +
+                                      std::to_string(row) + ")",
+              comp, row, NAN);
+      }
+    }
+    float newmax = maxnorm;
+    for (float nr : norms)
+      if (!(nr <= newmax)) newmax = std::isnan(nr) ? INFINITY : nr;
+    std::vector<uint32_t> sl(n);
+    for (uint64_t i = 0; i < n; ++i) sl[i] = slots.allocate();
+    const size_t hw = slots.high_water();
+    ensure_capacity(hw);
+    if (ids.size() < hw) {
+      ids.resize(hw, 0);
+      live.resize(hw, 0);
+    }
+    for (uint64_t i = 0; i < n; ++i) {
+      ids[sl[i]] = in_ids[i];
+      live[sl[i]] = 1;
+      by_id[in_ids[i]] = sl[i];
+      if (out_slots) out_slots[i] = sl[i];
+    }
+    maxnorm = newmax;
+    DevBuf<uint32_t> st_slots(chunk);
+    DevBuf<uint64_t> st_ids(chunk);
+    DevBuf<float> st_bias(chunk);
+    for (size_t a = 0; a < n; a += chunk) {
+      const size_t m = std::min<size_t>(chunk, n - a);
+      hipLaunchKernelGGL(flat_prep_queries, dim3((unsigned)m), dim3(64), 0, stream, d_vecs + a * dim, (int)dim,
+                         (int)ld, metric, 1, st_rows.p, st_b.p, st_n.p, bad.p);
+      PXG_HIP(hipGetLastError());
+      // bias: |x|^2 for Euclidean (st_b holds it), 0 otherwise
+      if (metric == PXG_EUCLIDEAN)
+        PXG_HIP(hipMemcpyAsync(st_bias.p, st_b.p, m * 4, hipMemcpyDeviceToDevice, stream));
+      else
+        PXG_HIP(hipMemsetAsync(st_bias.p, 0, m * 4, stream));
+      PXG_HIP(hipMemcpyAsync(st_slots.p, sl.data() + a, m * 4, hipMemcpyHostToDevice, stream));
+      PXG_HIP(hipMemcpyAsync(st_ids.p, in_ids + a, m * 8, hipMemcpyHostToDevice, stream));
+      hipLaunchKernelGGL(flat_scatter_rows, dim3((unsigned)m), dim3(256), 0, stream, st_rows.p, st_slots.p,
+                         st_bias.p, st_ids.p, (int)m, (int)ld, X.p, xb.p, d_live.p, d_ids.p);
+      PXG_HIP(hipGetLastError());
+      PXG_HIP(hipStreamSynchronize(stream));
+    }
+    rank_dirty = true;
   }
 };
 
@@ -753,6 +836,15 @@ int pxg_flat_insert(pxg_flat* index, const uint64_t* ids, const float* vectors, 
     if (n == 0) return;
     std::unique_lock<std::shared_mutex> lk(index->impl.mu);
     index->impl.insert(ids, vectors, n, out_slots);
+  });
+}
+
+int pxg_flat_insert_device(pxg_flat* index, const uint64_t* ids, const float* d_vectors, uint64_t n,
+                           uint32_t* out_slots) {
+  return pxg::guard([&] {
+    if (n == 0) return;
+    std::unique_lock<std::shared_mutex> lk(index->impl.mu);
+    index->impl.insert_device(ids, d_vectors, n, out_slots);
   });
 }
 

@@ -281,3 +281,24 @@ def test_concurrent_searches_on_one_handle(gpu):
     for g, w in zip(got, want):
         for a, b in zip(g, w):
             assert np.array_equal(a, b)
+
+
+def test_insert_device_matches_host_insert(gpu):
+    import torch
+    px = gpu
+    rng = np.random.default_rng(13)
+    data = (rng.standard_normal((5000, 77)) * 4).astype(np.float32)
+    for metric in (0, 1, 2):
+        a = make_index(px, data, metric)
+        b = px.FlatIndex(px.VectorSpace(77, metric))
+        b.insert_device(np.arange(5000, dtype=np.uint64), torch.from_numpy(data).cuda())
+        for i in (0, 17, 4999):
+            assert np.array_equal(a.vector(i).view(np.uint32), b.vector(i).view(np.uint32))
+        q = rng.standard_normal((40, 77)).astype(np.float32)
+        for x, y in zip(a.search_batch(q, 12), b.search_batch(q, 12)):
+            assert np.array_equal(x, y)
+    bad = torch.from_numpy(data[:10].copy()).cuda()
+    bad[3, 5] = float("inf")
+    with pytest.raises(px.NonFinite):
+        b.insert_device(np.arange(100_000, 100_010, dtype=np.uint64), bad)
+    assert len(b) == 5000
