@@ -1,0 +1,189 @@
+// Kernels shared by every index: query/vector preparation on the device, the
+// exact VALU scan (the reference's 8-lane arithmetic, exact (distance, id)
+// ordering) used for Manhattan, small problems, unproven MFMA queries and
+// untrained IVF-PQ indexes, and a shared-memory bitonic sort. Kernels are
+// `static` so each translation unit that includes this header owns a copy.
+#pragma once
+
+#include "device.hpp"
+
+namespace pxg {
+
+constexpr int EXACT_CH = 1024;
+
+// ---------------------------------------------------------------------------
+// 1. query preparation
+// ---------------------------------------------------------------------------
+static __global__ __launch_bounds__(64) void flat_prep_queries(const float* __restrict__ raw, int dim, int ld, int metric,
+                                                        int do_prepare, float* __restrict__ Qp,
+                                                        float* __restrict__ qb, float* __restrict__ qn,
+                                                        unsigned long long* __restrict__ bad) {
+  const int q = blockIdx.x;
+  const int lane = threadIdx.x;
+  const float* v = raw + (size_t)q * dim;
+  float* out = Qp + (size_t)q * ld;
+  __shared__ float s_inv;
+  // validate: first non-finite component (space.rs:104-121)
+  for (int i = lane; i < dim; i += 64) {
+    if (!isfinite(v[i])) atomicMin(bad, ((unsigned long long)q << 32) | (unsigned)i);
+  }
+  if (lane < 8) {
+    float d = dist_group8<2>(v, v, dim, lane);  // = -dot_unrolled(v, v)
+    if (lane == 0) {
+      float dot = -d;
+      float inv = 1.0f;
+      if (do_prepare && metric == 1) {
+        float n = sqrtf(dot);
+        inv = (n > 0.0f && isfinite(n)) ? 1.0f / n : 1.0f;
+        s_inv = (n > 0.0f && isfinite(n)) ? inv : 0.0f;  // 0 marks "leave untouched"
+      } else {
+        s_inv = 0.0f;
+      }
+    }
+  }
+  __syncthreads();
+  const float inv = s_inv;
+  for (int i = lane; i < ld; i += 64) {
+    float x = i < dim ? v[i] : 0.0f;
+    if (inv != 0.0f) x = x * inv;
+    out[i] = x;
+  }
+  __syncthreads();
+  if (lane < 8) {
+    float d = -dist_group8<2>(out, out, dim, lane);
+    if (lane == 0) {
+      qn[q] = sqrtf(d);
+      qb[q] = metric == 0 ? d : (metric == 1 ? 1.0f : 0.0f);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// shared-memory bitonic sort (ascending) of n = power-of-two keys
+// ---------------------------------------------------------------------------
+__device__ inline void block_bitonic_sort(uint64_t* keys, int n) {
+  for (int size = 2; size <= n; size <<= 1) {
+    for (int j = size >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < (n >> 1); i += blockDim.x) {
+        const int idx = ((i / j) * 2 * j) + (i % j);
+        const bool asc = (idx & size) == 0;
+        const uint64_t a = keys[idx], b = keys[idx + j];
+        if ((a > b) == asc) {
+          keys[idx] = b;
+          keys[idx + j] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 4. exact VALU scan for a list of queries
+// ---------------------------------------------------------------------------
+static __global__ __launch_bounds__(256) void flat_exact_candidates(
+    const int* __restrict__ qlist, const int* __restrict__ qcount, int nchunks, const float* __restrict__ Qp, int ld,
+    int dim, int metric, const float* __restrict__ X, int N, const uint8_t* __restrict__ live,
+    const uint8_t* __restrict__ accept, const uint32_t* __restrict__ rank, int k, uint64_t* __restrict__ ecand) {
+  __shared__ uint64_t keys[EXACT_CH];
+  const int total = (*qcount) * nchunks;
+  const int g = threadIdx.x & 7, grp = threadIdx.x >> 3;
+  const int kk = min(k, EXACT_CH);
+  for (int w = blockIdx.x; w < total; w += gridDim.x) {
+    const int f = w / nchunks, c = w % nchunks;
+    const int q = qlist[f];
+    const float* qv = Qp + (size_t)q * ld;
+    const int base = c * EXACT_CH;
+    for (int s = grp; s < EXACT_CH; s += 32) {
+      const int slot = base + s;
+      uint64_t key = KEY_MAX;
+      if (slot < N && live[slot] && (accept == nullptr || accept[slot])) {
+        const float d = dist_group8_rt(metric, qv, X + (size_t)slot * ld, dim, g);
+        key = ((uint64_t)ord_key(d) << 32) | rank[slot];
+      }
+      if (g == 0) keys[s] = key;
+    }
+    __syncthreads();
+    block_bitonic_sort(keys, EXACT_CH);
+    uint64_t* out = ecand + ((size_t)f * nchunks + c) * kk;
+    for (int i = threadIdx.x; i < kk; i += blockDim.x) out[i] = keys[i];
+    __syncthreads();
+  }
+}
+
+constexpr int EXACT_MERGE_MAXK = 1024;
+
+static __global__ __launch_bounds__(256) void flat_merge_exact(const int* __restrict__ qlist, const int* __restrict__ qcount,
+                                                        const uint64_t* __restrict__ ecand, int nchunks, int k,
+                                                        const uint32_t* __restrict__ rank_slot,
+                                                        const uint64_t* __restrict__ ids,
+                                                        uint64_t* __restrict__ out_ids, float* __restrict__ out_d,
+                                                        uint32_t* __restrict__ out_count) {
+  const int f = blockIdx.x;
+  if (f >= *qcount) return;
+  const int q = qlist[f];
+  __shared__ int hist[256];
+  __shared__ uint64_t sh[4];
+  __shared__ uint64_t sel[EXACT_MERGE_MAXK];
+  __shared__ int n_sel, n_valid;
+  const int kk = min(k, EXACT_CH);
+  const uint64_t* base = ecand + (size_t)f * nchunks * kk;
+  const int n = nchunks * kk;
+  auto get = [&](int i) -> uint64_t { return base[i]; };
+  if (threadIdx.x == 0) {
+    n_sel = 0;
+    n_valid = 0;
+  }
+  __syncthreads();
+  int local = 0;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) local += base[i] != KEY_MAX;
+  atomicAdd(&n_valid, local);
+  __syncthreads();
+  const int ksel = min(k, n_valid);
+  if (ksel == 0) {
+    if (threadIdx.x == 0) out_count[q] = 0;
+    return;
+  }
+  const uint64_t pivot = block_radix_select(get, n, ksel, hist, sh);
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const uint64_t x = base[i];
+    if (x <= pivot && x != KEY_MAX) sel[atomicAdd(&n_sel, 1)] = x;
+  }
+  __syncthreads();
+  int P = 1;
+  while (P < ksel) P <<= 1;
+  for (int i = ksel + threadIdx.x; i < P; i += blockDim.x) sel[i] = KEY_MAX;
+  __syncthreads();
+  block_bitonic_sort(sel, P);
+  for (int i = threadIdx.x; i < ksel; i += blockDim.x) {
+    const uint64_t key = sel[i];
+    out_ids[(size_t)q * k + i] = ids[rank_slot[(uint32_t)key]];
+    out_d[(size_t)q * k + i] = key_float((uint32_t)(key >> 32));
+  }
+  if (threadIdx.x == 0) out_count[q] = ksel;
+}
+
+static __global__ void iota_kernel(int* a, int n, int* count) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) a[i] = i;
+  if (i == 0) *count = n;
+}
+
+// Scatter staged rows into their slots (insert path).
+static __global__ void flat_scatter_rows(const float* __restrict__ staged, const uint32_t* __restrict__ slots,
+                                  const float* __restrict__ bias, const uint64_t* __restrict__ sid, int n, int ld,
+                                  float* __restrict__ X, float* __restrict__ xb, uint8_t* __restrict__ live,
+                                  uint64_t* __restrict__ ids) {
+  const int i = blockIdx.x;
+  if (i >= n) return;
+  const uint32_t s = slots[i];
+  for (int c = threadIdx.x; c < ld; c += blockDim.x) X[(size_t)s * ld + c] = staged[(size_t)i * ld + c];
+  if (threadIdx.x == 0) {
+    xb[s] = bias[i];
+    live[s] = 1;
+    ids[s] = sid[i];
+  }
+}
+
+
+}  // namespace pxg
