@@ -141,6 +141,109 @@ uint64_t pxg_flat_last_fallbacks(void);
  * and k allow it, 2 = exact VALU scan only. Results are identical. */
 int pxg_flat_set_search_mode(pxg_flat* index, int mode);
 
+/* ------------------------------------------------------------------------ */
+/* IVF-PQ: replaces IvfPqIndex, crates/proxima-index/src/ivfpq.rs:452-1228.  */
+typedef struct pxg_ivfpq pxg_ivfpq;
+
+/* IvfPqConfig (ivfpq.rs:106-304). */
+typedef struct pxg_ivfpq_config {
+  uint64_t nlist;
+  uint64_t subspaces;
+  uint64_t nprobe;
+  uint64_t rerank;
+  uint64_t seed;
+  uint64_t max_iterations;
+  uint64_t training_sample;
+  uint64_t train_threshold;
+  int32_t retain_vectors;
+} pxg_ivfpq_config;
+
+/* TrainingReport (ivfpq.rs:322-357). */
+typedef struct pxg_training_report {
+  uint64_t sampled;
+  double coarse_inertia;
+  uint64_t coarse_iterations;
+  double residual_inertia;
+  uint64_t populated_lists;
+  uint64_t largest_list;
+} pxg_training_report;
+
+/* IvfPqConfig::new (ivfpq.rs:124-150): nprobe nlist/16, seed 0x1FF9C0D, 25
+ * iterations, 100000-vector sample, threshold nlist*100, vectors retained. */
+int pxg_ivfpq_config_default(uint64_t nlist, uint64_t subspaces, pxg_ivfpq_config* out);
+/* IvfPqIndex::new (ivfpq.rs:481-509): Euclidean or Cosine only; config validated
+ * (ivfpq.rs:259-304). The GPU distance table holds at most 128 subspaces. */
+int pxg_ivfpq_create(uint32_t dim, int metric, const pxg_ivfpq_config* config, pxg_ivfpq** out);
+void pxg_ivfpq_destroy(pxg_ivfpq* index);
+/* VectorIndex::insert (ivfpq.rs:1129-1158), batched and all-or-nothing per
+ * validation; encodes when trained, auto-trains when the live count reaches
+ * train_threshold (splitting the batch at that insert). */
+int pxg_ivfpq_insert(pxg_ivfpq* index, const uint64_t* ids, const float* vectors, uint64_t n, uint32_t* out_slots);
+/* VectorIndex::remove (ivfpq.rs:1160-1180). */
+int pxg_ivfpq_remove(pxg_ivfpq* index, uint64_t id);
+int pxg_ivfpq_contains(const pxg_ivfpq* index, uint64_t id);
+uint64_t pxg_ivfpq_len(const pxg_ivfpq* index);
+int pxg_ivfpq_is_trained(const pxg_ivfpq* index);
+/* VectorIndex::stats (ivfpq.rs:1194-1214): graph_bytes = codes, lists, codebooks. */
+int pxg_ivfpq_stats(const pxg_ivfpq* index, pxg_index_stats* out);
+/* IvfPqIndex::vector (ivfpq.rs:544-552). */
+int pxg_ivfpq_get_vector(const pxg_ivfpq* index, uint64_t id, float* out);
+uint64_t pxg_ivfpq_slot_count(const pxg_ivfpq* index);
+int pxg_ivfpq_slots(const pxg_ivfpq* index, uint64_t* ids, uint8_t* live);
+/* IvfPqIndex::list_lengths (ivfpq.rs:567-569): list_count() entries. */
+uint64_t pxg_ivfpq_list_count(const pxg_ivfpq* index);
+int pxg_ivfpq_list_lengths(const pxg_ivfpq* index, uint64_t* out);
+/* IvfPqIndex::train (ivfpq.rs:735-825) on the GPU: stride sample, k-means with
+ * k-means++ (ChaCha8Rng(seed)), residual PQ training with a fresh generator
+ * from the same seed, encode every live vector. report may be NULL. */
+int pxg_ivfpq_train(pxg_ivfpq* index, pxg_training_report* report);
+int pxg_ivfpq_training_report(const pxg_ivfpq* index, pxg_training_report* report);
+/* IvfPqIndex::parts (ivfpq.rs:606-617): list_count() x dim centroids, the
+ * codebooks (sum over subspaces of 256 x width floats), slot_count() x M
+ * codes and slot_count() list assignments (UINT32_MAX when none). Any may be NULL. */
+int pxg_ivfpq_parts(const pxg_ivfpq* index, float* centroids, float* codebooks, uint8_t* codes, uint32_t* list_of);
+/* IvfPqIndex::from_parts (ivfpq.rs:624-717) for the trained state of an index
+ * whose vectors are already inserted: `produced` centroids, codebooks, and
+ * codes/list_of per slot (codes NULL = encode the live vectors on the GPU). */
+int pxg_ivfpq_load_trained(pxg_ivfpq* index, const float* centroids, uint64_t produced, const float* codebooks,
+                           const uint8_t* codes, const uint32_t* list_of);
+/* IvfPqIndex::search_with_nprobe (ivfpq.rs:981-996); nprobe 0 = the configured one. */
+int pxg_ivfpq_search(const pxg_ivfpq* index, const float* queries, uint64_t nq, uint64_t k, uint64_t nprobe,
+                     const uint8_t* accept, uint64_t* out_ids, float* out_dist, uint32_t* out_count);
+int pxg_ivfpq_search_device(const pxg_ivfpq* index, const float* d_queries, uint64_t nq, uint64_t k, uint64_t nprobe,
+                            const uint8_t* d_accept, uint64_t* d_out_ids, float* d_out_dist, uint32_t* d_out_count,
+                            void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* k-means and the product quantizer (crates/proxima-quantize).              */
+
+/* kmeans() (kmeans.rs:59-143) with ChaCha8Rng::seed_from_u64(seed): k-means++
+ * seeding then Lloyd; k is clamped to [1, n]; writes k_out x dim centroids. */
+int pxg_kmeans(const float* points, uint64_t n, uint32_t dim, uint64_t k, uint64_t max_iterations, uint64_t seed,
+               float* centroids_out, double* inertia, uint64_t* iterations, uint64_t* k_out);
+/* The Lloyd loop of kmeans() (kmeans.rs:85-136) from given initial centroids;
+ * assign_out (n, may be NULL) is the last assignment pass. */
+int pxg_kmeans_lloyd(const float* points, uint64_t n, uint32_t dim, uint64_t k, uint64_t max_iterations,
+                     const float* init, float* centroids_out, uint32_t* assign_out, double* inertia,
+                     uint64_t* iterations);
+/* pxg_kmeans / pxg_kmeans_lloyd with points, init, centroids and assignment in
+ * device memory (d_init NULL = k-means++ from seed). */
+int pxg_kmeans_device(const float* d_points, uint64_t n, uint32_t dim, uint64_t k, uint64_t max_iterations,
+                      uint64_t seed, const float* d_init, float* d_centroids_out, uint32_t* d_assign_out,
+                      double* inertia, uint64_t* iterations);
+/* kmeans_plus_plus (kmeans.rs:146-194) alone, 1 <= k <= n. */
+int pxg_kmeans_pp(const float* points, uint64_t n, uint32_t dim, uint64_t k, uint64_t seed, float* centroids_out);
+/* The assignment pass (kmeans.rs:90-97, nearest 200-212). */
+int pxg_kmeans_assign(const float* points, uint64_t n, uint32_t dim, const float* centroids, uint64_t k,
+                      uint32_t* assign_out, float* dist_out);
+/* ProductQuantizer::train (product.rs:198-296): codebooks_out holds, per
+ * subspace, 256 rows of its width (dim floats x 256 in total). */
+int pxg_pq_train(const float* training, uint64_t n, uint32_t dim, uint64_t subspaces, uint64_t max_iterations,
+                 uint64_t seed, float* codebooks_out, double* inertia, uint64_t* iterations);
+/* ProductQuantizer::encode_into (product.rs:361-380) for n vectors. */
+int pxg_pq_encode(const float* codebooks, uint32_t dim, uint64_t subspaces, const float* vectors, uint64_t n,
+                  uint8_t* codes_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -407,3 +407,304 @@ class FlatIndex(_IndexBase):
 
     def exact_ids(self, query, k, filter=None):  # flat.rs:201-212
         return [r.id for r in self.search(query, k, filter)]
+
+
+# --- IvfPqConfig / IvfPqIndex: ivfpq.rs:106-1228 -----------------------------------
+from ._capi import IvfPqConfigC as _IvfPqConfigC  # noqa: E402
+from ._capi import TrainingReportC as _TrainingReportC  # noqa: E402
+
+TrainingReport = namedtuple("TrainingReport", ["sampled", "coarse_inertia", "coarse_iterations", "residual_inertia",
+                                               "populated_lists", "largest_list"])  # ivfpq.rs:322-357
+
+
+class IvfPqConfig:
+    """Builder mirroring IvfPqConfig (ivfpq.rs:106-304)."""
+
+    def __init__(self, nlist, subspaces):
+        c = _IvfPqConfigC()
+        _check(_lib.pxg_ivfpq_config_default(nlist, subspaces, C.byref(c)))
+        self._c = c
+
+    def _with(self, field, value):
+        setattr(self._c, field, value)
+        return self
+
+    def with_nprobe(self, v):
+        return self._with("nprobe", v)
+
+    def with_rerank(self, v):
+        return self._with("rerank", v)
+
+    def with_seed(self, v):
+        return self._with("seed", v)
+
+    def with_max_iterations(self, v):
+        return self._with("max_iterations", v)
+
+    def with_training_sample(self, v):
+        return self._with("training_sample", v)
+
+    def with_train_threshold(self, v):
+        return self._with("train_threshold", min(int(v), (1 << 64) - 1))
+
+    def with_retain_vectors(self, v):
+        return self._with("retain_vectors", 1 if v else 0)
+
+    def __getattr__(self, name):
+        if name.startswith("_"):
+            raise AttributeError(name)
+        v = getattr(self._c, name)
+        return bool(v) if name == "retain_vectors" else v
+
+    def clone(self):
+        o = IvfPqConfig.__new__(IvfPqConfig)
+        o._c = _IvfPqConfigC()
+        C.memmove(C.byref(o._c), C.byref(self._c), C.sizeof(_IvfPqConfigC))
+        return o
+
+
+def _report(r):
+    return TrainingReport(r.sampled, r.coarse_inertia, r.coarse_iterations, r.residual_inertia, r.populated_lists,
+                          r.largest_list)
+
+
+class IvfPqIndex(_IndexBase):
+    """GPU IVF-PQ (ivfpq.rs:452-1228): coarse lists, residual PQ codes, ADC scan."""
+
+    def __init__(self, space, config):
+        self.space = space
+        self.config = config
+        h = C.c_void_p()
+        _check(_lib.pxg_ivfpq_create(space.dim, space.metric, C.byref(config._c), C.byref(h)))
+        self._h = h
+        self._meta = {}
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            _lib.pxg_ivfpq_destroy(h)
+            self._h = None
+
+    def insert(self, id, vector, metadata=None):
+        v = np.asarray(vector, dtype=np.float32).reshape(-1)
+        if v.size != self.space.dim:
+            raise DimensionMismatch(
+                f"dimension mismatch: index holds {self.space.dim}-dimensional vectors, got {v.size}",
+                self.space.dim, v.size)
+        self.insert_batch(np.array([id], np.uint64), v.reshape(1, -1))
+        if metadata:
+            self._meta[int(id)] = dict(metadata)
+
+    def insert_batch(self, ids, vectors):
+        ids = np.ascontiguousarray(ids, dtype=np.uint64).reshape(-1)
+        v = _rows(vectors, self.space.dim)
+        slots = np.zeros(ids.size, np.uint32)
+        _check(_lib.pxg_ivfpq_insert(self._h, _ptr(ids), _ptr(v), ids.size, _ptr(slots)))
+        return slots
+
+    def remove(self, id):
+        _check(_lib.pxg_ivfpq_remove(self._h, int(id)))
+        self._meta.pop(int(id), None)
+
+    def contains(self, id):
+        return bool(_lib.pxg_ivfpq_contains(self._h, int(id)))
+
+    def __len__(self):
+        return int(_lib.pxg_ivfpq_len(self._h))
+
+    def is_trained(self):
+        return bool(_lib.pxg_ivfpq_is_trained(self._h))
+
+    def stats(self):
+        s = _IndexStatsC()
+        _check(_lib.pxg_ivfpq_stats(self._h, C.byref(s)))
+        return _stats_from_c(s)
+
+    def vector_bytes(self):
+        return self.stats().vector_bytes
+
+    def compressed_bytes(self):
+        return self.stats().graph_bytes
+
+    def code_bytes_per_vector(self):
+        return self.config.subspaces
+
+    def vector(self, id):
+        out = np.zeros(self.space.dim, np.float32)
+        try:
+            _check(_lib.pxg_ivfpq_get_vector(self._h, int(id), _ptr(out)))
+        except (UnknownId, Configuration):
+            return None
+        return out
+
+    def slots(self):
+        n = int(_lib.pxg_ivfpq_slot_count(self._h))
+        ids = np.zeros(max(n, 1), np.uint64)
+        live = np.zeros(max(n, 1), np.uint8)
+        _check(_lib.pxg_ivfpq_slots(self._h, _ptr(ids), _ptr(live)))
+        return ids[:n], live[:n]
+
+    def list_lengths(self):
+        n = int(_lib.pxg_ivfpq_list_count(self._h))
+        out = np.zeros(max(n, 1), np.uint64)
+        _check(_lib.pxg_ivfpq_list_lengths(self._h, _ptr(out)))
+        return [int(x) for x in out[:n]]
+
+    def train(self):
+        r = _TrainingReportC()
+        _check(_lib.pxg_ivfpq_train(self._h, C.byref(r)))
+        return _report(r)
+
+    def training_report(self):
+        r = _TrainingReportC()
+        try:
+            _check(_lib.pxg_ivfpq_training_report(self._h, C.byref(r)))
+        except Configuration:
+            return None
+        return _report(r)
+
+    def parts(self):
+        """(centroids, codebooks, codes, list_of) of a trained index (ivfpq.rs:606-617)."""
+        nl = int(_lib.pxg_ivfpq_list_count(self._h))
+        ns = int(_lib.pxg_ivfpq_slot_count(self._h))
+        m = self.config.subspaces
+        cents = np.zeros((nl, self.space.dim), np.float32)
+        books = np.zeros(256 * self.space.dim, np.float32)
+        codes = np.zeros((max(ns, 1), m), np.uint8)
+        list_of = np.zeros(max(ns, 1), np.uint32)
+        _check(_lib.pxg_ivfpq_parts(self._h, _ptr(cents), _ptr(books), _ptr(codes), _ptr(list_of)))
+        return cents, books, codes[:ns], list_of[:ns]
+
+    def load_trained(self, centroids, codebooks, codes=None, list_of=None):
+        """IvfPqIndex::from_parts (ivfpq.rs:624-717) onto the inserted vectors."""
+        cents = np.ascontiguousarray(centroids, dtype=np.float32)
+        books = np.ascontiguousarray(codebooks, dtype=np.float32).reshape(-1)
+        c = None if codes is None else np.ascontiguousarray(codes, dtype=np.uint8)
+        lo = None if list_of is None else np.ascontiguousarray(list_of, dtype=np.uint32)
+        _check(_lib.pxg_ivfpq_load_trained(self._h, _ptr(cents), cents.shape[0], _ptr(books), _ptr(c), _ptr(lo)))
+
+    def search_batch(self, queries, k, filter=None, nprobe=None):
+        check_k(k)
+        q = _rows(queries, self.space.dim)
+        nq = q.shape[0]
+        acc = None
+        if filter is not None:
+            sid, live = self.slots()
+            acc = self._accept_mask(filter, sid, live)
+        kk = max(k, 1)
+        oi = np.zeros((nq, kk), np.uint64)
+        od = np.zeros((nq, kk), np.float32)
+        oc = np.zeros(max(nq, 1), np.uint32)
+        _check(_lib.pxg_ivfpq_search(self._h, _ptr(q), nq, k, 0 if nprobe is None else max(int(nprobe), 1),
+                                     _ptr(acc), _ptr(oi), _ptr(od), _ptr(oc)))
+        return oi[:, :k], od[:, :k], oc[:nq]
+
+    def search_with_nprobe(self, query, k, nprobe, filter=None):  # ivfpq.rs:981-996
+        ids, dists, counts = self.search_batch(np.asarray(query, dtype=np.float32).reshape(1, -1), k, filter,
+                                               max(int(nprobe), 1))
+        return [SearchResult(int(ids[0, i]), float(dists[0, i])) for i in range(int(counts[0]))]
+
+    def search_device(self, queries, k, out_ids, out_dist, out_count, nprobe=None, accept=None, stream=None):
+        _check(_lib.pxg_ivfpq_search_device(
+            self._h, _device_ptr(queries), queries.shape[0], k, 0 if nprobe is None else int(nprobe),
+            None if accept is None else _device_ptr(accept), _device_ptr(out_ids), _device_ptr(out_dist),
+            _device_ptr(out_count), None if stream is None else C.c_void_p(stream)))
+
+
+# --- k-means / product quantizer (crates/proxima-quantize) ----------------------------
+Clustering = namedtuple("Clustering", ["centroids", "inertia", "iterations"])  # kmeans.rs:34-48
+
+
+def kmeans(points, dim, k, max_iterations, seed):
+    """kmeans() (kmeans.rs:59-143) with ChaCha8Rng::seed_from_u64(seed), on the GPU."""
+    p = np.ascontiguousarray(points, dtype=np.float32).reshape(-1)
+    n = p.size // dim if dim else 0
+    kk = max(min(k, n), 1)
+    cents = np.zeros(kk * dim, np.float32)
+    inertia, iters, kout = C.c_double(), C.c_uint64(), C.c_uint64()
+    _check(_lib.pxg_kmeans(_ptr(p), n, dim, k, max_iterations, seed, _ptr(cents), C.byref(inertia), C.byref(iters),
+                           C.byref(kout)))
+    return Clustering(cents[: int(kout.value) * dim], inertia.value, iters.value)
+
+
+def kmeans_lloyd(points, init, max_iterations):
+    """The Lloyd loop (kmeans.rs:85-136) from the given initial centroids."""
+    p = np.ascontiguousarray(points, dtype=np.float32)
+    n, dim = p.shape
+    init = np.ascontiguousarray(init, dtype=np.float32)
+    k = init.shape[0]
+    cents = np.zeros((k, dim), np.float32)
+    assign = np.zeros(n, np.uint32)
+    inertia, iters = C.c_double(), C.c_uint64()
+    _check(_lib.pxg_kmeans_lloyd(_ptr(p), n, dim, k, max_iterations, _ptr(init), _ptr(cents), _ptr(assign),
+                                 C.byref(inertia), C.byref(iters)))
+    return cents, assign, inertia.value, iters.value
+
+
+def kmeans_pp(points, k, seed):
+    p = np.ascontiguousarray(points, dtype=np.float32)
+    n, dim = p.shape
+    cents = np.zeros((k, dim), np.float32)
+    _check(_lib.pxg_kmeans_pp(_ptr(p), n, dim, k, seed, _ptr(cents)))
+    return cents
+
+
+def kmeans_assign(points, centroids):
+    p = np.ascontiguousarray(points, dtype=np.float32)
+    c = np.ascontiguousarray(centroids, dtype=np.float32)
+    n, dim = p.shape
+    a = np.zeros(n, np.uint32)
+    d = np.zeros(n, np.float32)
+    _check(_lib.pxg_kmeans_assign(_ptr(p), n, dim, _ptr(c), c.shape[0], _ptr(a), _ptr(d)))
+    return a, d
+
+
+class PqConfig:
+    """PqConfig (product.rs:83-132)."""
+
+    def __init__(self, subspaces):
+        self.subspaces, self.max_iterations, self.seed = subspaces, 25, 0x5EED1EAF
+
+    def with_seed(self, seed):
+        self.seed = seed
+        return self
+
+    def with_max_iterations(self, n):
+        self.max_iterations = n
+        return self
+
+
+class ProductQuantizer:
+    """ProductQuantizer::train / encode (product.rs:198-380) on the GPU."""
+
+    def __init__(self, dim, subspaces, codebooks, training_inertia=0.0, training_iterations=0):
+        self.dim, self.subspaces, self.codebooks = dim, subspaces, codebooks
+        self.training_inertia, self.training_iterations = training_inertia, training_iterations
+
+    @classmethod
+    def train(cls, space, training, config):
+        t = np.ascontiguousarray(training, dtype=np.float32).reshape(-1)
+        if t.size == 0 or t.size % space.dim:
+            raise _config("training", t.size, "must be a non-empty multiple of the space dimension")
+        n = t.size // space.dim
+        books = np.zeros(256 * space.dim, np.float32)
+        inertia, iters = C.c_double(), C.c_uint64()
+        _check(_lib.pxg_pq_train(_ptr(t), n, space.dim, config.subspaces, config.max_iterations, config.seed,
+                                 _ptr(books), C.byref(inertia), C.byref(iters)))
+        return cls(space.dim, config.subspaces, books, inertia.value, iters.value)
+
+    def code_len(self):
+        return self.subspaces
+
+    def compression_ratio(self):
+        return self.dim * 4 / self.code_len()
+
+    def encode(self, vectors):
+        v = np.ascontiguousarray(vectors, dtype=np.float32).reshape(-1, self.dim)
+        out = np.zeros((v.shape[0], self.subspaces), np.uint8)
+        _check(_lib.pxg_pq_encode(_ptr(self.codebooks), self.dim, self.subspaces, _ptr(v), v.shape[0], _ptr(out)))
+        return out
+
+
+__all__ += ["IvfPqConfig", "IvfPqIndex", "TrainingReport", "Clustering", "kmeans", "kmeans_lloyd", "kmeans_pp",
+            "kmeans_assign", "PqConfig", "ProductQuantizer"]

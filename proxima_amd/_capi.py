@@ -90,6 +90,35 @@ SIGNATURES = {
     "pxg_flat_search_device": (_i32, [_vp, _vp, _u64, _u64, _vp, _vp, _vp, _vp, _vp]),
     "pxg_flat_last_fallbacks": (_u64, []),
     "pxg_flat_set_search_mode": (_i32, [_vp, _i32]),
+    # ivf-pq
+    "pxg_ivfpq_config_default": (_i32, [_u64, _u64, _P(IvfPqConfigC)]),
+    "pxg_ivfpq_create": (_i32, [_u32, _i32, _P(IvfPqConfigC), _P(_vp)]),
+    "pxg_ivfpq_destroy": (None, [_vp]),
+    "pxg_ivfpq_insert": (_i32, [_vp, _vp, _vp, _u64, _vp]),
+    "pxg_ivfpq_remove": (_i32, [_vp, _u64]),
+    "pxg_ivfpq_contains": (_i32, [_vp, _u64]),
+    "pxg_ivfpq_len": (_u64, [_vp]),
+    "pxg_ivfpq_is_trained": (_i32, [_vp]),
+    "pxg_ivfpq_stats": (_i32, [_vp, _P(IndexStats)]),
+    "pxg_ivfpq_get_vector": (_i32, [_vp, _u64, _vp]),
+    "pxg_ivfpq_slot_count": (_u64, [_vp]),
+    "pxg_ivfpq_slots": (_i32, [_vp, _vp, _vp]),
+    "pxg_ivfpq_list_count": (_u64, [_vp]),
+    "pxg_ivfpq_list_lengths": (_i32, [_vp, _vp]),
+    "pxg_ivfpq_train": (_i32, [_vp, _P(TrainingReportC)]),
+    "pxg_ivfpq_training_report": (_i32, [_vp, _P(TrainingReportC)]),
+    "pxg_ivfpq_parts": (_i32, [_vp, _vp, _vp, _vp, _vp]),
+    "pxg_ivfpq_load_trained": (_i32, [_vp, _vp, _u64, _vp, _vp, _vp]),
+    "pxg_ivfpq_search": (_i32, [_vp, _vp, _u64, _u64, _u64, _vp, _vp, _vp, _vp]),
+    "pxg_ivfpq_search_device": (_i32, [_vp, _vp, _u64, _u64, _u64, _vp, _vp, _vp, _vp, _vp]),
+    # k-means / PQ
+    "pxg_kmeans": (_i32, [_vp, _u64, _u32, _u64, _u64, _u64, _vp, _P(_f64), _P(_u64), _P(_u64)]),
+    "pxg_kmeans_lloyd": (_i32, [_vp, _u64, _u32, _u64, _u64, _vp, _vp, _vp, _P(_f64), _P(_u64)]),
+    "pxg_kmeans_device": (_i32, [_vp, _u64, _u32, _u64, _u64, _u64, _vp, _vp, _vp, _P(_f64), _P(_u64)]),
+    "pxg_kmeans_pp": (_i32, [_vp, _u64, _u32, _u64, _u64, _vp]),
+    "pxg_kmeans_assign": (_i32, [_vp, _u64, _u32, _vp, _u64, _vp, _vp]),
+    "pxg_pq_train": (_i32, [_vp, _u64, _u32, _u64, _u64, _u64, _vp, _P(_f64), _P(_u64)]),
+    "pxg_pq_encode": (_i32, [_vp, _u32, _u64, _vp, _u64, _vp]),
 }
 
 

@@ -338,10 +338,12 @@ struct FlatIndex {
     if (stream) (void)hipStreamDestroy(stream);
   }
 
-  void ensure_capacity(size_t need) {
+  // Grow the device arrays to hold `need` slots, keeping the first `keep`
+  // (the high-water mark before the current allocation, never above cap).
+  void ensure_capacity(size_t need, size_t keep) {
     if (need <= cap) return;
     size_t nc = std::max<size_t>(need, std::max<size_t>(cap * 2, 1024));
-    const size_t hw = slots.high_water();
+    const size_t hw = std::min(keep, cap);
     X.grow(nc * ld, hw * ld, stream);
     xb.grow(nc, hw, stream);
     d_live.grow(nc, hw, stream);
@@ -400,10 +402,11 @@ struct FlatIndex {
     if (by_id.size() + n > (size_t)UINT32_MAX - 1)
       raise(PXG_ERR_CAPACITY, "capacity exceeded: slot allocator limit is 4294967295", UINT32_MAX);
     std::vector<uint32_t> sl(n);
+    const size_t old_hw = slots.high_water();
     // Allocate in order, exactly as repeated VectorStore::insert would.
     for (uint64_t i = 0; i < n; ++i) sl[i] = slots.allocate();
     const size_t hw = slots.high_water();
-    ensure_capacity(hw);
+    ensure_capacity(hw, old_hw);
     if (ids.size() < hw) {
       ids.resize(hw, 0);
       live.resize(hw, 0);
@@ -583,9 +586,10 @@ struct FlatIndex {
     for (float nr : norms)
       if (!(nr <= newmax)) newmax = std::isnan(nr) ? INFINITY : nr;
     std::vector<uint32_t> sl(n);
+    const size_t old_hw = slots.high_water();
     for (uint64_t i = 0; i < n; ++i) sl[i] = slots.allocate();
     const size_t hw = slots.high_water();
-    ensure_capacity(hw);
+    ensure_capacity(hw, old_hw);
     if (ids.size() < hw) {
       ids.resize(hw, 0);
       live.resize(hw, 0);
@@ -646,7 +650,7 @@ int pxg_flat_create(uint32_t dim, int metric, uint64_t capacity, pxg_flat** out)
     f.metric = metric;
     try {
       PXG_HIP(hipStreamCreateWithFlags(&f.stream, hipStreamNonBlocking));
-      if (capacity) f.ensure_capacity(capacity);
+      if (capacity) f.ensure_capacity(capacity, 0);
     } catch (...) {
       delete h;
       throw;

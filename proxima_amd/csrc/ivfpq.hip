@@ -1,0 +1,955 @@
+// IVF-PQ on MI355X: IvfPqIndex (crates/proxima-index/src/ivfpq.rs) with the
+// product quantizer's distance table and ADC (crates/proxima-quantize/src/
+// product.rs:407-616).
+//
+// HBM layout of a trained index:
+//   cents      [produced][ld] f32   coarse centroids (zero padded rows)
+//   books      [sum_s 256*width_s] f32, subspace s at book_off[s], row c of
+//              width_s floats (product.rs:226-238 layout)
+//   codes      [cap][M] u8           slot-major PQ codes (product.rs:361-380)
+//   list_of    [cap] u32             coarse list per slot, UINT32_MAX if none
+//   CSR view rebuilt lazily after mutations, one entry per live slot, lists
+//   in order and slots ascending inside each list (ivfpq.rs:891-896):
+//     list_off [produced+1] u32, list_rank [entries] u32 (id rank),
+//     list_codes [entries][M] u8 -> M + 4 bytes per scanned vector.
+//   X          [cap][ld] f32 prepared vectors when retained (rerank, training,
+//              the untrained exhaustive path).
+//
+// Search (ivfpq.rs:998-1110), per batch:
+//   ivf_coarse  exact squared_euclidean_unrolled to every centroid (bit-exact,
+//               so the probed list set is the reference's), radix-select the
+//               nprobe smallest (distance, list).
+//   ivf_scan    one workgroup per (query, probe): build the distance table in
+//               LDS exactly as distance_table does (per subspace, per
+//               centroid, sequential d = q - c; l2 += d*d; ip += q*c), stream
+//               the list's codes coalesced (M bytes + a 4-byte id rank per
+//               entry), ADC-sum the table in subspace order (bit-exact),
+//               keep a per-wave top-kk by (score, id).
+//   ivf_merge   per query: select the shortlist over all probes, optionally
+//               rescore it exactly against the stored vectors (rerank), keep k.
+#include <algorithm>
+#include <cmath>
+#include <mutex>
+#include <shared_mutex>
+
+#include "common.hpp"
+#include "device.hpp"
+#include "exact_scan.hpp"
+#include "train.hpp"
+
+namespace pxg {
+
+constexpr uint32_t UNASSIGNED = 0xFFFFFFFFu;
+constexpr int IVF_MAX_M = 128;
+
+// ---------------------------------------------------------------------------
+// coarse stage
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void ivf_coarse_keys(const float* __restrict__ Qp, int ld, int dim,
+                                                       const float* __restrict__ cents, int produced,
+                                                       uint64_t* __restrict__ ck) {
+  const int q = blockIdx.x;
+  const int g = threadIdx.x & 7, grp = threadIdx.x >> 3;
+  const float* qv = Qp + (size_t)q * ld;
+  for (int l = grp; l < produced; l += 32) {
+    const float d = dist_group8<0>(qv, cents + (size_t)l * ld, dim, g);  // squared_l2, ivfpq.rs:1247-1249
+    if (g == 0) ck[(size_t)q * produced + l] = ((uint64_t)ord_key(d) << 32) | (uint32_t)l;
+  }
+}
+
+__global__ __launch_bounds__(256) void ivf_coarse_select(const uint64_t* __restrict__ ck, int produced, int nprobe,
+                                                         int* __restrict__ probes) {
+  const int q = blockIdx.x;
+  __shared__ int hist[256];
+  __shared__ uint64_t sh[4];
+  __shared__ int n_sel;
+  const uint64_t* base = ck + (size_t)q * produced;
+  auto get = [&](int i) -> uint64_t { return base[i]; };
+  if (threadIdx.x == 0) n_sel = 0;
+  __syncthreads();
+  // (distance total_cmp, list) order: ivfpq.rs:1025
+  const uint64_t pivot = block_radix_select(get, produced, nprobe, hist, sh);
+  for (int i = threadIdx.x; i < produced; i += blockDim.x) {
+    const uint64_t x = base[i];
+    if (x <= pivot) probes[(size_t)q * nprobe + atomicAdd(&n_sel, 1)] = (int)(uint32_t)x;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// ADC scan of one probed list per workgroup
+// ---------------------------------------------------------------------------
+template <int CAPW>
+__device__ inline void wave_compact(uint64_t* wb, int cnt, int kk, int lane) {
+  constexpr int E = CAPW / WAVE;
+  uint64_t kv[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int idx = lane * E + e;
+    kv[e] = idx < cnt ? wb[idx] : KEY_MAX;
+  }
+  wave_bitonic_sort<E>(kv, lane);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int idx = lane * E + e;
+    if (idx < kk) wb[idx] = kv[e];
+  }
+}
+
+template <int CAPW, int METRIC>
+__global__ __launch_bounds__(256) void ivf_scan(const float* __restrict__ Qp, int ld, int dim, int M,
+                                                const int* __restrict__ probes, int nprobe,
+                                                const float* __restrict__ cents, const float* __restrict__ books,
+                                                const int* __restrict__ sub_off, const int* __restrict__ book_off,
+                                                const uint32_t* __restrict__ list_off,
+                                                const uint32_t* __restrict__ list_rank,
+                                                const uint8_t* __restrict__ list_codes,
+                                                const uint32_t* __restrict__ rank_slot,
+                                                const uint8_t* __restrict__ accept, int kk,
+                                                uint64_t* __restrict__ out) {
+  extern __shared__ float lut[];  // M * 256 floats
+  __shared__ uint64_t wbuf[4][CAPW];
+  __shared__ float s_qdc;
+  const int q = blockIdx.x / nprobe, p = blockIdx.x % nprobe;
+  const int l = probes[(size_t)q * nprobe + p];
+  const float* qv = Qp + (size_t)q * ld;
+  const float* cv = cents + (size_t)l * ld;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+
+  if constexpr (METRIC == 1) {
+    // q . c for the cosine decomposition (ivfpq.rs:1068-1072, dot_unrolled)
+    if (tid < 8) {
+      const float d = -dist_group8<2>(qv, cv, dim, tid);
+      if (tid == 0) s_qdc = d;
+    }
+  }
+  // Distance table (product.rs:416-433). L2: on the residual q - c
+  // (ivfpq.rs:1052-1054); cosine: on the query itself (shared table).
+  for (int e = tid; e < M * 256; e += 256) {
+    const int s = e >> 8, c = e & 255;
+    const int w_s = sub_off[s + 1] - sub_off[s];
+    const float* b = books + book_off[s] + c * w_s;
+    const int o = sub_off[s];
+    float acc = 0.0f;
+    for (int j = 0; j < w_s; ++j) {
+      if constexpr (METRIC == 0) {
+        const float r = qv[o + j] - cv[o + j];
+        const float d = r - b[j];
+        acc += d * d;
+      } else {
+        acc += qv[o + j] * b[j];
+      }
+    }
+    lut[e] = acc;
+  }
+  __syncthreads();
+  const float one_minus_qdc = METRIC == 1 ? 1.0f - s_qdc : 0.0f;
+
+  uint64_t* wb = wbuf[w];
+  uint64_t thr = KEY_MAX;
+  int cnt = 0;
+  const uint32_t begin = list_off[l], end = list_off[l + 1];
+  for (uint32_t e0 = begin + w * 64; e0 < end; e0 += 256) {
+    const uint32_t e = e0 + lane;
+    uint64_t key = KEY_MAX;
+    if (e < end) {
+      const uint32_t rk = list_rank[e];
+      if (accept == nullptr || accept[rank_slot[rk]]) {
+        const uint8_t* code = list_codes + (size_t)e * M;
+        float sum = 0.0f;  // DistanceTable::squared_l2 / inner_product, product.rs:580-603
+        if (M == 16) {
+          const uint4 cw = *reinterpret_cast<const uint4*>(code);
+          const uint32_t wv[4] = {cw.x, cw.y, cw.z, cw.w};
+#pragma unroll
+          for (int s = 0; s < 16; ++s) sum += lut[s * 256 + ((wv[s >> 2] >> (8 * (s & 3))) & 255)];
+        } else {
+          for (int s = 0; s < M; ++s) sum += lut[s * 256 + code[s]];
+        }
+        const float score = METRIC == 0 ? sum : one_minus_qdc + (-sum);
+        key = ((uint64_t)ord_key(score) << 32) | rk;
+      }
+    }
+    const bool pass = key < thr;
+    const uint64_t mask = __ballot(pass);
+    const int pos = cnt + __popcll(mask & ((1ull << lane) - 1));
+    if (pass) wb[pos] = key;
+    cnt += __popcll(mask);
+    if (cnt > CAPW - 64) {
+      wave_compact<CAPW>(wb, cnt, kk, lane);
+      cnt = kk;
+      thr = wb[kk - 1];
+    }
+  }
+  wave_compact<CAPW>(wb, cnt, kk, lane);
+  uint64_t* o = out + (((size_t)q * nprobe + p) * 4 + w) * kk;
+  for (int i = lane; i < kk; i += 64) o[i] = i < cnt ? wb[i] : KEY_MAX;
+}
+
+// ---------------------------------------------------------------------------
+// merge over probes (+ optional exact rerank)
+// ---------------------------------------------------------------------------
+constexpr int IVF_MAX_SHORT = 960;
+
+__global__ __launch_bounds__(256) void ivf_merge(const uint64_t* __restrict__ cand, int n_per_q, int kk, int k,
+                                                 int rerank, const float* __restrict__ Qp, int ld, int dim,
+                                                 int metric, const float* __restrict__ X,
+                                                 const uint32_t* __restrict__ rank_slot,
+                                                 const uint64_t* __restrict__ ids, uint64_t* __restrict__ out_ids,
+                                                 float* __restrict__ out_d, uint32_t* __restrict__ out_count) {
+  const int q = blockIdx.x;
+  __shared__ int hist[256];
+  __shared__ uint64_t sh[4];
+  __shared__ uint64_t sel[1024];
+  __shared__ int n_sel, n_valid;
+  const uint64_t* base = cand + (size_t)q * n_per_q;
+  auto get = [&](int i) -> uint64_t { return base[i]; };
+  if (threadIdx.x == 0) {
+    n_sel = 0;
+    n_valid = 0;
+  }
+  __syncthreads();
+  int local = 0;
+  for (int i = threadIdx.x; i < n_per_q; i += blockDim.x) local += base[i] != KEY_MAX;
+  atomicAdd(&n_valid, local);
+  __syncthreads();
+  const int ksel = min(kk, n_valid);
+  if (ksel == 0) {
+    if (threadIdx.x == 0) out_count[q] = 0;
+    return;
+  }
+  const uint64_t pivot = block_radix_select(get, n_per_q, ksel, hist, sh);
+  for (int i = threadIdx.x; i < n_per_q; i += blockDim.x) {
+    const uint64_t x = base[i];
+    if (x <= pivot && x != KEY_MAX) sel[atomicAdd(&n_sel, 1)] = x;
+  }
+  __syncthreads();
+  int P = 1;
+  while (P < ksel) P <<= 1;
+  for (int i = ksel + threadIdx.x; i < P; i += blockDim.x) sel[i] = KEY_MAX;
+  __syncthreads();
+  block_bitonic_sort(sel, P);
+  int kout = min(k, ksel);
+  if (rerank) {
+    // exact rescoring of the shortlist (ivfpq.rs:1098-1109)
+    const int g = threadIdx.x & 7, grp = threadIdx.x >> 3;
+    const float* qv = Qp + (size_t)q * ld;
+    for (int c = grp; c < ksel; c += 32) {
+      const uint32_t rk = (uint32_t)sel[c];
+      const float d = dist_group8_rt(metric, qv, X + (size_t)rank_slot[rk] * ld, dim, g);
+      if (g == 0) sel[c] = ((uint64_t)ord_key(d) << 32) | rk;
+    }
+    __syncthreads();
+    block_bitonic_sort(sel, P);
+  }
+  for (int i = threadIdx.x; i < kout; i += blockDim.x) {
+    const uint64_t key = sel[i];
+    out_ids[(size_t)q * k + i] = ids[rank_slot[(uint32_t)key]];
+    out_d[(size_t)q * k + i] = key_float((uint32_t)(key >> 32));
+  }
+  if (threadIdx.x == 0) out_count[q] = kout;
+}
+
+__global__ void ivf_gather_rows(const float* __restrict__ X, int ld, const uint32_t* __restrict__ rows, int n,
+                                int dim, float* __restrict__ out) {
+  const int i = blockIdx.x;
+  if (i >= n) return;
+  for (int j = threadIdx.x; j < dim; j += blockDim.x) out[(size_t)i * dim + j] = X[(size_t)rows[i] * ld + j];
+}
+
+__global__ void ivf_residuals(const float* __restrict__ S, const float* __restrict__ C, const uint32_t* __restrict__ a,
+                              int dim, float* __restrict__ R) {
+  const int i = blockIdx.x;
+  for (int j = threadIdx.x; j < dim; j += blockDim.x)
+    R[(size_t)i * dim + j] = S[(size_t)i * dim + j] - C[(size_t)a[i] * dim + j];
+}
+
+__global__ void ivf_gather_csr(const uint32_t* __restrict__ entry_slot, int n, const uint32_t* __restrict__ rank,
+                               const uint8_t* __restrict__ codes, int M, uint32_t* __restrict__ list_rank,
+                               uint8_t* __restrict__ list_codes) {
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n) return;
+  const uint32_t s = entry_slot[e];
+  list_rank[e] = rank[s];
+  for (int j = 0; j < M; ++j) list_codes[(size_t)e * M + j] = codes[(size_t)s * M + j];
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+struct IvfPqIndex {
+  uint32_t dim = 0, ld = 0;
+  int metric = 0;
+  pxg_ivfpq_config cfg{};
+  PqLayout pq;
+
+  // slot table (ivfpq.rs:452-479)
+  std::vector<uint64_t> ids;
+  std::vector<uint8_t> live;
+  std::vector<uint32_t> list_of_h;
+  std::unordered_map<uint64_t, uint32_t> by_id;
+  SlotAllocator slots;
+  bool vectors_kept = true;  // false once trained with retain_vectors = false
+
+  // trained state
+  bool trained = false;
+  int produced = 0;
+  pxg_training_report report{};
+  bool has_report = false;
+
+  size_t cap = 0;
+  DevBuf<float> X;
+  DevBuf<uint8_t> d_live;
+  DevBuf<uint64_t> d_ids;
+  DevBuf<uint8_t> codes;
+  DevBuf<uint32_t> d_list_of;
+  DevBuf<float> cents, books;
+  DevBuf<int> d_sub_off, d_book_off;
+  DevBuf<uint32_t> d_rank, d_rank_slot;
+  DevBuf<uint32_t> list_off, list_rank;
+  DevBuf<uint8_t> list_codes;
+  std::vector<uint32_t> list_len_h;
+  bool rank_dirty = true, csr_dirty = true;
+  std::mutex lazy_mu;
+
+  mutable std::shared_mutex mu;
+  CtxPool pool;
+  hipStream_t stream = nullptr;
+
+  ~IvfPqIndex() {
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+
+  size_t M() const { return (size_t)cfg.subspaces; }
+
+  // Grow the device arrays to hold `need` slots, keeping the first `keep`
+  // (the high-water mark before the current allocation, never above cap).
+  void ensure_capacity(size_t need, size_t keep) {
+    if (need <= cap) return;
+    size_t nc = std::max<size_t>(need, std::max<size_t>(cap * 2, 1024));
+    const size_t hw = std::min(keep, cap);
+    if (vectors_kept) X.grow(nc * ld, hw * ld, stream);
+    d_live.grow(nc, hw, stream);
+    d_ids.grow(nc, hw, stream);
+    codes.grow(nc * M(), hw * M(), stream);
+    d_list_of.grow(nc, hw, stream);
+    d_rank.grow(nc, hw, stream);
+    PXG_HIP(hipMemsetAsync(d_live.p + hw, 0, nc - hw, stream));
+    PXG_HIP(hipStreamSynchronize(stream));
+    cap = nc;
+  }
+
+  // ranks of live ids + the CSR list view; rebuilt on first use after a change
+  void refresh(hipStream_t s) {
+    std::lock_guard<std::mutex> lk(lazy_mu);
+    const size_t hw = slots.high_water();
+    if (rank_dirty) {
+      std::vector<std::pair<uint64_t, uint32_t>> v;
+      v.reserve(by_id.size());
+      for (size_t i = 0; i < hw; ++i)
+        if (live[i]) v.emplace_back(ids[i], (uint32_t)i);
+      std::sort(v.begin(), v.end());
+      std::vector<uint32_t> rs(v.size()), rk(std::max<size_t>(hw, 1), 0);
+      for (size_t r = 0; r < v.size(); ++r) {
+        rs[r] = v[r].second;
+        rk[v[r].second] = (uint32_t)r;
+      }
+      d_rank_slot.reserve(std::max<size_t>(rs.size(), 1));
+      if (!rs.empty()) PXG_HIP(hipMemcpyAsync(d_rank_slot.p, rs.data(), rs.size() * 4, hipMemcpyHostToDevice, s));
+      if (hw) PXG_HIP(hipMemcpyAsync(d_rank.p, rk.data(), hw * 4, hipMemcpyHostToDevice, s));
+      PXG_HIP(hipStreamSynchronize(s));
+      rank_dirty = false;
+      csr_dirty = true;  // list_rank caches ranks
+    }
+    if (trained && csr_dirty) {
+      std::vector<uint32_t> count(produced + 1, 0);
+      for (size_t i = 0; i < hw; ++i)
+        if (live[i] && list_of_h[i] != UNASSIGNED) count[list_of_h[i] + 1]++;
+      for (int l = 0; l < produced; ++l) count[l + 1] += count[l];
+      const uint32_t total = count[produced];
+      std::vector<uint32_t> entry(std::max<uint32_t>(total, 1)), cur(count.begin(), count.end() - 1);
+      for (size_t i = 0; i < hw; ++i)
+        if (live[i] && list_of_h[i] != UNASSIGNED) entry[cur[list_of_h[i]]++] = (uint32_t)i;
+      list_len_h.assign(produced, 0);
+      for (int l = 0; l < produced; ++l) list_len_h[l] = count[l + 1] - count[l];
+      list_off.reserve(produced + 1);
+      list_rank.reserve(std::max<uint32_t>(total, 1));
+      list_codes.reserve(std::max<size_t>((size_t)total * M() + 16, 16));
+      DevBuf<uint32_t> d_entry(std::max<uint32_t>(total, 1));
+      PXG_HIP(hipMemcpyAsync(list_off.p, count.data(), (produced + 1) * 4, hipMemcpyHostToDevice, s));
+      if (total) {
+        PXG_HIP(hipMemcpyAsync(d_entry.p, entry.data(), total * 4, hipMemcpyHostToDevice, s));
+        hipLaunchKernelGGL(ivf_gather_csr, dim3((total + 255) / 256), dim3(256), 0, s, d_entry.p, (int)total,
+                           d_rank.p, codes.p, (int)M(), list_rank.p, list_codes.p);
+        PXG_HIP(hipGetLastError());
+      }
+      PXG_HIP(hipStreamSynchronize(s));
+      csr_dirty = false;
+    }
+  }
+
+  void upload_books(const float* h_cents, int nprod, const float* h_books) {
+    produced = nprod;
+    cents.alloc((size_t)std::max(nprod, 1) * ld);
+    PXG_HIP(hipMemsetAsync(cents.p, 0, (size_t)std::max(nprod, 1) * ld * 4, stream));
+    PXG_HIP(hipMemcpy2DAsync(cents.p, ld * 4, h_cents, dim * 4, dim * 4, nprod, hipMemcpyHostToDevice, stream));
+    books.alloc(pq.book_off[pq.M]);
+    PXG_HIP(hipMemcpyAsync(books.p, h_books, pq.book_off[pq.M] * 4, hipMemcpyHostToDevice, stream));
+    PXG_HIP(hipStreamSynchronize(stream));
+    trained = true;
+    csr_dirty = true;
+  }
+
+  // encode the given slots (vectors must be in X) on the device: nearest
+  // coarse centroid with the unrolled kernel (ivfpq.rs:1231-1243), residual,
+  // PQ code (product.rs:361-380)
+  void encode_slots(const std::vector<uint32_t>& sl) {
+    if (sl.empty()) return;
+    DevBuf<uint32_t> d_sl(sl.size()), d_as(sl.size());
+    PXG_HIP(hipMemcpyAsync(d_sl.p, sl.data(), sl.size() * 4, hipMemcpyHostToDevice, stream));
+    nearest_device(X.p, (int)ld, d_sl.p, sl.size(), (int)dim, cents.p, (int)ld, produced, true, d_as.p, nullptr,
+                   stream);
+    pq_encode_device(X.p, (int)ld, d_sl.p, sl.size(), (int)dim, cents.p, (int)ld, d_as.p, books.p, pq, codes.p,
+                     stream);
+    std::vector<uint32_t> as(sl.size());
+    PXG_HIP(hipMemcpyAsync(as.data(), d_as.p, as.size() * 4, hipMemcpyDeviceToHost, stream));
+    PXG_HIP(hipStreamSynchronize(stream));
+    for (size_t i = 0; i < sl.size(); ++i) list_of_h[sl[i]] = as[i];
+    // device copy of the assignment, slot-indexed
+    std::vector<uint32_t> lo(list_of_h.begin(), list_of_h.begin() + slots.high_water());
+    PXG_HIP(hipMemcpyAsync(d_list_of.p, lo.data(), lo.size() * 4, hipMemcpyHostToDevice, stream));
+    PXG_HIP(hipStreamSynchronize(stream));
+    csr_dirty = true;
+  }
+
+  // IvfPqIndex::train (ivfpq.rs:735-825)
+  pxg_training_report train() {
+    if (!vectors_kept && !by_id.empty())
+      config_error("retain_vectors", 0, "training needs the full-precision vectors, which were dropped");
+    std::vector<uint32_t> live_slots;
+    for (size_t i = 0; i < slots.high_water(); ++i)
+      if (live[i]) live_slots.push_back((uint32_t)i);
+    if (live_slots.empty()) config_error("len", 0, "an empty index has nothing to fit centroids to");
+    // deterministic stride sample (ivfpq.rs:758-768)
+    const size_t L = live_slots.size();
+    const size_t stride = std::max<size_t>((L + cfg.training_sample - 1) / cfg.training_sample, 1);
+    std::vector<uint32_t> sample;
+    for (size_t i = 0; i < L; i += stride) sample.push_back(live_slots[i]);
+    const size_t ns = sample.size();
+    DevBuf<uint32_t> d_sample(ns);
+    PXG_HIP(hipMemcpyAsync(d_sample.p, sample.data(), ns * 4, hipMemcpyHostToDevice, stream));
+    DevBuf<float> S(ns * dim);
+    hipLaunchKernelGGL(ivf_gather_rows, dim3((unsigned)ns), dim3(256), 0, stream, X.p, (int)ld, d_sample.p, (int)ns,
+                       (int)dim, S.p);
+    PXG_HIP(hipGetLastError());
+    // coarse quantizer: kmeans with ChaCha8Rng::seed_from_u64(seed) (ivfpq.rs:770-777)
+    ChaCha8 rng(cfg.seed);
+    DevBuf<float> coarse;
+    KmeansOut kc = kmeans_device(S.p, ns, (int)dim, (int)dim, cfg.nlist, cfg.max_iterations, &rng, nullptr, coarse,
+                                 nullptr, stream);
+    // residuals of the sample against their nearest centroid (ivfpq.rs:787-792)
+    DevBuf<uint32_t> as(ns);
+    nearest_device(S.p, (int)dim, nullptr, ns, (int)dim, coarse.p, (int)dim, kc.k, true, as.p, nullptr, stream);
+    DevBuf<float> R(ns * dim);
+    hipLaunchKernelGGL(ivf_residuals, dim3((unsigned)ns), dim3(256), 0, stream, S.p, coarse.p, as.p, (int)dim, R.p);
+    PXG_HIP(hipGetLastError());
+    // PQ with a fresh generator from the same seed (ivfpq.rs:794-801)
+    DevBuf<float> B(pq.book_floats());
+    double rin = 0.0;
+    size_t rit = 0;
+    pq_train_device(R.p, ns, (int)dim, (int)dim, pq, cfg.max_iterations, cfg.seed, B.p, &rin, &rit, stream);
+    // install (padded centroid rows) and encode every live vector
+    produced = (int)kc.k;
+    cents.alloc((size_t)produced * ld);
+    PXG_HIP(hipMemsetAsync(cents.p, 0, (size_t)produced * ld * 4, stream));
+    PXG_HIP(hipMemcpy2DAsync(cents.p, ld * 4, coarse.p, dim * 4, dim * 4, produced, hipMemcpyDeviceToDevice, stream));
+    books = std::move(B);
+    PXG_HIP(hipStreamSynchronize(stream));
+    trained = true;
+    encode_slots(live_slots);
+    if (!cfg.retain_vectors) {
+      X.release();
+      vectors_kept = false;
+    }
+    pxg_training_report rep{};
+    rep.sampled = ns;
+    rep.coarse_inertia = kc.inertia;
+    rep.coarse_iterations = kc.iterations;
+    rep.residual_inertia = rin;
+    std::vector<uint64_t> cnt(produced, 0);
+    for (uint32_t s : live_slots) cnt[list_of_h[s]]++;
+    rep.populated_lists = (uint64_t)std::count_if(cnt.begin(), cnt.end(), [](uint64_t c) { return c > 0; });
+    rep.largest_list = cnt.empty() ? 0 : *std::max_element(cnt.begin(), cnt.end());
+    report = rep;
+    has_report = true;
+    return rep;
+  }
+
+  void insert_rows(const uint64_t* in_ids, const float* vecs, uint64_t n, uint32_t* out_slots,
+                   std::vector<uint32_t>& new_slots) {
+    std::vector<float> prepared((size_t)n * ld, 0.0f);
+    for (uint64_t i = 0; i < n; ++i) {
+      long long bad = validate_prepare(metric, vecs + i * dim, dim, prepared.data() + i * ld);
+      if (bad >= 0)
+        raise(PXG_ERR_NON_FINITE,
+              "vector component " + std::to_string(bad) + " is not finite (" + std::to_string(vecs[i * dim + bad]) + ")",
+              (uint64_t)bad, i, vecs[i * dim + bad]);
+    }
+    {
+      std::unordered_map<uint64_t, int> seen;
+      for (uint64_t i = 0; i < n; ++i)
+        if (by_id.count(in_ids[i]) || !seen.emplace(in_ids[i], 1).second)
+          raise(PXG_ERR_DUPLICATE_ID, "duplicate vector id " + std::to_string(in_ids[i]), in_ids[i]);
+    }
+    std::vector<uint32_t> sl(n);
+    const size_t old_hw = slots.high_water();
+    for (uint64_t i = 0; i < n; ++i) sl[i] = slots.allocate();
+    const size_t hw = slots.high_water();
+    ensure_capacity(hw, old_hw);
+    if (ids.size() < hw) {
+      ids.resize(hw, 0);
+      live.resize(hw, 0);
+      list_of_h.resize(hw, UNASSIGNED);
+    }
+    // stage rows: vectors go to X when kept, else to a transient buffer
+    DevBuf<float> tmpX;
+    float* dst = X.p;
+    if (!vectors_kept) {
+      // encode-and-discard (ivfpq.rs:1134-1141): a scratch store indexed by slot
+      tmpX.alloc(hw * ld);
+      dst = tmpX.p;
+    }
+    DevBuf<float> st(n * ld);
+    DevBuf<uint32_t> st_sl(n);
+    PXG_HIP(hipMemcpyAsync(st.p, prepared.data(), n * ld * 4, hipMemcpyHostToDevice, stream));
+    PXG_HIP(hipMemcpyAsync(st_sl.p, sl.data(), n * 4, hipMemcpyHostToDevice, stream));
+    std::vector<float> zeros(n, 0.0f);
+    DevBuf<float> st_b(n);
+    PXG_HIP(hipMemcpyAsync(st_b.p, zeros.data(), n * 4, hipMemcpyHostToDevice, stream));
+    DevBuf<uint64_t> st_ids(n);
+    PXG_HIP(hipMemcpyAsync(st_ids.p, in_ids, n * 8, hipMemcpyHostToDevice, stream));
+    DevBuf<float> dummy_xb(hw);
+    hipLaunchKernelGGL(flat_scatter_rows, dim3((unsigned)n), dim3(256), 0, stream, st.p, st_sl.p, st_b.p, st_ids.p,
+                       (int)n, (int)ld, dst, dummy_xb.p, d_live.p, d_ids.p);
+    PXG_HIP(hipGetLastError());
+    PXG_HIP(hipStreamSynchronize(stream));
+    for (uint64_t i = 0; i < n; ++i) {
+      ids[sl[i]] = in_ids[i];
+      live[sl[i]] = 1;
+      list_of_h[sl[i]] = UNASSIGNED;
+      by_id[in_ids[i]] = sl[i];
+      if (out_slots) out_slots[i] = sl[i];
+    }
+    rank_dirty = true;
+    if (trained) {
+      if (!vectors_kept) {
+        std::swap(X, tmpX);
+        encode_slots(sl);
+        std::swap(X, tmpX);
+      } else {
+        encode_slots(sl);
+      }
+    }
+    new_slots = sl;
+  }
+
+  void remove(uint64_t id) {
+    auto it = by_id.find(id);
+    if (it == by_id.end()) raise(PXG_ERR_UNKNOWN_ID, "unknown vector id " + std::to_string(id), id);
+    const uint32_t s = it->second;
+    by_id.erase(it);
+    live[s] = 0;
+    list_of_h[s] = UNASSIGNED;
+    slots.release(s);
+    const uint32_t un = UNASSIGNED;
+    PXG_HIP(hipMemsetAsync(d_live.p + s, 0, 1, stream));
+    PXG_HIP(hipMemcpyAsync(d_list_of.p + s, &un, 4, hipMemcpyHostToDevice, stream));
+    PXG_HIP(hipStreamSynchronize(stream));
+    rank_dirty = true;
+    csr_dirty = true;
+  }
+
+  void search_device(const float* d_raw, bool do_prepare, uint64_t nq, uint64_t k, uint64_t nprobe_in,
+                     const uint8_t* d_accept, uint64_t* d_oid, float* d_od, uint32_t* d_oc, Ctx* ctx, hipStream_t s) {
+    check_k(k);
+    if (nq == 0) return;
+    if (k == 0 || by_id.empty()) {
+      PXG_HIP(hipMemsetAsync(d_oc, 0, nq * 4, s));
+      PXG_HIP(hipStreamSynchronize(s));
+      return;
+    }
+    refresh(s);
+    Timer tm(s);
+    tm.mark(0);
+    float* Qp = (float*)ctx->get(1, nq * ld * 4);
+    float* qb = (float*)ctx->get(2, nq * 4);
+    float* qn = (float*)ctx->get(3, nq * 4);
+    unsigned long long* bad = (unsigned long long*)ctx->get(4, 16);
+    int* flag_count = (int*)(bad + 1);
+    PXG_HIP(hipMemsetAsync(bad, 0xFF, 8, s));
+    hipLaunchKernelGGL(flat_prep_queries, dim3((unsigned)nq), dim3(64), 0, s, d_raw, (int)dim, (int)ld, metric,
+                       do_prepare ? 1 : 0, Qp, qb, qn, bad);
+    PXG_HIP(hipGetLastError());
+    const size_t N = slots.high_water();
+    if (!trained) {
+      // untrained: exact exhaustive scan (ivfpq.rs:1008-1012, 1113-1125)
+      if (k > 1024) config_error("k", k, "the GPU IVF-PQ search supports k up to 1024 per query");
+      int* qlist = (int*)ctx->get(5, nq * 4);
+      hipLaunchKernelGGL(iota_kernel, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s, qlist, (int)nq,
+                         flag_count);
+      const int nchunks = (int)((N + EXACT_CH - 1) / EXACT_CH);
+      const int kk = (int)std::min<uint64_t>(k, EXACT_CH);
+      uint64_t* ecand = (uint64_t*)ctx->get(7, (size_t)nq * nchunks * kk * 8);
+      tm.mark(1);
+      hipLaunchKernelGGL(flat_exact_candidates, dim3(std::min<int>((int)nq * nchunks, 4096)), dim3(256), 0, s, qlist,
+                         flag_count, nchunks, Qp, (int)ld, (int)dim, metric, X.p, (int)N, d_live.p, d_accept,
+                         d_rank.p, (int)k, ecand);
+      PXG_HIP(hipGetLastError());
+      tm.mark(2);
+      hipLaunchKernelGGL(flat_merge_exact, dim3((unsigned)nq), dim3(256), 0, s, qlist, flag_count, ecand, nchunks,
+                         (int)k, d_rank_slot.p, d_ids.p, d_oid, d_od, d_oc);
+      PXG_HIP(hipGetLastError());
+    } else {
+      const int np = (int)std::min<uint64_t>(std::max<uint64_t>(nprobe_in, 1), (uint64_t)std::max(produced, 1));
+      const bool rerank = cfg.rerank > 0 && vectors_kept;
+      const uint64_t shortlist = cfg.rerank > 0 ? std::max<uint64_t>(cfg.rerank, k) : k;
+      if (shortlist > IVF_MAX_SHORT)
+        config_error("k", shortlist, "the GPU IVF-PQ shortlist (max(rerank, k)) is limited to 960");
+      const int kk = (int)shortlist;
+      uint64_t* ck = (uint64_t*)ctx->get(8, (size_t)nq * produced * 8);
+      int* probes = (int*)ctx->get(9, (size_t)nq * np * 4);
+      tm.mark(0);
+      hipLaunchKernelGGL(ivf_coarse_keys, dim3((unsigned)nq), dim3(256), 0, s, Qp, (int)ld, (int)dim, cents.p,
+                         produced, ck);
+      hipLaunchKernelGGL(ivf_coarse_select, dim3((unsigned)nq), dim3(256), 0, s, ck, produced, np, probes);
+      PXG_HIP(hipGetLastError());
+      uint64_t* cand = (uint64_t*)ctx->get(10, (size_t)nq * np * 4 * kk * 8);
+      const size_t lds = (size_t)M() * 256 * 4;
+      const int grid = (int)(nq * np);
+      tm.mark(1);
+#define PXG_SCAN(CAPW, MET)                                                                                       \
+  hipLaunchKernelGGL((ivf_scan<CAPW, MET>), dim3(grid), dim3(256), lds, s, Qp, (int)ld, (int)dim, (int)M(), probes, \
+                     np, cents.p, books.p, d_sub_off.p, d_book_off.p, list_off.p, list_rank.p, list_codes.p,       \
+                     d_rank_slot.p, d_accept, kk, cand)
+      if (kk <= 192) {
+        if (metric == PXG_COSINE) PXG_SCAN(256, 1); else PXG_SCAN(256, 0);
+      } else if (kk <= 448) {
+        if (metric == PXG_COSINE) PXG_SCAN(512, 1); else PXG_SCAN(512, 0);
+      } else {
+        if (metric == PXG_COSINE) PXG_SCAN(1024, 1); else PXG_SCAN(1024, 0);
+      }
+#undef PXG_SCAN
+      PXG_HIP(hipGetLastError());
+      tm.mark(2);
+      hipLaunchKernelGGL(ivf_merge, dim3((unsigned)nq), dim3(256), 0, s, cand, np * 4 * kk, kk, (int)k,
+                         rerank ? 1 : 0, Qp, (int)ld, (int)dim, metric, X.p, d_rank_slot.p, d_ids.p, d_oid, d_od,
+                         d_oc);
+      PXG_HIP(hipGetLastError());
+    }
+    unsigned long long badv = 0;
+    PXG_HIP(hipMemcpyAsync(&badv, bad, 8, hipMemcpyDeviceToHost, s));
+    PXG_HIP(hipStreamSynchronize(s));
+    tm.finish();
+    if (badv != ~0ull) {
+      const uint32_t qi = (uint32_t)(badv >> 32), comp = (uint32_t)badv;
+      raise(PXG_ERR_NON_FINITE,
+            "vector component " + std::to_string(comp) + " is not finite (query " + std::to_string(qi) + ")", comp,
+            qi, NAN);
+    }
+  }
+};
+
+// IvfPqConfig::validate (ivfpq.rs:259-304)
+void validate_config(const pxg_ivfpq_config& c, uint32_t dim) {
+  if (c.nlist == 0) config_error("nlist", c.nlist, "must be at least 1");
+  if (c.subspaces == 0 || c.subspaces > dim) config_error("subspaces", c.subspaces, "must be between 1 and the space dimension");
+  if (c.nprobe == 0 || c.nprobe > c.nlist) config_error("nprobe", c.nprobe, "must be between 1 and nlist");
+  if (c.max_iterations == 0) config_error("max_iterations", c.max_iterations, "must be at least 1");
+  if (c.training_sample == 0) config_error("training_sample", c.training_sample, "must be at least 1");
+  if (c.rerank > 0 && !c.retain_vectors)
+    config_error("rerank", c.rerank, "requires retain_vectors, because reranking is against the exact vectors");
+  if (c.subspaces > IVF_MAX_M) config_error("subspaces", c.subspaces, "the GPU distance table holds at most 128 subspaces");
+}
+
+}  // namespace pxg
+
+using pxg::IvfPqIndex;
+
+struct pxg_ivfpq {
+  IvfPqIndex impl;
+};
+
+extern "C" {
+
+int pxg_ivfpq_config_default(uint64_t nlist, uint64_t subspaces, pxg_ivfpq_config* out) {
+  return pxg::guard([&] {
+    // IvfPqConfig::new (ivfpq.rs:124-150)
+    out->nlist = nlist;
+    out->subspaces = subspaces;
+    out->nprobe = std::max<uint64_t>(nlist / 16, 1);
+    out->rerank = 0;
+    out->seed = 0x1FF9C0D;
+    out->max_iterations = 25;
+    out->training_sample = 100000;
+    out->train_threshold = nlist > UINT64_MAX / 100 ? UINT64_MAX : nlist * 100;
+    out->retain_vectors = 1;
+  });
+}
+
+int pxg_ivfpq_create(uint32_t dim, int metric, const pxg_ivfpq_config* cfg, pxg_ivfpq** out) {
+  return pxg::guard([&] {
+    if (dim < 1) pxg::config_error("dim", dim, "must be at least 1; a 0-dimensional space makes all distances equal");
+    if (dim > (1u << 20)) pxg::config_error("dim", dim, "exceeds the 1048576 dimension ceiling");
+    if (metric != PXG_EUCLIDEAN && metric != PXG_COSINE)
+      pxg::config_error("metric", (uint64_t)metric, "IVF-PQ supports euclidean and cosine only; see the module docs");
+    pxg::validate_config(*cfg, dim);
+    auto* h = new pxg_ivfpq();
+    IvfPqIndex& f = h->impl;
+    f.dim = dim;
+    f.ld = (dim + 3) & ~3u;
+    f.metric = metric;
+    f.cfg = *cfg;
+    f.pq.build((int)dim, (int)cfg->subspaces);
+    try {
+      PXG_HIP(hipStreamCreateWithFlags(&f.stream, hipStreamNonBlocking));
+      f.d_sub_off.alloc(f.pq.M + 1);
+      f.d_book_off.alloc(f.pq.M + 1);
+      PXG_HIP(hipMemcpy(f.d_sub_off.p, f.pq.off.data(), (f.pq.M + 1) * 4, hipMemcpyHostToDevice));
+      PXG_HIP(hipMemcpy(f.d_book_off.p, f.pq.book_off.data(), (f.pq.M + 1) * 4, hipMemcpyHostToDevice));
+    } catch (...) {
+      delete h;
+      throw;
+    }
+    *out = h;
+  });
+}
+
+void pxg_ivfpq_destroy(pxg_ivfpq* index) { delete index; }
+
+int pxg_ivfpq_insert(pxg_ivfpq* index, const uint64_t* ids, const float* vectors, uint64_t n, uint32_t* out_slots) {
+  return pxg::guard([&] {
+    if (n == 0) return;
+    std::unique_lock<std::shared_mutex> lk(index->impl.mu);
+    IvfPqIndex& f = index->impl;
+    // Auto-training fires when the live count reaches train_threshold
+    // (ivfpq.rs:1154-1156): split the batch at that insert.
+    uint64_t done = 0;
+    while (done < n) {
+      uint64_t take = n - done;
+      if (!f.trained && f.cfg.train_threshold > f.by_id.size() && f.cfg.train_threshold - f.by_id.size() < take)
+        take = f.cfg.train_threshold - f.by_id.size();
+      std::vector<uint32_t> sl;
+      f.insert_rows(ids + done, vectors + done * f.dim, take, out_slots ? out_slots + done : nullptr, sl);
+      done += take;
+      if (!f.trained && f.by_id.size() >= f.cfg.train_threshold) {
+        lk.unlock();
+        int st = pxg_ivfpq_train(index, nullptr);
+        lk.lock();
+        if (st != PXG_OK) throw pxg::Raise{pxg::Error{st, pxg_last_error_message()}};
+      }
+    }
+  });
+}
+
+int pxg_ivfpq_train(pxg_ivfpq* index, pxg_training_report* report) {
+  return pxg::guard([&] {
+    std::unique_lock<std::shared_mutex> lk(index->impl.mu);
+    pxg_training_report r = index->impl.train();
+    if (report) *report = r;
+  });
+}
+
+int pxg_ivfpq_training_report(const pxg_ivfpq* index, pxg_training_report* report) {
+  return pxg::guard([&] {
+    std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+    if (!index->impl.has_report) pxg::config_error("trained", 0, "the index has not been trained");
+    *report = index->impl.report;
+  });
+}
+
+int pxg_ivfpq_remove(pxg_ivfpq* index, uint64_t id) {
+  return pxg::guard([&] {
+    std::unique_lock<std::shared_mutex> lk(index->impl.mu);
+    index->impl.remove(id);
+  });
+}
+
+int pxg_ivfpq_contains(const pxg_ivfpq* index, uint64_t id) {
+  std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+  return index->impl.by_id.count(id) ? 1 : 0;
+}
+
+uint64_t pxg_ivfpq_len(const pxg_ivfpq* index) {
+  std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+  return index->impl.by_id.size();
+}
+
+int pxg_ivfpq_is_trained(const pxg_ivfpq* index) {
+  std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+  return index->impl.trained ? 1 : 0;
+}
+
+int pxg_ivfpq_stats(const pxg_ivfpq* index, pxg_index_stats* out) {
+  return pxg::guard([&] {
+    std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+    const IvfPqIndex& f = index->impl;
+    out->len = f.by_id.size();
+    out->deleted = 0;
+    out->dim = f.dim;
+    out->metric = f.metric;
+    out->layers = 1;
+    out->edges = 0;
+    out->vector_bytes = f.vectors_kept ? f.X.bytes() : 0;
+    // codes, lists and codebooks (ivfpq.rs:575-588, 1207-1212)
+    out->graph_bytes = f.codes.bytes() + f.d_list_of.bytes() + f.list_rank.bytes() + f.list_off.bytes() +
+                       f.list_codes.bytes() + f.cents.bytes() + f.books.bytes();
+  });
+}
+
+int pxg_ivfpq_get_vector(const pxg_ivfpq* index, uint64_t id, float* out) {
+  return pxg::guard([&] {
+    std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+    const IvfPqIndex& f = index->impl;
+    auto it = f.by_id.find(id);
+    if (it == f.by_id.end()) pxg::raise(PXG_ERR_UNKNOWN_ID, "unknown vector id " + std::to_string(id), id);
+    if (!f.vectors_kept)
+      pxg::config_error("retain_vectors", 0, "the full-precision vectors were dropped after training");
+    PXG_HIP(hipMemcpy(out, f.X.p + (size_t)it->second * f.ld, f.dim * 4, hipMemcpyDeviceToHost));
+  });
+}
+
+uint64_t pxg_ivfpq_slot_count(const pxg_ivfpq* index) {
+  std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+  return index->impl.slots.high_water();
+}
+
+int pxg_ivfpq_slots(const pxg_ivfpq* index, uint64_t* ids, uint8_t* live) {
+  return pxg::guard([&] {
+    std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+    const IvfPqIndex& f = index->impl;
+    for (size_t s = 0; s < f.slots.high_water(); ++s) {
+      if (ids) ids[s] = f.live[s] ? f.ids[s] : 0;
+      if (live) live[s] = f.live[s];
+    }
+  });
+}
+
+uint64_t pxg_ivfpq_list_count(const pxg_ivfpq* index) {
+  std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+  return index->impl.trained ? (uint64_t)index->impl.produced : (uint64_t)index->impl.cfg.nlist;
+}
+
+int pxg_ivfpq_list_lengths(const pxg_ivfpq* index, uint64_t* out) {
+  return pxg::guard([&] {
+    std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+    const IvfPqIndex& f = index->impl;
+    const size_t nl = f.trained ? (size_t)f.produced : (size_t)f.cfg.nlist;
+    std::vector<uint64_t> cnt(nl, 0);
+    for (size_t s = 0; s < f.slots.high_water(); ++s)
+      if (f.live[s] && f.list_of_h[s] != pxg::UNASSIGNED) cnt[f.list_of_h[s]]++;
+    for (size_t l = 0; l < nl; ++l) out[l] = cnt[l];
+  });
+}
+
+// Download the trained parts (IvfPqIndex::parts, ivfpq.rs:606-617).
+int pxg_ivfpq_parts(const pxg_ivfpq* index, float* centroids, float* codebooks, uint8_t* codes, uint32_t* list_of) {
+  return pxg::guard([&] {
+    std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+    const IvfPqIndex& f = index->impl;
+    if (!f.trained) pxg::config_error("trained", 0, "the index has no codebooks yet");
+    const size_t hw = f.slots.high_water();
+    if (centroids)
+      PXG_HIP(hipMemcpy2D(centroids, f.dim * 4, f.cents.p, f.ld * 4, f.dim * 4, f.produced, hipMemcpyDeviceToHost));
+    if (codebooks) PXG_HIP(hipMemcpy(codebooks, f.books.p, f.pq.book_off[f.pq.M] * 4, hipMemcpyDeviceToHost));
+    if (codes && hw) PXG_HIP(hipMemcpy(codes, f.codes.p, hw * f.M(), hipMemcpyDeviceToHost));
+    if (list_of)
+      for (size_t s = 0; s < hw; ++s) list_of[s] = f.list_of_h[s];
+  });
+}
+
+// IvfPqIndex::from_parts (ivfpq.rs:624-717): install a trained state on an
+// index whose vectors are already inserted (slot table from inserts). codes
+// and list_of cover slot_count() slots; NULL codes means "encode on device".
+int pxg_ivfpq_load_trained(pxg_ivfpq* index, const float* centroids, uint64_t produced, const float* codebooks,
+                           const uint8_t* codes, const uint32_t* list_of) {
+  return pxg::guard([&] {
+    std::unique_lock<std::shared_mutex> lk(index->impl.mu);
+    IvfPqIndex& f = index->impl;
+    if (produced == 0 || produced > f.cfg.nlist) pxg::config_error("produced", produced, "must be between 1 and nlist");
+    f.upload_books(centroids, (int)produced, codebooks);
+    const size_t hw = f.slots.high_water();
+    if (codes) {
+      for (size_t s = 0; s < hw; ++s) {
+        if (f.live[s] && list_of[s] != pxg::UNASSIGNED && list_of[s] >= produced)
+          pxg::raise(PXG_ERR_CORRUPTION, "corrupt ivfpq index: slot " + std::to_string(s) + " names list " +
+                                             std::to_string(list_of[s]) + " of " + std::to_string(produced));
+        f.list_of_h[s] = f.live[s] ? list_of[s] : pxg::UNASSIGNED;
+      }
+      if (hw) {
+        PXG_HIP(hipMemcpy(f.codes.p, codes, hw * f.M(), hipMemcpyHostToDevice));
+        PXG_HIP(hipMemcpy(f.d_list_of.p, f.list_of_h.data(), hw * 4, hipMemcpyHostToDevice));
+      }
+      f.csr_dirty = true;
+    } else {
+      std::vector<uint32_t> sl;
+      for (size_t s = 0; s < hw; ++s)
+        if (f.live[s]) sl.push_back((uint32_t)s);
+      f.encode_slots(sl);
+    }
+  });
+}
+
+int pxg_ivfpq_search(const pxg_ivfpq* index, const float* queries, uint64_t nq, uint64_t k, uint64_t nprobe,
+                     const uint8_t* accept, uint64_t* out_ids, float* out_dist, uint32_t* out_count) {
+  return pxg::guard([&] {
+    pxg::check_k(k);
+    IvfPqIndex& f = const_cast<IvfPqIndex&>(index->impl);
+    std::shared_lock<std::shared_mutex> lk(f.mu);
+    if (nq == 0) return;
+    std::vector<float> prep((size_t)nq * f.dim);
+    for (uint64_t i = 0; i < nq; ++i) {
+      long long bad = pxg::validate_prepare(f.metric, queries + i * f.dim, f.dim, prep.data() + i * f.dim);
+      if (bad >= 0)
+        pxg::raise(PXG_ERR_NON_FINITE,
+                   "vector component " + std::to_string(bad) + " is not finite (" +
+                       std::to_string(queries[i * f.dim + bad]) + ")",
+                   (uint64_t)bad, i, queries[i * f.dim + bad]);
+    }
+    if (k == 0 || f.by_id.empty()) {
+      for (uint64_t i = 0; i < nq; ++i) out_count[i] = 0;
+      return;
+    }
+    pxg::CtxLease ctx(f.pool);
+    hipStream_t s = ctx->stream;
+    const size_t N = f.slots.high_water();
+    float* d_q = (float*)ctx->get(20, prep.size() * 4);
+    uint8_t* d_acc = nullptr;
+    if (accept) {
+      d_acc = ctx->get(21, N);
+      PXG_HIP(hipMemcpyAsync(d_acc, accept, N, hipMemcpyHostToDevice, s));
+    }
+    uint64_t* d_oid = (uint64_t*)ctx->get(22, nq * k * 8);
+    float* d_od = (float*)ctx->get(23, nq * k * 4);
+    uint32_t* d_oc = (uint32_t*)ctx->get(24, nq * 4);
+    PXG_HIP(hipMemcpyAsync(d_q, prep.data(), prep.size() * 4, hipMemcpyHostToDevice, s));
+    f.search_device(d_q, false, nq, k, nprobe ? nprobe : f.cfg.nprobe, d_acc, d_oid, d_od, d_oc, ctx.c, s);
+    PXG_HIP(hipMemcpyAsync(out_ids, d_oid, nq * k * 8, hipMemcpyDeviceToHost, s));
+    PXG_HIP(hipMemcpyAsync(out_dist, d_od, nq * k * 4, hipMemcpyDeviceToHost, s));
+    PXG_HIP(hipMemcpyAsync(out_count, d_oc, nq * 4, hipMemcpyDeviceToHost, s));
+    PXG_HIP(hipStreamSynchronize(s));
+  });
+}
+
+int pxg_ivfpq_search_device(const pxg_ivfpq* index, const float* d_queries, uint64_t nq, uint64_t k, uint64_t nprobe,
+                            const uint8_t* d_accept, uint64_t* d_out_ids, float* d_out_dist, uint32_t* d_out_count,
+                            void* stream) {
+  return pxg::guard([&] {
+    IvfPqIndex& f = const_cast<IvfPqIndex&>(index->impl);
+    std::shared_lock<std::shared_mutex> lk(f.mu);
+    pxg::CtxLease ctx(f.pool);
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    f.search_device(d_queries, true, nq, k, nprobe ? nprobe : f.cfg.nprobe, d_accept, d_out_ids, d_out_dist,
+                    d_out_count, ctx.c, s);
+    PXG_HIP(hipStreamSynchronize(s));
+  });
+}
+
+}  // extern "C"

@@ -302,3 +302,16 @@ def test_insert_device_matches_host_insert(gpu):
     with pytest.raises(px.NonFinite):
         b.insert_device(np.arange(100_000, 100_010, dtype=np.uint64), bad)
     assert len(b) == 5000
+
+
+def test_growth_preserves_contents(gpu):
+    px = gpu
+    rng = np.random.default_rng(21)
+    data = rng.standard_normal((5000, 24)).astype(np.float32)
+    idx = px.FlatIndex(px.VectorSpace(24, 0))  # capacity 0: grows 1024 -> 2048 -> 4096 -> 8192
+    for a in range(0, 5000, 700):
+        idx.insert_batch(np.arange(a, min(a + 700, 5000), dtype=np.uint64), data[a:a + 700])
+    for i in (0, 1023, 1024, 2047, 4999):
+        assert np.array_equal(idx.vector(i), data[i])
+    q = rng.standard_normal((20, 24)).astype(np.float32)
+    assert_same(idx.search_batch(q, 15), oracle_search(px, data, np.arange(5000), 0, q, 15))

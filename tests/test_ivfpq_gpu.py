@@ -1,0 +1,251 @@
+"""GPU IVF-PQ against the oracle and the reference's ivfpq.rs tests.
+
+Parity bar: with the same trained parts (centroids, codebooks, codes) the
+GPU search returns the oracle's ids and ADC distances bit for bit (the coarse
+stage, the distance tables and the ADC sums follow the reference's operation
+order), with and without exact rerank, for L2 and cosine, with filters and
+removals; and GPU training from the same seed reproduces the oracle's
+centroids, codebooks, codes and list assignment."""
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def corpus(count, dim, clusters):  # ivfpq.rs:1264-1276 (numpy f32 sin/cos)
+    i = np.arange(count)[:, None].astype(np.float32)
+    d = np.arange(dim)[None, :].astype(np.float32)
+    cl = (np.arange(count) % clusters)[:, None].astype(np.float32)
+    step = (np.arange(count) // clusters)[:, None].astype(np.float32)
+    v = np.sin(cl * np.float32(1.7) + d * np.float32(0.11)) * np.float32(5.0) + \
+        np.cos(step * np.float32(0.013) * (d + np.float32(1.0)))
+    del i
+    return v.astype(np.float32)
+
+
+def build(px, data, config, metric=0):
+    space = px.VectorSpace(data.shape[1], metric)
+    idx = px.IvfPqIndex(space, config)
+    idx.insert_batch(np.arange(data.shape[0], dtype=np.uint64), data)
+    return idx
+
+
+def assert_same(got, want):
+    gi, gd, gc = got
+    wi, wd, wc = want
+    assert np.array_equal(gc, wc), (gc, wc)
+    for q in range(gc.size):
+        c = int(gc[q])
+        assert np.array_equal(gi[q, :c], wi[q, :c]), (q, gi[q, :c], wi[q, :c], gd[q, :c], wd[q, :c])
+        assert np.array_equal(gd[q, :c].view(np.uint32), wd[q, :c].view(np.uint32)), (q, gd[q, :c], wd[q, :c])
+
+
+@pytest.mark.parametrize("metric", [0, 1])
+@pytest.mark.parametrize("rerank", [0, 50])
+def test_search_parity_on_oracle_parts(gpu, metric, rerank):
+    px = gpu
+    n, dim, nlist, m = 3000, 32, 32, 16
+    data = corpus(n, dim, 24) + np.random.default_rng(1).standard_normal((n, dim)).astype(np.float32) * 0.3
+    prep = orc.prepare_rows(metric, data)
+    cents, books, _ = orc.ivf_train(prep, nlist, m, max_iter=10, seed=5)
+    codes, list_of = orc.ivf_encode(prep, cents, books, m)
+    cfg = px.IvfPqConfig(nlist, m).with_train_threshold(1 << 62).with_rerank(rerank).with_seed(5)
+    idx = build(px, data, cfg, metric)
+    idx.load_trained(cents, books, codes, list_of)
+    q = data[::97] + 0.05
+    qp = orc.prepare_rows(metric, q)
+    for nprobe in (1, 4, 32):
+        for k in (1, 10, 40):
+            got = idx.search_batch(q, k, nprobe=nprobe)
+            want = orc.ivf_search(metric, cents, books, codes, list_of, np.arange(n), qp, k, nprobe, m,
+                                  vectors=prep if rerank else None, rerank=rerank, threads=8)
+            assert_same(got, want)
+
+
+def test_search_parity_with_removals_filter_and_reinsert(gpu):
+    px = gpu
+    n, dim, nlist, m = 2500, 16, 16, 8
+    data = corpus(n, dim, 20)
+    cents, books, _ = orc.ivf_train(data, nlist, m, max_iter=8, seed=3)
+    codes, list_of = orc.ivf_encode(data, cents, books, m)
+    idx = build(px, data, px.IvfPqConfig(nlist, m).with_train_threshold(1 << 62))
+    idx.load_trained(cents, books, codes, list_of)
+    live = np.ones(n, np.uint8)
+    for i in range(0, n, 7):
+        idx.remove(i)
+        live[i] = 0
+    q = data[3::50] + 0.1
+    want = orc.ivf_search(0, cents, books, codes, list_of, np.arange(n), q, 10, 6, m, live=live, threads=8)
+    assert_same(idx.search_batch(q, 10, nprobe=6), want)
+    acc = np.array([i % 3 == 0 for i in range(n)], np.uint8)
+    want = orc.ivf_search(0, cents, books, codes, list_of, np.arange(n), q, 10, 6, m, live=live, accept=acc,
+                          threads=8)
+    assert_same(idx.search_batch(q, 10, lambda i, _m: i % 3 == 0, nprobe=6), want)
+    # re-insert into the freed slots: encoded on the GPU exactly like encode_slot
+    new = data[: n // 7 + 1] * 1.01
+    new_ids = np.arange(10_000, 10_000 + new.shape[0], dtype=np.uint64)
+    slots = idx.insert_batch(new_ids, new)
+    data2, ids2 = data.copy(), np.arange(n, dtype=np.uint64)
+    for s, i, v in zip(slots, new_ids, new):
+        data2[s], ids2[s], live[s] = v, i, 1
+    codes2, list_of2 = orc.ivf_encode(data2, cents, books, m, live=live)
+    _, _, gc, glo = idx.parts()
+    assert np.array_equal(glo[live.astype(bool)], list_of2[live.astype(bool)])
+    assert np.array_equal(gc[live.astype(bool)], codes2[live.astype(bool)])
+    want = orc.ivf_search(0, cents, books, codes2, list_of2, ids2, q, 10, 6, m, live=live, threads=8)
+    assert_same(idx.search_batch(q, 10, nprobe=6), want)
+
+
+@pytest.mark.parametrize("metric", [0, 1])
+def test_gpu_training_matches_oracle(gpu, metric):
+    px = gpu
+    n, dim, nlist, m = 4000, 32, 24, 8
+    data = corpus(n, dim, 24) + np.random.default_rng(2).standard_normal((n, dim)).astype(np.float32) * 0.2
+    prep = orc.prepare_rows(metric, data)
+    cfg = px.IvfPqConfig(nlist, m).with_train_threshold(1 << 62).with_seed(11).with_max_iterations(12) \
+        .with_training_sample(1500)
+    idx = build(px, data, cfg, metric)
+    rep = idx.train()
+    cents, books, report = orc.ivf_train(prep, nlist, m, max_iter=12, training_sample=1500, seed=11)
+    gcents, gbooks, gcodes, glist = idx.parts()
+    assert np.array_equal(gcents.view(np.uint32), cents.view(np.uint32))
+    assert np.array_equal(gbooks.view(np.uint32), books.view(np.uint32))
+    codes, list_of = orc.ivf_encode(prep, cents, books, m)
+    assert np.array_equal(gcodes, codes) and np.array_equal(glist, list_of)
+    assert rep.sampled == int(report[3]) and rep.coarse_iterations == int(report[1])
+    assert rep.coarse_inertia == report[0] and rep.residual_inertia == report[2]
+    q = data[5::111]
+    want = orc.ivf_search(metric, cents, books, codes, list_of, np.arange(n), orc.prepare_rows(metric, q), 10, 3, m,
+                          threads=8)
+    assert_same(idx.search_batch(q, 10, nprobe=3), want)
+
+
+# --- ivfpq.rs:1282-1654 -------------------------------------------------------------
+def test_rejects_metrics_it_cannot_serve(gpu):
+    px = gpu
+    for metric in (px.Metric.INNER_PRODUCT, px.Metric.MANHATTAN):
+        with pytest.raises(px.Configuration) as e:
+            px.IvfPqIndex(px.VectorSpace(8, metric), px.IvfPqConfig(4, 4))
+        assert "metric" in str(e.value)
+
+
+def test_untrained_index_is_exact(gpu):
+    px = gpu
+    data = corpus(200, 16, 24)
+    idx = build(px, data, px.IvfPqConfig(8, 4).with_train_threshold(1 << 62))
+    flat = px.FlatIndex(px.VectorSpace(16, 0))
+    flat.insert_batch(np.arange(200, dtype=np.uint64), data)
+    assert not idx.is_trained()
+    for q in data[:10]:
+        assert idx.search_all(q, 5) == flat.search_all(q, 5)
+
+
+def test_training_populates_lists_and_auto_training(gpu):
+    px = gpu
+    idx = build(px, corpus(1000, 16, 24), px.IvfPqConfig(16, 8).with_seed(3).with_train_threshold(1 << 62))
+    rep = idx.train()
+    assert idx.is_trained() and rep.sampled == 1000 and rep.populated_lists > 1
+    assert sum(idx.list_lengths()) == 1000 and idx.code_bytes_per_vector() == 8
+    space = px.VectorSpace(8, 0)
+    auto = px.IvfPqIndex(space, px.IvfPqConfig(4, 4).with_train_threshold(50))
+    for i, v in enumerate(corpus(60, 8, 6)):
+        auto.insert(i, v)
+        assert auto.is_trained() == (i + 1 >= 50)
+    assert sum(auto.list_lengths()) == 60
+    batch = px.IvfPqIndex(space, px.IvfPqConfig(4, 4).with_train_threshold(50))
+    batch.insert_batch(np.arange(60, dtype=np.uint64), corpus(60, 8, 6))  # splits at the threshold
+    assert batch.is_trained() and sum(batch.list_lengths()) == 60
+    for a, b in zip(auto.parts(), batch.parts()):
+        assert np.array_equal(a, b)
+
+
+def test_recall_monotone_in_nprobe_and_rerank_helps(gpu):
+    px = gpu
+    data = corpus(2000, 32, 24)
+    idx = build(px, data, px.IvfPqConfig(32, 16).with_seed(11).with_train_threshold(1 << 62))
+    idx.train()
+    flat = px.FlatIndex(px.VectorSpace(32, 0))
+    flat.insert_batch(np.arange(2000, dtype=np.uint64), data)
+    qs = data[::40]
+    truth = [set(h.id for h in flat.search_all(q, 10)) for q in qs]
+    prev = 0.0
+    for nprobe in (1, 4, 16, 32):
+        hits = sum(len(t & set(h.id for h in idx.search_with_nprobe(q, 10, nprobe))) for q, t in zip(qs, truth))
+        recall = hits / (10 * len(qs))
+        assert recall + 0.02 >= prev
+        prev = recall
+    assert prev > 0.4
+    base = px.IvfPqConfig(32, 8).with_seed(7).with_nprobe(8).with_train_threshold(1 << 62)
+    plain = build(px, data, base.clone())
+    plain.train()
+    rr = build(px, data, base.clone().with_rerank(100))
+    rr.train()
+
+    def measure(ix):
+        return sum(len(t & set(h.id for h in ix.search_all(q, 10))) for q, t in zip(qs, truth)) / (10 * len(qs))
+    assert measure(rr) > measure(plain)
+
+
+def test_dropping_vectors_and_retrain_refused(gpu):
+    px = gpu
+    idx = build(px, corpus(1000, 64, 24),
+                px.IvfPqConfig(16, 8).with_seed(2).with_retain_vectors(False).with_train_threshold(1 << 62))
+    idx.train()
+    assert idx.vector_bytes() == 0 and idx.vector(0) is None
+    assert idx.compressed_bytes() / len(idx) < 256
+    assert len(idx.search_all(np.zeros(64, np.float32), 5)) == 5
+    idx.insert(9999, np.ones(64, np.float32))
+    assert idx.vector_bytes() == 0 and idx.contains(9999)
+    with pytest.raises(px.Configuration) as e:
+        idx.train()
+    assert "retain_vectors" in str(e.value)
+
+
+def test_remove_takes_slot_out_of_its_list(gpu):
+    px = gpu
+    idx = build(px, corpus(400, 16, 24), px.IvfPqConfig(8, 4).with_seed(1).with_train_threshold(1 << 62))
+    idx.train()
+    before = sum(idx.list_lengths())
+    idx.remove(5)
+    assert sum(idx.list_lengths()) == before - 1 and not idx.contains(5)
+    assert all(h.id != 5 for h in idx.search_all(np.zeros(16, np.float32), 400))
+    with pytest.raises(px.UnknownId):
+        idx.remove(5)
+
+
+def test_filters_cosine_seed_duplicates_stats(gpu):
+    px = gpu
+    data = corpus(800, 16, 24)
+    idx = build(px, data, px.IvfPqConfig(16, 8).with_nprobe(16).with_seed(6).with_train_threshold(1 << 62))
+    idx.train()
+    for i in range(800):
+        idx.set_metadata(i, {"even": i % 2 == 0})
+    hits = idx.search(data[0], 10, lambda _i, m: m.get("even") is True)
+    assert len(hits) == 10 and all(h.id % 2 == 0 for h in hits)
+    # cosine within quantization error (ivfpq.rs:1574-1604)
+    cdata = corpus(1000, 32, 20)
+    space = px.VectorSpace(32, px.Metric.COSINE)
+    cidx = px.IvfPqIndex(space, px.IvfPqConfig(8, 16).with_nprobe(8).with_seed(9).with_train_threshold(1 << 62))
+    cidx.insert_batch(np.arange(1000, dtype=np.uint64), cdata)
+    cidx.train()
+    qp, _ = orc.prepare(orc.COSINE, cdata[3])
+    for h in cidx.search_all(cdata[3], 20):
+        exact = orc.space_distance(orc.COSINE, qp, cidx.vector(h.id))
+        assert abs(h.distance - exact) < 0.25
+    # same seed, same index
+    cfg = px.IvfPqConfig(16, 8).with_seed(42).with_train_threshold(1 << 62)
+    a, b = build(px, data, cfg.clone()), build(px, data, cfg.clone())
+    a.train()
+    b.train()
+    assert a.list_lengths() == b.list_lengths()
+    for q in data[::80]:
+        assert a.search_all(q, 10) == b.search_all(q, 10)
+    with pytest.raises(px.DuplicateId):
+        a.insert(0, data[0])
+    big = build(px, corpus(1000, 64, 24), px.IvfPqConfig(16, 8).with_seed(8).with_train_threshold(1 << 62))
+    big.train()
+    st = big.stats()
+    assert st.len == 1000 and st.dim == 64 and st.deleted == 0
+    assert st.graph_bytes >= 1000 * 8 and st.vector_bytes >= 1000 * 64 * 4

@@ -1,0 +1,131 @@
+"""GPU k-means and product-quantizer training/encoding against the oracle.
+
+With the same seed the GPU trainer must reproduce the oracle bit for bit:
+k-means++ picks (same ChaCha8 stream, same sequential f64 sums below 2^17
+points), Lloyd assignments, f64 centroid updates, empty-cluster reseeding,
+inertia and iteration counts; PQ codebooks and codes. Plus the reference's own
+kmeans.rs / product.rs tests."""
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def blobs():  # kmeans.rs:259-268
+    pts = []
+    for cx, cy in [(0.0, 0.0), (100.0, 0.0), (0.0, 100.0)]:
+        for i in range(30):
+            j = np.float32(i) * np.float32(0.01)
+            pts.append([np.float32(cx) + j, np.float32(cy) - j])
+    return np.array(pts, np.float32)
+
+
+def clustered(rng, n, dim, clusters, sigma):
+    c = rng.standard_normal((clusters, dim)).astype(np.float32) * 3
+    return (c[np.arange(n) % clusters] + sigma * rng.standard_normal((n, dim))).astype(np.float32)
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("n,dim,k,iters,seed", [(90, 2, 3, 25, 0x00C0FFEE), (3000, 8, 16, 25, 7),
+                                                (5000, 10, 40, 15, 3), (20000, 128, 64, 8, 11), (700, 5, 256, 25, 9)])
+def test_kmeans_bit_exact_vs_oracle(gpu, n, dim, k, iters, seed):
+    px = gpu
+    rng = np.random.default_rng(seed)
+    pts = blobs() if dim == 2 else clustered(rng, n, dim, max(k // 2, 2), 0.5)
+    got = px.kmeans(pts, dim, k, iters, seed)
+    want_c, want_in, want_it = orc.kmeans(pts, k, iters, seed)
+    assert got.iterations == want_it
+    assert np.array_equal(bits(got.centroids), bits(want_c.reshape(-1)))
+    assert got.inertia == want_in
+
+
+def test_lloyd_from_init_with_empty_clusters(gpu):
+    px = gpu
+    rng = np.random.default_rng(5)
+    pts = clustered(rng, 4000, 16, 8, 0.3)
+    init = pts[:12].copy()
+    init[3] += 1000.0  # attracts nothing -> farthest-point reseed
+    init[7] -= 1000.0
+    got = px.kmeans_lloyd(pts, init, 20)
+    want = orc.kmeans_lloyd(pts, init, 20)
+    assert np.array_equal(bits(got[0]), bits(want[0]))
+    assert np.array_equal(got[1], want[1])
+    assert got[2] == want[2] and got[3] == want[3]
+
+
+def test_kmeans_pp_picks_match(gpu):
+    px = gpu
+    rng = np.random.default_rng(6)
+    pts = clustered(rng, 6000, 24, 20, 0.4)
+    assert np.array_equal(bits(px.kmeans_pp(pts, 50, 1234)), bits(orc.kmeans_pp(pts, 50, 1234)))
+
+
+def test_assign_matches_oracle(gpu):
+    px = gpu
+    rng = np.random.default_rng(8)
+    for dim in (3, 8, 13, 128, 200):
+        p = rng.standard_normal((3000, dim)).astype(np.float32)
+        c = rng.standard_normal((77, dim)).astype(np.float32)
+        c[5] = c[9]  # duplicate centroid: ties go to the lower index
+        a, d = px.kmeans_assign(p, c)
+        wa, wd = orc.kmeans_assign(p, c)
+        assert np.array_equal(a, wa)
+        assert np.array_equal(bits(d), bits(wd))
+
+
+def test_reference_kmeans_properties(gpu):  # kmeans.rs:271-336
+    px = gpu
+    r = px.kmeans(blobs(), 2, 3, 25, 0x00C0FFEE)
+    found = sorted((int(round(x)), int(round(y))) for x, y in r.centroids.reshape(-1, 2))
+    assert found == [(0, 0), (0, 100), (100, 0)] and r.inertia < 1.4
+    assert px.kmeans(np.array([1, 2, 3, 4], np.float32), 2, 16, 25, 1).centroids.size == 4
+    ident = px.kmeans(np.full(64, 7.0, np.float32), 4, 8, 25, 1)
+    assert ident.inertia == 0.0 and np.all(ident.centroids == 7.0)
+    empty = px.kmeans(np.zeros(0, np.float32), 4, 8, 25, 1)
+    assert empty.iterations == 0 and empty.centroids.size == 4
+    prev = float("inf")
+    for cap in range(1, 8):
+        r = px.kmeans(blobs(), 2, 3, cap, 0x00C0FFEE)
+        assert r.inertia <= prev + 1e-9
+        prev = r.inertia
+
+
+def _lcg_clustered(dim, count, seed):  # product.rs:635-654
+    state = seed
+    mask = (1 << 64) - 1
+    out = np.zeros((count, dim), np.float32)
+    centres = [[np.float32((c * 7 + d * 3) % 11) for d in range(dim)] for c in range(8)]
+    for i in range(count):
+        for d in range(dim):
+            state = (state * 6_364_136_223_846_793_005 + 1) & mask
+            v = np.float32(np.float32(state >> 33) / np.float32(1 << 31)) - np.float32(0.5)
+            out[i, d] = centres[i % 8][d] + v * np.float32(0.4)
+    return out
+
+
+@pytest.mark.parametrize("dim,m,count,seed", [(32, 8, 512, 3), (10, 4, 300, 2), (8, 2, 3, 6), (64, 16, 400, 1)])
+def test_pq_train_and_encode_bit_exact(gpu, dim, m, count, seed):
+    px = gpu
+    t = _lcg_clustered(dim, count, seed)
+    space = px.VectorSpace(dim, px.Metric.EUCLIDEAN)
+    pq = px.ProductQuantizer.train(space, t, px.PqConfig(m).with_seed(7))
+    books, inertia, iters = orc.pq_train(t, m, 25, 7)
+    assert np.array_equal(bits(pq.codebooks), bits(books))
+    assert pq.training_inertia == inertia and pq.training_iterations == iters
+    assert np.array_equal(pq.encode(t), orc.pq_encode(books, dim, m, t))
+
+
+def test_pq_validation(gpu):  # product.rs:775-809
+    px = gpu
+    space = px.VectorSpace(8, px.Metric.EUCLIDEAN)
+    t = _lcg_clustered(8, 32, 7)
+    for bad in (px.PqConfig(0), px.PqConfig(9), px.PqConfig(2).with_max_iterations(0)):
+        with pytest.raises(px.Configuration):
+            px.ProductQuantizer.train(space, t, bad)
+    with pytest.raises(px.Configuration):
+        px.ProductQuantizer.train(space, np.array([1.0, 2.0], np.float32), px.PqConfig(2))
