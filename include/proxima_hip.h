@@ -179,6 +179,9 @@ void pxg_ivfpq_destroy(pxg_ivfpq* index);
  * validation; encodes when trained, auto-trains when the live count reaches
  * train_threshold (splitting the batch at that insert). */
 int pxg_ivfpq_insert(pxg_ivfpq* index, const uint64_t* ids, const float* vectors, uint64_t n, uint32_t* out_slots);
+/* Same, vectors in device memory (ids and out_slots on the host). */
+int pxg_ivfpq_insert_device(pxg_ivfpq* index, const uint64_t* ids, const float* d_vectors, uint64_t n,
+                            uint32_t* out_slots);
 /* VectorIndex::remove (ivfpq.rs:1160-1180). */
 int pxg_ivfpq_remove(pxg_ivfpq* index, uint64_t id);
 int pxg_ivfpq_contains(const pxg_ivfpq* index, uint64_t id);
@@ -213,6 +216,10 @@ int pxg_ivfpq_search(const pxg_ivfpq* index, const float* queries, uint64_t nq, 
 int pxg_ivfpq_search_device(const pxg_ivfpq* index, const float* d_queries, uint64_t nq, uint64_t k, uint64_t nprobe,
                             const uint8_t* d_accept, uint64_t* d_out_ids, float* d_out_dist, uint32_t* d_out_count,
                             void* stream);
+
+/* Code entries (M bytes + a 4-byte id rank each) the last search on this
+ * thread streamed: the scan's algorithmic traffic. No reference counterpart. */
+uint64_t pxg_ivfpq_last_scanned(void);
 
 /* ------------------------------------------------------------------------ */
 /* k-means and the product quantizer (crates/proxima-quantize).              */

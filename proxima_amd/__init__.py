@@ -502,6 +502,21 @@ class IvfPqIndex(_IndexBase):
         _check(_lib.pxg_ivfpq_insert(self._h, _ptr(ids), _ptr(v), ids.size, _ptr(slots)))
         return slots
 
+    def insert_device(self, ids, vectors):
+        """Bulk insert from a contiguous GPU tensor [n, dim] (ids on the host)."""
+        ids = np.ascontiguousarray(ids, dtype=np.uint64).reshape(-1)
+        if vectors.shape[-1] != self.space.dim or vectors.shape[0] != ids.size:
+            raise DimensionMismatch("dimension mismatch: device batch does not match the index", self.space.dim,
+                                    vectors.shape[-1])
+        slots = np.zeros(ids.size, np.uint32)
+        _check(_lib.pxg_ivfpq_insert_device(self._h, _ptr(ids), _device_ptr(vectors), ids.size, _ptr(slots)))
+        return slots
+
+    @staticmethod
+    def last_scanned():
+        """Code entries streamed by the last search on this thread."""
+        return int(_lib.pxg_ivfpq_last_scanned())
+
     def remove(self, id):
         _check(_lib.pxg_ivfpq_remove(self._h, int(id)))
         self._meta.pop(int(id), None)

@@ -95,6 +95,7 @@ SIGNATURES = {
     "pxg_ivfpq_create": (_i32, [_u32, _i32, _P(IvfPqConfigC), _P(_vp)]),
     "pxg_ivfpq_destroy": (None, [_vp]),
     "pxg_ivfpq_insert": (_i32, [_vp, _vp, _vp, _u64, _vp]),
+    "pxg_ivfpq_insert_device": (_i32, [_vp, _vp, _vp, _u64, _vp]),
     "pxg_ivfpq_remove": (_i32, [_vp, _u64]),
     "pxg_ivfpq_contains": (_i32, [_vp, _u64]),
     "pxg_ivfpq_len": (_u64, [_vp]),
@@ -111,6 +112,7 @@ SIGNATURES = {
     "pxg_ivfpq_load_trained": (_i32, [_vp, _vp, _u64, _vp, _vp, _vp]),
     "pxg_ivfpq_search": (_i32, [_vp, _vp, _u64, _u64, _u64, _vp, _vp, _vp, _vp]),
     "pxg_ivfpq_search_device": (_i32, [_vp, _vp, _u64, _u64, _u64, _vp, _vp, _vp, _vp, _vp]),
+    "pxg_ivfpq_last_scanned": (_u64, []),
     # k-means / PQ
     "pxg_kmeans": (_i32, [_vp, _u64, _u32, _u64, _u64, _u64, _vp, _P(_f64), _P(_u64), _P(_u64)]),
     "pxg_kmeans_lloyd": (_i32, [_vp, _u64, _u32, _u64, _u64, _vp, _vp, _vp, _P(_f64), _P(_u64)]),
@@ -125,7 +127,7 @@ SIGNATURES = {
 def load():
     if not os.path.exists(LIB_PATH):
         raise ImportError(
-            f"{LIB_PATH} is missing: build it with `python -m proxima_amd.build` "
+            f"{LIB_PATH} is missing: build it with `python proxima_amd/build.py` "
             "(hipcc, gfx950). There is no CPU fallback.")
     lib = C.CDLL(LIB_PATH)
     for name, (res, args) in SIGNATURES.items():

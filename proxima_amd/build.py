@@ -1,5 +1,5 @@
 """Builds libproxima_hip.so in place from proxima_amd/csrc/*.hip with hipcc
-for gfx950. Run `python -m proxima_amd.build` (or __graft_entry__.build())."""
+for gfx950. Run `python proxima_amd/build.py` (or __graft_entry__.build())."""
 import glob
 import os
 import subprocess

@@ -41,6 +41,7 @@ namespace pxg {
 
 constexpr uint32_t UNASSIGNED = 0xFFFFFFFFu;
 constexpr int IVF_MAX_M = 128;
+thread_local uint64_t g_last_scanned = 0;
 
 // ---------------------------------------------------------------------------
 // coarse stage
@@ -185,6 +186,135 @@ __global__ __launch_bounds__(256) void ivf_scan(const float* __restrict__ Qp, in
 }
 
 // ---------------------------------------------------------------------------
+// ADC scan, register-resident codebooks (uniform subspace width W, M*W = dim
+// <= 128, shortlist <= 64). One workgroup per (query, group of probes); thread
+// t holds row t of every subspace codebook in VGPRs, so building a probe's
+// distance table is VALU work on LDS-broadcast residuals; each wave keeps its
+// best keys one per lane, sorted, across the whole probe group.
+// ---------------------------------------------------------------------------
+__device__ inline uint64_t readlane64(uint64_t v, int l) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Insert the passing keys of this batch (one candidate key per lane) into
+// the wave's sorted list `kept` (lane i = i-th smallest, KEY_MAX when empty).
+__device__ inline void wave_topk_insert(uint64_t key, uint64_t& kept, uint64_t& thr, int kk, int lane) {
+  uint64_t mask = __ballot(key < thr);
+  while (mask) {
+    const int src = __builtin_ctzll(mask);
+    mask &= mask - 1;
+    const uint64_t x = readlane64(key, src);
+    if (x < thr) {
+      const int pos = __popcll(__ballot(kept < x));
+      const uint32_t up_lo = __shfl_up((uint32_t)kept, 1, WAVE);
+      const uint32_t up_hi = __shfl_up((uint32_t)(kept >> 32), 1, WAVE);
+      const uint64_t up = ((uint64_t)up_hi << 32) | up_lo;
+      if (lane > pos) kept = up;
+      else if (lane == pos) kept = x;
+      thr = readlane64(kept, kk - 1);
+    }
+  }
+}
+
+constexpr int IVF_PG = 8;  // probes per workgroup item
+
+template <int W, int METRIC>
+__global__ __launch_bounds__(256) void ivf_scan_reg(const float* __restrict__ Qp, int ld, int dim, int M,
+                                                    const int* __restrict__ probes, int nprobe, int groups,
+                                                    const float* __restrict__ cents, const float* __restrict__ books,
+                                                    const uint32_t* __restrict__ list_off,
+                                                    const uint32_t* __restrict__ list_rank,
+                                                    const uint8_t* __restrict__ list_codes,
+                                                    const uint32_t* __restrict__ rank_slot,
+                                                    const uint8_t* __restrict__ accept, int kk,
+                                                    uint64_t* __restrict__ out) {
+  constexpr int MMAX = 128 / W;
+  extern __shared__ float lut[];  // M * 256 floats
+  __shared__ float sr[128];
+  __shared__ float s_qdc;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int q = blockIdx.x / groups, grp = blockIdx.x % groups;
+  const int p0 = grp * IVF_PG, p1 = min(nprobe, p0 + IVF_PG);
+  // codebook rows of centroid `tid`, all subspaces (book_off[s] = s*256*W)
+  float breg[MMAX][W];
+#pragma unroll
+  for (int s = 0; s < MMAX; ++s)
+#pragma unroll
+    for (int j = 0; j < W; ++j) breg[s][j] = s < M ? books[(size_t)s * 256 * W + tid * W + j] : 0.0f;
+  const float* qv = Qp + (size_t)q * ld;
+  if constexpr (METRIC == 1) {
+    // the cosine table depends on the query only (ivfpq.rs:1042-1045)
+    for (int j = tid; j < dim; j += 256) sr[j] = qv[j];
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < MMAX; ++s) {
+      if (s < M) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < W; ++j) acc += sr[s * W + j] * breg[s][j];
+        lut[s * 256 + tid] = acc;
+      }
+    }
+  }
+  uint64_t kept = KEY_MAX, thr = KEY_MAX;
+  for (int p = p0; p < p1; ++p) {
+    const int l = probes[(size_t)q * nprobe + p];
+    const float* cv = cents + (size_t)l * ld;
+    __syncthreads();  // previous probe's table no longer read
+    if constexpr (METRIC == 0) {
+      for (int j = tid; j < dim; j += 256) sr[j] = qv[j] - cv[j];  // residual (ivfpq.rs:1052-1054)
+      __syncthreads();
+#pragma unroll
+      for (int s = 0; s < MMAX; ++s) {
+        if (s < M) {
+          float acc = 0.0f;  // distance_table, product.rs:416-433
+#pragma unroll
+          for (int j = 0; j < W; ++j) {
+            const float d = sr[s * W + j] - breg[s][j];
+            acc += d * d;
+          }
+          lut[s * 256 + tid] = acc;
+        }
+      }
+    } else {
+      if (tid < 8) {
+        const float d = -dist_group8<2>(qv, cv, dim, tid);
+        if (tid == 0) s_qdc = d;
+      }
+    }
+    __syncthreads();
+    const float one_minus_qdc = METRIC == 1 ? 1.0f - s_qdc : 0.0f;
+    const uint32_t begin = list_off[l], end = list_off[l + 1];
+    for (uint32_t e0 = begin + w * 64; e0 < end; e0 += 256) {
+      const uint32_t e = e0 + lane;
+      uint64_t key = KEY_MAX;
+      if (e < end) {
+        const uint32_t rk = list_rank[e];
+        if (accept == nullptr || accept[rank_slot[rk]]) {
+          const uint8_t* code = list_codes + (size_t)e * M;
+          float sum = 0.0f;  // DistanceTable::squared_l2 / inner_product, product.rs:580-603
+          if (M == 16) {
+            const uint4 cw = *reinterpret_cast<const uint4*>(code);
+            const uint32_t wv[4] = {cw.x, cw.y, cw.z, cw.w};
+#pragma unroll
+            for (int s2 = 0; s2 < 16; ++s2) sum += lut[s2 * 256 + ((wv[s2 >> 2] >> (8 * (s2 & 3))) & 255)];
+          } else {
+            for (int s2 = 0; s2 < M; ++s2) sum += lut[s2 * 256 + code[s2]];
+          }
+          const float score = METRIC == 0 ? sum : one_minus_qdc + (-sum);
+          key = ((uint64_t)ord_key(score) << 32) | rk;
+        }
+      }
+      wave_topk_insert(key, kept, thr, kk, lane);
+    }
+  }
+  uint64_t* o = out + (((size_t)q * groups + grp) * 4 + w) * kk;
+  if (lane < kk) o[lane] = kept;
+}
+
+// ---------------------------------------------------------------------------
 // merge over probes (+ optional exact rerank)
 // ---------------------------------------------------------------------------
 constexpr int IVF_MAX_SHORT = 960;
@@ -246,6 +376,14 @@ __global__ __launch_bounds__(256) void ivf_merge(const uint64_t* __restrict__ ca
     out_d[(size_t)q * k + i] = key_float((uint32_t)(key >> 32));
   }
   if (threadIdx.x == 0) out_count[q] = kout;
+}
+
+__global__ void ivf_count_scanned(const int* __restrict__ probes, int n, const uint32_t* __restrict__ list_off,
+                                  unsigned long long* __restrict__ total) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int l = probes[i];
+  atomicAdd(total, (unsigned long long)(list_off[l + 1] - list_off[l]));
 }
 
 __global__ void ivf_gather_rows(const float* __restrict__ X, int ld, const uint32_t* __restrict__ rows, int n,
@@ -483,8 +621,10 @@ struct IvfPqIndex {
     return rep;
   }
 
-  void insert_rows(const uint64_t* in_ids, const float* vecs, uint64_t n, uint32_t* out_slots,
-                   std::vector<uint32_t>& new_slots) {
+  // Validate + prepare a batch into a device staging buffer [n][ld]:
+  // from host vectors (space.rs:130-138 on the host) or device vectors
+  // (the same arithmetic on the device). Nothing is mutated on failure.
+  void stage_host(const float* vecs, uint64_t n, DevBuf<float>& st) {
     std::vector<float> prepared((size_t)n * ld, 0.0f);
     for (uint64_t i = 0; i < n; ++i) {
       long long bad = validate_prepare(metric, vecs + i * dim, dim, prepared.data() + i * ld);
@@ -493,6 +633,31 @@ struct IvfPqIndex {
               "vector component " + std::to_string(bad) + " is not finite (" + std::to_string(vecs[i * dim + bad]) + ")",
               (uint64_t)bad, i, vecs[i * dim + bad]);
     }
+    st.alloc(n * ld);
+    PXG_HIP(hipMemcpyAsync(st.p, prepared.data(), n * ld * 4, hipMemcpyHostToDevice, stream));
+    PXG_HIP(hipStreamSynchronize(stream));
+  }
+  void stage_device(const float* d_vecs, uint64_t n, DevBuf<float>& st) {
+    st.alloc(n * ld);
+    DevBuf<float> b(n), nn(n);
+    DevBuf<unsigned long long> bad(1);
+    PXG_HIP(hipMemsetAsync(bad.p, 0xFF, 8, stream));
+    hipLaunchKernelGGL(flat_prep_queries, dim3((unsigned)n), dim3(64), 0, stream, d_vecs, (int)dim, (int)ld, metric,
+                       1, st.p, b.p, nn.p, bad.p);
+    PXG_HIP(hipGetLastError());
+    unsigned long long bv = 0;
+    PXG_HIP(hipMemcpyAsync(&bv, bad.p, 8, hipMemcpyDeviceToHost, stream));
+    PXG_HIP(hipStreamSynchronize(stream));
+    if (bv != ~0ull) {
+      const uint64_t row = bv >> 32, comp = (uint32_t)bv;
+      raise(PXG_ERR_NON_FINITE,
+            "vector component " + std::to_string(comp) + " is not finite (vector " + std::to_string(row) + ")", comp,
+            row, NAN);
+    }
+  }
+
+  // Insert prepared rows staged on the device (ivfpq.rs:1129-1158).
+  void insert_rows(const uint64_t* in_ids, const DevBuf<float>& st, uint64_t n, uint32_t* out_slots) {
     {
       std::unordered_map<uint64_t, int> seen;
       for (uint64_t i = 0; i < n; ++i)
@@ -509,24 +674,20 @@ struct IvfPqIndex {
       live.resize(hw, 0);
       list_of_h.resize(hw, UNASSIGNED);
     }
-    // stage rows: vectors go to X when kept, else to a transient buffer
+    // vectors go to X when kept, else to a transient slot-indexed store that
+    // only lives long enough to encode them (ivfpq.rs:1134-1141)
     DevBuf<float> tmpX;
     float* dst = X.p;
     if (!vectors_kept) {
-      // encode-and-discard (ivfpq.rs:1134-1141): a scratch store indexed by slot
       tmpX.alloc(hw * ld);
       dst = tmpX.p;
     }
-    DevBuf<float> st(n * ld);
     DevBuf<uint32_t> st_sl(n);
-    PXG_HIP(hipMemcpyAsync(st.p, prepared.data(), n * ld * 4, hipMemcpyHostToDevice, stream));
-    PXG_HIP(hipMemcpyAsync(st_sl.p, sl.data(), n * 4, hipMemcpyHostToDevice, stream));
-    std::vector<float> zeros(n, 0.0f);
-    DevBuf<float> st_b(n);
-    PXG_HIP(hipMemcpyAsync(st_b.p, zeros.data(), n * 4, hipMemcpyHostToDevice, stream));
+    DevBuf<float> st_b(n), dummy_xb(hw);
     DevBuf<uint64_t> st_ids(n);
+    PXG_HIP(hipMemcpyAsync(st_sl.p, sl.data(), n * 4, hipMemcpyHostToDevice, stream));
+    PXG_HIP(hipMemsetAsync(st_b.p, 0, n * 4, stream));
     PXG_HIP(hipMemcpyAsync(st_ids.p, in_ids, n * 8, hipMemcpyHostToDevice, stream));
-    DevBuf<float> dummy_xb(hw);
     hipLaunchKernelGGL(flat_scatter_rows, dim3((unsigned)n), dim3(256), 0, stream, st.p, st_sl.p, st_b.p, st_ids.p,
                        (int)n, (int)ld, dst, dummy_xb.p, d_live.p, d_ids.p);
     PXG_HIP(hipGetLastError());
@@ -548,7 +709,6 @@ struct IvfPqIndex {
         encode_slots(sl);
       }
     }
-    new_slots = sl;
   }
 
   void remove(uint64_t id) {
@@ -582,8 +742,9 @@ struct IvfPqIndex {
     float* Qp = (float*)ctx->get(1, nq * ld * 4);
     float* qb = (float*)ctx->get(2, nq * 4);
     float* qn = (float*)ctx->get(3, nq * 4);
-    unsigned long long* bad = (unsigned long long*)ctx->get(4, 16);
+    unsigned long long* bad = (unsigned long long*)ctx->get(4, 32);
     int* flag_count = (int*)(bad + 1);
+    unsigned long long* scanned_dev = nullptr;
     PXG_HIP(hipMemsetAsync(bad, 0xFF, 8, s));
     hipLaunchKernelGGL(flat_prep_queries, dim3((unsigned)nq), dim3(64), 0, s, d_raw, (int)dim, (int)ld, metric,
                        do_prepare ? 1 : 0, Qp, qb, qn, bad);
@@ -621,8 +782,47 @@ struct IvfPqIndex {
                          produced, ck);
       hipLaunchKernelGGL(ivf_coarse_select, dim3((unsigned)nq), dim3(256), 0, s, ck, produced, np, probes);
       PXG_HIP(hipGetLastError());
-      uint64_t* cand = (uint64_t*)ctx->get(10, (size_t)nq * np * 4 * kk * 8);
+      scanned_dev = (unsigned long long*)(flag_count + 2);
+      PXG_HIP(hipMemsetAsync(scanned_dev, 0, 8, s));
+      hipLaunchKernelGGL(ivf_count_scanned, dim3((unsigned)((nq * np + 255) / 256)), dim3(256), 0, s, probes,
+                         (int)(nq * np), list_off.p, scanned_dev);
       const size_t lds = (size_t)M() * 256 * 4;
+      const int W = (int)(dim / M());
+      const bool reg_path = dim <= 128 && dim % M() == 0 && kk <= 64 && (W == 1 || W == 2 || W == 4 || W == 8 ||
+                                                                          W == 16 || W == 32);
+      if (reg_path) {
+        const int groups = (np + IVF_PG - 1) / IVF_PG;
+        uint64_t* cand = (uint64_t*)ctx->get(10, (size_t)nq * groups * 4 * kk * 8);
+        const int grid = (int)(nq * groups);
+        tm.mark(1);
+#define PXG_SCANR(WW, MET)                                                                                          \
+  hipLaunchKernelGGL((ivf_scan_reg<WW, MET>), dim3(grid), dim3(256), lds, s, Qp, (int)ld, (int)dim, (int)M(), probes, \
+                     np, groups, cents.p, books.p, list_off.p, list_rank.p, list_codes.p, d_rank_slot.p, d_accept,  \
+                     kk, cand)
+#define PXG_SCANR_W(MET)                  \
+  switch (W) {                            \
+    case 1: PXG_SCANR(1, MET); break;     \
+    case 2: PXG_SCANR(2, MET); break;     \
+    case 4: PXG_SCANR(4, MET); break;     \
+    case 8: PXG_SCANR(8, MET); break;     \
+    case 16: PXG_SCANR(16, MET); break;   \
+    default: PXG_SCANR(32, MET); break;   \
+  }
+        if (metric == PXG_COSINE) {
+          PXG_SCANR_W(1)
+        } else {
+          PXG_SCANR_W(0)
+        }
+#undef PXG_SCANR_W
+#undef PXG_SCANR
+        PXG_HIP(hipGetLastError());
+        tm.mark(2);
+        hipLaunchKernelGGL(ivf_merge, dim3((unsigned)nq), dim3(256), 0, s, cand, groups * 4 * kk, kk, (int)k,
+                           rerank ? 1 : 0, Qp, (int)ld, (int)dim, metric, X.p, d_rank_slot.p, d_ids.p, d_oid, d_od,
+                           d_oc);
+        PXG_HIP(hipGetLastError());
+      } else {
+      uint64_t* cand = (uint64_t*)ctx->get(10, (size_t)nq * np * 4 * kk * 8);
       const int grid = (int)(nq * np);
       tm.mark(1);
 #define PXG_SCAN(CAPW, MET)                                                                                       \
@@ -643,11 +843,14 @@ struct IvfPqIndex {
                          rerank ? 1 : 0, Qp, (int)ld, (int)dim, metric, X.p, d_rank_slot.p, d_ids.p, d_oid, d_od,
                          d_oc);
       PXG_HIP(hipGetLastError());
+      }
     }
-    unsigned long long badv = 0;
+    unsigned long long badv = 0, scanned = 0;
     PXG_HIP(hipMemcpyAsync(&badv, bad, 8, hipMemcpyDeviceToHost, s));
+    if (scanned_dev) PXG_HIP(hipMemcpyAsync(&scanned, scanned_dev, 8, hipMemcpyDeviceToHost, s));
     PXG_HIP(hipStreamSynchronize(s));
     tm.finish();
+    g_last_scanned = scanned;
     if (badv != ~0ull) {
       const uint32_t qi = (uint32_t)(badv >> 32), comp = (uint32_t)badv;
       raise(PXG_ERR_NON_FINITE,
@@ -724,28 +927,51 @@ int pxg_ivfpq_create(uint32_t dim, int metric, const pxg_ivfpq_config* cfg, pxg_
 
 void pxg_ivfpq_destroy(pxg_ivfpq* index) { delete index; }
 
+static void ivfpq_insert_impl(pxg_ivfpq* index, const uint64_t* ids, const float* vectors, uint64_t n,
+                              uint32_t* out_slots, bool device) {
+  std::unique_lock<std::shared_mutex> lk(index->impl.mu);
+  IvfPqIndex& f = index->impl;
+  // validate and prepare the whole batch first (all-or-nothing)
+  pxg::DevBuf<float> st;
+  if (device)
+    f.stage_device(vectors, n, st);
+  else
+    f.stage_host(vectors, n, st);
+  {
+    std::unordered_map<uint64_t, int> seen;
+    for (uint64_t i = 0; i < n; ++i)
+      if (f.by_id.count(ids[i]) || !seen.emplace(ids[i], 1).second)
+        pxg::raise(PXG_ERR_DUPLICATE_ID, "duplicate vector id " + std::to_string(ids[i]), ids[i]);
+  }
+  // Auto-training fires when the live count reaches train_threshold
+  // (ivfpq.rs:1154-1156): split the batch at that insert.
+  uint64_t done = 0;
+  while (done < n) {
+    uint64_t take = n - done;
+    if (!f.trained && f.cfg.train_threshold > f.by_id.size() && f.cfg.train_threshold - f.by_id.size() < take)
+      take = f.cfg.train_threshold - f.by_id.size();
+    if (done == 0 && take == n) {
+      f.insert_rows(ids, st, n, out_slots);
+    } else {
+      pxg::DevBuf<float> part(take * f.ld);
+      PXG_HIP(hipMemcpyAsync(part.p, st.p + done * f.ld, take * f.ld * 4, hipMemcpyDeviceToDevice, f.stream));
+      f.insert_rows(ids + done, part, take, out_slots ? out_slots + done : nullptr);
+    }
+    done += take;
+    if (!f.trained && f.by_id.size() >= f.cfg.train_threshold) f.train();
+  }
+}
+
 int pxg_ivfpq_insert(pxg_ivfpq* index, const uint64_t* ids, const float* vectors, uint64_t n, uint32_t* out_slots) {
   return pxg::guard([&] {
-    if (n == 0) return;
-    std::unique_lock<std::shared_mutex> lk(index->impl.mu);
-    IvfPqIndex& f = index->impl;
-    // Auto-training fires when the live count reaches train_threshold
-    // (ivfpq.rs:1154-1156): split the batch at that insert.
-    uint64_t done = 0;
-    while (done < n) {
-      uint64_t take = n - done;
-      if (!f.trained && f.cfg.train_threshold > f.by_id.size() && f.cfg.train_threshold - f.by_id.size() < take)
-        take = f.cfg.train_threshold - f.by_id.size();
-      std::vector<uint32_t> sl;
-      f.insert_rows(ids + done, vectors + done * f.dim, take, out_slots ? out_slots + done : nullptr, sl);
-      done += take;
-      if (!f.trained && f.by_id.size() >= f.cfg.train_threshold) {
-        lk.unlock();
-        int st = pxg_ivfpq_train(index, nullptr);
-        lk.lock();
-        if (st != PXG_OK) throw pxg::Raise{pxg::Error{st, pxg_last_error_message()}};
-      }
-    }
+    if (n) ivfpq_insert_impl(index, ids, vectors, n, out_slots, false);
+  });
+}
+
+int pxg_ivfpq_insert_device(pxg_ivfpq* index, const uint64_t* ids, const float* d_vectors, uint64_t n,
+                            uint32_t* out_slots) {
+  return pxg::guard([&] {
+    if (n) ivfpq_insert_impl(index, ids, d_vectors, n, out_slots, true);
   });
 }
 
@@ -951,5 +1177,7 @@ int pxg_ivfpq_search_device(const pxg_ivfpq* index, const float* d_queries, uint
     PXG_HIP(hipStreamSynchronize(s));
   });
 }
+
+uint64_t pxg_ivfpq_last_scanned(void) { return pxg::g_last_scanned; }
 
 }  // extern "C"

@@ -169,6 +169,11 @@ void nearest_device(const float* P, int ldp, const uint32_t* rows, size_t n, int
 // ---------------------------------------------------------------------------
 // f64 sums in point order
 // ---------------------------------------------------------------------------
+// Uniform broadcast of lane i's value (a scalar read, no LDS round trip).
+__device__ inline float lane_value(float x, int i) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), i));
+}
+
 // One wave: every lane carries the same running sum; values arrive 64 at a
 // time and are added one by one in index order.
 __global__ __launch_bounds__(64) void seq_sum_f64(const float* __restrict__ v, int n, double* __restrict__ out) {
@@ -177,7 +182,7 @@ __global__ __launch_bounds__(64) void seq_sum_f64(const float* __restrict__ v, i
   for (int base = 0; base < n; base += 64) {
     const float x = base + lane < n ? v[base + lane] : 0.0f;
     const int m = min(64, n - base);
-    for (int i = 0; i < m; ++i) s += (double)__shfl(x, i, 64);
+    for (int i = 0; i < m; ++i) s += (double)lane_value(x, i);
   }
   if (lane == 0) *out = s;
 }
@@ -192,7 +197,7 @@ __global__ __launch_bounds__(64) void seq_find_cum(const float* __restrict__ v, 
     const float x = base + lane < n ? v[base + lane] : 0.0f;
     const int m = min(64, n - base);
     for (int i = 0; i < m; ++i) {
-      s += (double)__shfl(x, i, 64);
+      s += (double)lane_value(x, i);
       if (s >= target) {
         found = base + i;
         break;

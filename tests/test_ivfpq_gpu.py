@@ -249,3 +249,42 @@ def test_filters_cosine_seed_duplicates_stats(gpu):
     st = big.stats()
     assert st.len == 1000 and st.dim == 64 and st.deleted == 0
     assert st.graph_bytes >= 1000 * 8 and st.vector_bytes >= 1000 * 64 * 4
+
+
+def test_insert_device_matches_host_insert(gpu):
+    import torch
+    px = gpu
+    data = corpus(1500, 32, 24)
+    for metric in (0, 1):
+        cfg = px.IvfPqConfig(16, 8).with_seed(4).with_train_threshold(1 << 62)
+        a = build(px, data, cfg.clone(), metric)
+        b = px.IvfPqIndex(px.VectorSpace(32, metric), cfg.clone())
+        b.insert_device(np.arange(1500, dtype=np.uint64), torch.from_numpy(data).cuda())
+        a.train()
+        b.train()
+        for x, y in zip(a.parts(), b.parts()):
+            assert np.array_equal(x, y)
+        q = data[::150]
+        for x, y in zip(a.search_batch(q, 10), b.search_batch(q, 10)):
+            assert np.array_equal(x, y)
+    bad = torch.from_numpy(data[:4].copy()).cuda()
+    bad[2, 3] = float("nan")
+    with pytest.raises(px.NonFinite):
+        b.insert_device(np.arange(9000, 9004, dtype=np.uint64), bad)
+    assert len(b) == 1500
+
+
+@pytest.mark.parametrize("dim,m,k,rerank", [(20, 8, 10, 0), (32, 16, 100, 0), (32, 8, 10, 120), (24, 24, 70, 0)])
+def test_search_parity_general_path(gpu, dim, m, k, rerank):
+    """Shortlists above 64 and uneven subspace widths take the LDS-table scan."""
+    px = gpu
+    n, nlist = 2000, 16
+    data = corpus(n, dim, 20) + np.random.default_rng(3).standard_normal((n, dim)).astype(np.float32) * 0.3
+    cents, books, _ = orc.ivf_train(data, nlist, m, max_iter=6, seed=9)
+    codes, list_of = orc.ivf_encode(data, cents, books, m)
+    idx = build(px, data, px.IvfPqConfig(nlist, m).with_train_threshold(1 << 62).with_rerank(rerank))
+    idx.load_trained(cents, books, codes, list_of)
+    q = data[::131] - 0.05
+    want = orc.ivf_search(0, cents, books, codes, list_of, np.arange(n), q, k, 5, m,
+                          vectors=data if rerank else None, rerank=rerank, threads=8)
+    assert_same(idx.search_batch(q, k, nprobe=5), want)
