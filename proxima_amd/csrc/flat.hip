@@ -39,6 +39,7 @@
 #include "common.hpp"
 #include "device.hpp"
 #include "exact_scan.hpp"
+#include "flat.hpp"
 
 namespace pxg {
 
@@ -307,323 +308,295 @@ __global__ __launch_bounds__(256) void flat_merge_rescore(
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
-struct FlatIndex {
-  uint32_t dim = 0, ld = 0;
-  int metric = 0;
-  int mode = 0;  // 0 auto, 1 force MFMA candidates, 2 force exact scan
+FlatIndex::~FlatIndex() {
+  if (stream) (void)hipStreamDestroy(stream);
+}
 
-  // host mirror of the slot table (storage.rs:100-115)
-  std::vector<uint64_t> ids;
-  std::vector<uint8_t> live;
-  std::unordered_map<uint64_t, uint32_t> by_id;
-  SlotAllocator slots;
-  float maxnorm = 0.0f;
+// Grow the device arrays to hold `need` slots, keeping the first `keep`
+// (the high-water mark before the current allocation, never above cap).
+void FlatIndex::ensure_capacity(size_t need, size_t keep) {
+  if (need <= cap) return;
+  size_t nc = std::max<size_t>(need, std::max<size_t>(cap * 2, 1024));
+  const size_t hw = std::min(keep, cap);
+  X.grow(nc * ld, hw * ld, stream);
+  xb.grow(nc, hw, stream);
+  d_live.grow(nc, hw, stream);
+  d_ids.grow(nc, hw, stream);
+  d_rank.grow(nc, hw, stream);
+  // zero the new tail of the liveness map
+  PXG_HIP(hipMemsetAsync(d_live.p + hw, 0, nc - hw, stream));
+  PXG_HIP(hipStreamSynchronize(stream));
+  cap = nc;
+}
 
-  // device state
-  size_t cap = 0;
-  DevBuf<float> X;         // cap * ld, prepared vectors, zero padded
-  DevBuf<float> xb;        // cap: |x|^2 for L2, 0 otherwise
-  DevBuf<uint8_t> d_live;  // cap
-  DevBuf<uint64_t> d_ids;  // cap
-  DevBuf<uint32_t> d_rank;       // cap
-  DevBuf<uint32_t> d_rank_slot;  // len
-  bool rank_dirty = true;
-  std::mutex rank_mu;
-
-  mutable std::shared_mutex mu;
-  CtxPool pool;
-  hipStream_t stream = nullptr;
-
-  ~FlatIndex() {
-    if (stream) (void)hipStreamDestroy(stream);
+void FlatIndex::rebuild_ranks(hipStream_t s) {
+  std::lock_guard<std::mutex> lk(rank_mu);
+  if (!rank_dirty) return;
+  std::vector<std::pair<uint64_t, uint32_t>> v;
+  v.reserve(by_id.size());
+  for (size_t s2 = 0; s2 < ids.size(); ++s2)
+    if (live[s2]) v.emplace_back(ids[s2], (uint32_t)s2);
+  std::sort(v.begin(), v.end());
+  std::vector<uint32_t> rs(v.size()), rk(std::max<size_t>(ids.size(), 1), 0);
+  for (size_t r = 0; r < v.size(); ++r) {
+    rs[r] = v[r].second;
+    rk[v[r].second] = (uint32_t)r;
   }
+  d_rank_slot.reserve(std::max<size_t>(rs.size(), 1));
+  if (!rs.empty()) PXG_HIP(hipMemcpyAsync(d_rank_slot.p, rs.data(), rs.size() * 4, hipMemcpyHostToDevice, s));
+  if (!ids.empty()) PXG_HIP(hipMemcpyAsync(d_rank.p, rk.data(), ids.size() * 4, hipMemcpyHostToDevice, s));
+  PXG_HIP(hipStreamSynchronize(s));
+  rank_dirty = false;
+}
 
-  // Grow the device arrays to hold `need` slots, keeping the first `keep`
-  // (the high-water mark before the current allocation, never above cap).
-  void ensure_capacity(size_t need, size_t keep) {
-    if (need <= cap) return;
-    size_t nc = std::max<size_t>(need, std::max<size_t>(cap * 2, 1024));
-    const size_t hw = std::min(keep, cap);
-    X.grow(nc * ld, hw * ld, stream);
-    xb.grow(nc, hw, stream);
-    d_live.grow(nc, hw, stream);
-    d_ids.grow(nc, hw, stream);
-    d_rank.grow(nc, hw, stream);
-    // zero the new tail of the liveness map
-    PXG_HIP(hipMemsetAsync(d_live.p + hw, 0, nc - hw, stream));
-    PXG_HIP(hipStreamSynchronize(stream));
-    cap = nc;
+void FlatIndex::insert(const uint64_t* in_ids, const float* vecs, uint64_t n, uint32_t* out_slots) {
+  // Validate everything first: all-or-nothing.
+  std::vector<float> prepared((size_t)n * ld, 0.0f);
+  std::vector<float> bias(n);
+  float newmax = maxnorm;
+  for (uint64_t i = 0; i < n; ++i) {
+    long long bad = validate_prepare(metric, vecs + i * dim, dim, prepared.data() + i * ld);
+    if (bad >= 0)
+      raise(PXG_ERR_NON_FINITE,
+            "vector component " + std::to_string(bad) + " is not finite (" + std::to_string(vecs[i * dim + bad]) + ")",
+            (uint64_t)bad, i, vecs[i * dim + bad]);
+    const float* p = prepared.data() + i * ld;
+    float n2 = host_dot_unrolled(p, p, dim);
+    bias[i] = metric == PXG_EUCLIDEAN ? n2 : 0.0f;
+    float nr = std::sqrt(n2);
+    if (!(nr <= newmax)) newmax = std::isnan(nr) ? INFINITY : nr;
   }
-
-  void rebuild_ranks(hipStream_t s) {
-    std::lock_guard<std::mutex> lk(rank_mu);
-    if (!rank_dirty) return;
-    std::vector<std::pair<uint64_t, uint32_t>> v;
-    v.reserve(by_id.size());
-    for (size_t s2 = 0; s2 < ids.size(); ++s2)
-      if (live[s2]) v.emplace_back(ids[s2], (uint32_t)s2);
-    std::sort(v.begin(), v.end());
-    std::vector<uint32_t> rs(v.size()), rk(std::max<size_t>(ids.size(), 1), 0);
-    for (size_t r = 0; r < v.size(); ++r) {
-      rs[r] = v[r].second;
-      rk[v[r].second] = (uint32_t)r;
-    }
-    d_rank_slot.reserve(std::max<size_t>(rs.size(), 1));
-    if (!rs.empty()) PXG_HIP(hipMemcpyAsync(d_rank_slot.p, rs.data(), rs.size() * 4, hipMemcpyHostToDevice, s));
-    if (!ids.empty()) PXG_HIP(hipMemcpyAsync(d_rank.p, rk.data(), ids.size() * 4, hipMemcpyHostToDevice, s));
-    PXG_HIP(hipStreamSynchronize(s));
-    rank_dirty = false;
-  }
-
-  void insert(const uint64_t* in_ids, const float* vecs, uint64_t n, uint32_t* out_slots) {
-    // Validate everything first: all-or-nothing.
-    std::vector<float> prepared((size_t)n * ld, 0.0f);
-    std::vector<float> bias(n);
-    float newmax = maxnorm;
+  {
+    std::unordered_map<uint64_t, int> seen;
     for (uint64_t i = 0; i < n; ++i) {
-      long long bad = validate_prepare(metric, vecs + i * dim, dim, prepared.data() + i * ld);
-      if (bad >= 0)
-        raise(PXG_ERR_NON_FINITE,
-              "vector component " + std::to_string(bad) + " is not finite (" + std::to_string(vecs[i * dim + bad]) + ")",
-              (uint64_t)bad, i, vecs[i * dim + bad]);
-      const float* p = prepared.data() + i * ld;
-      float n2 = host_dot_unrolled(p, p, dim);
-      bias[i] = metric == PXG_EUCLIDEAN ? n2 : 0.0f;
-      float nr = std::sqrt(n2);
-      if (!(nr <= newmax)) newmax = std::isnan(nr) ? INFINITY : nr;
+      if (by_id.count(in_ids[i]) || !seen.emplace(in_ids[i], 1).second)
+        raise(PXG_ERR_DUPLICATE_ID, "duplicate vector id " + std::to_string(in_ids[i]), in_ids[i]);
     }
-    {
-      std::unordered_map<uint64_t, int> seen;
-      for (uint64_t i = 0; i < n; ++i) {
-        if (by_id.count(in_ids[i]) || !seen.emplace(in_ids[i], 1).second)
-          raise(PXG_ERR_DUPLICATE_ID, "duplicate vector id " + std::to_string(in_ids[i]), in_ids[i]);
-      }
-    }
-    if (by_id.size() + n > (size_t)UINT32_MAX - 1)
-      raise(PXG_ERR_CAPACITY, "capacity exceeded: slot allocator limit is 4294967295", UINT32_MAX);
-    std::vector<uint32_t> sl(n);
-    const size_t old_hw = slots.high_water();
-    // Allocate in order, exactly as repeated VectorStore::insert would.
-    for (uint64_t i = 0; i < n; ++i) sl[i] = slots.allocate();
-    const size_t hw = slots.high_water();
-    ensure_capacity(hw, old_hw);
-    if (ids.size() < hw) {
-      ids.resize(hw, 0);
-      live.resize(hw, 0);
-    }
-    for (uint64_t i = 0; i < n; ++i) {
-      ids[sl[i]] = in_ids[i];
-      live[sl[i]] = 1;
-      by_id[in_ids[i]] = sl[i];
-      if (out_slots) out_slots[i] = sl[i];
-    }
-    maxnorm = newmax;
-    // stage and scatter in chunks of <= 64 MiB of rows
-    const size_t rows_per = std::max<size_t>(1, (64u << 20) / ((size_t)ld * 4));
-    DevBuf<float> st_rows(std::min<size_t>(rows_per, n) * ld);
-    DevBuf<uint32_t> st_slots(std::min<size_t>(rows_per, n));
-    DevBuf<float> st_bias(std::min<size_t>(rows_per, n));
-    DevBuf<uint64_t> st_ids(std::min<size_t>(rows_per, n));
-    for (size_t a = 0; a < n; a += rows_per) {
-      const size_t m = std::min<size_t>(rows_per, n - a);
-      PXG_HIP(hipMemcpyAsync(st_rows.p, prepared.data() + a * ld, m * ld * 4, hipMemcpyHostToDevice, stream));
-      PXG_HIP(hipMemcpyAsync(st_slots.p, sl.data() + a, m * 4, hipMemcpyHostToDevice, stream));
-      PXG_HIP(hipMemcpyAsync(st_bias.p, bias.data() + a, m * 4, hipMemcpyHostToDevice, stream));
-      PXG_HIP(hipMemcpyAsync(st_ids.p, in_ids + a, m * 8, hipMemcpyHostToDevice, stream));
-      hipLaunchKernelGGL(flat_scatter_rows, dim3((unsigned)m), dim3(256), 0, stream, st_rows.p, st_slots.p,
-                         st_bias.p, st_ids.p, (int)m, (int)ld, X.p, xb.p, d_live.p, d_ids.p);
-      PXG_HIP(hipGetLastError());
-      PXG_HIP(hipStreamSynchronize(stream));
-    }
-    rank_dirty = true;
   }
-
-  void remove(uint64_t id) {
-    auto it = by_id.find(id);
-    if (it == by_id.end()) raise(PXG_ERR_UNKNOWN_ID, "unknown vector id " + std::to_string(id), id);
-    const uint32_t s = it->second;
-    by_id.erase(it);
-    live[s] = 0;
-    slots.release(s);
-    PXG_HIP(hipMemsetAsync(d_live.p + s, 0, 1, stream));
-    PXG_HIP(hipStreamSynchronize(stream));
-    rank_dirty = true;
+  if (by_id.size() + n > (size_t)UINT32_MAX - 1)
+    raise(PXG_ERR_CAPACITY, "capacity exceeded: slot allocator limit is 4294967295", UINT32_MAX);
+  std::vector<uint32_t> sl(n);
+  const size_t old_hw = slots.high_water();
+  // Allocate in order, exactly as repeated VectorStore::insert would.
+  for (uint64_t i = 0; i < n; ++i) sl[i] = slots.allocate();
+  const size_t hw = slots.high_water();
+  ensure_capacity(hw, old_hw);
+  if (ids.size() < hw) {
+    ids.resize(hw, 0);
+    live.resize(hw, 0);
   }
-
-  // Run the search pipeline on prepared-or-raw device queries.
-  void search_device(const float* d_raw, bool do_prepare, uint64_t nq, uint64_t k, const uint8_t* d_accept,
-                     uint64_t* d_oid, float* d_od, uint32_t* d_oc, Ctx* ctx, hipStream_t s, uint64_t* fallbacks) {
-    check_k(k);
-    *fallbacks = 0;
-    const size_t N = slots.high_water();
-    if (nq == 0) return;
-    if (k == 0 || by_id.empty()) {
-      PXG_HIP(hipMemsetAsync(d_oc, 0, nq * 4, s));
-      PXG_HIP(hipStreamSynchronize(s));
-      return;
-    }
-    if (k > EXACT_MERGE_MAXK)
-      config_error("k", k, "the GPU flat search supports k up to 1024 per query");
-    rebuild_ranks(s);
-
-    Timer tm(s);
-    tm.mark(0);
-    // 1. prepare queries
-    float* Qp = (float*)ctx->get(1, nq * ld * 4);
-    float* qb = (float*)ctx->get(2, nq * 4);
-    float* qn = (float*)ctx->get(3, nq * 4);
-    unsigned long long* bad = (unsigned long long*)ctx->get(4, 8 + 8);
-    int* flag_count = (int*)(bad + 1);
-    PXG_HIP(hipMemsetAsync(bad, 0xFF, 8, s));
-    PXG_HIP(hipMemsetAsync(flag_count, 0, 4, s));
-    hipLaunchKernelGGL(flat_prep_queries, dim3((unsigned)nq), dim3(64), 0, s, d_raw, (int)dim, (int)ld, metric,
-                       do_prepare ? 1 : 0, Qp, qb, qn, bad);
+  for (uint64_t i = 0; i < n; ++i) {
+    ids[sl[i]] = in_ids[i];
+    live[sl[i]] = 1;
+    by_id[in_ids[i]] = sl[i];
+    if (out_slots) out_slots[i] = sl[i];
+  }
+  maxnorm = newmax;
+  // stage and scatter in chunks of <= 64 MiB of rows
+  const size_t rows_per = std::max<size_t>(1, (64u << 20) / ((size_t)ld * 4));
+  DevBuf<float> st_rows(std::min<size_t>(rows_per, n) * ld);
+  DevBuf<uint32_t> st_slots(std::min<size_t>(rows_per, n));
+  DevBuf<float> st_bias(std::min<size_t>(rows_per, n));
+  DevBuf<uint64_t> st_ids(std::min<size_t>(rows_per, n));
+  for (size_t a = 0; a < n; a += rows_per) {
+    const size_t m = std::min<size_t>(rows_per, n - a);
+    PXG_HIP(hipMemcpyAsync(st_rows.p, prepared.data() + a * ld, m * ld * 4, hipMemcpyHostToDevice, stream));
+    PXG_HIP(hipMemcpyAsync(st_slots.p, sl.data() + a, m * 4, hipMemcpyHostToDevice, stream));
+    PXG_HIP(hipMemcpyAsync(st_bias.p, bias.data() + a, m * 4, hipMemcpyHostToDevice, stream));
+    PXG_HIP(hipMemcpyAsync(st_ids.p, in_ids + a, m * 8, hipMemcpyHostToDevice, stream));
+    hipLaunchKernelGGL(flat_scatter_rows, dim3((unsigned)m), dim3(256), 0, stream, st_rows.p, st_slots.p,
+                       st_bias.p, st_ids.p, (int)m, (int)ld, X.p, xb.p, d_live.p, d_ids.p);
     PXG_HIP(hipGetLastError());
+    PXG_HIP(hipStreamSynchronize(stream));
+  }
+  rank_dirty = true;
+}
 
-    int* flag_list = (int*)ctx->get(5, nq * 4);
-    // Manhattan has no inner-product form and k beyond FAST_KMAX exceeds the
-    // candidate buffers: both take the exact scan, as do small problems.
-    const bool exact_all = mode == 2 || metric == PXG_MANHATTAN || k > FAST_KMAX ||
-                           (mode == 0 && (N < 4096 || (double)N * (double)nq < 4.0e6));
-    if (!exact_all) {
-      const int Kp = (int)std::min<uint64_t>(k + MARGIN, (uint64_t)FAST_KMAX + MARGIN);
-      const int CAP = (Kp + FB_N) <= 256 ? 256 : 512;
-      const int QB = (int)((nq + FB_M - 1) / FB_M);
-      const int tiles = (int)((N + FB_N - 1) / FB_N);
-      int S = std::max(1, std::min(512 / QB, std::max(1, tiles / 4)));
-      const int tiles_per = (tiles + S - 1) / S;
-      const int per_split = tiles_per * FB_N;
-      S = (int)((N + per_split - 1) / per_split);
-      uint64_t* cand = (uint64_t*)ctx->get(6, (size_t)nq * S * CAP * 8);
-      const int total = QB * S;
-      tm.mark(1);
-      const int grid = ((total + 7) / 8) * 8;
-      const float scale = metric == PXG_EUCLIDEAN ? 2.0f : 1.0f;
-      if (CAP == 256)
-        hipLaunchKernelGGL(flat_mfma_candidates<256>, dim3(grid), dim3(256), 0, s, Qp, (int)nq, X.p, (int)N, (int)ld,
-                           qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, Kp, cand);
-      else
-        hipLaunchKernelGGL(flat_mfma_candidates<512>, dim3(grid), dim3(256), 0, s, Qp, (int)nq, X.p, (int)N, (int)ld,
-                           qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, Kp, cand);
-      PXG_HIP(hipGetLastError());
-      tm.mark(2);
-      hipLaunchKernelGGL(flat_merge_rescore, dim3((unsigned)nq), dim3(256), 0, s, cand, S, CAP, Kp, (int)k, Qp,
-                         (int)ld, (int)dim, metric, X.p, d_rank.p, d_rank_slot.p, d_ids.p, qn, maxnorm, 4.0f, d_oid,
-                         d_od, d_oc, flag_list, flag_count);
-      PXG_HIP(hipGetLastError());
-    } else {
-      hipLaunchKernelGGL(iota_kernel, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s, flag_list, (int)nq,
-                         flag_count);
-      PXG_HIP(hipGetLastError());
-    }
-    // exact scan for flagged queries (all of them on the exact path)
-    int nflag = 0;
-    PXG_HIP(hipMemcpyAsync(&nflag, flag_count, 4, hipMemcpyDeviceToHost, s));
-    unsigned long long badv = 0;
-    PXG_HIP(hipMemcpyAsync(&badv, bad, 8, hipMemcpyDeviceToHost, s));
+void FlatIndex::remove(uint64_t id) {
+  auto it = by_id.find(id);
+  if (it == by_id.end()) raise(PXG_ERR_UNKNOWN_ID, "unknown vector id " + std::to_string(id), id);
+  const uint32_t s = it->second;
+  by_id.erase(it);
+  live[s] = 0;
+  slots.release(s);
+  PXG_HIP(hipMemsetAsync(d_live.p + s, 0, 1, stream));
+  PXG_HIP(hipStreamSynchronize(stream));
+  rank_dirty = true;
+}
+
+// Run the search pipeline on prepared-or-raw device queries.
+void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, uint64_t k, const uint8_t* d_accept,
+                   uint64_t* d_oid, float* d_od, uint32_t* d_oc, Ctx* ctx, hipStream_t s, uint64_t* fallbacks) {
+  check_k(k);
+  *fallbacks = 0;
+  const size_t N = slots.high_water();
+  if (nq == 0) return;
+  if (k == 0 || by_id.empty()) {
+    PXG_HIP(hipMemsetAsync(d_oc, 0, nq * 4, s));
     PXG_HIP(hipStreamSynchronize(s));
-    if (badv != ~0ull) {
-      const uint32_t qi = (uint32_t)(badv >> 32), comp = (uint32_t)badv;
-      raise(PXG_ERR_NON_FINITE, "vector component " + std::to_string(comp) + " is not finite (query " +
-                                    std::to_string(qi) + ")",
-            comp, qi, NAN);
-    }
-    if (nflag > 0) {
-      const int nchunks = (int)((N + EXACT_CH - 1) / EXACT_CH);
-      const int kk = (int)std::min<uint64_t>(k, EXACT_CH);
-      uint64_t* ecand = (uint64_t*)ctx->get(7, (size_t)nflag * nchunks * kk * 8);
-      const int grid = std::min(nflag * nchunks, 4096);
-      tm.mark(exact_all ? 1 : 3);
-      hipLaunchKernelGGL(flat_exact_candidates, dim3(grid), dim3(256), 0, s, flag_list, flag_count, nchunks, Qp,
-                         (int)ld, (int)dim, metric, X.p, (int)N, d_live.p, d_accept, d_rank.p, (int)k, ecand);
-      PXG_HIP(hipGetLastError());
-      if (exact_all) tm.mark(2);
-      hipLaunchKernelGGL(flat_merge_exact, dim3((unsigned)nflag), dim3(256), 0, s, flag_list, flag_count, ecand,
-                         nchunks, (int)k, d_rank_slot.p, d_ids.p, d_oid, d_od, d_oc);
-      PXG_HIP(hipGetLastError());
-      PXG_HIP(hipStreamSynchronize(s));
-      *fallbacks = exact_all ? 0 : (uint64_t)nflag;
-    }
-    tm.finish();
+    return;
   }
+  if (k > EXACT_MERGE_MAXK)
+    config_error("k", k, "the GPU flat search supports k up to 1024 per query");
+  rebuild_ranks(s);
 
-  // Insert from device memory: validate + prepare on the device, then the
-  // same slot allocation and scatter as insert().
-  void insert_device(const uint64_t* in_ids, const float* d_vecs, uint64_t n, uint32_t* out_slots) {
-    {
-      std::unordered_map<uint64_t, int> seen;
-      for (uint64_t i = 0; i < n; ++i)
-        if (by_id.count(in_ids[i]) || !seen.emplace(in_ids[i], 1).second)
-          raise(PXG_ERR_DUPLICATE_ID, "duplicate vector id " + std::to_string(in_ids[i]), in_ids[i]);
-    }
-    if (by_id.size() + n > (size_t)UINT32_MAX - 1)
-      raise(PXG_ERR_CAPACITY, "capacity exceeded: slot allocator limit is 4294967295", UINT32_MAX);
-    const size_t rows_per = std::max<size_t>(1, (256u << 20) / ((size_t)ld * 4));
-    const size_t chunk = std::min<size_t>(rows_per, n);
-    DevBuf<float> st_rows(chunk * ld);
-    DevBuf<float> st_b(chunk), st_n(chunk);
-    DevBuf<unsigned long long> bad(1);
-    // pass 1: validate every row before touching any state (all-or-nothing)
-    std::vector<float> norms(n);
-    for (size_t a = 0; a < n; a += chunk) {
-      const size_t m = std::min<size_t>(chunk, n - a);
-      PXG_HIP(hipMemsetAsync(bad.p, 0xFF, 8, stream));
-      hipLaunchKernelGGL(flat_prep_queries, dim3((unsigned)m), dim3(64), 0, stream, d_vecs + a * dim, (int)dim,
-                         (int)ld, metric, 1, st_rows.p, st_b.p, st_n.p, bad.p);
-      PXG_HIP(hipGetLastError());
-      unsigned long long bv = 0;
-      PXG_HIP(hipMemcpyAsync(&bv, bad.p, 8, hipMemcpyDeviceToHost, stream));
-      PXG_HIP(hipMemcpyAsync(norms.data() + a, st_n.p, m * 4, hipMemcpyDeviceToHost, stream));
-      PXG_HIP(hipStreamSynchronize(stream));
-      if (bv != ~0ull) {
-        const uint64_t row = a + (bv >> 32), comp = (uint32_t)bv;
-        raise(PXG_ERR_NON_FINITE, "vector component " + std::to_string(comp) + " is not finite (vector " +
-                                      std::to_string(row) + ")",
-              comp, row, NAN);
-      }
-    }
-    float newmax = maxnorm;
-    for (float nr : norms)
-      if (!(nr <= newmax)) newmax = std::isnan(nr) ? INFINITY : nr;
-    std::vector<uint32_t> sl(n);
-    const size_t old_hw = slots.high_water();
-    for (uint64_t i = 0; i < n; ++i) sl[i] = slots.allocate();
-    const size_t hw = slots.high_water();
-    ensure_capacity(hw, old_hw);
-    if (ids.size() < hw) {
-      ids.resize(hw, 0);
-      live.resize(hw, 0);
-    }
-    for (uint64_t i = 0; i < n; ++i) {
-      ids[sl[i]] = in_ids[i];
-      live[sl[i]] = 1;
-      by_id[in_ids[i]] = sl[i];
-      if (out_slots) out_slots[i] = sl[i];
-    }
-    maxnorm = newmax;
-    DevBuf<uint32_t> st_slots(chunk);
-    DevBuf<uint64_t> st_ids(chunk);
-    DevBuf<float> st_bias(chunk);
-    for (size_t a = 0; a < n; a += chunk) {
-      const size_t m = std::min<size_t>(chunk, n - a);
-      hipLaunchKernelGGL(flat_prep_queries, dim3((unsigned)m), dim3(64), 0, stream, d_vecs + a * dim, (int)dim,
-                         (int)ld, metric, 1, st_rows.p, st_b.p, st_n.p, bad.p);
-      PXG_HIP(hipGetLastError());
-      // bias: |x|^2 for Euclidean (st_b holds it), 0 otherwise
-      if (metric == PXG_EUCLIDEAN)
-        PXG_HIP(hipMemcpyAsync(st_bias.p, st_b.p, m * 4, hipMemcpyDeviceToDevice, stream));
-      else
-        PXG_HIP(hipMemsetAsync(st_bias.p, 0, m * 4, stream));
-      PXG_HIP(hipMemcpyAsync(st_slots.p, sl.data() + a, m * 4, hipMemcpyHostToDevice, stream));
-      PXG_HIP(hipMemcpyAsync(st_ids.p, in_ids + a, m * 8, hipMemcpyHostToDevice, stream));
-      hipLaunchKernelGGL(flat_scatter_rows, dim3((unsigned)m), dim3(256), 0, stream, st_rows.p, st_slots.p,
-                         st_bias.p, st_ids.p, (int)m, (int)ld, X.p, xb.p, d_live.p, d_ids.p);
-      PXG_HIP(hipGetLastError());
-      PXG_HIP(hipStreamSynchronize(stream));
-    }
-    rank_dirty = true;
+  Timer tm(s);
+  tm.mark(0);
+  // 1. prepare queries
+  float* Qp = (float*)ctx->get(1, nq * ld * 4);
+  float* qb = (float*)ctx->get(2, nq * 4);
+  float* qn = (float*)ctx->get(3, nq * 4);
+  unsigned long long* bad = (unsigned long long*)ctx->get(4, 8 + 8);
+  int* flag_count = (int*)(bad + 1);
+  PXG_HIP(hipMemsetAsync(bad, 0xFF, 8, s));
+  PXG_HIP(hipMemsetAsync(flag_count, 0, 4, s));
+  hipLaunchKernelGGL(flat_prep_queries, dim3((unsigned)nq), dim3(64), 0, s, d_raw, (int)dim, (int)ld, metric,
+                     do_prepare ? 1 : 0, Qp, qb, qn, bad);
+  PXG_HIP(hipGetLastError());
+
+  int* flag_list = (int*)ctx->get(5, nq * 4);
+  // Manhattan has no inner-product form and k beyond FAST_KMAX exceeds the
+  // candidate buffers: both take the exact scan, as do small problems.
+  const bool exact_all = mode == 2 || metric == PXG_MANHATTAN || k > FAST_KMAX ||
+                         (mode == 0 && (N < 4096 || (double)N * (double)nq < 4.0e6));
+  if (!exact_all) {
+    const int Kp = (int)std::min<uint64_t>(k + MARGIN, (uint64_t)FAST_KMAX + MARGIN);
+    const int CAP = (Kp + FB_N) <= 256 ? 256 : 512;
+    const int QB = (int)((nq + FB_M - 1) / FB_M);
+    const int tiles = (int)((N + FB_N - 1) / FB_N);
+    int S = std::max(1, std::min(512 / QB, std::max(1, tiles / 4)));
+    const int tiles_per = (tiles + S - 1) / S;
+    const int per_split = tiles_per * FB_N;
+    S = (int)((N + per_split - 1) / per_split);
+    uint64_t* cand = (uint64_t*)ctx->get(6, (size_t)nq * S * CAP * 8);
+    const int total = QB * S;
+    tm.mark(1);
+    const int grid = ((total + 7) / 8) * 8;
+    const float scale = metric == PXG_EUCLIDEAN ? 2.0f : 1.0f;
+    if (CAP == 256)
+      hipLaunchKernelGGL(flat_mfma_candidates<256>, dim3(grid), dim3(256), 0, s, Qp, (int)nq, X.p, (int)N, (int)ld,
+                         qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, Kp, cand);
+    else
+      hipLaunchKernelGGL(flat_mfma_candidates<512>, dim3(grid), dim3(256), 0, s, Qp, (int)nq, X.p, (int)N, (int)ld,
+                         qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, Kp, cand);
+    PXG_HIP(hipGetLastError());
+    tm.mark(2);
+    hipLaunchKernelGGL(flat_merge_rescore, dim3((unsigned)nq), dim3(256), 0, s, cand, S, CAP, Kp, (int)k, Qp,
+                       (int)ld, (int)dim, metric, X.p, d_rank.p, d_rank_slot.p, d_ids.p, qn, maxnorm, 4.0f, d_oid,
+                       d_od, d_oc, flag_list, flag_count);
+    PXG_HIP(hipGetLastError());
+  } else {
+    hipLaunchKernelGGL(iota_kernel, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s, flag_list, (int)nq,
+                       flag_count);
+    PXG_HIP(hipGetLastError());
   }
-};
+  // exact scan for flagged queries (all of them on the exact path)
+  int nflag = 0;
+  PXG_HIP(hipMemcpyAsync(&nflag, flag_count, 4, hipMemcpyDeviceToHost, s));
+  unsigned long long badv = 0;
+  PXG_HIP(hipMemcpyAsync(&badv, bad, 8, hipMemcpyDeviceToHost, s));
+  PXG_HIP(hipStreamSynchronize(s));
+  if (badv != ~0ull) {
+    const uint32_t qi = (uint32_t)(badv >> 32), comp = (uint32_t)badv;
+    raise(PXG_ERR_NON_FINITE, "vector component " + std::to_string(comp) + " is not finite (query " +
+                                  std::to_string(qi) + ")",
+          comp, qi, NAN);
+  }
+  if (nflag > 0) {
+    const int nchunks = (int)((N + EXACT_CH - 1) / EXACT_CH);
+    const int kk = (int)std::min<uint64_t>(k, EXACT_CH);
+    uint64_t* ecand = (uint64_t*)ctx->get(7, (size_t)nflag * nchunks * kk * 8);
+    const int grid = std::min(nflag * nchunks, 4096);
+    tm.mark(exact_all ? 1 : 3);
+    hipLaunchKernelGGL(flat_exact_candidates, dim3(grid), dim3(256), 0, s, flag_list, flag_count, nchunks, Qp,
+                       (int)ld, (int)dim, metric, X.p, (int)N, d_live.p, d_accept, d_rank.p, (int)k, ecand);
+    PXG_HIP(hipGetLastError());
+    if (exact_all) tm.mark(2);
+    hipLaunchKernelGGL(flat_merge_exact, dim3((unsigned)nflag), dim3(256), 0, s, flag_list, flag_count, ecand,
+                       nchunks, (int)k, d_rank_slot.p, d_ids.p, d_oid, d_od, d_oc);
+    PXG_HIP(hipGetLastError());
+    PXG_HIP(hipStreamSynchronize(s));
+    *fallbacks = exact_all ? 0 : (uint64_t)nflag;
+  }
+  tm.finish();
+}
+
+// Insert from device memory: validate + prepare on the device, then the
+// same slot allocation and scatter as insert().
+void FlatIndex::insert_device(const uint64_t* in_ids, const float* d_vecs, uint64_t n, uint32_t* out_slots) {
+  {
+    std::unordered_map<uint64_t, int> seen;
+    for (uint64_t i = 0; i < n; ++i)
+      if (by_id.count(in_ids[i]) || !seen.emplace(in_ids[i], 1).second)
+        raise(PXG_ERR_DUPLICATE_ID, "duplicate vector id " + std::to_string(in_ids[i]), in_ids[i]);
+  }
+  if (by_id.size() + n > (size_t)UINT32_MAX - 1)
+    raise(PXG_ERR_CAPACITY, "capacity exceeded: slot allocator limit is 4294967295", UINT32_MAX);
+  const size_t rows_per = std::max<size_t>(1, (256u << 20) / ((size_t)ld * 4));
+  const size_t chunk = std::min<size_t>(rows_per, n);
+  DevBuf<float> st_rows(chunk * ld);
+  DevBuf<float> st_b(chunk), st_n(chunk);
+  DevBuf<unsigned long long> bad(1);
+  // pass 1: validate every row before touching any state (all-or-nothing)
+  std::vector<float> norms(n);
+  for (size_t a = 0; a < n; a += chunk) {
+    const size_t m = std::min<size_t>(chunk, n - a);
+    PXG_HIP(hipMemsetAsync(bad.p, 0xFF, 8, stream));
+    hipLaunchKernelGGL(flat_prep_queries, dim3((unsigned)m), dim3(64), 0, stream, d_vecs + a * dim, (int)dim,
+                       (int)ld, metric, 1, st_rows.p, st_b.p, st_n.p, bad.p);
+    PXG_HIP(hipGetLastError());
+    unsigned long long bv = 0;
+    PXG_HIP(hipMemcpyAsync(&bv, bad.p, 8, hipMemcpyDeviceToHost, stream));
+    PXG_HIP(hipMemcpyAsync(norms.data() + a, st_n.p, m * 4, hipMemcpyDeviceToHost, stream));
+    PXG_HIP(hipStreamSynchronize(stream));
+    if (bv != ~0ull) {
+      const uint64_t row = a + (bv >> 32), comp = (uint32_t)bv;
+      raise(PXG_ERR_NON_FINITE, "vector component " + std::to_string(comp) + " is not finite (vector " +
+                                    std::to_string(row) + ")",
+            comp, row, NAN);
+    }
+  }
+  float newmax = maxnorm;
+  for (float nr : norms)
+    if (!(nr <= newmax)) newmax = std::isnan(nr) ? INFINITY : nr;
+  std::vector<uint32_t> sl(n);
+  const size_t old_hw = slots.high_water();
+  for (uint64_t i = 0; i < n; ++i) sl[i] = slots.allocate();
+  const size_t hw = slots.high_water();
+  ensure_capacity(hw, old_hw);
+  if (ids.size() < hw) {
+    ids.resize(hw, 0);
+    live.resize(hw, 0);
+  }
+  for (uint64_t i = 0; i < n; ++i) {
+    ids[sl[i]] = in_ids[i];
+    live[sl[i]] = 1;
+    by_id[in_ids[i]] = sl[i];
+    if (out_slots) out_slots[i] = sl[i];
+  }
+  maxnorm = newmax;
+  DevBuf<uint32_t> st_slots(chunk);
+  DevBuf<uint64_t> st_ids(chunk);
+  DevBuf<float> st_bias(chunk);
+  for (size_t a = 0; a < n; a += chunk) {
+    const size_t m = std::min<size_t>(chunk, n - a);
+    hipLaunchKernelGGL(flat_prep_queries, dim3((unsigned)m), dim3(64), 0, stream, d_vecs + a * dim, (int)dim,
+                       (int)ld, metric, 1, st_rows.p, st_b.p, st_n.p, bad.p);
+    PXG_HIP(hipGetLastError());
+    // bias: |x|^2 for Euclidean (st_b holds it), 0 otherwise
+    if (metric == PXG_EUCLIDEAN)
+      PXG_HIP(hipMemcpyAsync(st_bias.p, st_b.p, m * 4, hipMemcpyDeviceToDevice, stream));
+    else
+      PXG_HIP(hipMemsetAsync(st_bias.p, 0, m * 4, stream));
+    PXG_HIP(hipMemcpyAsync(st_slots.p, sl.data() + a, m * 4, hipMemcpyHostToDevice, stream));
+    PXG_HIP(hipMemcpyAsync(st_ids.p, in_ids + a, m * 8, hipMemcpyHostToDevice, stream));
+    hipLaunchKernelGGL(flat_scatter_rows, dim3((unsigned)m), dim3(256), 0, stream, st_rows.p, st_slots.p,
+                       st_bias.p, st_ids.p, (int)m, (int)ld, X.p, xb.p, d_live.p, d_ids.p);
+    PXG_HIP(hipGetLastError());
+    PXG_HIP(hipStreamSynchronize(stream));
+  }
+  rank_dirty = true;
+}
 
 thread_local uint64_t g_last_fallbacks = 0;
 

@@ -1,0 +1,51 @@
+// FlatIndex: the device-resident exact index (crates/proxima-index/src/
+// flat.rs:68-236). Defined in flat.hip; the IVF-PQ coarse quantizer reuses it.
+#pragma once
+
+#include <mutex>
+#include <shared_mutex>
+#include <unordered_map>
+#include <vector>
+
+#include "common.hpp"
+
+namespace pxg {
+
+struct FlatIndex {
+  uint32_t dim = 0, ld = 0;
+  int metric = 0;
+  int mode = 0;  // 0 auto, 1 force MFMA candidates, 2 force exact scan
+
+  // host mirror of the slot table (storage.rs:100-115)
+  std::vector<uint64_t> ids;
+  std::vector<uint8_t> live;
+  std::unordered_map<uint64_t, uint32_t> by_id;
+  SlotAllocator slots;
+  float maxnorm = 0.0f;
+
+  // device state
+  size_t cap = 0;
+  DevBuf<float> X;         // cap * ld, prepared vectors, zero padded
+  DevBuf<float> xb;        // cap: |x|^2 for L2, 0 otherwise
+  DevBuf<uint8_t> d_live;  // cap
+  DevBuf<uint64_t> d_ids;  // cap
+  DevBuf<uint32_t> d_rank;       // cap
+  DevBuf<uint32_t> d_rank_slot;  // len
+  bool rank_dirty = true;
+  std::mutex rank_mu;
+
+  mutable std::shared_mutex mu;
+  CtxPool pool;
+  hipStream_t stream = nullptr;
+
+  ~FlatIndex();
+  void ensure_capacity(size_t need, size_t keep);
+  void rebuild_ranks(hipStream_t s);
+  void insert(const uint64_t* in_ids, const float* vecs, uint64_t n, uint32_t* out_slots);
+  void remove(uint64_t id);
+  void search_device(const float* d_raw, bool do_prepare, uint64_t nq, uint64_t k, const uint8_t* d_accept,
+                   uint64_t* d_oid, float* d_od, uint32_t* d_oc, Ctx* ctx, hipStream_t s, uint64_t* fallbacks);
+  void insert_device(const uint64_t* in_ids, const float* d_vecs, uint64_t n, uint32_t* out_slots);
+};
+
+}  // namespace pxg

@@ -35,7 +35,12 @@
 #include "common.hpp"
 #include "device.hpp"
 #include "exact_scan.hpp"
+#include "flat.hpp"
 #include "train.hpp"
+#include <chrono>
+#include <cstdio>
+#include <cstdlib>
+#include <memory>
 
 namespace pxg {
 
@@ -218,6 +223,57 @@ __device__ inline void wave_topk_insert(uint64_t key, uint64_t& kept, uint64_t& 
   }
 }
 
+// Coarse top-nprobe for nprobe <= 64: one wave per query; the block's four
+// queries share 64-row centroid tiles staged in LDS (row stride dim+1, so
+// lane l reading row l is conflict-free). Lane l computes the exact
+// squared_euclidean_unrolled distance (distance.rs:267-283) to centroid
+// c0 + l and the wave keeps the nprobe smallest (distance, list) keys in
+// registers, one per lane, in ascending order.
+__global__ __launch_bounds__(256) void ivf_coarse_topk(const float* __restrict__ Qp, int ld, int dim, int nq,
+                                                       const float* __restrict__ cents, int produced, int np,
+                                                       int* __restrict__ probes) {
+  extern __shared__ float sm[];
+  float* sq = sm;                 // [4][dim]
+  float* sc = sm + 4 * dim;       // [64][dim + 1]
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int q = blockIdx.x * 4 + w;
+  for (int j = lane; j < dim; j += 64) sq[w * dim + j] = q < nq ? Qp[(size_t)q * ld + j] : 0.0f;
+  const float* qv = sq + w * dim;
+  uint64_t kept = KEY_MAX, thr = KEY_MAX;
+  const int chunks = dim >> 3;
+  for (int c0 = 0; c0 < produced; c0 += 64) {
+    __syncthreads();
+    const int rows = min(64, produced - c0);
+    for (int r = w; r < rows; r += 4) {
+      const float* src = cents + (size_t)(c0 + r) * ld;
+      float* dst = sc + r * (dim + 1);
+      for (int j = lane; j < dim; j += 64) dst[j] = src[j];
+    }
+    __syncthreads();
+    uint64_t key = KEY_MAX;
+    if (lane < rows && q < nq) {
+      const float* cr = sc + lane * (dim + 1);
+      float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      for (int cc = 0; cc < chunks; ++cc) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float d = qv[cc * 8 + j] - cr[cc * 8 + j];
+          acc[j] += d * d;
+        }
+      }
+      float tail = 0.0f;
+      for (int i = chunks * 8; i < dim; ++i) {
+        const float d = qv[i] - cr[i];
+        tail += d * d;
+      }
+      const float dd = (((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]))) + tail;
+      key = ((uint64_t)ord_key(dd) << 32) | (uint32_t)(c0 + lane);
+    }
+    wave_topk_insert(key, kept, thr, np, lane);
+  }
+  if (q < nq && lane < np) probes[(size_t)q * np + lane] = (int)(uint32_t)kept;
+}
+
 constexpr int IVF_PG = 8;  // probes per workgroup item
 
 template <int W, int METRIC>
@@ -378,6 +434,11 @@ __global__ __launch_bounds__(256) void ivf_merge(const uint64_t* __restrict__ ca
   if (threadIdx.x == 0) out_count[q] = kout;
 }
 
+__global__ void ivf_probes_from_ids(const uint64_t* __restrict__ ids, int n, int* __restrict__ probes) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) probes[i] = (int)ids[i];
+}
+
 __global__ void ivf_count_scanned(const int* __restrict__ probes, int n, const uint32_t* __restrict__ list_off,
                                   unsigned long long* __restrict__ total) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -445,6 +506,10 @@ struct IvfPqIndex {
   DevBuf<uint32_t> list_off, list_rank;
   DevBuf<uint8_t> list_codes;
   std::vector<uint32_t> list_len_h;
+  // the coarse quantizer as an exact flat index over the centroids (ids =
+  // list numbers): MFMA candidates + exact unrolled rescoring give the
+  // reference's (distance, list) order for the probe selection
+  std::unique_ptr<FlatIndex> coarse;
   bool rank_dirty = true, csr_dirty = true;
   std::mutex lazy_mu;
 
@@ -524,6 +589,22 @@ struct IvfPqIndex {
     }
   }
 
+  void build_coarse() {
+    coarse.reset(new FlatIndex());
+    FlatIndex& c = *coarse;
+    c.dim = dim;
+    c.ld = ld;
+    c.metric = PXG_EUCLIDEAN;
+    PXG_HIP(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
+    c.ensure_capacity((size_t)produced, 0);
+    DevBuf<float> dense((size_t)produced * dim);
+    PXG_HIP(hipMemcpy2DAsync(dense.p, dim * 4, cents.p, ld * 4, dim * 4, produced, hipMemcpyDeviceToDevice, stream));
+    PXG_HIP(hipStreamSynchronize(stream));
+    std::vector<uint64_t> lid(produced);
+    for (int l = 0; l < produced; ++l) lid[l] = (uint64_t)l;
+    c.insert_device(lid.data(), dense.p, (uint64_t)produced, nullptr);
+  }
+
   void upload_books(const float* h_cents, int nprod, const float* h_books) {
     produced = nprod;
     cents.alloc((size_t)std::max(nprod, 1) * ld);
@@ -534,6 +615,7 @@ struct IvfPqIndex {
     PXG_HIP(hipStreamSynchronize(stream));
     trained = true;
     csr_dirty = true;
+    build_coarse();
   }
 
   // encode the given slots (vectors must be in X) on the device: nearest
@@ -602,7 +684,12 @@ struct IvfPqIndex {
     books = std::move(B);
     PXG_HIP(hipStreamSynchronize(stream));
     trained = true;
+    build_coarse();
+    const double t_enc = std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
     encode_slots(live_slots);
+    if (std::getenv("PXG_TRAIN_VERBOSE"))
+      std::fprintf(stderr, "[pxg ivfpq] encode %zu vectors %.3fs\n", live_slots.size(),
+                   std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count() - t_enc);
     if (!cfg.retain_vectors) {
       X.release();
       vectors_kept = false;
@@ -778,9 +865,31 @@ struct IvfPqIndex {
       uint64_t* ck = (uint64_t*)ctx->get(8, (size_t)nq * produced * 8);
       int* probes = (int*)ctx->get(9, (size_t)nq * np * 4);
       tm.mark(0);
-      hipLaunchKernelGGL(ivf_coarse_keys, dim3((unsigned)nq), dim3(256), 0, s, Qp, (int)ld, (int)dim, cents.p,
-                         produced, ck);
-      hipLaunchKernelGGL(ivf_coarse_select, dim3((unsigned)nq), dim3(256), 0, s, ck, produced, np, probes);
+      if (np <= 64 && dim <= 256) {
+        const size_t lds = (4 * (size_t)dim + 64 * ((size_t)dim + 1)) * 4;
+        hipLaunchKernelGGL(ivf_coarse_topk, dim3((unsigned)((nq + 3) / 4)), dim3(256), lds, s, Qp, (int)ld, (int)dim,
+                           (int)nq, cents.p, produced, np, probes);
+      } else if (np <= 1024 && coarse) {
+        // exact top-nprobe by (squared_l2, list) through the flat pipeline
+        const float* Qd = Qp;
+        if (ld != dim) {
+          float* dq = (float*)ctx->get(11, nq * dim * 4);
+          PXG_HIP(hipMemcpy2DAsync(dq, dim * 4, Qp, ld * 4, dim * 4, nq, hipMemcpyDeviceToDevice, s));
+          Qd = dq;
+        }
+        uint64_t* cid = (uint64_t*)ctx->get(12, nq * np * 8);
+        float* cdist = (float*)ctx->get(13, nq * np * 4);
+        uint32_t* ccnt = (uint32_t*)ctx->get(14, nq * 4);
+        CtxLease cl(coarse->pool);
+        uint64_t fb = 0;
+        coarse->search_device(Qd, false, nq, (uint64_t)np, nullptr, cid, cdist, ccnt, cl.c, s, &fb);
+        hipLaunchKernelGGL(ivf_probes_from_ids, dim3((unsigned)((nq * np + 255) / 256)), dim3(256), 0, s, cid,
+                           (int)(nq * np), probes);
+      } else {
+        hipLaunchKernelGGL(ivf_coarse_keys, dim3((unsigned)nq), dim3(256), 0, s, Qp, (int)ld, (int)dim, cents.p,
+                           produced, ck);
+        hipLaunchKernelGGL(ivf_coarse_select, dim3((unsigned)nq), dim3(256), 0, s, ck, produced, np, probes);
+      }
       PXG_HIP(hipGetLastError());
       scanned_dev = (unsigned long long*)(flag_count + 2);
       PXG_HIP(hipMemsetAsync(scanned_dev, 0, 8, s));

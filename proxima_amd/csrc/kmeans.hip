@@ -25,7 +25,10 @@
 #include <hipcub/hipcub.hpp>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
 
 #include "common.hpp"
 #include "device.hpp"
@@ -169,42 +172,65 @@ void nearest_device(const float* P, int ldp, const uint32_t* rows, size_t n, int
 // ---------------------------------------------------------------------------
 // f64 sums in point order
 // ---------------------------------------------------------------------------
-// Uniform broadcast of lane i's value (a scalar read, no LDS round trip).
-__device__ inline float lane_value(float x, int i) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), i));
-}
-
-// One wave: every lane carries the same running sum; values arrive 64 at a
-// time and are added one by one in index order.
-__global__ __launch_bounds__(64) void seq_sum_f64(const float* __restrict__ v, int n, double* __restrict__ out) {
+// Sequential f64 prefix sums of v[0..n) in index order: prefix[i] =
+// (((0 + v0) + v1) + ... + vi), total = prefix[n-1]. One wave: all lanes
+// stage the next 1024 values through LDS while lane 0 runs the dependent
+// chain on the current ones. The running sums are non-decreasing for
+// non-negative inputs, so "first index whose cumulative sum reaches target"
+// is a binary search over prefix (seq_find_prefix).
+__global__ __launch_bounds__(64) void seq_prefix_f64(const float* __restrict__ v, int n, double* __restrict__ prefix,
+                                                     double* __restrict__ total) {
+  __shared__ float buf[2][1024];
   const int lane = threadIdx.x;
+  const int nchunks = (n + 1023) / 1024;
+  auto stage = [&](int c, int b) {
+    for (int t = lane; t < 1024; t += 64) {
+      const int i = c * 1024 + t;
+      buf[b][t] = i < n ? v[i] : 0.0f;
+    }
+  };
   double s = 0.0;
-  for (int base = 0; base < n; base += 64) {
-    const float x = base + lane < n ? v[base + lane] : 0.0f;
-    const int m = min(64, n - base);
-    for (int i = 0; i < m; ++i) s += (double)lane_value(x, i);
-  }
-  if (lane == 0) *out = s;
-}
-
-// First index whose cumulative f64 sum reaches target (n - 1 if none).
-__global__ __launch_bounds__(64) void seq_find_cum(const float* __restrict__ v, int n, double target,
-                                                   long long* __restrict__ out) {
-  const int lane = threadIdx.x;
-  double s = 0.0;
-  long long found = n - 1;
-  for (int base = 0; base < n && found == n - 1; base += 64) {
-    const float x = base + lane < n ? v[base + lane] : 0.0f;
-    const int m = min(64, n - base);
-    for (int i = 0; i < m; ++i) {
-      s += (double)lane_value(x, i);
-      if (s >= target) {
-        found = base + i;
-        break;
+  if (nchunks > 0) stage(0, 0);
+  __syncthreads();
+  for (int c = 0; c < nchunks; ++c) {
+    const int b = c & 1;
+    // issue the next chunk's loads before the chain
+    float nx[16];
+    const bool more = c + 1 < nchunks;
+    if (more)
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int i = (c + 1) * 1024 + u * 64 + lane;
+        nx[u] = i < n ? v[i] : 0.0f;
+      }
+    if (lane == 0) {
+      const int m = min(1024, n - c * 1024);
+      double* pf = prefix + (size_t)c * 1024;
+      for (int t = 0; t < m; ++t) {
+        s += (double)buf[b][t];
+        pf[t] = s;
       }
     }
+    if (more)
+#pragma unroll
+      for (int u = 0; u < 16; ++u) buf[b ^ 1][u * 64 + lane] = nx[u];
+    __syncthreads();
   }
-  if (lane == 0) *out = found;
+  if (lane == 0) *total = s;
+}
+
+__global__ void seq_find_prefix(const double* __restrict__ prefix, int n, double target, long long* __restrict__ out) {
+  if (threadIdx.x != 0) return;
+  // first i with prefix[i] >= target; n - 1 if none (kmeans.rs:171-180)
+  int lo = 0, hi = n;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (prefix[mid] >= target)
+      hi = mid;
+    else
+      lo = mid + 1;
+  }
+  *out = lo < n ? lo : n - 1;
 }
 
 // Fixed-order tree sums: block b sums v[b*1024 ..) pairwise; partials summed in order.
@@ -257,12 +283,13 @@ __global__ __launch_bounds__(64) void tree_find_cum(const float* __restrict__ v,
 }
 
 struct F64Sum {
-  DevBuf<double> part, tot;
+  DevBuf<double> part, tot, prefix;
   DevBuf<long long> idx;
   double total(const float* v, size_t n, hipStream_t s) {
     tot.reserve(1);
     if (n <= SEQ_SUM_LIMIT) {
-      hipLaunchKernelGGL(seq_sum_f64, dim3(1), dim3(64), 0, s, v, (int)n, tot.p);
+      prefix.reserve(std::max<size_t>(n, 1));
+      hipLaunchKernelGGL(seq_prefix_f64, dim3(1), dim3(64), 0, s, v, (int)n, prefix.p, tot.p);
     } else {
       const int nb = (int)((n + TREE_SEG - 1) / TREE_SEG);
       part.reserve(nb);
@@ -275,11 +302,11 @@ struct F64Sum {
     PXG_HIP(hipStreamSynchronize(s));
     return h;
   }
-  // uses the partials of the last total() when n > SEQ_SUM_LIMIT
+  // uses the prefix (or partials) of the last total() over the same values
   size_t find(const float* v, size_t n, double target, hipStream_t s) {
     idx.reserve(1);
     if (n <= SEQ_SUM_LIMIT)
-      hipLaunchKernelGGL(seq_find_cum, dim3(1), dim3(64), 0, s, v, (int)n, target, idx.p);
+      hipLaunchKernelGGL(seq_find_prefix, dim3(1), dim3(64), 0, s, prefix.p, (int)n, target, idx.p);
     else
       hipLaunchKernelGGL(tree_find_cum, dim3(1), dim3(64), 0, s, v, (int)n, part.p,
                          (int)((n + TREE_SEG - 1) / TREE_SEG), target, idx.p);
@@ -329,6 +356,8 @@ void kmeans_pp_device(const float* P, size_t n, int dim, int ldp, size_t k, ChaC
   PXG_HIP(hipGetLastError());
   for (size_t chosen = 1; chosen < k; ++chosen) {
     const double total = sums.total(ns.p, n, s);
+    if (!std::isfinite(total))
+      internal_error("kmeans++", "the sum of squared distances is not finite; coordinates are too large to square");
     size_t picked;
     if (total <= 0.0) {
       picked = rng.gen_range_usize(n);
@@ -407,9 +436,17 @@ __global__ __launch_bounds__(1024) void km_farthest(const float* __restrict__ di
   }
 }
 
-struct SortTemp {
-  DevBuf<unsigned char> tmp;
-};
+// Optional phase timings on stderr (PXG_TRAIN_VERBOSE=1), for tuning.
+static bool train_verbose() {
+  static const bool v = [] {
+    const char* e = std::getenv("PXG_TRAIN_VERBOSE");
+    return e && *e && *e != '0';
+  }();
+  return v;
+}
+static double now_s() {
+  return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
 
 KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req, size_t max_iter, ChaCha8* rng,
                         const float* init, DevBuf<float>& cents, DevBuf<uint32_t>* assign_out, hipStream_t s) {
@@ -423,10 +460,13 @@ KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req
     PXG_HIP(hipStreamSynchronize(s));
     return out;
   }
+  const double t_start = now_s();
   if (init)
     PXG_HIP(hipMemcpyAsync(cents.p, init, k * dim * 4, hipMemcpyDeviceToDevice, s));
   else
     kmeans_pp_device(P, n, dim, ldp, k, *rng, cents.p, s);
+  const double t_seeded = now_s();
+  size_t empties = 0;
 
   DevBuf<uint32_t> assign(n), prev(n), counts(k), offsets(k), idx(n), keys_sorted(n), members(n);
   DevBuf<float> dist(n), newc(k * dim), work(k * dim);
@@ -470,6 +510,7 @@ KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req
     // empty clusters, ascending, against the partially updated array
     for (size_t c = 0; c < k; ++c) {
       if (h_counts[c] != 0) continue;
+      ++empties;
       PXG_HIP(hipMemcpyAsync(work.p, newc.p, c * dim * 4, hipMemcpyDeviceToDevice, s));
       PXG_HIP(hipMemcpyAsync(work.p + c * dim, cents.p + c * dim, (k - c) * dim * 4, hipMemcpyDeviceToDevice, s));
       nearest_device(P, ldp, nullptr, n, dim, work.p, dim, k, false, keys_sorted.p, dist.p, s);
@@ -486,6 +527,9 @@ KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req
     PXG_HIP(hipMemcpyAsync(assign_out->p, prev.p, n * 4, hipMemcpyDeviceToDevice, s));
   }
   PXG_HIP(hipStreamSynchronize(s));
+  if (train_verbose())
+    std::fprintf(stderr, "[pxg kmeans] n=%zu dim=%d k=%zu: seeding %.3fs, lloyd %zu it %.3fs, %zu empty reseeds\n", n,
+                 dim, k, t_seeded - t_start, out.iterations, now_s() - t_seeded, empties);
   return out;
 }
 
