@@ -223,55 +223,124 @@ __device__ inline void wave_topk_insert(uint64_t key, uint64_t& kept, uint64_t& 
   }
 }
 
-// Coarse top-nprobe for nprobe <= 64: one wave per query; the block's four
-// queries share 64-row centroid tiles staged in LDS (row stride dim+1, so
-// lane l reading row l is conflict-free). Lane l computes the exact
-// squared_euclidean_unrolled distance (distance.rs:267-283) to centroid
-// c0 + l and the wave keeps the nprobe smallest (distance, list) keys in
-// registers, one per lane, in ascending order.
-__global__ __launch_bounds__(256) void ivf_coarse_topk(const float* __restrict__ Qp, int ld, int dim, int nq,
-                                                       const float* __restrict__ cents, int produced, int np,
-                                                       int* __restrict__ probes) {
-  extern __shared__ float sm[];
-  float* sq = sm;                 // [4][dim]
-  float* sc = sm + 4 * dim;       // [64][dim + 1]
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int q = blockIdx.x * 4 + w;
-  for (int j = lane; j < dim; j += 64) sq[w * dim + j] = q < nq ? Qp[(size_t)q * ld + j] : 0.0f;
-  const float* qv = sq + w * dim;
-  uint64_t kept = KEY_MAX, thr = KEY_MAX;
-  const int chunks = dim >> 3;
-  for (int c0 = 0; c0 < produced; c0 += 64) {
-    __syncthreads();
-    const int rows = min(64, produced - c0);
-    for (int r = w; r < rows; r += 4) {
-      const float* src = cents + (size_t)(c0 + r) * ld;
-      float* dst = sc + r * (dim + 1);
-      for (int j = lane; j < dim; j += 64) dst[j] = src[j];
-    }
-    __syncthreads();
-    uint64_t key = KEY_MAX;
-    if (lane < rows && q < nq) {
-      const float* cr = sc + lane * (dim + 1);
-      float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      for (int cc = 0; cc < chunks; ++cc) {
+__device__ inline uint64_t shfl64(uint64_t v, int src) {
+  const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)v, src, WAVE);
+  const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(v >> 32), src, WAVE);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// `kept` (ascending over the lanes) becomes the 64 smallest of kept and
+// `other` (also ascending): min against the reversed list is bitonic and
+// holds those 64, and a half-cleaner cascade sorts it.
+__device__ inline void wave_merge_sorted(uint64_t& kept, uint64_t other, int lane) {
+  const uint64_t r = shfl64(other, WAVE - 1 - lane);
+  uint64_t v = kept < r ? kept : r;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float d = qv[cc * 8 + j] - cr[cc * 8 + j];
-          acc[j] += d * d;
-        }
-      }
-      float tail = 0.0f;
-      for (int i = chunks * 8; i < dim; ++i) {
-        const float d = qv[i] - cr[i];
-        tail += d * d;
-      }
-      const float dd = (((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]))) + tail;
-      key = ((uint64_t)ord_key(dd) << 32) | (uint32_t)(c0 + lane);
-    }
-    wave_topk_insert(key, kept, thr, np, lane);
+  for (int st = 32; st > 0; st >>= 1) {
+    const uint64_t p = shfl_xor64(v, st);
+    v = (lane & st) ? (v < p ? p : v) : (v < p ? v : p);
   }
-  if (q < nq && lane < np) probes[(size_t)q * np + lane] = (int)(uint32_t)kept;
+  kept = v;
+}
+
+// Add one candidate key per lane to the sorted list: a batch with many
+// passing keys is sorted and merged, a sparse one inserted key by key.
+__device__ inline void wave_topk_add(uint64_t key, uint64_t& kept, uint64_t& thr, int kk, int lane) {
+  const uint64_t mask = __ballot(key < thr);
+  if (mask == 0) return;
+  if (__popcll(mask) > 6) {
+    uint64_t b[1] = {key < thr ? key : KEY_MAX};
+    wave_bitonic_sort<1>(b, lane);
+    wave_merge_sorted(kept, b[0], lane);
+    thr = readlane64(kept, kk - 1);
+  } else {
+    wave_topk_insert(key, kept, thr, kk, lane);
+  }
+}
+
+// Coarse top-nprobe for nprobe <= 64 over the transposed centroid matrix
+// cT[dim][cst] (cst = list count rounded up to 64, zero padded): a block
+// takes IVF_CQ queries (staged in LDS as [dim][IVF_CQ], one broadcast float4
+// per dimension) and its IVF_CW waves split the lists in 64-wide tiles; lane
+// l of a tile computes the exact squared_euclidean_unrolled distance
+// (distance.rs:267-283) from each query to list c0 + l, loading the column
+// coalesced. Each wave keeps per query the 64 smallest (distance, list) keys
+// one per lane, ascending; the waves' lists are merged at the end.
+constexpr int IVF_CQ = 4, IVF_CW = 8;
+
+__global__ __launch_bounds__(IVF_CW * 64) void ivf_coarse_topk(const float* __restrict__ Qp, int ld, int dim, int nq,
+                                                               const float* __restrict__ cT, int cst, int produced,
+                                                               int np, int* __restrict__ probes) {
+  extern __shared__ float4 sm4[];
+  float* sq = (float*)sm4;                             // [dim][IVF_CQ]
+  uint64_t* mk = (uint64_t*)(sm4 + dim);               // [IVF_CW][IVF_CQ][64]
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int q0 = blockIdx.x * IVF_CQ;
+  for (int t = tid; t < dim * IVF_CQ; t += IVF_CW * 64) {
+    const int i = t / IVF_CQ, j = t % IVF_CQ;
+    sq[t] = q0 + j < nq ? Qp[(size_t)(q0 + j) * ld + i] : 0.0f;
+  }
+  __syncthreads();
+  uint64_t kept[IVF_CQ], thr[IVF_CQ];
+#pragma unroll
+  for (int j = 0; j < IVF_CQ; ++j) kept[j] = thr[j] = KEY_MAX;
+  const int chunks = dim >> 3;
+  for (int c0 = w * 64; c0 < produced; c0 += IVF_CW * 64) {
+    const float* col = cT + c0 + lane;
+    float acc[IVF_CQ][8];
+#pragma unroll
+    for (int j = 0; j < IVF_CQ; ++j)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc[j][u] = 0.0f;
+    for (int cc = 0; cc < chunks; ++cc) {
+      float cv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) cv[u] = col[(size_t)(cc * 8 + u) * cst];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float4 qv = sm4[cc * 8 + u];
+        float d;
+        d = qv.x - cv[u]; acc[0][u] += d * d;
+        d = qv.y - cv[u]; acc[1][u] += d * d;
+        d = qv.z - cv[u]; acc[2][u] += d * d;
+        d = qv.w - cv[u]; acc[3][u] += d * d;
+      }
+    }
+    float tail[IVF_CQ] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = chunks * 8; i < dim; ++i) {
+      const float c = col[(size_t)i * cst];
+      const float4 qv = sm4[i];
+      float d;
+      d = qv.x - c; tail[0] += d * d;
+      d = qv.y - c; tail[1] += d * d;
+      d = qv.z - c; tail[2] += d * d;
+      d = qv.w - c; tail[3] += d * d;
+    }
+    const bool valid = c0 + lane < produced;
+#pragma unroll
+    for (int j = 0; j < IVF_CQ; ++j) {
+      const float* a = acc[j];
+      const float dd = (((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))) + tail[j];
+      const uint64_t key = valid ? (((uint64_t)ord_key(dd) << 32) | (uint32_t)(c0 + lane)) : KEY_MAX;
+      wave_topk_add(key, kept[j], thr[j], np, lane);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < IVF_CQ; ++j) mk[(w * IVF_CQ + j) * 64 + lane] = kept[j];
+  __syncthreads();
+  if (w < IVF_CQ && q0 + w < nq) {
+    uint64_t v = mk[w * 64 + lane];
+    for (int ww = 1; ww < IVF_CW; ++ww) wave_merge_sorted(v, mk[(ww * IVF_CQ + w) * 64 + lane], lane);
+    if (lane < np) probes[(size_t)(q0 + w) * np + lane] = (int)(uint32_t)v;
+  }
+}
+
+__global__ void ivf_transpose_cents(const float* __restrict__ C, int ld, int dim, int produced, int cst,
+                                    float* __restrict__ cT) {
+  const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (size_t)dim * cst) return;
+  const int i = (int)(t / cst), c = (int)(t % cst);
+  cT[t] = c < produced ? C[(size_t)c * ld + i] : 0.0f;
 }
 
 constexpr int IVF_PG = 8;  // probes per workgroup item
@@ -501,6 +570,8 @@ struct IvfPqIndex {
   DevBuf<uint8_t> codes;
   DevBuf<uint32_t> d_list_of;
   DevBuf<float> cents, books;
+  DevBuf<float> cents_t;  // [dim][cst] transposed centroids for the coarse scan
+  int cst = 0;
   DevBuf<int> d_sub_off, d_book_off;
   DevBuf<uint32_t> d_rank, d_rank_slot;
   DevBuf<uint32_t> list_off, list_rank;
@@ -603,6 +674,13 @@ struct IvfPqIndex {
     std::vector<uint64_t> lid(produced);
     for (int l = 0; l < produced; ++l) lid[l] = (uint64_t)l;
     c.insert_device(lid.data(), dense.p, (uint64_t)produced, nullptr);
+    cst = (produced + 63) / 64 * 64;
+    cents_t.alloc((size_t)dim * cst);
+    const size_t tot = (size_t)dim * cst;
+    hipLaunchKernelGGL(ivf_transpose_cents, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, stream, cents.p,
+                       (int)ld, (int)dim, produced, cst, cents_t.p);
+    PXG_HIP(hipGetLastError());
+    PXG_HIP(hipStreamSynchronize(stream));
   }
 
   void upload_books(const float* h_cents, int nprod, const float* h_books) {
@@ -865,10 +943,10 @@ struct IvfPqIndex {
       uint64_t* ck = (uint64_t*)ctx->get(8, (size_t)nq * produced * 8);
       int* probes = (int*)ctx->get(9, (size_t)nq * np * 4);
       tm.mark(0);
-      if (np <= 64 && dim <= 256) {
-        const size_t lds = (4 * (size_t)dim + 64 * ((size_t)dim + 1)) * 4;
-        hipLaunchKernelGGL(ivf_coarse_topk, dim3((unsigned)((nq + 3) / 4)), dim3(256), lds, s, Qp, (int)ld, (int)dim,
-                           (int)nq, cents.p, produced, np, probes);
+      if (np <= 64 && dim <= 2048) {
+        const size_t lds = (size_t)dim * IVF_CQ * 4 + (size_t)IVF_CW * IVF_CQ * 64 * 8;
+        hipLaunchKernelGGL(ivf_coarse_topk, dim3((unsigned)((nq + IVF_CQ - 1) / IVF_CQ)), dim3(IVF_CW * 64), lds, s,
+                           Qp, (int)ld, (int)dim, (int)nq, cents_t.p, cst, produced, np, probes);
       } else if (np <= 1024 && coarse) {
         // exact top-nprobe by (squared_l2, list) through the flat pipeline
         const float* Qd = Qp;
@@ -1135,7 +1213,7 @@ int pxg_ivfpq_stats(const pxg_ivfpq* index, pxg_index_stats* out) {
     out->vector_bytes = f.vectors_kept ? f.X.bytes() : 0;
     // codes, lists and codebooks (ivfpq.rs:575-588, 1207-1212)
     out->graph_bytes = f.codes.bytes() + f.d_list_of.bytes() + f.list_rank.bytes() + f.list_off.bytes() +
-                       f.list_codes.bytes() + f.cents.bytes() + f.books.bytes();
+                       f.list_codes.bytes() + f.cents.bytes() + f.cents_t.bytes() + f.books.bytes();
   });
 }
 

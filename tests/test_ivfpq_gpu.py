@@ -288,3 +288,21 @@ def test_search_parity_general_path(gpu, dim, m, k, rerank):
     want = orc.ivf_search(0, cents, books, codes, list_of, np.arange(n), q, k, 5, m,
                           vectors=data if rerank else None, rerank=rerank, threads=8)
     assert_same(idx.search_batch(q, k, nprobe=5), want)
+
+
+@pytest.mark.parametrize("dim,nlist,nq", [(37, 700, 7), (64, 1100, 13), (8, 64, 4)])
+def test_coarse_selection_many_lists(gpu, dim, nlist, nq):
+    """Probe selection over many 64-list tiles split across waves, with a
+    dimension tail, a partial last tile and a partial query group."""
+    px = gpu
+    n, m = 6000, 8 if dim != 37 else 1
+    rng = np.random.default_rng(dim)
+    data = corpus(n, dim, 40) + rng.standard_normal((n, dim)).astype(np.float32) * 0.5
+    cents, books, _ = orc.ivf_train(data, nlist, m, max_iter=3, seed=2)
+    codes, list_of = orc.ivf_encode(data, cents, books, m)
+    idx = build(px, data, px.IvfPqConfig(nlist, m).with_train_threshold(1 << 62))
+    idx.load_trained(cents, books, codes, list_of)
+    q = data[rng.integers(0, n, nq)] + 0.01
+    for nprobe in (1, 33, 64):
+        want = orc.ivf_search(0, cents, books, codes, list_of, np.arange(n), q, 10, nprobe, m, threads=8)
+        assert_same(idx.search_batch(q, 10, nprobe=nprobe), want)
