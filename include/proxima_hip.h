@@ -251,6 +251,75 @@ int pxg_pq_train(const float* training, uint64_t n, uint32_t dim, uint64_t subsp
 int pxg_pq_encode(const float* codebooks, uint32_t dim, uint64_t subspaces, const float* vectors, uint64_t n,
                   uint8_t* codes_out);
 
+/* ------------------------------------------------------------------------ */
+/* Scalar quantizer (crates/proxima-quantize/src/scalar.rs:112-337), on the  */
+/* device. per_dim: 1 = RangeMode::PerDimension (dim ranges), 0 = Global (1). */
+/* code_type: 0 = CodeType::U8, 1 = CodeType::I8 (scalar.rs:25-52).          */
+
+/* ScalarQuantizer::train (scalar.rs:141-199): min / scale / inverse_scale per
+ * range group. A non-finite value fails with NonFinite (its component). */
+int pxg_sq_train(const float* training, uint64_t n, uint32_t dim, int per_dim, float* min, float* scale,
+                 float* inverse_scale);
+/* ScalarQuantizer::encode_into (scalar.rs:246-268) for n vectors (n x dim bytes out). */
+int pxg_sq_encode(const float* vectors, uint64_t n, uint32_t dim, int per_dim, int code_type, const float* min,
+                  const float* inverse_scale, uint8_t* out);
+/* ScalarQuantizer::decode (scalar.rs:271-281, reconstruct 323-327). */
+int pxg_sq_decode(const uint8_t* codes, uint64_t n, uint32_t dim, int per_dim, int code_type, const float* min,
+                  const float* scale, float* out);
+/* asymmetric_inner_product (inner_product != 0, scalar.rs:313-319) or
+ * asymmetric_squared_l2 (298-305) of one f32 query against n codes. */
+int pxg_sq_asymmetric(int inner_product, const float* query, const uint8_t* codes, uint64_t n, uint32_t dim,
+                      int per_dim, int code_type, const float* min, const float* scale, float* out);
+
+/* SQ8 flat index: a VectorIndex over I8 codes with no reference counterpart
+ * (the reference has the quantizer but no SQ index). The score of a stored
+ * vector is -(float)S, S the exact int32 dot product of the query's and the
+ * vector's I8 codes, ordered as TopK (topk.rs:63-67). Metric: inner product,
+ * or cosine (vectors and queries prepared as space.rs:130-138 first). */
+typedef struct pxg_sq8 pxg_sq8;
+int pxg_sq8_create(uint32_t dim, int metric, int per_dim, uint64_t capacity, pxg_sq8** out);
+void pxg_sq8_destroy(pxg_sq8* index);
+/* Fit the ranges (pxg_sq_train semantics) to a host or device sample. */
+int pxg_sq8_train(pxg_sq8* index, const float* training, uint64_t n);
+int pxg_sq8_train_device(pxg_sq8* index, const float* d_training, uint64_t n);
+/* Use ranges trained elsewhere (a ScalarQuantizer's min / scale / inverse_scale). */
+int pxg_sq8_set_ranges(pxg_sq8* index, const float* min, const float* scale, const float* inverse_scale);
+int pxg_sq8_ranges(const pxg_sq8* index, float* min, float* scale, float* inverse_scale);
+int pxg_sq8_is_trained(const pxg_sq8* index);
+/* VectorIndex::insert for n f32 vectors (encoded on the device; the index
+ * must be trained), all-or-nothing as pxg_flat_insert. */
+int pxg_sq8_insert(pxg_sq8* index, const uint64_t* ids, const float* vectors, uint64_t n, uint32_t* out_slots);
+int pxg_sq8_insert_device(pxg_sq8* index, const uint64_t* ids, const float* d_vectors, uint64_t n,
+                          uint32_t* out_slots);
+/* Insert already encoded I8 codes (n x dim bytes). */
+int pxg_sq8_add_codes(pxg_sq8* index, const uint64_t* ids, const int8_t* codes, uint64_t n, uint32_t* out_slots);
+int pxg_sq8_remove(pxg_sq8* index, uint64_t id);
+int pxg_sq8_contains(const pxg_sq8* index, uint64_t id);
+uint64_t pxg_sq8_len(const pxg_sq8* index);
+/* vector_bytes = device code bytes; graph_bytes = the range table (table_bytes). */
+int pxg_sq8_stats(const pxg_sq8* index, pxg_index_stats* out);
+int pxg_sq8_get_code(const pxg_sq8* index, uint64_t id, int8_t* out);
+uint64_t pxg_sq8_slot_count(const pxg_sq8* index);
+int pxg_sq8_slots(const pxg_sq8* index, uint64_t* ids, uint8_t* live);
+/* Search nq f32 queries (encoded with the index's ranges). rescore > 0:
+ * the best max(rescore, k) by integer score are rescored with
+ * asymmetric_inner_product and the best k by (distance, id) returned.
+ * accept as pxg_flat_search. max(k, rescore) <= 1024. */
+int pxg_sq8_search(const pxg_sq8* index, const float* queries, uint64_t nq, uint64_t k, uint64_t rescore,
+                   const uint8_t* accept, uint64_t* out_ids, float* out_dist, uint32_t* out_count);
+/* Search with queries given as I8 codes (nq x dim bytes); no rescoring. */
+int pxg_sq8_search_codes(const pxg_sq8* index, const int8_t* query_codes, uint64_t nq, uint64_t k,
+                         const uint8_t* accept, uint64_t* out_ids, float* out_dist, uint32_t* out_count);
+/* pxg_sq8_search with every pointer in device memory, ordered on `stream`. */
+int pxg_sq8_search_device(const pxg_sq8* index, const float* d_queries, uint64_t nq, uint64_t k, uint64_t rescore,
+                          const uint8_t* d_accept, uint64_t* d_out_ids, float* d_out_dist, uint32_t* d_out_count,
+                          void* stream);
+/* Queries of the last search on this thread that took the exact scan
+ * because their candidate set overflowed. No reference counterpart. */
+uint64_t pxg_sq8_last_fallbacks(void);
+/* 0 = automatic, 1 = integer MFMA whenever dim <= 256, 2 = exact scan. */
+int pxg_sq8_set_search_mode(pxg_sq8* index, int mode);
+
 #ifdef __cplusplus
 }
 #endif

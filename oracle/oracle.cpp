@@ -739,22 +739,48 @@ float orc_sq_asym(int ip, const float* q, const uint8_t* code, size_t dim, int p
 // SQ8 inner-product search over I8 codes (CodeType::I8 bytes). The reference
 // has no integer-domain distance (scalar.rs:298-319 is asymmetric f32); the
 // defined score is -(float)(sum_i q_i * x_i) with the sum an exact int32 over
-// the signed code bytes. Ties and order as TopK.
+// the signed code bytes, slots filtered by `accept` (flat.rs:162-167), ties
+// and order as TopK. With rescore > 0 the best max(rescore, k) by that score
+// are rescored with asymmetric_inner_product (scalar.rs:313-319) of the
+// prepared f32 query `qf` against the decoded code (ranges mn / scale,
+// per-dimension or global), and the best k by (distance, id) are kept.
 void orc_sq8_search(const int8_t* codes, const uint8_t* live, const uint64_t* ids, size_t slots, size_t dim,
-                    const int8_t* qcodes, size_t nq, size_t k, int threads, uint64_t* out_ids, float* out_d,
+                    const int8_t* qcodes, size_t nq, size_t k, const uint8_t* accept, size_t rescore, const float* qf,
+                    int per_dim, const float* mn, const float* scale, int threads, uint64_t* out_ids, float* out_d,
                     uint32_t* out_count) {
   auto work = [&](size_t q0, size_t q1) {
+    const size_t kk = rescore ? std::max(rescore, k) : k;
+    std::unordered_map<uint64_t, size_t> slot_of;
     for (size_t q = q0; q < q1; ++q) {
-      TopK top(k);
+      TopK top(kk);
       const int8_t* qc = qcodes + q * dim;
       for (size_t s = 0; s < slots; ++s) {
-        if (!live[s]) continue;
+        if (!live[s] || !accepted(accept, s)) continue;
         const int8_t* xc = codes + s * dim;
         int32_t acc = 0;
         for (size_t j = 0; j < dim; ++j) acc += (int32_t)qc[j] * (int32_t)xc[j];
         top.push(ids[s], -(float)acc);
       }
-      out_count[q] = (uint32_t)emit(top, out_ids + q * k, out_d + q * k);
+      if (!rescore) {
+        out_count[q] = (uint32_t)emit(top, out_ids + q * k, out_d + q * k);
+        continue;
+      }
+      if (slot_of.empty())
+        for (size_t s = 0; s < slots; ++s)
+          if (live[s]) slot_of[ids[s]] = s;
+      TopK fin(k);
+      for (const Hit& h : top.sorted()) {
+        const uint8_t* code = reinterpret_cast<const uint8_t*>(codes + slot_of[h.id] * dim);
+        float sum = 0.0f;
+        for (size_t c = 0; c < dim; ++c) {
+          const size_t g = per_dim ? c : 0;
+          const uint8_t level = (uint8_t)(code[c] + 128);
+          const float rec = mn[g] + (float)level * scale[g];
+          sum += qf[q * dim + c] * rec;
+        }
+        fin.push(h.id, -sum);
+      }
+      out_count[q] = (uint32_t)emit(fin, out_ids + q * k, out_d + q * k);
     }
   };
   if (threads <= 1 || nq <= 1) {

@@ -55,7 +55,8 @@ def _load():
         "orc_sq_encode": (None, [_f32p, _sz, C.c_int, C.c_int, _f32p, _f32p, _u8p]),
         "orc_sq_decode": (None, [_u8p, _sz, C.c_int, C.c_int, _f32p, _f32p, _f32p]),
         "orc_sq_asym": (C.c_float, [C.c_int, _f32p, _u8p, _sz, C.c_int, C.c_int, _f32p, _f32p]),
-        "orc_sq8_search": (None, [_i8p, _u8p, _u64p, _sz, _sz, _i8p, _sz, _sz, C.c_int, _u64p, _f32p, _u32p]),
+        "orc_sq8_search": (None, [_i8p, _u8p, _u64p, _sz, _sz, _i8p, _sz, _sz, C.c_void_p, _sz, C.c_void_p,
+                                  C.c_int, C.c_void_p, C.c_void_p, C.c_int, _u64p, _f32p, _u32p]),
         "orc_pq_layout": (None, [_sz, _sz, np.ctypeslib.ndpointer(np.uintp), np.ctypeslib.ndpointer(np.uintp)]),
         "orc_pq_table": (None, [_f32p, _sz, _sz, _f32p, _f32p, _f32p]),
         "orc_pq_adc_l2": (C.c_float, [_f32p, _sz, _u8p]),
@@ -222,10 +223,15 @@ def sq_encode(v, mn, inv, per_dim=True, code_type=1):
 
 
 def sq_decode(code, mn, scale, per_dim=True, code_type=1):
+    """Decode one code (1-D) or a batch of codes (one row each)."""
     code = np.ascontiguousarray(code, dtype=np.uint8)
-    out = np.zeros(code.size, np.float32)
-    lib.orc_sq_decode(code, code.size, int(per_dim), code_type, mn, scale, out)
-    return out
+    rows = code.reshape(-1, code.shape[-1])
+    out = np.zeros(rows.shape, np.float32)
+    for i in range(rows.shape[0]):
+        o = np.zeros(rows.shape[1], np.float32)
+        lib.orc_sq_decode(np.ascontiguousarray(rows[i]), rows.shape[1], int(per_dim), code_type, mn, scale, o)
+        out[i] = o
+    return out.reshape(code.shape)
 
 
 def sq_asym(ip, q, code, mn, scale, per_dim=True, code_type=1):
@@ -234,7 +240,12 @@ def sq_asym(ip, q, code, mn, scale, per_dim=True, code_type=1):
     return lib.orc_sq_asym(int(ip), q, code, q.size, int(per_dim), code_type, mn, scale)
 
 
-def sq8_search(codes, ids, qcodes, k, live=None, threads=1):
+def sq8_search(codes, ids, qcodes, k, live=None, threads=1, accept=None, rescore=0, qf=None, ranges=None,
+               per_dim=True):
+    """Integer-score SQ8 search over I8 codes; with rescore > 0 the best
+    max(rescore, k) are rescored with asymmetric_inner_product of the
+    prepared f32 queries `qf` against codes decoded with `ranges` = (min,
+    scale)."""
     codes = np.ascontiguousarray(codes, dtype=np.int8)
     slots, dim = codes.shape
     qcodes = np.ascontiguousarray(qcodes, dtype=np.int8).reshape(-1, dim)
@@ -244,8 +255,21 @@ def sq8_search(codes, ids, qcodes, k, live=None, threads=1):
     oi = np.zeros((nq, kk), np.uint64)
     od = np.zeros((nq, kk), np.float32)
     oc = np.zeros(nq, np.uint32)
-    lib.orc_sq8_search(codes, live, np.ascontiguousarray(ids, dtype=np.uint64), slots, dim, qcodes, nq, k, threads,
-                       oi, od, oc)
+    keep = []
+
+    def ptr(a, dt):
+        if a is None:
+            return None
+        a = np.ascontiguousarray(a, dtype=dt)
+        keep.append(a)
+        return a.ctypes.data
+
+    mn, sc = (None, None) if ranges is None else ranges
+    if rescore and (qf is None or ranges is None):
+        raise ValueError("rescore needs the f32 queries and the ranges")
+    lib.orc_sq8_search(codes, live, np.ascontiguousarray(ids, dtype=np.uint64), slots, dim, qcodes, nq, k,
+                       ptr(accept, np.uint8), rescore, ptr(qf, np.float32), int(per_dim), ptr(mn, np.float32),
+                       ptr(sc, np.float32), threads, oi, od, oc)
     return oi, od, oc
 
 

@@ -723,3 +723,281 @@ class ProductQuantizer:
 
 __all__ += ["IvfPqConfig", "IvfPqIndex", "TrainingReport", "Clustering", "kmeans", "kmeans_lloyd", "kmeans_pp",
             "kmeans_assign", "PqConfig", "ProductQuantizer"]
+
+
+# --- ScalarQuantizer: scalar.rs:25-337 ----------------------------------------------------
+class CodeType:
+    """CodeType (scalar.rs:25-52): U8 stores the level, I8 stores level - 128."""
+    U8 = 0
+    I8 = 1
+
+
+class RangeMode:
+    """RangeMode (scalar.rs:58-74)."""
+    GLOBAL = 0
+    PER_DIMENSION = 1
+
+
+class ScalarQuantizer:
+    """Affine f32 -> one-byte quantizer (scalar.rs:112-337); training, encoding,
+    decoding and the asymmetric distances run on the GPU."""
+
+    LEVELS = 256
+
+    def __init__(self, dim, mode, code_type, min, scale, inverse_scale):
+        self._dim, self._mode, self._code_type = dim, mode, code_type
+        self.min = np.ascontiguousarray(min, dtype=np.float32)
+        self.scale = np.ascontiguousarray(scale, dtype=np.float32)
+        self.inverse_scale = np.ascontiguousarray(inverse_scale, dtype=np.float32)
+
+    @classmethod
+    def train(cls, space, training, mode=RangeMode.PER_DIMENSION, code_type=CodeType.U8):
+        t = np.ascontiguousarray(training, dtype=np.float32).reshape(-1)
+        if t.size == 0 or t.size % space.dim:
+            raise _config("training", t.size, "must be a non-empty multiple of the space dimension")
+        g = space.dim if mode == RangeMode.PER_DIMENSION else 1
+        mn, sc, inv = (np.zeros(g, np.float32) for _ in range(3))
+        _check(_lib.pxg_sq_train(_ptr(t), t.size // space.dim, space.dim, int(mode == RangeMode.PER_DIMENSION),
+                                 _ptr(mn), _ptr(sc), _ptr(inv)))
+        return cls(space.dim, mode, code_type, mn, sc, inv)
+
+    def dim(self):
+        return self._dim
+
+    def code_len(self):
+        return self._dim
+
+    def range_mode(self):
+        return self._mode
+
+    def code_type(self):
+        return self._code_type
+
+    def compression_ratio(self):
+        return 4.0
+
+    def table_bytes(self):
+        return (self.min.size + self.scale.size + self.inverse_scale.size) * 4
+
+    def _per_dim(self):
+        return int(self._mode == RangeMode.PER_DIMENSION)
+
+    def encode(self, vector):
+        v = np.asarray(vector, dtype=np.float32).reshape(-1)
+        if v.size != self._dim:
+            raise DimensionMismatch(f"dimension mismatch: quantizer holds {self._dim} dimensions, got {v.size}",
+                                    self._dim, v.size)
+        return self.encode_batch(v.reshape(1, -1))[0]
+
+    def encode_batch(self, vectors):
+        v = _rows(vectors, self._dim)
+        out = np.zeros(v.shape, np.uint8)
+        _check(_lib.pxg_sq_encode(_ptr(v), v.shape[0], self._dim, self._per_dim(), self._code_type,
+                                  _ptr(self.min), _ptr(self.inverse_scale), _ptr(out)))
+        return out
+
+    def decode(self, code):
+        c = np.ascontiguousarray(code, dtype=np.uint8).reshape(-1)
+        if c.size % self._dim or c.size == 0:
+            raise DimensionMismatch(f"dimension mismatch: quantizer holds {self._dim} dimensions, got {c.size}",
+                                    self._dim, c.size)
+        out = np.zeros(c.size, np.float32)
+        _check(_lib.pxg_sq_decode(_ptr(c), c.size // self._dim, self._dim, self._per_dim(), self._code_type,
+                                  _ptr(self.min), _ptr(self.scale), _ptr(out)))
+        return out.reshape(np.shape(code)) if np.ndim(code) > 1 else out
+
+    def _asym(self, ip, query, codes):
+        q = np.ascontiguousarray(query, dtype=np.float32).reshape(-1)
+        c = np.ascontiguousarray(codes, dtype=np.uint8).reshape(-1, self._dim)
+        out = np.zeros(c.shape[0], np.float32)
+        _check(_lib.pxg_sq_asymmetric(ip, _ptr(q), _ptr(c), c.shape[0], self._dim, self._per_dim(),
+                                      self._code_type, _ptr(self.min), _ptr(self.scale), _ptr(out)))
+        return out if np.ndim(codes) > 1 else float(out[0])
+
+    def asymmetric_squared_l2(self, query, code):  # scalar.rs:298-305
+        return self._asym(0, query, code)
+
+    def asymmetric_inner_product(self, query, code):  # scalar.rs:313-319
+        return self._asym(1, query, code)
+
+
+class Sq8Index(_IndexBase):
+    """SQ8 flat index over I8 codes on integer MFMA (no reference counterpart:
+    the reference has the quantizer, not an SQ index). Score = -(float)S with S
+    the exact int32 dot product of the query's and the vector's I8 codes,
+    ordered as TopK; `rescore` rescores the best max(rescore, k) with
+    asymmetric_inner_product. Ranges are fitted to prepared vectors."""
+
+    def __init__(self, space, mode=RangeMode.PER_DIMENSION, capacity=0):
+        self.space = space
+        self._mode = mode
+        h = C.c_void_p()
+        _check(_lib.pxg_sq8_create(space.dim, space.metric, int(mode == RangeMode.PER_DIMENSION), capacity,
+                                   C.byref(h)))
+        self._h = h
+        self._meta = {}
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            _lib.pxg_sq8_destroy(h)
+            self._h = None
+
+    @classmethod
+    def from_array(cls, space, data, training_sample=100_000, mode=RangeMode.PER_DIMENSION):
+        """Train on the first `training_sample` vectors, then insert all with ids 0..n."""
+        data = _rows(data, space.dim)
+        idx = cls(space, mode, data.shape[0])
+        if data.shape[0]:
+            idx.train(data[:training_sample])
+            idx.insert_batch(np.arange(data.shape[0], dtype=np.uint64), data)
+        return idx
+
+    # -- quantizer --
+    def train(self, training):
+        t = np.ascontiguousarray(training, dtype=np.float32).reshape(-1)
+        if t.size == 0 or t.size % self.space.dim:
+            raise _config("training", t.size, "must be a non-empty multiple of the space dimension")
+        _check(_lib.pxg_sq8_train(self._h, _ptr(t), t.size // self.space.dim))
+
+    def train_device(self, training):
+        if training.shape[-1] != self.space.dim:
+            raise DimensionMismatch("dimension mismatch: device sample does not match the index", self.space.dim,
+                                    training.shape[-1])
+        _check(_lib.pxg_sq8_train_device(self._h, _device_ptr(training), training.shape[0]))
+
+    def _groups(self):
+        return self.space.dim if self._mode == RangeMode.PER_DIMENSION else 1
+
+    def set_quantizer(self, sq):
+        if sq.dim() != self.space.dim or sq.range_mode() != self._mode:
+            raise _config("quantizer", sq.dim(), "dimension or range mode differs from the index")
+        _check(_lib.pxg_sq8_set_ranges(self._h, _ptr(sq.min), _ptr(sq.scale), _ptr(sq.inverse_scale)))
+
+    def quantizer(self):
+        g = self._groups()
+        mn, sc, inv = (np.zeros(g, np.float32) for _ in range(3))
+        _check(_lib.pxg_sq8_ranges(self._h, _ptr(mn), _ptr(sc), _ptr(inv)))
+        return ScalarQuantizer(self.space.dim, self._mode, CodeType.I8, mn, sc, inv)
+
+    def is_trained(self):
+        return bool(_lib.pxg_sq8_is_trained(self._h))
+
+    # -- mutation --
+    def insert(self, id, vector, metadata=None):
+        v = np.asarray(vector, dtype=np.float32).reshape(-1)
+        if v.size != self.space.dim:
+            raise DimensionMismatch(
+                f"dimension mismatch: index holds {self.space.dim}-dimensional vectors, got {v.size}",
+                self.space.dim, v.size)
+        self.insert_batch(np.array([id], np.uint64), v.reshape(1, -1))
+        if metadata:
+            self._meta[int(id)] = dict(metadata)
+
+    def insert_batch(self, ids, vectors):
+        ids = np.ascontiguousarray(ids, dtype=np.uint64).reshape(-1)
+        v = _rows(vectors, self.space.dim)
+        if v.shape[0] != ids.size:
+            raise ValueError("ids and vectors disagree on the batch size")
+        slots = np.zeros(ids.size, np.uint32)
+        _check(_lib.pxg_sq8_insert(self._h, _ptr(ids), _ptr(v), ids.size, _ptr(slots)))
+        return slots
+
+    def insert_device(self, ids, vectors):
+        ids = np.ascontiguousarray(ids, dtype=np.uint64).reshape(-1)
+        if vectors.shape[-1] != self.space.dim or vectors.shape[0] != ids.size:
+            raise DimensionMismatch("dimension mismatch: device batch does not match the index", self.space.dim,
+                                    vectors.shape[-1])
+        slots = np.zeros(ids.size, np.uint32)
+        _check(_lib.pxg_sq8_insert_device(self._h, _ptr(ids), _device_ptr(vectors), ids.size, _ptr(slots)))
+        return slots
+
+    def add_codes(self, ids, codes):
+        ids = np.ascontiguousarray(ids, dtype=np.uint64).reshape(-1)
+        c = np.ascontiguousarray(codes, dtype=np.int8).reshape(-1, self.space.dim)
+        if c.shape[0] != ids.size:
+            raise ValueError("ids and codes disagree on the batch size")
+        slots = np.zeros(ids.size, np.uint32)
+        _check(_lib.pxg_sq8_add_codes(self._h, _ptr(ids), _ptr(c), ids.size, _ptr(slots)))
+        return slots
+
+    def remove(self, id):
+        _check(_lib.pxg_sq8_remove(self._h, int(id)))
+        self._meta.pop(int(id), None)
+
+    # -- queries --
+    def contains(self, id):
+        return bool(_lib.pxg_sq8_contains(self._h, int(id)))
+
+    def __len__(self):
+        return int(_lib.pxg_sq8_len(self._h))
+
+    def stats(self):
+        s = _IndexStatsC()
+        _check(_lib.pxg_sq8_stats(self._h, C.byref(s)))
+        return _stats_from_c(s)
+
+    def code(self, id):
+        out = np.zeros(self.space.dim, np.int8)
+        try:
+            _check(_lib.pxg_sq8_get_code(self._h, int(id), _ptr(out)))
+        except UnknownId:
+            return None
+        return out
+
+    def slots(self):
+        n = int(_lib.pxg_sq8_slot_count(self._h))
+        ids = np.zeros(max(n, 1), np.uint64)
+        live = np.zeros(max(n, 1), np.uint8)
+        _check(_lib.pxg_sq8_slots(self._h, _ptr(ids), _ptr(live)))
+        return ids[:n], live[:n]
+
+    def set_search_mode(self, mode):
+        _check(_lib.pxg_sq8_set_search_mode(self._h, mode))
+
+    def search(self, query, k, filter=None, rescore=0):
+        ids, dists, counts = self.search_batch(np.asarray(query, dtype=np.float32).reshape(1, -1), k, filter,
+                                               rescore)
+        return [SearchResult(int(ids[0, i]), float(dists[0, i])) for i in range(int(counts[0]))]
+
+    def _outputs(self, nq, k):
+        kk = max(k, 1)
+        return np.zeros((nq, kk), np.uint64), np.zeros((nq, kk), np.float32), np.zeros(max(nq, 1), np.uint32)
+
+    def _mask(self, filter):
+        if filter is None:
+            return None
+        sid, live = self.slots()
+        return self._accept_mask(filter, sid, live)
+
+    def search_batch(self, queries, k, filter=None, rescore=0):
+        check_k(k)
+        q = _rows(queries, self.space.dim)
+        nq = q.shape[0]
+        acc = self._mask(filter)
+        oi, od, oc = self._outputs(nq, k)
+        _check(_lib.pxg_sq8_search(self._h, _ptr(q), nq, k, rescore, _ptr(acc), _ptr(oi), _ptr(od), _ptr(oc)))
+        return oi[:, :k], od[:, :k], oc[:nq]
+
+    def search_codes(self, query_codes, k, filter=None):
+        """Search with queries given as I8 codes [nq, dim]."""
+        check_k(k)
+        c = np.ascontiguousarray(query_codes, dtype=np.int8).reshape(-1, self.space.dim)
+        nq = c.shape[0]
+        acc = self._mask(filter)
+        oi, od, oc = self._outputs(nq, k)
+        _check(_lib.pxg_sq8_search_codes(self._h, _ptr(c), nq, k, _ptr(acc), _ptr(oi), _ptr(od), _ptr(oc)))
+        return oi[:, :k], od[:, :k], oc[:nq]
+
+    def search_device(self, queries, k, out_ids, out_dist, out_count, rescore=0, accept=None, stream=None):
+        _check(_lib.pxg_sq8_search_device(
+            self._h, _device_ptr(queries), queries.shape[0], k, rescore,
+            None if accept is None else _device_ptr(accept), _device_ptr(out_ids), _device_ptr(out_dist),
+            _device_ptr(out_count), None if stream is None else C.c_void_p(stream)))
+
+    @staticmethod
+    def last_fallbacks():
+        return int(_lib.pxg_sq8_last_fallbacks())
+
+
+__all__ += ["CodeType", "RangeMode", "ScalarQuantizer", "Sq8Index"]

@@ -121,6 +121,33 @@ SIGNATURES = {
     "pxg_kmeans_assign": (_i32, [_vp, _u64, _u32, _vp, _u64, _vp, _vp]),
     "pxg_pq_train": (_i32, [_vp, _u64, _u32, _u64, _u64, _u64, _vp, _P(_f64), _P(_u64)]),
     "pxg_pq_encode": (_i32, [_vp, _u32, _u64, _vp, _u64, _vp]),
+    # scalar quantizer / SQ8 index
+    "pxg_sq_train": (_i32, [_vp, _u64, _u32, _i32, _vp, _vp, _vp]),
+    "pxg_sq_encode": (_i32, [_vp, _u64, _u32, _i32, _i32, _vp, _vp, _vp]),
+    "pxg_sq_decode": (_i32, [_vp, _u64, _u32, _i32, _i32, _vp, _vp, _vp]),
+    "pxg_sq_asymmetric": (_i32, [_i32, _vp, _vp, _u64, _u32, _i32, _i32, _vp, _vp, _vp]),
+    "pxg_sq8_create": (_i32, [_u32, _i32, _i32, _u64, _P(_vp)]),
+    "pxg_sq8_destroy": (None, [_vp]),
+    "pxg_sq8_train": (_i32, [_vp, _vp, _u64]),
+    "pxg_sq8_train_device": (_i32, [_vp, _vp, _u64]),
+    "pxg_sq8_set_ranges": (_i32, [_vp, _vp, _vp, _vp]),
+    "pxg_sq8_ranges": (_i32, [_vp, _vp, _vp, _vp]),
+    "pxg_sq8_is_trained": (_i32, [_vp]),
+    "pxg_sq8_insert": (_i32, [_vp, _vp, _vp, _u64, _vp]),
+    "pxg_sq8_insert_device": (_i32, [_vp, _vp, _vp, _u64, _vp]),
+    "pxg_sq8_add_codes": (_i32, [_vp, _vp, _vp, _u64, _vp]),
+    "pxg_sq8_remove": (_i32, [_vp, _u64]),
+    "pxg_sq8_contains": (_i32, [_vp, _u64]),
+    "pxg_sq8_len": (_u64, [_vp]),
+    "pxg_sq8_stats": (_i32, [_vp, _P(IndexStats)]),
+    "pxg_sq8_get_code": (_i32, [_vp, _u64, _vp]),
+    "pxg_sq8_slot_count": (_u64, [_vp]),
+    "pxg_sq8_slots": (_i32, [_vp, _vp, _vp]),
+    "pxg_sq8_search": (_i32, [_vp, _vp, _u64, _u64, _u64, _vp, _vp, _vp, _vp]),
+    "pxg_sq8_search_codes": (_i32, [_vp, _vp, _u64, _u64, _vp, _vp, _vp, _vp]),
+    "pxg_sq8_search_device": (_i32, [_vp, _vp, _u64, _u64, _u64, _vp, _vp, _vp, _vp, _vp]),
+    "pxg_sq8_last_fallbacks": (_u64, []),
+    "pxg_sq8_set_search_mode": (_i32, [_vp, _i32]),
 }
 
 

@@ -118,7 +118,8 @@ static __global__ __launch_bounds__(256) void flat_merge_exact(const int* __rest
                                                         const uint32_t* __restrict__ rank_slot,
                                                         const uint64_t* __restrict__ ids,
                                                         uint64_t* __restrict__ out_ids, float* __restrict__ out_d,
-                                                        uint32_t* __restrict__ out_count) {
+                                                        uint32_t* __restrict__ out_count,
+                                                        uint64_t* __restrict__ out_keys) {
   const int f = blockIdx.x;
   if (f >= *qcount) return;
   const int q = qlist[f];
@@ -157,8 +158,12 @@ static __global__ __launch_bounds__(256) void flat_merge_exact(const int* __rest
   block_bitonic_sort(sel, P);
   for (int i = threadIdx.x; i < ksel; i += blockDim.x) {
     const uint64_t key = sel[i];
-    out_ids[(size_t)q * k + i] = ids[rank_slot[(uint32_t)key]];
-    out_d[(size_t)q * k + i] = key_float((uint32_t)(key >> 32));
+    if (out_keys) {
+      out_keys[(size_t)q * k + i] = key;  // (distance, id rank) keys for a later stage
+    } else {
+      out_ids[(size_t)q * k + i] = ids[rank_slot[(uint32_t)key]];
+      out_d[(size_t)q * k + i] = key_float((uint32_t)(key >> 32));
+    }
   }
   if (threadIdx.x == 0) out_count[q] = ksel;
 }

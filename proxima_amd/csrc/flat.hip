@@ -513,7 +513,7 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
     PXG_HIP(hipGetLastError());
     if (exact_all) tm.mark(2);
     hipLaunchKernelGGL(flat_merge_exact, dim3((unsigned)nflag), dim3(256), 0, s, flag_list, flag_count, ecand,
-                       nchunks, (int)k, d_rank_slot.p, d_ids.p, d_oid, d_od, d_oc);
+                       nchunks, (int)k, d_rank_slot.p, d_ids.p, d_oid, d_od, d_oc, (uint64_t*)nullptr);
     PXG_HIP(hipGetLastError());
     PXG_HIP(hipStreamSynchronize(s));
     *fallbacks = exact_all ? 0 : (uint64_t)nflag;

@@ -931,7 +931,7 @@ struct IvfPqIndex {
       PXG_HIP(hipGetLastError());
       tm.mark(2);
       hipLaunchKernelGGL(flat_merge_exact, dim3((unsigned)nq), dim3(256), 0, s, qlist, flag_count, ecand, nchunks,
-                         (int)k, d_rank_slot.p, d_ids.p, d_oid, d_od, d_oc);
+                         (int)k, d_rank_slot.p, d_ids.p, d_oid, d_od, d_oc, (uint64_t*)nullptr);
       PXG_HIP(hipGetLastError());
     } else {
       const int np = (int)std::min<uint64_t>(std::max<uint64_t>(nprobe_in, 1), (uint64_t)std::max(produced, 1));

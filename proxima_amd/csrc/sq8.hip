@@ -1,0 +1,1310 @@
+// Scalar quantizer (crates/proxima-quantize/src/scalar.rs) and the SQ8 flat
+// index on gfx950.
+//
+// The reference has a ScalarQuantizer but no SQ index and no integer-domain
+// distance: its distance is the asymmetric f32 one (scalar.rs:298-319). The
+// SQ8 index defines, for I8 codes (level - 128) of the query and of every
+// stored vector, the score
+//
+//     distance = -(float) S,   S = sum_i q_i * x_i   (exact int32)
+//
+// ordered as TopK orders search results (topk.rs:63-67: distance, then id).
+// Optionally the best max(rescore, k) by that score are rescored with
+// asymmetric_inner_product (scalar.rs:313-319) on the prepared f32 query.
+//
+// Kernels
+//   sq_minmax / sq_encode_rows          range training and encoding
+//   sq8_mfma_scan<KB,QT,STAGE1>         i8 x i8 -> i32 on v_mfma_i32_32x32x32_i8
+//       stage 1: every SQ_SAMPLE-th row tile, per-lane maxima over usable rows
+//       stage 2: every tile; a v_max3 chain and one compare per 16 scores,
+//                rows scoring >= the query's threshold are appended
+//   sq8_thresholds                      k-th largest stage-1 maximum per query
+//   sq8_finish                          exact sort of each query's candidates
+//   sq8_exact_candidates                v_dot4 exact scan (overflowed queries,
+//                                       small or wide indexes)
+//   sq8_rescore / sq8_emit              f32 rescoring or id/distance output
+//
+// Why the threshold is safe: stage-1 maxima are scores of distinct usable
+// rows (each (chunk, lane half) covers its own rows), so the k-th largest of
+// them is <= the k-th best score of the whole index. Every row of the true
+// top k, ties at the boundary included, scores >= it and is appended; the
+// candidates are then ordered exactly. A query with more than `cap`
+// candidates takes the exact scan instead.
+#include <algorithm>
+#include <climits>
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <shared_mutex>
+#include <unordered_map>
+#include <vector>
+
+#include "common.hpp"
+#include "device.hpp"
+#include "exact_scan.hpp"
+
+namespace pxg {
+
+typedef int i4v __attribute__((ext_vector_type(4)));
+typedef int i16v __attribute__((ext_vector_type(16)));
+
+constexpr int SQ_NW = 8;              // waves per scan workgroup
+constexpr int SQ_SAMPLE = 8;          // stage 1 visits at most one row tile in 8
+constexpr int SQ_MAX_CHUNKS = 1024;   // stage-1 entries per query <= 2 * this
+constexpr int SQ_MAX_KB = 8;          // MFMA path: code rows up to 256 bytes
+constexpr uint32_t SQ_MAX_DIM = 65536;  // |S| < 2^31
+
+__host__ __device__ constexpr int sq_rows(int kb) { return kb <= 4 ? 128 : 64; }
+__host__ __device__ constexpr int sq_qt(int kb) { return kb <= 4 ? 4 : 2; }
+
+__device__ inline uint32_t f2ord(float f) {
+  const uint32_t b = __float_as_uint(f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+static float ord2f(uint32_t u) {
+  const uint32_t b = (u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u;
+  float f;
+  std::memcpy(&f, &b, 4);
+  return f;
+}
+
+// ---------------------------------------------------------------------------
+// Range training (scalar.rs:141-199): per-dimension or global min / max of a
+// training set, plus the first non-finite value in row-major order.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void sq_minmax(const float* __restrict__ X, int ld, uint64_t n, int dim,
+                                                 int per_dim, uint64_t row0, uint32_t* __restrict__ omin,
+                                                 uint32_t* __restrict__ omax, unsigned long long* __restrict__ bad) {
+  const uint64_t per = (n + gridDim.x - 1) / gridDim.x;
+  const uint64_t r0 = (uint64_t)blockIdx.x * per, r1 = r0 + per < n ? r0 + per : n;
+  if (r0 >= r1) return;
+  if (per_dim) {
+    for (int c = threadIdx.x; c < dim; c += blockDim.x) {
+      uint32_t mn = 0xFFFFFFFFu, mx = 0u;
+      for (uint64_t r = r0; r < r1; ++r) {
+        const float v = X[r * ld + c];
+        if (!isfinite(v)) {
+          atomicMin(bad, ((unsigned long long)(row0 + r) << 32) | (unsigned)c);
+          continue;
+        }
+        const uint32_t o = f2ord(v);
+        mn = min(mn, o);
+        mx = max(mx, o);
+      }
+      atomicMin(&omin[c], mn);
+      atomicMax(&omax[c], mx);
+    }
+  } else {
+    __shared__ uint32_t smn[256], smx[256];
+    uint32_t mn = 0xFFFFFFFFu, mx = 0u;
+    const uint64_t total = (r1 - r0) * (uint64_t)dim;
+    for (uint64_t e = threadIdx.x; e < total; e += blockDim.x) {
+      const float v = X[(r0 + e / dim) * ld + e % dim];
+      if (!isfinite(v)) {
+        atomicMin(bad, ((unsigned long long)(row0 + r0 + e / dim) << 32) | (unsigned)(e % dim));
+        continue;
+      }
+      const uint32_t o = f2ord(v);
+      mn = min(mn, o);
+      mx = max(mx, o);
+    }
+    smn[threadIdx.x] = mn;
+    smx[threadIdx.x] = mx;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+      if ((int)threadIdx.x < s) {
+        smn[threadIdx.x] = min(smn[threadIdx.x], smn[threadIdx.x + s]);
+        smx[threadIdx.x] = max(smx[threadIdx.x], smx[threadIdx.x + s]);
+      }
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+      atomicMin(&omin[0], smn[0]);
+      atomicMax(&omax[0], smx[0]);
+    }
+  }
+}
+
+// encode_into (scalar.rs:246-268): level = clamp(round((v - min) * inv),
+// 0, 255) with round half away from zero; I8 stores level - 128. Row i of P
+// (stride ld) goes to row dst[i] (or i) of `out` (stride ostride), zero padded.
+__global__ __launch_bounds__(64) void sq_encode_rows(const float* __restrict__ P, int ld, int n, int dim, int per_dim,
+                                                     int code_type, const float* __restrict__ mn,
+                                                     const float* __restrict__ inv, const uint32_t* __restrict__ dst,
+                                                     uint8_t* __restrict__ out, int ostride) {
+  const int i = blockIdx.x;
+  if (i >= n) return;
+  uint8_t* o = out + (size_t)(dst ? dst[i] : (uint32_t)i) * ostride;
+  const float* v = P + (size_t)i * ld;
+  for (int c = threadIdx.x; c < ostride; c += blockDim.x) {
+    uint8_t b = 0;
+    if (c < dim) {
+      const int g = per_dim ? c : 0;
+      float r = roundf((v[c] - mn[g]) * inv[g]);
+      r = fminf(fmaxf(r, 0.0f), 255.0f);
+      const uint8_t level = (uint8_t)r;
+      b = code_type == 1 ? (uint8_t)(level - 128u) : level;
+    }
+    o[c] = b;
+  }
+}
+
+// reconstruct (scalar.rs:323-327) and the asymmetric distances (298-319),
+// one code row per thread, components in order.
+__device__ inline float sq_reconstruct(uint8_t byte, int code_type, float mn, float scale) {
+  const uint8_t level = code_type == 1 ? (uint8_t)(byte + 128u) : byte;
+  return mn + (float)level * scale;
+}
+
+__global__ void sq_decode_rows(const uint8_t* __restrict__ codes, uint64_t n, int dim, int per_dim, int code_type,
+                               const float* __restrict__ mn, const float* __restrict__ scale, float* __restrict__ out) {
+  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n * (uint64_t)dim) return;
+  const int c = (int)(t % dim), g = per_dim ? c : 0;
+  out[t] = sq_reconstruct(codes[t], code_type, mn[g], scale[g]);
+}
+
+__global__ void sq_asym_rows(int ip, const float* __restrict__ q, const uint8_t* __restrict__ codes, uint64_t n,
+                             int dim, int per_dim, int code_type, const float* __restrict__ mn,
+                             const float* __restrict__ scale, float* __restrict__ out) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint8_t* code = codes + i * dim;
+  float sum = 0.0f;
+  for (int c = 0; c < dim; ++c) {
+    const int g = per_dim ? c : 0;
+    const float rec = sq_reconstruct(code[c], code_type, mn[g], scale[g]);
+    if (ip) {
+      sum += q[c] * rec;
+    } else {
+      const float d = q[c] - rec;
+      sum += d * d;
+    }
+  }
+  out[i] = ip ? -sum : sum;
+}
+
+// Copy caller codes (stride dim) into index rows (stride KP, zero padded).
+__global__ void sq8_place_codes(const int8_t* __restrict__ src, int n, int dim, int KP,
+                                const uint32_t* __restrict__ dst, int8_t* __restrict__ C) {
+  const int i = blockIdx.x;
+  if (i >= n) return;
+  int8_t* o = C + (size_t)(dst ? dst[i] : (uint32_t)i) * KP;
+  for (int c = threadIdx.x; c < KP; c += blockDim.x) o[c] = c < dim ? src[(size_t)i * dim + c] : (int8_t)0;
+}
+
+__global__ void sq8_mark(const uint32_t* __restrict__ slots, const uint64_t* __restrict__ sid, int n,
+                         uint8_t* __restrict__ live, uint64_t* __restrict__ ids) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  live[slots[i]] = 1;
+  ids[slots[i]] = sid[i];
+}
+
+// ---------------------------------------------------------------------------
+// Integer MFMA scan. Workgroup = SQ_NW waves; wave w holds QT tiles of 32
+// query codes in VGPRs (the MFMA B operand: lane l gives query l%32, bytes
+// [kb*32 + 16*(l/32), +16) of K block kb); database rows stream through a
+// double-buffered LDS tile of R rows (row stride KP+16 bytes: 16-byte reads
+// of 16 consecutive rows hit distinct banks) and feed the A operand the same
+// way. Output lane l, register v = row 8*(v/4) + 4*(l/32) + v%4 of the tile
+// against query l%32, so every lane filters scores of one query.
+// ---------------------------------------------------------------------------
+template <int KB, bool STAGE1>
+__global__ __launch_bounds__(SQ_NW * 64) void sq8_mfma_scan(
+    const int8_t* __restrict__ Qc, int nq, const int8_t* __restrict__ C, int N, const uint8_t* __restrict__ live,
+    const uint8_t* __restrict__ accept, const uint32_t* __restrict__ rank, int tiles_per_chunk, int sample,
+    const int* __restrict__ thr_in, int* __restrict__ tmax, int* __restrict__ ccount, uint64_t* __restrict__ cand,
+    int cap) {
+  constexpr int KP = KB * 32, SR = KP + 16, R = sq_rows(KB), RT = R / 32, QT = sq_qt(KB);
+  constexpr int PIECES = R * KP / 16, NT = SQ_NW * 64, CPT = (PIECES + NT - 1) / NT;
+  __shared__ __align__(16) int8_t tile[2][R * SR];
+  __shared__ __align__(4) uint8_t vb[2][R];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, r = lane & 31;
+  const int q0 = blockIdx.y * (SQ_NW * QT * 32) + w * (QT * 32);
+  const bool active = q0 < nq;
+
+  i4v qa[QT][KB];
+  int thr[QT], run[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const int q = q0 + qt * 32 + r;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+      qa[qt][kb] = q < nq ? *reinterpret_cast<const i4v*>(Qc + (size_t)q * KP + kb * 32 + h * 16) : i4v{0, 0, 0, 0};
+    thr[qt] = STAGE1 ? INT_MIN : (q < nq ? thr_in[q] : INT_MAX);
+    run[qt] = INT_MIN;
+  }
+
+  const int ntiles = (N + R - 1) / R;
+  const int tb = blockIdx.x * tiles_per_chunk;
+  const int te = min(ntiles, tb + tiles_per_chunk);
+  const int STEP = STAGE1 ? sample : 1;
+
+  i4v pre[CPT];
+  uint8_t pv = 0;
+  auto gload = [&](int t) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + i * NT;
+      i4v v = {0, 0, 0, 0};
+      if (c < PIECES) {
+        const int row = c / (KP / 16), part = c % (KP / 16);
+        const long g = (long)t * R + row;
+        if (g < N) v = *reinterpret_cast<const i4v*>(C + (size_t)g * KP + part * 16);
+      }
+      pre[i] = v;
+    }
+    if (STAGE1 && tid < R) {
+      const long g = (long)t * R + tid;
+      pv = (g < N && live[g] && (accept == nullptr || accept[g])) ? 1 : 0;
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + i * NT;
+      if (c < PIECES) {
+        const int row = c / (KP / 16), part = c % (KP / 16);
+        *reinterpret_cast<i4v*>(&tile[buf][row * SR + part * 16]) = pre[i];
+      }
+    }
+    if (STAGE1 && tid < R) vb[buf][tid] = pv;
+  };
+
+  int t = tb;
+  if (t < te) {
+    gload(t);
+    lstore(0);
+  }
+  __syncthreads();
+  int buf = 0;
+  for (; t < te; t += STEP) {
+    const int tn = t + STEP;
+    if (tn < te) gload(tn);
+    if (active) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        i4v a[KB];
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+          a[kb] = *reinterpret_cast<const i4v*>(&tile[buf][(rt * 32 + r) * SR + kb * 32 + h * 16]);
+        i16v acc[QT];
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[qt][v] = 0;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt)
+            acc[qt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[kb], qa[qt][kb], acc[qt], 0, 0, 0);
+        if constexpr (STAGE1) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const uint32_t vw = *reinterpret_cast<const uint32_t*>(&vb[buf][rt * 32 + 8 * g + 4 * h]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const bool ok = (vw >> (8 * j)) & 1u;
+#pragma unroll
+              for (int qt = 0; qt < QT; ++qt) run[qt] = ok ? max(run[qt], acc[qt][4 * g + j]) : run[qt];
+            }
+          }
+        } else {
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) {
+            const i16v x = acc[qt];
+            int m = max(x[0], max(x[1], x[2]));
+            m = max(m, max(x[3], x[4]));
+            m = max(m, max(x[5], x[6]));
+            m = max(m, max(x[7], x[8]));
+            m = max(m, max(x[9], x[10]));
+            m = max(m, max(x[11], x[12]));
+            m = max(m, max(x[13], x[14]));
+            m = max(m, x[15]);
+            if (__ballot(m >= thr[qt])) {
+              const int q = q0 + qt * 32 + r;
+#pragma unroll
+              for (int v = 0; v < 16; ++v) {
+                if (x[v] >= thr[qt]) {
+                  const int row = t * R + rt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                  if (row < N && q < nq && live[row] && (accept == nullptr || accept[row])) {
+                    const int pos = atomicAdd(&ccount[q], 1);
+                    if (pos < cap)
+                      cand[(size_t)q * cap + pos] = ((uint64_t)ord_key(-(float)x[v]) << 32) | rank[row];
+                  }
+                }
+              }
+            }
+          }
+        }
+      }
+    }
+    if (tn < te) lstore(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+  if constexpr (STAGE1) {
+    if (active) {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        const int q = q0 + qt * 32 + r;
+        if (q < nq) tmax[(size_t)q * (gridDim.x * 2) + blockIdx.x * 2 + h] = run[qt];
+      }
+    }
+  }
+}
+
+// Per query: the k-th largest of its E stage-1 maxima (INT_MIN when E < k).
+__global__ __launch_bounds__(256) void sq8_thresholds(const int* __restrict__ tmax, int E, int k,
+                                                      int* __restrict__ thr) {
+  __shared__ uint64_t keys[2 * SQ_MAX_CHUNKS];
+  const int q = blockIdx.x;
+  int P = 1;
+  while (P < E) P <<= 1;
+  for (int i = threadIdx.x; i < P; i += blockDim.x)
+    keys[i] = i < E ? (uint64_t)((int64_t)INT_MAX - (int64_t)tmax[(size_t)q * E + i]) : KEY_MAX;
+  __syncthreads();
+  block_bitonic_sort(keys, P);
+  if (threadIdx.x == 0) thr[q] = k <= E ? (int)((int64_t)INT_MAX - (int64_t)keys[k - 1]) : INT_MIN;
+}
+
+// Per query: sort the appended candidates and keep the first kk; a query
+// with more than `cap` candidates is listed for the exact scan.
+__global__ __launch_bounds__(256) void sq8_finish(const int* __restrict__ ccount, const uint64_t* __restrict__ cand,
+                                                  int cap, int kk, uint64_t* __restrict__ okeys,
+                                                  uint32_t* __restrict__ ocount, int* __restrict__ flag_list,
+                                                  int* __restrict__ flag_count) {
+  extern __shared__ uint64_t sk[];
+  const int q = blockIdx.x;
+  const int c = ccount[q];
+  if (c > cap) {
+    if (threadIdx.x == 0) flag_list[atomicAdd(flag_count, 1)] = q;
+    return;
+  }
+  int P = 1;
+  while (P < c) P <<= 1;
+  for (int i = threadIdx.x; i < P; i += blockDim.x) sk[i] = i < c ? cand[(size_t)q * cap + i] : KEY_MAX;
+  __syncthreads();
+  block_bitonic_sort(sk, P);
+  const int kout = min(kk, c);
+  for (int i = threadIdx.x; i < kout; i += blockDim.x) okeys[(size_t)q * kk + i] = sk[i];
+  if (threadIdx.x == 0) ocount[q] = (uint32_t)kout;
+}
+
+// Exact scan of listed queries in EXACT_CH-row chunks (v_dot4_i32_i8 over
+// the padded code rows; padding bytes are zero in both operands).
+__global__ __launch_bounds__(256) void sq8_exact_candidates(const int* __restrict__ qlist,
+                                                            const int* __restrict__ qcount, int nchunks,
+                                                            const int8_t* __restrict__ Qc, int KP,
+                                                            const int8_t* __restrict__ C, int N,
+                                                            const uint8_t* __restrict__ live,
+                                                            const uint8_t* __restrict__ accept,
+                                                            const uint32_t* __restrict__ rank, int k,
+                                                            uint64_t* __restrict__ ecand) {
+  __shared__ uint64_t keys[EXACT_CH];
+  const int total = (*qcount) * nchunks;
+  const int kk = min(k, EXACT_CH);
+  const int words = KP / 4;
+  for (int w = blockIdx.x; w < total; w += gridDim.x) {
+    const int f = w / nchunks, c = w % nchunks;
+    const int* qv = reinterpret_cast<const int*>(Qc + (size_t)qlist[f] * KP);
+    const int base = c * EXACT_CH;
+    for (int s = threadIdx.x; s < EXACT_CH; s += blockDim.x) {
+      const int slot = base + s;
+      uint64_t key = KEY_MAX;
+      if (slot < N && live[slot] && (accept == nullptr || accept[slot])) {
+        const int* xv = reinterpret_cast<const int*>(C + (size_t)slot * KP);
+        int acc = 0;
+        for (int j = 0; j < words; ++j) acc = __builtin_amdgcn_sdot4(qv[j], xv[j], acc, false);
+        key = ((uint64_t)ord_key(-(float)acc) << 32) | rank[slot];
+      }
+      keys[s] = key;
+    }
+    __syncthreads();
+    block_bitonic_sort(keys, EXACT_CH);
+    uint64_t* out = ecand + ((size_t)f * nchunks + c) * kk;
+    for (int i = threadIdx.x; i < kk; i += blockDim.x) out[i] = keys[i];
+    __syncthreads();
+  }
+}
+
+// Rescore a query's integer top kk with asymmetric_inner_product
+// (scalar.rs:313-319) and keep the best k by (distance, id).
+__global__ __launch_bounds__(256) void sq8_rescore(const uint64_t* __restrict__ okeys,
+                                                   const uint32_t* __restrict__ ocount, int kk, int k,
+                                                   const float* __restrict__ Qp, int ld, int dim,
+                                                   const int8_t* __restrict__ C, int KP, int per_dim,
+                                                   const float* __restrict__ mn, const float* __restrict__ scale,
+                                                   const uint32_t* __restrict__ rank_slot,
+                                                   const uint64_t* __restrict__ ids, uint64_t* __restrict__ out_ids,
+                                                   float* __restrict__ out_d, uint32_t* __restrict__ out_count) {
+  extern __shared__ uint64_t sk[];
+  const int q = blockIdx.x;
+  const int c = (int)ocount[q];
+  int P = 1;
+  while (P < c) P <<= 1;
+  const float* qv = Qp + (size_t)q * ld;
+  for (int i = threadIdx.x; i < P; i += blockDim.x) {
+    uint64_t key = KEY_MAX;
+    if (i < c) {
+      const uint32_t rk = (uint32_t)okeys[(size_t)q * kk + i];
+      const uint8_t* code = reinterpret_cast<const uint8_t*>(C + (size_t)rank_slot[rk] * KP);
+      float sum = 0.0f;
+      for (int j = 0; j < dim; ++j) {
+        const int g = per_dim ? j : 0;
+        sum += qv[j] * sq_reconstruct(code[j], 1, mn[g], scale[g]);
+      }
+      key = ((uint64_t)ord_key(-sum) << 32) | rk;
+    }
+    sk[i] = key;
+  }
+  __syncthreads();
+  block_bitonic_sort(sk, P);
+  const int kout = min(k, c);
+  for (int i = threadIdx.x; i < kout; i += blockDim.x) {
+    const uint64_t key = sk[i];
+    out_ids[(size_t)q * k + i] = ids[rank_slot[(uint32_t)key]];
+    out_d[(size_t)q * k + i] = key_float((uint32_t)(key >> 32));
+  }
+  if (threadIdx.x == 0) out_count[q] = (uint32_t)kout;
+}
+
+__global__ void sq8_emit(const uint64_t* __restrict__ okeys, const uint32_t* __restrict__ ocount, int kk, int k,
+                         const uint32_t* __restrict__ rank_slot, const uint64_t* __restrict__ ids,
+                         uint64_t* __restrict__ out_ids, float* __restrict__ out_d, uint32_t* __restrict__ out_count) {
+  const int q = blockIdx.x;
+  const int c = min((int)ocount[q], k);
+  for (int i = threadIdx.x; i < c; i += blockDim.x) {
+    const uint64_t key = okeys[(size_t)q * kk + i];
+    out_ids[(size_t)q * k + i] = ids[rank_slot[(uint32_t)key]];
+    out_d[(size_t)q * k + i] = key_float((uint32_t)(key >> 32));
+  }
+  if (threadIdx.x == 0) out_count[q] = (uint32_t)c;
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+struct Ranges {
+  std::vector<float> mn, scale, inv;
+};
+
+// Range training accumulator over device-resident rows (stride ld); rows may
+// arrive in several batches (row0 = index of the batch's first row).
+struct RangeTrainer {
+  int groups;
+  DevBuf<uint32_t> omin, omax;
+  DevBuf<unsigned long long> bad;
+  RangeTrainer(int g, hipStream_t s) : groups(g), omin(g), omax(g), bad(1) {
+    PXG_HIP(hipMemsetAsync(omin.p, 0xFF, g * 4, s));
+    PXG_HIP(hipMemsetAsync(omax.p, 0, g * 4, s));
+    PXG_HIP(hipMemsetAsync(bad.p, 0xFF, 8, s));
+  }
+  void add(const float* d_x, int ld, uint64_t n, uint32_t dim, int per_dim, uint64_t row0, hipStream_t s) {
+    if (!n) return;
+    const unsigned grid = (unsigned)std::min<uint64_t>(1024, std::max<uint64_t>(1, n / 16));
+    hipLaunchKernelGGL(sq_minmax, dim3(grid), dim3(256), 0, s, d_x, ld, n, (int)dim, per_dim, row0, omin.p, omax.p,
+                       bad.p);
+    PXG_HIP(hipGetLastError());
+  }
+  // first non-finite (row << 32 | component), or ~0
+  unsigned long long first_bad(hipStream_t s) {
+    unsigned long long hb = 0;
+    PXG_HIP(hipMemcpyAsync(&hb, bad.p, 8, hipMemcpyDeviceToHost, s));
+    PXG_HIP(hipStreamSynchronize(s));
+    return hb;
+  }
+  // scale = (max - min) / 255, inverse = scale > 0 ? 1 / scale : 0 (scalar.rs:181-188)
+  Ranges finish(hipStream_t s) {
+    std::vector<uint32_t> hmn(groups), hmx(groups);
+    PXG_HIP(hipMemcpyAsync(hmn.data(), omin.p, groups * 4, hipMemcpyDeviceToHost, s));
+    PXG_HIP(hipMemcpyAsync(hmx.data(), omax.p, groups * 4, hipMemcpyDeviceToHost, s));
+    PXG_HIP(hipStreamSynchronize(s));
+    Ranges rg;
+    rg.mn.resize(groups);
+    rg.scale.resize(groups);
+    rg.inv.resize(groups);
+    for (int g = 0; g < groups; ++g) {
+      const float lo = ord2f(hmn[g]), hi = ord2f(hmx[g]);
+      rg.mn[g] = lo;
+      rg.scale[g] = (hi - lo) / 255.0f;
+      rg.inv[g] = rg.scale[g] > 0.0f ? 1.0f / rg.scale[g] : 0.0f;
+    }
+    return rg;
+  }
+};
+
+static void check_training_len(uint64_t n) {
+  if (n == 0) config_error("training", 0, "must be a non-empty multiple of the space dimension");
+}
+
+// the first non-finite value in row-major order (scalar.rs:162-170)
+static void check_finite_host(const float* x, uint64_t n, uint32_t dim) {
+  for (uint64_t i = 0; i < n * dim; ++i)
+    if (!std::isfinite(x[i]))
+      raise(PXG_ERR_NON_FINITE,
+            "vector component " + std::to_string(i % dim) + " is not finite (" + std::to_string(x[i]) + ")", i % dim,
+            i / dim, x[i]);
+}
+
+// ScalarQuantizer::train over a host sample, streamed through the device.
+static Ranges train_ranges_host(const float* x, uint64_t n, uint32_t dim, int per_dim, hipStream_t s) {
+  check_training_len(n);
+  check_finite_host(x, n, dim);
+  RangeTrainer tr(per_dim ? (int)dim : 1, s);
+  const uint64_t rows_per = std::max<uint64_t>(1, (64u << 20) / ((uint64_t)dim * 4));
+  DevBuf<float> st(std::min<uint64_t>(rows_per, n) * dim);
+  for (uint64_t a = 0; a < n; a += rows_per) {
+    const uint64_t m = std::min<uint64_t>(rows_per, n - a);
+    PXG_HIP(hipMemcpyAsync(st.p, x + a * dim, m * dim * 4, hipMemcpyHostToDevice, s));
+    tr.add(st.p, (int)dim, m, dim, per_dim, a, s);
+    PXG_HIP(hipStreamSynchronize(s));
+  }
+  return tr.finish(s);
+}
+
+struct Sq8Index {
+  uint32_t dim = 0, ld = 0, KP = 0;
+  int metric = PXG_INNER_PRODUCT;
+  int per_dim = 1;
+  int mode = 0;  // 0 auto, 1 MFMA candidates, 2 exact scan
+  bool trained = false;
+  Ranges rg;
+  DevBuf<float> d_mn, d_scale, d_inv;
+
+  std::vector<uint64_t> ids;
+  std::vector<uint8_t> live;
+  std::unordered_map<uint64_t, uint32_t> by_id;
+  SlotAllocator slots;
+
+  size_t cap = 0;
+  DevBuf<int8_t> codes;  // cap * KP, I8 codes, zero padded
+  DevBuf<uint8_t> d_live;
+  DevBuf<uint64_t> d_ids;
+  DevBuf<uint32_t> d_rank, d_rank_slot;
+  bool rank_dirty = true;
+  std::mutex rank_mu;
+
+  mutable std::shared_mutex mu;
+  CtxPool pool;
+  hipStream_t stream = nullptr;
+
+  ~Sq8Index() {
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+
+  int groups() const { return per_dim ? (int)dim : 1; }
+
+  void set_ranges(const Ranges& r) {
+    rg = r;
+    const int g = groups();
+    d_mn.reserve(g);
+    d_scale.reserve(g);
+    d_inv.reserve(g);
+    PXG_HIP(hipMemcpyAsync(d_mn.p, rg.mn.data(), g * 4, hipMemcpyHostToDevice, stream));
+    PXG_HIP(hipMemcpyAsync(d_scale.p, rg.scale.data(), g * 4, hipMemcpyHostToDevice, stream));
+    PXG_HIP(hipMemcpyAsync(d_inv.p, rg.inv.data(), g * 4, hipMemcpyHostToDevice, stream));
+    PXG_HIP(hipStreamSynchronize(stream));
+    trained = true;
+  }
+
+  // Fit the ranges to the prepared (space.rs:130-138) training vectors,
+  // from host or device memory, in batches.
+  void train(const float* x, bool on_device, uint64_t n) {
+    check_training_len(n);
+    if (!on_device) check_finite_host(x, n, dim);
+    RangeTrainer tr(groups(), stream);
+    const size_t chunk = std::min<size_t>(std::max<size_t>(1, (128u << 20) / ((size_t)ld * 4)), n);
+    DevBuf<float> st(chunk * ld), sb(chunk), sn(chunk), raw(on_device ? 0 : chunk * dim);
+    DevBuf<unsigned long long> bad(1);
+    for (size_t a = 0; a < n; a += chunk) {
+      const size_t m = std::min<size_t>(chunk, n - a);
+      const float* src = x + a * dim;
+      if (!on_device) {
+        PXG_HIP(hipMemcpyAsync(raw.p, src, m * dim * 4, hipMemcpyHostToDevice, stream));
+        src = raw.p;
+      }
+      PXG_HIP(hipMemsetAsync(bad.p, 0xFF, 8, stream));
+      hipLaunchKernelGGL(flat_prep_queries, dim3((unsigned)m), dim3(64), 0, stream, src, (int)dim, (int)ld, metric, 1,
+                         st.p, sb.p, sn.p, bad.p);
+      PXG_HIP(hipGetLastError());
+      unsigned long long bv = 0;
+      PXG_HIP(hipMemcpyAsync(&bv, bad.p, 8, hipMemcpyDeviceToHost, stream));
+      PXG_HIP(hipStreamSynchronize(stream));
+      if (bv != ~0ull) {
+        const uint64_t row = a + (bv >> 32), comp = (uint32_t)bv;
+        float v = NAN;
+        if (on_device) PXG_HIP(hipMemcpy(&v, x + row * dim + comp, 4, hipMemcpyDeviceToHost));
+        raise(PXG_ERR_NON_FINITE, "vector component " + std::to_string(comp) + " is not finite (training vector " +
+                                      std::to_string(row) + ")",
+              comp, row, v);
+      }
+      tr.add(st.p, (int)ld, m, dim, per_dim, a, stream);
+      PXG_HIP(hipStreamSynchronize(stream));
+    }
+    set_ranges(tr.finish(stream));
+  }
+
+  void require_trained() const {
+    if (!trained)
+      config_error("quantizer", 0, "the SQ8 index must be trained (or given ranges) before vectors are added");
+  }
+
+  void ensure_capacity(size_t need, size_t keep) {
+    if (need <= cap) return;
+    const size_t nc = std::max<size_t>(need, std::max<size_t>(cap * 2, 1024));
+    const size_t hw = std::min(keep, cap);
+    codes.grow(nc * KP, hw * KP, stream);
+    d_live.grow(nc, hw, stream);
+    d_ids.grow(nc, hw, stream);
+    d_rank.grow(nc, hw, stream);
+    PXG_HIP(hipMemsetAsync(d_live.p + hw, 0, nc - hw, stream));
+    PXG_HIP(hipMemsetAsync(codes.p + hw * KP, 0, (nc - hw) * KP, stream));
+    PXG_HIP(hipStreamSynchronize(stream));
+    cap = nc;
+  }
+
+  void rebuild_ranks(hipStream_t s) {
+    std::lock_guard<std::mutex> lk(rank_mu);
+    if (!rank_dirty) return;
+    std::vector<std::pair<uint64_t, uint32_t>> v;
+    v.reserve(by_id.size());
+    for (size_t s2 = 0; s2 < ids.size(); ++s2)
+      if (live[s2]) v.emplace_back(ids[s2], (uint32_t)s2);
+    std::sort(v.begin(), v.end());
+    std::vector<uint32_t> rs(v.size()), rk(std::max<size_t>(ids.size(), 1), 0);
+    for (size_t r = 0; r < v.size(); ++r) {
+      rs[r] = v[r].second;
+      rk[v[r].second] = (uint32_t)r;
+    }
+    d_rank_slot.reserve(std::max<size_t>(rs.size(), 1));
+    if (!rs.empty()) PXG_HIP(hipMemcpyAsync(d_rank_slot.p, rs.data(), rs.size() * 4, hipMemcpyHostToDevice, s));
+    if (!ids.empty()) PXG_HIP(hipMemcpyAsync(d_rank.p, rk.data(), ids.size() * 4, hipMemcpyHostToDevice, s));
+    PXG_HIP(hipStreamSynchronize(s));
+    rank_dirty = false;
+  }
+
+  void check_new_ids(const uint64_t* in_ids, uint64_t n) {
+    std::unordered_map<uint64_t, int> seen;
+    for (uint64_t i = 0; i < n; ++i)
+      if (by_id.count(in_ids[i]) || !seen.emplace(in_ids[i], 1).second)
+        raise(PXG_ERR_DUPLICATE_ID, "duplicate vector id " + std::to_string(in_ids[i]), in_ids[i]);
+    if (by_id.size() + n > (size_t)UINT32_MAX - 1)
+      raise(PXG_ERR_CAPACITY, "capacity exceeded: slot allocator limit is 4294967295", UINT32_MAX);
+  }
+
+  std::vector<uint32_t> claim_slots(const uint64_t* in_ids, uint64_t n, uint32_t* out_slots) {
+    std::vector<uint32_t> sl(n);
+    const size_t old_hw = slots.high_water();
+    for (uint64_t i = 0; i < n; ++i) sl[i] = slots.allocate();
+    const size_t hw = slots.high_water();
+    ensure_capacity(hw, old_hw);
+    if (ids.size() < hw) {
+      ids.resize(hw, 0);
+      live.resize(hw, 0);
+    }
+    for (uint64_t i = 0; i < n; ++i) {
+      ids[sl[i]] = in_ids[i];
+      live[sl[i]] = 1;
+      by_id[in_ids[i]] = sl[i];
+      if (out_slots) out_slots[i] = sl[i];
+    }
+    rank_dirty = true;
+    return sl;
+  }
+
+  // prepare (space.rs:130-138) + validate every row of a device batch; raises
+  // NonFinite before any state changes.
+  void validate_device(const float* d_vecs, uint64_t n, size_t chunk, DevBuf<float>& st, DevBuf<float>& sb,
+                       DevBuf<float>& sn, DevBuf<unsigned long long>& bad) {
+    for (size_t a = 0; a < n; a += chunk) {
+      const size_t m = std::min<size_t>(chunk, n - a);
+      PXG_HIP(hipMemsetAsync(bad.p, 0xFF, 8, stream));
+      hipLaunchKernelGGL(flat_prep_queries, dim3((unsigned)m), dim3(64), 0, stream, d_vecs + a * dim, (int)dim,
+                         (int)ld, metric, 1, st.p, sb.p, sn.p, bad.p);
+      PXG_HIP(hipGetLastError());
+      unsigned long long bv = 0;
+      PXG_HIP(hipMemcpyAsync(&bv, bad.p, 8, hipMemcpyDeviceToHost, stream));
+      PXG_HIP(hipStreamSynchronize(stream));
+      if (bv != ~0ull) {
+        const uint64_t row = a + (bv >> 32), comp = (uint32_t)bv;
+        raise(PXG_ERR_NON_FINITE, "vector component " + std::to_string(comp) + " is not finite (vector " +
+                                      std::to_string(row) + ")",
+              comp, row, NAN);
+      }
+    }
+  }
+
+  void insert_device(const uint64_t* in_ids, const float* d_vecs, uint64_t n, uint32_t* out_slots) {
+    require_trained();
+    check_new_ids(in_ids, n);
+    const size_t chunk = std::min<size_t>(std::max<size_t>(1, (256u << 20) / ((size_t)ld * 4)), n);
+    DevBuf<float> st(chunk * ld), sb(chunk), sn(chunk);
+    DevBuf<unsigned long long> bad(1);
+    validate_device(d_vecs, n, chunk, st, sb, sn, bad);
+    std::vector<uint32_t> sl = claim_slots(in_ids, n, out_slots);
+    DevBuf<uint32_t> st_slots(chunk);
+    DevBuf<uint64_t> st_ids(chunk);
+    for (size_t a = 0; a < n; a += chunk) {
+      const size_t m = std::min<size_t>(chunk, n - a);
+      hipLaunchKernelGGL(flat_prep_queries, dim3((unsigned)m), dim3(64), 0, stream, d_vecs + a * dim, (int)dim,
+                         (int)ld, metric, 1, st.p, sb.p, sn.p, bad.p);
+      PXG_HIP(hipMemcpyAsync(st_slots.p, sl.data() + a, m * 4, hipMemcpyHostToDevice, stream));
+      PXG_HIP(hipMemcpyAsync(st_ids.p, in_ids + a, m * 8, hipMemcpyHostToDevice, stream));
+      hipLaunchKernelGGL(sq_encode_rows, dim3((unsigned)m), dim3(64), 0, stream, st.p, (int)ld, (int)m, (int)dim,
+                         per_dim, 1, d_mn.p, d_inv.p, st_slots.p, (uint8_t*)codes.p, (int)KP);
+      hipLaunchKernelGGL(sq8_mark, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, stream, st_slots.p, st_ids.p,
+                         (int)m, d_live.p, d_ids.p);
+      PXG_HIP(hipGetLastError());
+      PXG_HIP(hipStreamSynchronize(stream));
+    }
+  }
+
+  void insert_host(const uint64_t* in_ids, const float* vecs, uint64_t n, uint32_t* out_slots) {
+    require_trained();
+    // validate on the host first: all-or-nothing (space.rs:104-121)
+    for (uint64_t i = 0; i < n; ++i)
+      for (uint32_t c = 0; c < dim; ++c)
+        if (!std::isfinite(vecs[i * dim + c]))
+          raise(PXG_ERR_NON_FINITE,
+                "vector component " + std::to_string(c) + " is not finite (" + std::to_string(vecs[i * dim + c]) + ")",
+                c, i, vecs[i * dim + c]);
+    check_new_ids(in_ids, n);
+    const size_t chunk = std::min<size_t>(std::max<size_t>(1, (64u << 20) / ((size_t)dim * 4)), n);
+    DevBuf<float> raw(chunk * dim);
+    // the device path re-validates (finite rows pass) and prepares
+    for (size_t a = 0; a < n; a += chunk) {
+      const size_t m = std::min<size_t>(chunk, n - a);
+      PXG_HIP(hipMemcpyAsync(raw.p, vecs + a * dim, m * dim * 4, hipMemcpyHostToDevice, stream));
+      PXG_HIP(hipStreamSynchronize(stream));
+      std::vector<uint32_t> part(m);
+      insert_device(in_ids + a, raw.p, m, part.data());
+      if (out_slots) std::copy(part.begin(), part.end(), out_slots + a);
+    }
+  }
+
+  void add_codes(const uint64_t* in_ids, const int8_t* h_codes, uint64_t n, uint32_t* out_slots) {
+    check_new_ids(in_ids, n);
+    std::vector<uint32_t> sl = claim_slots(in_ids, n, out_slots);
+    const size_t chunk = std::min<size_t>(std::max<size_t>(1, (64u << 20) / (size_t)dim), n);
+    DevBuf<int8_t> st(chunk * dim);
+    DevBuf<uint32_t> st_slots(chunk);
+    DevBuf<uint64_t> st_ids(chunk);
+    for (size_t a = 0; a < n; a += chunk) {
+      const size_t m = std::min<size_t>(chunk, n - a);
+      PXG_HIP(hipMemcpyAsync(st.p, h_codes + a * dim, m * dim, hipMemcpyHostToDevice, stream));
+      PXG_HIP(hipMemcpyAsync(st_slots.p, sl.data() + a, m * 4, hipMemcpyHostToDevice, stream));
+      PXG_HIP(hipMemcpyAsync(st_ids.p, in_ids + a, m * 8, hipMemcpyHostToDevice, stream));
+      hipLaunchKernelGGL(sq8_place_codes, dim3((unsigned)m), dim3(64), 0, stream, st.p, (int)m, (int)dim, (int)KP,
+                         st_slots.p, codes.p);
+      hipLaunchKernelGGL(sq8_mark, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, stream, st_slots.p, st_ids.p,
+                         (int)m, d_live.p, d_ids.p);
+      PXG_HIP(hipGetLastError());
+      PXG_HIP(hipStreamSynchronize(stream));
+    }
+  }
+
+  void remove(uint64_t id) {
+    auto it = by_id.find(id);
+    if (it == by_id.end()) raise(PXG_ERR_UNKNOWN_ID, "unknown vector id " + std::to_string(id), id);
+    const uint32_t s = it->second;
+    by_id.erase(it);
+    live[s] = 0;
+    ids[s] = 0;
+    slots.release(s);
+    PXG_HIP(hipMemsetAsync(d_live.p + s, 0, 1, stream));
+    PXG_HIP(hipStreamSynchronize(stream));
+    rank_dirty = true;
+  }
+
+  // Queries: f32 (prepared + encoded here; rescoring possible) or I8 codes.
+  void search_device(const float* d_raw, const int8_t* d_qcodes, uint64_t nq, uint64_t k, uint64_t rescore,
+                     const uint8_t* d_accept, uint64_t* d_oid, float* d_od, uint32_t* d_oc, Ctx* ctx, hipStream_t s,
+                     uint64_t* fallbacks) {
+    check_k(k);
+    *fallbacks = 0;
+    if (nq == 0) return;
+    if (!d_raw && rescore) config_error("rescore", rescore, "rescoring needs the f32 queries");
+    if (d_raw) require_trained();
+    if (k == 0 || by_id.empty()) {
+      PXG_HIP(hipMemsetAsync(d_oc, 0, nq * 4, s));
+      PXG_HIP(hipStreamSynchronize(s));
+      return;
+    }
+    const uint64_t kk64 = std::max<uint64_t>(k, rescore);
+    if (kk64 > 1024) config_error("k", kk64, "the GPU SQ8 search supports max(k, rescore) up to 1024 per query");
+    const int kk = (int)kk64;
+    rebuild_ranks(s);
+    Timer tm(s);
+    tm.mark(0);
+    int8_t* Qc = (int8_t*)ctx->get(1, nq * KP);
+    float* Qp = nullptr;
+    unsigned long long* bad = (unsigned long long*)ctx->get(4, 64);
+    int* flag_count = (int*)(bad + 1);
+    if (d_raw) {
+      Qp = (float*)ctx->get(2, nq * ld * 4);
+      float* qb = (float*)ctx->get(3, nq * 4);
+      float* qn = (float*)ctx->get(5, nq * 4);
+      PXG_HIP(hipMemsetAsync(bad, 0xFF, 8, s));
+      hipLaunchKernelGGL(flat_prep_queries, dim3((unsigned)nq), dim3(64), 0, s, d_raw, (int)dim, (int)ld, metric, 1,
+                         Qp, qb, qn, bad);
+      hipLaunchKernelGGL(sq_encode_rows, dim3((unsigned)nq), dim3(64), 0, s, Qp, (int)ld, (int)nq, (int)dim, per_dim,
+                         1, d_mn.p, d_inv.p, (const uint32_t*)nullptr, (uint8_t*)Qc, (int)KP);
+      PXG_HIP(hipGetLastError());
+      unsigned long long bv = 0;
+      PXG_HIP(hipMemcpyAsync(&bv, bad, 8, hipMemcpyDeviceToHost, s));
+      PXG_HIP(hipStreamSynchronize(s));
+      if (bv != ~0ull) {
+        const uint64_t row = bv >> 32, comp = (uint32_t)bv;
+        raise(PXG_ERR_NON_FINITE, "vector component " + std::to_string(comp) + " is not finite (query " +
+                                      std::to_string(row) + ")",
+              comp, row, NAN);
+      }
+    } else {
+      hipLaunchKernelGGL(sq8_place_codes, dim3((unsigned)nq), dim3(64), 0, s, d_qcodes, (int)nq, (int)dim, (int)KP,
+                         (const uint32_t*)nullptr, Qc);
+      PXG_HIP(hipGetLastError());
+    }
+    const int N = (int)slots.high_water();
+    const int KB = (int)(KP / 32);
+    uint64_t* okeys = (uint64_t*)ctx->get(6, nq * kk * 8);
+    uint32_t* ocount = (uint32_t*)ctx->get(7, nq * 4);
+    int* flag_list = (int*)ctx->get(8, nq * 4);
+    PXG_HIP(hipMemsetAsync(flag_count, 0, 4, s));
+    const bool mfma = mode != 2 && KB <= SQ_MAX_KB && (mode == 1 || N >= 4096);
+    int nflag = 0;
+    if (mfma) {
+      const int R = sq_rows(KB), QT = sq_qt(KB);
+      // Chunks: about 512 (two per CU), and at least 2 * kk so that every
+      // query gets >= 4 * kk stage-1 maxima when the index has the tiles.
+      // Stage 1 samples every `sample`-th tile (a divisor of the chunk
+      // length, so every chunk contributes).
+      const int ntiles = (N + R - 1) / R;
+      const int target = std::min(std::min(SQ_MAX_CHUNKS, ntiles), std::max(512, 2 * kk));
+      int tpc = (ntiles + target - 1) / target;
+      int sample = SQ_SAMPLE;
+      if (tpc >= SQ_SAMPLE) {
+        tpc = (tpc + SQ_SAMPLE - 1) / SQ_SAMPLE * SQ_SAMPLE;
+      } else {
+        sample = 1;
+        while (sample * 2 <= tpc) sample *= 2;
+        tpc = sample;
+      }
+      const int nchunks = (ntiles + tpc - 1) / tpc;
+      if (nchunks > SQ_MAX_CHUNKS) internal_error("sq8", "chunk count above the stage-1 limit");
+      const int qgroups = (int)((nq + SQ_NW * QT * 32 - 1) / (SQ_NW * QT * 32));
+      const int E = nchunks * 2;
+      const int cap_c = kk <= 32 ? 1024 : 4096;
+      int* tmax = (int*)ctx->get(9, nq * E * 4);
+      int* thr = (int*)ctx->get(10, nq * 4);
+      int* ccount = (int*)ctx->get(11, nq * 4);
+      uint64_t* cand = (uint64_t*)ctx->get(12, nq * cap_c * 8);
+      const dim3 grid((unsigned)nchunks, (unsigned)qgroups);
+      tm.mark(1);
+#define PXG_SQ_SCAN(KBV, ST)                                                                                        \
+  hipLaunchKernelGGL((sq8_mfma_scan<KBV, ST>), grid, dim3(SQ_NW * 64), 0, s, (const int8_t*)Qc, (int)nq,           \
+                     (const int8_t*)codes.p, N, d_live.p, d_accept, d_rank.p, tpc, sample, (const int*)thr, tmax,  \
+                     ccount, cand, cap_c)
+#define PXG_SQ_SWITCH(ST)                  \
+  switch (KB) {                            \
+    case 1: PXG_SQ_SCAN(1, ST); break;     \
+    case 2: PXG_SQ_SCAN(2, ST); break;     \
+    case 3: PXG_SQ_SCAN(3, ST); break;     \
+    case 4: PXG_SQ_SCAN(4, ST); break;     \
+    case 5: PXG_SQ_SCAN(5, ST); break;     \
+    case 6: PXG_SQ_SCAN(6, ST); break;     \
+    case 7: PXG_SQ_SCAN(7, ST); break;     \
+    default: PXG_SQ_SCAN(8, ST); break;    \
+  }
+      PXG_SQ_SWITCH(true)
+      PXG_HIP(hipGetLastError());
+      hipLaunchKernelGGL(sq8_thresholds, dim3((unsigned)nq), dim3(256), 0, s, (const int*)tmax, E, kk, thr);
+      PXG_HIP(hipMemsetAsync(ccount, 0, nq * 4, s));
+      PXG_SQ_SWITCH(false)
+#undef PXG_SQ_SWITCH
+#undef PXG_SQ_SCAN
+      PXG_HIP(hipGetLastError());
+      tm.mark(2);
+      hipLaunchKernelGGL(sq8_finish, dim3((unsigned)nq), dim3(256), (size_t)cap_c * 8, s, (const int*)ccount,
+                         (const uint64_t*)cand, cap_c, kk, okeys, ocount, flag_list, flag_count);
+      PXG_HIP(hipGetLastError());
+      PXG_HIP(hipMemcpyAsync(&nflag, flag_count, 4, hipMemcpyDeviceToHost, s));
+      PXG_HIP(hipStreamSynchronize(s));
+      *fallbacks = (uint64_t)nflag;
+    } else {
+      tm.mark(1);
+      hipLaunchKernelGGL(iota_kernel, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s, flag_list, (int)nq,
+                         flag_count);
+      PXG_HIP(hipGetLastError());
+      nflag = (int)nq;
+    }
+    if (nflag > 0) {
+      if (mfma) tm.mark(3);
+      const int nchunks = (N + EXACT_CH - 1) / EXACT_CH;
+      const int kke = std::min(kk, EXACT_CH);
+      uint64_t* ecand = (uint64_t*)ctx->get(13, (size_t)nflag * nchunks * kke * 8);
+      hipLaunchKernelGGL(sq8_exact_candidates, dim3((unsigned)std::min<int64_t>((int64_t)nflag * nchunks, 4096)),
+                         dim3(256), 0, s, (const int*)flag_list, (const int*)flag_count, nchunks, (const int8_t*)Qc,
+                         (int)KP, (const int8_t*)codes.p, N, d_live.p, d_accept, d_rank.p, kk, ecand);
+      PXG_HIP(hipGetLastError());
+      if (!mfma) tm.mark(2);
+      hipLaunchKernelGGL(flat_merge_exact, dim3((unsigned)nflag), dim3(256), 0, s, (const int*)flag_list,
+                         (const int*)flag_count, (const uint64_t*)ecand, nchunks, kk, d_rank_slot.p, d_ids.p,
+                         (uint64_t*)nullptr, (float*)nullptr, ocount, okeys);
+      PXG_HIP(hipGetLastError());
+    }
+    if (rescore) {
+      int P = 1;
+      while (P < kk) P <<= 1;
+      hipLaunchKernelGGL(sq8_rescore, dim3((unsigned)nq), dim3(256), (size_t)P * 8, s, (const uint64_t*)okeys,
+                         (const uint32_t*)ocount, kk, (int)k, (const float*)Qp, (int)ld, (int)dim,
+                         (const int8_t*)codes.p, (int)KP, per_dim, d_mn.p, d_scale.p, d_rank_slot.p, d_ids.p, d_oid,
+                         d_od, d_oc);
+    } else {
+      hipLaunchKernelGGL(sq8_emit, dim3((unsigned)nq), dim3(64), 0, s, (const uint64_t*)okeys,
+                         (const uint32_t*)ocount, kk, (int)k, d_rank_slot.p, d_ids.p, d_oid, d_od, d_oc);
+    }
+    PXG_HIP(hipGetLastError());
+    PXG_HIP(hipStreamSynchronize(s));
+    tm.finish();
+  }
+};
+
+thread_local uint64_t g_sq8_fallbacks = 0;
+
+}  // namespace pxg
+
+using pxg::Sq8Index;
+
+struct pxg_sq8 {
+  Sq8Index impl;
+};
+
+namespace {
+
+void check_groups_args(uint32_t dim) {
+  if (dim < 1) pxg::config_error("dim", dim, "must be at least 1; a 0-dimensional space makes all distances equal");
+  if (dim > pxg::SQ_MAX_DIM) pxg::config_error("dim", dim, "the SQ8 path supports dimensions up to 65536");
+}
+
+}  // namespace
+
+extern "C" {
+
+int pxg_sq_train(const float* training, uint64_t n, uint32_t dim, int per_dim, float* min, float* scale,
+                 float* inverse_scale) {
+  return pxg::guard([&] {
+    check_groups_args(dim);
+    pxg::check_training_len(n);
+    pxg::check_finite_host(training, n, dim);
+    hipStream_t s = nullptr;
+    PXG_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    struct Del {
+      hipStream_t s;
+      ~Del() { (void)hipStreamDestroy(s); }
+    } del{s};
+    pxg::Ranges r = pxg::train_ranges_host(training, n, dim, per_dim ? 1 : 0, s);
+    std::copy(r.mn.begin(), r.mn.end(), min);
+    std::copy(r.scale.begin(), r.scale.end(), scale);
+    std::copy(r.inv.begin(), r.inv.end(), inverse_scale);
+  });
+}
+
+int pxg_sq_encode(const float* vectors, uint64_t n, uint32_t dim, int per_dim, int code_type, const float* min,
+                  const float* inverse_scale, uint8_t* out) {
+  return pxg::guard([&] {
+    check_groups_args(dim);
+    if (code_type != 0 && code_type != 1) pxg::config_error("code_type", (uint64_t)code_type, "0 = U8, 1 = I8");
+    if (n == 0) return;
+    for (uint64_t i = 0; i < n; ++i)
+      for (uint32_t c = 0; c < dim; ++c)
+        if (!std::isfinite(vectors[i * dim + c]))
+          pxg::raise(PXG_ERR_NON_FINITE,
+                     "vector component " + std::to_string(c) + " is not finite (" +
+                         std::to_string(vectors[i * dim + c]) + ")",
+                     c, i, vectors[i * dim + c]);
+    const int g = per_dim ? (int)dim : 1;
+    pxg::DevBuf<float> dv(n * dim), dmn(g), dinv(g);
+    pxg::DevBuf<uint8_t> dout(n * dim);
+    PXG_HIP(hipMemcpy(dv.p, vectors, n * dim * 4, hipMemcpyHostToDevice));
+    PXG_HIP(hipMemcpy(dmn.p, min, g * 4, hipMemcpyHostToDevice));
+    PXG_HIP(hipMemcpy(dinv.p, inverse_scale, g * 4, hipMemcpyHostToDevice));
+    hipLaunchKernelGGL(pxg::sq_encode_rows, dim3((unsigned)n), dim3(64), 0, 0, dv.p, (int)dim, (int)n, (int)dim,
+                       per_dim ? 1 : 0, code_type, dmn.p, dinv.p, (const uint32_t*)nullptr, dout.p, (int)dim);
+    PXG_HIP(hipGetLastError());
+    PXG_HIP(hipMemcpy(out, dout.p, n * dim, hipMemcpyDeviceToHost));
+  });
+}
+
+int pxg_sq_decode(const uint8_t* codes, uint64_t n, uint32_t dim, int per_dim, int code_type, const float* min,
+                  const float* scale, float* out) {
+  return pxg::guard([&] {
+    check_groups_args(dim);
+    if (code_type != 0 && code_type != 1) pxg::config_error("code_type", (uint64_t)code_type, "0 = U8, 1 = I8");
+    if (n == 0) return;
+    const int g = per_dim ? (int)dim : 1;
+    pxg::DevBuf<uint8_t> dc(n * dim);
+    pxg::DevBuf<float> dmn(g), dsc(g), dout(n * dim);
+    PXG_HIP(hipMemcpy(dc.p, codes, n * dim, hipMemcpyHostToDevice));
+    PXG_HIP(hipMemcpy(dmn.p, min, g * 4, hipMemcpyHostToDevice));
+    PXG_HIP(hipMemcpy(dsc.p, scale, g * 4, hipMemcpyHostToDevice));
+    const uint64_t tot = n * dim;
+    hipLaunchKernelGGL(pxg::sq_decode_rows, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, 0, dc.p, n, (int)dim,
+                       per_dim ? 1 : 0, code_type, dmn.p, dsc.p, dout.p);
+    PXG_HIP(hipGetLastError());
+    PXG_HIP(hipMemcpy(out, dout.p, tot * 4, hipMemcpyDeviceToHost));
+  });
+}
+
+int pxg_sq_asymmetric(int inner_product, const float* query, const uint8_t* codes, uint64_t n, uint32_t dim,
+                      int per_dim, int code_type, const float* min, const float* scale, float* out) {
+  return pxg::guard([&] {
+    check_groups_args(dim);
+    if (code_type != 0 && code_type != 1) pxg::config_error("code_type", (uint64_t)code_type, "0 = U8, 1 = I8");
+    if (n == 0) return;
+    const int g = per_dim ? (int)dim : 1;
+    pxg::DevBuf<uint8_t> dc(n * dim);
+    pxg::DevBuf<float> dq(dim), dmn(g), dsc(g), dout(n);
+    PXG_HIP(hipMemcpy(dc.p, codes, n * dim, hipMemcpyHostToDevice));
+    PXG_HIP(hipMemcpy(dq.p, query, dim * 4, hipMemcpyHostToDevice));
+    PXG_HIP(hipMemcpy(dmn.p, min, g * 4, hipMemcpyHostToDevice));
+    PXG_HIP(hipMemcpy(dsc.p, scale, g * 4, hipMemcpyHostToDevice));
+    hipLaunchKernelGGL(pxg::sq_asym_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, 0, inner_product ? 1 : 0,
+                       dq.p, dc.p, n, (int)dim, per_dim ? 1 : 0, code_type, dmn.p, dsc.p, dout.p);
+    PXG_HIP(hipGetLastError());
+    PXG_HIP(hipMemcpy(out, dout.p, n * 4, hipMemcpyDeviceToHost));
+  });
+}
+
+int pxg_sq8_create(uint32_t dim, int metric, int per_dim, uint64_t capacity, pxg_sq8** out) {
+  return pxg::guard([&] {
+    if (!out) pxg::config_error("out", 0, "must not be NULL");
+    check_groups_args(dim);
+    if (metric != PXG_INNER_PRODUCT && metric != PXG_COSINE)
+      pxg::config_error("metric", (uint64_t)metric, "the SQ8 index scores inner product (or cosine on prepared vectors)");
+    auto* h = new pxg_sq8();
+    Sq8Index& f = h->impl;
+    f.dim = dim;
+    f.ld = (dim + 3) & ~3u;
+    f.KP = (dim + 31) & ~31u;
+    f.metric = metric;
+    f.per_dim = per_dim ? 1 : 0;
+    try {
+      PXG_HIP(hipStreamCreateWithFlags(&f.stream, hipStreamNonBlocking));
+      if (capacity) f.ensure_capacity(capacity, 0);
+    } catch (...) {
+      delete h;
+      throw;
+    }
+    *out = h;
+  });
+}
+
+void pxg_sq8_destroy(pxg_sq8* index) { delete index; }
+
+int pxg_sq8_train(pxg_sq8* index, const float* training, uint64_t n) {
+  return pxg::guard([&] {
+    std::unique_lock<std::shared_mutex> lk(index->impl.mu);
+    index->impl.train(training, false, n);
+  });
+}
+
+int pxg_sq8_train_device(pxg_sq8* index, const float* d_training, uint64_t n) {
+  return pxg::guard([&] {
+    std::unique_lock<std::shared_mutex> lk(index->impl.mu);
+    index->impl.train(d_training, true, n);
+  });
+}
+
+int pxg_sq8_set_ranges(pxg_sq8* index, const float* min, const float* scale, const float* inverse_scale) {
+  return pxg::guard([&] {
+    std::unique_lock<std::shared_mutex> lk(index->impl.mu);
+    Sq8Index& f = index->impl;
+    const int g = f.groups();
+    pxg::Ranges r;
+    r.mn.assign(min, min + g);
+    r.scale.assign(scale, scale + g);
+    r.inv.assign(inverse_scale, inverse_scale + g);
+    f.set_ranges(r);
+  });
+}
+
+int pxg_sq8_ranges(const pxg_sq8* index, float* min, float* scale, float* inverse_scale) {
+  return pxg::guard([&] {
+    std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+    const Sq8Index& f = index->impl;
+    if (!f.trained) pxg::config_error("quantizer", 0, "the SQ8 index has not been trained");
+    std::copy(f.rg.mn.begin(), f.rg.mn.end(), min);
+    std::copy(f.rg.scale.begin(), f.rg.scale.end(), scale);
+    std::copy(f.rg.inv.begin(), f.rg.inv.end(), inverse_scale);
+  });
+}
+
+int pxg_sq8_is_trained(const pxg_sq8* index) {
+  std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+  return index->impl.trained ? 1 : 0;
+}
+
+int pxg_sq8_insert(pxg_sq8* index, const uint64_t* ids, const float* vectors, uint64_t n, uint32_t* out_slots) {
+  return pxg::guard([&] {
+    if (n == 0) return;
+    std::unique_lock<std::shared_mutex> lk(index->impl.mu);
+    index->impl.insert_host(ids, vectors, n, out_slots);
+  });
+}
+
+int pxg_sq8_insert_device(pxg_sq8* index, const uint64_t* ids, const float* d_vectors, uint64_t n,
+                          uint32_t* out_slots) {
+  return pxg::guard([&] {
+    if (n == 0) return;
+    std::unique_lock<std::shared_mutex> lk(index->impl.mu);
+    index->impl.insert_device(ids, d_vectors, n, out_slots);
+  });
+}
+
+int pxg_sq8_add_codes(pxg_sq8* index, const uint64_t* ids, const int8_t* codes, uint64_t n, uint32_t* out_slots) {
+  return pxg::guard([&] {
+    if (n == 0) return;
+    std::unique_lock<std::shared_mutex> lk(index->impl.mu);
+    index->impl.add_codes(ids, codes, n, out_slots);
+  });
+}
+
+int pxg_sq8_remove(pxg_sq8* index, uint64_t id) {
+  return pxg::guard([&] {
+    std::unique_lock<std::shared_mutex> lk(index->impl.mu);
+    index->impl.remove(id);
+  });
+}
+
+int pxg_sq8_contains(const pxg_sq8* index, uint64_t id) {
+  std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+  return index->impl.by_id.count(id) ? 1 : 0;
+}
+
+uint64_t pxg_sq8_len(const pxg_sq8* index) {
+  std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+  return index->impl.by_id.size();
+}
+
+int pxg_sq8_stats(const pxg_sq8* index, pxg_index_stats* out) {
+  return pxg::guard([&] {
+    std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+    const Sq8Index& f = index->impl;
+    out->len = f.by_id.size();
+    out->deleted = 0;
+    out->dim = f.dim;
+    out->metric = f.metric;
+    out->layers = 1;
+    out->edges = 0;
+    out->vector_bytes = f.codes.bytes();
+    out->graph_bytes = (uint64_t)(f.rg.mn.size() + f.rg.scale.size() + f.rg.inv.size()) * 4;  // table_bytes
+  });
+}
+
+int pxg_sq8_get_code(const pxg_sq8* index, uint64_t id, int8_t* out) {
+  return pxg::guard([&] {
+    std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+    const Sq8Index& f = index->impl;
+    auto it = f.by_id.find(id);
+    if (it == f.by_id.end()) pxg::raise(PXG_ERR_UNKNOWN_ID, "unknown vector id " + std::to_string(id), id);
+    PXG_HIP(hipMemcpy(out, f.codes.p + (size_t)it->second * f.KP, f.dim, hipMemcpyDeviceToHost));
+  });
+}
+
+uint64_t pxg_sq8_slot_count(const pxg_sq8* index) {
+  std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+  return index->impl.slots.high_water();
+}
+
+int pxg_sq8_slots(const pxg_sq8* index, uint64_t* ids, uint8_t* live) {
+  return pxg::guard([&] {
+    std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+    const Sq8Index& f = index->impl;
+    const size_t hw = f.slots.high_water();
+    for (size_t s = 0; s < hw; ++s) {
+      if (ids) ids[s] = f.live[s] ? f.ids[s] : 0;
+      if (live) live[s] = f.live[s];
+    }
+  });
+}
+
+static int sq8_search_host(const pxg_sq8* index, const float* queries, const int8_t* qcodes, uint64_t nq, uint64_t k,
+                           uint64_t rescore, const uint8_t* accept, uint64_t* out_ids, float* out_dist,
+                           uint32_t* out_count) {
+  return pxg::guard([&] {
+    pxg::check_k(k);
+    Sq8Index& f = const_cast<Sq8Index&>(index->impl);
+    std::shared_lock<std::shared_mutex> lk(f.mu);
+    if (nq == 0) return;
+    pxg::CtxLease ctx(f.pool);
+    hipStream_t s = ctx->stream;
+    const size_t N = f.slots.high_water();
+    uint8_t* d_acc = nullptr;
+    if (accept && N) {
+      d_acc = ctx->get(21, N);
+      PXG_HIP(hipMemcpyAsync(d_acc, accept, N, hipMemcpyHostToDevice, s));
+    }
+    const size_t kk = std::max<size_t>(k, 1);
+    uint64_t* d_oid = (uint64_t*)ctx->get(22, nq * kk * 8);
+    float* d_od = (float*)ctx->get(23, nq * kk * 4);
+    uint32_t* d_oc = (uint32_t*)ctx->get(24, nq * 4);
+    float* d_q = nullptr;
+    int8_t* d_qc = nullptr;
+    if (queries) {
+      d_q = (float*)ctx->get(20, nq * f.dim * 4);
+      PXG_HIP(hipMemcpyAsync(d_q, queries, nq * f.dim * 4, hipMemcpyHostToDevice, s));
+    } else {
+      d_qc = (int8_t*)ctx->get(25, nq * f.dim);
+      PXG_HIP(hipMemcpyAsync(d_qc, qcodes, nq * f.dim, hipMemcpyHostToDevice, s));
+    }
+    uint64_t fb = 0;
+    f.search_device(d_q, d_qc, nq, k, rescore, d_acc, d_oid, d_od, d_oc, ctx.c, s, &fb);
+    if (k) {
+      PXG_HIP(hipMemcpyAsync(out_ids, d_oid, nq * k * 8, hipMemcpyDeviceToHost, s));
+      PXG_HIP(hipMemcpyAsync(out_dist, d_od, nq * k * 4, hipMemcpyDeviceToHost, s));
+    }
+    PXG_HIP(hipMemcpyAsync(out_count, d_oc, nq * 4, hipMemcpyDeviceToHost, s));
+    PXG_HIP(hipStreamSynchronize(s));
+    pxg::g_sq8_fallbacks = fb;
+  });
+}
+
+int pxg_sq8_search(const pxg_sq8* index, const float* queries, uint64_t nq, uint64_t k, uint64_t rescore,
+                   const uint8_t* accept, uint64_t* out_ids, float* out_dist, uint32_t* out_count) {
+  return sq8_search_host(index, queries, nullptr, nq, k, rescore, accept, out_ids, out_dist, out_count);
+}
+
+int pxg_sq8_search_codes(const pxg_sq8* index, const int8_t* query_codes, uint64_t nq, uint64_t k,
+                         const uint8_t* accept, uint64_t* out_ids, float* out_dist, uint32_t* out_count) {
+  return sq8_search_host(index, nullptr, query_codes, nq, k, 0, accept, out_ids, out_dist, out_count);
+}
+
+int pxg_sq8_search_device(const pxg_sq8* index, const float* d_queries, uint64_t nq, uint64_t k, uint64_t rescore,
+                          const uint8_t* d_accept, uint64_t* d_out_ids, float* d_out_dist, uint32_t* d_out_count,
+                          void* stream) {
+  return pxg::guard([&] {
+    Sq8Index& f = const_cast<Sq8Index&>(index->impl);
+    std::shared_lock<std::shared_mutex> lk(f.mu);
+    pxg::CtxLease ctx(f.pool);
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    uint64_t fb = 0;
+    f.search_device(d_queries, nullptr, nq, k, rescore, d_accept, d_out_ids, d_out_dist, d_out_count, ctx.c, s, &fb);
+    PXG_HIP(hipStreamSynchronize(s));
+    pxg::g_sq8_fallbacks = fb;
+  });
+}
+
+uint64_t pxg_sq8_last_fallbacks(void) { return pxg::g_sq8_fallbacks; }
+
+int pxg_sq8_set_search_mode(pxg_sq8* index, int mode) {
+  return pxg::guard([&] {
+    if (mode < 0 || mode > 2) pxg::config_error("mode", (uint64_t)mode, "0 = auto, 1 = MFMA candidates, 2 = exact scan");
+    std::unique_lock<std::shared_mutex> lk(index->impl.mu);
+    index->impl.mode = mode;
+  });
+}
+
+}  // extern "C"

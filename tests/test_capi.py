@@ -76,3 +76,15 @@ def test_python_mirror_validation_without_gpu():
     px.check_k(1 << 24)
     with pytest.raises(px.Configuration):
         px.check_k((1 << 24) + 1)
+
+
+def test_sq8_configuration_errors_without_gpu(lib):
+    lib.pxg_last_error_message.restype = ctypes.c_char_p
+    h = ctypes.c_void_p()
+    assert lib.pxg_sq8_create(8, 0, 1, 0, ctypes.byref(h)) == 7  # Euclidean is not an SQ8 metric
+    assert b"metric" in lib.pxg_last_error_message()
+    assert lib.pxg_sq8_create(70000, 2, 1, 0, ctypes.byref(h)) == 7
+    assert b"dim" in lib.pxg_last_error_message()
+    three = (ctypes.c_float * 3)()
+    assert lib.pxg_sq_train(None, 0, 3, 1, three, three, three) == 7  # empty training (scalar.rs:145-152)
+    assert b"training" in lib.pxg_last_error_message()

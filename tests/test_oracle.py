@@ -296,6 +296,39 @@ def test_sq8_int_dot_search_exact():
         assert np.array_equal(d[i], s[order].astype(np.float32))
 
 
+def test_sq8_search_accept_ties_and_rescore():
+    """Filter, tie-break by id on duplicate codes, and the rescore stage
+    against an independent composition (numpy int64 matmul for the integer
+    stage, orc.sq_asym -- pinned above -- for the f32 stage)."""
+    rng = np.random.default_rng(9)
+    n, dim = 300, 20
+    x = rng.uniform(-1, 1, (n, dim)).astype(np.float32)
+    x[50] = x[7]  # identical codes: the lower id wins the tie
+    mn, sc, inv, _ = orc.sq_train(x)
+    codes = orc.sq_encode(x, mn, inv, True, 1).view(np.int8)
+    ids = (np.arange(n) * 3 + 1000).astype(np.uint64)
+    accept = (np.arange(n) % 4 != 1).astype(np.uint8)
+    qf = x[[7, 100, 201]] + np.float32(0.01)
+    qc = orc.sq_encode(qf, mn, inv, True, 1).view(np.int8)
+    got_i, got_d, got_c = orc.sq8_search(codes, ids, qc, 5, accept=accept, rescore=40, qf=qf, ranges=(mn, sc))
+    int_i, int_d, _ = orc.sq8_search(codes, ids, qc, 5, accept=accept)
+    for q in range(3):
+        s = -(codes.astype(np.int64) @ qc[q].astype(np.int64))
+        s = np.where(accept == 1, s, np.iinfo(np.int64).max)
+        order = np.lexsort((ids, s))
+        assert list(int_i[q]) == list(ids[order[:5]])
+        assert np.array_equal(int_d[q], s[order[:5]].astype(np.float32))
+        short = order[:40]
+        rs = np.array([orc.sq_asym(True, qf[q], codes[j].view(np.uint8), mn, sc, True, 1) for j in short], np.float32)
+        fin = np.lexsort((ids[short], rs))[:5]
+        assert got_c[q] == 5
+        assert list(got_i[q]) == list(ids[short][fin])
+        assert np.array_equal(got_d[q].view(np.uint32), rs[fin].view(np.uint32))
+    # the duplicated row: ids 1021 (slot 7) and 1150 (slot 50) tie; 1021 comes first
+    first = list(int_i[0]).index(1021)
+    assert 1150 in list(int_i[0]) and list(int_i[0]).index(1150) == first + 1
+
+
 # --- product.rs tests ------------------------------------------------------------------
 def _lcg_clustered(dim, count, seed):  # product.rs:635-654 fixture
     state = seed
