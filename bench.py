@@ -151,6 +151,100 @@ def bench_ivfpq(args, torch, px, dev):
     return out
 
 
+PEAK_INT8_MFMA_TOPS = 5000.0
+
+
+def bench_sq8(args, torch, px, dev):
+    """SQ8 flat search, inner product, k=10: 10M x 96 f32 ~U(-1,1), per-dimension
+    ranges calibrated on the first 100,000 vectors, I8 codes; 10,000 queries
+    ~U(-1,1) quantised the same way, batches of 1,024. Score = -(float) of the
+    exact int32 code dot product (integer MFMA)."""
+    n, dim, B, k = args.sq8_n, 96, args.batch, 10
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed + 11)
+    x = torch.rand((n, dim), generator=g, device=dev) * 2.0 - 1.0
+    queries = (torch.rand((args.queries, dim), generator=g, device=dev) * 2.0 - 1.0).contiguous()
+    ids = np.arange(n, dtype=np.uint64)
+    idx = px.Sq8Index(px.VectorSpace(dim, px.Metric.INNER_PRODUCT), capacity=n)
+    t0 = time.time()
+    idx.train_device(x[:100_000].contiguous())
+    idx.insert_device(ids, x)
+    torch.cuda.synchronize()
+    log(f"[bench] sq8: calibrated on 100000 and encoded {n}x{dim} in {time.time() - t0:.2f}s")
+    nb = args.queries // B
+    batches = [queries[i * B:(i + 1) * B] for i in range(nb)]
+    oi = torch.empty((B, k), dtype=torch.int64, device=dev)
+    od = torch.empty((B, k), dtype=torch.float32, device=dev)
+    oc = torch.empty((B,), dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    for s_ in range(3):
+        idx.search_device(batches[s_ % nb], k, oi, od, oc, stream=stream)
+    torch.cuda.synchronize()
+    fallbacks = 0
+    t0 = time.perf_counter()
+    for s_ in range(args.sq8_steps):
+        idx.search_device(batches[s_ % nb], k, oi, od, oc, stream=stream)
+        fallbacks += px.Sq8Index.last_fallbacks()
+    torch.cuda.synchronize()
+    step_s = (time.perf_counter() - t0) / args.sq8_steps
+    px.set_profiling(True)
+    stages = []
+    for s_ in range(args.sq8_steps):
+        idx.search_device(batches[s_ % nb], k, oi, od, oc, stream=stream)
+        stages.append(px.last_timings())
+    px.set_profiling(False)
+    scan_ms = float(np.mean([t["candidates_ms"] for t in stages]))
+    tops = 2.0 * n * dim * B / (scan_ms * 1e-3) / 1e12
+    log(f"[bench] sq8: {step_s * 1e3:.3f} ms/step = {B / step_s:.0f} QPS; stage-2 scan {scan_ms:.3f} ms = "
+        f"{tops:.0f} TOP/s; fallback queries {fallbacks}")
+    # recall@10 against exact f32 inner product over the same vectors
+    m = 200
+    qh = queries.cpu().numpy()
+    flat = px.FlatIndex(px.VectorSpace(dim, px.Metric.INNER_PRODUCT), n)
+    flat.insert_device(ids, x)
+    ti, _, _ = flat.search_batch(qh[:m], k)
+    del flat
+    gi, gd, gc = idx.search_batch(qh[:m], k)
+    recall = float(np.mean([len(set(ti[i].tolist()) & set(gi[i, :gc[i]].tolist())) / k for i in range(m)]))
+    ri, _, rc = idx.search_batch(qh[:m], k, rescore=100)
+    recall_rs = float(np.mean([len(set(ti[i].tolist()) & set(ri[i, :rc[i]].tolist())) / k for i in range(m)]))
+    x_host = None if args.no_cpu else x.cpu().numpy()
+    del x
+    torch.cuda.empty_cache()
+    out = {"value": round(B / step_s, 2), "unit": "queries/s", "ms_per_step": round(step_s * 1e3, 4),
+           "steps": args.sq8_steps,
+           "config": {"workload": "SQ8 flat search, inner product, 10M x 96 f32 ~U(-1,1) as I8 codes, batch 1024, "
+                                  "k=10", "n": n, "dim": dim, "batch": B, "k": k, "calibration": 100_000},
+           "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": PEAK_INT8_MFMA_TOPS, "unit": "TOP/s",
+                        "frac": round(tops / PEAK_INT8_MFMA_TOPS, 4), "traffic": load_traffic("sq8_mfma_scan")},
+           "kernel": "sq8_mfma_scan (stage 2)", "fallback_queries": fallbacks,
+           "stage_ms": {key: round(float(np.mean([t[key] for t in stages])), 4) for key in stages[0]},
+           "recall_at_10_vs_f32_ip": round(recall, 4), "recall_at_10_rescore100": round(recall_rs, 4)}
+    if not args.no_cpu:
+        from oracle import oracle as orc
+        mn, sc, inv, _ = orc.sq_train(x_host[:100_000], True)
+        qz = idx.quantizer()
+        ranges_same = bool(np.array_equal(qz.min.view(np.uint32), mn.view(np.uint32)) and
+                           np.array_equal(qz.inverse_scale.view(np.uint32), inv.view(np.uint32)))
+        codes = orc.sq_encode(x_host, mn, inv, True, 1, threads=args.cpu_threads).view(np.int8)
+        del x_host
+        mq = args.sq8_cpu_sample
+        qc = orc.sq_encode(qh[:mq], mn, inv, True, 1).view(np.int8)
+        log(f"[bench] sq8 CPU baseline: oracle integer SQ8 scan, {mq} queries, {args.cpu_threads} threads")
+        t0 = time.perf_counter()
+        wi, wd, wc = orc.sq8_search(codes, ids, qc, k, threads=args.cpu_threads)
+        cpu_s = time.perf_counter() - t0
+        gi, gd, gc = idx.search_batch(qh[:mq], k)
+        same = int(sum(np.array_equal(gi[i], wi[i]) and np.array_equal(gd[i].view(np.uint32), wd[i].view(np.uint32))
+                       for i in range(mq)))
+        out["cpu_baseline"] = {"value": round(mq / cpu_s, 3), "unit": "queries/s", "cores": args.cpu_threads,
+                               "kind": "port", "sample": f"{mq} queries, each a full 10M x 96 integer scan, oracle "
+                                                         f"SQ8 restatement, {args.cpu_threads} threads, {cpu_s:.2f}s"}
+        out["parity_sample"] = {"queries": mq, "bit_exact": same, "ranges_bit_exact": ranges_same}
+        log(f"[bench] sq8 CPU {mq / cpu_s:.2f} QPS; GPU/oracle bit-exact on {same}/{mq}; ranges equal {ranges_same}")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -169,6 +263,11 @@ def main():
     ap.add_argument("--ivf-only", action="store_true", help="run only the IVF-PQ leg (prints its JSON object)")
     ap.add_argument("--ivf-n", type=int, default=10_000_000)
     ap.add_argument("--ivf-steps", type=int, default=20)
+    ap.add_argument("--skip-sq8", action="store_true")
+    ap.add_argument("--sq8-only", action="store_true", help="run only the SQ8 leg (prints its JSON object)")
+    ap.add_argument("--sq8-n", type=int, default=10_000_000)
+    ap.add_argument("--sq8-steps", type=int, default=20)
+    ap.add_argument("--sq8-cpu-sample", type=int, default=2048)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also run one device copy of this size (a known-size kernel for scaling PMC byte counters)")
     args = ap.parse_args()
@@ -186,6 +285,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.ivf_only:
         print(json.dumps(bench_ivfpq(args, torch, px, dev)), flush=True)
+        return
+    if args.sq8_only:
+        print(json.dumps(bench_sq8(args, torch, px, dev)), flush=True)
         return
     n, dim, B = args.n, args.dim, args.batch
     log(f"[bench] generating {n}x{dim} corpus + {args.queries} queries on the GPU")
@@ -279,11 +381,15 @@ def main():
         parity = {"queries": m, "bit_exact": same}
         log(f"[bench] CPU {cpu['value']} QPS; GPU/oracle bit-exact on {same}/{m} sample queries")
 
+    del idx
+    torch.cuda.empty_cache()
     ivf = None
     if not args.skip_ivfpq:
-        del idx
-        torch.cuda.empty_cache()
         ivf = bench_ivfpq(args, torch, px, dev)
+        torch.cuda.empty_cache()
+    sq8 = None
+    if not args.skip_sq8:
+        sq8 = bench_sq8(args, torch, px, dev)
 
     out = {
         "metric": METRIC,
@@ -312,6 +418,7 @@ def main():
                  "fallback_queries": fb100},
         "parity_sample": parity,
         "ivfpq": ivf,
+        "sq8": sq8,
     }
     print(json.dumps(out), flush=True)
 

@@ -708,6 +708,26 @@ void orc_sq_encode(const float* v, size_t dim, int per_dim, int code_type, const
   }
 }
 
+// encode_into over n rows, rows split across threads (each row as above).
+void orc_sq_encode_rows(const float* v, size_t n, size_t dim, int per_dim, int code_type, const float* mn,
+                        const float* inv, int threads, uint8_t* out) {
+  auto work = [&](size_t a, size_t b) {
+    for (size_t i = a; i < b; ++i) orc_sq_encode(v + i * dim, dim, per_dim, code_type, mn, inv, out + i * dim);
+  };
+  if (threads <= 1 || n < 2) {
+    work(0, n);
+    return;
+  }
+  std::vector<std::thread> pool;
+  size_t per = (n + threads - 1) / threads;
+  for (int t = 0; t < threads; ++t) {
+    size_t a = t * per, b = std::min(n, a + per);
+    if (a >= b) break;
+    pool.emplace_back(work, a, b);
+  }
+  for (auto& th : pool) th.join();
+}
+
 // reconstruct: scalar.rs:323-327.
 void orc_sq_decode(const uint8_t* code, size_t dim, int per_dim, int code_type, const float* mn, const float* scale,
                    float* out) {

@@ -53,6 +53,7 @@ def _load():
                                    C.c_int, _u64p, _f32p, _u32p]),
         "orc_sq_train": (C.c_longlong, [_f32p, _sz, _sz, C.c_int, _f32p, _f32p, _f32p]),
         "orc_sq_encode": (None, [_f32p, _sz, C.c_int, C.c_int, _f32p, _f32p, _u8p]),
+        "orc_sq_encode_rows": (None, [_f32p, _sz, _sz, C.c_int, C.c_int, _f32p, _f32p, C.c_int, _u8p]),
         "orc_sq_decode": (None, [_u8p, _sz, C.c_int, C.c_int, _f32p, _f32p, _f32p]),
         "orc_sq_asym": (C.c_float, [C.c_int, _f32p, _u8p, _sz, C.c_int, C.c_int, _f32p, _f32p]),
         "orc_sq8_search": (None, [_i8p, _u8p, _u64p, _sz, _sz, _i8p, _sz, _sz, C.c_void_p, _sz, C.c_void_p,
@@ -210,15 +211,12 @@ def sq_train(training, per_dim=True):
     return mn, scale, inv, bad
 
 
-def sq_encode(v, mn, inv, per_dim=True, code_type=1):
+def sq_encode(v, mn, inv, per_dim=True, code_type=1, threads=1):
     v = f32(v)
     dim = v.shape[-1]
-    rows = v.reshape(-1, dim)
+    rows = np.ascontiguousarray(v.reshape(-1, dim))
     out = np.zeros(rows.shape, np.uint8)
-    for i in range(rows.shape[0]):
-        o = np.zeros(dim, np.uint8)
-        lib.orc_sq_encode(np.ascontiguousarray(rows[i]), dim, int(per_dim), code_type, mn, inv, o)
-        out[i] = o
+    lib.orc_sq_encode_rows(rows, rows.shape[0], dim, int(per_dim), code_type, f32(mn), f32(inv), threads, out)
     return out.reshape(v.shape)
 
 

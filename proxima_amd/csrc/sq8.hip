@@ -53,8 +53,19 @@ constexpr int SQ_SAMPLE = 8;          // stage 1 visits at most one row tile in 
 constexpr int SQ_MAX_CHUNKS = 1024;   // stage-1 entries per query <= 2 * this
 constexpr int SQ_MAX_KB = 8;          // MFMA path: code rows up to 256 bytes
 constexpr uint32_t SQ_MAX_DIM = 65536;  // |S| < 2^31
+// Buffer resource word 3 for raw (untyped, stride 0) gfx9 buffer accesses.
+constexpr int SQ_RSRC_WORD3 = 0x00020000;
+constexpr int SQ_LCAP = 1024;         // per-workgroup candidate list in LDS
 
-__host__ __device__ constexpr int sq_rows(int kb) { return kb <= 4 ? 128 : 64; }
+__host__ __device__ constexpr int sq_rows(int kb) { return kb <= 4 ? 256 : 128; }
+
+// s_waitcnt with vmcnt <= N (expcnt and lgkmcnt left unconstrained); gfx9
+// encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8.
+template <int N>
+__device__ inline void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 __host__ __device__ constexpr int sq_qt(int kb) { return kb <= 4 ? 4 : 2; }
 
 __device__ inline uint32_t f2ord(float f) {
@@ -202,88 +213,144 @@ __global__ void sq8_mark(const uint32_t* __restrict__ slots, const uint64_t* __r
 }
 
 // ---------------------------------------------------------------------------
-// Integer MFMA scan. Workgroup = SQ_NW waves; wave w holds QT tiles of 32
-// query codes in VGPRs (the MFMA B operand: lane l gives query l%32, bytes
-// [kb*32 + 16*(l/32), +16) of K block kb); database rows stream through a
-// double-buffered LDS tile of R rows (row stride KP+16 bytes: 16-byte reads
-// of 16 consecutive rows hit distinct banks) and feed the A operand the same
-// way. Output lane l, register v = row 8*(v/4) + 4*(l/32) + v%4 of the tile
-// against query l%32, so every lane filters scores of one query.
+// Integer MFMA scan. Workgroup = SQ_NW compute waves + one loader wave.
+// Compute wave w holds QT tiles of 32 query codes in VGPRs (the MFMA B
+// operand: lane l gives query l%32, bytes [kb*32 + 16*(l/32), +16) of K
+// block kb); database rows stream through a double-buffered LDS tile of R
+// rows (row stride KP+16 bytes: 16-byte reads of 16 consecutive rows hit
+// distinct banks) and feed the A operand the same way. Output lane l,
+// register v = row 8*(v/4) + 4*(l/32) + v%4 of the tile against query l%32,
+// so every lane filters scores of one query.
+//
+// The loader wave fetches the next tile into the idle LDS buffer while the
+// compute waves work on the current one, so the compute waves never wait on
+// HBM and never hold outstanding vector-memory loads.
 // ---------------------------------------------------------------------------
 template <int KB, bool STAGE1>
-__global__ __launch_bounds__(SQ_NW * 64) void sq8_mfma_scan(
+__global__ __launch_bounds__((SQ_NW + 1) * 64) void sq8_mfma_scan(
     const int8_t* __restrict__ Qc, int nq, const int8_t* __restrict__ C, int N, const uint8_t* __restrict__ live,
-    const uint8_t* __restrict__ accept, const uint32_t* __restrict__ rank, int tiles_per_chunk, int sample,
-    const int* __restrict__ thr_in, int* __restrict__ tmax, int* __restrict__ ccount, uint64_t* __restrict__ cand,
-    int cap) {
+    const uint8_t* __restrict__ accept, const uint32_t* __restrict__ rank, int nchunks, int qgroups,
+    int tiles_per_chunk, int sample, const int* __restrict__ thr_in, int* __restrict__ tmax,
+    int* __restrict__ ccount, uint64_t* __restrict__ cand, int cap) {
   constexpr int KP = KB * 32, SR = KP + 16, R = sq_rows(KB), RT = R / 32, QT = sq_qt(KB);
-  constexpr int PIECES = R * KP / 16, NT = SQ_NW * 64, CPT = (PIECES + NT - 1) / NT;
-  __shared__ __align__(16) int8_t tile[2][R * SR];
-  __shared__ __align__(4) uint8_t vb[2][R];
+  constexpr int PPR = KP / 16;         // 16-byte pieces per row
+  constexpr int D = 2;                // LDS tile buffers: the next tile loads during the current one
+  __shared__ __align__(16) int8_t tile[D][R * SR];
+  __shared__ __align__(4) uint8_t vb[STAGE1 ? 2 : 1][R];
+  // stage 2: the 16 scores per lane of a recomputed tile with a passing
+  // score, scanned by a rolled loop (each lane reads back only its own
+  // values, so no barrier is needed); passing scores go to a workgroup list
+  // in LDS, filtered and published after the scan.
+  __shared__ int stash[STAGE1 ? 1 : SQ_NW * 16 * 64];
+  __shared__ int lc_score[STAGE1 ? 1 : SQ_LCAP];
+  __shared__ int lc_row[STAGE1 ? 1 : SQ_LCAP];
+  __shared__ int lc_q[STAGE1 ? 1 : SQ_LCAP];
+  __shared__ int lc_n;
+
+  // XCD-aware mapping: workgroup ids are dealt round-robin over the 8 XCDs;
+  // consecutive logical ids (the query groups of one chunk) go to the same
+  // XCD at about the same time and share its L2 copy of the chunk.
+  const int total = nchunks * qgroups;
+  const int per_xcd = (total + 7) / 8;
+  const int lid = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  if (lid >= total) return;  // uniform over the workgroup, before any barrier
+  const int chunk = lid / qgroups, qgroup = lid % qgroups;
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, r = lane & 31;
-  const int q0 = blockIdx.y * (SQ_NW * QT * 32) + w * (QT * 32);
-  const bool active = q0 < nq;
+  const bool loader = w == SQ_NW;
+  const int q0 = qgroup * (SQ_NW * QT * 32) + w * (QT * 32);
+  const bool active = !loader && q0 < nq;
 
   i4v qa[QT][KB];
   int thr[QT], run[QT];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const int q = q0 + qt * 32 + r;
+    const bool ok = active && q < nq;
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
-      qa[qt][kb] = q < nq ? *reinterpret_cast<const i4v*>(Qc + (size_t)q * KP + kb * 32 + h * 16) : i4v{0, 0, 0, 0};
-    thr[qt] = STAGE1 ? INT_MIN : (q < nq ? thr_in[q] : INT_MAX);
+      qa[qt][kb] = ok ? *reinterpret_cast<const i4v*>(Qc + (size_t)q * KP + kb * 32 + h * 16) : i4v{0, 0, 0, 0};
+    thr[qt] = STAGE1 ? INT_MIN : (ok ? thr_in[q] : INT_MAX);
     run[qt] = INT_MIN;
   }
 
   const int ntiles = (N + R - 1) / R;
-  const int tb = blockIdx.x * tiles_per_chunk;
+  const int tb = chunk * tiles_per_chunk;
   const int te = min(ntiles, tb + tiles_per_chunk);
-  const int STEP = STAGE1 ? sample : 1;
+  const int step = STAGE1 ? sample : 1;
+  const int t0 = STAGE1 ? (tb + sample - 1) / sample * sample : tb;
+  const int niter = t0 < te ? (te - t0 + step - 1) / step : 0;
 
-  i4v pre[CPT];
-  uint8_t pv = 0;
-  auto gload = [&](int t) {
+  // The loader fills a tile with buffer_load_dwordx4 ... lds: instruction
+  // i writes 64 x 16 bytes at LDS offset 1024*i, lane l to byte 16*l, i.e.
+  // the 16-byte slot 64*i + l of the padded tile (PPR data slots + 1 padding
+  // slot per row). The buffer resource is rebased on each tile and covers
+  // its rows only, so rows past N and padding slots (given an offset beyond
+  // the range) read zeros. The per-lane offsets are the same for every tile:
+  // the loader steps slot 64*i + l -> (row, part) from one instruction to
+  // the next (64 slots = 64/SPR rows + 64%SPR parts).
+  constexpr int SPR = PPR + 1, NI = R * SPR / 64;
+  static_assert(R * SPR % 64 == 0 && NI < 64, "tile must split into whole DMA instructions");
+  static_assert(64 % SPR != 0 || SPR == 64, "slot stepping assumes 64 / SPR rows plus a part step");
+  auto issue = [&](int t, int buf) {
+    if (STAGE1) {
+      // usable-row bytes first; their wait leaves only the tile DMA in flight
+      uint8_t pv[(R + 63) / 64];
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = tid + i * NT;
-      i4v v = {0, 0, 0, 0};
-      if (c < PIECES) {
-        const int row = c / (KP / 16), part = c % (KP / 16);
+      for (int i = 0; i < (R + 63) / 64; ++i) {
+        const int row = lane + i * 64;
         const long g = (long)t * R + row;
-        if (g < N) v = *reinterpret_cast<const i4v*>(C + (size_t)g * KP + part * 16);
+        pv[i] = (row < R && g < N && live[g] && (accept == nullptr || accept[g])) ? 1 : 0;
       }
-      pre[i] = v;
-    }
-    if (STAGE1 && tid < R) {
-      const long g = (long)t * R + tid;
-      pv = (g < N && live[g] && (accept == nullptr || accept[g])) ? 1 : 0;
-    }
-  };
-  auto lstore = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = tid + i * NT;
-      if (c < PIECES) {
-        const int row = c / (KP / 16), part = c % (KP / 16);
-        *reinterpret_cast<i4v*>(&tile[buf][row * SR + part * 16]) = pre[i];
+      for (int i = 0; i < (R + 63) / 64; ++i)
+        if (lane + i * 64 < R) vb[buf][lane + i * 64] = pv[i];
+    }
+#if defined(__HIP_DEVICE_COMPILE__)
+    const int rows = min(R, N - t * R);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(C + (size_t)t * R * KP), 0, rows * KP, SQ_RSRC_WORD3);
+    int row = lane / SPR, part = lane % SPR;
+#pragma unroll 1
+    for (int i = 0; i < NI; ++i) {
+      const int off = part < PPR ? row * KP + part * 16 : 0x7FFFFFF0;  // padding: beyond the range, reads zeros
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)&tile[buf][i * 1024], 16,
+                                               off, 0, 0, 0);
+      row += 64 / SPR;
+      part += 64 % SPR;
+      if (part >= SPR) {
+        part -= SPR;
+        ++row;
       }
     }
-    if (STAGE1 && tid < R) vb[buf][tid] = pv;
+#endif
   };
 
-  int t = tb;
-  if (t < te) {
-    gload(t);
-    lstore(0);
+  // Loader pipeline: tile j goes to buffer j % D, issued D - 1 iterations
+  // before it is used (its buffer was last read in the iteration before the
+  // issue). Before each barrier the loader waits until only the DMAs of the
+  // tiles after the next one are outstanding.
+  if (tid == 0) lc_n = 0;
+  if (loader) {
+    for (int j = 0; j < D - 1 && j < niter; ++j) issue(t0 + j * step, j);
+    const int later = min(D - 2, niter - 1);  // tiles issued after tile 0
+    if (later >= 1) wait_vm<NI>();
+    else wait_vm<0>();
   }
   __syncthreads();
-  int buf = 0;
-  for (; t < te; t += STEP) {
-    const int tn = t + STEP;
-    if (tn < te) gload(tn);
-    if (active) {
+  for (int it = 0; it < niter; ++it) {
+    const int buf = it % D;
+    const int t = t0 + it * step;
+    if (loader) {
+      if (it + D - 1 < niter) issue(t0 + (it + D - 1) * step, (it + D - 1) % D);
+      // tiles it+2 .. min(it+D-1, niter-1) may stay in flight; tile it+1 must land
+      const int later = max(0, min(it + D - 1, niter - 1) - (it + 1));
+      static_assert(D <= 3, "the waits below cover at most one later tile");
+      if (later >= 1) wait_vm<NI>();
+      else wait_vm<0>();
+    } else if (active) {
+      static_assert(RT * QT <= 32, "one pass bit per 32 x 32 tile");
+      uint32_t passmask = 0;  // bit rt*QT+qt: that 32 x 32 tile has a score >= the threshold
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
         i4v a[KB];
@@ -315,24 +382,58 @@ __global__ __launch_bounds__(SQ_NW * 64) void sq8_mfma_scan(
 #pragma unroll
           for (int qt = 0; qt < QT; ++qt) {
             const i16v x = acc[qt];
-            int m = max(x[0], max(x[1], x[2]));
-            m = max(m, max(x[3], x[4]));
-            m = max(m, max(x[5], x[6]));
-            m = max(m, max(x[7], x[8]));
-            m = max(m, max(x[9], x[10]));
-            m = max(m, max(x[11], x[12]));
-            m = max(m, max(x[13], x[14]));
+            int m = max(max(x[0], x[1]), x[2]);  // a chain of v_max3
+            m = max(max(m, x[3]), x[4]);
+            m = max(max(m, x[5]), x[6]);
+            m = max(max(m, x[7]), x[8]);
+            m = max(max(m, x[9]), x[10]);
+            m = max(max(m, x[11]), x[12]);
+            m = max(max(m, x[13]), x[14]);
             m = max(m, x[15]);
-            if (__ballot(m >= thr[qt])) {
-              const int q = q0 + qt * 32 + r;
+            passmask |= (__ballot(m >= thr[qt]) != 0 ? 1u : 0u) << (rt * QT + qt);
+          }
+        }
+      }
+      // Rare: some 32 x 32 tiles hold a score >= the threshold. Recompute
+      // exactly those from the LDS tile (still valid until the barrier) and
+      // append their passing scores to the workgroup list.
+      if constexpr (!STAGE1) {
+        if (passmask) {
+#pragma unroll 1
+          for (int rt = 0; rt < RT; ++rt) {
+            const uint32_t bits = (passmask >> (rt * QT)) & ((1u << QT) - 1u);
+            if (!bits) continue;
+            i4v a[KB];
 #pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+              a[kb] = *reinterpret_cast<const i4v*>(&tile[buf][(rt * 32 + r) * SR + kb * 32 + h * 16]);
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
+              if (!((bits >> qt) & 1u)) continue;
+              i16v x;
+#pragma unroll
+              for (int v = 0; v < 16; ++v) x[v] = 0;
+#pragma unroll
+              for (int kb = 0; kb < KB; ++kb) x = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[kb], qa[qt][kb], x, 0, 0, 0);
+              int* sx = stash + w * 16 * 64 + lane;
+#pragma unroll
+              for (int v = 0; v < 16; ++v) sx[v * 64] = x[v];
+              const int q = q0 + qt * 32 + r;
+              const int tq = thr[qt];
+              const int rowb = t * R + rt * 32 + 4 * h;
+#pragma unroll 1
               for (int v = 0; v < 16; ++v) {
-                if (x[v] >= thr[qt]) {
-                  const int row = t * R + rt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-                  if (row < N && q < nq && live[row] && (accept == nullptr || accept[row])) {
-                    const int pos = atomicAdd(&ccount[q], 1);
-                    if (pos < cap)
-                      cand[(size_t)q * cap + pos] = ((uint64_t)ord_key(-(float)x[v]) << 32) | rank[row];
+                const int val = sx[v * 64];
+                const int row = rowb + 8 * (v >> 2) + (v & 3);
+                if (val >= tq && row < N && q < nq) {
+                  const int pos = atomicAdd(&lc_n, 1);
+                  if (pos < SQ_LCAP) {
+                    lc_score[pos] = val;
+                    lc_row[pos] = row;
+                    lc_q[pos] = q;
+                  } else if (live[row] && (accept == nullptr || accept[row])) {  // list full: publish directly
+                    const int gp = atomicAdd(&ccount[q], 1);
+                    if (gp < cap) cand[(size_t)q * cap + gp] = ((uint64_t)ord_key(-(float)val) << 32) | rank[row];
                   }
                 }
               }
@@ -341,16 +442,25 @@ __global__ __launch_bounds__(SQ_NW * 64) void sq8_mfma_scan(
         }
       }
     }
-    if (tn < te) lstore(buf ^ 1);
     __syncthreads();
-    buf ^= 1;
   }
   if constexpr (STAGE1) {
     if (active) {
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) {
         const int q = q0 + qt * 32 + r;
-        if (q < nq) tmax[(size_t)q * (gridDim.x * 2) + blockIdx.x * 2 + h] = run[qt];
+        if (q < nq) tmax[(size_t)q * (nchunks * 2) + chunk * 2 + h] = run[qt];
+      }
+    }
+  } else {
+    // publish the workgroup's candidates (the loop's last barrier ordered
+    // every append before this read)
+    const int n = min(lc_n, SQ_LCAP);
+    for (int i = tid; i < n; i += (SQ_NW + 1) * 64) {
+      const int row = lc_row[i], q = lc_q[i];
+      if (live[row] && (accept == nullptr || accept[row])) {
+        const int gp = atomicAdd(&ccount[q], 1);
+        if (gp < cap) cand[(size_t)q * cap + gp] = ((uint64_t)ord_key(-(float)lc_score[i]) << 32) | rank[row];
       }
     }
   }
@@ -873,7 +983,10 @@ struct Sq8Index {
     uint32_t* ocount = (uint32_t*)ctx->get(7, nq * 4);
     int* flag_list = (int*)ctx->get(8, nq * 4);
     PXG_HIP(hipMemsetAsync(flag_count, 0, 4, s));
-    const bool mfma = mode != 2 && KB <= SQ_MAX_KB && (mode == 1 || N >= 4096);
+    // automatic: the MFMA path when stage 1 can give every query >= 4 * kk
+    // maxima (two per sampled chunk); smaller indexes take the exact scan
+    const int ntiles_all = KB <= SQ_MAX_KB ? (N + sq_rows(KB) - 1) / sq_rows(KB) : 0;
+    const bool mfma = mode != 2 && KB <= SQ_MAX_KB && (mode == 1 || (N >= 4096 && 2 * ntiles_all >= 4 * kk));
     int nflag = 0;
     if (mfma) {
       const int R = sq_rows(KB), QT = sq_qt(KB);
@@ -882,12 +995,13 @@ struct Sq8Index {
       // Stage 1 samples every `sample`-th tile (a divisor of the chunk
       // length, so every chunk contributes).
       const int ntiles = (N + R - 1) / R;
+      // Stage 1 visits the tiles t % sample == 0; with chunks of >= sample
+      // tiles every full chunk holds one (a chunk without one only adds
+      // INT_MIN entries, which never raise the threshold).
       const int target = std::min(std::min(SQ_MAX_CHUNKS, ntiles), std::max(512, 2 * kk));
       int tpc = (ntiles + target - 1) / target;
       int sample = SQ_SAMPLE;
-      if (tpc >= SQ_SAMPLE) {
-        tpc = (tpc + SQ_SAMPLE - 1) / SQ_SAMPLE * SQ_SAMPLE;
-      } else {
+      if (tpc < SQ_SAMPLE) {
         sample = 1;
         while (sample * 2 <= tpc) sample *= 2;
         tpc = sample;
@@ -901,11 +1015,11 @@ struct Sq8Index {
       int* thr = (int*)ctx->get(10, nq * 4);
       int* ccount = (int*)ctx->get(11, nq * 4);
       uint64_t* cand = (uint64_t*)ctx->get(12, nq * cap_c * 8);
-      const dim3 grid((unsigned)nchunks, (unsigned)qgroups);
-      tm.mark(1);
+      const dim3 grid((unsigned)((nchunks * qgroups + 7) / 8 * 8));
 #define PXG_SQ_SCAN(KBV, ST)                                                                                        \
-  hipLaunchKernelGGL((sq8_mfma_scan<KBV, ST>), grid, dim3(SQ_NW * 64), 0, s, (const int8_t*)Qc, (int)nq,           \
-                     (const int8_t*)codes.p, N, d_live.p, d_accept, d_rank.p, tpc, sample, (const int*)thr, tmax,  \
+  hipLaunchKernelGGL((sq8_mfma_scan<KBV, ST>), grid, dim3((SQ_NW + 1) * 64), 0, s, (const int8_t*)Qc, (int)nq,           \
+                     (const int8_t*)codes.p, N, d_live.p, d_accept, d_rank.p, nchunks, qgroups, tpc, sample,       \
+                     (const int*)thr, tmax,                                                                        \
                      ccount, cand, cap_c)
 #define PXG_SQ_SWITCH(ST)                  \
   switch (KB) {                            \
@@ -918,10 +1032,13 @@ struct Sq8Index {
     case 7: PXG_SQ_SCAN(7, ST); break;     \
     default: PXG_SQ_SCAN(8, ST); break;    \
   }
+      // stage 1 and the thresholds count as preparation; the candidates
+      // stage is the stage-2 scan alone
       PXG_SQ_SWITCH(true)
       PXG_HIP(hipGetLastError());
       hipLaunchKernelGGL(sq8_thresholds, dim3((unsigned)nq), dim3(256), 0, s, (const int*)tmax, E, kk, thr);
       PXG_HIP(hipMemsetAsync(ccount, 0, nq * 4, s));
+      tm.mark(1);
       PXG_SQ_SWITCH(false)
 #undef PXG_SQ_SWITCH
 #undef PXG_SQ_SCAN

@@ -131,7 +131,7 @@ def test_search_parity_all_paths(gpu, dim, mode):
     q = uniform(rng, nq, dim)
     for k in (1, 10, 100):
         assert_same(idx.search_batch(q, k), oracle_search(codes, np.arange(n), q, ranges, k))
-    if mode != 2 and dim >= 37:  # 8-byte codes tie often; overflow there is legal, just slower
+    if mode == 0:  # automatic mode picks a path that needs no rescans
         assert px.Sq8Index.last_fallbacks() == 0
 
 
