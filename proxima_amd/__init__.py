@@ -1001,3 +1001,68 @@ class Sq8Index(_IndexBase):
 
 
 __all__ += ["CodeType", "RangeMode", "ScalarQuantizer", "Sq8Index"]
+
+
+# --- recall: crates/proxima-index/src/recall.rs:27-187 -----------------------------------
+class RecallReport:
+    """RecallReport (recall.rs:27-70): queries, k, mean, min, per_query, short_results."""
+
+    def __init__(self, queries, k, mean, min, per_query, short_results):
+        self.queries, self.k, self.mean, self.min = queries, k, mean, min
+        self.per_query, self.short_results = per_query, short_results
+
+    def below(self, threshold):  # recall.rs:49-55
+        if not self.per_query:
+            return 0.0
+        t = np.float32(threshold)
+        return float(np.float32(sum(1 for r in self.per_query if r < t)) / np.float32(len(self.per_query)))
+
+    def __str__(self):  # recall.rs:58-70
+        return (f"recall@{self.k}: mean {self.mean:.4f}, min {self.min:.4f}, below 0.9 "
+                f"{self.below(0.9) * 100.0:.1f}% ({self.queries} queries)")
+
+    __repr__ = __str__
+
+
+def _overlap(exact, approx):  # recall.rs:172-184: |exact ∩ approx| / |exact|
+    if len(exact) == 0:
+        return np.float32(1.0)
+    ex = set(int(i) for i in exact)
+    hits = sum(1 for i in approx if int(i) in ex)
+    return np.float32(hits) / np.float32(len(exact))
+
+
+def recall_at_k(candidate, truth, queries, k):
+    """recall_at_k (recall.rs:108-115): `candidate` is any index of this
+    module, `truth` a FlatIndex over the same vectors and ids."""
+    return recall_at_k_filtered(candidate, truth, queries, k, None)
+
+
+def recall_at_k_filtered(candidate, truth, queries, k, filter):
+    """recall_at_k_filtered (recall.rs:123-166). The exact side is one batched
+    exhaustive GPU scan over all queries (the flat kernel), the approximate
+    side one batched search; the statistics follow the reference's f32
+    arithmetic (sum in query order, then divide)."""
+    dim = truth.space.dim
+    q = np.asarray(queries, dtype=np.float32).reshape(-1)
+    if q.size % dim != 0:
+        raise _config("queries", q.size, "must be a multiple of the index dimension")
+    q = q.reshape(-1, dim)
+    per_query, short = [], 0
+    if q.shape[0]:
+        ti, _, tc = truth.search_batch(q, k, filter)
+        ai, _, ac = candidate.search_batch(q, k, filter)
+        for i in range(q.shape[0]):
+            if ac[i] < tc[i]:
+                short += 1
+            per_query.append(_overlap(ti[i, :tc[i]], ai[i, :ac[i]]))
+    n = len(per_query)
+    total = np.float32(0.0)
+    for r in per_query:
+        total = np.float32(total + r)
+    mean = float(total / np.float32(n)) if n else 0.0
+    mn = min(per_query) if per_query else np.float32(np.inf)
+    return RecallReport(n, k, mean, float(mn) if np.isfinite(mn) else 0.0, [float(r) for r in per_query], short)
+
+
+__all__ += ["RecallReport", "recall_at_k", "recall_at_k_filtered"]

@@ -16,15 +16,20 @@
 //              the untrained exhaustive path).
 //
 // Search (ivfpq.rs:998-1110), per batch:
-//   ivf_coarse  exact squared_euclidean_unrolled to every centroid (bit-exact,
-//               so the probed list set is the reference's), radix-select the
-//               nprobe smallest (distance, list).
-//   ivf_scan    one workgroup per (query, probe): build the distance table in
-//               LDS exactly as distance_table does (per subspace, per
-//               centroid, sequential d = q - c; l2 += d*d; ip += q*c), stream
-//               the list's codes coalesced (M bytes + a 4-byte id rank per
-//               entry), ADC-sum the table in subspace order (bit-exact),
-//               keep a per-wave top-kk by (score, id).
+//   coarse      exact squared_euclidean_unrolled to every centroid (bit-exact,
+//               so the probed list set is the reference's) and the nprobe
+//               smallest (distance, list): ivf_coarse_topk over the transposed
+//               centroids for nprobe <= 64, else the exact flat index over the
+//               centroids, else ivf_coarse_keys + ivf_coarse_select.
+//   scan        build each probe's distance table exactly as distance_table
+//               does (per subspace, per centroid, sequential d = q - c;
+//               l2 += d*d; ip += q*c), stream the list's codes coalesced (M
+//               bytes + a 4-byte id rank per entry), ADC-sum the table in
+//               subspace order (bit-exact), keep a per-wave top-kk by (score,
+//               id): ivf_scan_reg (codebooks in VGPRs, one workgroup per query
+//               and 8 probes) for dim <= 128 with equal subspace widths and
+//               kk <= 64, else ivf_scan (table in LDS, one workgroup per
+//               query and probe).
 //   ivf_merge   per query: select the shortlist over all probes, optionally
 //               rescore it exactly against the stored vectors (rerank), keep k.
 #include <algorithm>
