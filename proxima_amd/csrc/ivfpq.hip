@@ -348,99 +348,132 @@ __global__ void ivf_transpose_cents(const float* __restrict__ C, int ld, int dim
   cT[t] = c < produced ? C[(size_t)c * ld + i] : 0.0f;
 }
 
-constexpr int IVF_PG = 8;  // probes per workgroup item
+constexpr int IVF_PGMAX = 32;   // probes per scan workgroup, at most
+constexpr int IVF_SW = 8;       // waves per scan workgroup
 
+// ADC scan, register-resident codebooks (uniform subspace width W, M*W = dim
+// <= 128, shortlist <= 64). One workgroup of 512 threads per (query, group of
+// up to IVF_PGMAX probes); thread t holds row t%256 of the codebooks of half
+// of the subspaces (t/256 picks the half) in VGPRs. The group's residuals
+// are computed up front (one round of global-load latency); then per probe
+// the threads build their rows of the distance table (VALU work on
+// LDS-broadcast residual vectors) and the 8 waves stream the list: coalesced
+// 16-byte codes and 4-byte ranks, ADC sums in subspace order, and a per-wave
+// top-kk (sorted keys, one per lane) kept across the whole group.
 template <int W, int METRIC>
-__global__ __launch_bounds__(256) void ivf_scan_reg(const float* __restrict__ Qp, int ld, int dim, int M,
-                                                    const int* __restrict__ probes, int nprobe, int groups,
-                                                    const float* __restrict__ cents, const float* __restrict__ books,
-                                                    const uint32_t* __restrict__ list_off,
-                                                    const uint32_t* __restrict__ list_rank,
-                                                    const uint8_t* __restrict__ list_codes,
-                                                    const uint32_t* __restrict__ rank_slot,
-                                                    const uint8_t* __restrict__ accept, int kk,
-                                                    uint64_t* __restrict__ out) {
-  constexpr int MMAX = 128 / W;
+__global__ __launch_bounds__(IVF_SW * 64) void ivf_scan_reg(const float* __restrict__ Qp, int ld, int dim, int M,
+                                                         const int* __restrict__ probes, int nprobe, int pg,
+                                                         int groups, const float* __restrict__ cents,
+                                                         const float* __restrict__ books,
+                                                         const uint32_t* __restrict__ list_off,
+                                                         const uint32_t* __restrict__ list_rank,
+                                                         const uint8_t* __restrict__ list_codes,
+                                                         const uint32_t* __restrict__ rank_slot,
+                                                         const uint8_t* __restrict__ accept, int kk,
+                                                         uint64_t* __restrict__ out) {
+  constexpr int MMAX = 128 / W, MH = (MMAX + 1) / 2;
   extern __shared__ float lut[];  // M * 256 floats
-  __shared__ float sr[128];
-  __shared__ float s_qdc;
+  __shared__ __align__(16) float srs[IVF_PGMAX][128];
+  __shared__ float s_qdc[IVF_PGMAX];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int c = tid & 255, half = tid >> 8;
   const int q = blockIdx.x / groups, grp = blockIdx.x % groups;
-  const int p0 = grp * IVF_PG, p1 = min(nprobe, p0 + IVF_PG);
-  // codebook rows of centroid `tid`, all subspaces (book_off[s] = s*256*W)
-  float breg[MMAX][W];
+  const int p0 = grp * pg, np = min(nprobe, p0 + pg) - p0;
+  const int mh = (M + 1) / 2;           // subspaces per half
+  const int sb = half * mh;             // this thread's first subspace
+  const int ns = min(mh, M - sb);       // and how many
+  // codebook row c of subspaces sb .. sb+ns-1 (book_off[s] = s*256*W)
+  float breg[MH][W];
 #pragma unroll
-  for (int s = 0; s < MMAX; ++s)
+  for (int si = 0; si < MH; ++si)
 #pragma unroll
-    for (int j = 0; j < W; ++j) breg[s][j] = s < M ? books[(size_t)s * 256 * W + tid * W + j] : 0.0f;
+    for (int j = 0; j < W; ++j) breg[si][j] = si < ns ? books[(size_t)(sb + si) * 256 * W + c * W + j] : 0.0f;
   const float* qv = Qp + (size_t)q * ld;
-  if constexpr (METRIC == 1) {
-    // the cosine table depends on the query only (ivfpq.rs:1042-1045)
-    for (int j = tid; j < dim; j += 256) sr[j] = qv[j];
-    __syncthreads();
-#pragma unroll
-    for (int s = 0; s < MMAX; ++s) {
-      if (s < M) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int j = 0; j < W; ++j) acc += sr[s * W + j] * breg[s][j];
-        lut[s * 256 + tid] = acc;
+  // residuals of every probe of the group (ivfpq.rs:1052-1054); cosine: the
+  // query once and q.c per probe (ivfpq.rs:1042-1045)
+  const int nres = METRIC == 0 ? np : 1;
+  for (int i = tid; i < nres * dim; i += IVF_SW * 64) {
+    const int pi = i / dim, j = i % dim;
+    srs[pi][j] = METRIC == 0 ? qv[j] - cents[(size_t)probes[(size_t)q * nprobe + p0 + pi] * ld + j] : qv[j];
+  }
+  if (METRIC == 1) {
+    for (int pi = w; pi < np; pi += IVF_SW) {
+      if (lane < 8) {
+        const int l = probes[(size_t)q * nprobe + p0 + pi];
+        const float d = -dist_group8<2>(qv, cents + (size_t)l * ld, dim, lane);
+        if (lane == 0) s_qdc[pi] = d;
       }
     }
   }
-  uint64_t kept = KEY_MAX, thr = KEY_MAX;
-  for (int p = p0; p < p1; ++p) {
-    const int l = probes[(size_t)q * nprobe + p];
-    const float* cv = cents + (size_t)l * ld;
-    __syncthreads();  // previous probe's table no longer read
-    if constexpr (METRIC == 0) {
-      for (int j = tid; j < dim; j += 256) sr[j] = qv[j] - cv[j];  // residual (ivfpq.rs:1052-1054)
-      __syncthreads();
+  auto build = [&](const float* sr) {  // distance_table, product.rs:416-433
 #pragma unroll
-      for (int s = 0; s < MMAX; ++s) {
-        if (s < M) {
-          float acc = 0.0f;  // distance_table, product.rs:416-433
+    for (int si = 0; si < MH; ++si) {
+      if (si < ns) {
+        const int s2 = sb + si;
+        float rv[W];
+        if constexpr (W % 4 == 0) {
 #pragma unroll
-          for (int j = 0; j < W; ++j) {
-            const float d = sr[s * W + j] - breg[s][j];
-            acc += d * d;
+          for (int j = 0; j < W; j += 4) {
+            const float4 r4 = *reinterpret_cast<const float4*>(&sr[s2 * W + j]);
+            rv[j] = r4.x;
+            rv[j + 1] = r4.y;
+            rv[j + 2] = r4.z;
+            rv[j + 3] = r4.w;
           }
-          lut[s * 256 + tid] = acc;
+        } else {
+#pragma unroll
+          for (int j = 0; j < W; ++j) rv[j] = sr[s2 * W + j];
         }
-      }
-    } else {
-      if (tid < 8) {
-        const float d = -dist_group8<2>(qv, cv, dim, tid);
-        if (tid == 0) s_qdc = d;
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < W; ++j) {
+          if constexpr (METRIC == 0) {
+            const float d = rv[j] - breg[si][j];
+            acc += d * d;
+          } else {
+            acc += rv[j] * breg[si][j];
+          }
+        }
+        lut[s2 * 256 + c] = acc;
       }
     }
+  };
+  __syncthreads();
+  if constexpr (METRIC == 1) build(srs[0]);
+  uint64_t kept = KEY_MAX, thr = KEY_MAX;
+  for (int pi = 0; pi < np; ++pi) {
+    const int l = probes[(size_t)q * nprobe + p0 + pi];
+    if constexpr (METRIC == 0) {
+      __syncthreads();  // the previous probe's table is no longer read
+      build(srs[pi]);
+    }
     __syncthreads();
-    const float one_minus_qdc = METRIC == 1 ? 1.0f - s_qdc : 0.0f;
+    const float one_minus_qdc = METRIC == 1 ? 1.0f - s_qdc[pi] : 0.0f;
     const uint32_t begin = list_off[l], end = list_off[l + 1];
-    for (uint32_t e0 = begin + w * 64; e0 < end; e0 += 256) {
+    for (uint32_t e0 = begin + w * 64; e0 < end; e0 += IVF_SW * 64) {
       const uint32_t e = e0 + lane;
       uint64_t key = KEY_MAX;
       if (e < end) {
         const uint32_t rk = list_rank[e];
         if (accept == nullptr || accept[rank_slot[rk]]) {
-          const uint8_t* code = list_codes + (size_t)e * M;
           float sum = 0.0f;  // DistanceTable::squared_l2 / inner_product, product.rs:580-603
           if (M == 16) {
-            const uint4 cw = *reinterpret_cast<const uint4*>(code);
+            const uint4 cw = *reinterpret_cast<const uint4*>(list_codes + (size_t)e * 16);
             const uint32_t wv[4] = {cw.x, cw.y, cw.z, cw.w};
 #pragma unroll
             for (int s2 = 0; s2 < 16; ++s2) sum += lut[s2 * 256 + ((wv[s2 >> 2] >> (8 * (s2 & 3))) & 255)];
           } else {
+            const uint8_t* code = list_codes + (size_t)e * M;
             for (int s2 = 0; s2 < M; ++s2) sum += lut[s2 * 256 + code[s2]];
           }
           const float score = METRIC == 0 ? sum : one_minus_qdc + (-sum);
           key = ((uint64_t)ord_key(score) << 32) | rk;
         }
       }
-      wave_topk_insert(key, kept, thr, kk, lane);
+      wave_topk_add(key, kept, thr, kk, lane);
     }
   }
-  uint64_t* o = out + (((size_t)q * groups + grp) * 4 + w) * kk;
+  uint64_t* o = out + (((size_t)q * groups + grp) * IVF_SW + w) * kk;
   if (lane < kk) o[lane] = kept;
 }
 
@@ -978,19 +1011,23 @@ struct IvfPqIndex {
       PXG_HIP(hipMemsetAsync(scanned_dev, 0, 8, s));
       hipLaunchKernelGGL(ivf_count_scanned, dim3((unsigned)((nq * np + 255) / 256)), dim3(256), 0, s, probes,
                          (int)(nq * np), list_off.p, scanned_dev);
-      const size_t lds = (size_t)M() * 256 * 4;
       const int W = (int)(dim / M());
       const bool reg_path = dim <= 128 && dim % M() == 0 && kk <= 64 && (W == 1 || W == 2 || W == 4 || W == 8 ||
                                                                           W == 16 || W == 32);
       if (reg_path) {
-        const int groups = (np + IVF_PG - 1) / IVF_PG;
-        uint64_t* cand = (uint64_t*)ctx->get(10, (size_t)nq * groups * 4 * kk * 8);
+        const size_t lds = (size_t)M() * 256 * 4;
+        // probes per workgroup: up to IVF_PGMAX, fewer when that would leave
+        // the GPU with under ~2 workgroups per CU
+        int pg = IVF_PGMAX;
+        while (pg > 1 && (int64_t)nq * ((np + pg - 1) / pg) < 512) pg >>= 1;
+        const int groups = (np + pg - 1) / pg;
+        uint64_t* cand = (uint64_t*)ctx->get(10, (size_t)nq * groups * IVF_SW * kk * 8);
         const int grid = (int)(nq * groups);
         tm.mark(1);
 #define PXG_SCANR(WW, MET)                                                                                          \
-  hipLaunchKernelGGL((ivf_scan_reg<WW, MET>), dim3(grid), dim3(256), lds, s, Qp, (int)ld, (int)dim, (int)M(), probes, \
-                     np, groups, cents.p, books.p, list_off.p, list_rank.p, list_codes.p, d_rank_slot.p, d_accept,  \
-                     kk, cand)
+  hipLaunchKernelGGL((ivf_scan_reg<WW, MET>), dim3(grid), dim3(IVF_SW * 64), lds, s, Qp, (int)ld, (int)dim,        \
+                     (int)M(), probes, np, pg, groups, cents.p, books.p, list_off.p, list_rank.p, list_codes.p,      \
+                     d_rank_slot.p, d_accept, kk, cand)
 #define PXG_SCANR_W(MET)                  \
   switch (W) {                            \
     case 1: PXG_SCANR(1, MET); break;     \
@@ -1009,11 +1046,12 @@ struct IvfPqIndex {
 #undef PXG_SCANR
         PXG_HIP(hipGetLastError());
         tm.mark(2);
-        hipLaunchKernelGGL(ivf_merge, dim3((unsigned)nq), dim3(256), 0, s, cand, groups * 4 * kk, kk, (int)k,
+        hipLaunchKernelGGL(ivf_merge, dim3((unsigned)nq), dim3(256), 0, s, cand, groups * IVF_SW * kk, kk, (int)k,
                            rerank ? 1 : 0, Qp, (int)ld, (int)dim, metric, X.p, d_rank_slot.p, d_ids.p, d_oid, d_od,
                            d_oc);
         PXG_HIP(hipGetLastError());
       } else {
+      const size_t lds = (size_t)M() * 256 * 4;
       uint64_t* cand = (uint64_t*)ctx->get(10, (size_t)nq * np * 4 * kk * 8);
       const int grid = (int)(nq * np);
       tm.mark(1);
