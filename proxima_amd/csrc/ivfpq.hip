@@ -370,9 +370,13 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan_reg(const float* __restr
                                                          const uint8_t* __restrict__ list_codes,
                                                          const uint32_t* __restrict__ rank_slot,
                                                          const uint8_t* __restrict__ accept, int kk,
-                                                         uint64_t* __restrict__ out) {
+                                                         uint64_t* __restrict__ out, int k,
+                                                         const uint64_t* __restrict__ ids,
+                                                         uint64_t* __restrict__ out_ids, float* __restrict__ out_d,
+                                                         uint32_t* __restrict__ out_count) {
   constexpr int MMAX = 128 / W, MH = (MMAX + 1) / 2;
-  extern __shared__ float lut[];  // M * 256 floats
+  extern __shared__ float lut[];  // 2 x M * 256 floats (cosine: one table)
+  __shared__ uint64_t s_kept[IVF_SW][64];
   __shared__ __align__(16) float srs[IVF_PGMAX][128];
   __shared__ float s_qdc[IVF_PGMAX];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -405,7 +409,7 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan_reg(const float* __restr
       }
     }
   }
-  auto build = [&](const float* sr) {  // distance_table, product.rs:416-433
+  auto build = [&](const float* sr, float* tab) {  // distance_table, product.rs:416-433
 #pragma unroll
     for (int si = 0; si < MH; ++si) {
       if (si < ns) {
@@ -434,20 +438,22 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan_reg(const float* __restr
             acc += rv[j] * breg[si][j];
           }
         }
-        lut[s2 * 256 + c] = acc;
+        tab[s2 * 256 + c] = acc;
       }
     }
   };
+  // Tables are double-buffered (L2): each wave builds its rows of probe
+  // pi+1's table before scanning its share of probe pi, so building and
+  // scanning overlap across waves and one barrier per probe suffices.
+  const int tsz = M * 256;
   __syncthreads();
-  if constexpr (METRIC == 1) build(srs[0]);
+  build(srs[0], lut);
+  __syncthreads();
   uint64_t kept = KEY_MAX, thr = KEY_MAX;
   for (int pi = 0; pi < np; ++pi) {
     const int l = probes[(size_t)q * nprobe + p0 + pi];
-    if constexpr (METRIC == 0) {
-      __syncthreads();  // the previous probe's table is no longer read
-      build(srs[pi]);
-    }
-    __syncthreads();
+    if (METRIC == 0 && pi + 1 < np) build(srs[pi + 1], lut + ((pi + 1) & 1) * tsz);
+    const float* tab = lut + (METRIC == 0 ? (pi & 1) * tsz : 0);
     const float one_minus_qdc = METRIC == 1 ? 1.0f - s_qdc[pi] : 0.0f;
     const uint32_t begin = list_off[l], end = list_off[l + 1];
     for (uint32_t e0 = begin + w * 64; e0 < end; e0 += IVF_SW * 64) {
@@ -461,10 +467,10 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan_reg(const float* __restr
             const uint4 cw = *reinterpret_cast<const uint4*>(list_codes + (size_t)e * 16);
             const uint32_t wv[4] = {cw.x, cw.y, cw.z, cw.w};
 #pragma unroll
-            for (int s2 = 0; s2 < 16; ++s2) sum += lut[s2 * 256 + ((wv[s2 >> 2] >> (8 * (s2 & 3))) & 255)];
+            for (int s2 = 0; s2 < 16; ++s2) sum += tab[s2 * 256 + ((wv[s2 >> 2] >> (8 * (s2 & 3))) & 255)];
           } else {
             const uint8_t* code = list_codes + (size_t)e * M;
-            for (int s2 = 0; s2 < M; ++s2) sum += lut[s2 * 256 + code[s2]];
+            for (int s2 = 0; s2 < M; ++s2) sum += tab[s2 * 256 + code[s2]];
           }
           const float score = METRIC == 0 ? sum : one_minus_qdc + (-sum);
           key = ((uint64_t)ord_key(score) << 32) | rk;
@@ -472,9 +478,27 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan_reg(const float* __restr
       }
       wave_topk_add(key, kept, thr, kk, lane);
     }
+    __syncthreads();  // table pi+1 complete; table pi free for pi+2
   }
-  uint64_t* o = out + (((size_t)q * groups + grp) * IVF_SW + w) * kk;
-  if (lane < kk) o[lane] = kept;
+  if (out_ids == nullptr) {
+    uint64_t* o = out + (((size_t)q * groups + grp) * IVF_SW + w) * kk;
+    if (lane < kk) o[lane] = kept;
+    return;
+  }
+  // One group per query and no rerank: merge the waves' sorted lists here
+  // (bitonic half-cleaners) and write the query's results.
+  s_kept[w][lane] = kept;
+  __syncthreads();
+  if (w == 0) {
+    uint64_t v = s_kept[0][lane];
+    for (int ww = 1; ww < IVF_SW; ++ww) wave_merge_sorted(v, s_kept[ww][lane], lane);
+    const int n = min(k, (int)__popcll(__ballot(v != KEY_MAX)));
+    if (lane < n) {
+      out_ids[(size_t)q * k + lane] = ids[rank_slot[(uint32_t)v]];
+      out_d[(size_t)q * k + lane] = key_float((uint32_t)(v >> 32));
+    }
+    if (lane == 0) out_count[q] = (uint32_t)n;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1015,7 +1039,7 @@ struct IvfPqIndex {
       const bool reg_path = dim <= 128 && dim % M() == 0 && kk <= 64 && (W == 1 || W == 2 || W == 4 || W == 8 ||
                                                                           W == 16 || W == 32);
       if (reg_path) {
-        const size_t lds = (size_t)M() * 256 * 4;
+        const size_t lds = (size_t)(metric == PXG_COSINE ? 1 : 2) * M() * 256 * 4;
         // probes per workgroup: up to IVF_PGMAX, fewer when that would leave
         // the GPU with under ~2 workgroups per CU
         int pg = IVF_PGMAX;
@@ -1024,10 +1048,12 @@ struct IvfPqIndex {
         uint64_t* cand = (uint64_t*)ctx->get(10, (size_t)nq * groups * IVF_SW * kk * 8);
         const int grid = (int)(nq * groups);
         tm.mark(1);
+        // one group per query and no rerank: the scan writes the results
+        const bool fused = groups == 1 && !rerank;
 #define PXG_SCANR(WW, MET)                                                                                          \
   hipLaunchKernelGGL((ivf_scan_reg<WW, MET>), dim3(grid), dim3(IVF_SW * 64), lds, s, Qp, (int)ld, (int)dim,        \
                      (int)M(), probes, np, pg, groups, cents.p, books.p, list_off.p, list_rank.p, list_codes.p,      \
-                     d_rank_slot.p, d_accept, kk, cand)
+                     d_rank_slot.p, d_accept, kk, cand, (int)k, d_ids.p, fused ? d_oid : nullptr, d_od, d_oc)
 #define PXG_SCANR_W(MET)                  \
   switch (W) {                            \
     case 1: PXG_SCANR(1, MET); break;     \
@@ -1046,10 +1072,12 @@ struct IvfPqIndex {
 #undef PXG_SCANR
         PXG_HIP(hipGetLastError());
         tm.mark(2);
-        hipLaunchKernelGGL(ivf_merge, dim3((unsigned)nq), dim3(256), 0, s, cand, groups * IVF_SW * kk, kk, (int)k,
-                           rerank ? 1 : 0, Qp, (int)ld, (int)dim, metric, X.p, d_rank_slot.p, d_ids.p, d_oid, d_od,
-                           d_oc);
-        PXG_HIP(hipGetLastError());
+        if (!fused) {
+          hipLaunchKernelGGL(ivf_merge, dim3((unsigned)nq), dim3(256), 0, s, cand, groups * IVF_SW * kk, kk, (int)k,
+                             rerank ? 1 : 0, Qp, (int)ld, (int)dim, metric, X.p, d_rank_slot.p, d_ids.p, d_oid, d_od,
+                             d_oc);
+          PXG_HIP(hipGetLastError());
+        }
       } else {
       const size_t lds = (size_t)M() * 256 * 4;
       uint64_t* cand = (uint64_t*)ctx->get(10, (size_t)nq * np * 4 * kk * 8);
@@ -1075,11 +1103,13 @@ struct IvfPqIndex {
       PXG_HIP(hipGetLastError());
       }
     }
-    unsigned long long badv = 0, scanned = 0;
-    PXG_HIP(hipMemcpyAsync(&badv, bad, 8, hipMemcpyDeviceToHost, s));
-    if (scanned_dev) PXG_HIP(hipMemcpyAsync(&scanned, scanned_dev, 8, hipMemcpyDeviceToHost, s));
+    // one copy brings back the validation flag and the scanned-entry count
+    // (bytes 0-7 and 16-23 of the same scratch block)
+    unsigned long long tail[3] = {0, 0, 0};
+    PXG_HIP(hipMemcpyAsync(tail, bad, scanned_dev ? 24 : 8, hipMemcpyDeviceToHost, s));
     PXG_HIP(hipStreamSynchronize(s));
     tm.finish();
+    const unsigned long long badv = tail[0], scanned = scanned_dev ? tail[2] : 0;
     g_last_scanned = scanned;
     if (badv != ~0ull) {
       const uint32_t qi = (uint32_t)(badv >> 32), comp = (uint32_t)badv;
