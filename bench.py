@@ -245,6 +245,74 @@ def bench_sq8(args, torch, px, dev):
     return out
 
 
+def bench_kmeans(args, torch, px, dev):
+    """k-means training (Lloyd): 2,000,000 x 128 f32 from 4,096 Gaussian clusters
+    (centres N(0,1), sigma 0.2) into 4,096 centroids, k-means++ seeding from
+    the seed, 10 Lloyd iterations; then PQ 16 x 256 trained on the residuals
+    (25 iterations per subspace)."""
+    n, dim, K, iters = args.km_n, 128, 4096, 10
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed + 13)
+    centres = torch.randn((K, dim), generator=g, device=dev)
+    cid = torch.randint(0, K, (n,), generator=g, device=dev)
+    x = (centres[cid] + 0.2 * torch.randn((n, dim), generator=g, device=dev)).contiguous()
+    seeds = torch.empty((K, dim), device=dev)
+    cents = torch.empty((K, dim), device=dev)
+    assign = torch.empty(n, dtype=torch.int32, device=dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    px.kmeans_device(x, K, 0, args.seed, seeds)  # k-means++ seeding only
+    t_seed = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    inertia, its = px.kmeans_device(x, K, iters, args.seed, cents, assign, init=seeds)
+    t_lloyd = time.perf_counter() - t0
+    resid = (x - cents[assign.long()]).contiguous()
+    books = torch.empty(dim * 256, device=dev)
+    t0 = time.perf_counter()
+    pq = px.ProductQuantizer.train_device(px.VectorSpace(dim, px.Metric.EUCLIDEAN), resid,
+                                          px.PqConfig(16).with_seed(args.seed), books)
+    t_pq = time.perf_counter() - t0
+    per_iter = t_lloyd / max(its, 1)
+    flops = 2.0 * n * K * dim  # per assignment pass
+    tflops = flops / per_iter / 1e12
+    log(f"[bench] kmeans: seeding {t_seed:.2f}s, {its} Lloyd iterations {t_lloyd:.2f}s ({per_iter * 1e3:.1f} ms each, "
+        f"{tflops:.1f} TFLOP/s by 2nKd), inertia {inertia:.1f}; PQ 16x256 on residuals {t_pq:.2f}s "
+        f"({pq.training_iterations} iterations)")
+    out = {"value": round(1.0 / per_iter, 3), "unit": "Lloyd iterations/s", "ms_per_iteration": round(per_iter * 1e3, 2),
+           "config": {"workload": "k-means 2M x 128 f32 -> 4096, k-means++ then 10 Lloyd iterations; PQ 16x256 on "
+                                  "the residuals", "n": n, "dim": dim, "k": K, "iterations": its},
+           "roofline": {"bound": "valu", "achieved": round(tflops, 2), "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(tflops / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": None,
+                        "note": "2nKd per pass; the exact sequential f32 distance (3 VALU ops per element, no FMA, "
+                                "no MFMA) is the reference's arithmetic"},
+           "seeding_s": round(t_seed, 3), "lloyd_s": round(t_lloyd, 3), "pq_train_s": round(t_pq, 3),
+           "inertia": inertia}
+    if not args.no_cpu:
+        from oracle import oracle as orc
+        ns = args.km_cpu_sample
+        sample = x[:ns].cpu().numpy()
+        init = seeds.cpu().numpy()
+        log(f"[bench] kmeans CPU baseline: oracle assignment pass on {ns} points x {K} centroids, 1 thread")
+        t0 = time.perf_counter()
+        orc.kmeans_assign(sample, init)
+        cpu_s = time.perf_counter() - t0
+        cpu_iter = cpu_s * n / ns
+        # full-size parity of the assignment pass on a slice: GPU kernel vs oracle, final centroids
+        m = 4096
+        ch = cents.cpu().numpy()
+        ga, gd = px.kmeans_assign(x[:m].cpu().numpy(), ch)
+        wa, wd = orc.kmeans_assign(x[:m].cpu().numpy(), ch)
+        same = int(np.sum((ga == wa) & (gd.view(np.uint32) == wd.view(np.uint32))))
+        out["cpu_baseline"] = {"value": round(1.0 / cpu_iter, 6), "unit": "Lloyd iterations/s", "cores": 1,
+                               "kind": "port", "sample": f"the assignment pass of one Lloyd iteration (kmeans.rs:90-97 "
+                                                         f"restatement, single thread as the reference; the O(n d) "
+                                                         f"update is left out) on {ns} of the {n} points against the "
+                                                         f"{K} seeds: {cpu_s:.2f}s, scaled by n/{ns}"}
+        out["parity_sample"] = {"points": m, "assignments_and_distances_bit_exact": same}
+        log(f"[bench] kmeans CPU {cpu_iter:.1f} s per full iteration (1 core); assignment parity {same}/{m}")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -268,6 +336,10 @@ def main():
     ap.add_argument("--sq8-n", type=int, default=10_000_000)
     ap.add_argument("--sq8-steps", type=int, default=20)
     ap.add_argument("--sq8-cpu-sample", type=int, default=2048)
+    ap.add_argument("--skip-kmeans", action="store_true")
+    ap.add_argument("--kmeans-only", action="store_true", help="run only the k-means leg (prints its JSON object)")
+    ap.add_argument("--km-n", type=int, default=2_000_000)
+    ap.add_argument("--km-cpu-sample", type=int, default=16384)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also run one device copy of this size (a known-size kernel for scaling PMC byte counters)")
     args = ap.parse_args()
@@ -288,6 +360,9 @@ def main():
         return
     if args.sq8_only:
         print(json.dumps(bench_sq8(args, torch, px, dev)), flush=True)
+        return
+    if args.kmeans_only:
+        print(json.dumps(bench_kmeans(args, torch, px, dev)), flush=True)
         return
     n, dim, B = args.n, args.dim, args.batch
     log(f"[bench] generating {n}x{dim} corpus + {args.queries} queries on the GPU")
@@ -390,6 +465,10 @@ def main():
     sq8 = None
     if not args.skip_sq8:
         sq8 = bench_sq8(args, torch, px, dev)
+        torch.cuda.empty_cache()
+    km = None
+    if not args.skip_kmeans:
+        km = bench_kmeans(args, torch, px, dev)
 
     out = {
         "metric": METRIC,
@@ -419,6 +498,7 @@ def main():
         "parity_sample": parity,
         "ivfpq": ivf,
         "sq8": sq8,
+        "kmeans": km,
     }
     print(json.dumps(out), flush=True)
 

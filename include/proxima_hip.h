@@ -247,6 +247,11 @@ int pxg_kmeans_assign(const float* points, uint64_t n, uint32_t dim, const float
  * subspace, 256 rows of its width (dim floats x 256 in total). */
 int pxg_pq_train(const float* training, uint64_t n, uint32_t dim, uint64_t subspaces, uint64_t max_iterations,
                  uint64_t seed, float* codebooks_out, double* inertia, uint64_t* iterations);
+/* pxg_pq_train with the training vectors and the codebooks in device memory
+ * (training values are taken as finite: device data is not scanned). */
+int pxg_pq_train_device(const float* d_training, uint64_t n, uint32_t dim, uint64_t subspaces,
+                        uint64_t max_iterations, uint64_t seed, float* d_codebooks_out, double* inertia,
+                        uint64_t* iterations);
 /* ProductQuantizer::encode_into (product.rs:361-380) for n vectors. */
 int pxg_pq_encode(const float* codebooks, uint32_t dim, uint64_t subspaces, const float* vectors, uint64_t n,
                   uint8_t* codes_out);

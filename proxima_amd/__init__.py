@@ -656,6 +656,21 @@ def kmeans_lloyd(points, init, max_iterations):
     return cents, assign, inertia.value, iters.value
 
 
+def kmeans_device(points, k, max_iterations, seed, centroids_out, assign_out=None, init=None):
+    """kmeans() on device-resident data: points a contiguous GPU tensor
+    [n, dim] f32, centroids_out [min(k, n), dim] f32 and assign_out [n]
+    (int32, may be None) GPU tensors, init None (k-means++ from seed) or a GPU
+    tensor of initial centroids. max_iterations = 0 returns the k-means++
+    seeds. Returns (inertia, iterations)."""
+    n, dim = points.shape
+    inertia, iters = C.c_double(), C.c_uint64()
+    _check(_lib.pxg_kmeans_device(_device_ptr(points), n, dim, k, max_iterations, seed,
+                                  None if init is None else _device_ptr(init), _device_ptr(centroids_out),
+                                  None if assign_out is None else _device_ptr(assign_out), C.byref(inertia),
+                                  C.byref(iters)))
+    return inertia.value, iters.value
+
+
 def kmeans_pp(points, k, seed):
     p = np.ascontiguousarray(points, dtype=np.float32)
     n, dim = p.shape
@@ -708,6 +723,18 @@ class ProductQuantizer:
                                  _ptr(books), C.byref(inertia), C.byref(iters)))
         return cls(space.dim, config.subspaces, books, inertia.value, iters.value)
 
+    @classmethod
+    def train_device(cls, space, training, config, codebooks_out):
+        """train() on a contiguous GPU tensor [n, dim]; the codebooks (dim * 256
+        f32) are written to the GPU tensor codebooks_out and kept on the host too."""
+        if training.shape[-1] != space.dim or training.shape[0] == 0:
+            raise _config("training", int(training.numel()), "must be a non-empty multiple of the space dimension")
+        inertia, iters = C.c_double(), C.c_uint64()
+        _check(_lib.pxg_pq_train_device(_device_ptr(training), training.shape[0], space.dim, config.subspaces,
+                                        config.max_iterations, config.seed, _device_ptr(codebooks_out),
+                                        C.byref(inertia), C.byref(iters)))
+        return cls(space.dim, config.subspaces, codebooks_out.cpu().numpy().reshape(-1), inertia.value, iters.value)
+
     def code_len(self):
         return self.subspaces
 
@@ -721,7 +748,7 @@ class ProductQuantizer:
         return out
 
 
-__all__ += ["IvfPqConfig", "IvfPqIndex", "TrainingReport", "Clustering", "kmeans", "kmeans_lloyd", "kmeans_pp",
+__all__ += ["IvfPqConfig", "IvfPqIndex", "TrainingReport", "Clustering", "kmeans", "kmeans_device", "kmeans_lloyd", "kmeans_pp",
             "kmeans_assign", "PqConfig", "ProductQuantizer"]
 
 

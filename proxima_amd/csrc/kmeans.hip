@@ -733,6 +733,31 @@ int pxg_kmeans_assign(const float* points, uint64_t n, uint32_t dim, const float
   });
 }
 
+int pxg_pq_train_device(const float* d_training, uint64_t n, uint32_t dim, uint64_t subspaces,
+                        uint64_t max_iterations, uint64_t seed, float* d_codebooks_out, double* inertia,
+                        uint64_t* iterations) {
+  return pxg::guard([&] {
+    // ProductQuantizer::train validation (product.rs:200-223); the values
+    // are not scanned for non-finite entries here (device data)
+    if (subspaces == 0 || subspaces > dim) pxg::config_error("subspaces", subspaces, "must be between 1 and the space dimension");
+    if (max_iterations == 0) pxg::config_error("max_iterations", max_iterations, "must be at least 1");
+    if (n == 0) pxg::config_error("training", 0, "must be a non-empty multiple of the space dimension");
+    pxg::PqLayout L;
+    L.build((int)dim, (int)subspaces);
+    hipStream_t s;
+    PXG_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    struct SG {
+      hipStream_t s;
+      ~SG() { (void)hipStreamDestroy(s); }
+    } sg{s};
+    size_t its = 0;
+    pxg::pq_train_device(d_training, n, (int)dim, (int)dim, L, max_iterations, seed, d_codebooks_out, inertia, &its,
+                         s);
+    PXG_HIP(hipStreamSynchronize(s));
+    if (iterations) *iterations = its;
+  });
+}
+
 int pxg_pq_train(const float* training, uint64_t n, uint32_t dim, uint64_t subspaces, uint64_t max_iterations,
                  uint64_t seed, float* codebooks_out, double* inertia, uint64_t* iterations) {
   return pxg::guard([&] {
