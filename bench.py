@@ -324,7 +324,7 @@ def main():
     ap.add_argument("--batch", type=int, default=1024)
     ap.add_argument("--k", type=int, default=10)
     ap.add_argument("--seed", type=int, default=0x9E3779B9)
-    ap.add_argument("--cpu-sample", type=int, default=256)
+    ap.add_argument("--cpu-sample", type=int, default=2048)
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--skip-ivfpq", action="store_true")
@@ -339,7 +339,7 @@ def main():
     ap.add_argument("--skip-kmeans", action="store_true")
     ap.add_argument("--kmeans-only", action="store_true", help="run only the k-means leg (prints its JSON object)")
     ap.add_argument("--km-n", type=int, default=2_000_000)
-    ap.add_argument("--km-cpu-sample", type=int, default=16384)
+    ap.add_argument("--km-cpu-sample", type=int, default=131072)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also run one device copy of this size (a known-size kernel for scaling PMC byte counters)")
     args = ap.parse_args()
