@@ -502,6 +502,290 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan_reg(const float* __restr
 }
 
 // ---------------------------------------------------------------------------
+// ADC scan for 16 subspaces (16-byte codes), the common IVF-PQ shape: the
+// same work split as ivf_scan_reg, with the list stream staged through LDS
+// by the waves' own asynchronous loads so that HBM latency is hidden without
+// holding the data in VGPRs.
+//
+// Each wave owns a ring of IVF_NS chunk slots (64 entries: 1 KiB of codes +
+// 256 B of id ranks) and walks the group's (probe, 64-entry chunk) sequence
+// twice: a producer cursor issues global->LDS copies (global_load_lds,
+// vmcnt-tracked) up to IVF_NS chunks ahead, refilling each slot as soon as it
+// has been read, and the consumer cursor waits for its chunk with s_waitcnt
+// vmcnt and scores it. The copies cross probe boundaries (they
+// need no table), so the stream does not drain at the per-probe barrier.
+// Tables live at fixed LDS offsets (the probe loop is unrolled by two for the
+// double buffer), so every lookup is one SDWA byte-select shift plus one
+// ds_read_b32 with an immediate offset.
+// ---------------------------------------------------------------------------
+constexpr int IVF_NS = 3;                       // staged chunks per wave (all in flight)
+constexpr int IVF_CHUNK = 64 * 16 + 64 * 4;     // codes + ranks of 64 entries
+
+typedef __attribute__((address_space(3))) uint8_t lds_byte;
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const lds_byte*)p;
+}
+
+// Global -> LDS copies; lane i's data lands at m0 + 16*i (dwordx4) or m0 + 4*i
+// (dword); lanes off in exec copy nothing. Written as inline asm so that the
+// compiler neither sees LDS writes pending behind vmcnt (it would drain them
+// with vmcnt(0) at every barrier) nor schedules around them: the consumer
+// waits with an explicit vmcnt. The asm sets m0 itself; the kernels that use
+// these copies keep no value of their own in m0 (no dynamic register
+// indexing, no LDS-DMA builtins, no messages), so the clobber of the
+// reserved register is harmless there.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_copy16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_copy4(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(g) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N <= 15, "immediate vmcnt");
+  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else if constexpr (N == 2) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+  else if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  else if constexpr (N == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+  else static_assert(N == 0, "unsupported count");
+}
+
+// Byte B of x times 4 (the byte offset of a table entry): one SDWA shift.
+template <int B>
+__device__ __forceinline__ uint32_t byte_x4(uint32_t x) {
+  uint32_t r;
+  if constexpr (B == 0)
+    asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+        : "=v"(r) : "v"(x));
+  else if constexpr (B == 1)
+    asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
+        : "=v"(r) : "v"(x));
+  else if constexpr (B == 2)
+    asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
+        : "=v"(r) : "v"(x));
+  else
+    asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
+        : "=v"(r) : "v"(x));
+  return r;
+}
+
+template <int S>
+__device__ __forceinline__ float lut_at(const float* tab, const uint32_t (&wv)[4]) {
+  return *reinterpret_cast<const float*>(reinterpret_cast<const char*>(tab) + S * 1024 +
+                                         byte_x4<S & 3>(wv[S >> 2]));
+}
+
+// DistanceTable::squared_l2 / inner_product (product.rs:580-603) over one
+// 16-byte code: sum = 0.0 + t0 + t1 + ... + t15 in subspace order. Table
+// entries are never -0.0 (each starts from +0.0), so starting the sum at t0
+// gives the same bits as adding t0 to 0.0.
+__device__ __forceinline__ float adc16(const float* tab, const uint4& cw) {
+  const uint32_t wv[4] = {cw.x, cw.y, cw.z, cw.w};
+  float s = lut_at<0>(tab, wv);
+  s += lut_at<1>(tab, wv);
+  s += lut_at<2>(tab, wv);
+  s += lut_at<3>(tab, wv);
+  s += lut_at<4>(tab, wv);
+  s += lut_at<5>(tab, wv);
+  s += lut_at<6>(tab, wv);
+  s += lut_at<7>(tab, wv);
+  s += lut_at<8>(tab, wv);
+  s += lut_at<9>(tab, wv);
+  s += lut_at<10>(tab, wv);
+  s += lut_at<11>(tab, wv);
+  s += lut_at<12>(tab, wv);
+  s += lut_at<13>(tab, wv);
+  s += lut_at<14>(tab, wv);
+  s += lut_at<15>(tab, wv);
+  return s;
+}
+
+template <int W, int METRIC>
+__global__ __launch_bounds__(IVF_SW * 64) void ivf_scan16(const float* __restrict__ Qp, int ld,
+                                                          const int* __restrict__ probes, int nprobe, int pg,
+                                                          int groups, const float* __restrict__ cents,
+                                                          const float* __restrict__ books,
+                                                          const uint32_t* __restrict__ list_off,
+                                                          const uint32_t* __restrict__ list_rank,
+                                                          const uint8_t* __restrict__ list_codes,
+                                                          const uint32_t* __restrict__ rank_slot,
+                                                          const uint8_t* __restrict__ accept, int kk,
+                                                          uint64_t* __restrict__ out, int k,
+                                                          const uint64_t* __restrict__ ids,
+                                                          uint64_t* __restrict__ out_ids, float* __restrict__ out_d,
+                                                          uint32_t* __restrict__ out_count) {
+  constexpr int M = 16, DIM = 16 * W, MH = 8, NT = METRIC == 0 ? 2 : 1;
+  __shared__ __align__(16) float tabs[NT][M * 256];
+  __shared__ __align__(16) float srs[IVF_PGMAX][DIM];
+  __shared__ float s_qdc[IVF_PGMAX];
+  __shared__ uint32_t s_lb[IVF_PGMAX], s_le[IVF_PGMAX];  // the group's list ranges
+  __shared__ __align__(16) uint8_t ring[IVF_SW][IVF_NS][IVF_CHUNK];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = tid & 255, sb = (tid >> 8) * MH;  // centroid row, first subspace of this thread
+  const int q = blockIdx.x / groups, grp = blockIdx.x % groups;
+  const int p0 = grp * pg, np = min(nprobe, p0 + pg) - p0;
+  const int* pq = probes + (size_t)q * nprobe + p0;
+  float breg[MH][W];
+#pragma unroll
+  for (int si = 0; si < MH; ++si)
+#pragma unroll
+    for (int j = 0; j < W; ++j) breg[si][j] = books[(size_t)(sb + si) * 256 * W + c * W + j];
+  const float* qv = Qp + (size_t)q * ld;
+  // residuals of the group's probes (ivfpq.rs:1052-1054); cosine: the query
+  // once and q.c per probe (ivfpq.rs:1042-1045)
+  const int nres = METRIC == 0 ? np : 1;
+  for (int i = tid; i < nres * DIM; i += IVF_SW * 64) {
+    const int pi = i / DIM, j = i % DIM;
+    srs[pi][j] = METRIC == 0 ? qv[j] - cents[(size_t)pq[pi] * ld + j] : qv[j];
+  }
+  if (tid < np) {
+    s_lb[tid] = list_off[pq[tid]];
+    s_le[tid] = list_off[pq[tid] + 1];
+  }
+  if (METRIC == 1) {
+    for (int pi = w; pi < np; pi += IVF_SW) {
+      if (lane < 8) {
+        const float d = -dist_group8<2>(qv, cents + (size_t)pq[pi] * ld, DIM, lane);
+        if (lane == 0) s_qdc[pi] = d;
+      }
+    }
+  }
+  auto build = [&](const float* sr, float* tab) {  // distance_table, product.rs:416-433
+#pragma unroll
+    for (int si = 0; si < MH; ++si) {
+      float rv[W];
+      if constexpr (W % 4 == 0) {
+#pragma unroll
+        for (int j = 0; j < W; j += 4) {
+          const float4 r4 = *reinterpret_cast<const float4*>(&sr[(sb + si) * W + j]);
+          rv[j] = r4.x;
+          rv[j + 1] = r4.y;
+          rv[j + 2] = r4.z;
+          rv[j + 3] = r4.w;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < W; ++j) rv[j] = sr[(sb + si) * W + j];
+      }
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < W; ++j) {
+        if constexpr (METRIC == 0) {
+          const float d = rv[j] - breg[si][j];
+          acc += d * d;
+        } else {
+          acc += rv[j] * breg[si][j];
+        }
+      }
+      tab[(sb + si) * 256 + c] = acc;
+    }
+  };
+
+  // Cursors over this wave's chunks of the group: chunk (p, e) covers
+  // entries e .. e+63 of probe p's list (e advances by 512, the group's
+  // stride); seek moves past exhausted lists.
+  auto open = [&](int p, uint32_t& e, uint32_t& end) {
+    e = __builtin_amdgcn_readfirstlane(s_lb[p]) + (uint32_t)w * 64;
+    end = __builtin_amdgcn_readfirstlane(s_le[p]);
+  };
+  auto seek = [&](int& p, uint32_t& e, uint32_t& end) {
+    while (p < np && e >= end)
+      if (++p < np) open(p, e, end);
+  };
+  __syncthreads();
+  int pp = 0, cp;
+  uint32_t pe, pend, ce, cend;
+  open(0, pe, pend);
+  seek(pp, pe, pend);
+  cp = pp;
+  ce = pe;
+  cend = pend;
+  int issued = 0, consumed = 0;
+  uint8_t* myring = &ring[w][0][0];
+  auto issue = [&]() {
+    uint8_t* slot = myring + (issued % IVF_NS) * IVF_CHUNK;
+    const uint32_t e = pe + lane;
+    const uint32_t a = __builtin_amdgcn_readfirstlane(lds_addr(slot));
+    if (e < pend) {
+      lds_copy16(list_codes + (size_t)e * 16, a);
+      lds_copy4(list_rank + e, a + 1024);
+    }
+    ++issued;
+    pe += IVF_SW * 64;
+    seek(pp, pe, pend);
+  };
+  for (int i = 0; i < IVF_NS - 1 && pp < np; ++i) issue();
+  build(srs[0], tabs[0]);
+  __syncthreads();
+  uint64_t kept = KEY_MAX, thr = KEY_MAX;
+  auto probe_step = [&](auto bc, int pi) {
+    constexpr int B = decltype(bc)::value;
+    if (METRIC == 0 && pi + 1 < np) build(srs[pi + 1], tabs[METRIC == 0 ? (B ^ 1) : 0]);
+    const float* tab = tabs[METRIC == 0 ? B : 0];
+    const float one_minus_qdc = METRIC == 1 ? 1.0f - s_qdc[pi] : 0.0f;
+    while (cp == pi) {
+      // refill the slot read in the previous iteration (its reads are done),
+      // then wait for this chunk; the chunks issued after it stay in flight
+      if (pp < np) issue();
+      const int later = issued - consumed - 1;
+      if (later >= 2) vm_wait<4>();
+      else if (later == 1) vm_wait<2>();
+      else vm_wait<0>();
+      const uint8_t* slot = myring + (consumed % IVF_NS) * IVF_CHUNK;
+      const uint4 cw = *reinterpret_cast<const uint4*>(slot + lane * 16);
+      const uint32_t rk = *reinterpret_cast<const uint32_t*>(slot + 1024 + lane * 4);
+      const bool valid = ce + lane < cend;
+      ++consumed;
+      ce += IVF_SW * 64;
+      seek(cp, ce, cend);
+      uint64_t key = KEY_MAX;
+      if (valid && (accept == nullptr || accept[rank_slot[rk]])) {
+        const float sum = adc16(tab, cw);
+        if constexpr (METRIC == 0) {
+          // sums of squares are in [+0, +inf]: the order key is the bits with
+          // the sign bit set
+          key = ((uint64_t)(__float_as_uint(sum) | 0x80000000u) << 32) | rk;
+        } else {
+          key = ((uint64_t)ord_key(one_minus_qdc + (-sum)) << 32) | rk;
+        }
+      }
+      wave_topk_add(key, kept, thr, kk, lane);
+    }
+    __syncthreads();  // table pi+1 complete; table pi free for pi+2
+  };
+  for (int pi = 0; pi < np; pi += 2) {
+    probe_step(std::integral_constant<int, 0>{}, pi);
+    if (pi + 1 < np) probe_step(std::integral_constant<int, 1>{}, pi + 1);
+  }
+  if (out_ids == nullptr) {
+    uint64_t* o = out + (((size_t)q * groups + grp) * IVF_SW + w) * kk;
+    if (lane < kk) o[lane] = kept;
+    return;
+  }
+  // One group per query and no rerank: merge the waves' sorted lists here
+  // and write the query's results. Every copy has landed (the last chunk was
+  // waited with vmcnt(0)), so the rings are free.
+  uint64_t* s_kept = reinterpret_cast<uint64_t*>(&ring[0][0][0]);
+  s_kept[w * 64 + lane] = kept;
+  __syncthreads();
+  if (w == 0) {
+    uint64_t v = s_kept[lane];
+    for (int ww = 1; ww < IVF_SW; ++ww) wave_merge_sorted(v, s_kept[ww * 64 + lane], lane);
+    const int n = min(k, (int)__popcll(__ballot(v != KEY_MAX)));
+    if (lane < n) {
+      out_ids[(size_t)q * k + lane] = ids[rank_slot[(uint32_t)v]];
+      out_d[(size_t)q * k + lane] = key_float((uint32_t)(v >> 32));
+    }
+    if (lane == 0) out_count[q] = (uint32_t)n;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // merge over probes (+ optional exact rerank)
 // ---------------------------------------------------------------------------
 constexpr int IVF_MAX_SHORT = 960;
@@ -1036,8 +1320,12 @@ struct IvfPqIndex {
       hipLaunchKernelGGL(ivf_count_scanned, dim3((unsigned)((nq * np + 255) / 256)), dim3(256), 0, s, probes,
                          (int)(nq * np), list_off.p, scanned_dev);
       const int W = (int)(dim / M());
-      const bool reg_path = dim <= 128 && dim % M() == 0 && kk <= 64 && (W == 1 || W == 2 || W == 4 || W == 8 ||
-                                                                          W == 16 || W == 32);
+      // the register-codebook scans keep two distance tables in LDS (one for
+      // cosine): an L2 index with 128 subspaces takes the general scan
+      const bool reg_path = dim <= 128 && dim % M() == 0 && kk <= 64 &&
+                            (W == 1 || W == 2 || W == 4 || W == 8 || W == 16 || W == 32) &&
+                            (metric == PXG_COSINE || M() <= 64);
+      const bool staged16 = reg_path && M() == 16;
       if (reg_path) {
         const size_t lds = (size_t)(metric == PXG_COSINE ? 1 : 2) * M() * 256 * 4;
         // probes per workgroup: up to IVF_PGMAX, fewer when that would leave
@@ -1063,11 +1351,30 @@ struct IvfPqIndex {
     case 16: PXG_SCANR(16, MET); break;   \
     default: PXG_SCANR(32, MET); break;   \
   }
-        if (metric == PXG_COSINE) {
+#define PXG_SCAN16(WW, MET)                                                                                         \
+  hipLaunchKernelGGL((ivf_scan16<WW, MET>), dim3(grid), dim3(IVF_SW * 64), 0, s, Qp, (int)ld, probes, np, pg, groups, \
+                     cents.p, books.p, list_off.p, list_rank.p, list_codes.p, d_rank_slot.p, d_accept, kk, cand,     \
+                     (int)k, d_ids.p, fused ? d_oid : nullptr, d_od, d_oc)
+#define PXG_SCAN16_W(MET)                 \
+  switch (W) {                            \
+    case 1: PXG_SCAN16(1, MET); break;    \
+    case 2: PXG_SCAN16(2, MET); break;    \
+    case 4: PXG_SCAN16(4, MET); break;    \
+    default: PXG_SCAN16(8, MET); break;   \
+  }
+        if (staged16) {
+          if (metric == PXG_COSINE) {
+            PXG_SCAN16_W(1)
+          } else {
+            PXG_SCAN16_W(0)
+          }
+        } else if (metric == PXG_COSINE) {
           PXG_SCANR_W(1)
         } else {
           PXG_SCANR_W(0)
         }
+#undef PXG_SCAN16_W
+#undef PXG_SCAN16
 #undef PXG_SCANR_W
 #undef PXG_SCANR
         PXG_HIP(hipGetLastError());

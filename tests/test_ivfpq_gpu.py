@@ -306,3 +306,54 @@ def test_coarse_selection_many_lists(gpu, dim, nlist, nq):
     for nprobe in (1, 33, 64):
         want = orc.ivf_search(0, cents, books, codes, list_of, np.arange(n), q, 10, nprobe, m, threads=8)
         assert_same(idx.search_batch(q, 10, nprobe=nprobe), want)
+
+
+@pytest.mark.parametrize("dim", [16, 64, 128])
+@pytest.mark.parametrize("metric", [0, 1])
+def test_sixteen_subspace_scan_long_lists(gpu, dim, metric):
+    """16 subspaces take the LDS-staged scan: lists of ~2500 entries (several
+    64-entry chunks per wave and probe, chunks streamed across probe
+    boundaries), query counts that give one probe group per query (results
+    written by the scan) and several groups (merged afterwards), removals and
+    a filter."""
+    px = gpu
+    n, nlist, m = 20000, 8, 16
+    rng = np.random.default_rng(dim + metric)
+    data = corpus(n, dim, 16) + rng.standard_normal((n, dim)).astype(np.float32) * 0.4
+    prep = orc.prepare_rows(metric, data)
+    cents, books, _ = orc.ivf_train(prep, nlist, m, max_iter=3, seed=4)
+    codes, list_of = orc.ivf_encode(prep, cents, books, m)
+    idx = build(px, data, px.IvfPqConfig(nlist, m).with_train_threshold(1 << 62), metric)
+    idx.load_trained(cents, books, codes, list_of)
+    live = np.ones(n, np.uint8)
+    for i in range(5, n, 11):
+        idx.remove(i)
+        live[i] = 0
+    for nq in (5, 600):
+        q = data[rng.integers(0, n, nq)] + np.float32(0.03)
+        qp = orc.prepare_rows(metric, q)
+        for nprobe, k in ((3, 10), (8, 64)):
+            want = orc.ivf_search(metric, cents, books, codes, list_of, np.arange(n), qp, k, nprobe, m, live=live,
+                                  threads=8)
+            assert_same(idx.search_batch(q, k, nprobe=nprobe), want)
+    q = data[:40] - np.float32(0.02)
+    qp = orc.prepare_rows(metric, q)
+    acc = np.array([i % 4 != 1 for i in range(n)], np.uint8)
+    want = orc.ivf_search(metric, cents, books, codes, list_of, np.arange(n), qp, 10, 5, m, live=live, accept=acc,
+                          threads=8)
+    assert_same(idx.search_batch(q, 10, lambda i, _m: i % 4 != 1, nprobe=5), want)
+
+
+def test_l2_one_dimension_subspaces_take_the_general_scan(gpu):
+    """128 one-wide subspaces: two L2 tables would not fit in LDS, so the
+    general scan serves them."""
+    px = gpu
+    n, dim, nlist, m = 1500, 128, 4, 128
+    data = corpus(n, dim, 12) + np.random.default_rng(8).standard_normal((n, dim)).astype(np.float32) * 0.2
+    cents, books, _ = orc.ivf_train(data, nlist, m, max_iter=2, seed=1)
+    codes, list_of = orc.ivf_encode(data, cents, books, m)
+    idx = build(px, data, px.IvfPqConfig(nlist, m).with_train_threshold(1 << 62))
+    idx.load_trained(cents, books, codes, list_of)
+    q = data[::150] + np.float32(0.01)
+    want = orc.ivf_search(0, cents, books, codes, list_of, np.arange(n), q, 10, 2, m, threads=8)
+    assert_same(idx.search_batch(q, 10, nprobe=2), want)
