@@ -626,15 +626,18 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan16(const float* __restric
   __shared__ __align__(16) uint8_t ring[IVF_SW][IVF_NS][IVF_CHUNK];
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int c = tid & 255, sb = (tid >> 8) * MH;  // centroid row, first subspace of this thread
+  // thread t builds subspace ts = t/32 of every table, centroid rows
+  // t%32 + 32*(i ^ (ts&1)), i < 8: one residual slice per table, and the two
+  // half-waves (even and odd subspace) write distinct banks at every store
+  const int ts = tid >> 5, g = tid & 31, flip = ts & 1;
   const int q = blockIdx.x / groups, grp = blockIdx.x % groups;
   const int p0 = grp * pg, np = min(nprobe, p0 + pg) - p0;
   const int* pq = probes + (size_t)q * nprobe + p0;
   float breg[MH][W];
 #pragma unroll
-  for (int si = 0; si < MH; ++si)
+  for (int i = 0; i < MH; ++i)
 #pragma unroll
-    for (int j = 0; j < W; ++j) breg[si][j] = books[(size_t)(sb + si) * 256 * W + c * W + j];
+    for (int j = 0; j < W; ++j) breg[i][j] = books[((size_t)ts * 256 + g + 32 * (i ^ flip)) * W + j];
   const float* qv = Qp + (size_t)q * ld;
   // residuals of the group's probes (ivfpq.rs:1052-1054); cosine: the query
   // once and q.c per probe (ivfpq.rs:1042-1045)
@@ -655,36 +658,52 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan16(const float* __restric
       }
     }
   }
-  auto build = [&](const float* sr, float* tab) {  // distance_table, product.rs:416-433
+  // distance_table (product.rs:416-433): per entry, in dimension order,
+  // d = r - c; l2 += d*d (ip += r*c). The L2 sum starts at d0*d0, which is
+  // what 0.0 + d0*d0 gives (a square is never -0.0); the inner product keeps
+  // the 0.0 start, which turns a -0.0 first product into +0.0.
+  auto load_slice = [&](const float* sr, float (&rv)[W]) {
+    if constexpr (W % 4 == 0) {
 #pragma unroll
-    for (int si = 0; si < MH; ++si) {
-      float rv[W];
-      if constexpr (W % 4 == 0) {
-#pragma unroll
-        for (int j = 0; j < W; j += 4) {
-          const float4 r4 = *reinterpret_cast<const float4*>(&sr[(sb + si) * W + j]);
-          rv[j] = r4.x;
-          rv[j + 1] = r4.y;
-          rv[j + 2] = r4.z;
-          rv[j + 3] = r4.w;
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < W; ++j) rv[j] = sr[(sb + si) * W + j];
+      for (int j = 0; j < W; j += 4) {
+        const float4 r4 = *reinterpret_cast<const float4*>(&sr[ts * W + j]);
+        rv[j] = r4.x;
+        rv[j + 1] = r4.y;
+        rv[j + 2] = r4.z;
+        rv[j + 3] = r4.w;
       }
-      float acc = 0.0f;
+    } else {
 #pragma unroll
-      for (int j = 0; j < W; ++j) {
-        if constexpr (METRIC == 0) {
-          const float d = rv[j] - breg[si][j];
-          acc += d * d;
-        } else {
-          acc += rv[j] * breg[si][j];
-        }
-      }
-      tab[(sb + si) * 256 + c] = acc;
+      for (int j = 0; j < W; ++j) rv[j] = sr[ts * W + j];
     }
   };
+  // entries I .. I+N-1 of this thread's share of a table
+  auto build_part = [&](auto ic, auto nc, const float (&rv)[W], float* tab) {
+    constexpr int I = decltype(ic)::value, N = decltype(nc)::value;
+#pragma unroll
+    for (int i = I; i < I + N; ++i) {
+      float acc;
+      if constexpr (METRIC == 0) {
+        const float d0 = rv[0] - breg[i][0];
+        acc = d0 * d0;
+#pragma unroll
+        for (int j = 1; j < W; ++j) {
+          const float d = rv[j] - breg[i][j];
+          acc += d * d;
+        }
+      } else {
+        acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < W; ++j) acc += rv[j] * breg[i][j];
+      }
+      tab[ts * 256 + g + 32 * (i ^ flip)] = acc;
+    }
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I2 = std::integral_constant<int, 2>;
+  using I4 = std::integral_constant<int, 4>;
+  using I6 = std::integral_constant<int, 6>;
+  using I8 = std::integral_constant<int, 8>;
 
   // Cursors over this wave's chunks of the group: chunk (p, e) covers
   // entries e .. e+63 of probe p's list (e advances by 512, the group's
@@ -720,42 +739,62 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan16(const float* __restric
     seek(pp, pe, pend);
   };
   for (int i = 0; i < IVF_NS - 1 && pp < np; ++i) issue();
-  build(srs[0], tabs[0]);
+  {
+    float rv[W];
+    load_slice(srs[0], rv);
+    build_part(I0{}, I8{}, rv, tabs[0]);
+  }
   __syncthreads();
   uint64_t kept = KEY_MAX, thr = KEY_MAX;
+  // One consumer iteration: refill the slot read in the previous iteration
+  // (its reads are done), wait for this chunk (the chunks issued after it
+  // stay in flight), score it and keep the wave's best.
+  auto chunk = [&](const float* tab, float one_minus_qdc) {
+    if (pp < np) issue();
+    const int later = issued - consumed - 1;
+    if (later >= 2) vm_wait<4>();
+    else if (later == 1) vm_wait<2>();
+    else vm_wait<0>();
+    const uint8_t* slot = myring + (consumed % IVF_NS) * IVF_CHUNK;
+    const uint4 cw = *reinterpret_cast<const uint4*>(slot + lane * 16);
+    const uint32_t rk = *reinterpret_cast<const uint32_t*>(slot + 1024 + lane * 4);
+    const bool valid = ce + lane < cend;
+    ++consumed;
+    ce += IVF_SW * 64;
+    seek(cp, ce, cend);
+    uint64_t key = KEY_MAX;
+    if (valid && (accept == nullptr || accept[rank_slot[rk]])) {
+      const float sum = adc16(tab, cw);
+      if constexpr (METRIC == 0) {
+        // sums of squares are in [+0, +inf]: the order key is the bits with
+        // the sign bit set
+        key = ((uint64_t)(__float_as_uint(sum) | 0x80000000u) << 32) | rk;
+      } else {
+        key = ((uint64_t)ord_key(one_minus_qdc + (-sum)) << 32) | rk;
+      }
+    }
+    wave_topk_add(key, kept, thr, kk, lane);
+  };
+  // Probe pi scans table B while building table B^1 for probe pi+1 (L2),
+  // two entries per thread between the first chunks so that the build's VALU
+  // work overlaps the lookups' LDS latency.
   auto probe_step = [&](auto bc, int pi) {
     constexpr int B = decltype(bc)::value;
-    if (METRIC == 0 && pi + 1 < np) build(srs[pi + 1], tabs[METRIC == 0 ? (B ^ 1) : 0]);
     const float* tab = tabs[METRIC == 0 ? B : 0];
     const float one_minus_qdc = METRIC == 1 ? 1.0f - s_qdc[pi] : 0.0f;
-    while (cp == pi) {
-      // refill the slot read in the previous iteration (its reads are done),
-      // then wait for this chunk; the chunks issued after it stay in flight
-      if (pp < np) issue();
-      const int later = issued - consumed - 1;
-      if (later >= 2) vm_wait<4>();
-      else if (later == 1) vm_wait<2>();
-      else vm_wait<0>();
-      const uint8_t* slot = myring + (consumed % IVF_NS) * IVF_CHUNK;
-      const uint4 cw = *reinterpret_cast<const uint4*>(slot + lane * 16);
-      const uint32_t rk = *reinterpret_cast<const uint32_t*>(slot + 1024 + lane * 4);
-      const bool valid = ce + lane < cend;
-      ++consumed;
-      ce += IVF_SW * 64;
-      seek(cp, ce, cend);
-      uint64_t key = KEY_MAX;
-      if (valid && (accept == nullptr || accept[rank_slot[rk]])) {
-        const float sum = adc16(tab, cw);
-        if constexpr (METRIC == 0) {
-          // sums of squares are in [+0, +inf]: the order key is the bits with
-          // the sign bit set
-          key = ((uint64_t)(__float_as_uint(sum) | 0x80000000u) << 32) | rk;
-        } else {
-          key = ((uint64_t)ord_key(one_minus_qdc + (-sum)) << 32) | rk;
-        }
-      }
-      wave_topk_add(key, kept, thr, kk, lane);
+    if (METRIC == 0 && pi + 1 < np) {
+      float* nt = tabs[METRIC == 0 ? (B ^ 1) : 0];
+      float rv[W];
+      load_slice(srs[pi + 1], rv);
+      build_part(I0{}, I2{}, rv, nt);
+      if (cp == pi) chunk(tab, one_minus_qdc);
+      build_part(I2{}, I2{}, rv, nt);
+      if (cp == pi) chunk(tab, one_minus_qdc);
+      build_part(I4{}, I2{}, rv, nt);
+      if (cp == pi) chunk(tab, one_minus_qdc);
+      build_part(I6{}, I2{}, rv, nt);
     }
+    while (cp == pi) chunk(tab, one_minus_qdc);
     __syncthreads();  // table pi+1 complete; table pi free for pi+2
   };
   for (int pi = 0; pi < np; pi += 2) {
