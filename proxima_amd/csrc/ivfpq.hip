@@ -26,12 +26,16 @@
 //               l2 += d*d; ip += q*c), stream the list's codes coalesced (M
 //               bytes + a 4-byte id rank per entry), ADC-sum the table in
 //               subspace order (bit-exact), keep a per-wave top-kk by (score,
-//               id): ivf_scan_reg (codebooks in VGPRs, one workgroup per query
-//               and 8 probes) for dim <= 128 with equal subspace widths and
-//               kk <= 64, else ivf_scan (table in LDS, one workgroup per
-//               query and probe).
+//               id): ivf_scan16 (16 subspaces, dim <= 128, kk <= 64: codebook
+//               rows in VGPRs, one workgroup per query and up to 32 probes,
+//               list stream staged through LDS by asynchronous copies),
+//               ivf_scan_reg (other equal-width layouts, same work split),
+//               else ivf_scan (table in LDS, one workgroup per query and
+//               probe).
 //   ivf_merge   per query: select the shortlist over all probes, optionally
-//               rescore it exactly against the stored vectors (rerank), keep k.
+//               rescore it exactly against the stored vectors (rerank), keep k;
+//               skipped when one probe group covers each query and there is
+//               no rerank (the scan merges its waves and writes the results).
 #include <algorithm>
 #include <cmath>
 #include <mutex>
