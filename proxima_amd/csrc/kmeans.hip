@@ -16,12 +16,16 @@
 // farthest_point (kmeans.rs:215-226) evaluated against the partially updated
 // centroid array, exactly as the sequential loop sees it.
 //
-// Inertia and k-means++ totals are f64 sums over points in point order. Up to
-// SEQ_SUM_LIMIT points they are evaluated sequentially on the device (the
-// reference's rounding); above it, in a fixed tree order (deterministic; the
-// last bits can differ from the sequential sum, which can change a k-means++
-// pick only when the drawn target falls within that difference of a
-// cumulative boundary).
+// Inertia, cluster sums and k-means++ totals are f64 sums of f32 values in
+// point order. They are summed in parallel with an exactness certificate
+// (every nonzero term a multiple of 2^e and sum |x| < 2^(e+53) makes every
+// partial sum exact, so any order gives the sequential bits); where the
+// certificate fails, sequentially on the device, except k-means++ and inertia
+// totals above SEQ_SUM_LIMIT points, which then keep a fixed parallel order
+// (deterministic; a k-means++ pick can differ from the reference only when
+// the drawn target falls within the last-bit difference of a cumulative
+// boundary). k-means++ runs all rounds on the device, with the generator's
+// state copied there and back.
 #include <hipcub/hipcub.hpp>
 
 #include <algorithm>
@@ -170,207 +174,390 @@ void nearest_device(const float* P, int ldp, const uint32_t* rows, size_t n, int
 }
 
 // ---------------------------------------------------------------------------
-// f64 sums in point order
+// f64 sums of f32 values in point order
 // ---------------------------------------------------------------------------
-// Sequential f64 prefix sums of v[0..n) in index order: prefix[i] =
-// (((0 + v0) + v1) + ... + vi), total = prefix[n-1]. One wave: all lanes
-// stage the next 1024 values through LDS while lane 0 runs the dependent
-// chain on the current ones. The running sums are non-decreasing for
-// non-negative inputs, so "first index whose cumulative sum reaches target"
-// is a binary search over prefix (seq_find_prefix).
-__global__ __launch_bounds__(64) void seq_prefix_f64(const float* __restrict__ v, int n, double* __restrict__ prefix,
-                                                     double* __restrict__ total) {
-  __shared__ float buf[2][1024];
-  const int lane = threadIdx.x;
-  const int nchunks = (n + 1023) / 1024;
-  auto stage = [&](int c, int b) {
-    for (int t = lane; t < 1024; t += 64) {
-      const int i = c * 1024 + t;
-      buf[b][t] = i < n ? v[i] : 0.0f;
-    }
-  };
-  double s = 0.0;
-  if (nchunks > 0) stage(0, 0);
-  __syncthreads();
-  for (int c = 0; c < nchunks; ++c) {
-    const int b = c & 1;
-    // issue the next chunk's loads before the chain
-    float nx[16];
-    const bool more = c + 1 < nchunks;
-    if (more)
+// The reference adds f32 values into an f64 accumulator in point order
+// (kmeans.rs:94, 107-112, 161, 171-176). If every nonzero term is a multiple
+// of 2^e (e = the smallest ulp exponent among them) and sum |x| < 2^(e+53),
+// every partial sum of any subset is a multiple of 2^e below 2^(e+53), hence
+// an exact f64: a parallel sum then has the sequential sum's bits. The
+// kernels below carry that certificate (f64 sum, f64 sum of |x|, smallest ulp
+// exponent) per block; where it fails the sum is redone sequentially up to
+// SEQ_SUM_LIMIT terms, and kept in the fixed parallel order above that.
+constexpr int NO_TERMS = 1 << 20;  // ulp exponent of a set with no nonzero term
+
+__device__ inline int ulp_exp(float x) {  // nonzero finite x
+  const int e = (int)((__float_as_uint(x) >> 23) & 0xFFu);
+  return (e > 0 ? e : 1) - 150;
+}
+
+__host__ __device__ inline bool sums_exact(double abs_sum, int emin) {
+  if (emin >= NO_TERMS) return true;
+  // the margin covers rounding in abs_sum itself (n < 2^30 terms)
+  return abs_sum < ldexp(1.0 - 0x1p-20, emin + 53);
+}
+
+struct SumCert {
+  double s, a;
+  int e;
+};
+
+__device__ inline double shfl_xor_f64(double v, int m) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)b, m, WAVE);
+  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(b >> 32), m, WAVE);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// Fixed-order reduction over a 256-thread block (xor butterflies, then the
+// four wave results in wave order); every thread gets the result.
+__device__ inline SumCert block_cert_256(SumCert v, SumCert* sh) {
 #pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        const int i = (c + 1) * 1024 + u * 64 + lane;
-        nx[u] = i < n ? v[i] : 0.0f;
-      }
-    if (lane == 0) {
-      const int m = min(1024, n - c * 1024);
-      double* pf = prefix + (size_t)c * 1024;
-      for (int t = 0; t < m; ++t) {
-        s += (double)buf[b][t];
-        pf[t] = s;
-      }
-    }
-    if (more)
-#pragma unroll
-      for (int u = 0; u < 16; ++u) buf[b ^ 1][u * 64 + lane] = nx[u];
-    __syncthreads();
+  for (int o = 32; o > 0; o >>= 1) {
+    v.s += shfl_xor_f64(v.s, o);
+    v.a += shfl_xor_f64(v.a, o);
+    v.e = min(v.e, __shfl_xor(v.e, o, WAVE));
   }
-  if (lane == 0) *total = s;
-}
-
-__global__ void seq_find_prefix(const double* __restrict__ prefix, int n, double target, long long* __restrict__ out) {
-  if (threadIdx.x != 0) return;
-  // first i with prefix[i] >= target; n - 1 if none (kmeans.rs:171-180)
-  int lo = 0, hi = n;
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    if (prefix[mid] >= target)
-      hi = mid;
-    else
-      lo = mid + 1;
-  }
-  *out = lo < n ? lo : n - 1;
-}
-
-// Fixed-order tree sums: block b sums v[b*1024 ..) pairwise; partials summed in order.
-constexpr int TREE_SEG = 1024;
-__global__ __launch_bounds__(256) void tree_partials(const float* __restrict__ v, int n, double* __restrict__ part) {
-  __shared__ double sh[256];
-  const int b = blockIdx.x, t = threadIdx.x;
-  double acc = 0.0;
-  for (int j = 0; j < TREE_SEG / 256; ++j) {
-    const int i = b * TREE_SEG + j * 256 + t;
-    acc += i < n ? (double)v[i] : 0.0;
-  }
-  sh[t] = acc;
+  const int w = threadIdx.x >> 6;
   __syncthreads();
-  for (int o = 128; o > 0; o >>= 1) {
-    if (t < o) sh[t] = sh[t] + sh[t + o];
-    __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh[w] = v;
+  __syncthreads();
+  SumCert r = sh[0];
+  for (int i = 1; i < 4; ++i) {
+    r.s += sh[i].s;
+    r.a += sh[i].a;
+    r.e = min(r.e, sh[i].e);
   }
-  if (t == 0) part[b] = sh[0];
+  return r;
 }
 
-__global__ __launch_bounds__(64) void tree_total(const double* __restrict__ part, int nb, double* __restrict__ out) {
+__device__ inline SumCert cert_of(float x) {
+  return SumCert{(double)x, (double)fabsf(x), x != 0.0f ? ulp_exp(x) : NO_TERMS};
+}
+
+// per-256-value block certificates of v[0..n)
+__global__ __launch_bounds__(256) void f64_partials(const float* __restrict__ v, int n, double* __restrict__ ps,
+                                                    double* __restrict__ pa, int* __restrict__ pe) {
+  __shared__ SumCert sh[4];
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const SumCert r = block_cert_256(cert_of(i < n ? v[i] : 0.0f), sh);
   if (threadIdx.x == 0) {
-    double s = 0.0;
-    for (int b = 0; b < nb; ++b) s += part[b];
-    *out = s;
+    ps[blockIdx.x] = r.s;
+    pa[blockIdx.x] = r.a;
+    pe[blockIdx.x] = r.e;
   }
 }
 
-__global__ __launch_bounds__(64) void tree_find_cum(const float* __restrict__ v, int n, const double* __restrict__ part,
-                                                    int nb, double target, long long* __restrict__ out) {
-  if (threadIdx.x != 0) return;
+// Sequential sum of v[0..n) by one block: all threads stage 4096 values in
+// LDS, thread 0 runs the dependent chain.
+__device__ inline double seq_sum_block(const float* __restrict__ v, int n, float* stage) {
   double s = 0.0;
-  int b = 0;
-  for (; b < nb; ++b) {
-    if (s + part[b] >= target) break;
-    s += part[b];
+  for (int c0 = 0; c0 < n; c0 += 4096) {
+    const int m = min(4096, n - c0);
+    __syncthreads();
+    for (int t = threadIdx.x; t < m; t += blockDim.x) stage[t] = v[c0 + t];
+    __syncthreads();
+    if (threadIdx.x == 0)
+      for (int t = 0; t < m; ++t) s += (double)stage[t];
   }
-  long long found = n - 1;
-  if (b < nb) {
-    for (int i = b * TREE_SEG; i < min(n, (b + 1) * TREE_SEG); ++i) {
-      s += (double)v[i];
-      if (s >= target) {
-        found = i;
-        break;
-      }
+  return s;
+}
+
+// Total of v from its block certificates (one 1024-thread block): exact when
+// the certificate holds, else sequential (n <= SEQ_SUM_LIMIT) or the fixed
+// order. out[0] = total, out[1] = 1.0 if it equals the sequential sum.
+__global__ __launch_bounds__(1024) void f64_total(const float* __restrict__ v, int n, const double* __restrict__ ps,
+                                                  const double* __restrict__ pa, const int* __restrict__ pe, int nb,
+                                                  double* __restrict__ out) {
+  __shared__ double ss[1024], sa[1024];
+  __shared__ int se[1024];
+  __shared__ float stage[4096];
+  const int t = threadIdx.x, per = (nb + 1023) / 1024;
+  double s = 0.0, a = 0.0;
+  int e = NO_TERMS;
+  for (int b = t * per; b < min(nb, (t + 1) * per); ++b) {
+    s += ps[b];
+    a += pa[b];
+    e = min(e, pe[b]);
+  }
+  ss[t] = s;
+  sa[t] = a;
+  se[t] = e;
+  __syncthreads();
+  for (int o = 512; o > 0; o >>= 1) {
+    if (t < o) {
+      ss[t] += ss[t + o];
+      sa[t] += sa[t + o];
+      se[t] = min(se[t], se[t + o]);
     }
+    __syncthreads();
   }
-  *out = found;
+  const bool exact = sums_exact(sa[0], se[0]);
+  double total = ss[0];
+  if (!exact && n <= (int)SEQ_SUM_LIMIT) total = seq_sum_block(v, n, stage);
+  if (t == 0) {
+    out[0] = total;
+    out[1] = (exact || n <= (int)SEQ_SUM_LIMIT) ? 1.0 : 0.0;
+  }
 }
 
 struct F64Sum {
-  DevBuf<double> part, tot, prefix;
-  DevBuf<long long> idx;
+  DevBuf<double> ps, pa, out;
+  DevBuf<int> pe;
+  bool last_exact = true;  // the last total equals the sequential sum
+  // f64 sum of v[0..n) in point order (see above); synchronises the stream
   double total(const float* v, size_t n, hipStream_t s) {
-    tot.reserve(1);
-    if (n <= SEQ_SUM_LIMIT) {
-      prefix.reserve(std::max<size_t>(n, 1));
-      hipLaunchKernelGGL(seq_prefix_f64, dim3(1), dim3(64), 0, s, v, (int)n, prefix.p, tot.p);
-    } else {
-      const int nb = (int)((n + TREE_SEG - 1) / TREE_SEG);
-      part.reserve(nb);
-      hipLaunchKernelGGL(tree_partials, dim3(nb), dim3(256), 0, s, v, (int)n, part.p);
-      hipLaunchKernelGGL(tree_total, dim3(1), dim3(64), 0, s, part.p, nb, tot.p);
-    }
+    const int nb = (int)std::max<size_t>((n + 255) / 256, 1);
+    ps.reserve(nb);
+    pa.reserve(nb);
+    pe.reserve(nb);
+    out.reserve(2);
+    hipLaunchKernelGGL(f64_partials, dim3(nb), dim3(256), 0, s, v, (int)n, ps.p, pa.p, pe.p);
+    hipLaunchKernelGGL(f64_total, dim3(1), dim3(1024), 0, s, v, (int)n, ps.p, pa.p, pe.p, nb, out.p);
     PXG_HIP(hipGetLastError());
-    double h = 0;
-    PXG_HIP(hipMemcpyAsync(&h, tot.p, 8, hipMemcpyDeviceToHost, s));
+    double h[2] = {0, 0};
+    PXG_HIP(hipMemcpyAsync(h, out.p, 16, hipMemcpyDeviceToHost, s));
     PXG_HIP(hipStreamSynchronize(s));
-    return h;
-  }
-  // uses the prefix (or partials) of the last total() over the same values
-  size_t find(const float* v, size_t n, double target, hipStream_t s) {
-    idx.reserve(1);
-    if (n <= SEQ_SUM_LIMIT)
-      hipLaunchKernelGGL(seq_find_prefix, dim3(1), dim3(64), 0, s, prefix.p, (int)n, target, idx.p);
-    else
-      hipLaunchKernelGGL(tree_find_cum, dim3(1), dim3(64), 0, s, v, (int)n, part.p,
-                         (int)((n + TREE_SEG - 1) / TREE_SEG), target, idx.p);
-    PXG_HIP(hipGetLastError());
-    long long h = 0;
-    PXG_HIP(hipMemcpyAsync(&h, idx.p, 8, hipMemcpyDeviceToHost, s));
-    PXG_HIP(hipStreamSynchronize(s));
-    return (size_t)h;
+    last_exact = h[1] != 0.0;
+    return h[0];
   }
 };
 
 // ---------------------------------------------------------------------------
-// k-means++ (kmeans.rs:146-194)
+// k-means++ (kmeans.rs:146-194), all rounds on the device
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void km_pp_update(const float* __restrict__ P, int ldp, int n, int dim,
-                                                    const float* __restrict__ c, float* __restrict__ ns, int init) {
-  __shared__ float cs[KM_LDS_FLOATS];
-  const bool staged = dim <= KM_LDS_FLOATS;
-  if (staged) {
-    for (int t = threadIdx.x; t < dim; t += 256) cs[t] = c[t];
+// Round r: km_pp_pick draws the next centre from the distances left by round
+// r-1 (total, target = gen_range(0.0..total) from the device copy of the
+// generator, first point whose cumulative sum reaches it) and copies its row;
+// km_pp_round then lowers every point's distance to that centre (strict <)
+// and leaves per-block sum certificates for the next pick. No host round trip.
+constexpr int PP_ROWS = 256;  // points per km_pp_round block
+
+// Sequential squared (kmeans.rs:234-241) of each of the block's 256 points to
+// centre c: the block's rows are staged through LDS 32 coordinates at a time
+// (coalesced loads), each thread then runs its point's chain.
+__global__ __launch_bounds__(256) void km_pp_round(const float* __restrict__ P, int ldp, int n, int dim,
+                                                   const float* __restrict__ c, float* __restrict__ ns, int init,
+                                                   double* __restrict__ ps, int* __restrict__ pe, int vec4) {
+  constexpr int CS = 2048;  // centre coordinates staged in LDS
+  __shared__ float tile[PP_ROWS * 33];
+  __shared__ float cs[CS];
+  __shared__ SumCert sh[4];
+  const int t = threadIdx.x;
+  const int r0 = blockIdx.x * PP_ROWS;
+  const bool staged_c = dim <= CS;
+  if (staged_c)
+    for (int j = t; j < dim; j += 256) cs[j] = c[j];
+  const float* cc = staged_c ? cs : c;
+  float sum = 0.0f;
+  for (int j0 = 0; j0 < dim; j0 += 32) {
+    const int w = min(32, dim - j0);
+    __syncthreads();
+    if (vec4) {
+      // w is a multiple of 4: 8 threads per row slice, 16 bytes each
+      for (int f = t; f < PP_ROWS * 8; f += 256) {
+        const int r = f >> 3, c4 = (f & 7) * 4;
+        if (c4 < w) {
+          float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+          if (r0 + r < n) x = *reinterpret_cast<const float4*>(P + (size_t)(r0 + r) * ldp + j0 + c4);
+          float* d = tile + r * 33 + c4;
+          d[0] = x.x;
+          d[1] = x.y;
+          d[2] = x.z;
+          d[3] = x.w;
+        }
+      }
+    } else {
+      for (int f = t; f < PP_ROWS * 32; f += 256) {
+        const int r = f >> 5, cidx = f & 31;
+        if (cidx < w) tile[r * 33 + cidx] = r0 + r < n ? P[(size_t)(r0 + r) * ldp + j0 + cidx] : 0.0f;
+      }
+    }
+    __syncthreads();
+    const float* row = tile + t * 33;
+    for (int jj = 0; jj < w; ++jj) {
+      const float d = row[jj] - cc[j0 + jj];
+      sum += d * d;
+    }
+  }
+  const int i = r0 + t;
+  float nv = 0.0f;
+  if (i < n) {
+    nv = sum;
+    if (!init) {
+      const float cur = ns[i];
+      if (!(sum < cur)) nv = cur;
+    }
+    ns[i] = nv;
+  }
+  const SumCert r = block_cert_256(cert_of(nv), sh);
+  if (t == 0) {
+    ps[blockIdx.x] = r.s;
+    pe[blockIdx.x] = r.e;
+  }
+}
+
+// One 1024-thread block: the pick of one round and the copy of its row.
+// status: 0 ok, 1 non-finite total (the round and all later ones stop).
+__global__ __launch_bounds__(1024) void km_pp_pick(const float* __restrict__ P, int ldp, int n, int dim,
+                                                   const float* __restrict__ ns, const double* __restrict__ ps,
+                                                   const int* __restrict__ pe, int nb, ChaCha8* __restrict__ grng,
+                                                   float* __restrict__ row_out, int* __restrict__ status,
+                                                   int* __restrict__ inexact) {
+  __shared__ double ex[1024];
+  __shared__ int se[1024];
+  __shared__ float stage[4096];
+  __shared__ __align__(8) unsigned char rng_mem[sizeof(ChaCha8)];
+  ChaCha8& rng = *reinterpret_cast<ChaCha8*>(rng_mem);
+  __shared__ double s_target;
+  __shared__ int s_mode, s_pick, s_block;
+  const int t = threadIdx.x;
+  if (*status != 0) return;
+  if (t == 0) rng = *grng;
+  // each thread sums a contiguous run of block partials
+  const int per = (nb + 1023) / 1024;
+  const int b0 = min(nb, t * per), b1 = min(nb, (t + 1) * per);
+  double ls = 0.0;
+  int le = NO_TERMS;
+  for (int b = b0; b < b1; ++b) {
+    ls += ps[b];
+    le = min(le, pe[b]);
+  }
+  // inclusive scan over the threads in a fixed order (Hillis-Steele)
+  ex[t] = ls;
+  se[t] = le;
+  __syncthreads();
+  for (int o = 1; o < 1024; o <<= 1) {
+    const double add = t >= o ? ex[t - o] : 0.0;
+    const int me = t >= o ? se[t - o] : NO_TERMS;
+    __syncthreads();
+    ex[t] += add;
+    se[t] = min(se[t], me);
     __syncthreads();
   }
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= n) return;
-  const float* cc = staged ? cs : c;
-  const float* pr = P + (size_t)i * ldp;
-  float sum = 0.0f;
-  for (int j = 0; j < dim; ++j) {
-    const float d = pr[j] - cc[j];
-    sum += d * d;
+  double total = ex[1023];
+  const int emin = se[1023];
+  const double before = ex[t] - ls;  // exact when the certificate holds
+  // distances are >= 0, so the sum of |x| is the total itself
+  const bool exact = sums_exact(total, emin);
+  const bool sequential = !exact && n <= (int)SEQ_SUM_LIMIT;
+  if (sequential) total = seq_sum_block(ns, n, stage);
+  if (t == 0) {
+    if (!(total <= 1.79769313486231570e308 && total >= 0.0)) {
+      *status = 1;
+      s_mode = -1;
+    } else if (total <= 0.0) {
+      s_pick = (int)rng.gen_range_usize((uint64_t)n);  // kmeans.rs:162-166
+      s_mode = 0;
+    } else {
+      s_target = rng.gen_range_f64(0.0, total);
+      s_mode = sequential ? 2 : 1;
+      s_pick = n - 1;
+      s_block = nb;
+    }
+    if (!exact && !sequential) atomicAdd(inexact, 1);
   }
-  if (init || sum < ns[i]) ns[i] = sum;
+  __syncthreads();
+  const int mode = s_mode;
+  if (mode < 0) return;
+  const double target = s_target;
+  if (mode == 2) {
+    // the reference's cumulative scan, sequentially (kmeans.rs:169-176)
+    double cum = 0.0;
+    bool found = false;
+    for (int c0 = 0; c0 < n; c0 += 4096) {
+      const int m = min(4096, n - c0);
+      __syncthreads();
+      for (int u = t; u < m; u += 1024) stage[u] = ns[c0 + u];
+      __syncthreads();
+      if (t == 0 && !found)
+        for (int u = 0; u < m; ++u) {
+          cum += (double)stage[u];
+          if (cum >= target) {
+            s_pick = c0 + u;
+            found = true;
+            break;
+          }
+        }
+    }
+  } else if (mode == 1) {
+    // first block whose inclusive prefix reaches the target, then the first
+    // point inside it
+    double run = before;
+    for (int b = b0; b < b1; ++b) {
+      if (run + ps[b] >= target) {
+        atomicMin(&s_block, b);
+        break;
+      }
+      run += ps[b];
+    }
+    __syncthreads();
+    const int bb = s_block;
+    if (bb < nb) {
+      // prefix before block bb: recomputed by the owning thread's run
+      __syncthreads();
+      if (b0 <= bb && bb < b1) {
+        double pre = before;
+        for (int b = b0; b < bb; ++b) pre += ps[b];
+        ex[0] = pre;  // ex is free after the scan
+      }
+      __syncthreads();
+      const double pre = ex[0];
+      __syncthreads();
+      const int i = bb * PP_ROWS + t;
+      ex[t] = (t < PP_ROWS && i < n) ? (double)ns[i] : 0.0;
+      __syncthreads();
+      for (int o = 1; o < PP_ROWS; o <<= 1) {
+        const double add = (t < PP_ROWS && t >= o) ? ex[t - o] : 0.0;
+        __syncthreads();
+        if (t < PP_ROWS) ex[t] += add;
+        __syncthreads();
+      }
+      if (t < PP_ROWS && i < n && pre + ex[t] >= target) atomicMin(&s_pick, i);
+    }
+  }
+  __syncthreads();
+  const int picked = s_pick;
+  for (int j = t; j < dim; j += 1024) row_out[j] = P[(size_t)picked * ldp + j];
+  if (t == 0) *grng = rng;
 }
 
 __global__ void copy_row(const float* __restrict__ src, int ld_src, size_t row, int dim, float* __restrict__ dst) {
   for (int j = threadIdx.x; j < dim; j += blockDim.x) dst[j] = src[row * ld_src + j];
 }
 
-void kmeans_pp_device(const float* P, size_t n, int dim, int ldp, size_t k, ChaCha8& rng, float* cents,
-                      hipStream_t s) {
+// Returns the number of rounds whose pick used the fixed parallel order
+// instead of the reference's sequential sums (0 whenever the certificate
+// holds or n <= SEQ_SUM_LIMIT).
+size_t kmeans_pp_device(const float* P, size_t n, int dim, int ldp, size_t k, ChaCha8& rng, float* cents,
+                        hipStream_t s) {
+  const int nb = (int)((n + PP_ROWS - 1) / PP_ROWS);
   DevBuf<float> ns(n);
-  F64Sum sums;
+  DevBuf<double> ps(nb);
+  DevBuf<int> pe(nb), flags(2);
+  DevBuf<ChaCha8> drng(1);
   const size_t first = rng.gen_range_usize(n);
   hipLaunchKernelGGL(copy_row, dim3(1), dim3(256), 0, s, P, ldp, first, dim, cents);
-  const dim3 g((unsigned)((n + 255) / 256));
-  hipLaunchKernelGGL(km_pp_update, g, dim3(256), 0, s, P, ldp, (int)n, dim, cents, ns.p, 1);
+  PXG_HIP(hipMemcpyAsync(drng.p, &rng, sizeof(ChaCha8), hipMemcpyHostToDevice, s));
+  PXG_HIP(hipMemsetAsync(flags.p, 0, 8, s));
+  const int vec4 = (ldp % 4 == 0 && dim % 4 == 0 && ((uintptr_t)P & 15) == 0) ? 1 : 0;
+  hipLaunchKernelGGL(km_pp_round, dim3(nb), dim3(256), 0, s, P, ldp, (int)n, dim, cents, ns.p, 1, ps.p, pe.p, vec4);
   PXG_HIP(hipGetLastError());
   for (size_t chosen = 1; chosen < k; ++chosen) {
-    const double total = sums.total(ns.p, n, s);
-    if (!std::isfinite(total))
-      internal_error("kmeans++", "the sum of squared distances is not finite; coordinates are too large to square");
-    size_t picked;
-    if (total <= 0.0) {
-      picked = rng.gen_range_usize(n);
-    } else {
-      const double target = rng.gen_range_f64(0.0, total);
-      picked = sums.find(ns.p, n, target, s);
-    }
     float* c = cents + chosen * dim;
-    hipLaunchKernelGGL(copy_row, dim3(1), dim3(256), 0, s, P, ldp, picked, dim, c);
-    hipLaunchKernelGGL(km_pp_update, g, dim3(256), 0, s, P, ldp, (int)n, dim, c, ns.p, 0);
+    hipLaunchKernelGGL(km_pp_pick, dim3(1), dim3(1024), 0, s, P, ldp, (int)n, dim, ns.p, ps.p, pe.p, nb, drng.p, c,
+                       flags.p, flags.p + 1);
+    if (chosen + 1 < k)
+      hipLaunchKernelGGL(km_pp_round, dim3(nb), dim3(256), 0, s, P, ldp, (int)n, dim, c, ns.p, 0, ps.p, pe.p, vec4);
     PXG_HIP(hipGetLastError());
   }
+  int h[2] = {0, 0};
+  PXG_HIP(hipMemcpyAsync(&rng, drng.p, sizeof(ChaCha8), hipMemcpyDeviceToHost, s));
+  PXG_HIP(hipMemcpyAsync(h, flags.p, 8, hipMemcpyDeviceToHost, s));
   PXG_HIP(hipStreamSynchronize(s));
+  if (h[0] != 0)
+    internal_error("kmeans++", "the sum of squared distances is not finite; coordinates are too large to square");
+  return (size_t)h[1];
 }
 
 // ---------------------------------------------------------------------------
@@ -389,20 +576,50 @@ __global__ void km_changed_counts(const uint32_t* __restrict__ a, uint32_t* __re
   idx[i] = (uint32_t)i;
 }
 
-// One thread per (cluster, coordinate): f64 sum of the members in point order.
-__global__ void km_sums(const float* __restrict__ P, int ldp, int dim, const uint32_t* __restrict__ members,
-                        const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ counts, int k,
-                        float* __restrict__ newc) {
+// Cluster means (kmeans.rs:104-135): one block per (cluster, JW-coordinate
+// slice), 256/JW member groups. Each (cluster, coordinate) f64 sum carries
+// the exactness certificate; where it fails, one thread redoes it in point
+// order. The mean is (float)(sum * (1.0 / count)).
+template <int JW>
+__global__ __launch_bounds__(256) void km_sums(const float* __restrict__ P, int ldp, int dim,
+                                               const uint32_t* __restrict__ members,
+                                               const uint32_t* __restrict__ offsets,
+                                               const uint32_t* __restrict__ counts, int k, float* __restrict__ newc) {
+  constexpr int G = 256 / JW;
+  __shared__ double ss[G][JW], sa[G][JW];
+  __shared__ int se[G][JW];
   const int c = blockIdx.x;
-  const int j = blockIdx.y * blockDim.x + threadIdx.x;
-  if (c >= k || j >= dim) return;
+  const int jl = threadIdx.x % JW, g = threadIdx.x / JW;
+  const int j = blockIdx.y * JW + jl;
   const uint32_t cnt = counts[c];
   if (cnt == 0) return;
   const uint32_t off = offsets[c];
-  double sum = 0.0;
-  for (uint32_t m = 0; m < cnt; ++m) sum += (double)P[(size_t)members[off + m] * ldp + j];
-  const double inv = 1.0 / (double)cnt;
-  newc[(size_t)c * dim + j] = (float)(sum * inv);
+  double s = 0.0, a = 0.0;
+  int e = NO_TERMS;
+  if (j < dim)
+    for (uint32_t m = g; m < cnt; m += G) {
+      const float x = P[(size_t)members[off + m] * ldp + j];
+      s += (double)x;
+      a += (double)fabsf(x);
+      if (x != 0.0f) e = min(e, ulp_exp(x));
+    }
+  ss[g][jl] = s;
+  sa[g][jl] = a;
+  se[g][jl] = e;
+  __syncthreads();
+  if (g == 0 && j < dim) {
+    for (int q = 1; q < G; ++q) {
+      s += ss[q][jl];
+      a += sa[q][jl];
+      e = min(e, se[q][jl]);
+    }
+    if (!sums_exact(a, e)) {
+      s = 0.0;
+      for (uint32_t m = 0; m < cnt; ++m) s += (double)P[(size_t)members[off + m] * ldp + j];
+    }
+    const double inv = 1.0 / (double)cnt;
+    newc[(size_t)c * dim + j] = (float)(s * inv);
+  }
 }
 
 // farthest_point (kmeans.rs:215-226): first point with the largest distance
@@ -464,7 +681,7 @@ KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req
   if (init)
     PXG_HIP(hipMemcpyAsync(cents.p, init, k * dim * 4, hipMemcpyDeviceToDevice, s));
   else
-    kmeans_pp_device(P, n, dim, ldp, k, *rng, cents.p, s);
+    out.inexact_sums += kmeans_pp_device(P, n, dim, ldp, k, *rng, cents.p, s);
   const double t_seeded = now_s();
   size_t empties = 0;
 
@@ -485,6 +702,7 @@ KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req
     out.iterations = it + 1;
     nearest_device(P, ldp, nullptr, n, dim, cents.p, dim, k, false, assign.p, dist.p, s);
     out.inertia = sums.total(dist.p, n, s);
+    if (!sums.last_exact) ++out.inexact_sums;
     PXG_HIP(hipMemsetAsync(changed.p, 0, 4, s));
     PXG_HIP(hipMemsetAsync(counts.p, 0, k * 4, s));
     hipLaunchKernelGGL(km_changed_counts, gn, dim3(256), 0, s, assign.p, prev.p, (int)n, counts.p, changed.p, idx.p);
@@ -504,8 +722,15 @@ KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req
     }
     PXG_HIP(hipMemcpyAsync(offsets.p, h_off.data(), k * 4, hipMemcpyHostToDevice, s));
     PXG_HIP(hipMemcpyAsync(newc.p, cents.p, k * dim * 4, hipMemcpyDeviceToDevice, s));
-    hipLaunchKernelGGL(km_sums, dim3((unsigned)k, (unsigned)((dim + 63) / 64)), dim3(64), 0, s, P, ldp, dim,
-                       members.p, offsets.p, counts.p, (int)k, newc.p);
+    if (dim <= 8)
+      hipLaunchKernelGGL(km_sums<8>, dim3((unsigned)k, 1), dim3(256), 0, s, P, ldp, dim, members.p, offsets.p,
+                         counts.p, (int)k, newc.p);
+    else if (dim <= 16)
+      hipLaunchKernelGGL(km_sums<16>, dim3((unsigned)k, 1), dim3(256), 0, s, P, ldp, dim, members.p, offsets.p,
+                         counts.p, (int)k, newc.p);
+    else
+      hipLaunchKernelGGL(km_sums<32>, dim3((unsigned)k, (unsigned)((dim + 31) / 32)), dim3(256), 0, s, P, ldp, dim,
+                         members.p, offsets.p, counts.p, (int)k, newc.p);
     PXG_HIP(hipGetLastError());
     // empty clusters, ascending, against the partially updated array
     for (size_t c = 0; c < k; ++c) {

@@ -4,11 +4,14 @@
 // expansion into the 32-byte key), and the rand 0.8 samplers used at the call
 // sites kmeans.rs:150,167-169 (usize gen_range: widening multiply with zone
 // rejection; f64 gen_range: 52 random bits as [1,2) - 1, scaled, rejected if
-// >= high). Restated from those crates' published algorithms; host only.
+// >= high). Restated from those crates' published algorithms. The state is
+// plain data: the host seeds it, a device kernel can continue the stream from
+// a copy in device memory, and the host picks it up again afterwards.
 #pragma once
 
+#include <hip/hip_runtime.h>
+
 #include <cstdint>
-#include <cstring>
 
 namespace pxg {
 
@@ -18,13 +21,14 @@ struct ChaCha8 {
   uint32_t buf[64];
   int index = 64;
 
-  static inline uint32_t rotl(uint32_t x, int r) { return (x << r) | (x >> (32 - r)); }
+  __host__ __device__ static inline uint32_t rotl(uint32_t x, int r) { return (x << r) | (x >> (32 - r)); }
 
-  static void block(const uint32_t k[8], uint64_t ctr, uint32_t out[16]) {
-    uint32_t s[16] = {0x61707865u, 0x3320646eu, 0x79622d32u, 0x6b206574u, k[0], k[1], k[2], k[3],
-                      k[4],        k[5],        k[6],        k[7],        (uint32_t)ctr, (uint32_t)(ctr >> 32), 0, 0};
+  __host__ __device__ static void block(const uint32_t k[8], uint64_t ctr, uint32_t out[16]) {
+    const uint32_t s[16] = {0x61707865u, 0x3320646eu, 0x79622d32u, 0x6b206574u, k[0], k[1], k[2], k[3],
+                            k[4],        k[5],        k[6],        k[7],        (uint32_t)ctr, (uint32_t)(ctr >> 32),
+                            0,           0};
     uint32_t x[16];
-    std::memcpy(x, s, sizeof x);
+    for (int i = 0; i < 16; ++i) x[i] = s[i];
     auto qr = [&](int a, int b, int c, int d) {
       x[a] += x[b]; x[d] = rotl(x[d] ^ x[a], 16);
       x[c] += x[d]; x[b] = rotl(x[b] ^ x[c], 12);
@@ -38,7 +42,8 @@ struct ChaCha8 {
     for (int i = 0; i < 16; ++i) out[i] = x[i] + s[i];
   }
 
-  explicit ChaCha8(uint64_t seed) {
+  ChaCha8() = default;
+  __host__ __device__ explicit ChaCha8(uint64_t seed) {
     const uint64_t MUL = 6364136223846793005ull, INC = 11634580027462260723ull;
     uint64_t st = seed;
     for (int i = 0; i < 8; ++i) {
@@ -49,16 +54,16 @@ struct ChaCha8 {
     }
   }
 
-  void refill() {
+  __host__ __device__ void refill() {
     for (int b = 0; b < 4; ++b) block(key, counter + b, buf + 16 * b);
     counter += 4;
     index = 0;
   }
-  uint32_t next_u32() {
+  __host__ __device__ uint32_t next_u32() {
     if (index >= 64) refill();
     return buf[index++];
   }
-  uint64_t next_u64() {
+  __host__ __device__ uint64_t next_u64() {
     if (index < 63) {
       const uint64_t lo = buf[index], hi = buf[index + 1];
       index += 2;
@@ -74,20 +79,28 @@ struct ChaCha8 {
     index = 1;
     return ((uint64_t)buf[0] << 32) | lo;
   }
-  uint64_t gen_range_usize(uint64_t n) {  // 0..n
+  // high and low 64 bits of a * b
+  __host__ __device__ static void mul_wide(uint64_t a, uint64_t b, uint64_t& hi, uint64_t& lo) {
+    const uint64_t a0 = (uint32_t)a, a1 = a >> 32, b0 = (uint32_t)b, b1 = b >> 32;
+    const uint64_t p00 = a0 * b0, p01 = a0 * b1, p10 = a1 * b0, p11 = a1 * b1;
+    const uint64_t mid = (p00 >> 32) + (uint32_t)p01 + (uint32_t)p10;
+    lo = (mid << 32) | (uint32_t)p00;
+    hi = p11 + (p01 >> 32) + (p10 >> 32) + (mid >> 32);
+  }
+  __host__ __device__ uint64_t gen_range_usize(uint64_t n) {  // 0..n
     const uint64_t zone = (n << __builtin_clzll(n)) - 1;
     for (;;) {
       const uint64_t v = next_u64();
-      const unsigned __int128 m = (unsigned __int128)v * n;
-      if ((uint64_t)m <= zone) return (uint64_t)(m >> 64);
+      uint64_t hi, lo;
+      mul_wide(v, n, hi, lo);
+      if (lo <= zone) return hi;
     }
   }
-  double gen_range_f64(double low, double high) {
+  __host__ __device__ double gen_range_f64(double low, double high) {
     const double scale = high - low;
     for (;;) {
       const uint64_t bits = (next_u64() >> 12) | (uint64_t(1023) << 52);
-      double v;
-      std::memcpy(&v, &bits, 8);
+      const double v = __builtin_bit_cast(double, bits);
       const double res = (v - 1.0) * scale + low;
       if (res < high) return res;
     }

@@ -41,6 +41,7 @@ struct KmeansOut {
   size_t k = 0;
   double inertia = 0.0;
   size_t iterations = 0;
+  size_t inexact_sums = 0;  // f64 sums kept in the fixed parallel order
 };
 
 // Nearest centroid for points P[rows ? rows[i] : i] (first dim columns of rows
@@ -54,9 +55,12 @@ void nearest_device(const float* P, int ldp, const uint32_t* rows, size_t n, int
 KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k, size_t max_iter, ChaCha8* rng,
                         const float* init, DevBuf<float>& cents, DevBuf<uint32_t>* assign_out, hipStream_t s);
 
-// k-means++ seeding alone (kmeans.rs:146-194): k*dim dense device centroids.
-void kmeans_pp_device(const float* P, size_t n, int dim, int ldp, size_t k, ChaCha8& rng, float* cents,
-                      hipStream_t s);
+// k-means++ seeding alone (kmeans.rs:146-194): k*dim dense device centroids;
+// `rng` continues from the state the device rounds left. Returns the number
+// of rounds whose f64 sums could not be proven equal to the sequential ones
+// (above 2^17 points only; 0 otherwise).
+size_t kmeans_pp_device(const float* P, size_t n, int dim, int ldp, size_t k, ChaCha8& rng, float* cents,
+                        hipStream_t s);
 
 // ProductQuantizer::train on device rows R[n][ldr]: one ChaCha8(seed) advanced
 // across subspaces, 256 centroids each, padded with the last centroid.

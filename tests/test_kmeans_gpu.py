@@ -1,8 +1,8 @@
 """GPU k-means and product-quantizer training/encoding against the oracle.
 
 With the same seed the GPU trainer must reproduce the oracle bit for bit:
-k-means++ picks (same ChaCha8 stream, same sequential f64 sums below 2^17
-points), Lloyd assignments, f64 centroid updates, empty-cluster reseeding,
+k-means++ picks (same ChaCha8 stream continued on the device; f64 sums that
+are provably exact in parallel, else sequential below 2^17 points), Lloyd assignments, f64 centroid updates, empty-cluster reseeding,
 inertia and iteration counts; PQ codebooks and codes. Plus the reference's own
 kmeans.rs / product.rs tests."""
 import numpy as np
@@ -63,6 +63,42 @@ def test_kmeans_pp_picks_match(gpu):
     rng = np.random.default_rng(6)
     pts = clustered(rng, 6000, 24, 20, 0.4)
     assert np.array_equal(bits(px.kmeans_pp(pts, 50, 1234)), bits(orc.kmeans_pp(pts, 50, 1234)))
+
+
+def test_kmeans_pp_parallel_sums_above_2_17_points(gpu):
+    """300k points on a 1/4 grid: every distance is a multiple of 1/16 and the
+    totals stay far below 2^53 such units, so the parallel f64 sums are exact
+    and the picks are the reference's, across more block partials (1172)
+    than the pick kernel has threads."""
+    px = gpu
+    rng = np.random.default_rng(21)
+    pts = (rng.integers(0, 16, (300_000, 4)) / 4).astype(np.float32)
+    assert np.array_equal(bits(px.kmeans_pp(pts, 24, 77)), bits(orc.kmeans_pp(pts, 24, 77)))
+
+
+def test_kmeans_pp_sequential_sums_when_not_provably_exact(gpu):
+    """Near-duplicate points at scale 1000: distances from ~1e-5 to ~1e7, so
+    an f64 sum of them rounds and only the sequential order reproduces it."""
+    px = gpu
+    rng = np.random.default_rng(22)
+    pts = clustered(rng, 5000, 6, 10, 0.5) * np.float32(1000)
+    pts[1::9] = pts[0::9][: pts[1::9].shape[0]] + np.float32(1e-3)
+    assert np.array_equal(bits(px.kmeans_pp(pts, 40, 5)), bits(orc.kmeans_pp(pts, 40, 5)))
+
+
+def test_kmeans_cluster_sums_with_mixed_magnitudes(gpu):
+    """Coordinates of 1e-20 next to O(1) ones in the same cluster: their f64
+    sums round, so those cluster means are summed in point order."""
+    px = gpu
+    rng = np.random.default_rng(23)
+    pts = clustered(rng, 4000, 8, 6, 0.5)
+    pts[::7, 0] = np.float32(1e-20)
+    pts[::11, 3] = np.float32(-3e-25)
+    got = px.kmeans(pts, 8, 12, 10, 31)
+    want_c, want_in, want_it = orc.kmeans(pts, 12, 10, 31)
+    assert got.iterations == want_it
+    assert np.array_equal(bits(got.centroids), bits(want_c.reshape(-1)))
+    assert got.inertia == want_in
 
 
 def test_assign_matches_oracle(gpu):
