@@ -41,6 +41,9 @@
 namespace pxg {
 
 constexpr int KM_LDS_FLOATS = 8192;  // 32 KiB of staged centroids
+typedef float f16v __attribute__((ext_vector_type(16)));
+// points of the last nearest_device call that the MFMA pass could not certify
+thread_local size_t g_last_redo = 0;
 constexpr size_t SEQ_SUM_LIMIT = 1u << 17;
 
 // ---------------------------------------------------------------------------
@@ -164,13 +167,268 @@ static void launch_assign(const float* P, int ldp, const uint32_t* rows, size_t 
   PXG_HIP(hipGetLastError());
 }
 
+// ---------------------------------------------------------------------------
+// assignment on FP32 MFMA with exact verification
+// ---------------------------------------------------------------------------
+// km_mfma_top: for a block of 128 points, approximate squared distances to
+// every centroid, (|p|^2 + |c|^2) - 2 p.c with the dot product on
+// v_mfma_f32_32x32x2f32 (128x128 tiles, 32-wide k slices double-buffered in
+// LDS). Each lane keeps, per row it owns, the smallest and second-smallest
+// approximate distance (and the smallest's centroid) over the columns it
+// sees; the lanes and waves are merged at the end.
+//
+// km_mfma_verify: with eps a bound on |approx - exact| for every centroid of
+// the point, every centroid whose exact distance could tie or beat the
+// approximate winner's has approx <= best + 2 eps. If the second-smallest
+// approximation is above best + 2 eps, the winner is the exact argmin
+// (including the lower-index tie rule, since a tied centroid would be within
+// 2 eps too); its exact distance is recomputed with the reference's own
+// arithmetic. Other points are listed and take the exact VALU scan.
+//
+// eps: the fp32 dot product and norms over d terms, the final two roundings
+// and the exact sequential (or 8-lane) sum of squares each stay within
+// (2d + 6) * 2^-24 * (|p| + max|c|)^2; twice that is used.
+constexpr int KA_M = 128, KA_N = 128, KA_K = 32, KA_LDR = KA_K + 4;
+
+__global__ __launch_bounds__(256) void km_row_norms(const float* __restrict__ P, int ldp,
+                                                    const uint32_t* __restrict__ rows, int n, int dim,
+                                                    float* __restrict__ out) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float* pr = P + (size_t)(rows ? rows[i] : (uint32_t)i) * ldp;
+  float s = 0.0f;
+  for (int j = 0; j < dim; ++j) s += pr[j] * pr[j];
+  out[i] = s;
+}
+
+__global__ __launch_bounds__(1024) void km_max_of(const float* __restrict__ v, int n, float* __restrict__ out) {
+  __shared__ float sh[1024];
+  float m = 0.0f;
+  for (int i = threadIdx.x; i < n; i += 1024) m = fmaxf(m, v[i]);
+  sh[threadIdx.x] = m;
+  __syncthreads();
+  for (int o = 512; o > 0; o >>= 1) {
+    if (threadIdx.x < o) sh[threadIdx.x] = fmaxf(sh[threadIdx.x], sh[threadIdx.x + o]);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[0] = sh[0];
+}
+
+__global__ __launch_bounds__(256, 2) void km_mfma_top(const float* __restrict__ P, int ldp,
+                                                      const uint32_t* __restrict__ rows, int n, int dim,
+                                                      const float* __restrict__ C, int ldc, int k,
+                                                      const float* __restrict__ pn, const float* __restrict__ cn,
+                                                      uint32_t* __restrict__ best_idx, float* __restrict__ best,
+                                                      float* __restrict__ second) {
+  // k slices (sA, sB) and, after each tile's k loop, the tile's dot
+  // products (dt, [KA_M][KA_N + 1]) share one LDS buffer
+  constexpr int SLICE = KA_M * KA_LDR, DT_LD = KA_N + 1;
+  static_assert(KA_M * DT_LD <= 4 * SLICE, "tile of dot products fits the slice buffers");
+  __shared__ __align__(16) float smem[4 * SLICE];
+  __shared__ float spn[KA_M], scn[KA_N];
+  float* dt = smem;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int h = lane >> 5, r = lane & 31;
+  const int wm = (wid >> 1) * 64, wn = (wid & 1) * 64;
+  const int p0 = blockIdx.x * KA_M;
+  for (int i = tid; i < KA_M; i += 256) spn[i] = p0 + i < n ? pn[p0 + i] : 0.0f;
+  const int lr = tid >> 3, lc = (tid & 7) * 4;
+  const float* prow[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int p = p0 + lr + 32 * u;
+    prow[u] = p < n ? P + (size_t)(rows ? rows[p] : (uint32_t)p) * ldp : nullptr;
+  }
+  const int nK = (dim + KA_K - 1) / KA_K;
+  // this thread scans row tid/2, columns 2m + (tid&1) of every tile
+  const int my_row = tid >> 1, my_par = tid & 1;
+  float b1 = INFINITY, b2 = INFINITY;
+  int i1 = 0;
+  for (int n0 = 0; n0 < k; n0 += KA_N) {
+    f16v acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+    float4 ra[4], rb[4];
+    auto gload = [&](int k0) {
+      const int kc = k0 + lc;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int c = n0 + lr + 32 * u;
+        ra[u] = (prow[u] && kc < dim) ? *reinterpret_cast<const float4*>(prow[u] + kc) : make_float4(0.f, 0.f, 0.f, 0.f);
+        rb[u] = (c < k && kc < dim) ? *reinterpret_cast<const float4*>(C + (size_t)c * ldc + kc)
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int row = lr + 32 * u;
+        *reinterpret_cast<float4*>(&smem[buf * SLICE + row * KA_LDR + lc]) = ra[u];
+        *reinterpret_cast<float4*>(&smem[(2 + buf) * SLICE + row * KA_LDR + lc]) = rb[u];
+      }
+    };
+    gload(0);
+    __syncthreads();  // the previous tile's scan of dt is done
+    lstore(0);
+    if (tid < KA_N) scn[tid] = n0 + tid < k ? cn[n0 + tid] : 0.0f;
+    __syncthreads();
+    for (int kt = 0; kt < nK; ++kt) {
+      const int cur = kt & 1;
+      if (kt + 1 < nK) gload((kt + 1) * KA_K);
+      // lane (h, r) feeds k = h*16 + kk of row r; A and B agree on that map
+      const float* a0p = &smem[cur * SLICE + (wm + r) * KA_LDR + h * 16];
+      const float* a1p = &smem[cur * SLICE + (wm + 32 + r) * KA_LDR + h * 16];
+      const float* b0p = &smem[(2 + cur) * SLICE + (wn + r) * KA_LDR + h * 16];
+      const float* b1p = &smem[(2 + cur) * SLICE + (wn + 32 + r) * KA_LDR + h * 16];
+#pragma unroll
+      for (int k4 = 0; k4 < 4; ++k4) {
+        const float4 a0 = *reinterpret_cast<const float4*>(a0p + k4 * 4);
+        const float4 a1 = *reinterpret_cast<const float4*>(a1p + k4 * 4);
+        const float4 q0 = *reinterpret_cast<const float4*>(b0p + k4 * 4);
+        const float4 q1 = *reinterpret_cast<const float4*>(b1p + k4 * 4);
+        const float av0[4] = {a0.x, a0.y, a0.z, a0.w}, av1[4] = {a1.x, a1.y, a1.z, a1.w};
+        const float bv0[4] = {q0.x, q0.y, q0.z, q0.w}, bv1[4] = {q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(av0[t], bv0[t], acc[0][0], 0, 0, 0);
+          acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(av0[t], bv1[t], acc[0][1], 0, 0, 0);
+          acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(av1[t], bv0[t], acc[1][0], 0, 0, 0);
+          acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(av1[t], bv1[t], acc[1][1], 0, 0, 0);
+        }
+      }
+      if (kt + 1 < nK) lstore(cur ^ 1);
+      __syncthreads();
+    }
+    // the tile's dot products to LDS, then each thread scans its row's
+    // columns in ascending order (strict < keeps the first of equal values)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          dt[(wm + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3)) * DT_LD + wn + j * 32 + r] = acc[i][j][v];
+    __syncthreads();
+    const float prn = spn[my_row];
+    const float* drow = dt + my_row * DT_LD;
+    const int cols = min(KA_N, k - n0);
+    for (int m = my_par; m < cols; m += 2) {
+      const float x = (prn + scn[m]) - 2.0f * drow[m];
+      if (x < b1) {
+        b2 = fminf(b1, b2);  // keeps a -inf mark
+        b1 = x;
+        i1 = n0 + m;
+      } else if (x < b2) {
+        b2 = x;
+      } else if (!(x == x)) {
+        b2 = -INFINITY;  // NaN: the point takes the exact scan
+      }
+    }
+  }
+  // merge the two threads of each row
+  const float y1 = __shfl_xor(b1, 1, WAVE), y2 = __shfl_xor(b2, 1, WAVE);
+  const int yi = __shfl_xor(i1, 1, WAVE);
+  if (my_par == 0 && p0 + my_row < n) {
+    const bool take = y1 < b1 || (y1 == b1 && yi < i1);
+    best[p0 + my_row] = take ? y1 : b1;
+    best_idx[p0 + my_row] = (uint32_t)(take ? yi : i1);
+    second[p0 + my_row] = fminf(take ? b1 : y1, fminf(b2, y2));
+  }
+}
+
+template <bool UNR>
+__global__ __launch_bounds__(256) void km_mfma_verify(const float* __restrict__ P, int ldp,
+                                                      const uint32_t* __restrict__ rows, int n, int dim,
+                                                      const float* __restrict__ C, int ldc,
+                                                      const float* __restrict__ pn, const float* __restrict__ cmax,
+                                                      const uint32_t* __restrict__ best_idx,
+                                                      const float* __restrict__ best, const float* __restrict__ second,
+                                                      uint32_t* __restrict__ assign, float* __restrict__ dist,
+                                                      uint32_t* __restrict__ redo, int* __restrict__ nredo) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float s = (sqrtf(pn[i]) + sqrtf(cmax[0])) * 1.0001f;
+  const float eps = 2.0f * (2.0f * (float)dim + 6.0f) * 5.9604645e-08f * s * s;
+  const float b = best[i];
+  if (second[i] > b + 2.0f * eps) {
+    const uint32_t c = best_idx[i];
+    const float* pr = P + (size_t)(rows ? rows[i] : (uint32_t)i) * ldp;
+    assign[i] = c;
+    if (dist) dist[i] = point_dist<0, UNR>(pr, C + (size_t)c * ldc, dim);
+  } else {
+    redo[atomicAdd(nredo, 1)] = (uint32_t)i;
+  }
+}
+
+__global__ void km_scatter_redo(const uint32_t* __restrict__ redo, int m, const uint32_t* __restrict__ a,
+                                const float* __restrict__ d, uint32_t* __restrict__ assign, float* __restrict__ dist) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= m) return;
+  assign[redo[t]] = a[t];
+  if (dist) dist[redo[t]] = d[t];
+}
+
+__global__ void km_compose_rows(const uint32_t* __restrict__ redo, int m, const uint32_t* __restrict__ rows,
+                                uint32_t* __restrict__ out) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < m) out[t] = rows ? rows[redo[t]] : redo[t];
+}
+
+// Points with enough work for the matrix cores (and float4-aligned rows)
+// take the MFMA pass; the exact VALU scan serves the rest and the points the
+// MFMA pass cannot certify.
 void nearest_device(const float* P, int ldp, const uint32_t* rows, size_t n, int dim, const float* C, int ldc,
                     size_t k, bool unrolled, uint32_t* assign, float* dist, hipStream_t s) {
+  g_last_redo = 0;
   if (n == 0) return;
+  const bool aligned = ldp % 4 == 0 && ldc % 4 == 0 && dim % 4 == 0 && ((uintptr_t)P & 15) == 0 &&
+                       ((uintptr_t)C & 15) == 0;
+  if (!(aligned && dim >= 32 && k >= 64 && n >= 4096)) {
+    if (unrolled)
+      launch_assign<true>(P, ldp, rows, n, dim, C, ldc, k, assign, dist, s);
+    else
+      launch_assign<false>(P, ldp, rows, n, dim, C, ldc, k, assign, dist, s);
+    return;
+  }
+  DevBuf<float> pn(n), cn(k), cmax(1), best(n), second(n);
+  DevBuf<uint32_t> bidx(n), redo(n);
+  DevBuf<int> nredo(1);
+  hipLaunchKernelGGL(km_row_norms, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, P, ldp, rows, (int)n, dim,
+                     pn.p);
+  hipLaunchKernelGGL(km_row_norms, dim3((unsigned)((k + 255) / 256)), dim3(256), 0, s, C, ldc,
+                     (const uint32_t*)nullptr, (int)k, dim, cn.p);
+  hipLaunchKernelGGL(km_max_of, dim3(1), dim3(1024), 0, s, cn.p, (int)k, cmax.p);
+  hipLaunchKernelGGL(km_mfma_top, dim3((unsigned)((n + KA_M - 1) / KA_M)), dim3(256), 0, s, P, ldp, rows, (int)n,
+                     dim, C, ldc, (int)k, pn.p, cn.p, bidx.p, best.p, second.p);
+  PXG_HIP(hipMemsetAsync(nredo.p, 0, 4, s));
+  const dim3 g((unsigned)((n + 255) / 256));
   if (unrolled)
-    launch_assign<true>(P, ldp, rows, n, dim, C, ldc, k, assign, dist, s);
+    hipLaunchKernelGGL(km_mfma_verify<true>, g, dim3(256), 0, s, P, ldp, rows, (int)n, dim, C, ldc, pn.p, cmax.p,
+                       bidx.p, best.p, second.p, assign, dist, redo.p, nredo.p);
   else
-    launch_assign<false>(P, ldp, rows, n, dim, C, ldc, k, assign, dist, s);
+    hipLaunchKernelGGL(km_mfma_verify<false>, g, dim3(256), 0, s, P, ldp, rows, (int)n, dim, C, ldc, pn.p, cmax.p,
+                       bidx.p, best.p, second.p, assign, dist, redo.p, nredo.p);
+  PXG_HIP(hipGetLastError());
+  int m = 0;
+  PXG_HIP(hipMemcpyAsync(&m, nredo.p, 4, hipMemcpyDeviceToHost, s));
+  PXG_HIP(hipStreamSynchronize(s));
+  g_last_redo = (size_t)m;
+  if (m == 0) return;
+  // the uncertified points: exact scan over their rows, results scattered back
+  DevBuf<uint32_t> rrows(m), ra(m);
+  DevBuf<float> rd(m);
+  hipLaunchKernelGGL(km_compose_rows, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, s, redo.p, m, rows, rrows.p);
+  if (unrolled)
+    launch_assign<true>(P, ldp, rrows.p, m, dim, C, ldc, k, ra.p, rd.p, s);
+  else
+    launch_assign<false>(P, ldp, rrows.p, m, dim, C, ldc, k, ra.p, rd.p, s);
+  hipLaunchKernelGGL(km_scatter_redo, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, s, redo.p, m, ra.p, rd.p,
+                     assign, dist);
+  PXG_HIP(hipGetLastError());
 }
 
 // ---------------------------------------------------------------------------
@@ -563,31 +821,56 @@ size_t kmeans_pp_device(const float* P, size_t n, int dim, int ldp, size_t k, Ch
 // ---------------------------------------------------------------------------
 // update step
 // ---------------------------------------------------------------------------
-__global__ void km_changed_counts(const uint32_t* __restrict__ a, uint32_t* __restrict__ prev, int n,
-                                  uint32_t* __restrict__ counts, int* __restrict__ changed, uint32_t* __restrict__ idx) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const uint32_t c = a[i];
-  if (prev[i] != c) {
-    *changed = 1;
-    prev[i] = c;
+// Records changed assignments (kmeans.rs:93-96), counts members per cluster
+// (a block histogram in LDS when k fits) and writes the identity permutation
+// the radix sort carries along. 2048 points per block.
+constexpr int KM_HIST = 8192;
+__global__ __launch_bounds__(256) void km_changed_counts(const uint32_t* __restrict__ a, uint32_t* __restrict__ prev,
+                                                         int n, int k, uint32_t* __restrict__ counts,
+                                                         int* __restrict__ changed, uint32_t* __restrict__ idx) {
+  __shared__ uint32_t hist[KM_HIST];
+  __shared__ int any;
+  const bool local = k <= KM_HIST;
+  if (local)
+    for (int c = threadIdx.x; c < k; c += 256) hist[c] = 0;
+  if (threadIdx.x == 0) any = 0;
+  __syncthreads();
+  const int end = min(n, (int)(blockIdx.x + 1) * 2048);
+  for (int i = blockIdx.x * 2048 + threadIdx.x; i < end; i += 256) {
+    const uint32_t c = a[i];
+    if (prev[i] != c) {
+      any = 1;
+      prev[i] = c;
+    }
+    if (local)
+      atomicAdd(&hist[c], 1u);
+    else
+      atomicAdd(&counts[c], 1u);
+    idx[i] = (uint32_t)i;
   }
-  atomicAdd(&counts[c], 1u);
-  idx[i] = (uint32_t)i;
+  __syncthreads();
+  if (local)
+    for (int c = threadIdx.x; c < k; c += 256)
+      if (hist[c]) atomicAdd(&counts[c], hist[c]);
+  if (threadIdx.x == 0 && any) *changed = 1;
 }
 
 // Cluster means (kmeans.rs:104-135): one block per (cluster, JW-coordinate
 // slice), 256/JW member groups. Each (cluster, coordinate) f64 sum carries
-// the exactness certificate; where it fails, one thread redoes it in point
-// order. The mean is (float)(sum * (1.0 / count)).
+// the exactness certificate; where it fails for any coordinate of the slice,
+// the block stages the members' values through LDS in point order and one
+// thread per coordinate redoes the sum sequentially. The mean is
+// (float)(sum * (1.0 / count)).
 template <int JW>
 __global__ __launch_bounds__(256) void km_sums(const float* __restrict__ P, int ldp, int dim,
                                                const uint32_t* __restrict__ members,
                                                const uint32_t* __restrict__ offsets,
                                                const uint32_t* __restrict__ counts, int k, float* __restrict__ newc) {
-  constexpr int G = 256 / JW;
+  constexpr int G = 256 / JW, ROWS = 8192 / JW;  // 32 KiB of staged values
   __shared__ double ss[G][JW], sa[G][JW];
   __shared__ int se[G][JW];
+  __shared__ float stage[ROWS][JW];
+  __shared__ int redo;
   const int c = blockIdx.x;
   const int jl = threadIdx.x % JW, g = threadIdx.x / JW;
   const int j = blockIdx.y * JW + jl;
@@ -606,17 +889,32 @@ __global__ __launch_bounds__(256) void km_sums(const float* __restrict__ P, int 
   ss[g][jl] = s;
   sa[g][jl] = a;
   se[g][jl] = e;
+  if (threadIdx.x == 0) redo = 0;
   __syncthreads();
+  bool exact = true;
   if (g == 0 && j < dim) {
     for (int q = 1; q < G; ++q) {
       s += ss[q][jl];
       a += sa[q][jl];
       e = min(e, se[q][jl]);
     }
-    if (!sums_exact(a, e)) {
-      s = 0.0;
-      for (uint32_t m = 0; m < cnt; ++m) s += (double)P[(size_t)members[off + m] * ldp + j];
+    exact = sums_exact(a, e);
+    if (!exact) redo = 1;
+  }
+  __syncthreads();
+  if (redo) {
+    double q = 0.0;
+    for (uint32_t m0 = 0; m0 < cnt; m0 += ROWS) {
+      const uint32_t rows = min((uint32_t)ROWS, cnt - m0);
+      __syncthreads();
+      for (uint32_t r = g; r < rows; r += G) stage[r][jl] = j < dim ? P[(size_t)members[off + m0 + r] * ldp + j] : 0.0f;
+      __syncthreads();
+      if (g == 0 && !exact)
+        for (uint32_t r = 0; r < rows; ++r) q += (double)stage[r][jl];
     }
+    if (g == 0 && !exact) s = q;
+  }
+  if (g == 0 && j < dim) {
     const double inv = 1.0 / (double)cnt;
     newc[(size_t)c * dim + j] = (float)(s * inv);
   }
@@ -705,7 +1003,8 @@ KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req
     if (!sums.last_exact) ++out.inexact_sums;
     PXG_HIP(hipMemsetAsync(changed.p, 0, 4, s));
     PXG_HIP(hipMemsetAsync(counts.p, 0, k * 4, s));
-    hipLaunchKernelGGL(km_changed_counts, gn, dim3(256), 0, s, assign.p, prev.p, (int)n, counts.p, changed.p, idx.p);
+    hipLaunchKernelGGL(km_changed_counts, dim3((unsigned)((n + 2047) / 2048)), dim3(256), 0, s, assign.p, prev.p,
+                       (int)n, (int)k, counts.p, changed.p, idx.p);
     PXG_HIP(hipGetLastError());
     int h_changed = 0;
     PXG_HIP(hipMemcpyAsync(&h_changed, changed.p, 4, hipMemcpyDeviceToHost, s));
@@ -753,8 +1052,10 @@ KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req
   }
   PXG_HIP(hipStreamSynchronize(s));
   if (train_verbose())
-    std::fprintf(stderr, "[pxg kmeans] n=%zu dim=%d k=%zu: seeding %.3fs, lloyd %zu it %.3fs, %zu empty reseeds\n", n,
-                 dim, k, t_seeded - t_start, out.iterations, now_s() - t_seeded, empties);
+    std::fprintf(stderr,
+                 "[pxg kmeans] n=%zu dim=%d k=%zu: seeding %.3fs, lloyd %zu it %.3fs, %zu empty reseeds, %zu points "
+                 "rescanned exactly in the last assignment\n",
+                 n, dim, k, t_seeded - t_start, out.iterations, now_s() - t_seeded, empties, g_last_redo);
   return out;
 }
 

@@ -122,6 +122,26 @@ def test_gpu_training_matches_oracle(gpu, metric):
     assert_same(idx.search_batch(q, 10, nprobe=3), want)
 
 
+def test_gpu_training_on_matrix_cores_matches_oracle(gpu):
+    """8000 sampled points into 96 lists: the Lloyd assignments and the
+    encode pass go through the MFMA nearest-centroid pass and must still be
+    the oracle's bit for bit."""
+    px = gpu
+    n, dim, nlist, m = 8000, 64, 96, 8
+    data = corpus(n, dim, 90) + np.random.default_rng(12).standard_normal((n, dim)).astype(np.float32) * 0.3
+    cfg = px.IvfPqConfig(nlist, m).with_train_threshold(1 << 62).with_seed(3).with_max_iterations(8) \
+        .with_training_sample(8000)
+    idx = build(px, data, cfg)
+    rep = idx.train()
+    cents, books, report = orc.ivf_train(data, nlist, m, max_iter=8, training_sample=8000, seed=3)
+    gcents, gbooks, gcodes, glist = idx.parts()
+    assert np.array_equal(gcents.view(np.uint32), cents.view(np.uint32))
+    assert np.array_equal(gbooks.view(np.uint32), books.view(np.uint32))
+    codes, list_of = orc.ivf_encode(data, cents, books, m)
+    assert np.array_equal(gcodes, codes) and np.array_equal(glist, list_of)
+    assert rep.coarse_inertia == report[0] and rep.residual_inertia == report[2]
+
+
 # --- ivfpq.rs:1282-1654 -------------------------------------------------------------
 def test_rejects_metrics_it_cannot_serve(gpu):
     px = gpu

@@ -114,6 +114,27 @@ def test_assign_matches_oracle(gpu):
         assert np.array_equal(bits(d), bits(wd))
 
 
+def test_assign_matrix_core_path_matches_oracle(gpu):
+    """Enough points and centroids for the MFMA pass: approximate winners are
+    certified against the runner-up and rescored exactly; duplicated
+    centroids (exact ties, lower index wins), points equidistant from two
+    centroids and rows whose norms overflow take the exact scan."""
+    px = gpu
+    rng = np.random.default_rng(9)
+    for dim in (32, 96, 128):
+        p = clustered(rng, 9000, dim, 40, 0.3)
+        c = p[rng.choice(9000, 300, replace=False)] + rng.standard_normal((300, dim)).astype(np.float32) * 0.05
+        c[5] = c[9]
+        c[17] = c[250]
+        p[:40] = c[5] + np.float32(0.01)                      # nearest: the tied pair 5/9
+        p[40:80] = (c[20] + c[21]) * np.float32(0.5)          # on a bisector
+        p[80, :4] = np.float32(3e18)                          # |p|^2 overflows
+        a, d = px.kmeans_assign(p, c)
+        wa, wd = orc.kmeans_assign(p, c)
+        assert np.array_equal(a, wa), dim
+        assert np.array_equal(bits(d), bits(wd)), dim
+
+
 def test_reference_kmeans_properties(gpu):  # kmeans.rs:271-336
     px = gpu
     r = px.kmeans(blobs(), 2, 3, 25, 0x00C0FFEE)
