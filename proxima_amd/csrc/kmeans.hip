@@ -190,15 +190,24 @@ static void launch_assign(const float* P, int ldp, const uint32_t* rows, size_t 
 // (2d + 6) * 2^-24 * (|p| + max|c|)^2; twice that is used.
 constexpr int KA_M = 128, KA_N = 128, KA_K = 32, KA_LDR = KA_K + 4;
 
+// |row|^2 in fp32 (any order; it only feeds the approximation): eight lanes
+// per row, float4 loads (rows 16-byte aligned, dim a multiple of 4).
 __global__ __launch_bounds__(256) void km_row_norms(const float* __restrict__ P, int ldp,
                                                     const uint32_t* __restrict__ rows, int n, int dim,
                                                     float* __restrict__ out) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= n) return;
-  const float* pr = P + (size_t)(rows ? rows[i] : (uint32_t)i) * ldp;
+  const int i = blockIdx.x * 32 + (threadIdx.x >> 3), sub = threadIdx.x & 7;
   float s = 0.0f;
-  for (int j = 0; j < dim; ++j) s += pr[j] * pr[j];
-  out[i] = s;
+  if (i < n) {
+    const float* pr = P + (size_t)(rows ? rows[i] : (uint32_t)i) * ldp;
+    for (int j = sub * 4; j < dim; j += 32) {
+      const float4 x = *reinterpret_cast<const float4*>(pr + j);
+      s += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+    }
+  }
+  s += __shfl_xor(s, 4, WAVE);
+  s += __shfl_xor(s, 2, WAVE);
+  s += __shfl_xor(s, 1, WAVE);
+  if (i < n && sub == 0) out[i] = s;
 }
 
 __global__ __launch_bounds__(1024) void km_max_of(const float* __restrict__ v, int n, float* __restrict__ out) {
@@ -349,18 +358,143 @@ __global__ __launch_bounds__(256) void km_mfma_verify(const float* __restrict__ 
                                                       const float* __restrict__ best, const float* __restrict__ second,
                                                       uint32_t* __restrict__ assign, float* __restrict__ dist,
                                                       uint32_t* __restrict__ redo, int* __restrict__ nredo) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= n) return;
-  const float s = (sqrtf(pn[i]) + sqrtf(cmax[0])) * 1.0001f;
-  const float eps = 2.0f * (2.0f * (float)dim + 6.0f) * 5.9604645e-08f * s * s;
-  const float b = best[i];
-  if (second[i] > b + 2.0f * eps) {
-    const uint32_t c = best_idx[i];
-    const float* pr = P + (size_t)(rows ? rows[i] : (uint32_t)i) * ldp;
-    assign[i] = c;
-    if (dist) dist[i] = point_dist<0, UNR>(pr, C + (size_t)c * ldc, dim);
+  // the block's 256 points and their winning centroids, staged through LDS
+  // 32 coordinates at a time (eight lanes per 128-byte row slice)
+  __shared__ float tp[256 * 33], tc[256 * 33];
+  __shared__ uint32_t sr[256], sc[256];
+  const int t = threadIdx.x, i0 = blockIdx.x * 256, i = i0 + t;
+  bool ok = false;
+  if (i < n) {
+    const float s = (sqrtf(pn[i]) + sqrtf(cmax[0])) * 1.0001f;
+    const float eps = 2.0f * (2.0f * (float)dim + 6.0f) * 5.9604645e-08f * s * s;
+    ok = second[i] > best[i] + 2.0f * eps;
+    if (!ok) redo[atomicAdd(nredo, 1)] = (uint32_t)i;
+    sr[t] = rows ? rows[i] : (uint32_t)i;
+    sc[t] = best_idx[i];
   } else {
-    redo[atomicAdd(nredo, 1)] = (uint32_t)i;
+    sr[t] = 0;
+    sc[t] = 0;
+  }
+  float sum = 0.0f, acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  const int ch8 = (dim >> 3) << 3;
+  for (int j0 = 0; j0 < dim; j0 += 32) {
+    const int w = min(32, dim - j0);
+    __syncthreads();
+    for (int f = t; f < 256 * 8; f += 256) {
+      const int r = f >> 3, c4 = (f & 7) * 4;
+      if (c4 < w && i0 + r < n) {
+        const float4 x = *reinterpret_cast<const float4*>(P + (size_t)sr[r] * ldp + j0 + c4);
+        const float4 y = *reinterpret_cast<const float4*>(C + (size_t)sc[r] * ldc + j0 + c4);
+        float* dp = tp + r * 33 + c4;
+        float* dc = tc + r * 33 + c4;
+        dp[0] = x.x; dp[1] = x.y; dp[2] = x.z; dp[3] = x.w;
+        dc[0] = y.x; dc[1] = y.y; dc[2] = y.z; dc[3] = y.w;
+      }
+    }
+    __syncthreads();
+    if (ok) {
+      const float* a = tp + t * 33;
+      const float* b = tc + t * 33;
+      int jj = 0;
+      if constexpr (UNR) {
+        // squared_euclidean_unrolled: lane j & 7 for the 8-wide chunks
+        // (j0 and ch8 are multiples of 8), then the sequential tail
+        for (; jj + 8 <= w && j0 + jj < ch8; jj += 8)
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const float d = a[jj + u] - b[jj + u];
+            acc[u] += d * d;
+          }
+      }
+      for (; jj < w; ++jj) {
+        const float d = a[jj] - b[jj];
+        sum += d * d;  // squared(), kmeans.rs:234-241 (or the unrolled tail)
+      }
+    }
+  }
+  if (ok) {
+    assign[i] = sc[t];
+    if (dist) {
+      if constexpr (UNR)
+        dist[i] = (((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]))) + sum;
+      else
+        dist[i] = sum;
+    }
+  }
+}
+
+// Exact nearest centroid for the listed points: one wave per point, lane l
+// scans centroids l, l+64, ... in order (strict <), and the wave keeps the
+// smallest distance with the lowest index: the reference's sequential scan.
+// The point is staged in LDS; centroid rows are read as float4 (rows
+// 16-byte aligned, dim a multiple of 4, dim <= KW_DMAX).
+constexpr int KW_DMAX = 2048;
+template <bool UNR>
+__global__ __launch_bounds__(256) void km_exact_wave(const float* __restrict__ P, int ldp,
+                                                     const uint32_t* __restrict__ rows, int m, int dim,
+                                                     const float* __restrict__ C, int ldc, int k,
+                                                     uint32_t* __restrict__ assign, float* __restrict__ dist) {
+  __shared__ __align__(16) float sp[4][KW_DMAX];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, p = blockIdx.x * 4 + w;
+  if (p >= m) return;
+  const float* pr = P + (size_t)rows[p] * ldp;
+  for (int j = lane; j < dim; j += 64) sp[w][j] = pr[j];
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  const float* x = sp[w];
+  const int ch8 = (dim >> 3) << 3;
+  float bd = INFINITY;
+  int bi = 0;
+  for (int c = lane; c < k; c += 64) {
+    const float* cr = C + (size_t)c * ldc;
+    float sum = 0.0f;
+    if constexpr (UNR) {
+      float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      for (int j = 0; j < ch8; j += 8) {
+        const float4 c0 = *reinterpret_cast<const float4*>(cr + j);
+        const float4 c1 = *reinterpret_cast<const float4*>(cr + j + 4);
+        const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const float d = x[j + u] - cv[u];
+          acc[u] += d * d;
+        }
+      }
+      for (int j = ch8; j < dim; ++j) {
+        const float d = x[j] - cr[j];
+        sum += d * d;
+      }
+      sum = (((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]))) + sum;
+    } else {
+      for (int j = 0; j < dim; j += 4) {
+        const float4 cv = *reinterpret_cast<const float4*>(cr + j);
+        float d = x[j] - cv.x;
+        sum += d * d;
+        d = x[j + 1] - cv.y;
+        sum += d * d;
+        d = x[j + 2] - cv.z;
+        sum += d * d;
+        d = x[j + 3] - cv.w;
+        sum += d * d;
+      }
+    }
+    if (sum < bd) {
+      bd = sum;
+      bi = c;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float od = __shfl_xor(bd, o, WAVE);
+    const int oi = __shfl_xor(bi, o, WAVE);
+    if (od < bd || (od == bd && oi < bi)) {
+      bd = od;
+      bi = oi;
+    }
+  }
+  if (lane == 0) {
+    assign[p] = (uint32_t)bi;
+    dist[p] = bd;
   }
 }
 
@@ -387,7 +521,7 @@ void nearest_device(const float* P, int ldp, const uint32_t* rows, size_t n, int
   if (n == 0) return;
   const bool aligned = ldp % 4 == 0 && ldc % 4 == 0 && dim % 4 == 0 && ((uintptr_t)P & 15) == 0 &&
                        ((uintptr_t)C & 15) == 0;
-  if (!(aligned && dim >= 32 && k >= 64 && n >= 4096)) {
+  if (!(aligned && dim >= 32 && dim <= KW_DMAX && k >= 64 && n >= 4096)) {
     if (unrolled)
       launch_assign<true>(P, ldp, rows, n, dim, C, ldc, k, assign, dist, s);
     else
@@ -397,9 +531,9 @@ void nearest_device(const float* P, int ldp, const uint32_t* rows, size_t n, int
   DevBuf<float> pn(n), cn(k), cmax(1), best(n), second(n);
   DevBuf<uint32_t> bidx(n), redo(n);
   DevBuf<int> nredo(1);
-  hipLaunchKernelGGL(km_row_norms, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, P, ldp, rows, (int)n, dim,
+  hipLaunchKernelGGL(km_row_norms, dim3((unsigned)((n + 31) / 32)), dim3(256), 0, s, P, ldp, rows, (int)n, dim,
                      pn.p);
-  hipLaunchKernelGGL(km_row_norms, dim3((unsigned)((k + 255) / 256)), dim3(256), 0, s, C, ldc,
+  hipLaunchKernelGGL(km_row_norms, dim3((unsigned)((k + 31) / 32)), dim3(256), 0, s, C, ldc,
                      (const uint32_t*)nullptr, (int)k, dim, cn.p);
   hipLaunchKernelGGL(km_max_of, dim3(1), dim3(1024), 0, s, cn.p, (int)k, cmax.p);
   hipLaunchKernelGGL(km_mfma_top, dim3((unsigned)((n + KA_M - 1) / KA_M)), dim3(256), 0, s, P, ldp, rows, (int)n,
@@ -423,9 +557,11 @@ void nearest_device(const float* P, int ldp, const uint32_t* rows, size_t n, int
   DevBuf<float> rd(m);
   hipLaunchKernelGGL(km_compose_rows, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, s, redo.p, m, rows, rrows.p);
   if (unrolled)
-    launch_assign<true>(P, ldp, rrows.p, m, dim, C, ldc, k, ra.p, rd.p, s);
+    hipLaunchKernelGGL(km_exact_wave<true>, dim3((unsigned)((m + 3) / 4)), dim3(256), 0, s, P, ldp, rrows.p, m, dim, C,
+                       ldc, (int)k, ra.p, rd.p);
   else
-    launch_assign<false>(P, ldp, rrows.p, m, dim, C, ldc, k, ra.p, rd.p, s);
+    hipLaunchKernelGGL(km_exact_wave<false>, dim3((unsigned)((m + 3) / 4)), dim3(256), 0, s, P, ldp, rrows.p, m, dim,
+                       C, ldc, (int)k, ra.p, rd.p);
   hipLaunchKernelGGL(km_scatter_redo, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, s, redo.p, m, ra.p, rd.p,
                      assign, dist);
   PXG_HIP(hipGetLastError());
@@ -608,23 +744,35 @@ __global__ __launch_bounds__(256) void km_pp_round(const float* __restrict__ P, 
     for (int j = t; j < dim; j += 256) cs[j] = c[j];
   const float* cc = staged_c ? cs : c;
   float sum = 0.0f;
+  // vec4: 8 threads per 32-coordinate row slice, 16 bytes each (w is a
+  // multiple of 4); the next slice is loaded into registers while this one
+  // is scored
+  constexpr int PF = PP_ROWS * 8 / 256;
+  float4 nx[PF];
+  auto gload = [&](int j0) {
+    const int w = min(32, dim - j0);
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      const int f = t + 256 * u, r = f >> 3, c4 = (f & 7) * 4;
+      nx[u] = (c4 < w && r0 + r < n) ? *reinterpret_cast<const float4*>(P + (size_t)(r0 + r) * ldp + j0 + c4)
+                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  if (vec4) gload(0);
   for (int j0 = 0; j0 < dim; j0 += 32) {
     const int w = min(32, dim - j0);
     __syncthreads();
     if (vec4) {
-      // w is a multiple of 4: 8 threads per row slice, 16 bytes each
-      for (int f = t; f < PP_ROWS * 8; f += 256) {
-        const int r = f >> 3, c4 = (f & 7) * 4;
-        if (c4 < w) {
-          float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-          if (r0 + r < n) x = *reinterpret_cast<const float4*>(P + (size_t)(r0 + r) * ldp + j0 + c4);
-          float* d = tile + r * 33 + c4;
-          d[0] = x.x;
-          d[1] = x.y;
-          d[2] = x.z;
-          d[3] = x.w;
-        }
+#pragma unroll
+      for (int u = 0; u < PF; ++u) {
+        const int f = t + 256 * u, r = f >> 3, c4 = (f & 7) * 4;
+        float* d = tile + r * 33 + c4;
+        d[0] = nx[u].x;
+        d[1] = nx[u].y;
+        d[2] = nx[u].z;
+        d[3] = nx[u].w;
       }
+      if (j0 + 32 < dim) gload(j0 + 32);
     } else {
       for (int f = t; f < PP_ROWS * 32; f += 256) {
         const int r = f >> 5, cidx = f & 31;
@@ -861,12 +1009,12 @@ __global__ __launch_bounds__(256) void km_changed_counts(const uint32_t* __restr
 // the block stages the members' values through LDS in point order and one
 // thread per coordinate redoes the sum sequentially. The mean is
 // (float)(sum * (1.0 / count)).
-template <int JW>
-__global__ __launch_bounds__(256) void km_sums(const float* __restrict__ P, int ldp, int dim,
+template <int JW, int NT>
+__global__ __launch_bounds__(NT) void km_sums(const float* __restrict__ P, int ldp, int dim,
                                                const uint32_t* __restrict__ members,
                                                const uint32_t* __restrict__ offsets,
                                                const uint32_t* __restrict__ counts, int k, float* __restrict__ newc) {
-  constexpr int G = 256 / JW, ROWS = 8192 / JW;  // 32 KiB of staged values
+  constexpr int G = NT / JW, ROWS = 8192 / JW;  // 32 KiB of staged values
   __shared__ double ss[G][JW], sa[G][JW];
   __shared__ int se[G][JW];
   __shared__ float stage[ROWS][JW];
@@ -1021,15 +1169,20 @@ KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req
     }
     PXG_HIP(hipMemcpyAsync(offsets.p, h_off.data(), k * 4, hipMemcpyHostToDevice, s));
     PXG_HIP(hipMemcpyAsync(newc.p, cents.p, k * dim * 4, hipMemcpyDeviceToDevice, s));
-    if (dim <= 8)
-      hipLaunchKernelGGL(km_sums<8>, dim3((unsigned)k, 1), dim3(256), 0, s, P, ldp, dim, members.p, offsets.p,
+    // more member groups per block when the clusters are few and large
+    const bool wide = n >= 64 * k;
+    if (dim <= 8 && wide)
+      hipLaunchKernelGGL((km_sums<8, 1024>), dim3((unsigned)k, 1), dim3(1024), 0, s, P, ldp, dim, members.p,
+                         offsets.p, counts.p, (int)k, newc.p);
+    else if (dim <= 8)
+      hipLaunchKernelGGL((km_sums<8, 256>), dim3((unsigned)k, 1), dim3(256), 0, s, P, ldp, dim, members.p, offsets.p,
                          counts.p, (int)k, newc.p);
     else if (dim <= 16)
-      hipLaunchKernelGGL(km_sums<16>, dim3((unsigned)k, 1), dim3(256), 0, s, P, ldp, dim, members.p, offsets.p,
-                         counts.p, (int)k, newc.p);
+      hipLaunchKernelGGL((km_sums<16, 256>), dim3((unsigned)k, 1), dim3(256), 0, s, P, ldp, dim, members.p,
+                         offsets.p, counts.p, (int)k, newc.p);
     else
-      hipLaunchKernelGGL(km_sums<32>, dim3((unsigned)k, (unsigned)((dim + 31) / 32)), dim3(256), 0, s, P, ldp, dim,
-                         members.p, offsets.p, counts.p, (int)k, newc.p);
+      hipLaunchKernelGGL((km_sums<32, 256>), dim3((unsigned)k, (unsigned)((dim + 31) / 32)), dim3(256), 0, s, P, ldp,
+                         dim, members.p, offsets.p, counts.p, (int)k, newc.p);
     PXG_HIP(hipGetLastError());
     // empty clusters, ascending, against the partially updated array
     for (size_t c = 0; c < k; ++c) {
