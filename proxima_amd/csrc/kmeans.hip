@@ -33,6 +33,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
+#include <string>
 
 #include "common.hpp"
 #include "device.hpp"
@@ -932,6 +933,29 @@ __global__ void copy_row(const float* __restrict__ src, int ld_src, size_t row, 
   for (int j = threadIdx.x; j < dim; j += blockDim.x) dst[j] = src[row * ld_src + j];
 }
 
+// copy_row with the row index read from device memory
+__global__ void copy_row_at(const float* __restrict__ src, int ld_src, const long long* __restrict__ row, int dim,
+                            float* __restrict__ dst) {
+  const size_t r = (size_t)*row;
+  for (int j = threadIdx.x; j < dim; j += blockDim.x) dst[j] = src[r * ld_src + j];
+}
+
+// a[i] = min(a[i], b[i]); out (if given) receives the result instead of a
+__global__ void km_min_into(float* __restrict__ a, const float* __restrict__ b, int n, float* __restrict__ out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float v = fminf(a[i], b[i]);
+  if (out)
+    out[i] = v;
+  else
+    a[i] = v;
+}
+
+__global__ void km_fill(float* __restrict__ a, int n, float v) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) a[i] = v;
+}
+
 // Returns the number of rounds whose pick used the fixed parallel order
 // instead of the reference's sequential sums (0 whenever the certificate
 // holds or n <= SEQ_SUM_LIMIT).
@@ -1130,6 +1154,7 @@ KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req
     out.inexact_sums += kmeans_pp_device(P, n, dim, ldp, k, *rng, cents.p, s);
   const double t_seeded = now_s();
   size_t empties = 0;
+  std::string empties_per_it;
 
   DevBuf<uint32_t> assign(n), prev(n), counts(k), offsets(k), idx(n), keys_sorted(n), members(n);
   DevBuf<float> dist(n), newc(k * dim), work(k * dim);
@@ -1185,8 +1210,56 @@ KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req
                          dim, members.p, offsets.p, counts.p, (int)k, newc.p);
     PXG_HIP(hipGetLastError());
     // empty clusters, ascending, against the partially updated array
-    for (size_t c = 0; c < k; ++c) {
-      if (h_counts[c] != 0) continue;
+    if (train_verbose()) {
+      size_t e = 0;
+      for (size_t c = 0; c < k; ++c) e += h_counts[c] == 0;
+      empties_per_it += " " + std::to_string(e);
+    }
+    std::vector<size_t> E;
+    for (size_t c = 0; c < k; ++c)
+      if (h_counts[c] == 0) E.push_back(c);
+    const size_t m = E.size();
+    if (m >= 2 && m * n <= ((size_t)1 << 29)) {
+      // Several empty clusters: the nearest distance of a point against the
+      // array seen at empty cluster E[i] is min(L_i, R_i), L_i over the rows
+      // below E[i] (new means and the victims chosen so far), R_i over the
+      // old rows from E[i] on. R_i are suffix minima of exact per-segment
+      // minima over the old rows; L_i grows by the new means between
+      // consecutive empties and by each victim. Minima of exact distances
+      // are exact, so each farthest point is the reference's.
+      empties += m;
+      const int nb = (int)((n + PP_ROWS - 1) / PP_ROWS);
+      DevBuf<float> R(m * n), L(n), tmp(n);
+      DevBuf<double> rps(nb);
+      DevBuf<int> rpe(nb);
+      const dim3 gm((unsigned)((n + 255) / 256));
+      for (size_t ii = m; ii-- > 0;) {
+        const size_t lo = E[ii], hi = ii + 1 < m ? E[ii + 1] : k;
+        nearest_device(P, ldp, nullptr, n, dim, cents.p + lo * dim, dim, hi - lo, false, keys_sorted.p,
+                       R.p + ii * n, s);
+        if (ii + 1 < m)
+          hipLaunchKernelGGL(km_min_into, gm, dim3(256), 0, s, R.p + ii * n, R.p + (ii + 1) * n, (int)n,
+                             (float*)nullptr);
+      }
+      hipLaunchKernelGGL(km_fill, gm, dim3(256), 0, s, L.p, (int)n, INFINITY);
+      const int vec4 = (ldp % 4 == 0 && dim % 4 == 0 && ((uintptr_t)P & 15) == 0) ? 1 : 0;
+      for (size_t ii = 0; ii < m; ++ii) {
+        const size_t lo = ii == 0 ? 0 : E[ii - 1] + 1, hi = E[ii];
+        if (hi > lo) {
+          nearest_device(P, ldp, nullptr, n, dim, newc.p + lo * dim, dim, hi - lo, false, keys_sorted.p, tmp.p, s);
+          hipLaunchKernelGGL(km_min_into, gm, dim3(256), 0, s, L.p, tmp.p, (int)n, (float*)nullptr);
+        }
+        hipLaunchKernelGGL(km_min_into, gm, dim3(256), 0, s, L.p, R.p + ii * n, (int)n, tmp.p);
+        hipLaunchKernelGGL(km_farthest, dim3(1), dim3(1024), 0, s, tmp.p, (int)n, far.p);
+        hipLaunchKernelGGL(copy_row_at, dim3(1), dim3(256), 0, s, P, ldp, far.p, dim, newc.p + E[ii] * dim);
+        if (ii + 1 < m)
+          hipLaunchKernelGGL(km_pp_round, dim3(nb), dim3(256), 0, s, P, ldp, (int)n, dim, newc.p + E[ii] * dim, L.p,
+                             0, rps.p, rpe.p, vec4);
+        PXG_HIP(hipGetLastError());
+      }
+      E.clear();
+    }
+    for (size_t c : E) {
       ++empties;
       PXG_HIP(hipMemcpyAsync(work.p, newc.p, c * dim * 4, hipMemcpyDeviceToDevice, s));
       PXG_HIP(hipMemcpyAsync(work.p + c * dim, cents.p + c * dim, (k - c) * dim * 4, hipMemcpyDeviceToDevice, s));
@@ -1207,8 +1280,9 @@ KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req
   if (train_verbose())
     std::fprintf(stderr,
                  "[pxg kmeans] n=%zu dim=%d k=%zu: seeding %.3fs, lloyd %zu it %.3fs, %zu empty reseeds, %zu points "
-                 "rescanned exactly in the last assignment\n",
-                 n, dim, k, t_seeded - t_start, out.iterations, now_s() - t_seeded, empties, g_last_redo);
+                 "rescanned exactly in the last assignment; empties per iteration:%s\n",
+                 n, dim, k, t_seeded - t_start, out.iterations, now_s() - t_seeded, empties, g_last_redo,
+                 empties_per_it.c_str());
   return out;
 }
 

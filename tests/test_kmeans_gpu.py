@@ -58,6 +58,24 @@ def test_lloyd_from_init_with_empty_clusters(gpu):
     assert got[2] == want[2] and got[3] == want[3]
 
 
+def test_lloyd_several_empty_clusters_in_one_iteration(gpu):
+    """Five centroids that attract nothing, spread over 512: the reseeds of
+    one iteration go through the segmented farthest-point search (exact
+    segment minima over old and new rows, MFMA-sized segments) and must
+    pick the reference's points in order."""
+    px = gpu
+    rng = np.random.default_rng(15)
+    pts = clustered(rng, 9000, 32, 300, 0.4)
+    init = pts[rng.choice(9000, 512, replace=False)].copy()
+    for c, off in ((40, 900.0), (170, -800.0), (171, 700.0), (333, 650.0), (500, -950.0)):
+        init[c] += np.float32(off)
+    got = px.kmeans_lloyd(pts, init, 6)
+    want = orc.kmeans_lloyd(pts, init, 6)
+    assert np.array_equal(bits(got[0]), bits(want[0]))
+    assert np.array_equal(got[1], want[1])
+    assert got[2] == want[2] and got[3] == want[3]
+
+
 def test_kmeans_pp_picks_match(gpu):
     px = gpu
     rng = np.random.default_rng(6)
