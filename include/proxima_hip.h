@@ -243,6 +243,15 @@ int pxg_kmeans_pp(const float* points, uint64_t n, uint32_t dim, uint64_t k, uin
 /* The assignment pass (kmeans.rs:90-97, nearest 200-212). */
 int pxg_kmeans_assign(const float* points, uint64_t n, uint32_t dim, const float* centroids, uint64_t k,
                       uint32_t* assign_out, float* dist_out);
+/* Counters of the calling thread's last k-means run (the last one inside a
+ * pxg_kmeans* or pxg_pq_train* call). No counterpart in the reference; it is
+ * for measurement: time and algorithmic flops (2*n*k*dim per pass) of the
+ * FP32-MFMA distance passes of its assignments, the number of those passes,
+ * the points they could not certify (rescanned exactly), and the f64
+ * point-order sums that had to keep the fixed parallel order. Any pointer may
+ * be NULL. */
+int pxg_kmeans_last_stats(double* mfma_ms, double* mfma_flops, uint64_t* mfma_passes, uint64_t* rescanned,
+                          uint64_t* inexact_sums);
 /* ProductQuantizer::train (product.rs:198-296): codebooks_out holds, per
  * subspace, 256 rows of its width (dim floats x 256 in total). */
 int pxg_pq_train(const float* training, uint64_t n, uint32_t dim, uint64_t subspaces, uint64_t max_iterations,

@@ -671,6 +671,17 @@ def kmeans_device(points, k, max_iterations, seed, centroids_out, assign_out=Non
     return inertia.value, iters.value
 
 
+def kmeans_last_stats():
+    """Counters of this thread's last k-means run (measurement only): MFMA
+    distance-pass time (ms) and algorithmic flops, number of passes, points
+    rescanned exactly, f64 sums kept in the fixed parallel order."""
+    ms, fl = C.c_double(), C.c_double()
+    passes, resc, inex = C.c_uint64(), C.c_uint64(), C.c_uint64()
+    _check(_lib.pxg_kmeans_last_stats(C.byref(ms), C.byref(fl), C.byref(passes), C.byref(resc), C.byref(inex)))
+    return {"mfma_ms": ms.value, "mfma_flops": fl.value, "mfma_passes": passes.value, "rescanned": resc.value,
+            "inexact_sums": inex.value}
+
+
 def kmeans_pp(points, k, seed):
     p = np.ascontiguousarray(points, dtype=np.float32)
     n, dim = p.shape
@@ -748,7 +759,7 @@ class ProductQuantizer:
         return out
 
 
-__all__ += ["IvfPqConfig", "IvfPqIndex", "TrainingReport", "Clustering", "kmeans", "kmeans_device", "kmeans_lloyd", "kmeans_pp",
+__all__ += ["IvfPqConfig", "IvfPqIndex", "TrainingReport", "Clustering", "kmeans", "kmeans_device", "kmeans_lloyd", "kmeans_pp", "kmeans_last_stats",
             "kmeans_assign", "PqConfig", "ProductQuantizer"]
 
 

@@ -45,6 +45,12 @@ constexpr int KM_LDS_FLOATS = 8192;  // 32 KiB of staged centroids
 typedef float f16v __attribute__((ext_vector_type(16)));
 // points of the last nearest_device call that the MFMA pass could not certify
 thread_local size_t g_last_redo = 0;
+// counters of this thread's last k-means run (measurement only)
+struct KmStats {
+  double mfma_ms = 0.0, mfma_flops = 0.0;
+  uint64_t passes = 0, rescanned = 0, inexact_sums = 0;
+};
+thread_local KmStats g_km;
 constexpr size_t SEQ_SUM_LIMIT = 1u << 17;
 
 // ---------------------------------------------------------------------------
@@ -537,8 +543,13 @@ void nearest_device(const float* P, int ldp, const uint32_t* rows, size_t n, int
   hipLaunchKernelGGL(km_row_norms, dim3((unsigned)((k + 31) / 32)), dim3(256), 0, s, C, ldc,
                      (const uint32_t*)nullptr, (int)k, dim, cn.p);
   hipLaunchKernelGGL(km_max_of, dim3(1), dim3(1024), 0, s, cn.p, (int)k, cmax.p);
+  hipEvent_t e0, e1;
+  PXG_HIP(hipEventCreate(&e0));
+  PXG_HIP(hipEventCreate(&e1));
+  PXG_HIP(hipEventRecord(e0, s));
   hipLaunchKernelGGL(km_mfma_top, dim3((unsigned)((n + KA_M - 1) / KA_M)), dim3(256), 0, s, P, ldp, rows, (int)n,
                      dim, C, ldc, (int)k, pn.p, cn.p, bidx.p, best.p, second.p);
+  PXG_HIP(hipEventRecord(e1, s));
   PXG_HIP(hipMemsetAsync(nredo.p, 0, 4, s));
   const dim3 g((unsigned)((n + 255) / 256));
   if (unrolled)
@@ -551,6 +562,14 @@ void nearest_device(const float* P, int ldp, const uint32_t* rows, size_t n, int
   int m = 0;
   PXG_HIP(hipMemcpyAsync(&m, nredo.p, 4, hipMemcpyDeviceToHost, s));
   PXG_HIP(hipStreamSynchronize(s));
+  float ms = 0.0f;
+  PXG_HIP(hipEventElapsedTime(&ms, e0, e1));
+  PXG_HIP(hipEventDestroy(e0));
+  PXG_HIP(hipEventDestroy(e1));
+  g_km.mfma_ms += ms;
+  g_km.mfma_flops += 2.0 * (double)n * (double)k * (double)dim;
+  g_km.passes += 1;
+  g_km.rescanned += (uint64_t)m;
   g_last_redo = (size_t)m;
   if (m == 0) return;
   // the uncertified points: exact scan over their rows, results scattered back
@@ -1138,6 +1157,7 @@ static double now_s() {
 KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req, size_t max_iter, ChaCha8* rng,
                         const float* init, DevBuf<float>& cents, DevBuf<uint32_t>* assign_out, hipStream_t s) {
   KmeansOut out;
+  g_km = KmStats();
   if (dim == 0) n = 0;
   const size_t k = std::max<size_t>(std::min(k_req, n), 1);
   out.k = k;
@@ -1277,6 +1297,7 @@ KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req
     PXG_HIP(hipMemcpyAsync(assign_out->p, prev.p, n * 4, hipMemcpyDeviceToDevice, s));
   }
   PXG_HIP(hipStreamSynchronize(s));
+  g_km.inexact_sums = out.inexact_sums;
   if (train_verbose())
     std::fprintf(stderr,
                  "[pxg kmeans] n=%zu dim=%d k=%zu: seeding %.3fs, lloyd %zu it %.3fs, %zu empty reseeds, %zu points "
@@ -1465,6 +1486,17 @@ int pxg_kmeans_pp(const float* points, uint64_t n, uint32_t dim, uint64_t k, uin
     PXG_HIP(hipMemcpyAsync(centroids_out, c.p, k * dim * 4, hipMemcpyDeviceToHost, s));
     PXG_HIP(hipStreamSynchronize(s));
     (void)hipStreamDestroy(s);
+  });
+}
+
+int pxg_kmeans_last_stats(double* mfma_ms, double* mfma_flops, uint64_t* mfma_passes, uint64_t* rescanned,
+                          uint64_t* inexact_sums) {
+  return pxg::guard([&] {
+    if (mfma_ms) *mfma_ms = pxg::g_km.mfma_ms;
+    if (mfma_flops) *mfma_flops = pxg::g_km.mfma_flops;
+    if (mfma_passes) *mfma_passes = pxg::g_km.passes;
+    if (rescanned) *rescanned = pxg::g_km.rescanned;
+    if (inexact_sums) *inexact_sums = pxg::g_km.inexact_sums;
   });
 }
 
