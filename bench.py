@@ -326,6 +326,51 @@ def bench_kmeans(args, torch, px, dev):
     return out
 
 
+def bench_fixture(args, torch, px, dev):
+    """fixture::generate (proxima-cli/src/fixture.rs:71-123) on the GPU: the
+    reference bench harness's corpus generator, at 10M x 128 from 1000
+    clusters with 10,000 queries. Bound by the HBM writes of the output."""
+    n, dim, clusters, nq = args.fx_n, 128, 1000, 10_000
+    v = torch.empty((n, dim), dtype=torch.float32, device=dev)
+    q = torch.empty((nq, dim), dtype=torch.float32, device=dev)
+    px.fixture_generate_device(n, dim, clusters, nq, args.seed, v, q)  # warm-up
+    torch.cuda.synchronize()
+    reps = 3
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        px.fixture_generate_device(n, dim, clusters, nq, args.seed, v, q)
+    torch.cuda.synchronize()
+    t = (time.perf_counter() - t0) / reps
+    written = (n + nq) * dim * 4
+    gbs = written / t / 1e9
+    out = {"value": round(written / t / 2**20, 1), "unit": "MiB/s of f32 generated", "ms_per_run": round(t * 1e3, 3),
+           "config": {"workload": "fixture::generate 10M x 128 f32, 1000 clusters, 10,000 queries", "count": n,
+                      "dim": dim, "clusters": clusters, "queries": nq},
+           "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                        "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                        "note": "bytes written per run over the host-timed run (3 launches + one host sync); "
+                                "the kernels are bound by the f64 ln and cos of the Box-Muller step, not by HBM"}}
+    log(f"[bench] fixture: {n}x{dim} + {nq} queries in {t * 1e3:.2f} ms = {gbs:.0f} GB/s written")
+    if not args.no_cpu:
+        from oracle import oracle as orc
+        ns = 200_000
+        t0 = time.perf_counter()
+        wv, _ = orc.fixture_generate(ns, dim, clusters, 0, args.seed)
+        cpu_s = time.perf_counter() - t0
+        got = v[:ns].cpu().numpy()
+        same = float(np.mean(got.view(np.uint32) == wv.view(np.uint32)))
+        worst = float(np.max(np.abs(got.astype(np.float64) - wv.astype(np.float64))))
+        out["cpu_baseline"] = {"value": round(ns * dim * 4 / cpu_s / 2**20, 1), "unit": "MiB/s of f32 generated",
+                               "cores": 1, "kind": "port",
+                               "sample": f"oracle fixture_generate restatement, {ns} x {dim} points, 1 thread, "
+                                         f"{cpu_s:.2f}s"}
+        out["parity"] = {"points": ns, "bit_identical_fraction": round(same, 6), "max_abs_diff": worst}
+        log(f"[bench] fixture CPU {ns * dim * 4 / cpu_s / 2**20:.1f} MiB/s (1 core); bit-identical {same:.6f} of "
+            f"the first {ns} points, max |diff| {worst:.2e}")
+    del v, q
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -353,6 +398,9 @@ def main():
     ap.add_argument("--kmeans-only", action="store_true", help="run only the k-means leg (prints its JSON object)")
     ap.add_argument("--km-n", type=int, default=2_000_000)
     ap.add_argument("--km-cpu-sample", type=int, default=131072)
+    ap.add_argument("--skip-fixture", action="store_true")
+    ap.add_argument("--fixture-only", action="store_true", help="run only the fixture leg (prints its JSON object)")
+    ap.add_argument("--fx-n", type=int, default=10_000_000)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also run one device copy of this size (a known-size kernel for scaling PMC byte counters)")
     args = ap.parse_args()
@@ -376,6 +424,9 @@ def main():
         return
     if args.kmeans_only:
         print(json.dumps(bench_kmeans(args, torch, px, dev)), flush=True)
+        return
+    if args.fixture_only:
+        print(json.dumps(bench_fixture(args, torch, px, dev)), flush=True)
         return
     n, dim, B = args.n, args.dim, args.batch
     log(f"[bench] generating {n}x{dim} corpus + {args.queries} queries on the GPU")
@@ -482,6 +533,10 @@ def main():
     km = None
     if not args.skip_kmeans:
         km = bench_kmeans(args, torch, px, dev)
+        torch.cuda.empty_cache()
+    fx = None
+    if not args.skip_fixture:
+        fx = bench_fixture(args, torch, px, dev)
 
     out = {
         "metric": METRIC,
@@ -512,6 +567,7 @@ def main():
         "ivfpq": ivf,
         "sq8": sq8,
         "kmeans": km,
+        "fixture": fx,
     }
     print(json.dumps(out), flush=True)
 

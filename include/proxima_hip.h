@@ -334,6 +334,22 @@ uint64_t pxg_sq8_last_fallbacks(void);
 /* 0 = automatic, 1 = integer MFMA whenever dim <= 256, 2 = exact scan. */
 int pxg_sq8_set_search_mode(pxg_sq8* index, int mode);
 
+/* ------------------------------------------------------------------------ */
+/* The benchmark fixture (crates/proxima-cli/src/fixture.rs).               */
+
+/* fixture::generate (fixture.rs:71-123) from ChaCha8Rng::seed_from_u64(seed):
+ * vectors (count x dim) = centre[i % clusters] + gaussian, centres =
+ * 4 * gaussian; queries (queries x dim) = vectors[(q * stride) % count] +
+ * 0.25 * gaussian with stride = max(count / max(queries, 1), 1). ln and cos
+ * of the Box-Muller step are correctly rounded f32 values (the reference
+ * uses the platform libm). Configuration error when clusters = 0 with
+ * count > 0, or queries > 0 with count = 0 (the reference would panic). */
+int pxg_fixture_generate(uint64_t count, uint32_t dim, uint64_t clusters, uint64_t queries, uint64_t seed,
+                         float* vectors, float* query_vectors);
+/* pxg_fixture_generate writing to device memory. */
+int pxg_fixture_generate_device(uint64_t count, uint32_t dim, uint64_t clusters, uint64_t queries, uint64_t seed,
+                                float* d_vectors, float* d_queries);
+
 #ifdef __cplusplus
 }
 #endif

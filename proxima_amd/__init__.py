@@ -1104,3 +1104,31 @@ def recall_at_k_filtered(candidate, truth, queries, k, filter):
 
 
 __all__ += ["RecallReport", "recall_at_k", "recall_at_k_filtered"]
+
+
+# ---------------------------------------------------------------------------
+# the benchmark fixture (crates/proxima-cli/src/fixture.rs)
+# ---------------------------------------------------------------------------
+def fixture_generate(count, dim, clusters, queries, seed):
+    """fixture::generate (fixture.rs:71-123) on the GPU: returns (vectors
+    [count, dim], queries [queries, dim]) as f32 arrays."""
+    v = np.zeros((count, dim), np.float32)
+    q = np.zeros((queries, dim), np.float32)
+    _check(_lib.pxg_fixture_generate(count, dim, clusters, queries, seed, _ptr(v) if v.size else None,
+                                     _ptr(q) if q.size else None))
+    return v, q
+
+
+def fixture_generate_device(count, dim, clusters, queries, seed, vectors_out, queries_out=None):
+    """fixture_generate into contiguous f32 GPU tensors [count, dim] and
+    [queries, dim] (queries_out may be None when queries == 0)."""
+    for t, rows, name in ((vectors_out, count, "vectors_out"), (queries_out, queries, "queries_out")):
+        if rows == 0 and t is None:
+            continue
+        if t is None or not t.is_cuda or str(t.dtype) != "torch.float32" or t.numel() < rows * dim:
+            raise ValueError(f"{name} must be a float32 GPU tensor of at least {rows} x {dim} elements")
+    _check(_lib.pxg_fixture_generate_device(count, dim, clusters, queries, seed, _device_ptr(vectors_out),
+                                            None if queries_out is None else _device_ptr(queries_out)))
+
+
+__all__ += ["fixture_generate", "fixture_generate_device"]

@@ -123,6 +123,8 @@ SIGNATURES = {
     "pxg_pq_train": (_i32, [_vp, _u64, _u32, _u64, _u64, _u64, _vp, _P(_f64), _P(_u64)]),
     "pxg_pq_encode": (_i32, [_vp, _u32, _u64, _vp, _u64, _vp]),
     "pxg_pq_train_device": (_i32, [_vp, _u64, _u32, _u64, _u64, _u64, _vp, _P(_f64), _P(_u64)]),
+    "pxg_fixture_generate": (_i32, [_u64, _u32, _u64, _u64, _u64, _vp, _vp]),
+    "pxg_fixture_generate_device": (_i32, [_u64, _u32, _u64, _u64, _u64, _vp, _vp]),
     # scalar quantizer / SQ8 index
     "pxg_sq_train": (_i32, [_vp, _u64, _u32, _i32, _vp, _vp, _vp]),
     "pxg_sq_encode": (_i32, [_vp, _u64, _u32, _i32, _i32, _vp, _vp, _vp]),

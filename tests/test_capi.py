@@ -88,3 +88,16 @@ def test_sq8_configuration_errors_without_gpu(lib):
     three = (ctypes.c_float * 3)()
     assert lib.pxg_sq_train(None, 0, 3, 1, three, three, three) == 7  # empty training (scalar.rs:145-152)
     assert b"training" in lib.pxg_last_error_message()
+
+
+def test_fixture_configuration_errors_without_gpu(lib):
+    lib.pxg_last_error_message.restype = ctypes.c_char_p
+    buf = (ctypes.c_float * 16)()
+    # a point needs a cluster (fixture.rs:93, index % clusters)
+    assert lib.pxg_fixture_generate(ctypes.c_uint64(4), ctypes.c_uint32(4), ctypes.c_uint64(0), ctypes.c_uint64(0),
+                                    ctypes.c_uint64(1), buf, buf) == 7
+    assert b"clusters" in lib.pxg_last_error_message()
+    # a query needs a corpus point (fixture.rs:102-103, % count)
+    assert lib.pxg_fixture_generate(ctypes.c_uint64(0), ctypes.c_uint32(4), ctypes.c_uint64(1), ctypes.c_uint64(2),
+                                    ctypes.c_uint64(1), buf, buf) == 7
+    assert b"count" in lib.pxg_last_error_message()
