@@ -123,17 +123,35 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
         for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
     float4 rq[4], rx[4];
+#if defined(__HIP_DEVICE_COMPILE__)
+    // Buffer loads over this tile's query and slot rows: rows past the valid
+    // ones fall outside the resource and read as zero, so full k slices need
+    // no per-element guards (and no VALU work beyond one offset add).
+    const __amdgpu_buffer_rsrc_t rs_q = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(Q + (size_t)q0 * ld), 0, (int)(max(min(nq - q0, FB_M), 0) * ld * 4), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs_x = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(X + (size_t)n0 * ld), 0, (int)(max(min(s_end - n0, FB_N), 0) * ld * 4), 0x00020000);
+    const int voff = (lr * ld + lc) * 4, vstep = 32 * ld * 4;
+#endif
     auto gload = [&](int k0) {
+#if defined(__HIP_DEVICE_COMPILE__)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int row = lr + 32 * i;
-        const int kc = k0 + lc;
-        const int q = q0 + row, x = n0 + row;
-        rq[i] = (q < nq && kc < ld) ? *reinterpret_cast<const float4*>(Q + (size_t)q * ld + kc)
-                                    : make_float4(0.f, 0.f, 0.f, 0.f);
-        rx[i] = (x < s_end && kc < ld) ? *reinterpret_cast<const float4*>(X + (size_t)x * ld + kc)
-                                       : make_float4(0.f, 0.f, 0.f, 0.f);
+        const auto a = __builtin_amdgcn_raw_buffer_load_b128(rs_q, voff + i * vstep + k0 * 4, 0, 0);
+        const auto b = __builtin_amdgcn_raw_buffer_load_b128(rs_x, voff + i * vstep + k0 * 4, 0, 0);
+        rq[i] = __builtin_bit_cast(float4, a);
+        rx[i] = __builtin_bit_cast(float4, b);
       }
+      // the last slice of a row whose stride is not a multiple of FB_K: the
+      // float4s past the row end belong to the next row
+      if (k0 + FB_K > ld && k0 + lc >= ld) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          rq[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+          rx[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+#endif
     };
     auto lstore = [&](int buf) {
 #pragma unroll
