@@ -929,6 +929,119 @@ __global__ void ivf_gather_csr(const uint32_t* __restrict__ entry_slot, int n, c
   for (int j = 0; j < M; ++j) list_codes[(size_t)e * M + j] = codes[(size_t)s * M + j];
 }
 
+// Entry order within each list of a 16-subspace index, chosen for the scan's
+// table gathers. A scan wave reads one table entry per lane per subspace, lane
+// l taking entry (list start + 64j + l). The LDS serves a ds_read_b32 one
+// half-wave (32 lanes) at a time over 32 four-byte banks, and a half-wave
+// takes as many passes as its most loaded bank holds distinct addresses
+// (lanes on the same code share one broadcast). Every table starts on a bank
+// boundary, so code c of any subspace falls in bank c mod 32.
+//
+// The entries of a list are dealt into 32-entry groups, aligned to the list
+// start. Each place of a group takes, among the BO_WIN oldest entries not yet
+// placed, the one that adds the least sum over subspaces of load^3, where
+// load is the number of distinct codes the group already has on that entry's
+// bank (a code already present adds nothing); ties go to the lowest window
+// position, so the order is deterministic. On uniform random codes this
+// lowers the mean passes per half-wave gather from ~3.1 to ~2.0.
+//
+// Scan keys are (distance, id rank), so no result depends on this order.
+constexpr int BO_PER_LANE = 2, BO_WIN = 64 * BO_PER_LANE;
+
+__device__ __forceinline__ uint32_t bo_byte(const uint4& w, int s) {
+  const uint32_t v = s < 4 ? w.x : s < 8 ? w.y : s < 12 ? w.z : w.w;
+  return (v >> (8 * (s & 3))) & 0xFFu;
+}
+
+__global__ __launch_bounds__(64) void ivf_bank_order(const uint32_t* __restrict__ list_off,
+                                                     const uint32_t* __restrict__ entry_in,
+                                                     const uint8_t* __restrict__ codes,
+                                                     uint32_t* __restrict__ entry_out) {
+  // per (subspace, bank): distinct codes placed (bits 0-7) and which of the
+  // bank's 8 codes are present (bit 8 + (c >> 5))
+  __shared__ uint32_t st[16 * 32];
+  const int lane = threadIdx.x;
+  const uint32_t b = list_off[blockIdx.x], n = list_off[blockIdx.x + 1] - b;
+  if (n <= 32) {  // one group: every order costs the same
+    if ((uint32_t)lane < n) entry_out[b + lane] = entry_in[b + lane];
+    return;
+  }
+  uint32_t slot[BO_PER_LANE];
+  uint4 cw[BO_PER_LANE];
+  bool ok[BO_PER_LANE];
+#pragma unroll
+  for (int j = 0; j < BO_PER_LANE; ++j) {
+    const uint32_t i = (uint32_t)(j * 64 + lane);
+    ok[j] = i < n;
+    slot[j] = ok[j] ? entry_in[b + i] : 0u;
+    cw[j] = ok[j] ? *reinterpret_cast<const uint4*>(codes + (size_t)slot[j] * 16) : make_uint4(0, 0, 0, 0);
+  }
+  uint32_t next = n < (uint32_t)BO_WIN ? n : (uint32_t)BO_WIN;
+  for (uint32_t g0 = 0; g0 < n; g0 += 32) {
+    for (int i = lane; i < 16 * 32; i += 64) st[i] = 0;
+    __syncthreads();
+    const uint32_t gs = n - g0 < 32 ? n - g0 : 32;
+    for (uint32_t k = 0; k < gs; ++k) {
+      uint32_t key = 0xFFFFFFFFu;
+#pragma unroll
+      for (int j = 0; j < BO_PER_LANE; ++j) {
+        uint32_t cost = 0;
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+          const uint32_t c = bo_byte(cw[j], s);
+          const uint32_t w = st[s * 32 + (c & 31)];
+          const uint32_t l = w & 0xFFu;
+          cost += ((w >> (8 + (c >> 5))) & 1u) ? 0u : l * l * l;
+        }
+        // cost <= 16 * 32^3 < 2^20; position j*64 + lane < 2^7
+        const uint32_t kj = (cost << 7) | (uint32_t)(j * 64 + lane);
+        if (ok[j] && kj < key) key = kj;
+      }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t o = (uint32_t)__shfl_xor((int)key, off);
+        key = o < key ? o : key;
+      }
+      const int pos = (int)(key & 127u), wl = pos & 63, wj = pos >> 6;
+      const uint32_t mine = wj == 0 ? slot[0] : slot[1];
+      const uint4 mc = wj == 0 ? cw[0] : cw[1];
+      const uint32_t wslot = (uint32_t)__builtin_amdgcn_readlane((int)mine, wl);
+      const uint4 wc = make_uint4((uint32_t)__builtin_amdgcn_readlane((int)mc.x, wl),
+                                  (uint32_t)__builtin_amdgcn_readlane((int)mc.y, wl),
+                                  (uint32_t)__builtin_amdgcn_readlane((int)mc.z, wl),
+                                  (uint32_t)__builtin_amdgcn_readlane((int)mc.w, wl));
+      if (lane == 0) entry_out[b + g0 + k] = wslot;
+      __syncthreads();  // every lane has read st for this place
+      if (lane < 16) {
+        uint32_t c = 0;
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+          if (lane == s) c = bo_byte(wc, s);
+        const int i = lane * 32 + (int)(c & 31);
+        const uint32_t bit = 1u << (8 + (c >> 5)), w = st[i];
+        if (!(w & bit)) st[i] = (w + 1) | bit;
+      }
+      __syncthreads();
+      if (lane == wl) {  // refill the winner's window place from the list
+        const bool more = next < n;
+        const uint32_t ns = more ? entry_in[b + next] : 0u;
+        const uint4 nc = more ? *reinterpret_cast<const uint4*>(codes + (size_t)ns * 16) : make_uint4(0, 0, 0, 0);
+        if (wj == 0) {
+          slot[0] = ns;
+          cw[0] = nc;
+          ok[0] = more;
+        } else {
+          slot[1] = ns;
+          cw[1] = nc;
+          ok[1] = more;
+        }
+      }
+      if (next < n) ++next;
+    }
+    __syncthreads();
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -1036,11 +1149,19 @@ struct IvfPqIndex {
       list_off.reserve(produced + 1);
       list_rank.reserve(std::max<uint32_t>(total, 1));
       list_codes.reserve(std::max<size_t>((size_t)total * M() + 16, 16));
-      DevBuf<uint32_t> d_entry(std::max<uint32_t>(total, 1));
+      DevBuf<uint32_t> d_entry(std::max<uint32_t>(total, 1)), d_banked;
       PXG_HIP(hipMemcpyAsync(list_off.p, count.data(), (produced + 1) * 4, hipMemcpyHostToDevice, s));
       if (total) {
         PXG_HIP(hipMemcpyAsync(d_entry.p, entry.data(), total * 4, hipMemcpyHostToDevice, s));
-        hipLaunchKernelGGL(ivf_gather_csr, dim3((total + 255) / 256), dim3(256), 0, s, d_entry.p, (int)total,
+        const uint32_t* order = d_entry.p;
+        if (M() == 16) {  // the staged 16-subspace scan gathers by half-wave
+          d_banked.reserve(total);
+          hipLaunchKernelGGL(ivf_bank_order, dim3(produced), dim3(64), 0, s, list_off.p, d_entry.p, codes.p,
+                             d_banked.p);
+          PXG_HIP(hipGetLastError());
+          order = d_banked.p;
+        }
+        hipLaunchKernelGGL(ivf_gather_csr, dim3((total + 255) / 256), dim3(256), 0, s, order, (int)total,
                            d_rank.p, codes.p, (int)M(), list_rank.p, list_codes.p);
         PXG_HIP(hipGetLastError());
       }
