@@ -377,3 +377,59 @@ def test_l2_one_dimension_subspaces_take_the_general_scan(gpu):
     q = data[::150] + np.float32(0.01)
     want = orc.ivf_search(0, cents, books, codes, list_of, np.arange(n), q, 10, 2, m, threads=8)
     assert_same(idx.search_batch(q, 10, nprobe=2), want)
+
+
+@pytest.mark.parametrize("dim,metric,rerank", [(16, 0, 0), (32, 1, 0), (64, 0, 40), (128, 1, 40), (128, 0, 0)])
+def test_large_batch_scan(gpu, dim, metric, rerank):
+    """A 700-query batch over 12 lists (4200 and 8400 (query, probe) pairs,
+    every list probed by hundreds of queries): ids and ADC distances match the
+    oracle with rerank, a filter, removals, and a list that removals have
+    emptied (probed when nprobe = nlist)."""
+    px = gpu
+    n, nlist, m = 20000, 12, 16
+    rng = np.random.default_rng(100 + dim + metric)
+    data = corpus(n, dim, 16) + rng.standard_normal((n, dim)).astype(np.float32) * 0.4
+    prep = orc.prepare_rows(metric, data)
+    cents, books, _ = orc.ivf_train(prep, nlist, m, max_iter=3, seed=4)
+    codes, list_of = orc.ivf_encode(prep, cents, books, m)
+    cfg = px.IvfPqConfig(nlist, m).with_train_threshold(1 << 62).with_rerank(rerank)
+    idx = build(px, data, cfg, metric)
+    idx.load_trained(cents, books, codes, list_of)
+    live = np.ones(n, np.uint8)
+    emptied = int(np.argmin(np.bincount(list_of, minlength=nlist)))
+    for i in list(np.flatnonzero(list_of == emptied)) + list(range(7, n, 13)):
+        if live[i]:
+            idx.remove(int(i))
+            live[i] = 0
+    q = data[rng.integers(0, n, 700)] + np.float32(0.03)
+    qp = orc.prepare_rows(metric, q)
+    vec = prep if rerank else None
+    for nprobe, k in ((6, 10), (12, 33)):  # 4200 and 8400 pairs over 12 lists
+        want = orc.ivf_search(metric, cents, books, codes, list_of, np.arange(n), qp, k, nprobe, m, live=live,
+                              vectors=vec, rerank=rerank, threads=8)
+        assert_same(idx.search_batch(q, k, nprobe=nprobe), want)
+    acc = np.array([i % 5 != 2 for i in range(n)], np.uint8)
+    want = orc.ivf_search(metric, cents, books, codes, list_of, np.arange(n), qp, 10, 7, m, live=live, accept=acc,
+                          vectors=vec, rerank=rerank, threads=8)
+    assert_same(idx.search_batch(q, 10, lambda i, _m: i % 5 != 2, nprobe=7), want)
+
+
+def test_scan_of_a_list_over_65536_entries(gpu):
+    """One list of 70000 entries beside five short ones, all probed by 800
+    queries: results match the oracle."""
+    px = gpu
+    dim, m, nlist = 16, 16, 6
+    rng = np.random.default_rng(8)
+    centres = rng.standard_normal((nlist, dim)).astype(np.float32) * np.float32(8)
+    sizes = (70000, 800, 700, 600, 500, 400)
+    data = np.concatenate([centres[i] + np.float32(0.3) * rng.standard_normal((s, dim)).astype(np.float32)
+                           for i, s in enumerate(sizes)])
+    n = data.shape[0]
+    cents, books, _ = orc.ivf_train(data, nlist, m, max_iter=3, training_sample=8000, seed=1)
+    codes, list_of = orc.ivf_encode(data, cents, books, m)
+    assert np.bincount(list_of, minlength=nlist).max() > 65536
+    idx = build(px, data, px.IvfPqConfig(nlist, m).with_train_threshold(1 << 62))
+    idx.load_trained(cents, books, codes, list_of)
+    q = data[rng.integers(0, n, 800)] + np.float32(0.01)
+    want = orc.ivf_search(0, cents, books, codes, list_of, np.arange(n), q, 10, nlist, m, threads=8)
+    assert_same(idx.search_batch(q, 10, nprobe=nlist), want)
