@@ -945,15 +945,21 @@ __global__ void ivf_gather_csr(const uint32_t* __restrict__ entry_slot, int n, c
 // position, so the order is deterministic. On uniform random codes this
 // lowers the mean passes per half-wave gather from ~3.1 to ~2.0.
 //
+// A wave orders one segment {first entry, entries} of at most BO_SEG entries
+// (lists are cut at multiples of BO_SEG from their start, so the groups stay
+// aligned), which keeps long lists from serialising the pass.
+//
 // Scan keys are (distance, id rank), so no result depends on this order.
 constexpr int BO_PER_LANE = 2, BO_WIN = 64 * BO_PER_LANE;
+constexpr uint32_t BO_SEG = 2048;
+static_assert(BO_SEG % 32 == 0, "segments hold whole groups");
 
 __device__ __forceinline__ uint32_t bo_byte(const uint4& w, int s) {
   const uint32_t v = s < 4 ? w.x : s < 8 ? w.y : s < 12 ? w.z : w.w;
   return (v >> (8 * (s & 3))) & 0xFFu;
 }
 
-__global__ __launch_bounds__(64) void ivf_bank_order(const uint32_t* __restrict__ list_off,
+__global__ __launch_bounds__(64) void ivf_bank_order(const uint2* __restrict__ segs,
                                                      const uint32_t* __restrict__ entry_in,
                                                      const uint8_t* __restrict__ codes,
                                                      uint32_t* __restrict__ entry_out) {
@@ -961,7 +967,7 @@ __global__ __launch_bounds__(64) void ivf_bank_order(const uint32_t* __restrict_
   // bank's 8 codes are present (bit 8 + (c >> 5))
   __shared__ uint32_t st[16 * 32];
   const int lane = threadIdx.x;
-  const uint32_t b = list_off[blockIdx.x], n = list_off[blockIdx.x + 1] - b;
+  const uint32_t b = segs[blockIdx.x].x, n = segs[blockIdx.x].y;
   if (n <= 32) {  // one group: every order costs the same
     if ((uint32_t)lane < n) entry_out[b + lane] = entry_in[b + lane];
     return;
@@ -1150,14 +1156,21 @@ struct IvfPqIndex {
       list_rank.reserve(std::max<uint32_t>(total, 1));
       list_codes.reserve(std::max<size_t>((size_t)total * M() + 16, 16));
       DevBuf<uint32_t> d_entry(std::max<uint32_t>(total, 1)), d_banked;
+      DevBuf<uint2> d_segs;
+      std::vector<uint2> segs;  // read by an async copy: lives to the sync below
       PXG_HIP(hipMemcpyAsync(list_off.p, count.data(), (produced + 1) * 4, hipMemcpyHostToDevice, s));
       if (total) {
         PXG_HIP(hipMemcpyAsync(d_entry.p, entry.data(), total * 4, hipMemcpyHostToDevice, s));
         const uint32_t* order = d_entry.p;
         if (M() == 16) {  // the staged 16-subspace scan gathers by half-wave
+          for (int l = 0; l < produced; ++l)
+            for (uint32_t s0 = 0; s0 < list_len_h[l]; s0 += BO_SEG)
+              segs.push_back(make_uint2(count[l] + s0, std::min(BO_SEG, list_len_h[l] - s0)));
           d_banked.reserve(total);
-          hipLaunchKernelGGL(ivf_bank_order, dim3(produced), dim3(64), 0, s, list_off.p, d_entry.p, codes.p,
-                             d_banked.p);
+          d_segs.reserve(segs.size());
+          PXG_HIP(hipMemcpyAsync(d_segs.p, segs.data(), segs.size() * sizeof(uint2), hipMemcpyHostToDevice, s));
+          hipLaunchKernelGGL(ivf_bank_order, dim3((unsigned)segs.size()), dim3(64), 0, s, d_segs.p, d_entry.p,
+                             codes.p, d_banked.p);
           PXG_HIP(hipGetLastError());
           order = d_banked.p;
         }
