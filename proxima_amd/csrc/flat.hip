@@ -55,9 +55,20 @@ constexpr int FAST_KMAX = 256;
 // ---------------------------------------------------------------------------
 // 2. MFMA distance GEMM fused with a per-query top-k' filter
 // ---------------------------------------------------------------------------
+#if defined(__HIP_DEVICE_COMPILE__)
+// A raw buffer resource over [p, p + bytes), built from wave-uniform scalars.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* p, int bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+  const int n = __builtin_amdgcn_readfirstlane(bytes);
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)(((uint64_t)hi << 32) | lo), 0, n, 0x00020000);
+}
+#endif
+
 template <int CAP>
 __device__ inline void compact_row(uint64_t* __restrict__ base, int c, int Kp, int lane, uint64_t* thr_row,
-                                   int* cnt_row, bool final_pass) {
+                                   float* thrf_row, int* cnt_row, unsigned long long* gthr_row, bool final_pass) {
   constexpr int E = CAP / WAVE;
   uint64_t kk[E];
 #pragma unroll
@@ -70,7 +81,13 @@ __device__ inline void compact_row(uint64_t* __restrict__ base, int c, int Kp, i
   for (int e = 0; e < E; ++e) {
     const int idx = lane * E + e;
     if (idx < Kp) base[idx] = kk[e];
-    if (idx == Kp - 1 && !final_pass) *thr_row = kk[e];
+    if (idx == Kp - 1 && !final_pass) {
+      *thr_row = kk[e];
+      *thrf_row = key_float((uint32_t)(kk[e] >> 32));
+      // this split keeps Kp candidates at or below kk[e] to the end, so no
+      // key above it can be in the query's top Kp over all splits
+      if (kk[e] != KEY_MAX) atomicMin(gthr_row, (unsigned long long)kk[e]);
+    }
   }
   if (lane == 0 && !final_pass) *cnt_row = Kp;
 }
@@ -79,12 +96,15 @@ template <int CAP>
 __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
     const float* __restrict__ Q, int nq, const float* __restrict__ X, int N, int ld,
     const float* __restrict__ qb, const float* __restrict__ xb, float scale, const uint8_t* __restrict__ live,
-    const uint8_t* __restrict__ accept, int S, int QB, int per_split, int Kp, uint64_t* __restrict__ cand) {
+    const uint8_t* __restrict__ accept, int S, int QB, int per_split, int Kp, uint64_t* __restrict__ cand,
+    unsigned long long* __restrict__ gthr) {
   __shared__ float sQ[2][FB_M * FB_LDR];
   __shared__ float sX[2][FB_N * FB_LDR];
   __shared__ uint64_t thr[FB_M];
   __shared__ int cnt[FB_M];
-  __shared__ float sqb[FB_M];
+  __shared__ __align__(16) float sqb[FB_M];
+  // thr as a float, key_float(thr >> 32): NaN while thr is KEY_MAX
+  __shared__ __align__(16) float thr_f[FB_M];
 
   // XCD-aware mapping: consecutive workgroup ids are dealt round-robin over
   // the 8 XCDs, so give each XCD a contiguous range of (split, query block)
@@ -105,6 +125,7 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
 
   for (int i = tid; i < FB_M; i += 256) {
     thr[i] = KEY_MAX;
+    thr_f[i] = key_float((uint32_t)(KEY_MAX >> 32));
     cnt[i] = 0;
     sqb[i] = (q0 + i < nq) ? qb[q0 + i] : 0.0f;
   }
@@ -114,6 +135,11 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
   const int nK = (ld + FB_K - 1) / FB_K;
 
   for (int n0 = s_begin; n0 < s_end; n0 += FB_N) {
+    // the other splits' published thresholds for this tile's rows, read now
+    // and applied after the k loop (an older value is only looser)
+    const uint64_t g_thr = tid < FB_M && q0 + tid < nq
+                               ? __hip_atomic_load(gthr + q0 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                               : KEY_MAX;
     f16v acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -127,14 +153,18 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
     // Buffer loads over this tile's query and slot rows: rows past the valid
     // ones fall outside the resource and read as zero, so full k slices need
     // no per-element guards (and no VALU work beyond one offset add).
-    const __amdgpu_buffer_rsrc_t rs_q = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(Q + (size_t)q0 * ld), 0, (int)(max(min(nq - q0, FB_M), 0) * ld * 4), 0x00020000);
-    const __amdgpu_buffer_rsrc_t rs_x = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(X + (size_t)n0 * ld), 0, (int)(max(min(s_end - n0, FB_N), 0) * ld * 4), 0x00020000);
+    const float* q_rows = Q + (size_t)q0 * ld;
+    const float* x_rows = X + (size_t)n0 * ld;
+    const int q_bytes = max(min(nq - q0, FB_M), 0) * ld * 4, x_bytes = max(min(s_end - n0, FB_N), 0) * ld * 4;
     const int voff = (lr * ld + lc) * 4, vstep = 32 * ld * 4;
 #endif
     auto gload = [&](int k0) {
 #if defined(__HIP_DEVICE_COMPILE__)
+      // The resources are rebuilt per call from readfirstlane'd scalars: a
+      // resource the compiler hoists and keeps in VGPRs is not known to be
+      // uniform at its use, and each load then runs in a waterfall loop.
+      const __amdgpu_buffer_rsrc_t rs_q = uniform_rsrc(q_rows, q_bytes);
+      const __amdgpu_buffer_rsrc_t rs_x = uniform_rsrc(x_rows, x_bytes);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const auto a = __builtin_amdgcn_raw_buffer_load_b128(rs_q, voff + i * vstep + k0 * 4, 0, 0);
@@ -194,41 +224,81 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
       if (kt + 1 < nK) lstore(cur ^ 1);
       __syncthreads();
     }
+    if (tid < FB_M && g_thr < thr[tid]) {
+      thr[tid] = g_thr;
+      thr_f[tid] = key_float((uint32_t)(g_thr >> 32));
+    }
+    __syncthreads();
 
-    // Epilogue: approximate score, threshold filter, append.
+    // Epilogue: approximate score, threshold filter, append. Lane (h, r)
+    // holds rows wm + 32i + 8vb + 4h + e (e < 4) of slots n0 + wn + 32j + r.
+    // A branch-free pass marks the values a with !(a > thr_f[row]), reading
+    // four rows' norms and thresholds per LDS read. That test passes every
+    // key below thr[row] (key_float inverts ord_key; NaN and the sign of zero
+    // pass), so only the marked values take the exact key test and append.
+    {
+      int slotj[2];
+      bool okj[2];
+      float xbj[2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int slot = n0 + wn + j * 32 + r;
-      const bool ok = slot < s_end && live[slot] && (accept == nullptr || accept[slot]);
-      const float xbv = ok ? xb[slot] : 0.0f;
+      for (int j = 0; j < 2; ++j) {
+        slotj[j] = n0 + wn + j * 32 + r;
+        okj[j] = slotj[j] < s_end && live[slotj[j]] && (accept == nullptr || accept[slotj[j]]);
+        xbj[j] = okj[j] ? xb[slotj[j]] : 0.0f;
+      }
+      uint32_t pass[2] = {0u, 0u};  // pass[i], bit j * 16 + v
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int row = wm + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-          if (ok && q0 + row < nq) {
-            const float a = (sqb[row] + xbv) - scale * acc[i][j][v];
-            const uint64_t key = ((uint64_t)ord_key(a) << 32) | (uint32_t)slot;
-            if (key < thr[row]) {
-              const int pos = atomicAdd(&cnt[row], 1);
-              cand[((size_t)(q0 + row) * S + split) * CAP + pos] = key;
+        for (int vb = 0; vb < 4; ++vb) {
+          const int row0 = wm + i * 32 + 8 * vb + 4 * h;
+          const float4 sq = *reinterpret_cast<const float4*>(&sqb[row0]);
+          const float4 tf = *reinterpret_cast<const float4*>(&thr_f[row0]);
+          const float sqv[4] = {sq.x, sq.y, sq.z, sq.w}, tfv[4] = {tf.x, tf.y, tf.z, tf.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const bool rok = q0 + row0 + e < nq;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              const float a = (sqv[e] + xbj[j]) - scale * acc[i][j][vb * 4 + e];
+              pass[i] |= (okj[j] && rok && !(a > tfv[e])) ? 1u << (j * 16 + vb * 4 + e) : 0u;
             }
           }
+          __builtin_amdgcn_sched_barrier(0);  // bounds the live rows (no spills)
         }
+      if (__ballot((pass[0] | pass[1]) != 0)) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+              if (pass[i] & (1u << (j * 16 + v))) {
+                const int row = wm + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                const float a = (sqb[row] + xbj[j]) - scale * acc[i][j][v];
+                const uint64_t key = ((uint64_t)ord_key(a) << 32) | (uint32_t)slotj[j];
+                if (key < thr[row]) {
+                  const int pos = atomicAdd(&cnt[row], 1);
+                  cand[((size_t)(q0 + row) * S + split) * CAP + pos] = key;
+                }
+              }
+            }
       }
     }
     __syncthreads();
     for (int row = wid; row < FB_M; row += 4) {
       const int c = cnt[row];
       if (c > CAP - FB_N)
-        compact_row<CAP>(cand + ((size_t)(q0 + row) * S + split) * CAP, c, Kp, lane, &thr[row], &cnt[row], false);
+        compact_row<CAP>(cand + ((size_t)(q0 + row) * S + split) * CAP, c, Kp, lane, &thr[row], &thr_f[row],
+                         &cnt[row], gthr + q0 + row, false);
     }
     __syncthreads();
   }
   // Final: every row leaves exactly Kp sorted keys (KEY_MAX padded).
   for (int row = wid; row < FB_M; row += 4) {
     if (q0 + row >= nq) continue;
-    compact_row<CAP>(cand + ((size_t)(q0 + row) * S + split) * CAP, cnt[row], Kp, lane, &thr[row], &cnt[row], true);
+    compact_row<CAP>(cand + ((size_t)(q0 + row) * S + split) * CAP, cnt[row], Kp, lane, &thr[row], &thr_f[row],
+                     &cnt[row], gthr + q0 + row, true);
   }
 }
 
@@ -487,16 +557,19 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
     const int per_split = tiles_per * FB_N;
     S = (int)((N + per_split - 1) / per_split);
     uint64_t* cand = (uint64_t*)ctx->get(6, (size_t)nq * S * CAP * 8);
+    // per query, the least threshold any split has published
+    unsigned long long* gthr = (unsigned long long*)ctx->get(25, nq * 8);
+    PXG_HIP(hipMemsetAsync(gthr, 0xFF, nq * 8, s));
     const int total = QB * S;
     tm.mark(1);
     const int grid = ((total + 7) / 8) * 8;
     const float scale = metric == PXG_EUCLIDEAN ? 2.0f : 1.0f;
     if (CAP == 256)
       hipLaunchKernelGGL(flat_mfma_candidates<256>, dim3(grid), dim3(256), 0, s, Qp, (int)nq, X.p, (int)N, (int)ld,
-                         qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, Kp, cand);
+                         qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, Kp, cand, gthr);
     else
       hipLaunchKernelGGL(flat_mfma_candidates<512>, dim3(grid), dim3(256), 0, s, Qp, (int)nq, X.p, (int)N, (int)ld,
-                         qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, Kp, cand);
+                         qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, Kp, cand, gthr);
     PXG_HIP(hipGetLastError());
     tm.mark(2);
     hipLaunchKernelGGL(flat_merge_rescore, dim3((unsigned)nq), dim3(256), 0, s, cand, S, CAP, Kp, (int)k, Qp,
