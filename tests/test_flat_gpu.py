@@ -315,3 +315,26 @@ def test_growth_preserves_contents(gpu):
         assert np.array_equal(idx.vector(i), data[i])
     q = rng.standard_normal((20, 24)).astype(np.float32)
     assert_same(idx.search_batch(q, 15), oracle_search(px, data, np.arange(5000), 0, q, 15))
+
+
+@pytest.mark.parametrize("metric", [0, 2])
+def test_thresholds_shared_across_splits(gpu, metric):
+    """The MFMA path splits the store over many workgroups per query block,
+    which share each query's running k'-th key. Queries whose neighbours sit
+    in the last split, queries spread over the store, k from 1 to 64 and a
+    filter: ids and distances match the oracle bit for bit."""
+    px = gpu
+    rng = np.random.default_rng(77 + metric)
+    n, dim = 200_000, 64
+    data = rng.standard_normal((n, dim)).astype(np.float32)
+    idx = make_index(px, data, metric, mode=1)
+    near_end = data[n - 500 + rng.integers(0, 500, 128)] + np.float32(0.01) * rng.standard_normal(
+        (128, dim)).astype(np.float32)
+    spread = rng.standard_normal((128, dim)).astype(np.float32)
+    q = np.concatenate([near_end, spread])
+    ids = np.arange(n, dtype=np.uint64)
+    for k in (1, 10, 64):
+        assert_same(idx.search_batch(q, k), oracle_search(px, data, ids, metric, q, k))
+    acc = (np.arange(n) % 3 == 1).astype(np.uint8)
+    got = idx.search_batch(q, 10, lambda i, _m: i % 3 == 1)
+    assert_same(got, oracle_search(px, data, ids, metric, q, 10, accept=acc))
