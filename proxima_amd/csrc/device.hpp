@@ -26,11 +26,50 @@ __host__ __device__ inline float key_float(uint32_t k) {
   return __builtin_bit_cast(float, b);
 }
 
-// 64-bit shuffle across the wave.
+// The value held by lane (lane ^ M), M a power of two below 64, by VALU lane
+// exchanges rather than the LDS crossbar: DPP quad permutes for 1 and 2, row
+// shifts for 4 (left for lanes with bit 2 clear, right for the others), a
+// half-row rotate for 8, and the gfx950 permlane swaps for 16 and 32 (which,
+// given the same register twice, return a wave with the upper and one with
+// the lower half of each 32- or 16-lane pair).
+template <int M>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t x) {
+  const int lane = __lane_id();
+  if constexpr (M == 1) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  } else if constexpr (M == 2) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  } else if constexpr (M == 4) {
+    const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x104, 0xF, 0xF, false);  // row_shl:4
+    const uint32_t dn = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xF, 0xF, false);  // row_shr:4
+    return (lane & 4) ? dn : up;
+  } else if constexpr (M == 8) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x128, 0xF, 0xF, false);  // row_ror:8
+  } else if constexpr (M == 16) {
+    const auto p = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return (lane & 16) ? p[0] : p[1];
+  } else {
+    static_assert(M == 32, "xor distance");
+    const auto p = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return (lane & 32) ? p[0] : p[1];
+  }
+}
+
+__device__ __forceinline__ uint32_t xor_lane_rt(uint32_t x, int mask) {
+  switch (mask) {  // folds wherever the mask is a constant (unrolled networks)
+    case 1: return xor_lane<1>(x);
+    case 2: return xor_lane<2>(x);
+    case 4: return xor_lane<4>(x);
+    case 8: return xor_lane<8>(x);
+    case 16: return xor_lane<16>(x);
+    case 32: return xor_lane<32>(x);
+    default: return (uint32_t)__shfl_xor((int)x, mask, WAVE);
+  }
+}
+
+// 64-bit shuffle across the wave: lane (lane ^ mask)'s value.
 __device__ inline uint64_t shfl_xor64(uint64_t v, int mask) {
-  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-  lo = __shfl_xor(lo, mask, WAVE);
-  hi = __shfl_xor(hi, mask, WAVE);
+  const uint32_t lo = xor_lane_rt((uint32_t)v, mask), hi = xor_lane_rt((uint32_t)(v >> 32), mask);
   return ((uint64_t)hi << 32) | lo;
 }
 
