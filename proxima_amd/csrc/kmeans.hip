@@ -237,11 +237,15 @@ __global__ __launch_bounds__(256, 2) void km_mfma_top(const float* __restrict__ 
                                                       uint32_t* __restrict__ best_idx, float* __restrict__ best,
                                                       float* __restrict__ second) {
   // k slices (sA, sB) and, after each tile's k loop, the tile's dot
-  // products (dt, [KA_M][KA_N + 1]) share one LDS buffer
-  constexpr int SLICE = KA_M * KA_LDR, DT_LD = KA_N + 1;
+  // products (dt) share one LDS buffer. A dt row holds columns 0-63, a
+  // 4-float gap, then columns 64-127, so that the two threads of a row read
+  // their halves as float4 without bank conflicts.
+  constexpr int SLICE = KA_M * KA_LDR, DT_LD = KA_N + 8;
   static_assert(KA_M * DT_LD <= 4 * SLICE, "tile of dot products fits the slice buffers");
+  static_assert(KA_N == 128, "two 64-column halves per row");
   __shared__ __align__(16) float smem[4 * SLICE];
-  __shared__ float spn[KA_M], scn[KA_N];
+  __shared__ __align__(16) float spn[KA_M];
+  __shared__ __align__(16) float scn[KA_N];
   float* dt = smem;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int h = lane >> 5, r = lane & 31;
@@ -256,7 +260,7 @@ __global__ __launch_bounds__(256, 2) void km_mfma_top(const float* __restrict__ 
     prow[u] = p < n ? P + (size_t)(rows ? rows[p] : (uint32_t)p) * ldp : nullptr;
   }
   const int nK = (dim + KA_K - 1) / KA_K;
-  // this thread scans row tid/2, columns 2m + (tid&1) of every tile
+  // this thread scans row tid/2, columns 64 (tid&1) .. +63 of every tile
   const int my_row = tid >> 1, my_par = tid & 1;
   float b1 = INFINITY, b2 = INFINITY;
   int i1 = 0;
@@ -327,13 +331,12 @@ __global__ __launch_bounds__(256, 2) void km_mfma_top(const float* __restrict__ 
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v)
-          dt[(wm + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3)) * DT_LD + wn + j * 32 + r] = acc[i][j][v];
+          dt[(wm + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3)) * DT_LD + wn + (wn >> 4) + j * 32 + r] = acc[i][j][v];
     __syncthreads();
     const float prn = spn[my_row];
-    const float* drow = dt + my_row * DT_LD;
-    const int cols = min(KA_N, k - n0);
-    for (int m = my_par; m < cols; m += 2) {
-      const float x = (prn + scn[m]) - 2.0f * drow[m];
+    const float* drow = dt + my_row * DT_LD + my_par * 68;
+    const int c0 = my_par * 64, cols = min(KA_N, k - n0);
+    auto take = [&](float x, int m) {
       if (x < b1) {
         b2 = fminf(b1, b2);  // keeps a -inf mark
         b1 = x;
@@ -343,6 +346,19 @@ __global__ __launch_bounds__(256, 2) void km_mfma_top(const float* __restrict__ 
       } else if (!(x == x)) {
         b2 = -INFINITY;  // NaN: the point takes the exact scan
       }
+    };
+    if (cols == KA_N) {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const float4 d4 = *reinterpret_cast<const float4*>(drow + 4 * q);
+        const float4 s4 = *reinterpret_cast<const float4*>(scn + c0 + 4 * q);
+        take((prn + s4.x) - 2.0f * d4.x, c0 + 4 * q);
+        take((prn + s4.y) - 2.0f * d4.y, c0 + 4 * q + 1);
+        take((prn + s4.z) - 2.0f * d4.z, c0 + 4 * q + 2);
+        take((prn + s4.w) - 2.0f * d4.w, c0 + 4 * q + 3);
+      }
+    } else {
+      for (int m = c0; m < min(cols, c0 + 64); ++m) take((prn + scn[m]) - 2.0f * drow[m - c0], m);
     }
   }
   // merge the two threads of each row
