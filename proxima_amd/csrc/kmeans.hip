@@ -336,16 +336,15 @@ __global__ __launch_bounds__(256, 2) void km_mfma_top(const float* __restrict__ 
     const float prn = spn[my_row];
     const float* drow = dt + my_row * DT_LD + my_par * 68;
     const int c0 = my_par * 64, cols = min(KA_N, k - n0);
+    // branch-free form of: x < b1 -> (b2 = min(b1, b2), b1 = x, i1 = m);
+    // else x < b2 -> b2 = x; else NaN -> b2 = -inf (the point takes the exact
+    // scan; fminf keeps that mark)
     auto take = [&](float x, int m) {
-      if (x < b1) {
-        b2 = fminf(b1, b2);  // keeps a -inf mark
-        b1 = x;
-        i1 = n0 + m;
-      } else if (x < b2) {
-        b2 = x;
-      } else if (!(x == x)) {
-        b2 = -INFINITY;  // NaN: the point takes the exact scan
-      }
+      const bool lt1 = x < b1, lt2 = x < b2, nan = !(x == x);
+      const float nb2 = lt1 ? fminf(b1, b2) : lt2 ? x : nan ? -INFINITY : b2;
+      i1 = lt1 ? n0 + m : i1;
+      b1 = lt1 ? x : b1;
+      b2 = nb2;
     };
     if (cols == KA_N) {
 #pragma unroll
