@@ -67,6 +67,18 @@ __device__ __forceinline__ uint32_t xor_lane_rt(uint32_t x, int mask) {
   }
 }
 
+// Lane (lane - 1)'s value (DPP wave_shr:1; lane 0 gets 0).
+__device__ __forceinline__ uint32_t lane_up1(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x138, 0xF, 0xF, false);
+}
+
+// Lane (63 - lane)'s value: a row mirror (lane ^ 15 within each 16-lane row),
+// then the xor 16 and xor 32 exchanges.
+__device__ __forceinline__ uint32_t lane_reverse(uint32_t x) {
+  const uint32_t m = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x140, 0xF, 0xF, false);  // row_mirror
+  return xor_lane<32>(xor_lane<16>(m));
+}
+
 // 64-bit shuffle across the wave: lane (lane ^ mask)'s value.
 __device__ inline uint64_t shfl_xor64(uint64_t v, int mask) {
   const uint32_t lo = xor_lane_rt((uint32_t)v, mask), hi = xor_lane_rt((uint32_t)(v >> 32), mask);

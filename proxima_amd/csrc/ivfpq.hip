@@ -222,8 +222,8 @@ __device__ inline void wave_topk_insert(uint64_t key, uint64_t& kept, uint64_t& 
     const uint64_t x = readlane64(key, src);
     if (x < thr) {
       const int pos = __popcll(__ballot(kept < x));
-      const uint32_t up_lo = __shfl_up((uint32_t)kept, 1, WAVE);
-      const uint32_t up_hi = __shfl_up((uint32_t)(kept >> 32), 1, WAVE);
+      const uint32_t up_lo = lane_up1((uint32_t)kept);
+      const uint32_t up_hi = lane_up1((uint32_t)(kept >> 32));
       const uint64_t up = ((uint64_t)up_hi << 32) | up_lo;
       if (lane > pos) kept = up;
       else if (lane == pos) kept = x;
@@ -232,17 +232,11 @@ __device__ inline void wave_topk_insert(uint64_t key, uint64_t& kept, uint64_t& 
   }
 }
 
-__device__ inline uint64_t shfl64(uint64_t v, int src) {
-  const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)v, src, WAVE);
-  const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(v >> 32), src, WAVE);
-  return ((uint64_t)hi << 32) | lo;
-}
-
 // `kept` (ascending over the lanes) becomes the 64 smallest of kept and
 // `other` (also ascending): min against the reversed list is bitonic and
 // holds those 64, and a half-cleaner cascade sorts it.
 __device__ inline void wave_merge_sorted(uint64_t& kept, uint64_t other, int lane) {
-  const uint64_t r = shfl64(other, WAVE - 1 - lane);
+  const uint64_t r = ((uint64_t)lane_reverse((uint32_t)(other >> 32)) << 32) | lane_reverse((uint32_t)other);
   uint64_t v = kept < r ? kept : r;
 #pragma unroll
   for (int st = 32; st > 0; st >>= 1) {
