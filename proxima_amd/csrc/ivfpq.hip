@@ -271,9 +271,12 @@ __device__ inline void wave_topk_add(uint64_t key, uint64_t& kept, uint64_t& thr
 // one per lane, ascending; the waves' lists are merged at the end.
 constexpr int IVF_CQ = 4, IVF_CW = 8;
 
+// It also adds the query's probed entries (the list lengths) to *scanned.
 __global__ __launch_bounds__(IVF_CW * 64) void ivf_coarse_topk(const float* __restrict__ Qp, int ld, int dim, int nq,
                                                                const float* __restrict__ cT, int cst, int produced,
-                                                               int np, int* __restrict__ probes) {
+                                                               int np, int* __restrict__ probes,
+                                                               const uint32_t* __restrict__ list_off,
+                                                               unsigned long long* __restrict__ scanned) {
   extern __shared__ float4 sm4[];
   float* sq = (float*)sm4;                             // [dim][IVF_CQ]
   uint64_t* mk = (uint64_t*)(sm4 + dim);               // [IVF_CW][IVF_CQ][64]
@@ -334,7 +337,12 @@ __global__ __launch_bounds__(IVF_CW * 64) void ivf_coarse_topk(const float* __re
   if (w < IVF_CQ && q0 + w < nq) {
     uint64_t v = mk[w * 64 + lane];
     for (int ww = 1; ww < IVF_CW; ++ww) wave_merge_sorted(v, mk[(ww * IVF_CQ + w) * 64 + lane], lane);
-    if (lane < np) probes[(size_t)(q0 + w) * np + lane] = (int)(uint32_t)v;
+    const int l = (int)(uint32_t)v;
+    if (lane < np) probes[(size_t)(q0 + w) * np + lane] = l;
+    uint32_t len = lane < np ? list_off[l + 1] - list_off[l] : 0u;
+#pragma unroll
+    for (int st = 32; st > 0; st >>= 1) len += xor_lane_rt(len, st);
+    if (lane == 0) atomicAdd(scanned, (unsigned long long)len);
   }
 }
 
@@ -1460,10 +1468,14 @@ struct IvfPqIndex {
       uint64_t* ck = (uint64_t*)ctx->get(8, (size_t)nq * produced * 8);
       int* probes = (int*)ctx->get(9, (size_t)nq * np * 4);
       tm.mark(0);
-      if (np <= 64 && dim <= 2048) {
+      scanned_dev = (unsigned long long*)(flag_count + 2);
+      PXG_HIP(hipMemsetAsync(scanned_dev, 0, 8, s));
+      const bool fused_count = np <= 64 && dim <= 2048;
+      if (fused_count) {
         const size_t lds = (size_t)dim * IVF_CQ * 4 + (size_t)IVF_CW * IVF_CQ * 64 * 8;
         hipLaunchKernelGGL(ivf_coarse_topk, dim3((unsigned)((nq + IVF_CQ - 1) / IVF_CQ)), dim3(IVF_CW * 64), lds, s,
-                           Qp, (int)ld, (int)dim, (int)nq, cents_t.p, cst, produced, np, probes);
+                           Qp, (int)ld, (int)dim, (int)nq, cents_t.p, cst, produced, np, probes, list_off.p,
+                           scanned_dev);
       } else if (np <= 1024 && coarse) {
         // exact top-nprobe by (squared_l2, list) through the flat pipeline
         const float* Qd = Qp;
@@ -1486,10 +1498,9 @@ struct IvfPqIndex {
         hipLaunchKernelGGL(ivf_coarse_select, dim3((unsigned)nq), dim3(256), 0, s, ck, produced, np, probes);
       }
       PXG_HIP(hipGetLastError());
-      scanned_dev = (unsigned long long*)(flag_count + 2);
-      PXG_HIP(hipMemsetAsync(scanned_dev, 0, 8, s));
-      hipLaunchKernelGGL(ivf_count_scanned, dim3((unsigned)((nq * np + 255) / 256)), dim3(256), 0, s, probes,
-                         (int)(nq * np), list_off.p, scanned_dev);
+      if (!fused_count)
+        hipLaunchKernelGGL(ivf_count_scanned, dim3((unsigned)((nq * np + 255) / 256)), dim3(256), 0, s, probes,
+                           (int)(nq * np), list_off.p, scanned_dev);
       const int W = (int)(dim / M());
       // the register-codebook scans keep two distance tables in LDS (one for
       // cosine): an L2 index with 128 subspaces takes the general scan
