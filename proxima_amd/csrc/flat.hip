@@ -48,7 +48,9 @@ typedef float f16v __attribute__((ext_vector_type(16)));
 constexpr int FB_M = 128;   // queries per workgroup tile
 constexpr int FB_N = 128;   // slots per workgroup tile
 constexpr int FB_K = 32;    // k-slice staged in LDS
-constexpr int FB_LDR = FB_K + 4;
+// A staged slice is [rows][FB_K] floats without padding; 16-byte chunk c of
+// row r sits at chunk position c ^ (r & 7), so 8 lanes reading chunk c of 8
+// consecutive rows touch 8 different groups of banks.
 constexpr int MARGIN = 32;  // k' = k + MARGIN
 constexpr int FAST_KMAX = 256;
 
@@ -64,7 +66,27 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* p, in
   const int n = __builtin_amdgcn_readfirstlane(bytes);
   return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)(((uint64_t)hi << 32) | lo), 0, n, 0x00020000);
 }
+
+// Buffer load of 16 bytes per lane straight into LDS: lane i's bytes land at
+// m0 + 16 i, and an offset outside the resource lands as zeros. Inline asm,
+// so that the compiler neither tracks these loads under vmcnt (it would wait
+// for them before every LDS read) nor needs m0 elsewhere: this kernel has no
+// other use of m0 (no LDS-DMA builtins, no indirect register indexing). The
+// wait is vm_wait0().
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff), "s"(rs)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
 #endif
+
+// LDS byte address of a __shared__ location.
+__device__ __forceinline__ uint32_t lds_u32(const float* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float*)p;
+}
+__device__ __forceinline__ void vm_wait0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 template <int CAP>
 __device__ inline void compact_row(uint64_t* __restrict__ base, int c, int Kp, int lane, uint64_t* thr_row,
@@ -98,8 +120,8 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
     const float* __restrict__ qb, const float* __restrict__ xb, float scale, const uint8_t* __restrict__ live,
     const uint8_t* __restrict__ accept, int S, int QB, int per_split, int Kp, uint64_t* __restrict__ cand,
     unsigned long long* __restrict__ gthr) {
-  __shared__ float sQ[2][FB_M * FB_LDR];
-  __shared__ float sX[2][FB_N * FB_LDR];
+  __shared__ __align__(16) float sQ[2][FB_M * FB_K];
+  __shared__ __align__(16) float sX[2][FB_N * FB_K];
   __shared__ uint64_t thr[FB_M];
   __shared__ int cnt[FB_M];
   __shared__ __align__(16) float sqb[FB_M];
@@ -131,7 +153,10 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
   }
   __syncthreads();
 
-  const int lr = tid >> 3, lc = (tid & 7) * 4;  // global->LDS copy: row, column
+  // global->LDS copy: instruction u of wave wid fills rows 32 wid + 8 u ..
+  // +7 of a slice; lane l lands at chunk position l & 7 of row 8 u + l / 8,
+  // so it fetches that row's chunk (l & 7) ^ (row & 7)
+  const int crow = 32 * wid + (lane >> 3), cchunk = (lane & 7) ^ ((lane >> 3) & 7);
   const int nK = (ld + FB_K - 1) / FB_K;
 
   for (int n0 = s_begin; n0 < s_end; n0 += FB_N) {
@@ -148,69 +173,56 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    float4 rq[4], rx[4];
 #if defined(__HIP_DEVICE_COMPILE__)
-    // Buffer loads over this tile's query and slot rows: rows past the valid
-    // ones fall outside the resource and read as zero, so full k slices need
-    // no per-element guards (and no VALU work beyond one offset add).
+    // Buffer loads over this tile's query and slot rows, straight to LDS:
+    // rows past the valid ones, and the chunks past a row's end in the last
+    // slice of a stride that is not a multiple of FB_K, are given an offset
+    // outside the resource and land as zeros.
     const float* q_rows = Q + (size_t)q0 * ld;
     const float* x_rows = X + (size_t)n0 * ld;
     const int q_bytes = max(min(nq - q0, FB_M), 0) * ld * 4, x_bytes = max(min(s_end - n0, FB_N), 0) * ld * 4;
-    const int voff = (lr * ld + lc) * 4, vstep = 32 * ld * 4;
 #endif
-    auto gload = [&](int k0) {
+    auto gload = [&](int k0, int buf) {
 #if defined(__HIP_DEVICE_COMPILE__)
-      // The resources are rebuilt per call from readfirstlane'd scalars: a
-      // resource the compiler hoists and keeps in VGPRs is not known to be
-      // uniform at its use, and each load then runs in a waterfall loop.
+      // the resources are rebuilt per call from readfirstlane'd scalars (a
+      // hoisted resource kept in VGPRs is not known to be uniform)
       const __amdgpu_buffer_rsrc_t rs_q = uniform_rsrc(q_rows, q_bytes);
       const __amdgpu_buffer_rsrc_t rs_x = uniform_rsrc(x_rows, x_bytes);
+      const int kc = k0 + cchunk * 4;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const auto a = __builtin_amdgcn_raw_buffer_load_b128(rs_q, voff + i * vstep + k0 * 4, 0, 0);
-        const auto b = __builtin_amdgcn_raw_buffer_load_b128(rs_x, voff + i * vstep + k0 * 4, 0, 0);
-        rq[i] = __builtin_bit_cast(float4, a);
-        rx[i] = __builtin_bit_cast(float4, b);
-      }
-      // the last slice of a row whose stride is not a multiple of FB_K: the
-      // float4s past the row end belong to the next row
-      if (k0 + FB_K > ld && k0 + lc >= ld) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          rq[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-          rx[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t voff = kc < ld ? (uint32_t)(((crow + 8 * u) * ld + kc) * 4) : 0x7FFFFFF0u;
+        const uint32_t mq = __builtin_amdgcn_readfirstlane(lds_u32(&sQ[buf][(32 * wid + 8 * u) * FB_K]));
+        const uint32_t mx = __builtin_amdgcn_readfirstlane(lds_u32(&sX[buf][(32 * wid + 8 * u) * FB_K]));
+        lds_dma16(rs_q, voff, mq);
+        lds_dma16(rs_x, voff, mx);
       }
 #endif
     };
-    auto lstore = [&](int buf) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = lr + 32 * i;
-        *reinterpret_cast<float4*>(&sQ[buf][row * FB_LDR + lc]) = rq[i];
-        *reinterpret_cast<float4*>(&sX[buf][row * FB_LDR + lc]) = rx[i];
-      }
-    };
 
-    gload(0);
-    lstore(0);
+    gload(0, 0);
+    vm_wait0();
     __syncthreads();
     for (int kt = 0; kt < nK; ++kt) {
       const int cur = kt & 1;
-      if (kt + 1 < nK) gload((kt + 1) * FB_K);
+      if (kt + 1 < nK) gload((kt + 1) * FB_K, cur ^ 1);
       // Lane (h, r) feeds k = h*16 + kk of row r: the MFMA pairs A and B by
       // lane half, so any fixed permutation of k within the slice is a
-      // valid dot product; this one lets each lane read 16 contiguous floats.
-      const float* a0p = &sQ[cur][(wm + r) * FB_LDR + h * 16];
-      const float* a1p = &sQ[cur][(wm + 32 + r) * FB_LDR + h * 16];
-      const float* b0p = &sX[cur][(wn + r) * FB_LDR + h * 16];
-      const float* b1p = &sX[cur][(wn + 32 + r) * FB_LDR + h * 16];
+      // valid dot product; this one lets each lane read 16 contiguous floats
+      // (chunks 4h .. 4h+3 of its row, swizzled by r & 7; wm, wn and 32 are
+      // multiples of 8).
+      const float* a0p = &sQ[cur][(wm + r) * FB_K];
+      const float* a1p = &sQ[cur][(wm + 32 + r) * FB_K];
+      const float* b0p = &sX[cur][(wn + r) * FB_K];
+      const float* b1p = &sX[cur][(wn + 32 + r) * FB_K];
+      const int r7 = r & 7;
 #pragma unroll
       for (int k4 = 0; k4 < 4; ++k4) {
-        const float4 a0 = *reinterpret_cast<const float4*>(a0p + k4 * 4);
-        const float4 a1 = *reinterpret_cast<const float4*>(a1p + k4 * 4);
-        const float4 b0 = *reinterpret_cast<const float4*>(b0p + k4 * 4);
-        const float4 b1 = *reinterpret_cast<const float4*>(b1p + k4 * 4);
+        const int co = ((4 * h + k4) ^ r7) * 4;
+        const float4 a0 = *reinterpret_cast<const float4*>(a0p + co);
+        const float4 a1 = *reinterpret_cast<const float4*>(a1p + co);
+        const float4 b0 = *reinterpret_cast<const float4*>(b0p + co);
+        const float4 b1 = *reinterpret_cast<const float4*>(b1p + co);
         const float av0[4] = {a0.x, a0.y, a0.z, a0.w}, av1[4] = {a1.x, a1.y, a1.z, a1.w};
         const float bv0[4] = {b0.x, b0.y, b0.z, b0.w}, bv1[4] = {b1.x, b1.y, b1.z, b1.w};
 #pragma unroll
@@ -221,7 +233,7 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
           acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(av1[t], bv1[t], acc[1][1], 0, 0, 0);
         }
       }
-      if (kt + 1 < nK) lstore(cur ^ 1);
+      vm_wait0();  // this wave's copies of the next slice have landed
       __syncthreads();
     }
     if (tid < FB_M && g_thr < thr[tid]) {
