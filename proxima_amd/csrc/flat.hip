@@ -75,8 +75,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* p, in
 // wait is vm_wait0().
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t m0) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff), "s"(rs)
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(m0), "v"(voff), "s"(rs),
+               "s"(soff)
                : "memory", "m0");
 }
 #pragma clang diagnostic pop
@@ -157,6 +158,7 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
   // +7 of a slice; lane l lands at chunk position l & 7 of row 8 u + l / 8,
   // so it fetches that row's chunk (l & 7) ^ (row & 7)
   const int crow = 32 * wid + (lane >> 3), cchunk = (lane & 7) ^ ((lane >> 3) & 7);
+  const int wid_s = __builtin_amdgcn_readfirstlane(wid);
   const int nK = (ld + FB_K - 1) / FB_K;
 
   for (int n0 = s_begin; n0 < s_end; n0 += FB_N) {
@@ -188,14 +190,16 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
       // hoisted resource kept in VGPRs is not known to be uniform)
       const __amdgpu_buffer_rsrc_t rs_q = uniform_rsrc(q_rows, q_bytes);
       const __amdgpu_buffer_rsrc_t rs_x = uniform_rsrc(x_rows, x_bytes);
+      // row group u adds 8 u rows through the scalar offset; a lane past the
+      // row end stays outside the resource for every group
       const int kc = k0 + cchunk * 4;
+      const uint32_t voff = kc < ld ? (uint32_t)((crow * ld + kc) * 4) : 0x7FFFFFF0u;
+      const uint32_t q_lds = lds_u32(&sQ[buf][0]), x_lds = lds_u32(&sX[buf][0]);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const uint32_t voff = kc < ld ? (uint32_t)(((crow + 8 * u) * ld + kc) * 4) : 0x7FFFFFF0u;
-        const uint32_t mq = __builtin_amdgcn_readfirstlane(lds_u32(&sQ[buf][(32 * wid + 8 * u) * FB_K]));
-        const uint32_t mx = __builtin_amdgcn_readfirstlane(lds_u32(&sX[buf][(32 * wid + 8 * u) * FB_K]));
-        lds_dma16(rs_q, voff, mq);
-        lds_dma16(rs_x, voff, mx);
+        const uint32_t soff = (uint32_t)(8 * u * ld * 4), grp = (uint32_t)((32 * wid_s + 8 * u) * FB_K * 4);
+        lds_dma16(rs_q, voff, soff, q_lds + grp);
+        lds_dma16(rs_x, voff, soff, x_lds + grp);
       }
 #endif
     };
