@@ -167,6 +167,22 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
     const uint64_t g_thr = tid < FB_M && q0 + tid < nq
                                ? __hip_atomic_load(gthr + q0 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                                : KEY_MAX;
+    // this lane's two slots of the tile (live, accepted, norm), also read
+    // before the k loop so that the epilogue does not wait for them
+    // (unconditional loads at a clamped slot, so that nothing waits for them
+    // before the epilogue; slots past s_end are masked there)
+    int slotj[2];
+    uint32_t lvj[2], acj[2];
+    float xbr[2];
+    const uint8_t* acc_src = accept != nullptr ? accept : live;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      slotj[j] = n0 + wn + j * 32 + r;
+      const int sl = min(slotj[j], N - 1);
+      lvj[j] = live[sl];
+      acj[j] = acc_src[sl];
+      xbr[j] = xb[sl];
+    }
     f16v acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -253,14 +269,12 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
     // key below thr[row] (key_float inverts ord_key; NaN and the sign of zero
     // pass), so only the marked values take the exact key test and append.
     {
-      int slotj[2];
       bool okj[2];
       float xbj[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        slotj[j] = n0 + wn + j * 32 + r;
-        okj[j] = slotj[j] < s_end && live[slotj[j]] && (accept == nullptr || accept[slotj[j]]);
-        xbj[j] = okj[j] ? xb[slotj[j]] : 0.0f;
+        okj[j] = slotj[j] < s_end && (lvj[j] & acj[j]) != 0u;
+        xbj[j] = okj[j] ? xbr[j] : 0.0f;
       }
       uint32_t pass[2] = {0u, 0u};  // pass[i], bit j * 16 + v
 #pragma unroll
