@@ -146,13 +146,22 @@ struct Ctx {
   hipStream_t stream = nullptr;
   std::unordered_map<int, DevBuf<unsigned char>> scratch;  // keyed by purpose
   std::vector<unsigned char> host;                         // pinned-free host staging
+  unsigned long long* pinned = nullptr;                    // 64 pinned host bytes for a search's flags
   unsigned char* get(int key, size_t bytes) {
     auto& b = scratch[key];
     if (b.n < bytes) b.alloc(bytes + bytes / 8 + 256);
     return b.p;
   }
+  // Eight pinned host words: a search copies its device flags and counts
+  // here, so the copy is one direct DMA rather than a staged copy into
+  // pageable memory.
+  unsigned long long* tail_host() {
+    if (!pinned) PXG_HIP(hipHostMalloc((void**)&pinned, 64, hipHostMallocDefault));
+    return pinned;
+  }
   ~Ctx() {
     scratch.clear();
+    if (pinned) (void)hipHostFree(pinned);
     if (stream) (void)hipStreamDestroy(stream);
   }
 };

@@ -32,6 +32,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cmath>
+#include <cstring>
 #include <mutex>
 #include <numeric>
 #include <shared_mutex>
@@ -612,11 +613,13 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
     PXG_HIP(hipGetLastError());
   }
   // exact scan for flagged queries (all of them on the exact path)
-  int nflag = 0;
-  PXG_HIP(hipMemcpyAsync(&nflag, flag_count, 4, hipMemcpyDeviceToHost, s));
-  unsigned long long badv = 0;
-  PXG_HIP(hipMemcpyAsync(&badv, bad, 8, hipMemcpyDeviceToHost, s));
+  // bad (8 bytes) and flag_count (the int after it) in one copy
+  unsigned long long* tail = ctx->tail_host();
+  PXG_HIP(hipMemcpyAsync(tail, bad, 16, hipMemcpyDeviceToHost, s));
   PXG_HIP(hipStreamSynchronize(s));
+  const unsigned long long badv = tail[0];
+  int nflag;
+  std::memcpy(&nflag, &tail[1], sizeof nflag);
   if (badv != ~0ull) {
     const uint32_t qi = (uint32_t)(badv >> 32), comp = (uint32_t)badv;
     raise(PXG_ERR_NON_FINITE, "vector component " + std::to_string(comp) + " is not finite (query " +

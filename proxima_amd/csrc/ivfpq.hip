@@ -1594,7 +1594,8 @@ struct IvfPqIndex {
     }
     // one copy brings back the validation flag and the scanned-entry count
     // (bytes 0-7 and 16-23 of the same scratch block)
-    unsigned long long tail[3] = {0, 0, 0};
+    unsigned long long* tail = ctx->tail_host();
+    tail[0] = tail[1] = tail[2] = 0;
     PXG_HIP(hipMemcpyAsync(tail, bad, scanned_dev ? 24 : 8, hipMemcpyDeviceToHost, s));
     PXG_HIP(hipStreamSynchronize(s));
     tm.finish();

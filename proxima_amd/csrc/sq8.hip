@@ -963,9 +963,10 @@ struct Sq8Index {
       hipLaunchKernelGGL(sq_encode_rows, dim3((unsigned)nq), dim3(64), 0, s, Qp, (int)ld, (int)nq, (int)dim, per_dim,
                          1, d_mn.p, d_inv.p, (const uint32_t*)nullptr, (uint8_t*)Qc, (int)KP);
       PXG_HIP(hipGetLastError());
-      unsigned long long bv = 0;
-      PXG_HIP(hipMemcpyAsync(&bv, bad, 8, hipMemcpyDeviceToHost, s));
+      unsigned long long* tail = ctx->tail_host();
+      PXG_HIP(hipMemcpyAsync(tail, bad, 8, hipMemcpyDeviceToHost, s));
       PXG_HIP(hipStreamSynchronize(s));
+      const unsigned long long bv = tail[0];
       if (bv != ~0ull) {
         const uint64_t row = bv >> 32, comp = (uint32_t)bv;
         raise(PXG_ERR_NON_FINITE, "vector component " + std::to_string(comp) + " is not finite (query " +
@@ -1047,8 +1048,10 @@ struct Sq8Index {
       hipLaunchKernelGGL(sq8_finish, dim3((unsigned)nq), dim3(256), (size_t)cap_c * 8, s, (const int*)ccount,
                          (const uint64_t*)cand, cap_c, kk, okeys, ocount, flag_list, flag_count);
       PXG_HIP(hipGetLastError());
-      PXG_HIP(hipMemcpyAsync(&nflag, flag_count, 4, hipMemcpyDeviceToHost, s));
+      int* tail = reinterpret_cast<int*>(ctx->tail_host());
+      PXG_HIP(hipMemcpyAsync(tail, flag_count, 4, hipMemcpyDeviceToHost, s));
       PXG_HIP(hipStreamSynchronize(s));
+      nflag = tail[0];
       *fallbacks = (uint64_t)nflag;
     } else {
       tm.mark(1);
