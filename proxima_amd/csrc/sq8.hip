@@ -963,16 +963,8 @@ struct Sq8Index {
       hipLaunchKernelGGL(sq_encode_rows, dim3((unsigned)nq), dim3(64), 0, s, Qp, (int)ld, (int)nq, (int)dim, per_dim,
                          1, d_mn.p, d_inv.p, (const uint32_t*)nullptr, (uint8_t*)Qc, (int)KP);
       PXG_HIP(hipGetLastError());
-      unsigned long long* tail = ctx->tail_host();
-      PXG_HIP(hipMemcpyAsync(tail, bad, 8, hipMemcpyDeviceToHost, s));
-      PXG_HIP(hipStreamSynchronize(s));
-      const unsigned long long bv = tail[0];
-      if (bv != ~0ull) {
-        const uint64_t row = bv >> 32, comp = (uint32_t)bv;
-        raise(PXG_ERR_NON_FINITE, "vector component " + std::to_string(comp) + " is not finite (query " +
-                                      std::to_string(row) + ")",
-              comp, row, NAN);
-      }
+      // the non-finite flag is read with the search's next host sync (a
+      // non-finite query only scores garbage until then)
     } else {
       hipLaunchKernelGGL(sq8_place_codes, dim3((unsigned)nq), dim3(64), 0, s, d_qcodes, (int)nq, (int)dim, (int)KP,
                          (const uint32_t*)nullptr, Qc);
@@ -1048,10 +1040,12 @@ struct Sq8Index {
       hipLaunchKernelGGL(sq8_finish, dim3((unsigned)nq), dim3(256), (size_t)cap_c * 8, s, (const int*)ccount,
                          (const uint64_t*)cand, cap_c, kk, okeys, ocount, flag_list, flag_count);
       PXG_HIP(hipGetLastError());
-      int* tail = reinterpret_cast<int*>(ctx->tail_host());
-      PXG_HIP(hipMemcpyAsync(tail, flag_count, 4, hipMemcpyDeviceToHost, s));
+      // bad (8 bytes) and flag_count (the int after it) in one copy
+      unsigned long long* tail = ctx->tail_host();
+      PXG_HIP(hipMemcpyAsync(tail, bad, 16, hipMemcpyDeviceToHost, s));
       PXG_HIP(hipStreamSynchronize(s));
-      nflag = tail[0];
+      if (d_raw) check_non_finite(tail[0]);
+      std::memcpy(&nflag, &tail[1], sizeof nflag);
       *fallbacks = (uint64_t)nflag;
     } else {
       tm.mark(1);
@@ -1087,8 +1081,21 @@ struct Sq8Index {
                          (const uint32_t*)ocount, kk, (int)k, d_rank_slot.p, d_ids.p, d_oid, d_od, d_oc);
     }
     PXG_HIP(hipGetLastError());
+    unsigned long long* tail = ctx->tail_host();
+    if (d_raw && !mfma) PXG_HIP(hipMemcpyAsync(tail, bad, 8, hipMemcpyDeviceToHost, s));
     PXG_HIP(hipStreamSynchronize(s));
+    if (d_raw && !mfma) check_non_finite(tail[0]);
     tm.finish();
+  }
+
+  // flat_prep_queries' flag: ~0 or (query << 32 | component) of the first
+  // non-finite component
+  static void check_non_finite(unsigned long long bv) {
+    if (bv == ~0ull) return;
+    const uint64_t row = bv >> 32, comp = (uint32_t)bv;
+    raise(PXG_ERR_NON_FINITE,
+          "vector component " + std::to_string(comp) + " is not finite (query " + std::to_string(row) + ")", comp,
+          row, NAN);
   }
 };
 

@@ -225,6 +225,29 @@ def test_cosine_search_codes_device_paths(gpu):
     assert_same((out_i.cpu().numpy().view(np.uint64), out_d.cpu().numpy(), out_c.cpu().numpy().view(np.uint32)), want)
 
 
+@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("rescore", [0, 20])
+def test_non_finite_query_raises_and_the_index_still_searches(gpu, mode, rescore):
+    px = gpu
+    rng = np.random.default_rng(11 + mode)
+    n, dim = 9000, 64
+    x = uniform(rng, n, dim)
+    idx = px.Sq8Index(px.VectorSpace(dim, px.Metric.INNER_PRODUCT), capacity=n)
+    idx.train(x[:4000])
+    idx.insert_batch(np.arange(n, dtype=np.uint64), x)
+    idx.set_search_mode(mode)
+    q = uniform(rng, 40, dim)
+    for pos, val in ((0, np.nan), (39, np.inf), (17, -np.inf)):
+        bad = q.copy()
+        bad[pos, 5 + pos] = val
+        with pytest.raises(px.NonFinite) as e:
+            idx.search_batch(bad, 10, rescore=rescore)
+        assert e.value.index == 5 + pos
+    codes, ranges = oracle_index(x, x[:4000])
+    assert_same(idx.search_batch(q, 10, rescore=rescore),
+                oracle_search(codes, np.arange(n), q, ranges, 10, rescore=rescore))
+
+
 def test_sq8_errors_and_edges(gpu):
     px = gpu
     sp = px.VectorSpace(16, px.Metric.INNER_PRODUCT)
