@@ -1126,35 +1126,54 @@ __global__ __launch_bounds__(NT) void km_sums(const float* __restrict__ P, int l
   }
 }
 
-// farthest_point (kmeans.rs:215-226): first point with the largest distance
-// (strict >, starting from -1.0).
-__global__ __launch_bounds__(1024) void km_farthest(const float* __restrict__ dist, int n, long long* __restrict__ out) {
-  __shared__ float sd[1024];
-  __shared__ int si[1024];
-  float bd = -1.0f;
-  int bi = 0;
-  const int t = threadIdx.x;
-  // contiguous ranges keep the "first" rule with a per-thread strict >
-  const int per = (n + 1023) / 1024;
-  for (int i = t * per; i < min(n, (t + 1) * per); ++i) {
-    if (dist[i] > bd) {
-      bd = dist[i];
-      bi = i;
-    }
+// farthest_point (kmeans.rs:215-226): the first point with the largest
+// distance (strict >, starting from -1.0). Distances are >= 0 (sums of
+// squares and minima of them; + 0.0 folds a -0.0 into +0.0, which compares
+// equal), so that is the largest value and, among equal values, the smallest
+// index: the largest key (value bits << 32 | ~index). Stage 1 gives one key
+// per block over a contiguous range read coalesced, stage 2 the largest.
+constexpr int KF_BLOCKS = 512;
+
+__device__ inline unsigned long long block_max_u64_256(unsigned long long v, unsigned long long* sh) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const unsigned long long p = shfl_xor64(v, o);
+    v = p > v ? p : v;
   }
-  sd[t] = bd;
-  si[t] = bi;
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
   __syncthreads();
-  if (t == 0) {
-    float b = -1.0f;
-    int best = 0;
-    for (int u = 0; u < 1024; ++u)
-      if (sd[u] > b) {
-        b = sd[u];
-        best = si[u];
-      }
-    *out = best;
+  unsigned long long r = sh[0];
+  for (int i = 1; i < 4; ++i) r = sh[i] > r ? sh[i] : r;
+  return r;
+}
+
+__global__ __launch_bounds__(256) void km_farthest_part(const float* __restrict__ dist, int n,
+                                                        unsigned long long* __restrict__ part) {
+  __shared__ unsigned long long sh[4];
+  const int per = (n + KF_BLOCKS - 1) / KF_BLOCKS;
+  const int lo = blockIdx.x * per, hi = min(n, lo + per);
+  unsigned long long best = 0;  // below every point's key (~index is never 0)
+  for (int i = lo + (int)threadIdx.x; i < hi; i += 256) {
+    const unsigned long long key =
+        ((unsigned long long)__float_as_uint(dist[i] + 0.0f) << 32) | (0xFFFFFFFFu - (uint32_t)i);
+    best = key > best ? key : best;
   }
+  best = block_max_u64_256(best, sh);
+  if (threadIdx.x == 0) part[blockIdx.x] = best;
+}
+
+__global__ __launch_bounds__(256) void km_farthest_pick(const unsigned long long* __restrict__ part,
+                                                        long long* __restrict__ out) {
+  __shared__ unsigned long long sh[4];
+  unsigned long long best = 0;
+  for (int i = threadIdx.x; i < KF_BLOCKS; i += 256) best = part[i] > best ? part[i] : best;
+  best = block_max_u64_256(best, sh);
+  if (threadIdx.x == 0) *out = (long long)(0xFFFFFFFFu - (uint32_t)best);
+}
+
+static void launch_farthest(const float* dist, size_t n, unsigned long long* part, long long* out, hipStream_t s) {
+  hipLaunchKernelGGL(km_farthest_part, dim3(KF_BLOCKS), dim3(256), 0, s, dist, (int)n, part);
+  hipLaunchKernelGGL(km_farthest_pick, dim3(1), dim3(256), 0, s, (const unsigned long long*)part, out);
 }
 
 // Optional phase timings on stderr (PXG_TRAIN_VERBOSE=1), for tuning.
@@ -1195,6 +1214,7 @@ KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req
   DevBuf<float> dist(n), newc(k * dim), work(k * dim);
   DevBuf<int> changed(1);
   DevBuf<long long> far(1);
+  DevBuf<unsigned long long> far_part(KF_BLOCKS);
   PXG_HIP(hipMemsetAsync(prev.p, 0, n * 4, s));
   F64Sum sums;
   size_t tmp_bytes = 0;
@@ -1285,7 +1305,7 @@ KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req
           hipLaunchKernelGGL(km_min_into, gm, dim3(256), 0, s, L.p, tmp.p, (int)n, (float*)nullptr);
         }
         hipLaunchKernelGGL(km_min_into, gm, dim3(256), 0, s, L.p, R.p + ii * n, (int)n, tmp.p);
-        hipLaunchKernelGGL(km_farthest, dim3(1), dim3(1024), 0, s, tmp.p, (int)n, far.p);
+        launch_farthest(tmp.p, n, far_part.p, far.p, s);
         hipLaunchKernelGGL(copy_row_at, dim3(1), dim3(256), 0, s, P, ldp, far.p, dim, newc.p + E[ii] * dim);
         if (ii + 1 < m)
           hipLaunchKernelGGL(km_pp_round, dim3(nb), dim3(256), 0, s, P, ldp, (int)n, dim, newc.p + E[ii] * dim, L.p,
@@ -1299,7 +1319,7 @@ KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req
       PXG_HIP(hipMemcpyAsync(work.p, newc.p, c * dim * 4, hipMemcpyDeviceToDevice, s));
       PXG_HIP(hipMemcpyAsync(work.p + c * dim, cents.p + c * dim, (k - c) * dim * 4, hipMemcpyDeviceToDevice, s));
       nearest_device(P, ldp, nullptr, n, dim, work.p, dim, k, false, keys_sorted.p, dist.p, s);
-      hipLaunchKernelGGL(km_farthest, dim3(1), dim3(1024), 0, s, dist.p, (int)n, far.p);
+      launch_farthest(dist.p, n, far_part.p, far.p, s);
       long long victim = 0;
       PXG_HIP(hipMemcpyAsync(&victim, far.p, 8, hipMemcpyDeviceToHost, s));
       PXG_HIP(hipStreamSynchronize(s));

@@ -76,6 +76,41 @@ def test_lloyd_several_empty_clusters_in_one_iteration(gpu):
     assert got[2] == want[2] and got[3] == want[3]
 
 
+@pytest.mark.parametrize("empties", [(7,), (7, 60)])
+def test_farthest_point_ties_take_the_first_index(gpu, empties):
+    """Two distinct outliers, m - 20 e0 (index 1000) and m + 20 e0 (index
+    4000), are the farthest points at exactly equal distance 400 from their
+    centroid m, whose 8-point group keeps the mean m exactly: the reseed takes
+    index 1000 (strict > from -1.0), through the one-empty and the segmented
+    several-empty searches."""
+    px = gpu
+    rng = np.random.default_rng(21)
+    dim = 32
+    pts = clustered(rng, 6000, dim, 40, 0.3)
+    m = np.zeros(dim, np.float32)
+    m[0] = 100.0
+    group = {1000: -20.0, 4000: 20.0}
+    for j, idx in enumerate(range(2000, 2006)):
+        group[idx] = None
+        pts[idx] = m
+        pts[idx][1 + j // 2] += np.float32(1.0 if j % 2 == 0 else -1.0)
+    for idx in (1000, 4000):
+        pts[idx] = m
+        pts[idx][0] += np.float32(group[idx])
+    pool = np.setdiff1d(np.arange(6000), list(group))
+    init = pts[rng.choice(pool, 80, replace=False)].copy()
+    init[30] = m
+    for c in empties:
+        init[c] += np.float32(5000.0)  # attracts nothing
+    got = px.kmeans_lloyd(pts, init, 3)
+    want = orc.kmeans_lloyd(pts, init, 3)
+    assert np.array_equal(bits(got[0]), bits(want[0]))
+    assert np.array_equal(got[1], want[1])
+    assert got[2] == want[2] and got[3] == want[3]
+    one = px.kmeans_lloyd(pts, init, 1)[0].reshape(80, dim)
+    assert np.array_equal(bits(one[empties[0]]), bits(pts[1000]))  # the first of the tied pair
+
+
 def test_kmeans_pp_picks_match(gpu):
     px = gpu
     rng = np.random.default_rng(6)
