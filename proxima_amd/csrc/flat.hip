@@ -158,8 +158,8 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
   // global->LDS copy: instruction u of wave wid fills rows 32 wid + 8 u ..
   // +7 of a slice; lane l lands at chunk position l & 7 of row 8 u + l / 8,
   // so it fetches that row's chunk (l & 7) ^ (row & 7)
-  const int crow = 32 * wid + (lane >> 3), cchunk = (lane & 7) ^ ((lane >> 3) & 7);
-  const int wid_s = __builtin_amdgcn_readfirstlane(wid);
+  [[maybe_unused]] const int crow = 32 * wid + (lane >> 3), cchunk = (lane & 7) ^ ((lane >> 3) & 7);
+  [[maybe_unused]] const int wid_s = __builtin_amdgcn_readfirstlane(wid);
   const int nK = (ld + FB_K - 1) / FB_K;
 
   for (int n0 = s_begin; n0 < s_end; n0 += FB_N) {

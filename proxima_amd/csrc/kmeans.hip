@@ -539,6 +539,11 @@ __global__ void km_compose_rows(const uint32_t* __restrict__ redo, int m, const 
 // MFMA pass cannot certify.
 void nearest_device(const float* P, int ldp, const uint32_t* rows, size_t n, int dim, const float* C, int ldc,
                     size_t k, bool unrolled, uint32_t* assign, float* dist, hipStream_t s) {
+  nearest_device(P, ldp, rows, n, dim, C, ldc, k, unrolled, assign, dist, s, nullptr);
+}
+
+void nearest_device(const float* P, int ldp, const uint32_t* rows, size_t n, int dim, const float* C, int ldc,
+                    size_t k, bool unrolled, uint32_t* assign, float* dist, hipStream_t s, NearestWork* ws) {
   g_last_redo = 0;
   if (n == 0) return;
   const bool aligned = ldp % 4 == 0 && ldc % 4 == 0 && dim % 4 == 0 && ((uintptr_t)P & 15) == 0 &&
@@ -550,32 +555,52 @@ void nearest_device(const float* P, int ldp, const uint32_t* rows, size_t n, int
       launch_assign<false>(P, ldp, rows, n, dim, C, ldc, k, assign, dist, s);
     return;
   }
-  DevBuf<float> pn(n), cn(k), cmax(1), best(n), second(n);
-  DevBuf<uint32_t> bidx(n), redo(n);
-  DevBuf<int> nredo(1);
-  hipLaunchKernelGGL(km_row_norms, dim3((unsigned)((n + 31) / 32)), dim3(256), 0, s, P, ldp, rows, (int)n, dim,
-                     pn.p);
+  NearestWork local;
+  NearestWork& w = ws ? *ws : local;
+  w.pn.reserve(n);
+  w.cn.reserve(k);
+  w.cmax.reserve(1);
+  w.best.reserve(n);
+  w.second.reserve(n);
+  w.bidx.reserve(n);
+  w.redo.reserve(n);
+  w.nredo.reserve(1);
+  float *const pn = w.pn.p, *const cn = w.cn.p, *const cmax = w.cmax.p, *const best = w.best.p,
+               *const second = w.second.p;
+  uint32_t *const bidx = w.bidx.p, *const redo = w.redo.p;
+  int* const nredo = w.nredo.p;
+  const bool keyed = rows == nullptr;
+  if (!(keyed && w.pn_of == P && w.pn_ld == ldp && w.pn_dim == dim && w.pn_n == n)) {
+    hipLaunchKernelGGL(km_row_norms, dim3((unsigned)((n + 31) / 32)), dim3(256), 0, s, P, ldp, rows, (int)n, dim,
+                       pn);
+    w.pn_of = keyed ? P : nullptr;
+    w.pn_ld = ldp;
+    w.pn_dim = dim;
+    w.pn_n = n;
+  }
   hipLaunchKernelGGL(km_row_norms, dim3((unsigned)((k + 31) / 32)), dim3(256), 0, s, C, ldc,
-                     (const uint32_t*)nullptr, (int)k, dim, cn.p);
-  hipLaunchKernelGGL(km_max_of, dim3(1), dim3(1024), 0, s, cn.p, (int)k, cmax.p);
+                     (const uint32_t*)nullptr, (int)k, dim, cn);
+  hipLaunchKernelGGL(km_max_of, dim3(1), dim3(1024), 0, s, cn, (int)k, cmax);
   hipEvent_t e0, e1;
   PXG_HIP(hipEventCreate(&e0));
   PXG_HIP(hipEventCreate(&e1));
   PXG_HIP(hipEventRecord(e0, s));
   hipLaunchKernelGGL(km_mfma_top, dim3((unsigned)((n + KA_M - 1) / KA_M)), dim3(256), 0, s, P, ldp, rows, (int)n,
-                     dim, C, ldc, (int)k, pn.p, cn.p, bidx.p, best.p, second.p);
+                     dim, C, ldc, (int)k, (const float*)pn, (const float*)cn, bidx, best, second);
   PXG_HIP(hipEventRecord(e1, s));
-  PXG_HIP(hipMemsetAsync(nredo.p, 0, 4, s));
+  PXG_HIP(hipMemsetAsync(nredo, 0, 4, s));
   const dim3 g((unsigned)((n + 255) / 256));
   if (unrolled)
-    hipLaunchKernelGGL(km_mfma_verify<true>, g, dim3(256), 0, s, P, ldp, rows, (int)n, dim, C, ldc, pn.p, cmax.p,
-                       bidx.p, best.p, second.p, assign, dist, redo.p, nredo.p);
+    hipLaunchKernelGGL(km_mfma_verify<true>, g, dim3(256), 0, s, P, ldp, rows, (int)n, dim, C, ldc, (const float*)pn,
+                       (const float*)cmax, (const uint32_t*)bidx, (const float*)best, (const float*)second, assign,
+                       dist, redo, nredo);
   else
-    hipLaunchKernelGGL(km_mfma_verify<false>, g, dim3(256), 0, s, P, ldp, rows, (int)n, dim, C, ldc, pn.p, cmax.p,
-                       bidx.p, best.p, second.p, assign, dist, redo.p, nredo.p);
+    hipLaunchKernelGGL(km_mfma_verify<false>, g, dim3(256), 0, s, P, ldp, rows, (int)n, dim, C, ldc, (const float*)pn,
+                       (const float*)cmax, (const uint32_t*)bidx, (const float*)best, (const float*)second, assign,
+                       dist, redo, nredo);
   PXG_HIP(hipGetLastError());
   int m = 0;
-  PXG_HIP(hipMemcpyAsync(&m, nredo.p, 4, hipMemcpyDeviceToHost, s));
+  PXG_HIP(hipMemcpyAsync(&m, nredo, 4, hipMemcpyDeviceToHost, s));
   PXG_HIP(hipStreamSynchronize(s));
   float ms = 0.0f;
   PXG_HIP(hipEventElapsedTime(&ms, e0, e1));
@@ -588,17 +613,21 @@ void nearest_device(const float* P, int ldp, const uint32_t* rows, size_t n, int
   g_last_redo = (size_t)m;
   if (m == 0) return;
   // the uncertified points: exact scan over their rows, results scattered back
-  DevBuf<uint32_t> rrows(m), ra(m);
-  DevBuf<float> rd(m);
-  hipLaunchKernelGGL(km_compose_rows, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, s, redo.p, m, rows, rrows.p);
+  w.rrows.reserve(m);
+  w.ra.reserve(m);
+  w.rd.reserve(m);
+  uint32_t *const rrows = w.rrows.p, *const ra = w.ra.p;
+  float* const rd = w.rd.p;
+  hipLaunchKernelGGL(km_compose_rows, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, s, (const uint32_t*)redo, m,
+                     rows, rrows);
   if (unrolled)
-    hipLaunchKernelGGL(km_exact_wave<true>, dim3((unsigned)((m + 3) / 4)), dim3(256), 0, s, P, ldp, rrows.p, m, dim, C,
-                       ldc, (int)k, ra.p, rd.p);
+    hipLaunchKernelGGL(km_exact_wave<true>, dim3((unsigned)((m + 3) / 4)), dim3(256), 0, s, P, ldp,
+                       (const uint32_t*)rrows, m, dim, C, ldc, (int)k, ra, rd);
   else
-    hipLaunchKernelGGL(km_exact_wave<false>, dim3((unsigned)((m + 3) / 4)), dim3(256), 0, s, P, ldp, rrows.p, m, dim,
-                       C, ldc, (int)k, ra.p, rd.p);
-  hipLaunchKernelGGL(km_scatter_redo, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, s, redo.p, m, ra.p, rd.p,
-                     assign, dist);
+    hipLaunchKernelGGL(km_exact_wave<false>, dim3((unsigned)((m + 3) / 4)), dim3(256), 0, s, P, ldp,
+                       (const uint32_t*)rrows, m, dim, C, ldc, (int)k, ra, rd);
+  hipLaunchKernelGGL(km_scatter_redo, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, s, (const uint32_t*)redo, m,
+                     (const uint32_t*)ra, (const float*)rd, assign, dist);
   PXG_HIP(hipGetLastError());
 }
 
@@ -1215,6 +1244,7 @@ KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req
   DevBuf<int> changed(1);
   DevBuf<long long> far(1);
   DevBuf<unsigned long long> far_part(KF_BLOCKS);
+  NearestWork nw;  // the points do not change during the run
   PXG_HIP(hipMemsetAsync(prev.p, 0, n * 4, s));
   F64Sum sums;
   size_t tmp_bytes = 0;
@@ -1226,7 +1256,7 @@ KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req
   const dim3 gn((unsigned)((n + 255) / 256));
   for (size_t it = 0; it < max_iter; ++it) {
     out.iterations = it + 1;
-    nearest_device(P, ldp, nullptr, n, dim, cents.p, dim, k, false, assign.p, dist.p, s);
+    nearest_device(P, ldp, nullptr, n, dim, cents.p, dim, k, false, assign.p, dist.p, s, &nw);
     out.inertia = sums.total(dist.p, n, s);
     if (!sums.last_exact) ++out.inexact_sums;
     PXG_HIP(hipMemsetAsync(changed.p, 0, 4, s));
@@ -1291,7 +1321,7 @@ KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req
       for (size_t ii = m; ii-- > 0;) {
         const size_t lo = E[ii], hi = ii + 1 < m ? E[ii + 1] : k;
         nearest_device(P, ldp, nullptr, n, dim, cents.p + lo * dim, dim, hi - lo, false, keys_sorted.p,
-                       R.p + ii * n, s);
+                       R.p + ii * n, s, &nw);
         if (ii + 1 < m)
           hipLaunchKernelGGL(km_min_into, gm, dim3(256), 0, s, R.p + ii * n, R.p + (ii + 1) * n, (int)n,
                              (float*)nullptr);
@@ -1301,7 +1331,8 @@ KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req
       for (size_t ii = 0; ii < m; ++ii) {
         const size_t lo = ii == 0 ? 0 : E[ii - 1] + 1, hi = E[ii];
         if (hi > lo) {
-          nearest_device(P, ldp, nullptr, n, dim, newc.p + lo * dim, dim, hi - lo, false, keys_sorted.p, tmp.p, s);
+          nearest_device(P, ldp, nullptr, n, dim, newc.p + lo * dim, dim, hi - lo, false, keys_sorted.p, tmp.p, s,
+                         &nw);
           hipLaunchKernelGGL(km_min_into, gm, dim3(256), 0, s, L.p, tmp.p, (int)n, (float*)nullptr);
         }
         hipLaunchKernelGGL(km_min_into, gm, dim3(256), 0, s, L.p, R.p + ii * n, (int)n, tmp.p);
@@ -1318,7 +1349,7 @@ KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req
       ++empties;
       PXG_HIP(hipMemcpyAsync(work.p, newc.p, c * dim * 4, hipMemcpyDeviceToDevice, s));
       PXG_HIP(hipMemcpyAsync(work.p + c * dim, cents.p + c * dim, (k - c) * dim * 4, hipMemcpyDeviceToDevice, s));
-      nearest_device(P, ldp, nullptr, n, dim, work.p, dim, k, false, keys_sorted.p, dist.p, s);
+      nearest_device(P, ldp, nullptr, n, dim, work.p, dim, k, false, keys_sorted.p, dist.p, s, &nw);
       launch_farthest(dist.p, n, far_part.p, far.p, s);
       long long victim = 0;
       PXG_HIP(hipMemcpyAsync(&victim, far.p, 8, hipMemcpyDeviceToHost, s));

@@ -50,6 +50,21 @@ struct KmeansOut {
 void nearest_device(const float* P, int ldp, const uint32_t* rows, size_t n, int dim, const float* C, int ldc,
                     size_t k, bool unrolled, uint32_t* assign, float* dist, hipStream_t s);
 
+// Scratch of the MFMA assignment, kept across calls on one stream. Without a
+// row list and with the same P, ldp, dim and n as the call that computed
+// them, the point norms are reused: the caller promises the points did not
+// change in between.
+struct NearestWork {
+  DevBuf<float> pn, cn, cmax, best, second, rd;
+  DevBuf<uint32_t> bidx, redo, rrows, ra;
+  DevBuf<int> nredo;
+  const float* pn_of = nullptr;
+  int pn_ld = 0, pn_dim = 0;
+  size_t pn_n = 0;
+};
+void nearest_device(const float* P, int ldp, const uint32_t* rows, size_t n, int dim, const float* C, int ldc,
+                    size_t k, bool unrolled, uint32_t* assign, float* dist, hipStream_t s, NearestWork* ws);
+
 // kmeans(): Lloyd from k-means++ seeds drawn from `rng` (or from `init`, k*dim
 // dense device floats), points P[n][ldp]. Writes k*dim dense centroids.
 KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k, size_t max_iter, ChaCha8* rng,
