@@ -33,44 +33,81 @@ __device__ inline float fx_gaussian(uint32_t w1, uint32_t w2) {
   return sqrtf(-2.0f * l) * c;
 }
 
-// Gaussians g in [g0, g1) of the stream, written through `emit(g, value)`.
-template <class Emit>
-__device__ inline void fx_block(const uint32_t* key, uint64_t g0, uint64_t g1, Emit emit) {
+// This thread's block of the stream: Gaussians first .. first+7 into v.
+// False when the block starts at or past g1.
+__device__ inline bool fx_values(const uint32_t* key, uint64_t g0, uint64_t g1, uint64_t& first, float (&v)[8]) {
   const uint64_t blk = (g0 / 8) + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const uint64_t first = blk * 8;
-  if (first >= g1) return;
+  first = blk * 8;
+  if (first >= g1) return false;
   uint32_t k[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) k[i] = key[i];
   uint32_t w[16];
   ChaCha8::block(k, blk, w);
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const uint64_t g = first + u;
-    if (g >= g0 && g < g1) emit(g, fx_gaussian(w[2 * u], w[2 * u + 1]));
-  }
+  for (int u = 0; u < 8; ++u) v[u] = fx_gaussian(w[2 * u], w[2 * u + 1]);
+  return true;
 }
 
 __global__ void fx_centres(const uint32_t* __restrict__ key, uint64_t total, float* __restrict__ centres) {
-  fx_block(key, 0, total, [&](uint64_t g, float v) { centres[g] = v * 4.0f; });
+  uint64_t first;
+  float v[8];
+  if (!fx_values(key, 0, total, first, v)) return;
+#pragma unroll
+  for (int u = 0; u < 8; ++u)
+    if (first + u < total) centres[first + u] = v[u] * 4.0f;
 }
 
+// Point t = i * dim + d (Gaussian base + t) is centre (i % clusters) plus the
+// Gaussian. A thread's Gaussians are consecutive, so (i, d, i % clusters) is
+// divided out once for its first one and then stepped.
 __global__ void fx_points(const uint32_t* __restrict__ key, uint64_t base, uint64_t total, uint32_t dim,
                           uint64_t clusters, const float* __restrict__ centres, float* __restrict__ vectors) {
-  fx_block(key, base, base + total, [&](uint64_t g, float v) {
-    const uint64_t t = g - base, i = t / dim, d = t % dim;
-    vectors[t] = centres[(i % clusters) * dim + d] + v;
-  });
+  uint64_t first;
+  float v[8];
+  if (!fx_values(key, base, base + total, first, v)) return;
+  const uint64_t t0 = (first > base ? first : base) - base, i0 = t0 / dim;
+  uint32_t d = (uint32_t)(t0 - i0 * dim);
+  uint64_t ci = i0 % clusters;
+  const float* crow = centres + ci * dim;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const uint64_t g = first + u;
+    if (g >= base && g < base + total) {
+      vectors[g - base] = crow[d] + v[u];
+      if (++d == dim) {
+        d = 0;
+        if (++ci == clusters) ci = 0;
+        crow = centres + ci * dim;
+      }
+    }
+  }
 }
 
+// Query t = q * dim + d is corpus point (q * stride) % count plus a quarter
+// of the Gaussian; the source row changes only when q does.
 __global__ void fx_queries(const uint32_t* __restrict__ key, uint64_t base, uint64_t total, uint32_t dim,
                            uint64_t count, uint64_t stride, const float* __restrict__ vectors,
                            float* __restrict__ queries) {
-  fx_block(key, base, base + total, [&](uint64_t g, float v) {
-    const uint64_t t = g - base, q = t / dim, d = t % dim;
-    const uint64_t src = (q * stride) % count;
-    queries[t] = vectors[src * dim + d] + v * 0.25f;
-  });
+  uint64_t first;
+  float v[8];
+  if (!fx_values(key, base, base + total, first, v)) return;
+  const uint64_t t0 = (first > base ? first : base) - base;
+  uint64_t q = t0 / dim;
+  uint32_t d = (uint32_t)(t0 - q * dim);
+  const float* srow = vectors + ((q * stride) % count) * dim;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const uint64_t g = first + u;
+    if (g >= base && g < base + total) {
+      queries[g - base] = srow[d] + v[u] * 0.25f;
+      if (++d == dim) {
+        d = 0;
+        ++q;
+        srow = vectors + ((q * stride) % count) * dim;
+      }
+    }
+  }
 }
 
 static void launch_blocks(uint64_t g0, uint64_t g1, dim3& grid) {
