@@ -18,9 +18,10 @@
 // Search (ivfpq.rs:998-1110), per batch:
 //   coarse      exact squared_euclidean_unrolled to every centroid (bit-exact,
 //               so the probed list set is the reference's) and the nprobe
-//               smallest (distance, list): ivf_coarse_topk over the transposed
-//               centroids for nprobe <= 64, else the exact flat index over the
-//               centroids, else ivf_coarse_keys + ivf_coarse_select.
+//               smallest (distance, list): ivf_coarse_dist (all keys, over
+//               the transposed centroids) + ivf_coarse_pick for nprobe <= 64,
+//               else the exact flat index over the centroids, else
+//               ivf_coarse_keys + ivf_coarse_select.
 //   scan        build each probe's distance table exactly as distance_table
 //               does (per subspace, per centroid, sequential d = q - c;
 //               l2 += d*d; ip += q*c), stream the list's codes coalesced (M
@@ -262,83 +263,152 @@ __device__ inline void wave_topk_add(uint64_t key, uint64_t& kept, uint64_t& thr
 }
 
 // Coarse top-nprobe for nprobe <= 64 over the transposed centroid matrix
-// cT[dim][cst] (cst = list count rounded up to 64, zero padded): a block
-// takes IVF_CQ queries (staged in LDS as [dim][IVF_CQ], one broadcast float4
-// per dimension) and its IVF_CW waves split the lists in 64-wide tiles; lane
-// l of a tile computes the exact squared_euclidean_unrolled distance
-// (distance.rs:267-283) from each query to list c0 + l, loading the column
-// coalesced. Each wave keeps per query the 64 smallest (distance, list) keys
-// one per lane, ascending; the waves' lists are merged at the end.
+// cT[dim][cst] (cst = list count rounded up to 64, zero padded), in two
+// phases: keys of IVF_CQ queries against slices of IVF_CW * 64 lists, then a
+// selection per query.
 constexpr int IVF_CQ = 4, IVF_CW = 8;
 
-// It also adds the query's probed entries (the list lengths) to *scanned.
-__global__ __launch_bounds__(IVF_CW * 64) void ivf_coarse_topk(const float* __restrict__ Qp, int ld, int dim, int nq,
+// Two-phase coarse stage (np <= 64, dim <= 2048). Phase one: the (distance,
+// list) keys of IVF_CQ queries against one slice of IVF_CW * 64 lists per
+// workgroup (grid: query groups x list slices), with the arithmetic of
+// squared_euclidean_unrolled (distance.rs:267-283): lane l of a wave takes
+// list c0 + l, the queries broadcast from LDS as one
+// float4 per dimension, the transposed centroids loaded coalesced. A wave
+// keeping its own top-np lists instead (one workgroup per 4 queries over all
+// lists) took 0.12 ms at 1024 x 4096 x 128: nearly every tile passed its
+// threshold and took the sort-and-merge path.
+__global__ __launch_bounds__(IVF_CW * 64) void ivf_coarse_dist(const float* __restrict__ Qp, int ld, int dim, int nq,
                                                                const float* __restrict__ cT, int cst, int produced,
-                                                               int np, int* __restrict__ probes,
-                                                               const uint32_t* __restrict__ list_off,
-                                                               unsigned long long* __restrict__ scanned) {
+                                                               uint64_t* __restrict__ ck) {
   extern __shared__ float4 sm4[];
-  float* sq = (float*)sm4;                             // [dim][IVF_CQ]
-  uint64_t* mk = (uint64_t*)(sm4 + dim);               // [IVF_CW][IVF_CQ][64]
+  float* sq = (float*)sm4;  // [dim][IVF_CQ]
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int q0 = blockIdx.x * IVF_CQ;
+  const int c0 = blockIdx.y * (IVF_CW * 64) + w * 64;
   for (int t = tid; t < dim * IVF_CQ; t += IVF_CW * 64) {
     const int i = t / IVF_CQ, j = t % IVF_CQ;
     sq[t] = q0 + j < nq ? Qp[(size_t)(q0 + j) * ld + i] : 0.0f;
   }
   __syncthreads();
-  uint64_t kept[IVF_CQ], thr[IVF_CQ];
-#pragma unroll
-  for (int j = 0; j < IVF_CQ; ++j) kept[j] = thr[j] = KEY_MAX;
+  if (c0 >= produced) return;
   const int chunks = dim >> 3;
-  for (int c0 = w * 64; c0 < produced; c0 += IVF_CW * 64) {
-    const float* col = cT + c0 + lane;
-    float acc[IVF_CQ][8];
+  const float* col = cT + c0 + lane;
+  float acc[IVF_CQ][8];
 #pragma unroll
-    for (int j = 0; j < IVF_CQ; ++j)
+  for (int j = 0; j < IVF_CQ; ++j)
 #pragma unroll
-      for (int u = 0; u < 8; ++u) acc[j][u] = 0.0f;
-    for (int cc = 0; cc < chunks; ++cc) {
-      float cv[8];
+    for (int u = 0; u < 8; ++u) acc[j][u] = 0.0f;
+  for (int cc = 0; cc < chunks; ++cc) {
+    float cv[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) cv[u] = col[(size_t)(cc * 8 + u) * cst];
+    for (int u = 0; u < 8; ++u) cv[u] = col[(size_t)(cc * 8 + u) * cst];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float4 qv = sm4[cc * 8 + u];
-        float d;
-        d = qv.x - cv[u]; acc[0][u] += d * d;
-        d = qv.y - cv[u]; acc[1][u] += d * d;
-        d = qv.z - cv[u]; acc[2][u] += d * d;
-        d = qv.w - cv[u]; acc[3][u] += d * d;
-      }
-    }
-    float tail[IVF_CQ] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int i = chunks * 8; i < dim; ++i) {
-      const float c = col[(size_t)i * cst];
-      const float4 qv = sm4[i];
+    for (int u = 0; u < 8; ++u) {
+      const float4 qv = sm4[cc * 8 + u];
       float d;
-      d = qv.x - c; tail[0] += d * d;
-      d = qv.y - c; tail[1] += d * d;
-      d = qv.z - c; tail[2] += d * d;
-      d = qv.w - c; tail[3] += d * d;
-    }
-    const bool valid = c0 + lane < produced;
-#pragma unroll
-    for (int j = 0; j < IVF_CQ; ++j) {
-      const float* a = acc[j];
-      const float dd = (((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))) + tail[j];
-      const uint64_t key = valid ? (((uint64_t)ord_key(dd) << 32) | (uint32_t)(c0 + lane)) : KEY_MAX;
-      wave_topk_add(key, kept[j], thr[j], np, lane);
+      d = qv.x - cv[u]; acc[0][u] += d * d;
+      d = qv.y - cv[u]; acc[1][u] += d * d;
+      d = qv.z - cv[u]; acc[2][u] += d * d;
+      d = qv.w - cv[u]; acc[3][u] += d * d;
     }
   }
+  float tail[IVF_CQ] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int i = chunks * 8; i < dim; ++i) {
+    const float c = col[(size_t)i * cst];
+    const float4 qv = sm4[i];
+    float d;
+    d = qv.x - c; tail[0] += d * d;
+    d = qv.y - c; tail[1] += d * d;
+    d = qv.z - c; tail[2] += d * d;
+    d = qv.w - c; tail[3] += d * d;
+  }
+  if (c0 + lane >= produced) return;
 #pragma unroll
-  for (int j = 0; j < IVF_CQ; ++j) mk[(w * IVF_CQ + j) * 64 + lane] = kept[j];
+  for (int j = 0; j < IVF_CQ; ++j) {
+    const float* a = acc[j];
+    const float dd = (((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))) + tail[j];
+    if (q0 + j < nq) ck[(size_t)(q0 + j) * cst + c0 + lane] = ((uint64_t)ord_key(dd) << 32) | (uint32_t)(c0 + lane);
+  }
+}
+
+// Phase two, one workgroup per query: the np smallest keys, sorted, give the
+// probes in (distance, list) order (ivfpq.rs:1025), and the probed list
+// lengths go to *scanned. The keys are cut into ng = min(64, produced)
+// groups; the np-th smallest group minimum T bounds the np-th smallest key
+// from above (np distinct keys are <= T), so the keys <= T hold the answer:
+// they are gathered in LDS and sorted. Should they exceed IVF_PICK_CAP, a
+// radix select of the np-th key takes over.
+constexpr int IVF_PICK_CAP = 1024;
+__global__ __launch_bounds__(256) void ivf_coarse_pick(const uint64_t* __restrict__ ck, int cst, int produced, int np,
+                                                       int* __restrict__ probes, const uint32_t* __restrict__ list_off,
+                                                       unsigned long long* __restrict__ scanned) {
+  const int q = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  __shared__ uint64_t cand[IVF_PICK_CAP];
+  __shared__ uint64_t gmin[64];
+  __shared__ int hist[256];
+  __shared__ uint64_t sh[4];
+  __shared__ int ncand;
+  __shared__ uint64_t s_t;
+  const uint64_t* base = ck + (size_t)q * cst;
+  const int ng = min(64, produced), gs = (produced + ng - 1) / ng;
+  if (tid == 0) ncand = 0;
+  for (int g = w; g < 64; g += 4) {
+    uint64_t m = KEY_MAX;
+    if (g < ng) {
+      const int b = g * gs, e = min(produced, b + gs);
+      for (int i = b + lane; i < e; i += 64) m = base[i] < m ? base[i] : m;
+    }
+#pragma unroll
+    for (int st = 32; st > 0; st >>= 1) {
+      const uint64_t o = shfl_xor64(m, st);
+      m = o < m ? o : m;
+    }
+    if (lane == 0) gmin[g] = m;
+  }
   __syncthreads();
-  if (w < IVF_CQ && q0 + w < nq) {
-    uint64_t v = mk[w * 64 + lane];
-    for (int ww = 1; ww < IVF_CW; ++ww) wave_merge_sorted(v, mk[(ww * IVF_CQ + w) * 64 + lane], lane);
-    const int l = (int)(uint32_t)v;
-    if (lane < np) probes[(size_t)(q0 + w) * np + lane] = l;
+  if (w == 0) {
+    uint64_t v[1] = {gmin[lane]};
+    wave_bitonic_sort<1>(v, lane);
+    const uint64_t t = readlane64(v[0], np - 1);
+    if (lane == 0) s_t = t;
+  }
+  __syncthreads();
+  const uint64_t t = s_t;
+  for (int i = tid; i < produced; i += 256) {
+    const uint64_t x = base[i];
+    if (x <= t) {
+      const int at = atomicAdd(&ncand, 1);
+      if (at < IVF_PICK_CAP) cand[at] = x;
+    }
+  }
+  __syncthreads();
+  const int nc = ncand;
+  if (nc <= IVF_PICK_CAP) {
+    int P = 64;
+    while (P < nc) P <<= 1;
+    for (int i = nc + tid; i < P; i += 256) cand[i] = KEY_MAX;
+    __syncthreads();
+    block_bitonic_sort(cand, P);
+  } else {
+    auto get = [&](int i) -> uint64_t { return base[i]; };
+    const uint64_t pivot = block_radix_select(get, produced, np, hist, sh);
+    if (tid == 0) ncand = 0;
+    __syncthreads();
+    for (int i = tid; i < produced; i += 256) {
+      const uint64_t x = base[i];
+      if (x <= pivot) cand[atomicAdd(&ncand, 1)] = x;  // np <= 64 of them
+    }
+    __syncthreads();
+    if (w == 0) {
+      uint64_t v[1] = {lane < np ? cand[lane] : KEY_MAX};
+      wave_bitonic_sort<1>(v, lane);
+      cand[lane] = v[0];
+    }
+    __syncthreads();
+  }
+  if (w == 0) {
+    const int l = (int)(uint32_t)cand[lane];
+    if (lane < np) probes[(size_t)q * np + lane] = l;
     uint32_t len = lane < np ? list_off[l + 1] - list_off[l] : 0u;
 #pragma unroll
     for (int st = 32; st > 0; st >>= 1) len += xor_lane_rt(len, st);
@@ -1472,10 +1542,12 @@ struct IvfPqIndex {
       PXG_HIP(hipMemsetAsync(scanned_dev, 0, 8, s));
       const bool fused_count = np <= 64 && dim <= 2048;
       if (fused_count) {
-        const size_t lds = (size_t)dim * IVF_CQ * 4 + (size_t)IVF_CW * IVF_CQ * 64 * 8;
-        hipLaunchKernelGGL(ivf_coarse_topk, dim3((unsigned)((nq + IVF_CQ - 1) / IVF_CQ)), dim3(IVF_CW * 64), lds, s,
-                           Qp, (int)ld, (int)dim, (int)nq, cents_t.p, cst, produced, np, probes, list_off.p,
-                           scanned_dev);
+        uint64_t* keys = (uint64_t*)ctx->get(13, (size_t)nq * cst * 8);
+        const dim3 gd((unsigned)((nq + IVF_CQ - 1) / IVF_CQ), (unsigned)((produced + IVF_CW * 64 - 1) / (IVF_CW * 64)));
+        hipLaunchKernelGGL(ivf_coarse_dist, gd, dim3(IVF_CW * 64), (size_t)dim * IVF_CQ * 4, s, Qp, (int)ld, (int)dim,
+                           (int)nq, cents_t.p, cst, produced, keys);
+        hipLaunchKernelGGL(ivf_coarse_pick, dim3((unsigned)nq), dim3(256), 0, s, (const uint64_t*)keys, cst, produced,
+                           np, probes, list_off.p, scanned_dev);
       } else if (np <= 1024 && coarse) {
         // exact top-nprobe by (squared_l2, list) through the flat pipeline
         const float* Qd = Qp;

@@ -414,6 +414,33 @@ def test_large_batch_scan(gpu, dim, metric, rerank):
     assert_same(idx.search_batch(q, 10, lambda i, _m: i % 5 != 2, nprobe=7), want)
 
 
+@pytest.mark.parametrize("nlist,nprobe", [(2048, 64), (2048, 32), (100, 64), (40, 33)])
+def test_coarse_selection_ties_and_group_bounds(gpu, nlist, nprobe):
+    """Coarse centroids of entries +-1 all lie at squared distance exactly 16
+    from the zero query, so its probes are the lowest list ids (the (distance,
+    list) order). The selection's candidates (keys up to the nprobe-th
+    smallest of 64 group minima) then number 2017 at nlist 2048, nprobe 64
+    (over the 1024 the sort holds: the radix-select fallback) and 993 at
+    nprobe 32; a query at 0.5 e0 splits the lists into two tied halves; with
+    fewer than 64 lists per 64 groups some groups are empty."""
+    px = gpu
+    dim, m, n = 16, 16, 6000
+    rng = np.random.default_rng(nlist + nprobe)
+    signs = rng.choice(1 << dim, nlist, replace=False)
+    cents = (((signs[:, None] >> np.arange(dim)) & 1) * 2 - 1).astype(np.float32)
+    data = cents[rng.integers(0, nlist, n)] + rng.standard_normal((n, dim)).astype(np.float32) * np.float32(0.2)
+    _, books, _ = orc.ivf_train(data, 16, m, max_iter=3, seed=2)
+    codes, list_of = orc.ivf_encode(data, cents, books, m)
+    idx = build(px, data, px.IvfPqConfig(nlist, m).with_train_threshold(1 << 62))
+    idx.load_trained(cents, books, codes, list_of)
+    q = np.zeros((3, dim), np.float32)
+    q[1, 0] = 0.5
+    q[2] = data[5]
+    want = orc.ivf_search(0, cents, books, codes, list_of, np.arange(n), orc.prepare_rows(0, q), 10, nprobe, m,
+                          threads=8)
+    assert_same(idx.search_batch(q, 10, nprobe=nprobe), want)
+
+
 def test_scan_of_a_list_over_65536_entries(gpu):
     """One list of 70000 entries beside five short ones, all probed by 800
     queries: results match the oracle."""
