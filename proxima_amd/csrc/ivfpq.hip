@@ -383,8 +383,15 @@ __global__ __launch_bounds__(256) void ivf_coarse_pick(const uint64_t* __restric
   }
   __syncthreads();
   const int nc = ncand;
-  if (nc <= IVF_PICK_CAP) {
-    int P = 64;
+  if (nc <= 64) {  // the usual case: one wave sorts them
+    if (w == 0) {
+      uint64_t v[1] = {lane < nc ? cand[lane] : KEY_MAX};
+      wave_bitonic_sort<1>(v, lane);
+      cand[lane] = v[0];
+    }
+    __syncthreads();
+  } else if (nc <= IVF_PICK_CAP) {
+    int P = 128;
     while (P < nc) P <<= 1;
     for (int i = nc + tid; i < P; i += 256) cand[i] = KEY_MAX;
     __syncthreads();
