@@ -445,78 +445,129 @@ __global__ __launch_bounds__(256) void km_mfma_verify(const float* __restrict__ 
   }
 }
 
-// Exact nearest centroid for the listed points: one wave per point, lane l
-// scans centroids l, l+64, ... in order (strict <), and the wave keeps the
-// smallest distance with the lowest index: the reference's sequential scan.
-// The point is staged in LDS; centroid rows are read as float4 (rows
+constexpr int KW_DMAX = 2048;  // largest dim of the MFMA assignment path
+
+// Exact nearest centroid for the listed points, KX_PB points per workgroup
+// staged in LDS: each lane takes centroids c, c+256, ... in order (strict <)
+// and applies the values it loads to all KX_PB points, so the centroids
+// stream once per KX_PB points. Per point the distance is the reference's
+// sequential `squared` (or, UNR, the 8-lane kernel); the lanes' and waves'
+// bests merge lexicographically in (distance, centroid), which keeps the
+// lowest index among equal distances. Centroid rows are read as float4 (rows
 // 16-byte aligned, dim a multiple of 4, dim <= KW_DMAX).
-constexpr int KW_DMAX = 2048;
+constexpr int KX_PB = 8;
 template <bool UNR>
-__global__ __launch_bounds__(256) void km_exact_wave(const float* __restrict__ P, int ldp,
-                                                     const uint32_t* __restrict__ rows, int m, int dim,
-                                                     const float* __restrict__ C, int ldc, int k,
-                                                     uint32_t* __restrict__ assign, float* __restrict__ dist) {
-  __shared__ __align__(16) float sp[4][KW_DMAX];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, p = blockIdx.x * 4 + w;
-  if (p >= m) return;
-  const float* pr = P + (size_t)rows[p] * ldp;
-  for (int j = lane; j < dim; j += 64) sp[w][j] = pr[j];
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-  const float* x = sp[w];
+__global__ __launch_bounds__(256) void km_exact_multi(const float* __restrict__ P, int ldp,
+                                                      const uint32_t* __restrict__ rows, int m, int dim,
+                                                      const float* __restrict__ C, int ldc, int k,
+                                                      uint32_t* __restrict__ assign, float* __restrict__ dist) {
+  extern __shared__ float4 kx_sm[];
+  float* sp = reinterpret_cast<float*>(kx_sm);  // [KX_PB][dim]
+  __shared__ float sbd[4][KX_PB];
+  __shared__ int sbi[4][KX_PB];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int p0 = blockIdx.x * KX_PB, np = min(KX_PB, m - p0);
+  for (int t = tid; t < KX_PB * dim; t += 256) {
+    const int i = t / dim, j = t - i * dim;
+    sp[t] = i < np ? P[(size_t)rows[p0 + i] * ldp + j] : 0.0f;
+  }
+  __syncthreads();
+  float bd[KX_PB];
+  int bi[KX_PB];
+#pragma unroll
+  for (int i = 0; i < KX_PB; ++i) {
+    bd[i] = INFINITY;
+    bi[i] = 0;
+  }
   const int ch8 = (dim >> 3) << 3;
-  float bd = INFINITY;
-  int bi = 0;
-  for (int c = lane; c < k; c += 64) {
+  for (int c = w * 64 + lane; c < k; c += 256) {
     const float* cr = C + (size_t)c * ldc;
-    float sum = 0.0f;
+    float sum[KX_PB];
     if constexpr (UNR) {
-      float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      float acc[KX_PB][8];
+#pragma unroll
+      for (int i = 0; i < KX_PB; ++i)
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc[i][u] = 0.0f;
       for (int j = 0; j < ch8; j += 8) {
         const float4 c0 = *reinterpret_cast<const float4*>(cr + j);
         const float4 c1 = *reinterpret_cast<const float4*>(cr + j + 4);
         const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const float d = x[j + u] - cv[u];
-          acc[u] += d * d;
+        for (int i = 0; i < KX_PB; ++i) {
+          const float4 x0 = *reinterpret_cast<const float4*>(sp + i * dim + j);
+          const float4 x1 = *reinterpret_cast<const float4*>(sp + i * dim + j + 4);
+          const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const float d = xv[u] - cv[u];
+            acc[i][u] += d * d;
+          }
         }
       }
-      for (int j = ch8; j < dim; ++j) {
-        const float d = x[j] - cr[j];
-        sum += d * d;
+#pragma unroll
+      for (int i = 0; i < KX_PB; ++i) {
+        float t = 0.0f;
+        for (int j = ch8; j < dim; ++j) {
+          const float d = sp[i * dim + j] - cr[j];
+          t += d * d;
+        }
+        const float* a = acc[i];
+        sum[i] = (((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))) + t;
       }
-      sum = (((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]))) + sum;
     } else {
+#pragma unroll
+      for (int i = 0; i < KX_PB; ++i) sum[i] = 0.0f;
       for (int j = 0; j < dim; j += 4) {
         const float4 cv = *reinterpret_cast<const float4*>(cr + j);
-        float d = x[j] - cv.x;
-        sum += d * d;
-        d = x[j + 1] - cv.y;
-        sum += d * d;
-        d = x[j + 2] - cv.z;
-        sum += d * d;
-        d = x[j + 3] - cv.w;
-        sum += d * d;
+#pragma unroll
+        for (int i = 0; i < KX_PB; ++i) {
+          const float4 x = *reinterpret_cast<const float4*>(sp + i * dim + j);
+          float d = x.x - cv.x;
+          sum[i] += d * d;
+          d = x.y - cv.y;
+          sum[i] += d * d;
+          d = x.z - cv.z;
+          sum[i] += d * d;
+          d = x.w - cv.w;
+          sum[i] += d * d;
+        }
       }
     }
-    if (sum < bd) {
-      bd = sum;
-      bi = c;
-    }
+#pragma unroll
+    for (int i = 0; i < KX_PB; ++i)
+      if (sum[i] < bd[i]) {
+        bd[i] = sum[i];
+        bi[i] = c;
+      }
   }
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float od = __shfl_xor(bd, o, WAVE);
-    const int oi = __shfl_xor(bi, o, WAVE);
-    if (od < bd || (od == bd && oi < bi)) {
-      bd = od;
-      bi = oi;
+  for (int i = 0; i < KX_PB; ++i) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float od = __shfl_xor(bd[i], o, WAVE);
+      const int oi = __shfl_xor(bi[i], o, WAVE);
+      if (od < bd[i] || (od == bd[i] && oi < bi[i])) {
+        bd[i] = od;
+        bi[i] = oi;
+      }
+    }
+    if (lane == 0) {
+      sbd[w][i] = bd[i];
+      sbi[w][i] = bi[i];
     }
   }
-  if (lane == 0) {
-    assign[p] = (uint32_t)bi;
-    dist[p] = bd;
+  __syncthreads();
+  if (tid < np) {
+    float b = sbd[0][tid];
+    int x = sbi[0][tid];
+    for (int v = 1; v < 4; ++v)
+      if (sbd[v][tid] < b || (sbd[v][tid] == b && sbi[v][tid] < x)) {
+        b = sbd[v][tid];
+        x = sbi[v][tid];
+      }
+    assign[p0 + tid] = (uint32_t)x;
+    dist[p0 + tid] = b;
   }
 }
 
@@ -620,12 +671,14 @@ void nearest_device(const float* P, int ldp, const uint32_t* rows, size_t n, int
   float* const rd = w.rd.p;
   hipLaunchKernelGGL(km_compose_rows, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, s, (const uint32_t*)redo, m,
                      rows, rrows);
+  const dim3 gx((unsigned)((m + KX_PB - 1) / KX_PB));
+  const size_t lx = (size_t)KX_PB * dim * 4;
   if (unrolled)
-    hipLaunchKernelGGL(km_exact_wave<true>, dim3((unsigned)((m + 3) / 4)), dim3(256), 0, s, P, ldp,
-                       (const uint32_t*)rrows, m, dim, C, ldc, (int)k, ra, rd);
+    hipLaunchKernelGGL(km_exact_multi<true>, gx, dim3(256), lx, s, P, ldp, (const uint32_t*)rrows, m, dim, C, ldc,
+                       (int)k, ra, rd);
   else
-    hipLaunchKernelGGL(km_exact_wave<false>, dim3((unsigned)((m + 3) / 4)), dim3(256), 0, s, P, ldp,
-                       (const uint32_t*)rrows, m, dim, C, ldc, (int)k, ra, rd);
+    hipLaunchKernelGGL(km_exact_multi<false>, gx, dim3(256), lx, s, P, ldp, (const uint32_t*)rrows, m, dim, C, ldc,
+                       (int)k, ra, rd);
   hipLaunchKernelGGL(km_scatter_redo, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, s, (const uint32_t*)redo, m,
                      (const uint32_t*)ra, (const float*)rd, assign, dist);
   PXG_HIP(hipGetLastError());
