@@ -108,7 +108,7 @@ __device__ inline float point_dist(const float* x, const float* __restrict__ c, 
 template <int D, bool UNR>
 __global__ __launch_bounds__(256) void km_assign(const float* __restrict__ P, int ldp, const uint32_t* __restrict__ rows,
                                                  int n, int dim, const float* __restrict__ C, int ldc, int k,
-                                                 uint32_t* __restrict__ assign, float* __restrict__ dist) {
+                                                 uint32_t* __restrict__ assign, float* __restrict__ dist, int vec4) {
   __shared__ float cs[KM_LDS_FLOATS];
   const int i = blockIdx.x * 256 + threadIdx.x;
   const bool valid = i < n;
@@ -117,8 +117,24 @@ __global__ __launch_bounds__(256) void km_assign(const float* __restrict__ P, in
   constexpr int DR = D > 0 ? D : 1;
   float x[DR];
   if constexpr (D > 0) {
+    bool loaded = false;
+    if constexpr (D % 4 == 0) {
+      if (vec4) {  // rows 16-byte aligned: a quarter of the load instructions
 #pragma unroll
-    for (int j = 0; j < D; ++j) x[j] = valid ? pr[j] : 0.0f;
+        for (int j = 0; j < D; j += 4) {
+          const float4 v = *reinterpret_cast<const float4*>(pr + j);
+          x[j] = valid ? v.x : 0.0f;
+          x[j + 1] = valid ? v.y : 0.0f;
+          x[j + 2] = valid ? v.z : 0.0f;
+          x[j + 3] = valid ? v.w : 0.0f;
+        }
+        loaded = true;
+      }
+    }
+    if (!loaded) {
+#pragma unroll
+      for (int j = 0; j < D; ++j) x[j] = valid ? pr[j] : 0.0f;
+    }
   }
   float bd = INFINITY;
   int bi = 0;
@@ -156,8 +172,10 @@ template <bool UNR>
 static void launch_assign(const float* P, int ldp, const uint32_t* rows, size_t n, int dim, const float* C, int ldc,
                           size_t k, uint32_t* assign, float* dist, hipStream_t s) {
   const dim3 g((unsigned)((n + 255) / 256)), b(256);
-#define PXG_ASSIGN(DD) \
-  hipLaunchKernelGGL((km_assign<DD, UNR>), g, b, 0, s, P, ldp, rows, (int)n, dim, C, ldc, (int)k, assign, dist)
+  const int vec4 = (ldp % 4 == 0 && ((uintptr_t)P & 15) == 0) ? 1 : 0;
+#define PXG_ASSIGN(DD)                                                                                             \
+  hipLaunchKernelGGL((km_assign<DD, UNR>), g, b, 0, s, P, ldp, rows, (int)n, dim, C, ldc, (int)k, assign, dist, \
+                     vec4)
   switch (dim) {
     case 1: PXG_ASSIGN(1); break;
     case 2: PXG_ASSIGN(2); break;
