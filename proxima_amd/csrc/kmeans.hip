@@ -1172,7 +1172,7 @@ __global__ __launch_bounds__(NT) void km_sums(const float* __restrict__ P, int l
                                                const uint32_t* __restrict__ members,
                                                const uint32_t* __restrict__ offsets,
                                                const uint32_t* __restrict__ counts, int k, float* __restrict__ newc) {
-  constexpr int G = NT / JW, ROWS = 8192 / JW;  // 32 KiB of staged values
+  constexpr int G = NT / JW, ROWS = 2048 / JW;  // 8 KiB of staged values (the sequential redo)
   __shared__ double ss[G][JW], sa[G][JW];
   __shared__ int se[G][JW];
   __shared__ float stage[ROWS][JW];
@@ -1185,13 +1185,27 @@ __global__ __launch_bounds__(NT) void km_sums(const float* __restrict__ P, int l
   const uint32_t off = offsets[c];
   double s = 0.0, a = 0.0;
   int e = NO_TERMS;
-  if (j < dim)
-    for (uint32_t m = g; m < cnt; m += G) {
-      const float x = P[(size_t)members[off + m] * ldp + j];
-      s += (double)x;
-      a += (double)fabsf(x);
-      if (x != 0.0f) e = min(e, ulp_exp(x));
+  // Under the certificate every order gives the same bits, so four members
+  // are loaded at a time (four index loads, then four row loads in flight).
+  auto add = [&](float x) {
+    s += (double)x;
+    a += (double)fabsf(x);
+    if (x != 0.0f) e = min(e, ulp_exp(x));
+  };
+  if (j < dim) {
+    uint32_t m = g;
+    for (; m + 3 * G < cnt; m += 4 * G) {
+      const uint32_t r0 = members[off + m], r1 = members[off + m + G], r2 = members[off + m + 2 * G],
+                     r3 = members[off + m + 3 * G];
+      const float x0 = P[(size_t)r0 * ldp + j], x1 = P[(size_t)r1 * ldp + j], x2 = P[(size_t)r2 * ldp + j],
+                  x3 = P[(size_t)r3 * ldp + j];
+      add(x0);
+      add(x1);
+      add(x2);
+      add(x3);
     }
+    for (; m < cnt; m += G) add(P[(size_t)members[off + m] * ldp + j]);
+  }
   ss[g][jl] = s;
   sa[g][jl] = a;
   se[g][jl] = e;
