@@ -389,6 +389,7 @@ __global__ __launch_bounds__(256, 2) void km_mfma_top(const float* __restrict__ 
   }
 }
 
+constexpr int KV_PB = 128;  // points per km_mfma_verify block (256 threads)
 template <bool UNR>
 __global__ __launch_bounds__(256) void km_mfma_verify(const float* __restrict__ P, int ldp,
                                                       const uint32_t* __restrict__ rows, int n, int dim,
@@ -398,29 +399,32 @@ __global__ __launch_bounds__(256) void km_mfma_verify(const float* __restrict__ 
                                                       const float* __restrict__ best, const float* __restrict__ second,
                                                       uint32_t* __restrict__ assign, float* __restrict__ dist,
                                                       uint32_t* __restrict__ redo, int* __restrict__ nredo) {
-  // the block's 256 points and their winning centroids, staged through LDS
-  // 32 coordinates at a time (eight lanes per 128-byte row slice)
-  __shared__ float tp[256 * 33], tc[256 * 33];
-  __shared__ uint32_t sr[256], sc[256];
-  const int t = threadIdx.x, i0 = blockIdx.x * 256, i = i0 + t;
+  // the block's KV_PB points and their winning centroids, staged through LDS
+  // 32 coordinates at a time (eight lanes per 128-byte row slice); 34 KB of
+  // LDS, so four blocks per CU keep the row loads in flight
+  __shared__ float tp[KV_PB * 33], tc[KV_PB * 33];
+  __shared__ uint32_t sr[KV_PB], sc[KV_PB];
+  const int t = threadIdx.x, i0 = blockIdx.x * KV_PB, i = i0 + t;
   bool ok = false;
-  if (i < n) {
-    const float s = (sqrtf(pn[i]) + sqrtf(cmax[0])) * 1.0001f;
-    const float eps = 2.0f * (2.0f * (float)dim + 6.0f) * 5.9604645e-08f * s * s;
-    ok = second[i] > best[i] + 2.0f * eps;
-    if (!ok) redo[atomicAdd(nredo, 1)] = (uint32_t)i;
-    sr[t] = rows ? rows[i] : (uint32_t)i;
-    sc[t] = best_idx[i];
-  } else {
-    sr[t] = 0;
-    sc[t] = 0;
+  if (t < KV_PB) {  // threads KV_PB.. only help with the loads
+    if (i < n) {
+      const float s = (sqrtf(pn[i]) + sqrtf(cmax[0])) * 1.0001f;
+      const float eps = 2.0f * (2.0f * (float)dim + 6.0f) * 5.9604645e-08f * s * s;
+      ok = second[i] > best[i] + 2.0f * eps;
+      if (!ok) redo[atomicAdd(nredo, 1)] = (uint32_t)i;
+      sr[t] = rows ? rows[i] : (uint32_t)i;
+      sc[t] = best_idx[i];
+    } else {
+      sr[t] = 0;
+      sc[t] = 0;
+    }
   }
   float sum = 0.0f, acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   const int ch8 = (dim >> 3) << 3;
   for (int j0 = 0; j0 < dim; j0 += 32) {
     const int w = min(32, dim - j0);
     __syncthreads();
-    for (int f = t; f < 256 * 8; f += 256) {
+    for (int f = t; f < KV_PB * 8; f += 256) {
       const int r = f >> 3, c4 = (f & 7) * 4;
       if (c4 < w && i0 + r < n) {
         const float4 x = *reinterpret_cast<const float4*>(P + (size_t)sr[r] * ldp + j0 + c4);
@@ -658,7 +662,7 @@ void nearest_device(const float* P, int ldp, const uint32_t* rows, size_t n, int
                      dim, C, ldc, (int)k, (const float*)pn, (const float*)cn, bidx, best, second);
   PXG_HIP(hipEventRecord(e1, s));
   PXG_HIP(hipMemsetAsync(nredo, 0, 4, s));
-  const dim3 g((unsigned)((n + 255) / 256));
+  const dim3 g((unsigned)((n + KV_PB - 1) / KV_PB));
   if (unrolled)
     hipLaunchKernelGGL(km_mfma_verify<true>, g, dim3(256), 0, s, P, ldp, rows, (int)n, dim, C, ldc, (const float*)pn,
                        (const float*)cmax, (const uint32_t*)bidx, (const float*)best, (const float*)second, assign,
