@@ -32,10 +32,30 @@
 #include <vector>
 #include <thread>
 #include <unordered_map>
+#include <limits>
 
 namespace {
 
 constexpr size_t LANES = 8;  // distance.rs:72
+
+// NaN results. Rust, like IEEE 754, leaves the sign of a NaN produced by
+// arithmetic to the hardware. On the reference's benchmark platform, aarch64
+// (BENCHMARKS.md:13-21; FPCR.DN clear), an invalid operation such as
+// inf + (-inf) or inf * 0 yields the default NaN 0x7FC00000 (sign clear), and
+// an operation with one NaN operand returns that NaN. Inputs are finite
+// (space.rs:104-128), so every NaN inside a sum is that default NaN and only a
+// later negation (inner_product, the IP ADC, the SQ inner product) flips its
+// sign, which decides where total_cmp ranks it (topk.rs:63-67). x86 yields
+// 0xFFC00000 instead, so the oracle maps a NaN result to 0x7FC00000 before any
+// negation.
+inline float arm_nan(float x) { return std::isnan(x) ? std::numeric_limits<float>::quiet_NaN() : x; }
+// a + b where both may be NaN: aarch64 FADD returns its first NaN operand,
+// else the default NaN for inf + (-inf).
+inline float arm_add(float a, float b) {
+  if (std::isnan(a)) return a;
+  if (std::isnan(b)) return b;
+  return arm_nan(a + b);
+}
 
 // reduce(): distance.rs:534-538. Pairwise over the eight lane accumulators.
 inline float reduce8(const float acc[LANES]) {
@@ -80,14 +100,14 @@ float dot_unrolled(const float* a, const float* b, size_t n) {
     for (size_t j = 0; j < LANES; ++j) acc[j] += a[c * LANES + j] * b[c * LANES + j];
   float tail = 0.0f;
   for (size_t i = chunks * LANES; i < n; ++i) tail += a[i] * b[i];
-  return reduce8(acc) + tail;
+  return arm_nan(reduce8(acc) + tail);
 }
 
 // dot_scalar: distance.rs:307-313.
 float dot_scalar(const float* a, const float* b, size_t n) {
   float sum = 0.0f;
   for (size_t i = 0; i < n; ++i) sum += a[i] * b[i];
-  return sum;
+  return arm_nan(sum);
 }
 
 // manhattan_unrolled: distance.rs:358-372; scalar 345-351.
@@ -126,7 +146,7 @@ float cosine_unrolled(const float* a, const float* b, size_t n) {
   float dot = reduce8(ad) + d, norm_a = reduce8(aa) + na, norm_b = reduce8(ab) + nb;
   float denom = std::sqrt(norm_a * norm_b);
   if (denom <= 0.0f) return 1.0f;
-  return 1.0f - dot / denom;
+  return arm_nan(1.0f - dot / denom);
 }
 
 // cosine_scalar: distance.rs:406-421.
@@ -139,7 +159,7 @@ float cosine_scalar(const float* a, const float* b, size_t n) {
   }
   float denom = std::sqrt(na * nb);
   if (denom <= 0.0f) return 1.0f;
-  return 1.0f - dot / denom;
+  return arm_nan(1.0f - dot / denom);
 }
 
 enum Metric { EUCLIDEAN = 0, COSINE = 1, INNER_PRODUCT = 2, MANHATTAN = 3 };  // distance.rs:90-118
@@ -148,7 +168,7 @@ enum Metric { EUCLIDEAN = 0, COSINE = 1, INNER_PRODUCT = 2, MANHATTAN = 3 };  //
 float space_distance(int metric, const float* a, const float* b, size_t n) {
   switch (metric) {
     case EUCLIDEAN: return sq_l2_unrolled(a, b, n);
-    case COSINE: return 1.0f - dot_unrolled(a, b, n);         // cosine_normalized distance.rs:400-402
+    case COSINE: return arm_nan(1.0f - dot_unrolled(a, b, n));  // cosine_normalized distance.rs:400-402
     case INNER_PRODUCT: return -dot_unrolled(a, b, n);        // inner_product distance.rs:291-293
     default: return l1_unrolled(a, b, n);
   }
@@ -525,7 +545,7 @@ void pq_table(const PqLayout& L, const float* books, size_t m, const float* q, f
         ip += qq * cc;
       }
       squared[s * 256 + c] = l2;
-      dotv[s * 256 + c] = ip;
+      dotv[s * 256 + c] = arm_nan(ip);
     }
   }
 }
@@ -539,7 +559,7 @@ inline float adc_l2(const float* squared, size_t m, const uint8_t* code) {
 inline float adc_ip(const float* dotv, size_t m, const uint8_t* code) {
   float sum = 0.0f;
   for (size_t s = 0; s < m; ++s) sum += dotv[s * 256 + code[s]];
-  return -sum;
+  return -arm_nan(sum);
 }
 
 // ProductQuantizer::train: product.rs:198-296 (one RNG advanced across
@@ -753,7 +773,7 @@ float orc_sq_asym(int ip, const float* q, const uint8_t* code, size_t dim, int p
       sum += d * d;
     }
   }
-  return ip ? -sum : sum;
+  return ip ? -arm_nan(sum) : sum;
 }
 
 // SQ8 inner-product search over I8 codes (CodeType::I8 bytes). The reference
@@ -798,7 +818,7 @@ void orc_sq8_search(const int8_t* codes, const uint8_t* live, const uint64_t* id
           const float rec = mn[g] + (float)level * scale[g];
           sum += qf[q * dim + c] * rec;
         }
-        fin.push(h.id, -sum);
+        fin.push(h.id, -arm_nan(sum));
       }
       out_count[q] = (uint32_t)emit(fin, out_ids + q * k, out_d + q * k);
     }
@@ -1064,7 +1084,8 @@ void orc_ivf_search(int metric, const float* cents, size_t produced, const float
         for (uint32_t s : lists[l]) {
           if (!accepted(accept, s)) continue;
           const uint8_t* code = codes + (size_t)s * m;
-          float score = metric == COSINE ? (1.0f - qdc) + adc_ip(dt.data(), m, code) : adc_l2(sq.data(), m, code);
+          float score = metric == COSINE ? arm_add(arm_nan(1.0f - qdc), adc_ip(dt.data(), m, code))
+                                         : adc_l2(sq.data(), m, code);
           top.push(ids[s], score);
         }
       }

@@ -12,7 +12,9 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+# PXG_ORACLE_LIB names another build of oracle.cpp (the mutation tests load
+# deliberately broken copies through it to show that the pins catch them)
+_LIB_PATH = os.environ.get("PXG_ORACLE_LIB") or os.path.join(_HERE, "liboracle.so")
 
 EUCLIDEAN, COSINE, INNER_PRODUCT, MANHATTAN = 0, 1, 2, 3
 

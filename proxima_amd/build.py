@@ -4,6 +4,7 @@ import glob
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
@@ -15,7 +16,6 @@ FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     # exact kernels restate the reference's arithmetic: no FMA contraction
     "-ffp-contract=off",
     # packed FP32 ops are kept out of every kernel
@@ -29,20 +29,36 @@ def sources():
     return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
 
 
-def build(verbose=False):
-    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-    tmp = LIB + ".tmp"
-    cmd = [hipcc, *FLAGS, *sources(), "-o", tmp]
+NOISE = ("unknown target feature", "packed-fp32-ops", "warning: argument unused")
+
+
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
-    noise = ("unknown target feature", "packed-fp32-ops", "warning: argument unused")
-    msgs = [ln for ln in (res.stdout + res.stderr).splitlines() if not any(n in ln for n in noise)]
+    msgs = [ln for ln in (res.stdout + res.stderr).splitlines() if not any(n in ln for n in NOISE)]
     if res.returncode != 0:
         sys.stderr.write("\n".join(msgs) + "\n")
-        raise RuntimeError(f"hipcc failed ({res.returncode})")
+        raise RuntimeError(f"hipcc failed ({res.returncode}): {' '.join(cmd)}")
     if verbose and msgs:
         print("\n".join(msgs))
+
+
+def build(verbose=False, jobs=None):
+    """Compile each source to an object in parallel (every source is
+    self-contained: kernels and their device helpers live in one translation
+    unit), then link the shared library."""
+    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    srcs = sources()
+    objs = [os.path.join(objdir, os.path.basename(s)[:-4] + ".o") for s in srcs]
+    jobs = jobs or min(len(srcs), os.cpu_count() or 4, 8)
+    with ThreadPoolExecutor(jobs) as pool:
+        for f in [pool.submit(_run, [hipcc, *FLAGS, "-c", s, "-o", o], verbose) for s, o in zip(srcs, objs)]:
+            f.result()
+    tmp = LIB + ".tmp"
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp], verbose)
     os.replace(tmp, LIB)
     return LIB
 

@@ -85,6 +85,25 @@ __device__ inline uint64_t shfl_xor64(uint64_t v, int mask) {
   return ((uint64_t)hi << 32) | lo;
 }
 
+// NaN results, as on the reference's aarch64 platform: an invalid operation
+// (inf + -inf) yields the default NaN 0x7FC00000 with its sign clear, and a
+// NaN operand propagates. Inputs are finite, so every NaN inside a dot-type
+// sum is that default NaN, and only a later negation (inner product, the IP
+// ADC) flips its sign, which decides where total_cmp ranks it. The sums are
+// mapped to 0x7FC00000 before any negation so that no result depends on the
+// sign this GPU gives a generated NaN.
+__host__ __device__ inline float arm_nan(float x) { return x != x ? __builtin_bit_cast(float, 0x7FC00000u) : x; }
+
+// The IVF cosine score (1 - q.c) + inner_product(code) (ivfpq.rs:1068-1074)
+// under the same rule: omq = arm_nan(1 - q.c) is +NaN when NaN, a NaN ADC sum
+// negates to -NaN, the addition returns its first NaN operand, and
+// inf + (-inf) gives +NaN.
+__device__ inline float ivf_cos_score(float omq, float sum) {
+  const float s = omq + (-sum);
+  if (s == s) return s;
+  return (omq != omq || sum == sum) ? __builtin_bit_cast(float, 0x7FC00000u) : __builtin_bit_cast(float, 0xFFC00000u);
+}
+
 // ----------------------------------------------------------------------------
 // Exact distances in the reference's arithmetic.
 //
@@ -121,8 +140,8 @@ __device__ inline float dist_group8(const float* __restrict__ a, const float* __
   float tail = 0.0f;
   for (int i = chunks * 8; i < dim; ++i) tail += lane_term<METRIC>(a[i], b[i]);
   float r = acc + tail;
-  if constexpr (METRIC == 1) return 1.0f - r;   // cosine_normalized, distance.rs:400-402
-  if constexpr (METRIC == 2) return -r;         // inner_product, distance.rs:291-293
+  if constexpr (METRIC == 1) return arm_nan(1.0f - arm_nan(r));  // cosine_normalized, distance.rs:400-402
+  if constexpr (METRIC == 2) return -arm_nan(r);                 // inner_product, distance.rs:291-293
   return r;
 }
 
@@ -139,8 +158,8 @@ __device__ inline float dist_thread(const float* __restrict__ a, const float* __
   for (int i = chunks * 8; i < dim; ++i) tail += lane_term<METRIC>(a[i], b[i]);
   float r = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
   r = r + tail;
-  if constexpr (METRIC == 1) return 1.0f - r;
-  if constexpr (METRIC == 2) return -r;
+  if constexpr (METRIC == 1) return arm_nan(1.0f - arm_nan(r));
+  if constexpr (METRIC == 2) return -arm_nan(r);
   return r;
 }
 

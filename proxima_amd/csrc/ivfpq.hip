@@ -158,7 +158,7 @@ __global__ __launch_bounds__(256) void ivf_scan(const float* __restrict__ Qp, in
     lut[e] = acc;
   }
   __syncthreads();
-  const float one_minus_qdc = METRIC == 1 ? 1.0f - s_qdc : 0.0f;
+  const float one_minus_qdc = METRIC == 1 ? arm_nan(1.0f - s_qdc) : 0.0f;
 
   uint64_t* wb = wbuf[w];
   uint64_t thr = KEY_MAX;
@@ -180,7 +180,7 @@ __global__ __launch_bounds__(256) void ivf_scan(const float* __restrict__ Qp, in
         } else {
           for (int s = 0; s < M; ++s) sum += lut[s * 256 + code[s]];
         }
-        const float score = METRIC == 0 ? sum : one_minus_qdc + (-sum);
+        const float score = METRIC == 0 ? sum : ivf_cos_score(one_minus_qdc, sum);
         key = ((uint64_t)ord_key(score) << 32) | rk;
       }
     }
@@ -537,7 +537,7 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan_reg(const float* __restr
     const int l = probes[(size_t)q * nprobe + p0 + pi];
     if (METRIC == 0 && pi + 1 < np) build(srs[pi + 1], lut + ((pi + 1) & 1) * tsz);
     const float* tab = lut + (METRIC == 0 ? (pi & 1) * tsz : 0);
-    const float one_minus_qdc = METRIC == 1 ? 1.0f - s_qdc[pi] : 0.0f;
+    const float one_minus_qdc = METRIC == 1 ? arm_nan(1.0f - s_qdc[pi]) : 0.0f;
     const uint32_t begin = list_off[l], end = list_off[l + 1];
     for (uint32_t e0 = begin + w * 64; e0 < end; e0 += IVF_SW * 64) {
       const uint32_t e = e0 + lane;
@@ -555,7 +555,7 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan_reg(const float* __restr
             const uint8_t* code = list_codes + (size_t)e * M;
             for (int s2 = 0; s2 < M; ++s2) sum += tab[s2 * 256 + code[s2]];
           }
-          const float score = METRIC == 0 ? sum : one_minus_qdc + (-sum);
+          const float score = METRIC == 0 ? sum : ivf_cos_score(one_minus_qdc, sum);
           key = ((uint64_t)ord_key(score) << 32) | rk;
         }
       }
@@ -853,7 +853,7 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan16(const float* __restric
         // the sign bit set
         key = ((uint64_t)(__float_as_uint(sum) | 0x80000000u) << 32) | rk;
       } else {
-        key = ((uint64_t)ord_key(one_minus_qdc + (-sum)) << 32) | rk;
+        key = ((uint64_t)ord_key(ivf_cos_score(one_minus_qdc, sum)) << 32) | rk;
       }
     }
     wave_topk_add(key, kept, thr, kk, lane);
@@ -864,7 +864,7 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan16(const float* __restric
   auto probe_step = [&](auto bc, int pi) {
     constexpr int B = decltype(bc)::value;
     const float* tab = tabs[METRIC == 0 ? B : 0];
-    const float one_minus_qdc = METRIC == 1 ? 1.0f - s_qdc[pi] : 0.0f;
+    const float one_minus_qdc = METRIC == 1 ? arm_nan(1.0f - s_qdc[pi]) : 0.0f;
     if (METRIC == 0 && pi + 1 < np) {
       float* nt = tabs[METRIC == 0 ? (B ^ 1) : 0];
       float rv[W];

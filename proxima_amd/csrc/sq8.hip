@@ -192,7 +192,7 @@ __global__ void sq_asym_rows(int ip, const float* __restrict__ q, const uint8_t*
       sum += d * d;
     }
   }
-  out[i] = ip ? -sum : sum;
+  out[i] = ip ? -arm_nan(sum) : sum;
 }
 
 // Copy caller codes (stride dim) into index rows (stride KP, zero padded).
@@ -566,7 +566,7 @@ __global__ __launch_bounds__(256) void sq8_rescore(const uint64_t* __restrict__ 
         const int g = per_dim ? j : 0;
         sum += qv[j] * sq_reconstruct(code[j], 1, mn[g], scale[g]);
       }
-      key = ((uint64_t)ord_key(-sum) << 32) | rk;
+      key = ((uint64_t)ord_key(-arm_nan(sum)) << 32) | rk;
     }
     sk[i] = key;
   }
