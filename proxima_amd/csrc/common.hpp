@@ -166,6 +166,59 @@ struct Ctx {
   }
 };
 
+// Device scratch of one search, by purpose, plus host words for the flag
+// readback at its end. A Ctx allocates on demand; an Arena hands out regions
+// of a fixed block and never allocates.
+struct Scratch {
+  virtual ~Scratch() = default;
+  virtual unsigned char* get(int key, size_t bytes) = 0;
+  // bytes an arena can still hand out (an allocating scratch has no limit)
+  virtual size_t room() const { return SIZE_MAX; }
+  // an arena takes back the region of `key` and everything carved after it
+  virtual void release_from(int key) { (void)key; }
+  virtual unsigned long long* host_words() = 0;  // at least 8 words
+  virtual bool timing() const { return true; }   // stage timers may create events
+};
+
+struct CtxScratch : Scratch {
+  Ctx* c;
+  explicit CtxScratch(Ctx* ctx) : c(ctx) {}
+  unsigned char* get(int key, size_t bytes) override { return c->get(key, bytes); }
+  unsigned long long* host_words() override { return c->tail_host(); }
+};
+
+struct Arena : Scratch {
+  static constexpr int KEYS = 64;
+  unsigned char* base;
+  size_t cap, off = 0;
+  size_t start[KEYS];
+  unsigned long long words[8] = {};
+  Arena(void* p, size_t bytes) : base((unsigned char*)p), cap(bytes) {
+    for (size_t& x : start) x = SIZE_MAX;
+  }
+  unsigned char* get(int key, size_t bytes) override {
+    const size_t at = (off + 255) & ~(size_t)255;
+    if (key < 0 || key >= KEYS || at > cap || bytes > cap - at)
+      raise(PXG_ERR_CAPACITY,
+            "this search needs more than the " + std::to_string(cap >> 20) +
+                " MiB of the no-allocation scratch (region " + std::to_string(key) + " of " + std::to_string(bytes) +
+                " bytes at offset " + std::to_string(at) + ")",
+            at + bytes);
+    start[key] = at;
+    off = at + bytes;
+    return base + at;
+  }
+  size_t room() const override {
+    const size_t at = (off + 255) & ~(size_t)255;
+    return at >= cap ? 0 : cap - at;
+  }
+  void release_from(int key) override {
+    if (key >= 0 && key < KEYS && start[key] != SIZE_MAX) off = start[key];
+  }
+  unsigned long long* host_words() override { return words; }
+  bool timing() const override { return false; }
+};
+
 struct CtxPool {
   std::mutex mu;
   std::vector<Ctx*> idle;

@@ -11,6 +11,22 @@ namespace pxg {
 
 constexpr int EXACT_CH = 1024;
 
+// Small fills done by kernels rather than memsets (so that a caller's stream
+// holds only kernel work): the query flag word ~0, the flagged-query count 0.
+static __global__ void init_search_flags(unsigned long long* bad, int* flag_count) {
+  if (threadIdx.x == 0) {
+    *bad = ~0ull;
+    *flag_count = 0;
+  }
+}
+static __global__ void fill_u32(uint32_t* p, size_t n, uint32_t v) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+static __global__ void set_int(int* p, int v) {
+  if (threadIdx.x == 0) *p = v;
+}
+
 // ---------------------------------------------------------------------------
 // 1. query preparation
 // ---------------------------------------------------------------------------
@@ -119,7 +135,7 @@ static __global__ __launch_bounds__(256) void flat_merge_exact(const int* __rest
                                                         const uint64_t* __restrict__ ids,
                                                         uint64_t* __restrict__ out_ids, float* __restrict__ out_d,
                                                         uint32_t* __restrict__ out_count,
-                                                        uint64_t* __restrict__ out_keys) {
+                                                        uint64_t* __restrict__ out_keys, size_t ldo) {
   const int f = blockIdx.x;
   if (f >= *qcount) return;
   const int q = qlist[f];
@@ -159,10 +175,10 @@ static __global__ __launch_bounds__(256) void flat_merge_exact(const int* __rest
   for (int i = threadIdx.x; i < ksel; i += blockDim.x) {
     const uint64_t key = sel[i];
     if (out_keys) {
-      out_keys[(size_t)q * k + i] = key;  // (distance, id rank) keys for a later stage
+      out_keys[(size_t)q * ldo + i] = key;  // (distance, id rank) keys for a later stage
     } else {
-      out_ids[(size_t)q * k + i] = ids[rank_slot[(uint32_t)key]];
-      out_d[(size_t)q * k + i] = key_float((uint32_t)(key >> 32));
+      out_ids[(size_t)q * ldo + i] = ids[rank_slot[(uint32_t)key]];
+      out_d[(size_t)q * ldo + i] = key_float((uint32_t)(key >> 32));
     }
   }
   if (threadIdx.x == 0) out_count[q] = ksel;
@@ -174,7 +190,8 @@ static __global__ void iota_kernel(int* a, int n, int* count) {
   if (i == 0) *count = n;
 }
 
-// Scatter staged rows into their slots (insert path).
+// Scatter staged rows into their slots (insert path); X and xb may be null
+// (an index that keeps no full-precision rows).
 static __global__ void flat_scatter_rows(const float* __restrict__ staged, const uint32_t* __restrict__ slots,
                                   const float* __restrict__ bias, const uint64_t* __restrict__ sid, int n, int ld,
                                   float* __restrict__ X, float* __restrict__ xb, uint8_t* __restrict__ live,
@@ -182,9 +199,10 @@ static __global__ void flat_scatter_rows(const float* __restrict__ staged, const
   const int i = blockIdx.x;
   if (i >= n) return;
   const uint32_t s = slots[i];
-  for (int c = threadIdx.x; c < ld; c += blockDim.x) X[(size_t)s * ld + c] = staged[(size_t)i * ld + c];
+  if (X != nullptr)
+    for (int c = threadIdx.x; c < ld; c += blockDim.x) X[(size_t)s * ld + c] = staged[(size_t)i * ld + c];
   if (threadIdx.x == 0) {
-    xb[s] = bias[i];
+    if (xb != nullptr) xb[s] = bias[i];
     live[s] = 1;
     ids[s] = sid[i];
   }

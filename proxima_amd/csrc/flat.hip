@@ -41,6 +41,7 @@
 #include "device.hpp"
 #include "exact_scan.hpp"
 #include "flat.hpp"
+#include "wide.hpp"
 
 namespace pxg {
 
@@ -343,7 +344,7 @@ __global__ __launch_bounds__(256) void flat_merge_rescore(
     int metric, const float* __restrict__ X, const uint32_t* __restrict__ rank, const uint32_t* __restrict__ rank_slot,
     const uint64_t* __restrict__ ids, const float* __restrict__ qn, float maxnorm, float eps_c,
     uint64_t* __restrict__ out_ids, float* __restrict__ out_d, uint32_t* __restrict__ out_count,
-    int* __restrict__ flag_list, int* __restrict__ flag_count) {
+    int* __restrict__ flag_list, int* __restrict__ flag_count, size_t ldo) {
   const int q = blockIdx.x;
   __shared__ int hist[256];
   __shared__ uint64_t sh[4];
@@ -396,8 +397,8 @@ __global__ __launch_bounds__(256) void flat_merge_rescore(
   for (int i = threadIdx.x; i < kout; i += blockDim.x) {
     const uint64_t key = sel[i];
     const uint32_t slot = rank_slot[(uint32_t)key];
-    out_ids[(size_t)q * k + i] = ids[slot];
-    out_d[(size_t)q * k + i] = key_float((uint32_t)(key >> 32));
+    out_ids[(size_t)q * ldo + i] = ids[slot];
+    out_d[(size_t)q * ldo + i] = key_float((uint32_t)(key >> 32));
   }
   if (threadIdx.x == 0) {
     out_count[q] = kout;
@@ -424,6 +425,27 @@ __global__ __launch_bounds__(256) void flat_merge_rescore(
   }
 }
 
+// Exact (distance, id rank) keys of every slot for queries q0 .. q0 + G - 1
+// (grid (ceil(N / 32), G), 8 threads per slot), KEY_MAX for free or
+// filtered slots; segment g starts at g * seg.
+__global__ __launch_bounds__(256) void flat_wide_keys(const float* __restrict__ Qp, int ld, int dim, int metric,
+                                                      const float* __restrict__ X, int N,
+                                                      const uint8_t* __restrict__ live,
+                                                      const uint8_t* __restrict__ accept,
+                                                      const uint32_t* __restrict__ rank, int q0, size_t seg,
+                                                      uint64_t* __restrict__ keys) {
+  const int g = threadIdx.x & 7;
+  const int slot = blockIdx.x * 32 + (threadIdx.x >> 3);
+  const float* qv = Qp + (size_t)(q0 + blockIdx.y) * ld;
+  if (slot >= N) return;
+  uint64_t key = KEY_MAX;
+  if (live[slot] && (accept == nullptr || accept[slot])) {
+    const float d = dist_group8_rt(metric, qv, X + (size_t)slot * ld, dim, g);
+    key = ((uint64_t)ord_key(d) << 32) | rank[slot];
+  }
+  if (g == 0) keys[(size_t)blockIdx.y * seg + slot] = key;
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -441,31 +463,11 @@ void FlatIndex::ensure_capacity(size_t need, size_t keep) {
   xb.grow(nc, hw, stream);
   d_live.grow(nc, hw, stream);
   d_ids.grow(nc, hw, stream);
-  d_rank.grow(nc, hw, stream);
+  ranks.grow(nc, hw, stream);
   // zero the new tail of the liveness map
   PXG_HIP(hipMemsetAsync(d_live.p + hw, 0, nc - hw, stream));
   PXG_HIP(hipStreamSynchronize(stream));
   cap = nc;
-}
-
-void FlatIndex::rebuild_ranks(hipStream_t s) {
-  std::lock_guard<std::mutex> lk(rank_mu);
-  if (!rank_dirty) return;
-  std::vector<std::pair<uint64_t, uint32_t>> v;
-  v.reserve(by_id.size());
-  for (size_t s2 = 0; s2 < ids.size(); ++s2)
-    if (live[s2]) v.emplace_back(ids[s2], (uint32_t)s2);
-  std::sort(v.begin(), v.end());
-  std::vector<uint32_t> rs(v.size()), rk(std::max<size_t>(ids.size(), 1), 0);
-  for (size_t r = 0; r < v.size(); ++r) {
-    rs[r] = v[r].second;
-    rk[v[r].second] = (uint32_t)r;
-  }
-  d_rank_slot.reserve(std::max<size_t>(rs.size(), 1));
-  if (!rs.empty()) PXG_HIP(hipMemcpyAsync(d_rank_slot.p, rs.data(), rs.size() * 4, hipMemcpyHostToDevice, s));
-  if (!ids.empty()) PXG_HIP(hipMemcpyAsync(d_rank.p, rk.data(), ids.size() * 4, hipMemcpyHostToDevice, s));
-  PXG_HIP(hipStreamSynchronize(s));
-  rank_dirty = false;
 }
 
 void FlatIndex::insert(const uint64_t* in_ids, const float* vecs, uint64_t n, uint32_t* out_slots) {
@@ -528,7 +530,7 @@ void FlatIndex::insert(const uint64_t* in_ids, const float* vecs, uint64_t n, ui
     PXG_HIP(hipGetLastError());
     PXG_HIP(hipStreamSynchronize(stream));
   }
-  rank_dirty = true;
+  ranks.insert(in_ids, sl.data(), n, d_ids.p, stream);
 }
 
 void FlatIndex::remove(uint64_t id) {
@@ -539,58 +541,87 @@ void FlatIndex::remove(uint64_t id) {
   live[s] = 0;
   slots.release(s);
   PXG_HIP(hipMemsetAsync(d_live.p + s, 0, 1, stream));
+  ranks.remove(s, stream);
   PXG_HIP(hipStreamSynchronize(stream));
-  rank_dirty = true;
 }
 
 // Run the search pipeline on prepared-or-raw device queries.
 void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, uint64_t k, const uint8_t* d_accept,
-                   uint64_t* d_oid, float* d_od, uint32_t* d_oc, Ctx* ctx, hipStream_t s, uint64_t* fallbacks) {
+                              uint64_t* d_oid, float* d_od, uint32_t* d_oc, Scratch& sc, hipStream_t s,
+                              uint64_t* fallbacks, size_t ldo) {
   check_k(k);
   *fallbacks = 0;
-  const size_t N = slots.high_water();
   if (nq == 0) return;
-  if (k == 0 || by_id.empty()) {
-    PXG_HIP(hipMemsetAsync(d_oc, 0, nq * 4, s));
-    PXG_HIP(hipStreamSynchronize(s));
-    return;
-  }
-  if (k > EXACT_MERGE_MAXK)
-    config_error("k", k, "the GPU flat search supports k up to 1024 per query");
-  rebuild_ranks(s);
+  const size_t N = slots.high_water();
+  // A search returns at most the live count per query, so k is clamped to it
+  // before any path is chosen.
+  const uint64_t kq = std::min<uint64_t>(k, by_id.size());
 
   Timer tm(s);
+  tm.on = tm.on && sc.timing();
   tm.mark(0);
-  // 1. prepare queries
-  float* Qp = (float*)ctx->get(1, nq * ld * 4);
-  float* qb = (float*)ctx->get(2, nq * 4);
-  float* qn = (float*)ctx->get(3, nq * 4);
-  unsigned long long* bad = (unsigned long long*)ctx->get(4, 8 + 8);
+  // 1. prepare queries; a non-finite query fails the call whatever k is
+  // (space.rs:104-121 runs before the scan, flat.rs:153-155)
+  float* Qp = (float*)sc.get(1, nq * ld * 4);
+  float* qb = (float*)sc.get(2, nq * 4);
+  float* qn = (float*)sc.get(3, nq * 4);
+  unsigned long long* bad = (unsigned long long*)sc.get(4, 8 + 8);
   int* flag_count = (int*)(bad + 1);
-  PXG_HIP(hipMemsetAsync(bad, 0xFF, 8, s));
-  PXG_HIP(hipMemsetAsync(flag_count, 0, 4, s));
+  int* grp_count = flag_count + 1;
+  hipLaunchKernelGGL(init_search_flags, dim3(1), dim3(64), 0, s, bad, flag_count);
   hipLaunchKernelGGL(flat_prep_queries, dim3((unsigned)nq), dim3(64), 0, s, d_raw, (int)dim, (int)ld, metric,
                      do_prepare ? 1 : 0, Qp, qb, qn, bad);
   PXG_HIP(hipGetLastError());
+  unsigned long long* tail = sc.host_words();
+  auto read_flags = [&](int* nflag) {
+    PXG_HIP(hipMemcpyAsync(tail, bad, 16, hipMemcpyDeviceToHost, s));
+    PXG_HIP(hipStreamSynchronize(s));
+    const unsigned long long badv = tail[0];
+    if (nflag) std::memcpy(nflag, &tail[1], sizeof(int));
+    if (badv != ~0ull) {
+      const uint32_t qi = (uint32_t)(badv >> 32), comp = (uint32_t)badv;
+      raise(PXG_ERR_NON_FINITE, "vector component " + std::to_string(comp) + " is not finite (query " +
+                                    std::to_string(qi) + ")",
+            comp, qi, NAN);
+    }
+  };
+  if (kq == 0) {
+    hipLaunchKernelGGL(fill_u32, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s, d_oc, (size_t)nq, 0u);
+    PXG_HIP(hipGetLastError());
+    read_flags(nullptr);
+    return;
+  }
+  if (kq > EXACT_MERGE_MAXK) {
+    search_wide(Qp, nq, kq, d_accept, d_oid, d_od, d_oc, sc, s, ldo);
+    read_flags(nullptr);
+    tm.finish();
+    return;
+  }
 
-  int* flag_list = (int*)ctx->get(5, nq * 4);
+  int* flag_list = (int*)sc.get(5, nq * 4);
   // Manhattan has no inner-product form and k beyond FAST_KMAX exceeds the
   // candidate buffers: both take the exact scan, as do small problems.
-  const bool exact_all = mode == 2 || metric == PXG_MANHATTAN || k > FAST_KMAX ||
+  const bool exact_all = mode == 2 || metric == PXG_MANHATTAN || kq > FAST_KMAX ||
                          (mode == 0 && (N < 4096 || (double)N * (double)nq < 4.0e6));
   if (!exact_all) {
-    const int Kp = (int)std::min<uint64_t>(k + MARGIN, (uint64_t)FAST_KMAX + MARGIN);
+    const int Kp = (int)std::min<uint64_t>(kq + MARGIN, (uint64_t)FAST_KMAX + MARGIN);
     const int CAP = (Kp + FB_N) <= 256 ? 256 : 512;
     const int QB = (int)((nq + FB_M - 1) / FB_M);
     const int tiles = (int)((N + FB_N - 1) / FB_N);
+    // per query, the least threshold any split has published
+    unsigned long long* gthr = (unsigned long long*)sc.get(25, nq * 8);
     int S = std::max(1, std::min(512 / QB, std::max(1, tiles / 4)));
+    // a fixed scratch may hold fewer splits (the results do not depend on S)
+    const size_t per_split_bytes = (size_t)nq * CAP * 8;
+    const size_t fit = sc.room() / per_split_bytes;
+    if (fit == 0) (void)sc.get(6, per_split_bytes);  // raises the capacity error
+    S = (int)std::min<size_t>((size_t)S, fit);
     const int tiles_per = (tiles + S - 1) / S;
     const int per_split = tiles_per * FB_N;
     S = (int)((N + per_split - 1) / per_split);
-    uint64_t* cand = (uint64_t*)ctx->get(6, (size_t)nq * S * CAP * 8);
-    // per query, the least threshold any split has published
-    unsigned long long* gthr = (unsigned long long*)ctx->get(25, nq * 8);
-    PXG_HIP(hipMemsetAsync(gthr, 0xFF, nq * 8, s));
+    uint64_t* cand = (uint64_t*)sc.get(6, (size_t)nq * S * CAP * 8);
+    hipLaunchKernelGGL(fill_u32, dim3((unsigned)((nq * 2 + 255) / 256)), dim3(256), 0, s, (uint32_t*)gthr,
+                       (size_t)nq * 2, ~0u);
     const int total = QB * S;
     tm.mark(1);
     const int grid = ((total + 7) / 8) * 8;
@@ -603,9 +634,9 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
                          qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, Kp, cand, gthr);
     PXG_HIP(hipGetLastError());
     tm.mark(2);
-    hipLaunchKernelGGL(flat_merge_rescore, dim3((unsigned)nq), dim3(256), 0, s, cand, S, CAP, Kp, (int)k, Qp,
-                       (int)ld, (int)dim, metric, X.p, d_rank.p, d_rank_slot.p, d_ids.p, qn, maxnorm, 4.0f, d_oid,
-                       d_od, d_oc, flag_list, flag_count);
+    hipLaunchKernelGGL(flat_merge_rescore, dim3((unsigned)nq), dim3(256), 0, s, cand, S, CAP, Kp, (int)kq, Qp,
+                       (int)ld, (int)dim, metric, X.p, ranks.rank.p, ranks.rank_slot.p, d_ids.p, qn, maxnorm, 4.0f,
+                       d_oid, d_od, d_oc, flag_list, flag_count, ldo);
     PXG_HIP(hipGetLastError());
   } else {
     hipLaunchKernelGGL(iota_kernel, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s, flag_list, (int)nq,
@@ -613,36 +644,73 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
     PXG_HIP(hipGetLastError());
   }
   // exact scan for flagged queries (all of them on the exact path)
-  // bad (8 bytes) and flag_count (the int after it) in one copy
-  unsigned long long* tail = ctx->tail_host();
-  PXG_HIP(hipMemcpyAsync(tail, bad, 16, hipMemcpyDeviceToHost, s));
-  PXG_HIP(hipStreamSynchronize(s));
-  const unsigned long long badv = tail[0];
-  int nflag;
-  std::memcpy(&nflag, &tail[1], sizeof nflag);
-  if (badv != ~0ull) {
-    const uint32_t qi = (uint32_t)(badv >> 32), comp = (uint32_t)badv;
-    raise(PXG_ERR_NON_FINITE, "vector component " + std::to_string(comp) + " is not finite (query " +
-                                  std::to_string(qi) + ")",
-          comp, qi, NAN);
-  }
+  int nflag = 0;
+  read_flags(&nflag);
   if (nflag > 0) {
+    sc.release_from(6);  // the candidate buffers are dead
     const int nchunks = (int)((N + EXACT_CH - 1) / EXACT_CH);
-    const int kk = (int)std::min<uint64_t>(k, EXACT_CH);
-    uint64_t* ecand = (uint64_t*)ctx->get(7, (size_t)nflag * nchunks * kk * 8);
-    const int grid = std::min(nflag * nchunks, 4096);
+    const int kk = (int)std::min<uint64_t>(kq, EXACT_CH);
+    const size_t per_query = (size_t)nchunks * kk * 8;
+    size_t fit = sc.room() / per_query;
+    if (fit == 0) (void)sc.get(7, per_query);  // raises the capacity error
+    const int G = (int)std::min<size_t>((size_t)nflag, fit);
+    uint64_t* ecand = (uint64_t*)sc.get(7, (size_t)G * per_query);
     tm.mark(exact_all ? 1 : 3);
-    hipLaunchKernelGGL(flat_exact_candidates, dim3(grid), dim3(256), 0, s, flag_list, flag_count, nchunks, Qp,
-                       (int)ld, (int)dim, metric, X.p, (int)N, d_live.p, d_accept, d_rank.p, (int)k, ecand);
-    PXG_HIP(hipGetLastError());
-    if (exact_all) tm.mark(2);
-    hipLaunchKernelGGL(flat_merge_exact, dim3((unsigned)nflag), dim3(256), 0, s, flag_list, flag_count, ecand,
-                       nchunks, (int)k, d_rank_slot.p, d_ids.p, d_oid, d_od, d_oc, (uint64_t*)nullptr);
-    PXG_HIP(hipGetLastError());
+    for (int g0 = 0; g0 < nflag; g0 += G) {
+      const int gn = std::min(G, nflag - g0);
+      const int* count = flag_count;
+      if (gn != nflag) {  // a fixed scratch takes the flagged queries in groups
+        hipLaunchKernelGGL(set_int, dim3(1), dim3(64), 0, s, grp_count, gn);
+        count = grp_count;
+      }
+      hipLaunchKernelGGL(flat_exact_candidates, dim3(std::min(gn * nchunks, 4096)), dim3(256), 0, s,
+                         flag_list + g0, count, nchunks, Qp, (int)ld, (int)dim, metric, X.p, (int)N, d_live.p,
+                         d_accept, ranks.rank.p, (int)kq, ecand);
+      PXG_HIP(hipGetLastError());
+      if (exact_all && g0 == 0) tm.mark(2);
+      hipLaunchKernelGGL(flat_merge_exact, dim3((unsigned)gn), dim3(256), 0, s, flag_list + g0, count, ecand,
+                         nchunks, (int)kq, ranks.rank_slot.p, d_ids.p, d_oid, d_od, d_oc, (uint64_t*)nullptr, ldo);
+      PXG_HIP(hipGetLastError());
+    }
     PXG_HIP(hipStreamSynchronize(s));
     *fallbacks = exact_all ? 0 : (uint64_t)nflag;
   }
   tm.finish();
+}
+
+// k beyond the block selections: exact keys of every slot per query, a
+// segmented radix sort, the first kq of each segment.
+void FlatIndex::search_wide(const float* Qp, uint64_t nq, uint64_t kq, const uint8_t* d_accept, uint64_t* d_oid,
+                            float* d_od, uint32_t* d_oc, Scratch& sc, hipStream_t s, size_t ldo) {
+  const size_t N = slots.high_water();
+  // queries per group: two key buffers of N each, within 1 GiB (or what a
+  // fixed scratch holds) and within the sort's 32-bit sizes
+  const size_t per_query = 2 * N * 8 + 8;
+  size_t G = std::max<size_t>(1, std::min<size_t>((1ull << 30) / per_query, ((1ull << 32) - 1) / N));
+  G = std::min<size_t>(G, nq);
+  for (;;) {
+    const size_t need = G * per_query + 256 * 4 + wide_sort_temp_bytes((uint32_t)(G * N), (uint32_t)G) + 1024;
+    if (need <= sc.room() || G == 1) break;
+    G = std::max<size_t>(1, G / 2);
+  }
+  uint64_t* keys = (uint64_t*)sc.get(8, G * N * 8);
+  uint64_t* sorted = (uint64_t*)sc.get(9, G * N * 8);
+  uint32_t* offs = (uint32_t*)sc.get(10, (G + 1) * 4);
+  const size_t temp_bytes = wide_sort_temp_bytes((uint32_t)(G * N), (uint32_t)G);
+  void* temp = sc.get(11, std::max<size_t>(temp_bytes, 1));
+  for (size_t q0 = 0; q0 < nq; q0 += G) {
+    const int gn = (int)std::min<size_t>(G, nq - q0);
+    hipLaunchKernelGGL(flat_wide_keys, dim3((unsigned)((N + 31) / 32), (unsigned)gn), dim3(256), 0, s, Qp, (int)ld,
+                       (int)dim, metric, X.p, (int)N, d_live.p, d_accept, ranks.rank.p, (int)q0, N, keys);
+    hipLaunchKernelGGL(wide_offsets, dim3((unsigned)((gn + 256) / 256)), dim3(256), 0, s, offs, gn, (uint32_t)N);
+    PXG_HIP(hipGetLastError());
+    if (wide_sort_temp_bytes((uint32_t)(gn * N), (uint32_t)gn) > temp_bytes)
+      internal_error("FlatIndex::search_wide", "sort scratch smaller than the sort asks for");
+    wide_sort(temp, temp_bytes, keys, sorted, (uint32_t)(gn * N), (uint32_t)gn, offs, s);
+    hipLaunchKernelGGL(wide_emit, dim3((unsigned)((kq + 255) / 256), (unsigned)gn), dim3(256), 0, s, sorted, offs,
+                       (int)q0, kq, ranks.rank_slot.p, d_ids.p, d_oid, d_od, d_oc, ldo);
+    PXG_HIP(hipGetLastError());
+  }
 }
 
 // Insert from device memory: validate + prepare on the device, then the
@@ -719,18 +787,17 @@ void FlatIndex::insert_device(const uint64_t* in_ids, const float* d_vecs, uint6
     PXG_HIP(hipGetLastError());
     PXG_HIP(hipStreamSynchronize(stream));
   }
-  rank_dirty = true;
+  ranks.insert(in_ids, sl.data(), n, d_ids.p, stream);
 }
 
 thread_local uint64_t g_last_fallbacks = 0;
+void set_last_fallbacks(uint64_t v) { g_last_fallbacks = v; }
+
 
 }  // namespace pxg
 
 using pxg::FlatIndex;
 
-struct pxg_flat {
-  FlatIndex impl;
-};
 
 extern "C" {
 
@@ -851,11 +918,15 @@ int pxg_flat_search(const pxg_flat* index, const float* queries, uint64_t nq, ui
                        std::to_string(queries[i * f.dim + bad]) + ")",
                    (uint64_t)bad, i, queries[i * f.dim + bad]);
     }
-    if (k == 0 || f.by_id.empty()) {
+    // at most the live count per query: device rows of kq, copied into the
+    // caller's rows of k
+    const uint64_t kq = std::min<uint64_t>(k, f.by_id.size());
+    if (kq == 0) {
       for (uint64_t i = 0; i < nq; ++i) out_count[i] = 0;
       return;
     }
     pxg::CtxLease ctx(f.pool);
+    pxg::CtxScratch sc(ctx.c);
     hipStream_t s = ctx->stream;
     const size_t N = f.slots.high_water();
     float* d_q = (float*)ctx->get(20, prep.size() * 4);
@@ -864,14 +935,14 @@ int pxg_flat_search(const pxg_flat* index, const float* queries, uint64_t nq, ui
       d_acc = ctx->get(21, N);
       PXG_HIP(hipMemcpyAsync(d_acc, accept, N, hipMemcpyHostToDevice, s));
     }
-    uint64_t* d_oid = (uint64_t*)ctx->get(22, nq * k * 8);
-    float* d_od = (float*)ctx->get(23, nq * k * 4);
+    uint64_t* d_oid = (uint64_t*)ctx->get(22, nq * kq * 8);
+    float* d_od = (float*)ctx->get(23, nq * kq * 4);
     uint32_t* d_oc = (uint32_t*)ctx->get(24, nq * 4);
     PXG_HIP(hipMemcpyAsync(d_q, prep.data(), prep.size() * 4, hipMemcpyHostToDevice, s));
     uint64_t fb = 0;
-    f.search_device(d_q, false, nq, k, d_acc, d_oid, d_od, d_oc, ctx.c, s, &fb);
-    PXG_HIP(hipMemcpyAsync(out_ids, d_oid, nq * k * 8, hipMemcpyDeviceToHost, s));
-    PXG_HIP(hipMemcpyAsync(out_dist, d_od, nq * k * 4, hipMemcpyDeviceToHost, s));
+    f.search_device(d_q, false, nq, kq, d_acc, d_oid, d_od, d_oc, sc, s, &fb, kq);
+    PXG_HIP(hipMemcpy2DAsync(out_ids, k * 8, d_oid, kq * 8, kq * 8, nq, hipMemcpyDeviceToHost, s));
+    PXG_HIP(hipMemcpy2DAsync(out_dist, k * 4, d_od, kq * 4, kq * 4, nq, hipMemcpyDeviceToHost, s));
     PXG_HIP(hipMemcpyAsync(out_count, d_oc, nq * 4, hipMemcpyDeviceToHost, s));
     PXG_HIP(hipStreamSynchronize(s));
     pxg::g_last_fallbacks = fb;
@@ -885,9 +956,10 @@ int pxg_flat_search_device(const pxg_flat* index, const float* d_queries, uint64
     FlatIndex& f = const_cast<FlatIndex&>(index->impl);
     std::shared_lock<std::shared_mutex> lk(f.mu);
     pxg::CtxLease ctx(f.pool);
+    pxg::CtxScratch sc(ctx.c);
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
     uint64_t fb = 0;
-    f.search_device(d_queries, true, nq, k, d_accept, d_out_ids, d_out_dist, d_out_count, ctx.c, s, &fb);
+    f.search_device(d_queries, true, nq, k, d_accept, d_out_ids, d_out_dist, d_out_count, sc, s, &fb, k);
     PXG_HIP(hipStreamSynchronize(s));
     pxg::g_last_fallbacks = fb;
   });

@@ -8,6 +8,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "rank.hpp"
 
 namespace pxg {
 
@@ -29,10 +30,7 @@ struct FlatIndex {
   DevBuf<float> xb;        // cap: |x|^2 for L2, 0 otherwise
   DevBuf<uint8_t> d_live;  // cap
   DevBuf<uint64_t> d_ids;  // cap
-  DevBuf<uint32_t> d_rank;       // cap
-  DevBuf<uint32_t> d_rank_slot;  // len
-  bool rank_dirty = true;
-  std::mutex rank_mu;
+  RankTable ranks;         // id ranks of the live slots, current after every mutation
 
   mutable std::shared_mutex mu;
   CtxPool pool;
@@ -40,12 +38,22 @@ struct FlatIndex {
 
   ~FlatIndex();
   void ensure_capacity(size_t need, size_t keep);
-  void rebuild_ranks(hipStream_t s);
   void insert(const uint64_t* in_ids, const float* vecs, uint64_t n, uint32_t* out_slots);
   void remove(uint64_t id);
+  // Search nq device queries (raw when do_prepare, else already prepared
+  // rows of ld floats); results go to rows of ldo entries. Scratch comes from
+  // `sc`; the call returns after the results are complete.
   void search_device(const float* d_raw, bool do_prepare, uint64_t nq, uint64_t k, const uint8_t* d_accept,
-                   uint64_t* d_oid, float* d_od, uint32_t* d_oc, Ctx* ctx, hipStream_t s, uint64_t* fallbacks);
+                     uint64_t* d_oid, float* d_od, uint32_t* d_oc, Scratch& sc, hipStream_t s, uint64_t* fallbacks,
+                     size_t ldo);
+  void search_wide(const float* Qp, uint64_t nq, uint64_t kq, const uint8_t* d_accept, uint64_t* d_oid, float* d_od,
+                   uint32_t* d_oc, Scratch& sc, hipStream_t s, size_t ldo);
   void insert_device(const uint64_t* in_ids, const float* d_vecs, uint64_t n, uint32_t* out_slots);
 };
 
 }  // namespace pxg
+
+// The C ABI handle (include/proxima_hip.h).
+struct pxg_flat {
+  pxg::FlatIndex impl;
+};

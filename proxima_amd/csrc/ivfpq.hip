@@ -998,6 +998,23 @@ __global__ void ivf_residuals(const float* __restrict__ S, const float* __restri
     R[(size_t)i * dim + j] = S[(size_t)i * dim + j] - C[(size_t)a[i] * dim + j];
 }
 
+__global__ void ivf_scatter_u32(const uint32_t* __restrict__ idx, const uint32_t* __restrict__ val, int n,
+                                uint32_t* __restrict__ out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[idx[i]] = val[i];
+}
+
+// Codes and list assignments of n compactly encoded rows, to their slots.
+__global__ void ivf_scatter_codes(const uint8_t* __restrict__ tmp, const uint32_t* __restrict__ sl,
+                                  const uint32_t* __restrict__ as, int n, int M, uint8_t* __restrict__ codes,
+                                  uint32_t* __restrict__ list_of) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const size_t s = sl[i];
+  for (int j = 0; j < M; ++j) codes[s * M + j] = tmp[(size_t)i * M + j];
+  list_of[s] = as[i];
+}
+
 __global__ void ivf_gather_csr(const uint32_t* __restrict__ entry_slot, int n, const uint32_t* __restrict__ rank,
                                const uint8_t* __restrict__ codes, int M, uint32_t* __restrict__ list_rank,
                                uint8_t* __restrict__ list_codes) {
@@ -1160,7 +1177,7 @@ struct IvfPqIndex {
   DevBuf<float> cents_t;  // [dim][cst] transposed centroids for the coarse scan
   int cst = 0;
   DevBuf<int> d_sub_off, d_book_off;
-  DevBuf<uint32_t> d_rank, d_rank_slot;
+  RankTable ranks;  // id ranks of the live slots, current after every mutation
   DevBuf<uint32_t> list_off, list_rank;
   DevBuf<uint8_t> list_codes;
   std::vector<uint32_t> list_len_h;
@@ -1168,7 +1185,7 @@ struct IvfPqIndex {
   // list numbers): MFMA candidates + exact unrolled rescoring give the
   // reference's (distance, list) order for the probe selection
   std::unique_ptr<FlatIndex> coarse;
-  bool rank_dirty = true, csr_dirty = true;
+  bool csr_dirty = true;
   std::mutex lazy_mu;
 
   mutable std::shared_mutex mu;
@@ -1192,34 +1209,16 @@ struct IvfPqIndex {
     d_ids.grow(nc, hw, stream);
     codes.grow(nc * M(), hw * M(), stream);
     d_list_of.grow(nc, hw, stream);
-    d_rank.grow(nc, hw, stream);
+    ranks.grow(nc, hw, stream);
     PXG_HIP(hipMemsetAsync(d_live.p + hw, 0, nc - hw, stream));
     PXG_HIP(hipStreamSynchronize(stream));
     cap = nc;
   }
 
-  // ranks of live ids + the CSR list view; rebuilt on first use after a change
+  // the CSR list view (it caches id ranks); rebuilt on first use after a change
   void refresh(hipStream_t s) {
     std::lock_guard<std::mutex> lk(lazy_mu);
     const size_t hw = slots.high_water();
-    if (rank_dirty) {
-      std::vector<std::pair<uint64_t, uint32_t>> v;
-      v.reserve(by_id.size());
-      for (size_t i = 0; i < hw; ++i)
-        if (live[i]) v.emplace_back(ids[i], (uint32_t)i);
-      std::sort(v.begin(), v.end());
-      std::vector<uint32_t> rs(v.size()), rk(std::max<size_t>(hw, 1), 0);
-      for (size_t r = 0; r < v.size(); ++r) {
-        rs[r] = v[r].second;
-        rk[v[r].second] = (uint32_t)r;
-      }
-      d_rank_slot.reserve(std::max<size_t>(rs.size(), 1));
-      if (!rs.empty()) PXG_HIP(hipMemcpyAsync(d_rank_slot.p, rs.data(), rs.size() * 4, hipMemcpyHostToDevice, s));
-      if (hw) PXG_HIP(hipMemcpyAsync(d_rank.p, rk.data(), hw * 4, hipMemcpyHostToDevice, s));
-      PXG_HIP(hipStreamSynchronize(s));
-      rank_dirty = false;
-      csr_dirty = true;  // list_rank caches ranks
-    }
     if (trained && csr_dirty) {
       std::vector<uint32_t> count(produced + 1, 0);
       for (size_t i = 0; i < hw; ++i)
@@ -1254,7 +1253,7 @@ struct IvfPqIndex {
           order = d_banked.p;
         }
         hipLaunchKernelGGL(ivf_gather_csr, dim3((total + 255) / 256), dim3(256), 0, s, order, (int)total,
-                           d_rank.p, codes.p, (int)M(), list_rank.p, list_codes.p);
+                           ranks.rank.p, codes.p, (int)M(), list_rank.p, list_codes.p);
         PXG_HIP(hipGetLastError());
       }
       PXG_HIP(hipStreamSynchronize(s));
@@ -1313,10 +1312,32 @@ struct IvfPqIndex {
     PXG_HIP(hipMemcpyAsync(as.data(), d_as.p, as.size() * 4, hipMemcpyDeviceToHost, stream));
     PXG_HIP(hipStreamSynchronize(stream));
     for (size_t i = 0; i < sl.size(); ++i) list_of_h[sl[i]] = as[i];
-    // device copy of the assignment, slot-indexed
-    std::vector<uint32_t> lo(list_of_h.begin(), list_of_h.begin() + slots.high_water());
-    PXG_HIP(hipMemcpyAsync(d_list_of.p, lo.data(), lo.size() * 4, hipMemcpyHostToDevice, stream));
+    // device copy of the assignment, slot-indexed: only the encoded slots
+    hipLaunchKernelGGL(ivf_scatter_u32, dim3((unsigned)((sl.size() + 255) / 256)), dim3(256), 0, stream, d_sl.p,
+                       d_as.p, (int)sl.size(), d_list_of.p);
+    PXG_HIP(hipGetLastError());
     PXG_HIP(hipStreamSynchronize(stream));
+    csr_dirty = true;
+  }
+
+  // Encode n prepared rows staged compactly on the device (st[n][ld]) into
+  // their slots: the same nearest-centroid and PQ arithmetic as encode_slots,
+  // without a slot-indexed copy of the rows.
+  void encode_staged(const float* st, const std::vector<uint32_t>& sl) {
+    const size_t n = sl.size();
+    if (n == 0) return;
+    DevBuf<uint32_t> d_sl(n), d_as(n);
+    DevBuf<uint8_t> tmp(n * M());
+    PXG_HIP(hipMemcpyAsync(d_sl.p, sl.data(), n * 4, hipMemcpyHostToDevice, stream));
+    nearest_device(st, (int)ld, nullptr, n, (int)dim, cents.p, (int)ld, produced, true, d_as.p, nullptr, stream);
+    pq_encode_device(st, (int)ld, nullptr, n, (int)dim, cents.p, (int)ld, d_as.p, books.p, pq, tmp.p, stream);
+    hipLaunchKernelGGL(ivf_scatter_codes, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, tmp.p, d_sl.p,
+                       d_as.p, (int)n, (int)M(), codes.p, d_list_of.p);
+    PXG_HIP(hipGetLastError());
+    std::vector<uint32_t> as(n);
+    PXG_HIP(hipMemcpyAsync(as.data(), d_as.p, n * 4, hipMemcpyDeviceToHost, stream));
+    PXG_HIP(hipStreamSynchronize(stream));
+    for (size_t i = 0; i < n; ++i) list_of_h[sl[i]] = as[i];
     csr_dirty = true;
   }
 
@@ -1441,22 +1462,15 @@ struct IvfPqIndex {
       live.resize(hw, 0);
       list_of_h.resize(hw, UNASSIGNED);
     }
-    // vectors go to X when kept, else to a transient slot-indexed store that
-    // only lives long enough to encode them (ivfpq.rs:1134-1141)
-    DevBuf<float> tmpX;
-    float* dst = X.p;
-    if (!vectors_kept) {
-      tmpX.alloc(hw * ld);
-      dst = tmpX.p;
-    }
+    // vectors go to X when kept; an index that drops them encodes from the
+    // staged rows and keeps only the codes (ivfpq.rs:1134-1141)
     DevBuf<uint32_t> st_sl(n);
-    DevBuf<float> st_b(n), dummy_xb(hw);
     DevBuf<uint64_t> st_ids(n);
     PXG_HIP(hipMemcpyAsync(st_sl.p, sl.data(), n * 4, hipMemcpyHostToDevice, stream));
-    PXG_HIP(hipMemsetAsync(st_b.p, 0, n * 4, stream));
     PXG_HIP(hipMemcpyAsync(st_ids.p, in_ids, n * 8, hipMemcpyHostToDevice, stream));
-    hipLaunchKernelGGL(flat_scatter_rows, dim3((unsigned)n), dim3(256), 0, stream, st.p, st_sl.p, st_b.p, st_ids.p,
-                       (int)n, (int)ld, dst, dummy_xb.p, d_live.p, d_ids.p);
+    hipLaunchKernelGGL(flat_scatter_rows, dim3((unsigned)n), dim3(256), 0, stream, st.p, st_sl.p, (const float*)nullptr,
+                       st_ids.p, (int)n, (int)ld, vectors_kept ? X.p : (float*)nullptr, (float*)nullptr, d_live.p,
+                       d_ids.p);
     PXG_HIP(hipGetLastError());
     PXG_HIP(hipStreamSynchronize(stream));
     for (uint64_t i = 0; i < n; ++i) {
@@ -1466,16 +1480,9 @@ struct IvfPqIndex {
       by_id[in_ids[i]] = sl[i];
       if (out_slots) out_slots[i] = sl[i];
     }
-    rank_dirty = true;
-    if (trained) {
-      if (!vectors_kept) {
-        std::swap(X, tmpX);
-        encode_slots(sl);
-        std::swap(X, tmpX);
-      } else {
-        encode_slots(sl);
-      }
-    }
+    ranks.insert(in_ids, sl.data(), n, d_ids.p, stream);
+    csr_dirty = true;  // the list view caches ranks
+    if (trained) encode_staged(st.p, sl);
   }
 
   void remove(uint64_t id) {
@@ -1489,8 +1496,8 @@ struct IvfPqIndex {
     const uint32_t un = UNASSIGNED;
     PXG_HIP(hipMemsetAsync(d_live.p + s, 0, 1, stream));
     PXG_HIP(hipMemcpyAsync(d_list_of.p + s, &un, 4, hipMemcpyHostToDevice, stream));
+    ranks.remove(s, stream);
     PXG_HIP(hipStreamSynchronize(stream));
-    rank_dirty = true;
     csr_dirty = true;
   }
 
@@ -1529,11 +1536,11 @@ struct IvfPqIndex {
       tm.mark(1);
       hipLaunchKernelGGL(flat_exact_candidates, dim3(std::min<int>((int)nq * nchunks, 4096)), dim3(256), 0, s, qlist,
                          flag_count, nchunks, Qp, (int)ld, (int)dim, metric, X.p, (int)N, d_live.p, d_accept,
-                         d_rank.p, (int)k, ecand);
+                         ranks.rank.p, (int)k, ecand);
       PXG_HIP(hipGetLastError());
       tm.mark(2);
       hipLaunchKernelGGL(flat_merge_exact, dim3((unsigned)nq), dim3(256), 0, s, qlist, flag_count, ecand, nchunks,
-                         (int)k, d_rank_slot.p, d_ids.p, d_oid, d_od, d_oc, (uint64_t*)nullptr);
+                         (int)k, ranks.rank_slot.p, d_ids.p, d_oid, d_od, d_oc, (uint64_t*)nullptr, (size_t)k);
       PXG_HIP(hipGetLastError());
     } else {
       const int np = (int)std::min<uint64_t>(std::max<uint64_t>(nprobe_in, 1), (uint64_t)std::max(produced, 1));
@@ -1568,7 +1575,8 @@ struct IvfPqIndex {
         uint32_t* ccnt = (uint32_t*)ctx->get(14, nq * 4);
         CtxLease cl(coarse->pool);
         uint64_t fb = 0;
-        coarse->search_device(Qd, false, nq, (uint64_t)np, nullptr, cid, cdist, ccnt, cl.c, s, &fb);
+        CtxScratch csc(cl.c);
+        coarse->search_device(Qd, false, nq, (uint64_t)np, nullptr, cid, cdist, ccnt, csc, s, &fb, (size_t)np);
         hipLaunchKernelGGL(ivf_probes_from_ids, dim3((unsigned)((nq * np + 255) / 256)), dim3(256), 0, s, cid,
                            (int)(nq * np), probes);
       } else {
@@ -1602,7 +1610,7 @@ struct IvfPqIndex {
 #define PXG_SCANR(WW, MET)                                                                                          \
   hipLaunchKernelGGL((ivf_scan_reg<WW, MET>), dim3(grid), dim3(IVF_SW * 64), lds, s, Qp, (int)ld, (int)dim,        \
                      (int)M(), probes, np, pg, groups, cents.p, books.p, list_off.p, list_rank.p, list_codes.p,      \
-                     d_rank_slot.p, d_accept, kk, cand, (int)k, d_ids.p, fused ? d_oid : nullptr, d_od, d_oc)
+                     ranks.rank_slot.p, d_accept, kk, cand, (int)k, d_ids.p, fused ? d_oid : nullptr, d_od, d_oc)
 #define PXG_SCANR_W(MET)                  \
   switch (W) {                            \
     case 1: PXG_SCANR(1, MET); break;     \
@@ -1614,7 +1622,7 @@ struct IvfPqIndex {
   }
 #define PXG_SCAN16(WW, MET)                                                                                         \
   hipLaunchKernelGGL((ivf_scan16<WW, MET>), dim3(grid), dim3(IVF_SW * 64), 0, s, Qp, (int)ld, probes, np, pg, groups, \
-                     cents.p, books.p, list_off.p, list_rank.p, list_codes.p, d_rank_slot.p, d_accept, kk, cand,     \
+                     cents.p, books.p, list_off.p, list_rank.p, list_codes.p, ranks.rank_slot.p, d_accept, kk, cand,     \
                      (int)k, d_ids.p, fused ? d_oid : nullptr, d_od, d_oc)
 #define PXG_SCAN16_W(MET)                 \
   switch (W) {                            \
@@ -1642,7 +1650,7 @@ struct IvfPqIndex {
         tm.mark(2);
         if (!fused) {
           hipLaunchKernelGGL(ivf_merge, dim3((unsigned)nq), dim3(256), 0, s, cand, groups * IVF_SW * kk, kk, (int)k,
-                             rerank ? 1 : 0, Qp, (int)ld, (int)dim, metric, X.p, d_rank_slot.p, d_ids.p, d_oid, d_od,
+                             rerank ? 1 : 0, Qp, (int)ld, (int)dim, metric, X.p, ranks.rank_slot.p, d_ids.p, d_oid, d_od,
                              d_oc);
           PXG_HIP(hipGetLastError());
         }
@@ -1654,7 +1662,7 @@ struct IvfPqIndex {
 #define PXG_SCAN(CAPW, MET)                                                                                       \
   hipLaunchKernelGGL((ivf_scan<CAPW, MET>), dim3(grid), dim3(256), lds, s, Qp, (int)ld, (int)dim, (int)M(), probes, \
                      np, cents.p, books.p, d_sub_off.p, d_book_off.p, list_off.p, list_rank.p, list_codes.p,       \
-                     d_rank_slot.p, d_accept, kk, cand)
+                     ranks.rank_slot.p, d_accept, kk, cand)
       if (kk <= 192) {
         if (metric == PXG_COSINE) PXG_SCAN(256, 1); else PXG_SCAN(256, 0);
       } else if (kk <= 448) {
@@ -1666,7 +1674,7 @@ struct IvfPqIndex {
       PXG_HIP(hipGetLastError());
       tm.mark(2);
       hipLaunchKernelGGL(ivf_merge, dim3((unsigned)nq), dim3(256), 0, s, cand, np * 4 * kk, kk, (int)k,
-                         rerank ? 1 : 0, Qp, (int)ld, (int)dim, metric, X.p, d_rank_slot.p, d_ids.p, d_oid, d_od,
+                         rerank ? 1 : 0, Qp, (int)ld, (int)dim, metric, X.p, ranks.rank_slot.p, d_ids.p, d_oid, d_od,
                          d_oc);
       PXG_HIP(hipGetLastError());
       }

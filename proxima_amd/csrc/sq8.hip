@@ -41,6 +41,7 @@
 
 #include "common.hpp"
 #include "device.hpp"
+#include "rank.hpp"
 #include "exact_scan.hpp"
 
 namespace pxg {
@@ -693,9 +694,7 @@ struct Sq8Index {
   DevBuf<int8_t> codes;  // cap * KP, I8 codes, zero padded
   DevBuf<uint8_t> d_live;
   DevBuf<uint64_t> d_ids;
-  DevBuf<uint32_t> d_rank, d_rank_slot;
-  bool rank_dirty = true;
-  std::mutex rank_mu;
+  RankTable ranks;  // id ranks of the live slots, current after every mutation
 
   mutable std::shared_mutex mu;
   CtxPool pool;
@@ -769,31 +768,11 @@ struct Sq8Index {
     codes.grow(nc * KP, hw * KP, stream);
     d_live.grow(nc, hw, stream);
     d_ids.grow(nc, hw, stream);
-    d_rank.grow(nc, hw, stream);
+    ranks.grow(nc, hw, stream);
     PXG_HIP(hipMemsetAsync(d_live.p + hw, 0, nc - hw, stream));
     PXG_HIP(hipMemsetAsync(codes.p + hw * KP, 0, (nc - hw) * KP, stream));
     PXG_HIP(hipStreamSynchronize(stream));
     cap = nc;
-  }
-
-  void rebuild_ranks(hipStream_t s) {
-    std::lock_guard<std::mutex> lk(rank_mu);
-    if (!rank_dirty) return;
-    std::vector<std::pair<uint64_t, uint32_t>> v;
-    v.reserve(by_id.size());
-    for (size_t s2 = 0; s2 < ids.size(); ++s2)
-      if (live[s2]) v.emplace_back(ids[s2], (uint32_t)s2);
-    std::sort(v.begin(), v.end());
-    std::vector<uint32_t> rs(v.size()), rk(std::max<size_t>(ids.size(), 1), 0);
-    for (size_t r = 0; r < v.size(); ++r) {
-      rs[r] = v[r].second;
-      rk[v[r].second] = (uint32_t)r;
-    }
-    d_rank_slot.reserve(std::max<size_t>(rs.size(), 1));
-    if (!rs.empty()) PXG_HIP(hipMemcpyAsync(d_rank_slot.p, rs.data(), rs.size() * 4, hipMemcpyHostToDevice, s));
-    if (!ids.empty()) PXG_HIP(hipMemcpyAsync(d_rank.p, rk.data(), ids.size() * 4, hipMemcpyHostToDevice, s));
-    PXG_HIP(hipStreamSynchronize(s));
-    rank_dirty = false;
   }
 
   void check_new_ids(const uint64_t* in_ids, uint64_t n) {
@@ -821,7 +800,6 @@ struct Sq8Index {
       by_id[in_ids[i]] = sl[i];
       if (out_slots) out_slots[i] = sl[i];
     }
-    rank_dirty = true;
     return sl;
   }
 
@@ -870,6 +848,7 @@ struct Sq8Index {
       PXG_HIP(hipGetLastError());
       PXG_HIP(hipStreamSynchronize(stream));
     }
+    ranks.insert(in_ids, sl.data(), n, d_ids.p, stream);
   }
 
   void insert_host(const uint64_t* in_ids, const float* vecs, uint64_t n, uint32_t* out_slots) {
@@ -914,6 +893,7 @@ struct Sq8Index {
       PXG_HIP(hipGetLastError());
       PXG_HIP(hipStreamSynchronize(stream));
     }
+    ranks.insert(in_ids, sl.data(), n, d_ids.p, stream);
   }
 
   void remove(uint64_t id) {
@@ -925,8 +905,8 @@ struct Sq8Index {
     ids[s] = 0;
     slots.release(s);
     PXG_HIP(hipMemsetAsync(d_live.p + s, 0, 1, stream));
+    ranks.remove(s, stream);
     PXG_HIP(hipStreamSynchronize(stream));
-    rank_dirty = true;
   }
 
   // Queries: f32 (prepared + encoded here; rescoring possible) or I8 codes.
@@ -946,7 +926,6 @@ struct Sq8Index {
     const uint64_t kk64 = std::max<uint64_t>(k, rescore);
     if (kk64 > 1024) config_error("k", kk64, "the GPU SQ8 search supports max(k, rescore) up to 1024 per query");
     const int kk = (int)kk64;
-    rebuild_ranks(s);
     Timer tm(s);
     tm.mark(0);
     int8_t* Qc = (int8_t*)ctx->get(1, nq * KP);
@@ -1011,7 +990,7 @@ struct Sq8Index {
       const dim3 grid((unsigned)((nchunks * qgroups + 7) / 8 * 8));
 #define PXG_SQ_SCAN(KBV, ST)                                                                                        \
   hipLaunchKernelGGL((sq8_mfma_scan<KBV, ST>), grid, dim3((SQ_NW + 1) * 64), 0, s, (const int8_t*)Qc, (int)nq,           \
-                     (const int8_t*)codes.p, N, d_live.p, d_accept, d_rank.p, nchunks, qgroups, tpc, sample,       \
+                     (const int8_t*)codes.p, N, d_live.p, d_accept, ranks.rank.p, nchunks, qgroups, tpc, sample,       \
                      (const int*)thr, tmax,                                                                        \
                      ccount, cand, cap_c)
 #define PXG_SQ_SWITCH(ST)                  \
@@ -1061,12 +1040,12 @@ struct Sq8Index {
       uint64_t* ecand = (uint64_t*)ctx->get(13, (size_t)nflag * nchunks * kke * 8);
       hipLaunchKernelGGL(sq8_exact_candidates, dim3((unsigned)std::min<int64_t>((int64_t)nflag * nchunks, 4096)),
                          dim3(256), 0, s, (const int*)flag_list, (const int*)flag_count, nchunks, (const int8_t*)Qc,
-                         (int)KP, (const int8_t*)codes.p, N, d_live.p, d_accept, d_rank.p, kk, ecand);
+                         (int)KP, (const int8_t*)codes.p, N, d_live.p, d_accept, ranks.rank.p, kk, ecand);
       PXG_HIP(hipGetLastError());
       if (!mfma) tm.mark(2);
       hipLaunchKernelGGL(flat_merge_exact, dim3((unsigned)nflag), dim3(256), 0, s, (const int*)flag_list,
-                         (const int*)flag_count, (const uint64_t*)ecand, nchunks, kk, d_rank_slot.p, d_ids.p,
-                         (uint64_t*)nullptr, (float*)nullptr, ocount, okeys);
+                         (const int*)flag_count, (const uint64_t*)ecand, nchunks, kk, ranks.rank_slot.p, d_ids.p,
+                         (uint64_t*)nullptr, (float*)nullptr, ocount, okeys, (size_t)kk);
       PXG_HIP(hipGetLastError());
     }
     if (rescore) {
@@ -1074,11 +1053,11 @@ struct Sq8Index {
       while (P < kk) P <<= 1;
       hipLaunchKernelGGL(sq8_rescore, dim3((unsigned)nq), dim3(256), (size_t)P * 8, s, (const uint64_t*)okeys,
                          (const uint32_t*)ocount, kk, (int)k, (const float*)Qp, (int)ld, (int)dim,
-                         (const int8_t*)codes.p, (int)KP, per_dim, d_mn.p, d_scale.p, d_rank_slot.p, d_ids.p, d_oid,
+                         (const int8_t*)codes.p, (int)KP, per_dim, d_mn.p, d_scale.p, ranks.rank_slot.p, d_ids.p, d_oid,
                          d_od, d_oc);
     } else {
       hipLaunchKernelGGL(sq8_emit, dim3((unsigned)nq), dim3(64), 0, s, (const uint64_t*)okeys,
-                         (const uint32_t*)ocount, kk, (int)k, d_rank_slot.p, d_ids.p, d_oid, d_od, d_oc);
+                         (const uint32_t*)ocount, kk, (int)k, ranks.rank_slot.p, d_ids.p, d_oid, d_od, d_oc);
     }
     PXG_HIP(hipGetLastError());
     unsigned long long* tail = ctx->tail_host();

@@ -338,3 +338,45 @@ def test_thresholds_shared_across_splits(gpu, metric):
     acc = (np.arange(n) % 3 == 1).astype(np.uint8)
     got = idx.search_batch(q, 10, lambda i, _m: i % 3 == 1)
     assert_same(got, oracle_search(px, data, ids, metric, q, 10, accept=acc))
+
+
+# --- k beyond the block selections (check_k allows up to 2^24, index.rs:212-224) ----------
+@pytest.mark.parametrize("metric", [0, 2, 3])
+def test_large_k_matches_oracle(gpu, metric):
+    px = gpu
+    rng = np.random.default_rng(70 + metric)
+    n, dim = 20_000, 24
+    data = rng.standard_normal((n, dim)).astype(np.float32)
+    data[100:140] = data[7]  # exact ties across the cut
+    ids = rng.permutation(n).astype(np.uint64)
+    idx = make_index(px, data, metric, ids=ids)
+    for s in (3, 9, 11):
+        idx.remove(int(ids[s]))
+    live = np.ones(n, np.uint8)
+    live[[3, 9, 11]] = 0
+    q = rng.standard_normal((6, dim)).astype(np.float32)
+    q[0] = data[7]
+    for k in (1025, 5000, n + 5):
+        got = idx.search_batch(q, k)
+        want = oracle_search(px, data, ids, metric, q, k, live=live)
+        assert_same(got, want)
+    # a filter with the wide path
+    keep = lambda i, _m: int(i) % 5 != 0  # noqa: E731
+    acc = np.array([0 if not live[s] else (int(ids[s]) % 5 != 0) for s in range(n)], np.uint8)
+    assert_same(idx.search_batch(q, 3000, keep), oracle_search(px, data, ids, metric, q, 3000, accept=acc, live=live))
+
+
+def test_k_far_above_the_live_count(gpu):
+    px = gpu
+    rng = np.random.default_rng(3)
+    data = rng.standard_normal((100, 16)).astype(np.float32)
+    for mode in MODES:
+        idx = make_index(px, data, 0, mode=mode)
+        q = rng.standard_normal((4, 16)).astype(np.float32)
+        got = idx.search_batch(q, 1 << 20)
+        want = oracle_search(px, data, np.arange(100, dtype=np.uint64), 0, q, 100)
+        gi, gd, gc = got
+        assert list(gc) == [100] * 4
+        assert_same((gi[:, :100], gd[:, :100], gc), want)
+    with pytest.raises(px.Configuration):
+        idx.search_batch(q, (1 << 24) + 1)
