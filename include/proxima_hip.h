@@ -132,6 +132,20 @@ int pxg_flat_search(const pxg_flat* index, const float* queries, uint64_t nq, ui
 int pxg_flat_search_device(const pxg_flat* index, const float* d_queries, uint64_t nq, uint64_t k,
                            const uint8_t* d_accept, uint64_t* d_out_ids, float* d_out_dist, uint32_t* d_out_count,
                            void* stream);
+/* pxg_flat_search_device that allocates nothing: no hipMalloc, hipFree,
+ * pinned host memory, stream or event. No counterpart in the reference; it is
+ * for callers that cannot allocate (serving loops with a fixed memory budget,
+ * code that must not touch the allocator). Its scratch is one static device
+ * array of 128 MiB per GPU, held until the process ends; a call that needs
+ * more (prepared queries, candidate buffers, exact-scan keys) fails with
+ * PXG_ERR_CAPACITY before any work is queued, detail a = bytes it would need.
+ * Calls on one GPU share that array: a per-GPU lock inside the library
+ * serializes them, and each call has finished on the GPU when it returns.
+ * stream: the caller's (NULL = the null stream). Results equal
+ * pxg_flat_search_device's bit for bit. */
+int pxg_flat_search_device_noalloc(const pxg_flat* index, const float* d_queries, uint64_t nq, uint64_t k,
+                                   const uint8_t* d_accept, uint64_t* d_out_ids, float* d_out_dist,
+                                   uint32_t* d_out_count, void* stream);
 /* Search statistics of the last search on this thread: queries whose MFMA
  * candidate set could not be proven to contain the exact top-k and were
  * rescanned exactly. */

@@ -88,6 +88,7 @@ SIGNATURES = {
     "pxg_flat_slots": (_i32, [_vp, _vp, _vp]),
     "pxg_flat_search": (_i32, [_vp, _vp, _u64, _u64, _vp, _vp, _vp, _vp]),
     "pxg_flat_search_device": (_i32, [_vp, _vp, _u64, _u64, _vp, _vp, _vp, _vp, _vp]),
+    "pxg_flat_search_device_noalloc": (_i32, [_vp, _vp, _u64, _u64, _vp, _vp, _vp, _vp, _vp]),
     "pxg_flat_last_fallbacks": (_u64, []),
     "pxg_flat_set_search_mode": (_i32, [_vp, _i32]),
     # ivf-pq
