@@ -198,6 +198,11 @@ int pxg_ivfpq_insert_device(pxg_ivfpq* index, const uint64_t* ids, const float* 
                             uint32_t* out_slots);
 /* VectorIndex::remove (ivfpq.rs:1160-1180). */
 int pxg_ivfpq_remove(pxg_ivfpq* index, uint64_t id);
+/* IvfPqIndex::compact (ivfpq.rs:907-975), reached through AnyIndex::compact
+ * (proxima-store/src/index.rs:114-120): drop the free slots and renumber the
+ * live ones in slot order; results are unchanged. reclaimed (may be NULL) =
+ * slots given back (high-water mark minus the live count). */
+int pxg_ivfpq_compact(pxg_ivfpq* index, uint64_t* reclaimed);
 int pxg_ivfpq_contains(const pxg_ivfpq* index, uint64_t id);
 uint64_t pxg_ivfpq_len(const pxg_ivfpq* index);
 int pxg_ivfpq_is_trained(const pxg_ivfpq* index);

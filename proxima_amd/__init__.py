@@ -517,6 +517,13 @@ class IvfPqIndex(_IndexBase):
         """Code entries streamed by the last search on this thread."""
         return int(_lib.pxg_ivfpq_last_scanned())
 
+    def compact(self):
+        """IvfPqIndex::compact (ivfpq.rs:907-975): drop free slots, renumber the
+        live ones in slot order; returns the number of slots reclaimed."""
+        r = C.c_uint64()
+        _check(_lib.pxg_ivfpq_compact(self._h, C.byref(r)))
+        return int(r.value)
+
     def remove(self, id):
         _check(_lib.pxg_ivfpq_remove(self._h, int(id)))
         self._meta.pop(int(id), None)

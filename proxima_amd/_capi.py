@@ -98,6 +98,7 @@ SIGNATURES = {
     "pxg_ivfpq_insert": (_i32, [_vp, _vp, _vp, _u64, _vp]),
     "pxg_ivfpq_insert_device": (_i32, [_vp, _vp, _vp, _u64, _vp]),
     "pxg_ivfpq_remove": (_i32, [_vp, _u64]),
+    "pxg_ivfpq_compact": (_i32, [_vp, _P(_u64)]),
     "pxg_ivfpq_contains": (_i32, [_vp, _u64]),
     "pxg_ivfpq_len": (_u64, [_vp]),
     "pxg_ivfpq_is_trained": (_i32, [_vp]),

@@ -425,27 +425,6 @@ __global__ __launch_bounds__(256) void flat_merge_rescore(
   }
 }
 
-// Exact (distance, id rank) keys of every slot for queries q0 .. q0 + G - 1
-// (grid (ceil(N / 32), G), 8 threads per slot), KEY_MAX for free or
-// filtered slots; segment g starts at g * seg.
-__global__ __launch_bounds__(256) void flat_wide_keys(const float* __restrict__ Qp, int ld, int dim, int metric,
-                                                      const float* __restrict__ X, int N,
-                                                      const uint8_t* __restrict__ live,
-                                                      const uint8_t* __restrict__ accept,
-                                                      const uint32_t* __restrict__ rank, int q0, size_t seg,
-                                                      uint64_t* __restrict__ keys) {
-  const int g = threadIdx.x & 7;
-  const int slot = blockIdx.x * 32 + (threadIdx.x >> 3);
-  const float* qv = Qp + (size_t)(q0 + blockIdx.y) * ld;
-  if (slot >= N) return;
-  uint64_t key = KEY_MAX;
-  if (live[slot] && (accept == nullptr || accept[slot])) {
-    const float d = dist_group8_rt(metric, qv, X + (size_t)slot * ld, dim, g);
-    key = ((uint64_t)ord_key(d) << 32) | rank[slot];
-  }
-  if (g == 0) keys[(size_t)blockIdx.y * seg + slot] = key;
-}
-
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -682,35 +661,8 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
 // segmented radix sort, the first kq of each segment.
 void FlatIndex::search_wide(const float* Qp, uint64_t nq, uint64_t kq, const uint8_t* d_accept, uint64_t* d_oid,
                             float* d_od, uint32_t* d_oc, Scratch& sc, hipStream_t s, size_t ldo) {
-  const size_t N = slots.high_water();
-  // queries per group: two key buffers of N each, within 1 GiB (or what a
-  // fixed scratch holds) and within the sort's 32-bit sizes
-  const size_t per_query = 2 * N * 8 + 8;
-  size_t G = std::max<size_t>(1, std::min<size_t>((1ull << 30) / per_query, ((1ull << 32) - 1) / N));
-  G = std::min<size_t>(G, nq);
-  for (;;) {
-    const size_t need = G * per_query + 256 * 4 + wide_sort_temp_bytes((uint32_t)(G * N), (uint32_t)G) + 1024;
-    if (need <= sc.room() || G == 1) break;
-    G = std::max<size_t>(1, G / 2);
-  }
-  uint64_t* keys = (uint64_t*)sc.get(8, G * N * 8);
-  uint64_t* sorted = (uint64_t*)sc.get(9, G * N * 8);
-  uint32_t* offs = (uint32_t*)sc.get(10, (G + 1) * 4);
-  const size_t temp_bytes = wide_sort_temp_bytes((uint32_t)(G * N), (uint32_t)G);
-  void* temp = sc.get(11, std::max<size_t>(temp_bytes, 1));
-  for (size_t q0 = 0; q0 < nq; q0 += G) {
-    const int gn = (int)std::min<size_t>(G, nq - q0);
-    hipLaunchKernelGGL(flat_wide_keys, dim3((unsigned)((N + 31) / 32), (unsigned)gn), dim3(256), 0, s, Qp, (int)ld,
-                       (int)dim, metric, X.p, (int)N, d_live.p, d_accept, ranks.rank.p, (int)q0, N, keys);
-    hipLaunchKernelGGL(wide_offsets, dim3((unsigned)((gn + 256) / 256)), dim3(256), 0, s, offs, gn, (uint32_t)N);
-    PXG_HIP(hipGetLastError());
-    if (wide_sort_temp_bytes((uint32_t)(gn * N), (uint32_t)gn) > temp_bytes)
-      internal_error("FlatIndex::search_wide", "sort scratch smaller than the sort asks for");
-    wide_sort(temp, temp_bytes, keys, sorted, (uint32_t)(gn * N), (uint32_t)gn, offs, s);
-    hipLaunchKernelGGL(wide_emit, dim3((unsigned)((kq + 255) / 256), (unsigned)gn), dim3(256), 0, s, sorted, offs,
-                       (int)q0, kq, ranks.rank_slot.p, d_ids.p, d_oid, d_od, d_oc, ldo);
-    PXG_HIP(hipGetLastError());
-  }
+  exact_wide_search(Qp, (int)ld, (int)dim, metric, nq, kq, X.p, slots.high_water(), d_live.p, d_accept, ranks.rank.p,
+                    ranks.rank_slot.p, d_ids.p, d_oid, d_od, d_oc, ldo, sc, s);
 }
 
 // Insert from device memory: validate + prepare on the device, then the

@@ -46,6 +46,7 @@
 #include "device.hpp"
 #include "exact_scan.hpp"
 #include "flat.hpp"
+#include "wide.hpp"
 #include "train.hpp"
 #include <chrono>
 #include <cstdio>
@@ -1015,6 +1016,137 @@ __global__ void ivf_scatter_codes(const uint8_t* __restrict__ tmp, const uint32_
   list_of[s] = as[i];
 }
 
+// ---------------------------------------------------------------------------
+// Wide path (shortlist beyond the block selections, or tables beyond the
+// LDS): per (query, probe) item, a distance table in device memory, the ADC
+// keys of every entry of the probed list into the query's segment, then the
+// segmented sort and optional rerank of wide.hpp.
+// ---------------------------------------------------------------------------
+// Table of item i = q * np + p (grid: items of queries q0 .. q0 + G - 1), the
+// loop of product.rs:416-433 per (subspace, centroid): L2 on the residual
+// q - c_list (ivfpq.rs:1052-1054), cosine on the query; for cosine also
+// omq = 1 - q.c_list (ivfpq.rs:1068-1072).
+__global__ __launch_bounds__(256) void ivf_wide_tables(const float* __restrict__ Qp, int ld, int dim, int M,
+                                                       int metric, const int* __restrict__ probes, int np, int q0,
+                                                       const float* __restrict__ cents,
+                                                       const float* __restrict__ books,
+                                                       const int* __restrict__ sub_off,
+                                                       const int* __restrict__ book_off, float* __restrict__ tables,
+                                                       float* __restrict__ omq) {
+  const int item = blockIdx.x;
+  const int q = q0 + item / np;
+  const int l = probes[(size_t)q0 * np + item];
+  const float* qv = Qp + (size_t)q * ld;
+  const float* cv = cents + (size_t)l * ld;
+  float* tab = tables + (size_t)item * M * 256;
+  for (int e = threadIdx.x; e < M * 256; e += blockDim.x) {
+    const int sidx = e >> 8, c = e & 255;
+    const int o = sub_off[sidx], w = sub_off[sidx + 1] - o;
+    const float* b = books + book_off[sidx] + c * w;
+    float acc = 0.0f;
+    for (int j = 0; j < w; ++j) {
+      if (metric == 0) {
+        const float r = qv[o + j] - cv[o + j];
+        const float d = r - b[j];
+        acc += d * d;
+      } else {
+        acc += qv[o + j] * b[j];
+      }
+    }
+    tab[e] = acc;
+  }
+  if (metric == 1 && threadIdx.x < 8) {
+    const float d = -dist_group8<2>(qv, cv, dim, threadIdx.x);
+    if (threadIdx.x == 0) omq[item] = arm_nan(1.0f - d);
+  }
+}
+
+// ADC keys of every entry of item i's list, at pofs[i] onwards (same sums and
+// scores as the scans: DistanceTable::squared_l2 / inner_product,
+// product.rs:580-603, in subspace order).
+__global__ __launch_bounds__(256) void ivf_wide_keys(const int* __restrict__ probes, int np, int q0, int M,
+                                                     int metric, const float* __restrict__ tables,
+                                                     const float* __restrict__ omq,
+                                                     const uint32_t* __restrict__ list_off,
+                                                     const uint32_t* __restrict__ list_rank,
+                                                     const uint8_t* __restrict__ list_codes,
+                                                     const uint32_t* __restrict__ rank_slot,
+                                                     const uint8_t* __restrict__ accept,
+                                                     const uint32_t* __restrict__ pofs, uint64_t* __restrict__ keys) {
+  const int item = blockIdx.x;
+  const int l = probes[(size_t)q0 * np + item];
+  const float* tab = tables + (size_t)item * M * 256;
+  const uint32_t begin = list_off[l], end = list_off[l + 1];
+  uint64_t* out = keys + pofs[item];
+  const float om = metric == 1 ? omq[item] : 0.0f;
+  for (uint32_t e = begin + threadIdx.x; e < end; e += blockDim.x) {
+    const uint32_t rk = list_rank[e];
+    uint64_t key = KEY_MAX;
+    if (accept == nullptr || accept[rank_slot[rk]]) {
+      const uint8_t* code = list_codes + (size_t)e * M;
+      float sum = 0.0f;
+      for (int sidx = 0; sidx < M; ++sidx) sum += tab[sidx * 256 + code[sidx]];
+      const float score = metric == 0 ? sum : ivf_cos_score(om, sum);
+      key = ((uint64_t)ord_key(score) << 32) | rk;
+    }
+    out[e - begin] = key;
+  }
+}
+
+// Exact rescoring of the first min(t, len) keys of each segment (the rerank
+// of ivfpq.rs:1094-1109), from `sorted` into the same positions of `keys`.
+// Grid (ceil(t / 32), G), 8 threads per candidate.
+__global__ __launch_bounds__(256) void ivf_wide_rerank(const uint64_t* __restrict__ sorted,
+                                                       const uint32_t* __restrict__ begins,
+                                                       const uint32_t* __restrict__ ends, uint64_t t, int q0,
+                                                       const float* __restrict__ Qp, int ld, int dim, int metric,
+                                                       const float* __restrict__ X,
+                                                       const uint32_t* __restrict__ rank_slot,
+                                                       uint64_t* __restrict__ keys) {
+  const int gq = blockIdx.y;
+  const uint64_t len = ends[gq] - begins[gq];
+  const uint64_t take = t < len ? t : len;
+  const uint64_t i = (uint64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+  const int g = threadIdx.x & 7;
+  if (i >= take) return;
+  const uint64_t key = sorted[begins[gq] + i];
+  uint64_t nk = KEY_MAX;
+  if (key != KEY_MAX) {
+    const uint32_t rk = (uint32_t)key;
+    const float d = dist_group8_rt(metric, Qp + (size_t)(q0 + gq) * ld, X + (size_t)rank_slot[rk] * ld, dim, g);
+    nk = ((uint64_t)ord_key(d) << 32) | rk;
+  }
+  if (g == 0) keys[begins[gq] + i] = nk;
+}
+
+// Compaction (ivfpq.rs:907-975): new slot i takes old slot keep[i].
+__global__ void ivf_compact_rows(const uint32_t* __restrict__ keep, int n, int ld, int M, const float* __restrict__ X0,
+                                 float* __restrict__ X1, const uint8_t* __restrict__ c0, uint8_t* __restrict__ c1,
+                                 const uint32_t* __restrict__ l0, uint32_t* __restrict__ l1,
+                                 const uint64_t* __restrict__ i0, uint64_t* __restrict__ i1,
+                                 const uint32_t* __restrict__ r0, uint32_t* __restrict__ r1,
+                                 uint8_t* __restrict__ live1) {
+  const int i = blockIdx.x;
+  if (i >= n) return;
+  const size_t o = keep[i];
+  if (X0 != nullptr)
+    for (int c = threadIdx.x; c < ld; c += blockDim.x) X1[(size_t)i * ld + c] = X0[o * ld + c];
+  for (int j = threadIdx.x; j < M; j += blockDim.x) c1[(size_t)i * M + j] = c0[o * M + j];
+  if (threadIdx.x == 0) {
+    l1[i] = l0[o];
+    i1[i] = i0[o];
+    r1[i] = r0[o];
+    live1[i] = 1;
+  }
+}
+
+// rank_slot[r] = new_of_old[rank_slot[r]]
+__global__ void ivf_remap_slots(uint32_t* __restrict__ rank_slot, uint32_t len,
+                                const uint32_t* __restrict__ new_of_old) {
+  const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r < len) rank_slot[r] = new_of_old[rank_slot[r]];
+}
+
 __global__ void ivf_gather_csr(const uint32_t* __restrict__ entry_slot, int n, const uint32_t* __restrict__ rank,
                                const uint8_t* __restrict__ codes, int M, uint32_t* __restrict__ list_rank,
                                uint8_t* __restrict__ list_codes) {
@@ -1485,6 +1617,64 @@ struct IvfPqIndex {
     if (trained) encode_staged(st.p, sl);
   }
 
+  // IvfPqIndex::compact (ivfpq.rs:907-975): drop the free slots, renumber
+  // the live ones in slot order, shrink every array. Codebooks, centroids,
+  // codes and ids are unchanged, so searches return the same results.
+  uint64_t compact() {
+    const size_t hw = slots.high_water();
+    const uint64_t reclaimed = hw - by_id.size();
+    if (reclaimed == 0) return 0;
+    std::vector<uint32_t> keep, new_of_old(std::max<size_t>(hw, 1), UINT32_MAX);
+    keep.reserve(by_id.size());
+    for (size_t i = 0; i < hw; ++i)
+      if (live[i]) {
+        new_of_old[i] = (uint32_t)keep.size();
+        keep.push_back((uint32_t)i);
+      }
+    const size_t n = keep.size();
+    const size_t nc = std::max<size_t>(n, 1024);
+    DevBuf<float> X1;
+    if (vectors_kept) X1.alloc(nc * ld);
+    DevBuf<uint8_t> c1(nc * M()), live1(nc);
+    DevBuf<uint32_t> l1(nc), r1(nc), d_keep(std::max<size_t>(n, 1)), d_map(std::max<size_t>(hw, 1));
+    DevBuf<uint64_t> i1(nc);
+    PXG_HIP(hipMemsetAsync(live1.p, 0, nc, stream));
+    if (n) {
+      PXG_HIP(hipMemcpyAsync(d_keep.p, keep.data(), n * 4, hipMemcpyHostToDevice, stream));
+      hipLaunchKernelGGL(ivf_compact_rows, dim3((unsigned)n), dim3(128), 0, stream, d_keep.p, (int)n, (int)ld,
+                         (int)M(), vectors_kept ? X.p : (const float*)nullptr, X1.p, codes.p, c1.p, d_list_of.p, l1.p,
+                         d_ids.p, i1.p, ranks.rank.p, r1.p, live1.p);
+      PXG_HIP(hipMemcpyAsync(d_map.p, new_of_old.data(), hw * 4, hipMemcpyHostToDevice, stream));
+      hipLaunchKernelGGL(ivf_remap_slots, dim3((ranks.len + 255) / 256), dim3(256), 0, stream, ranks.rank_slot.p,
+                         ranks.len, d_map.p);
+      PXG_HIP(hipGetLastError());
+    }
+    PXG_HIP(hipStreamSynchronize(stream));
+    if (vectors_kept) std::swap(X, X1);
+    std::swap(codes, c1);
+    std::swap(d_live, live1);
+    std::swap(d_list_of, l1);
+    std::swap(d_ids, i1);
+    std::swap(ranks.rank, r1);
+    cap = nc;
+    std::vector<uint64_t> ids1(n);
+    std::vector<uint8_t> live_h(n, 1);
+    std::vector<uint32_t> lo1(n);
+    by_id.clear();
+    for (size_t i = 0; i < n; ++i) {
+      ids1[i] = ids[keep[i]];
+      lo1[i] = list_of_h[keep[i]];
+      by_id[ids1[i]] = (uint32_t)i;
+    }
+    ids.swap(ids1);
+    live.swap(live_h);
+    list_of_h.swap(lo1);
+    slots.clear();
+    for (size_t i = 0; i < n; ++i) slots.allocate();
+    csr_dirty = true;
+    return reclaimed;
+  }
+
   void remove(uint64_t id) {
     auto it = by_id.find(id);
     if (it == by_id.end()) raise(PXG_ERR_UNKNOWN_ID, "unknown vector id " + std::to_string(id), id);
@@ -1501,62 +1691,164 @@ struct IvfPqIndex {
     csr_dirty = true;
   }
 
+  // The wide search of a trained index over the probes already chosen: all
+  // entries of the probed lists keyed, each query's segment sorted, the
+  // shortlist optionally reranked and sorted again, the first kq emitted.
+  // Returns the number of entries scanned.
+  uint64_t search_wide_trained(const float* Qp, uint64_t nq, const int* probes, int np, uint64_t kq,
+                               uint64_t shortlist, bool rerank, const uint8_t* d_accept, uint64_t* d_oid, float* d_od,
+                               uint32_t* d_oc, Scratch& sc, hipStream_t s, size_t ldo) {
+    std::vector<int> hp((size_t)nq * np);
+    PXG_HIP(hipMemcpyAsync(hp.data(), probes, hp.size() * 4, hipMemcpyDeviceToHost, s));
+    PXG_HIP(hipStreamSynchronize(s));
+    std::vector<uint64_t> tot(nq, 0);
+    uint64_t scanned = 0;
+    for (uint64_t q = 0; q < nq; ++q) {
+      for (int p = 0; p < np; ++p) tot[q] += list_len_h[hp[q * np + p]];
+      scanned += tot[q];
+    }
+    // query groups: keys + sorted keys within 1 GiB, tables within 512 MiB,
+    // sizes within 32 bits (a single query is always taken)
+    const size_t table_bytes = (size_t)np * M() * 256 * 4;
+    const uint64_t key_cap = std::min<uint64_t>((1ull << 30) / 16, (1ull << 32) - 1);
+    const uint64_t qmax = std::max<uint64_t>(1, (512ull << 20) / table_bytes);
+    std::vector<std::pair<uint64_t, uint64_t>> groups;  // [q0, q1)
+    for (uint64_t q0 = 0; q0 < nq;) {
+      uint64_t q1 = q0, keys = 0;
+      while (q1 < nq && q1 - q0 < qmax && (q1 == q0 || keys + tot[q1] <= key_cap)) keys += tot[q1++];
+      if (keys >= (1ull << 32)) config_error("nprobe", (uint64_t)np, "a query's probed lists hold 2^32 entries or more");
+      groups.emplace_back(q0, q1);
+      q0 = q1;
+    }
+    uint64_t max_keys = 0, max_q = 0;
+    for (auto& g : groups) {
+      uint64_t kk = 0;
+      for (uint64_t q = g.first; q < g.second; ++q) kk += tot[q];
+      max_keys = std::max(max_keys, kk);
+      max_q = std::max(max_q, g.second - g.first);
+    }
+    const size_t nk = std::max<uint64_t>(max_keys, 1);
+    uint64_t* keys = (uint64_t*)sc.get(30, nk * 8);
+    uint64_t* sorted = (uint64_t*)sc.get(31, nk * 8);
+    uint32_t* d_be = (uint32_t*)sc.get(32, (3 * max_q + max_q * np) * 4);  // begins, ends, ends2, pofs
+    float* tables = (float*)sc.get(33, max_q * table_bytes);
+    float* omq = (float*)sc.get(34, max_q * np * 4);
+    const size_t temp_bytes = wide_sort_temp_bytes((uint32_t)nk, (uint32_t)max_q);
+    void* temp = sc.get(35, std::max<size_t>(temp_bytes, 1));
+    std::vector<uint32_t> hb(3 * max_q + max_q * np);
+    for (auto& g : groups) {
+      const int gn = (int)(g.second - g.first);
+      uint32_t* begins = hb.data();
+      uint32_t* ends = begins + max_q;
+      uint32_t* pofs = ends + 2 * max_q;
+      uint32_t at = 0;
+      for (int i = 0; i < gn; ++i) {
+        const uint64_t q = g.first + i;
+        begins[i] = at;
+        for (int p = 0; p < np; ++p) {
+          pofs[i * np + p] = at;
+          at += list_len_h[hp[q * np + p]];
+        }
+        ends[i] = at;
+      }
+      PXG_HIP(hipMemcpyAsync(d_be, hb.data(), hb.size() * 4, hipMemcpyHostToDevice, s));
+      const uint32_t* dbeg = d_be;
+      const uint32_t* dend = d_be + max_q;
+      uint32_t* dend2 = d_be + 2 * max_q;
+      const uint32_t* dpofs = d_be + 3 * max_q;
+      const int items = gn * np;
+      hipLaunchKernelGGL(ivf_wide_tables, dim3((unsigned)items), dim3(256), 0, s, Qp, (int)ld, (int)dim, (int)M(),
+                         metric, probes, np, (int)g.first, cents.p, books.p, d_sub_off.p, d_book_off.p, tables, omq);
+      hipLaunchKernelGGL(ivf_wide_keys, dim3((unsigned)items), dim3(256), 0, s, probes, np, (int)g.first, (int)M(),
+                         metric, tables, omq, list_off.p, list_rank.p, list_codes.p, ranks.rank_slot.p, d_accept,
+                         dpofs, keys);
+      PXG_HIP(hipGetLastError());
+      wide_sort(temp, temp_bytes, keys, sorted, at, (uint32_t)gn, dbeg, dend, s);
+      const uint32_t* emit_end = dend;
+      if (rerank) {
+        const uint64_t t = shortlist;
+        hipLaunchKernelGGL(ivf_wide_rerank, dim3((unsigned)((t + 31) / 32), (unsigned)gn), dim3(256), 0, s, sorted,
+                           dbeg, dend, t, (int)g.first, Qp, (int)ld, (int)dim, metric, X.p, ranks.rank_slot.p, keys);
+        hipLaunchKernelGGL(wide_truncate, dim3((unsigned)((gn + 255) / 256)), dim3(256), 0, s, dbeg, dend, gn, t,
+                           dend2);
+        PXG_HIP(hipGetLastError());
+        wide_sort(temp, temp_bytes, keys, sorted, at, (uint32_t)gn, dbeg, dend2, s);
+        emit_end = dend2;
+      } else if (shortlist < kq) {
+        internal_error("IvfPqIndex::search_wide_trained", "shortlist below k");
+      }
+      hipLaunchKernelGGL(wide_emit, dim3((unsigned)((kq + 255) / 256), (unsigned)gn), dim3(256), 0, s, sorted, dbeg,
+                         emit_end, (int)g.first, kq, ranks.rank_slot.p, d_ids.p, d_oid, d_od, d_oc, ldo);
+      PXG_HIP(hipGetLastError());
+      PXG_HIP(hipStreamSynchronize(s));  // the host offsets are rewritten for the next group
+    }
+    return scanned;
+  }
+
   void search_device(const float* d_raw, bool do_prepare, uint64_t nq, uint64_t k, uint64_t nprobe_in,
-                     const uint8_t* d_accept, uint64_t* d_oid, float* d_od, uint32_t* d_oc, Ctx* ctx, hipStream_t s) {
+                     const uint8_t* d_accept, uint64_t* d_oid, float* d_od, uint32_t* d_oc, Scratch& sc,
+                     hipStream_t s, size_t ldo) {
     check_k(k);
     if (nq == 0) return;
-    if (k == 0 || by_id.empty()) {
-      PXG_HIP(hipMemsetAsync(d_oc, 0, nq * 4, s));
-      PXG_HIP(hipStreamSynchronize(s));
-      return;
-    }
+    // at most the live count per query (the probed lists hold no more)
+    const uint64_t kq = std::min<uint64_t>(k, by_id.size());
     refresh(s);
     Timer tm(s);
+    tm.on = tm.on && sc.timing();
     tm.mark(0);
-    float* Qp = (float*)ctx->get(1, nq * ld * 4);
-    float* qb = (float*)ctx->get(2, nq * 4);
-    float* qn = (float*)ctx->get(3, nq * 4);
-    unsigned long long* bad = (unsigned long long*)ctx->get(4, 32);
+    float* Qp = (float*)sc.get(1, nq * ld * 4);
+    float* qb = (float*)sc.get(2, nq * 4);
+    float* qn = (float*)sc.get(3, nq * 4);
+    unsigned long long* bad = (unsigned long long*)sc.get(4, 32);
     int* flag_count = (int*)(bad + 1);
     unsigned long long* scanned_dev = nullptr;
-    PXG_HIP(hipMemsetAsync(bad, 0xFF, 8, s));
+    uint64_t scanned_host = 0;
+    hipLaunchKernelGGL(init_search_flags, dim3(1), dim3(64), 0, s, bad, flag_count);
     hipLaunchKernelGGL(flat_prep_queries, dim3((unsigned)nq), dim3(64), 0, s, d_raw, (int)dim, (int)ld, metric,
                        do_prepare ? 1 : 0, Qp, qb, qn, bad);
     PXG_HIP(hipGetLastError());
     const size_t N = slots.high_water();
-    if (!trained) {
+    if (kq == 0) {
+      hipLaunchKernelGGL(fill_u32, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s, d_oc, (size_t)nq, 0u);
+      PXG_HIP(hipGetLastError());
+    } else if (!trained && kq > EXACT_MERGE_MAXK) {
+      exact_wide_search(Qp, (int)ld, (int)dim, metric, nq, kq, X.p, N, d_live.p, d_accept, ranks.rank.p,
+                        ranks.rank_slot.p, d_ids.p, d_oid, d_od, d_oc, ldo, sc, s);
+    } else if (!trained) {
       // untrained: exact exhaustive scan (ivfpq.rs:1008-1012, 1113-1125)
-      if (k > 1024) config_error("k", k, "the GPU IVF-PQ search supports k up to 1024 per query");
-      int* qlist = (int*)ctx->get(5, nq * 4);
+      int* qlist = (int*)sc.get(5, nq * 4);
       hipLaunchKernelGGL(iota_kernel, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s, qlist, (int)nq,
                          flag_count);
       const int nchunks = (int)((N + EXACT_CH - 1) / EXACT_CH);
-      const int kk = (int)std::min<uint64_t>(k, EXACT_CH);
-      uint64_t* ecand = (uint64_t*)ctx->get(7, (size_t)nq * nchunks * kk * 8);
+      const int kk = (int)std::min<uint64_t>(kq, EXACT_CH);
+      uint64_t* ecand = (uint64_t*)sc.get(7, (size_t)nq * nchunks * kk * 8);
       tm.mark(1);
       hipLaunchKernelGGL(flat_exact_candidates, dim3(std::min<int>((int)nq * nchunks, 4096)), dim3(256), 0, s, qlist,
                          flag_count, nchunks, Qp, (int)ld, (int)dim, metric, X.p, (int)N, d_live.p, d_accept,
-                         ranks.rank.p, (int)k, ecand);
+                         ranks.rank.p, (int)kq, ecand);
       PXG_HIP(hipGetLastError());
       tm.mark(2);
       hipLaunchKernelGGL(flat_merge_exact, dim3((unsigned)nq), dim3(256), 0, s, qlist, flag_count, ecand, nchunks,
-                         (int)k, ranks.rank_slot.p, d_ids.p, d_oid, d_od, d_oc, (uint64_t*)nullptr, (size_t)k);
+                         (int)kq, ranks.rank_slot.p, d_ids.p, d_oid, d_od, d_oc, (uint64_t*)nullptr, ldo);
       PXG_HIP(hipGetLastError());
     } else {
       const int np = (int)std::min<uint64_t>(std::max<uint64_t>(nprobe_in, 1), (uint64_t)std::max(produced, 1));
       const bool rerank = cfg.rerank > 0 && vectors_kept;
-      const uint64_t shortlist = cfg.rerank > 0 ? std::max<uint64_t>(cfg.rerank, k) : k;
-      if (shortlist > IVF_MAX_SHORT)
-        config_error("k", shortlist, "the GPU IVF-PQ shortlist (max(rerank, k)) is limited to 960");
-      const int kk = (int)shortlist;
-      uint64_t* ck = (uint64_t*)ctx->get(8, (size_t)nq * produced * 8);
-      int* probes = (int*)ctx->get(9, (size_t)nq * np * 4);
+      // TopK(max(rerank, k)) of the ADC scores (ivfpq.rs:1060-1064), never
+      // more than the live count
+      const uint64_t shortlist =
+          std::min<uint64_t>(cfg.rerank > 0 ? std::max<uint64_t>(cfg.rerank, kq) : kq, by_id.size());
+      // beyond the block selections, or tables beyond the LDS: sorted segments
+      const bool wide = shortlist > IVF_MAX_SHORT || M() > IVF_MAX_M;
+      const int kk = (int)std::min<uint64_t>(shortlist, IVF_MAX_SHORT);
+      uint64_t* ck = (uint64_t*)sc.get(8, (size_t)nq * produced * 8);
+      int* probes = (int*)sc.get(9, (size_t)nq * np * 4);
       tm.mark(0);
       scanned_dev = (unsigned long long*)(flag_count + 2);
-      PXG_HIP(hipMemsetAsync(scanned_dev, 0, 8, s));
+      hipLaunchKernelGGL(fill_u32, dim3(1), dim3(64), 0, s, (uint32_t*)scanned_dev, (size_t)2, 0u);
       const bool fused_count = np <= 64 && dim <= 2048;
       if (fused_count) {
-        uint64_t* keys = (uint64_t*)ctx->get(13, (size_t)nq * cst * 8);
+        uint64_t* keys = (uint64_t*)sc.get(13, (size_t)nq * cst * 8);
         const dim3 gd((unsigned)((nq + IVF_CQ - 1) / IVF_CQ), (unsigned)((produced + IVF_CW * 64 - 1) / (IVF_CW * 64)));
         hipLaunchKernelGGL(ivf_coarse_dist, gd, dim3(IVF_CW * 64), (size_t)dim * IVF_CQ * 4, s, Qp, (int)ld, (int)dim,
                            (int)nq, cents_t.p, cst, produced, keys);
@@ -1566,13 +1858,13 @@ struct IvfPqIndex {
         // exact top-nprobe by (squared_l2, list) through the flat pipeline
         const float* Qd = Qp;
         if (ld != dim) {
-          float* dq = (float*)ctx->get(11, nq * dim * 4);
+          float* dq = (float*)sc.get(11, nq * dim * 4);
           PXG_HIP(hipMemcpy2DAsync(dq, dim * 4, Qp, ld * 4, dim * 4, nq, hipMemcpyDeviceToDevice, s));
           Qd = dq;
         }
-        uint64_t* cid = (uint64_t*)ctx->get(12, nq * np * 8);
-        float* cdist = (float*)ctx->get(13, nq * np * 4);
-        uint32_t* ccnt = (uint32_t*)ctx->get(14, nq * 4);
+        uint64_t* cid = (uint64_t*)sc.get(12, nq * np * 8);
+        float* cdist = (float*)sc.get(13, nq * np * 4);
+        uint32_t* ccnt = (uint32_t*)sc.get(14, nq * 4);
         CtxLease cl(coarse->pool);
         uint64_t fb = 0;
         CtxScratch csc(cl.c);
@@ -1591,7 +1883,7 @@ struct IvfPqIndex {
       const int W = (int)(dim / M());
       // the register-codebook scans keep two distance tables in LDS (one for
       // cosine): an L2 index with 128 subspaces takes the general scan
-      const bool reg_path = dim <= 128 && dim % M() == 0 && kk <= 64 &&
+      const bool reg_path = !wide && dim <= 128 && dim % M() == 0 && kk <= 64 &&
                             (W == 1 || W == 2 || W == 4 || W == 8 || W == 16 || W == 32) &&
                             (metric == PXG_COSINE || M() <= 64);
       const bool staged16 = reg_path && M() == 16;
@@ -1602,7 +1894,7 @@ struct IvfPqIndex {
         int pg = IVF_PGMAX;
         while (pg > 1 && (int64_t)nq * ((np + pg - 1) / pg) < 512) pg >>= 1;
         const int groups = (np + pg - 1) / pg;
-        uint64_t* cand = (uint64_t*)ctx->get(10, (size_t)nq * groups * IVF_SW * kk * 8);
+        uint64_t* cand = (uint64_t*)sc.get(10, (size_t)nq * groups * IVF_SW * kk * 8);
         const int grid = (int)(nq * groups);
         tm.mark(1);
         // one group per query and no rerank: the scan writes the results
@@ -1610,7 +1902,7 @@ struct IvfPqIndex {
 #define PXG_SCANR(WW, MET)                                                                                          \
   hipLaunchKernelGGL((ivf_scan_reg<WW, MET>), dim3(grid), dim3(IVF_SW * 64), lds, s, Qp, (int)ld, (int)dim,        \
                      (int)M(), probes, np, pg, groups, cents.p, books.p, list_off.p, list_rank.p, list_codes.p,      \
-                     ranks.rank_slot.p, d_accept, kk, cand, (int)k, d_ids.p, fused ? d_oid : nullptr, d_od, d_oc)
+                     ranks.rank_slot.p, d_accept, kk, cand, (int)ldo, d_ids.p, fused ? d_oid : nullptr, d_od, d_oc)
 #define PXG_SCANR_W(MET)                  \
   switch (W) {                            \
     case 1: PXG_SCANR(1, MET); break;     \
@@ -1623,7 +1915,7 @@ struct IvfPqIndex {
 #define PXG_SCAN16(WW, MET)                                                                                         \
   hipLaunchKernelGGL((ivf_scan16<WW, MET>), dim3(grid), dim3(IVF_SW * 64), 0, s, Qp, (int)ld, probes, np, pg, groups, \
                      cents.p, books.p, list_off.p, list_rank.p, list_codes.p, ranks.rank_slot.p, d_accept, kk, cand,     \
-                     (int)k, d_ids.p, fused ? d_oid : nullptr, d_od, d_oc)
+                     (int)ldo, d_ids.p, fused ? d_oid : nullptr, d_od, d_oc)
 #define PXG_SCAN16_W(MET)                 \
   switch (W) {                            \
     case 1: PXG_SCAN16(1, MET); break;    \
@@ -1649,14 +1941,19 @@ struct IvfPqIndex {
         PXG_HIP(hipGetLastError());
         tm.mark(2);
         if (!fused) {
-          hipLaunchKernelGGL(ivf_merge, dim3((unsigned)nq), dim3(256), 0, s, cand, groups * IVF_SW * kk, kk, (int)k,
+          hipLaunchKernelGGL(ivf_merge, dim3((unsigned)nq), dim3(256), 0, s, cand, groups * IVF_SW * kk, kk, (int)ldo,
                              rerank ? 1 : 0, Qp, (int)ld, (int)dim, metric, X.p, ranks.rank_slot.p, d_ids.p, d_oid, d_od,
                              d_oc);
           PXG_HIP(hipGetLastError());
         }
+      } else if (wide) {
+        tm.mark(1);
+        scanned_host = search_wide_trained(Qp, nq, probes, np, kq, shortlist, rerank, d_accept, d_oid, d_od, d_oc, sc,
+                                           s, ldo);
+        scanned_dev = nullptr;
       } else {
       const size_t lds = (size_t)M() * 256 * 4;
-      uint64_t* cand = (uint64_t*)ctx->get(10, (size_t)nq * np * 4 * kk * 8);
+      uint64_t* cand = (uint64_t*)sc.get(10, (size_t)nq * np * 4 * kk * 8);
       const int grid = (int)(nq * np);
       tm.mark(1);
 #define PXG_SCAN(CAPW, MET)                                                                                       \
@@ -1673,7 +1970,7 @@ struct IvfPqIndex {
 #undef PXG_SCAN
       PXG_HIP(hipGetLastError());
       tm.mark(2);
-      hipLaunchKernelGGL(ivf_merge, dim3((unsigned)nq), dim3(256), 0, s, cand, np * 4 * kk, kk, (int)k,
+      hipLaunchKernelGGL(ivf_merge, dim3((unsigned)nq), dim3(256), 0, s, cand, np * 4 * kk, kk, (int)ldo,
                          rerank ? 1 : 0, Qp, (int)ld, (int)dim, metric, X.p, ranks.rank_slot.p, d_ids.p, d_oid, d_od,
                          d_oc);
       PXG_HIP(hipGetLastError());
@@ -1681,12 +1978,12 @@ struct IvfPqIndex {
     }
     // one copy brings back the validation flag and the scanned-entry count
     // (bytes 0-7 and 16-23 of the same scratch block)
-    unsigned long long* tail = ctx->tail_host();
+    unsigned long long* tail = sc.host_words();
     tail[0] = tail[1] = tail[2] = 0;
     PXG_HIP(hipMemcpyAsync(tail, bad, scanned_dev ? 24 : 8, hipMemcpyDeviceToHost, s));
     PXG_HIP(hipStreamSynchronize(s));
     tm.finish();
-    const unsigned long long badv = tail[0], scanned = scanned_dev ? tail[2] : 0;
+    const unsigned long long badv = tail[0], scanned = scanned_dev ? tail[2] : scanned_host;
     g_last_scanned = scanned;
     if (badv != ~0ull) {
       const uint32_t qi = (uint32_t)(badv >> 32), comp = (uint32_t)badv;
@@ -1706,7 +2003,6 @@ void validate_config(const pxg_ivfpq_config& c, uint32_t dim) {
   if (c.training_sample == 0) config_error("training_sample", c.training_sample, "must be at least 1");
   if (c.rerank > 0 && !c.retain_vectors)
     config_error("rerank", c.rerank, "requires retain_vectors, because reranking is against the exact vectors");
-  if (c.subspaces > IVF_MAX_M) config_error("subspaces", c.subspaces, "the GPU distance table holds at most 128 subspaces");
 }
 
 }  // namespace pxg
@@ -1832,6 +2128,14 @@ int pxg_ivfpq_remove(pxg_ivfpq* index, uint64_t id) {
   return pxg::guard([&] {
     std::unique_lock<std::shared_mutex> lk(index->impl.mu);
     index->impl.remove(id);
+  });
+}
+
+int pxg_ivfpq_compact(pxg_ivfpq* index, uint64_t* reclaimed) {
+  return pxg::guard([&] {
+    std::unique_lock<std::shared_mutex> lk(index->impl.mu);
+    const uint64_t r = index->impl.compact();
+    if (reclaimed) *reclaimed = r;
   });
 }
 
@@ -1976,11 +2280,15 @@ int pxg_ivfpq_search(const pxg_ivfpq* index, const float* queries, uint64_t nq, 
                        std::to_string(queries[i * f.dim + bad]) + ")",
                    (uint64_t)bad, i, queries[i * f.dim + bad]);
     }
-    if (k == 0 || f.by_id.empty()) {
+    // at most the live count per query: device rows of kq, copied into the
+    // caller's rows of k
+    const uint64_t kq = std::min<uint64_t>(k, f.by_id.size());
+    if (kq == 0) {
       for (uint64_t i = 0; i < nq; ++i) out_count[i] = 0;
       return;
     }
     pxg::CtxLease ctx(f.pool);
+    pxg::CtxScratch sc(ctx.c);
     hipStream_t s = ctx->stream;
     const size_t N = f.slots.high_water();
     float* d_q = (float*)ctx->get(20, prep.size() * 4);
@@ -1989,13 +2297,13 @@ int pxg_ivfpq_search(const pxg_ivfpq* index, const float* queries, uint64_t nq, 
       d_acc = ctx->get(21, N);
       PXG_HIP(hipMemcpyAsync(d_acc, accept, N, hipMemcpyHostToDevice, s));
     }
-    uint64_t* d_oid = (uint64_t*)ctx->get(22, nq * k * 8);
-    float* d_od = (float*)ctx->get(23, nq * k * 4);
+    uint64_t* d_oid = (uint64_t*)ctx->get(22, nq * kq * 8);
+    float* d_od = (float*)ctx->get(23, nq * kq * 4);
     uint32_t* d_oc = (uint32_t*)ctx->get(24, nq * 4);
     PXG_HIP(hipMemcpyAsync(d_q, prep.data(), prep.size() * 4, hipMemcpyHostToDevice, s));
-    f.search_device(d_q, false, nq, k, nprobe ? nprobe : f.cfg.nprobe, d_acc, d_oid, d_od, d_oc, ctx.c, s);
-    PXG_HIP(hipMemcpyAsync(out_ids, d_oid, nq * k * 8, hipMemcpyDeviceToHost, s));
-    PXG_HIP(hipMemcpyAsync(out_dist, d_od, nq * k * 4, hipMemcpyDeviceToHost, s));
+    f.search_device(d_q, false, nq, kq, nprobe ? nprobe : f.cfg.nprobe, d_acc, d_oid, d_od, d_oc, sc, s, kq);
+    PXG_HIP(hipMemcpy2DAsync(out_ids, k * 8, d_oid, kq * 8, kq * 8, nq, hipMemcpyDeviceToHost, s));
+    PXG_HIP(hipMemcpy2DAsync(out_dist, k * 4, d_od, kq * 4, kq * 4, nq, hipMemcpyDeviceToHost, s));
     PXG_HIP(hipMemcpyAsync(out_count, d_oc, nq * 4, hipMemcpyDeviceToHost, s));
     PXG_HIP(hipStreamSynchronize(s));
   });
@@ -2008,9 +2316,10 @@ int pxg_ivfpq_search_device(const pxg_ivfpq* index, const float* d_queries, uint
     IvfPqIndex& f = const_cast<IvfPqIndex&>(index->impl);
     std::shared_lock<std::shared_mutex> lk(f.mu);
     pxg::CtxLease ctx(f.pool);
+    pxg::CtxScratch sc(ctx.c);
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
     f.search_device(d_queries, true, nq, k, nprobe ? nprobe : f.cfg.nprobe, d_accept, d_out_ids, d_out_dist,
-                    d_out_count, ctx.c, s);
+                    d_out_count, sc, s, k);
     PXG_HIP(hipStreamSynchronize(s));
   });
 }

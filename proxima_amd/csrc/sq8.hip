@@ -42,6 +42,7 @@
 #include "common.hpp"
 #include "device.hpp"
 #include "rank.hpp"
+#include "wide.hpp"
 #include "exact_scan.hpp"
 
 namespace pxg {
@@ -541,6 +542,61 @@ __global__ __launch_bounds__(256) void sq8_exact_candidates(const int* __restric
   }
 }
 
+// Integer-score keys (the exact int32 dot of the codes, as
+// sq8_exact_candidates) of every slot for queries q0 .. q0 + G - 1: grid
+// (ceil(N / 256), G), segment g at g * N.
+__global__ __launch_bounds__(256) void sq8_wide_keys(const int8_t* __restrict__ Qc, int KP,
+                                                     const int8_t* __restrict__ C, int N,
+                                                     const uint8_t* __restrict__ live,
+                                                     const uint8_t* __restrict__ accept,
+                                                     const uint32_t* __restrict__ rank, int q0,
+                                                     uint64_t* __restrict__ keys) {
+  const int slot = blockIdx.x * blockDim.x + threadIdx.x;
+  if (slot >= N) return;
+  const int words = KP / 4;
+  const int* qv = reinterpret_cast<const int*>(Qc + (size_t)(q0 + blockIdx.y) * KP);
+  uint64_t key = KEY_MAX;
+  if (live[slot] && (accept == nullptr || accept[slot])) {
+    const int* xv = reinterpret_cast<const int*>(C + (size_t)slot * KP);
+    int acc = 0;
+    for (int j = 0; j < words; ++j) acc = __builtin_amdgcn_sdot4(qv[j], xv[j], acc, false);
+    key = ((uint64_t)ord_key(-(float)acc) << 32) | rank[slot];
+  }
+  keys[(size_t)blockIdx.y * N + slot] = key;
+}
+
+// asymmetric_inner_product (scalar.rs:313-319) of the first min(t, len) keys
+// of each sorted segment, into the same positions of `keys` (as sq8_rescore).
+__global__ __launch_bounds__(256) void sq8_wide_rescore(const uint64_t* __restrict__ sorted,
+                                                        const uint32_t* __restrict__ begins,
+                                                        const uint32_t* __restrict__ ends, uint64_t t, int q0,
+                                                        const float* __restrict__ Qp, int ld, int dim,
+                                                        const int8_t* __restrict__ C, int KP, int per_dim,
+                                                        const float* __restrict__ mn,
+                                                        const float* __restrict__ scale,
+                                                        const uint32_t* __restrict__ rank_slot,
+                                                        uint64_t* __restrict__ keys) {
+  const int gq = blockIdx.y;
+  const uint64_t len = ends[gq] - begins[gq];
+  const uint64_t take = t < len ? t : len;
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= take) return;
+  const uint64_t key = sorted[begins[gq] + i];
+  uint64_t nk = KEY_MAX;
+  if (key != KEY_MAX) {
+    const uint32_t rk = (uint32_t)key;
+    const uint8_t* code = reinterpret_cast<const uint8_t*>(C + (size_t)rank_slot[rk] * KP);
+    const float* qv = Qp + (size_t)(q0 + gq) * ld;
+    float sum = 0.0f;
+    for (int j = 0; j < dim; ++j) {
+      const int g = per_dim ? j : 0;
+      sum += qv[j] * sq_reconstruct(code[j], 1, mn[g], scale[g]);
+    }
+    nk = ((uint64_t)ord_key(-arm_nan(sum)) << 32) | rk;
+  }
+  keys[begins[gq] + i] = nk;
+}
+
 // Rescore a query's integer top kk with asymmetric_inner_product
 // (scalar.rs:313-319) and keep the best k by (distance, id).
 __global__ __launch_bounds__(256) void sq8_rescore(const uint64_t* __restrict__ okeys,
@@ -909,34 +965,70 @@ struct Sq8Index {
     PXG_HIP(hipStreamSynchronize(stream));
   }
 
+  // max(k, rescore) beyond the block selections: integer keys of every slot,
+  // segmented sort, optional rescoring of the first t and a second sort, the
+  // first kq emitted. t = 0: no rescoring.
+  void search_wide(const int8_t* Qc, const float* Qp, uint64_t nq, uint64_t kq, uint64_t t, const uint8_t* d_accept,
+                   uint64_t* d_oid, float* d_od, uint32_t* d_oc, Scratch& sc, hipStream_t s, size_t ldo) {
+    const size_t N = slots.high_water();
+    const size_t per_query = 2 * N * 8 + 16;
+    size_t G = std::max<size_t>(1, std::min<size_t>((1ull << 30) / per_query, ((1ull << 32) - 1) / N));
+    G = std::min<size_t>(G, nq);
+    uint64_t* keys = (uint64_t*)sc.get(40, G * N * 8);
+    uint64_t* sorted = (uint64_t*)sc.get(41, G * N * 8);
+    uint32_t* offs = (uint32_t*)sc.get(42, (2 * G + 2) * 4);
+    uint32_t* ends2 = offs + G + 1;
+    const size_t temp_bytes = wide_sort_temp_bytes((uint32_t)(G * N), (uint32_t)G);
+    void* temp = sc.get(43, std::max<size_t>(temp_bytes, 1));
+    for (size_t q0 = 0; q0 < nq; q0 += G) {
+      const int gn = (int)std::min<size_t>(G, nq - q0);
+      hipLaunchKernelGGL(sq8_wide_keys, dim3((unsigned)((N + 255) / 256), (unsigned)gn), dim3(256), 0, s, Qc,
+                         (int)KP, (const int8_t*)codes.p, (int)N, d_live.p, d_accept, ranks.rank.p, (int)q0, keys);
+      hipLaunchKernelGGL(wide_offsets, dim3((unsigned)((gn + 256) / 256)), dim3(256), 0, s, offs, gn, (uint32_t)N);
+      PXG_HIP(hipGetLastError());
+      wide_sort(temp, temp_bytes, keys, sorted, (uint32_t)(gn * N), (uint32_t)gn, offs, offs + 1, s);
+      const uint32_t* emit_end = offs + 1;
+      if (t) {
+        hipLaunchKernelGGL(sq8_wide_rescore, dim3((unsigned)((t + 255) / 256), (unsigned)gn), dim3(256), 0, s, sorted,
+                           offs, offs + 1, t, (int)q0, Qp, (int)ld, (int)dim, (const int8_t*)codes.p, (int)KP,
+                           per_dim, d_mn.p, d_scale.p, ranks.rank_slot.p, keys);
+        hipLaunchKernelGGL(wide_truncate, dim3((unsigned)((gn + 255) / 256)), dim3(256), 0, s, offs, offs + 1, gn, t,
+                           ends2);
+        PXG_HIP(hipGetLastError());
+        wide_sort(temp, temp_bytes, keys, sorted, (uint32_t)(gn * N), (uint32_t)gn, offs, ends2, s);
+        emit_end = ends2;
+      }
+      hipLaunchKernelGGL(wide_emit, dim3((unsigned)((kq + 255) / 256), (unsigned)gn), dim3(256), 0, s, sorted, offs,
+                         emit_end, (int)q0, kq, ranks.rank_slot.p, d_ids.p, d_oid, d_od, d_oc, ldo);
+      PXG_HIP(hipGetLastError());
+    }
+  }
+
   // Queries: f32 (prepared + encoded here; rescoring possible) or I8 codes.
   void search_device(const float* d_raw, const int8_t* d_qcodes, uint64_t nq, uint64_t k, uint64_t rescore,
-                     const uint8_t* d_accept, uint64_t* d_oid, float* d_od, uint32_t* d_oc, Ctx* ctx, hipStream_t s,
-                     uint64_t* fallbacks) {
+                     const uint8_t* d_accept, uint64_t* d_oid, float* d_od, uint32_t* d_oc, Scratch& sc,
+                     hipStream_t s, uint64_t* fallbacks, size_t ldo) {
     check_k(k);
     *fallbacks = 0;
     if (nq == 0) return;
     if (!d_raw && rescore) config_error("rescore", rescore, "rescoring needs the f32 queries");
     if (d_raw) require_trained();
-    if (k == 0 || by_id.empty()) {
-      PXG_HIP(hipMemsetAsync(d_oc, 0, nq * 4, s));
-      PXG_HIP(hipStreamSynchronize(s));
-      return;
-    }
-    const uint64_t kk64 = std::max<uint64_t>(k, rescore);
-    if (kk64 > 1024) config_error("k", kk64, "the GPU SQ8 search supports max(k, rescore) up to 1024 per query");
-    const int kk = (int)kk64;
+    // at most the live count per query; the integer candidates are the best
+    // max(k, rescore), also clamped to the live count
+    const uint64_t kq = std::min<uint64_t>(k, by_id.size());
+    const uint64_t kk64 = std::min<uint64_t>(std::max<uint64_t>(kq, rescore), by_id.size());
     Timer tm(s);
+    tm.on = tm.on && sc.timing();
     tm.mark(0);
-    int8_t* Qc = (int8_t*)ctx->get(1, nq * KP);
+    int8_t* Qc = (int8_t*)sc.get(1, nq * KP);
     float* Qp = nullptr;
-    unsigned long long* bad = (unsigned long long*)ctx->get(4, 64);
+    unsigned long long* bad = (unsigned long long*)sc.get(4, 64);
     int* flag_count = (int*)(bad + 1);
+    hipLaunchKernelGGL(init_search_flags, dim3(1), dim3(64), 0, s, bad, flag_count);
     if (d_raw) {
-      Qp = (float*)ctx->get(2, nq * ld * 4);
-      float* qb = (float*)ctx->get(3, nq * 4);
-      float* qn = (float*)ctx->get(5, nq * 4);
-      PXG_HIP(hipMemsetAsync(bad, 0xFF, 8, s));
+      Qp = (float*)sc.get(2, nq * ld * 4);
+      float* qb = (float*)sc.get(3, nq * 4);
+      float* qn = (float*)sc.get(5, nq * 4);
       hipLaunchKernelGGL(flat_prep_queries, dim3((unsigned)nq), dim3(64), 0, s, d_raw, (int)dim, (int)ld, metric, 1,
                          Qp, qb, qn, bad);
       hipLaunchKernelGGL(sq_encode_rows, dim3((unsigned)nq), dim3(64), 0, s, Qp, (int)ld, (int)nq, (int)dim, per_dim,
@@ -950,11 +1042,25 @@ struct Sq8Index {
       PXG_HIP(hipGetLastError());
     }
     const int N = (int)slots.high_water();
+    if (kq == 0 || kk64 > 1024) {
+      if (kq == 0) {
+        hipLaunchKernelGGL(fill_u32, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s, d_oc, (size_t)nq, 0u);
+        PXG_HIP(hipGetLastError());
+      } else {
+        search_wide(Qc, Qp, nq, kq, rescore ? kk64 : 0, d_accept, d_oid, d_od, d_oc, sc, s, ldo);
+      }
+      unsigned long long* tail = sc.host_words();
+      PXG_HIP(hipMemcpyAsync(tail, bad, 8, hipMemcpyDeviceToHost, s));
+      PXG_HIP(hipStreamSynchronize(s));
+      if (d_raw) check_non_finite(tail[0]);
+      tm.finish();
+      return;
+    }
+    const int kk = (int)kk64;
     const int KB = (int)(KP / 32);
-    uint64_t* okeys = (uint64_t*)ctx->get(6, nq * kk * 8);
-    uint32_t* ocount = (uint32_t*)ctx->get(7, nq * 4);
-    int* flag_list = (int*)ctx->get(8, nq * 4);
-    PXG_HIP(hipMemsetAsync(flag_count, 0, 4, s));
+    uint64_t* okeys = (uint64_t*)sc.get(6, nq * kk * 8);
+    uint32_t* ocount = (uint32_t*)sc.get(7, nq * 4);
+    int* flag_list = (int*)sc.get(8, nq * 4);
     // automatic: the MFMA path when stage 1 can give every query >= 4 * kk
     // maxima (two per sampled chunk); smaller indexes take the exact scan
     const int ntiles_all = KB <= SQ_MAX_KB ? (N + sq_rows(KB) - 1) / sq_rows(KB) : 0;
@@ -983,10 +1089,10 @@ struct Sq8Index {
       const int qgroups = (int)((nq + SQ_NW * QT * 32 - 1) / (SQ_NW * QT * 32));
       const int E = nchunks * 2;
       const int cap_c = kk <= 32 ? 1024 : 4096;
-      int* tmax = (int*)ctx->get(9, nq * E * 4);
-      int* thr = (int*)ctx->get(10, nq * 4);
-      int* ccount = (int*)ctx->get(11, nq * 4);
-      uint64_t* cand = (uint64_t*)ctx->get(12, nq * cap_c * 8);
+      int* tmax = (int*)sc.get(9, nq * E * 4);
+      int* thr = (int*)sc.get(10, nq * 4);
+      int* ccount = (int*)sc.get(11, nq * 4);
+      uint64_t* cand = (uint64_t*)sc.get(12, nq * cap_c * 8);
       const dim3 grid((unsigned)((nchunks * qgroups + 7) / 8 * 8));
 #define PXG_SQ_SCAN(KBV, ST)                                                                                        \
   hipLaunchKernelGGL((sq8_mfma_scan<KBV, ST>), grid, dim3((SQ_NW + 1) * 64), 0, s, (const int8_t*)Qc, (int)nq,           \
@@ -1009,7 +1115,8 @@ struct Sq8Index {
       PXG_SQ_SWITCH(true)
       PXG_HIP(hipGetLastError());
       hipLaunchKernelGGL(sq8_thresholds, dim3((unsigned)nq), dim3(256), 0, s, (const int*)tmax, E, kk, thr);
-      PXG_HIP(hipMemsetAsync(ccount, 0, nq * 4, s));
+      hipLaunchKernelGGL(fill_u32, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s, (uint32_t*)ccount, (size_t)nq,
+                         0u);
       tm.mark(1);
       PXG_SQ_SWITCH(false)
 #undef PXG_SQ_SWITCH
@@ -1020,7 +1127,7 @@ struct Sq8Index {
                          (const uint64_t*)cand, cap_c, kk, okeys, ocount, flag_list, flag_count);
       PXG_HIP(hipGetLastError());
       // bad (8 bytes) and flag_count (the int after it) in one copy
-      unsigned long long* tail = ctx->tail_host();
+      unsigned long long* tail = sc.host_words();
       PXG_HIP(hipMemcpyAsync(tail, bad, 16, hipMemcpyDeviceToHost, s));
       PXG_HIP(hipStreamSynchronize(s));
       if (d_raw) check_non_finite(tail[0]);
@@ -1037,7 +1144,7 @@ struct Sq8Index {
       if (mfma) tm.mark(3);
       const int nchunks = (N + EXACT_CH - 1) / EXACT_CH;
       const int kke = std::min(kk, EXACT_CH);
-      uint64_t* ecand = (uint64_t*)ctx->get(13, (size_t)nflag * nchunks * kke * 8);
+      uint64_t* ecand = (uint64_t*)sc.get(13, (size_t)nflag * nchunks * kke * 8);
       hipLaunchKernelGGL(sq8_exact_candidates, dim3((unsigned)std::min<int64_t>((int64_t)nflag * nchunks, 4096)),
                          dim3(256), 0, s, (const int*)flag_list, (const int*)flag_count, nchunks, (const int8_t*)Qc,
                          (int)KP, (const int8_t*)codes.p, N, d_live.p, d_accept, ranks.rank.p, kk, ecand);
@@ -1052,15 +1159,15 @@ struct Sq8Index {
       int P = 1;
       while (P < kk) P <<= 1;
       hipLaunchKernelGGL(sq8_rescore, dim3((unsigned)nq), dim3(256), (size_t)P * 8, s, (const uint64_t*)okeys,
-                         (const uint32_t*)ocount, kk, (int)k, (const float*)Qp, (int)ld, (int)dim,
+                         (const uint32_t*)ocount, kk, (int)ldo, (const float*)Qp, (int)ld, (int)dim,
                          (const int8_t*)codes.p, (int)KP, per_dim, d_mn.p, d_scale.p, ranks.rank_slot.p, d_ids.p, d_oid,
                          d_od, d_oc);
     } else {
       hipLaunchKernelGGL(sq8_emit, dim3((unsigned)nq), dim3(64), 0, s, (const uint64_t*)okeys,
-                         (const uint32_t*)ocount, kk, (int)k, ranks.rank_slot.p, d_ids.p, d_oid, d_od, d_oc);
+                         (const uint32_t*)ocount, kk, (int)ldo, ranks.rank_slot.p, d_ids.p, d_oid, d_od, d_oc);
     }
     PXG_HIP(hipGetLastError());
-    unsigned long long* tail = ctx->tail_host();
+    unsigned long long* tail = sc.host_words();
     if (d_raw && !mfma) PXG_HIP(hipMemcpyAsync(tail, bad, 8, hipMemcpyDeviceToHost, s));
     PXG_HIP(hipStreamSynchronize(s));
     if (d_raw && !mfma) check_non_finite(tail[0]);
@@ -1346,6 +1453,7 @@ static int sq8_search_host(const pxg_sq8* index, const float* queries, const int
     std::shared_lock<std::shared_mutex> lk(f.mu);
     if (nq == 0) return;
     pxg::CtxLease ctx(f.pool);
+    pxg::CtxScratch sc(ctx.c);
     hipStream_t s = ctx->stream;
     const size_t N = f.slots.high_water();
     uint8_t* d_acc = nullptr;
@@ -1353,7 +1461,10 @@ static int sq8_search_host(const pxg_sq8* index, const float* queries, const int
       d_acc = ctx->get(21, N);
       PXG_HIP(hipMemcpyAsync(d_acc, accept, N, hipMemcpyHostToDevice, s));
     }
-    const size_t kk = std::max<size_t>(k, 1);
+    // at most the live count per query: device rows of kq, copied into the
+    // caller's rows of k
+    const uint64_t kq = std::min<uint64_t>(k, f.by_id.size());
+    const size_t kk = std::max<size_t>(kq, 1);
     uint64_t* d_oid = (uint64_t*)ctx->get(22, nq * kk * 8);
     float* d_od = (float*)ctx->get(23, nq * kk * 4);
     uint32_t* d_oc = (uint32_t*)ctx->get(24, nq * 4);
@@ -1367,10 +1478,10 @@ static int sq8_search_host(const pxg_sq8* index, const float* queries, const int
       PXG_HIP(hipMemcpyAsync(d_qc, qcodes, nq * f.dim, hipMemcpyHostToDevice, s));
     }
     uint64_t fb = 0;
-    f.search_device(d_q, d_qc, nq, k, rescore, d_acc, d_oid, d_od, d_oc, ctx.c, s, &fb);
-    if (k) {
-      PXG_HIP(hipMemcpyAsync(out_ids, d_oid, nq * k * 8, hipMemcpyDeviceToHost, s));
-      PXG_HIP(hipMemcpyAsync(out_dist, d_od, nq * k * 4, hipMemcpyDeviceToHost, s));
+    f.search_device(d_q, d_qc, nq, kq, rescore, d_acc, d_oid, d_od, d_oc, sc, s, &fb, kk);
+    if (kq) {
+      PXG_HIP(hipMemcpy2DAsync(out_ids, k * 8, d_oid, kk * 8, kq * 8, nq, hipMemcpyDeviceToHost, s));
+      PXG_HIP(hipMemcpy2DAsync(out_dist, k * 4, d_od, kk * 4, kq * 4, nq, hipMemcpyDeviceToHost, s));
     }
     PXG_HIP(hipMemcpyAsync(out_count, d_oc, nq * 4, hipMemcpyDeviceToHost, s));
     PXG_HIP(hipStreamSynchronize(s));
@@ -1395,9 +1506,10 @@ int pxg_sq8_search_device(const pxg_sq8* index, const float* d_queries, uint64_t
     Sq8Index& f = const_cast<Sq8Index&>(index->impl);
     std::shared_lock<std::shared_mutex> lk(f.mu);
     pxg::CtxLease ctx(f.pool);
+    pxg::CtxScratch sc(ctx.c);
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
     uint64_t fb = 0;
-    f.search_device(d_queries, nullptr, nq, k, rescore, d_accept, d_out_ids, d_out_dist, d_out_count, ctx.c, s, &fb);
+    f.search_device(d_queries, nullptr, nq, k, rescore, d_accept, d_out_ids, d_out_dist, d_out_count, sc, s, &fb, k);
     PXG_HIP(hipStreamSynchronize(s));
     pxg::g_sq8_fallbacks = fb;
   });

@@ -267,8 +267,8 @@ def test_sq8_errors_and_edges(gpu):
         idx.insert_batch(np.arange(500, 503, dtype=np.uint64), bad)
     assert e.value.index == 4 and len(idx) == 100  # all-or-nothing
     assert idx.search(x[0], 0) == []
-    with pytest.raises(px.Configuration):
-        idx.search_batch(x[:2], 10, rescore=2000)
+    # max(k, rescore) beyond the index is clamped to its live count
+    assert list(idx.search_batch(x[:2], 10, rescore=2000)[2]) == [10, 10]
     with pytest.raises(px.UnknownId):
         idx.remove(777)
     assert len(idx.search(x[0], 1000)) == 100  # k above len
