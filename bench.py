@@ -10,7 +10,10 @@ headline value; k=100 reported alongside).
 Prints ONE JSON line with the contract fields plus `roofline` (dominant
 kernel: the FP32-MFMA candidate GEMM, timed with HIP events on its own stream)
 and `cpu_baseline` (the oracle's restatement of the reference CPU path on a
-bounded sample of the same workload, on this host's cores).
+bounded sample of the same workload, on this host's cores; one-thread figures
+beside it). Every leg also reports the host-pointer path (PCIe both ways) and
+single-query latency (mean and p95, bench.rs:381-409); the sub-objects `c1`,
+`ivfpq`, `sq8`, `kmeans` and `fixture` carry the other workloads.
 """
 import argparse
 import json
@@ -49,6 +52,124 @@ def load_traffic(name):
             return json.load(f).get(name)
     except (OSError, ValueError):
         return None
+
+
+def cpu_model():
+    """The host CPU's model string (from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def host_path(search_batch, batches_host, k, reps=3):
+    """The host-pointer entry point a VectorIndex drop-in calls: queries copied
+    over PCIe, results copied back, per batch (median of `reps` passes over the
+    batches after one untimed pass)."""
+    for b in batches_host:
+        search_batch(b, k)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        for b in batches_host:
+            search_batch(b, k)
+        times.append((time.perf_counter() - t0) / len(batches_host))
+    t = float(np.median(times))
+    nq = batches_host[0].shape[0]
+    return {"ms_per_batch": round(t * 1e3, 4), "queries_per_s": round(nq / t, 2), "batch": nq,
+            "note": "host-pointer search: host queries in, host results out (PCIe both ways)"}
+
+
+def latency_batch1(search_one, queries_host, k, repeats=200):
+    """bench.rs:381-409: one untimed warm pass, then `repeats` single-query
+    searches through the host-pointer entry point; mean and p95 (index
+    len * 95 / 100 of the sorted samples)."""
+    m = min(repeats, queries_host.shape[0])
+    for i in range(m):
+        search_one(queries_host[i], k)
+    samples = []
+    for i in range(m):
+        t0 = time.perf_counter()
+        search_one(queries_host[i], k)
+        samples.append(time.perf_counter() - t0)
+    samples.sort()
+    return {"mean_us": round(1e6 * float(np.mean(samples)), 2), "p95_us": round(1e6 * samples[m * 95 // 100], 2),
+            "samples": m, "note": "single queries, host pointers, after one untimed pass"}
+
+
+def bench_c1(args, torch, px, dev):
+    """Flat exact search, Euclidean, k=10: 100,000 x 128 f32 from a mixture of
+    100 Gaussian clusters (centres N(0,1), sigma 0.15); 1,000 queries drawn
+    fresh from the same mixture, searched as one batch of 1,000."""
+    n, dim, nq, k = 100_000, 128, 1000, 10
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed + 3)
+    centres = torch.randn((100, dim), generator=g, device=dev)
+    x = (centres[torch.arange(n, device=dev) % 100] + 0.15 * torch.randn((n, dim), generator=g, device=dev)).contiguous()
+    qc = torch.randint(0, 100, (nq,), generator=g, device=dev)
+    q = (centres[qc] + 0.15 * torch.randn((nq, dim), generator=g, device=dev)).contiguous()
+    ids = np.arange(n, dtype=np.uint64)
+    idx = px.FlatIndex(px.VectorSpace(dim, px.Metric.EUCLIDEAN), n)
+    idx.insert_device(ids, x)
+    oi = torch.empty((nq, k), dtype=torch.int64, device=dev)
+    od = torch.empty((nq, k), dtype=torch.float32, device=dev)
+    oc = torch.empty((nq,), dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    for _ in range(5):
+        idx.search_device(q, k, oi, od, oc, stream=stream)
+    torch.cuda.synchronize()
+    steps = args.c1_steps
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        idx.search_device(q, k, oi, od, oc, stream=stream)
+    torch.cuda.synchronize()
+    step_s = (time.perf_counter() - t0) / steps
+    px.set_profiling(True)
+    stages = []
+    for _ in range(steps):
+        idx.search_device(q, k, oi, od, oc, stream=stream)
+        stages.append(px.last_timings())
+    px.set_profiling(False)
+    cand_ms = float(np.mean([t["candidates_ms"] for t in stages]))
+    tflops = 2.0 * n * dim * nq / (cand_ms * 1e-3) / 1e12
+    qh = q.cpu().numpy()
+    log(f"[bench] c1: {step_s * 1e3:.3f} ms/batch = {nq / step_s:.0f} QPS; candidate GEMM {cand_ms:.3f} ms = "
+        f"{tflops:.1f} TFLOP/s")
+    out = {"value": round(nq / step_s, 2), "unit": "queries/s", "ms_per_step": round(step_s * 1e3, 4), "steps": steps,
+           "config": {"workload": "flat exact search, Euclidean, 100k x 128 f32 (100 Gaussian clusters, sigma 0.15), "
+                                  "1,000 queries in one batch, k=10", "n": n, "dim": dim, "batch": nq, "k": k},
+           "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(tflops / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": None,
+                        "kernel": "flat_mfma_candidates", "ms_per_launch": round(cand_ms, 4)},
+           "stage_ms": {key: round(float(np.mean([t[key] for t in stages])), 4) for key in stages[0]},
+           "host_path": host_path(idx.search_batch, [qh], k),
+           "latency_batch1": latency_batch1(idx.search_all, qh, k)}
+    if not args.no_cpu:
+        from oracle import oracle as orc
+        xh = x.cpu().numpy()
+        t0 = time.perf_counter()
+        wi, wd, wc = orc.flat_search(xh, ids, orc.EUCLIDEAN, qh, k, threads=args.cpu_threads)
+        cpu_mt = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        orc.flat_search(xh, ids, orc.EUCLIDEAN, qh, k, threads=1)
+        cpu_1 = time.perf_counter() - t0
+        gi, gd, gc = idx.search_batch(qh, k)
+        same = int(sum(np.array_equal(gi[i], wi[i]) and np.array_equal(gd[i].view(np.uint32), wd[i].view(np.uint32))
+                       for i in range(nq)))
+        out["cpu_baseline"] = {"value": round(nq / cpu_mt, 2), "unit": "queries/s", "cores": args.cpu_threads,
+                               "kind": "port", "sample": f"the whole workload (all {nq} queries over 100k x 128), "
+                                                         f"oracle FlatIndex::search restatement, {cpu_mt:.2f}s"}
+        out["cpu_baseline_1core"] = {"value": round(nq / cpu_1, 2), "unit": "queries/s", "cores": 1, "kind": "port",
+                                     "sample": f"the whole workload on one thread, {cpu_1:.2f}s"}
+        out["parity_sample"] = {"queries": nq, "bit_exact": same}
+        log(f"[bench] c1 CPU {nq / cpu_mt:.0f} QPS ({args.cpu_threads} threads), {nq / cpu_1:.0f} QPS (1 thread); "
+            f"GPU/oracle bit-exact {same}/{nq}")
+    del idx, x
+    return out
 
 
 def bench_ivfpq(args, torch, px, dev):
@@ -113,13 +234,36 @@ def bench_ivfpq(args, torch, px, dev):
     m = 200
     flat = px.FlatIndex(px.VectorSpace(dim, px.Metric.EUCLIDEAN), n)
     flat.insert_device(ids, x)
-    del x
-    torch.cuda.empty_cache()
     qh = queries.cpu().numpy()
     ti, _, _ = flat.search_batch(qh[:m], k)
     gi, gd, gc = idx.search_batch(qh[:m], k)
     recall = float(np.mean([len(set(ti[i].tolist()) & set(gi[i, :gc[i]].tolist())) / k for i in range(m)]))
     del flat
+    # the same trained parts with an exact rerank of the best 100 ADC
+    # candidates (IvfPqConfig::with_rerank, ivfpq.rs:1094-1109)
+    rr = 100
+    cents_h, books_h, codes_h, list_of_h = idx.parts()
+    idx_rr = px.IvfPqIndex(px.VectorSpace(dim, px.Metric.EUCLIDEAN),
+                           px.IvfPqConfig(4096, 16).with_nprobe(nprobe).with_rerank(rr).with_train_threshold(1 << 63))
+    idx_rr.insert_device(ids, x)
+    idx_rr.load_trained(cents_h, books_h, codes_h, list_of_h)
+    del x
+    torch.cuda.empty_cache()
+    for s_ in range(3):
+        idx_rr.search_device(batches[s_ % nb], k, oi, od, oc, stream=stream)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s_ in range(args.ivf_steps):
+        idx_rr.search_device(batches[s_ % nb], k, oi, od, oc, stream=stream)
+    torch.cuda.synchronize()
+    rr_step = (time.perf_counter() - t0) / args.ivf_steps
+    ri, _, rc = idx_rr.search_batch(qh[:m], k)
+    recall_rr = float(np.mean([len(set(ti[i].tolist()) & set(ri[i, :rc[i]].tolist())) / k for i in range(m)]))
+    del idx_rr
+    torch.cuda.empty_cache()
+    log(f"[bench] ivfpq rerank {rr}: {rr_step * 1e3:.3f} ms/step = {B / rr_step:.0f} QPS, recall@10 {recall_rr:.4f}")
+    host = host_path(idx.search_batch, [qh[i * B:(i + 1) * B] for i in range(3)], k)
+    lat = latency_batch1(idx.search_all, qh, k)
     out = {"value": round(B / step_s, 2), "unit": "queries/s", "ms_per_step": round(step_s * 1e3, 4),
            "steps": args.ivf_steps,
            "config": {"workload": "IVF-PQ search, Euclidean, 10M x 128 f32, nlist 4096, PQ 16x256, nprobe 32, "
@@ -129,10 +273,14 @@ def bench_ivfpq(args, torch, px, dev):
                         "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": load_traffic("ivf_scan")},
            "kernel": "ivf_scan", "scanned_entries_per_launch": float(np.mean(scanned)),
            "stage_ms": {key: round(float(np.mean([t[key] for t in stages])), 4) for key in stages[0]},
-           "train_s": round(train_s, 2), "training_report": rep._asdict(), "recall_at_10_vs_exact": round(recall, 4)}
+           "train_s": round(train_s, 2), "training_report": rep._asdict(), "recall_at_10_vs_exact": round(recall, 4),
+           "rerank100": {"value": round(B / rr_step, 2), "unit": "queries/s", "ms_per_step": round(rr_step * 1e3, 4),
+                         "recall_at_10_vs_exact": round(recall_rr, 4),
+                         "note": "same trained parts, exact rerank of the best 100 ADC candidates per query"},
+           "host_path": host, "latency_batch1": lat}
     if not args.no_cpu:
         from oracle import oracle as orc
-        cents, books, codes, list_of = idx.parts()
+        cents, books, codes, list_of = cents_h, books_h, codes_h, list_of_h
         mq = args.queries
         log(f"[bench] ivfpq CPU baseline: oracle IVF-PQ search, {mq} queries, {args.cpu_threads} threads")
         t0 = time.perf_counter()
@@ -146,8 +294,16 @@ def bench_ivfpq(args, torch, px, dev):
                                "kind": "port", "sample": f"all {mq} queries, oracle IvfPqIndex::search restatement on "
                                                          f"the GPU-trained parts, {args.cpu_threads} threads, "
                                                          f"{cpu_s:.2f}s (includes its O(n) list build)"}
+        m1 = args.ivf_cpu1_sample
+        t0 = time.perf_counter()
+        orc.ivf_search(0, cents, books, codes, list_of, ids, qh[:m1], k, nprobe, 16, threads=1)
+        cpu_1 = time.perf_counter() - t0
+        out["cpu_baseline_1core"] = {"value": round(m1 / cpu_1, 2), "unit": "queries/s", "cores": 1, "kind": "port",
+                                     "sample": f"{m1} queries on one thread, {cpu_1:.2f}s (includes its O(n) list "
+                                               f"build)"}
         out["parity_sample"] = {"queries": mq, "bit_exact": same}
-        log(f"[bench] ivfpq CPU {mq / cpu_s:.1f} QPS; GPU/oracle bit-exact on {same}/{mq}")
+        log(f"[bench] ivfpq CPU {mq / cpu_s:.1f} QPS ({args.cpu_threads} threads), {m1 / cpu_1:.1f} QPS (1 thread); "
+            f"GPU/oracle bit-exact on {same}/{mq}")
     return out
 
 
@@ -208,6 +364,8 @@ def bench_sq8(args, torch, px, dev):
     recall = float(np.mean([len(set(ti[i].tolist()) & set(gi[i, :gc[i]].tolist())) / k for i in range(m)]))
     ri, _, rc = idx.search_batch(qh[:m], k, rescore=100)
     recall_rs = float(np.mean([len(set(ti[i].tolist()) & set(ri[i, :rc[i]].tolist())) / k for i in range(m)]))
+    host = host_path(idx.search_batch, [qh[i * B:(i + 1) * B] for i in range(3)], k)
+    lat = latency_batch1(idx.search_all, qh, k)
     x_host = None if args.no_cpu else x.cpu().numpy()
     del x
     torch.cuda.empty_cache()
@@ -219,7 +377,8 @@ def bench_sq8(args, torch, px, dev):
                         "frac": round(tops / PEAK_INT8_MFMA_TOPS, 4), "traffic": load_traffic("sq8_mfma_scan")},
            "kernel": "sq8_mfma_scan (stage 2)", "fallback_queries": fallbacks,
            "stage_ms": {key: round(float(np.mean([t[key] for t in stages])), 4) for key in stages[0]},
-           "recall_at_10_vs_f32_ip": round(recall, 4), "recall_at_10_rescore100": round(recall_rs, 4)}
+           "recall_at_10_vs_f32_ip": round(recall, 4), "recall_at_10_rescore100": round(recall_rs, 4),
+           "host_path": host, "latency_batch1": lat}
     if not args.no_cpu:
         from oracle import oracle as orc
         mn, sc, inv, _ = orc.sq_train(x_host[:100_000], True)
@@ -240,8 +399,16 @@ def bench_sq8(args, torch, px, dev):
         out["cpu_baseline"] = {"value": round(mq / cpu_s, 3), "unit": "queries/s", "cores": args.cpu_threads,
                                "kind": "port", "sample": f"{mq} queries, each a full 10M x 96 integer scan, oracle "
                                                          f"SQ8 restatement, {args.cpu_threads} threads, {cpu_s:.2f}s"}
+        m1 = args.sq8_cpu1_sample
+        t0 = time.perf_counter()
+        orc.sq8_search(codes, ids, qc[:m1], k, threads=1)
+        cpu_1 = time.perf_counter() - t0
+        out["cpu_baseline_1core"] = {"value": round(m1 / cpu_1, 3), "unit": "queries/s", "cores": 1, "kind": "port",
+                                     "sample": f"{m1} queries on one thread, each a full 10M x 96 integer scan, "
+                                               f"{cpu_1:.2f}s"}
         out["parity_sample"] = {"queries": mq, "bit_exact": same, "ranges_bit_exact": ranges_same}
-        log(f"[bench] sq8 CPU {mq / cpu_s:.2f} QPS; GPU/oracle bit-exact on {same}/{mq}; ranges equal {ranges_same}")
+        log(f"[bench] sq8 CPU {mq / cpu_s:.2f} QPS ({args.cpu_threads} threads), {m1 / cpu_1:.2f} QPS (1 thread); "
+            f"GPU/oracle bit-exact on {same}/{mq}; ranges equal {ranges_same}")
     return out
 
 
@@ -310,19 +477,30 @@ def bench_kmeans(args, torch, px, dev):
         orc.kmeans_assign(sample, init)
         cpu_s = time.perf_counter() - t0
         cpu_iter = cpu_s * n / ns
+        nmt = ns * args.cpu_threads // 2
+        sample_mt = x[:nmt].cpu().numpy()
+        t0 = time.perf_counter()
+        orc.kmeans_assign(sample_mt, init, threads=args.cpu_threads)
+        cpu_mt = time.perf_counter() - t0
+        cpu_iter_mt = cpu_mt * n / nmt
         # full-size parity of the assignment pass on a slice: GPU kernel vs oracle, final centroids
         m = 4096
         ch = cents.cpu().numpy()
         ga, gd = px.kmeans_assign(x[:m].cpu().numpy(), ch)
         wa, wd = orc.kmeans_assign(x[:m].cpu().numpy(), ch)
         same = int(np.sum((ga == wa) & (gd.view(np.uint32) == wd.view(np.uint32))))
-        out["cpu_baseline"] = {"value": round(1.0 / cpu_iter, 6), "unit": "Lloyd iterations/s", "cores": 1,
-                               "kind": "port", "sample": f"the assignment pass of one Lloyd iteration (kmeans.rs:90-97 "
-                                                         f"restatement, single thread as the reference; the O(n d) "
-                                                         f"update is left out) on {ns} of the {n} points against the "
-                                                         f"{K} seeds: {cpu_s:.2f}s, scaled by n/{ns}"}
+        out["cpu_baseline"] = {"value": round(1.0 / cpu_iter_mt, 6), "unit": "Lloyd iterations/s",
+                               "cores": args.cpu_threads, "kind": "port",
+                               "sample": f"the assignment pass of one Lloyd iteration (kmeans.rs:90-97 restatement; "
+                                         f"the O(n d) update is left out) on {nmt} of the {n} points against the {K} "
+                                         f"seeds, points split over {args.cpu_threads} threads: {cpu_mt:.2f}s, scaled "
+                                         f"by n/{nmt}"}
+        out["cpu_baseline_1core"] = {"value": round(1.0 / cpu_iter, 6), "unit": "Lloyd iterations/s", "cores": 1,
+                                     "kind": "port", "sample": f"the same pass on {ns} points, one thread as the "
+                                                               f"reference: {cpu_s:.2f}s, scaled by n/{ns}"}
         out["parity_sample"] = {"points": m, "assignments_and_distances_bit_exact": same}
-        log(f"[bench] kmeans CPU {cpu_iter:.1f} s per full iteration (1 core); assignment parity {same}/{m}")
+        log(f"[bench] kmeans CPU {cpu_iter:.1f} s per full iteration (1 core), {cpu_iter_mt:.1f} s "
+            f"({args.cpu_threads} threads); assignment parity {same}/{m}")
     return out
 
 
@@ -363,7 +541,8 @@ def bench_fixture(args, torch, px, dev):
         out["cpu_baseline"] = {"value": round(ns * dim * 4 / cpu_s / 2**20, 1), "unit": "MiB/s of f32 generated",
                                "cores": 1, "kind": "port",
                                "sample": f"oracle fixture_generate restatement, {ns} x {dim} points, 1 thread, "
-                                         f"{cpu_s:.2f}s"}
+                                         f"{cpu_s:.2f}s (the reference draws every value from one sequential "
+                                         f"ChaCha8 stream, so its CPU path has no multi-thread form)"}
         out["parity"] = {"points": ns, "bit_identical_fraction": round(same, 6), "max_abs_diff": worst}
         log(f"[bench] fixture CPU {ns * dim * 4 / cpu_s / 2**20:.1f} MiB/s (1 core); bit-identical {same:.6f} of "
             f"the first {ns} points, max |diff| {worst:.2e}")
@@ -394,6 +573,12 @@ def main():
     ap.add_argument("--sq8-n", type=int, default=10_000_000)
     ap.add_argument("--sq8-steps", type=int, default=20)
     ap.add_argument("--sq8-cpu-sample", type=int, default=2048)
+    ap.add_argument("--sq8-cpu1-sample", type=int, default=32)
+    ap.add_argument("--ivf-cpu1-sample", type=int, default=1000)
+    ap.add_argument("--cpu1-sample", type=int, default=32, help="queries of the one-thread C2 CPU baseline")
+    ap.add_argument("--skip-c1", action="store_true")
+    ap.add_argument("--c1-only", action="store_true", help="run only the 100k x 128 flat leg (prints its JSON object)")
+    ap.add_argument("--c1-steps", type=int, default=50)
     ap.add_argument("--skip-kmeans", action="store_true")
     ap.add_argument("--kmeans-only", action="store_true", help="run only the k-means leg (prints its JSON object)")
     ap.add_argument("--km-n", type=int, default=2_000_000)
@@ -416,6 +601,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.c1_only:
+        print(json.dumps(bench_c1(args, torch, px, dev)), flush=True)
+        return
     if args.ivf_only:
         print(json.dumps(bench_ivfpq(args, torch, px, dev)), flush=True)
         return
@@ -496,7 +684,37 @@ def main():
     step100, stages100, fb100 = run(k2, max(5, args.steps // 2), 1, prof=True)
     log(f"[bench] k=100: {step100 * 1e3:.3f} ms/step")
 
+    # the partial last batch of the 10,000 queries (9 x 1024 + 784)
+    tail = queries[nb * B:]
+    tail_info = None
+    if tail.shape[0]:
+        nt = tail.shape[0]
+        toi = torch.empty((nt, args.k), dtype=torch.int64, device=dev)
+        tod = torch.empty((nt, args.k), dtype=torch.float32, device=dev)
+        toc = torch.empty((nt,), dtype=torch.int32, device=dev)
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        idx.search_device(tail, args.k, toi, tod, toc, stream=stream)
+        torch.cuda.synchronize()
+        reps = 5
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            idx.search_device(tail, args.k, toi, tod, toc, stream=stream)
+        torch.cuda.synchronize()
+        tail_s = (time.perf_counter() - t0) / reps
+        all_s = nb * step_s + tail_s
+        tail_info = {"queries": nt, "ms": round(tail_s * 1e3, 4),
+                     "all_queries_per_s": round(args.queries / all_s, 2),
+                     "note": f"{nb} full batches at ms_per_step plus this tail: the whole {args.queries}-query set"}
+        log(f"[bench] tail batch of {nt}: {tail_s * 1e3:.3f} ms; all {args.queries} queries at "
+            f"{args.queries / all_s:.0f} QPS")
+    qhost = queries.cpu().numpy()
+    host = host_path(idx.search_batch, [qhost[i * B:(i + 1) * B] for i in range(2)], args.k, reps=2)
+    lat = latency_batch1(idx.search_all, qhost, args.k, repeats=100)
+    log(f"[bench] host path {host['ms_per_batch']} ms/batch; batch-1 latency mean {lat['mean_us']} us, "
+        f"p95 {lat['p95_us']} us")
+
     cpu = None
+    cpu1 = None
     parity = None
     if not args.no_cpu:
         from oracle import oracle as orc
@@ -513,6 +731,12 @@ def main():
         cpu = {"value": round(m / cpu_s, 3), "unit": "queries/s", "cores": args.cpu_threads, "kind": "port",
                "sample": f"{m} queries of the same workload (each a full 1M x 768 exact scan), oracle "
                          f"FlatIndex::search restatement, {args.cpu_threads} host threads, {cpu_s:.2f}s"}
+        m1 = min(args.cpu1_sample, m)
+        t0 = time.perf_counter()
+        orc.flat_search(xp, ids, orc.COSINE, qp[:m1], args.k, threads=1)
+        cpu_1 = time.perf_counter() - t0
+        cpu1 = {"value": round(m1 / cpu_1, 3), "unit": "queries/s", "cores": 1, "kind": "port",
+                "sample": f"{m1} queries on one thread (the reference's single-threaded scan), {cpu_1:.2f}s"}
         # parity of the GPU results on the same sample, full size
         gi, gd, gc = idx.search_batch(qh, args.k)
         same = int(sum(np.array_equal(gi[i], wi[i]) and np.array_equal(gd[i].view(np.uint32), wd[i].view(np.uint32))
@@ -522,6 +746,10 @@ def main():
 
     del idx
     torch.cuda.empty_cache()
+    c1 = None
+    if not args.skip_c1:
+        c1 = bench_c1(args, torch, px, dev)
+        torch.cuda.empty_cache()
     ivf = None
     if not args.skip_ivfpq:
         ivf = bench_ivfpq(args, torch, px, dev)
@@ -557,6 +785,8 @@ def main():
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
                      "traffic": load_traffic("flat_mfma_candidates")},
         "cpu_baseline": cpu,
+        "cpu_baseline_1core": cpu1,
+        "host": {"cpu_model": cpu_model(), "cpu_count": os.cpu_count(), "cpu_threads_used": args.cpu_threads},
         "kernel": "flat_mfma_candidates",
         "stage_ms": stage_mean,
         "fallback_queries": fb,
@@ -564,6 +794,10 @@ def main():
                  "candidates_ms": round(float(np.mean([s["candidates_ms"] for s in stages100])), 4),
                  "fallback_queries": fb100},
         "parity_sample": parity,
+        "tail_batch": tail_info,
+        "host_path": host,
+        "latency_batch1": lat,
+        "c1": c1,
         "ivfpq": ivf,
         "sq8": sq8,
         "kmeans": km,

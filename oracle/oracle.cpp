@@ -898,6 +898,21 @@ void orc_kmeans_assign(const float* pts, size_t n, size_t dim, const float* cent
   }
 }
 
+// The same assignment pass with the points split across host threads (each
+// point's nearest() is independent, so the results are identical).
+void orc_kmeans_assign_mt(const float* pts, size_t n, size_t dim, const float* cents, size_t k, uint32_t* assign,
+                          float* dist, int threads) {
+  if (threads < 1) threads = 1;
+  std::vector<std::thread> pool;
+  const size_t per = (n + threads - 1) / threads;
+  for (int t = 0; t < threads; ++t) {
+    const size_t a = t * per, b = std::min(n, a + per);
+    if (a >= b) break;
+    pool.emplace_back([=] { orc_kmeans_assign(pts + a * dim, b - a, dim, cents, k, assign + a, dist + a); });
+  }
+  for (auto& th : pool) th.join();
+}
+
 // --- RNG surface -------------------------------------------------------------
 void* orc_rng_new(uint64_t seed, int rounds) {
   Rng* r = new Rng();
@@ -992,6 +1007,15 @@ size_t orc_ivf_train(const float* vectors, const uint8_t* live, size_t slots, si
     size_t l = ivf_nearest(&sample[i * dim], cents.data(), dim, produced);
     for (size_t j = 0; j < dim; ++j) resid[i * dim + j] = sample[i * dim + j] - cents[l * dim + j];
   }
+  // ProductQuantizer::train validates every residual first (product.rs:221-223):
+  // the first non-finite one is reported as (component, vector, value)
+  for (size_t i = 0; i < resid.size(); ++i)
+    if (!std::isfinite(resid[i])) {
+      report[0] = (double)(i % dim);
+      report[1] = (double)(i / dim);
+      report[2] = (double)resid[i];
+      return SIZE_MAX;
+    }
   double rin;
   size_t rit;
   pq_train(resid.data(), sampled, dim, m, max_iter, seed, books_out, &rin, &rit);

@@ -74,6 +74,7 @@ def _load():
         "orc_kmeans": (_sz, [_f32p, _sz, _sz, _sz, _sz, C.c_uint64, _f32p, C.POINTER(C.c_double),
                              C.POINTER(C.c_size_t)]),
         "orc_kmeans_assign": (None, [_f32p, _sz, _sz, _f32p, _sz, _u32p, _f32p]),
+        "orc_kmeans_assign_mt": (None, [_f32p, _sz, _sz, _f32p, _sz, _u32p, _f32p, C.c_int]),
         "orc_rng_new": (C.c_void_p, [C.c_uint64, C.c_int]),
         "orc_rng_set_key": (None, [C.c_void_p, _u32p]),
         "orc_rng_key": (None, [C.c_void_p, _u32p]),
@@ -354,12 +355,15 @@ def kmeans(points, k, max_iter, seed):
     return cents.reshape(got, dim), inertia.value, iters.value
 
 
-def kmeans_assign(points, cents):
+def kmeans_assign(points, cents, threads=1):
     points, cents = f32(points), f32(cents)
     n, dim = points.shape
     a = np.zeros(n, np.uint32)
     d = np.zeros(n, np.float32)
-    lib.orc_kmeans_assign(points, n, dim, cents, cents.shape[0], a, d)
+    if threads > 1:
+        lib.orc_kmeans_assign_mt(points, n, dim, cents, cents.shape[0], a, d, threads)
+    else:
+        lib.orc_kmeans_assign(points, n, dim, cents, cents.shape[0], a, d)
     return a, d
 
 
@@ -421,6 +425,9 @@ def ivf_train(vectors, nlist, m, max_iter=25, training_sample=100_000, seed=0x1F
     report = np.zeros(4, np.float64)
     produced = lib.orc_ivf_train(vectors, live, slots, dim, nlist, m, max_iter, training_sample, seed, cents, books,
                                  report)
+    if produced == np.iinfo(np.uintp).max:
+        raise ValueError(f"NonFinite residual: component {int(report[0])} of sample vector {int(report[1])} "
+                         f"({report[2]})", int(report[0]), int(report[1]), float(report[2]))
     return cents[: produced * dim].reshape(produced, dim), books, report
 
 

@@ -120,6 +120,24 @@ struct DevBuf {
   size_t bytes() const { return n * sizeof(T); }
 };
 
+// Copy `rows` rows of `width` bytes from device rows `spitch` bytes apart to
+// host rows `dpitch` bytes apart. A strided copy into pageable memory goes
+// row by row, so the rows come over in one contiguous copy and are spread on
+// the host; equal pitches take one direct copy. Returns after the copy.
+inline void rows_to_host(void* dst, size_t dpitch, const void* src, size_t spitch, size_t width, size_t rows,
+                         hipStream_t s) {
+  if (rows == 0 || width == 0) return;
+  if (dpitch == spitch && width == spitch) {
+    PXG_HIP(hipMemcpyAsync(dst, src, rows * width, hipMemcpyDeviceToHost, s));
+    PXG_HIP(hipStreamSynchronize(s));
+    return;
+  }
+  std::vector<unsigned char> tmp(rows * spitch);
+  PXG_HIP(hipMemcpyAsync(tmp.data(), src, rows * spitch, hipMemcpyDeviceToHost, s));
+  PXG_HIP(hipStreamSynchronize(s));
+  for (size_t r = 0; r < rows; ++r) std::memcpy((unsigned char*)dst + r * dpitch, tmp.data() + r * spitch, width);
+}
+
 // LIFO slot allocator: id.rs:137-229 (most recently released slot first).
 struct SlotAllocator {
   uint32_t next = 0;

@@ -893,8 +893,8 @@ int pxg_flat_search(const pxg_flat* index, const float* queries, uint64_t nq, ui
     PXG_HIP(hipMemcpyAsync(d_q, prep.data(), prep.size() * 4, hipMemcpyHostToDevice, s));
     uint64_t fb = 0;
     f.search_device(d_q, false, nq, kq, d_acc, d_oid, d_od, d_oc, sc, s, &fb, kq);
-    PXG_HIP(hipMemcpy2DAsync(out_ids, k * 8, d_oid, kq * 8, kq * 8, nq, hipMemcpyDeviceToHost, s));
-    PXG_HIP(hipMemcpy2DAsync(out_dist, k * 4, d_od, kq * 4, kq * 4, nq, hipMemcpyDeviceToHost, s));
+    pxg::rows_to_host(out_ids, k * 8, d_oid, kq * 8, kq * 8, nq, s);
+    pxg::rows_to_host(out_dist, k * 4, d_od, kq * 4, kq * 4, nq, s);
     PXG_HIP(hipMemcpyAsync(out_count, d_oc, nq * 4, hipMemcpyDeviceToHost, s));
     PXG_HIP(hipStreamSynchronize(s));
     pxg::g_last_fallbacks = fb;

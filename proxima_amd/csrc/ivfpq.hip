@@ -992,6 +992,14 @@ __global__ void ivf_gather_rows(const float* __restrict__ X, int ld, const uint3
   for (int j = threadIdx.x; j < dim; j += blockDim.x) out[(size_t)i * dim + j] = X[(size_t)rows[i] * ld + j];
 }
 
+// First non-finite value of n rows (row-major order): the vector and
+// component `space.validate` reports first (space.rs:104-121).
+__global__ void ivf_first_nonfinite(const float* __restrict__ R, size_t n, int dim, unsigned long long* bad) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n * (size_t)dim) return;
+  if (!isfinite(R[i])) atomicMin(bad, ((unsigned long long)(i / dim) << 32) | (unsigned)(i % dim));
+}
+
 __global__ void ivf_residuals(const float* __restrict__ S, const float* __restrict__ C, const uint32_t* __restrict__ a,
                               int dim, float* __restrict__ R) {
   const int i = blockIdx.x;
@@ -1504,6 +1512,26 @@ struct IvfPqIndex {
     DevBuf<float> R(ns * dim);
     hipLaunchKernelGGL(ivf_residuals, dim3((unsigned)ns), dim3(256), 0, stream, S.p, coarse.p, as.p, (int)dim, R.p);
     PXG_HIP(hipGetLastError());
+    {
+      // ProductQuantizer::train validates every residual (product.rs:221-223):
+      // x - c can overflow even though x and c are finite
+      DevBuf<unsigned long long> bad(1);
+      PXG_HIP(hipMemsetAsync(bad.p, 0xFF, 8, stream));
+      const size_t tot = ns * dim;
+      hipLaunchKernelGGL(ivf_first_nonfinite, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, stream, R.p, ns,
+                         (int)dim, bad.p);
+      PXG_HIP(hipGetLastError());
+      unsigned long long bv = 0;
+      PXG_HIP(hipMemcpyAsync(&bv, bad.p, 8, hipMemcpyDeviceToHost, stream));
+      PXG_HIP(hipStreamSynchronize(stream));
+      if (bv != ~0ull) {
+        const uint64_t row = bv >> 32, comp = (uint32_t)bv;
+        float v = NAN;
+        PXG_HIP(hipMemcpy(&v, R.p + row * dim + comp, 4, hipMemcpyDeviceToHost));
+        raise(PXG_ERR_NON_FINITE,
+              "vector component " + std::to_string(comp) + " is not finite (" + std::to_string(v) + ")", comp, row, v);
+      }
+    }
     // PQ with a fresh generator from the same seed (ivfpq.rs:794-801)
     DevBuf<float> B(pq.book_floats());
     double rin = 0.0;
@@ -2241,15 +2269,22 @@ int pxg_ivfpq_load_trained(pxg_ivfpq* index, const float* centroids, uint64_t pr
     std::unique_lock<std::shared_mutex> lk(index->impl.mu);
     IvfPqIndex& f = index->impl;
     if (produced == 0 || produced > f.cfg.nlist) pxg::config_error("produced", produced, "must be between 1 and nlist");
-    f.upload_books(centroids, (int)produced, codebooks);
+    // every check before any state changes (IvfPqIndex::from_parts builds
+    // nothing when it returns an error, ivfpq.rs:624-717)
     const size_t hw = f.slots.high_water();
+    if ((codes == nullptr) != (list_of == nullptr))
+      pxg::raise(PXG_ERR_CORRUPTION, "corrupt ivfpq index: codes and list assignments come together");
     if (codes) {
-      for (size_t s = 0; s < hw; ++s) {
+      for (size_t s = 0; s < hw; ++s)
         if (f.live[s] && list_of[s] != pxg::UNASSIGNED && list_of[s] >= produced)
           pxg::raise(PXG_ERR_CORRUPTION, "corrupt ivfpq index: slot " + std::to_string(s) + " names list " +
                                              std::to_string(list_of[s]) + " of " + std::to_string(produced));
-        f.list_of_h[s] = f.live[s] ? list_of[s] : pxg::UNASSIGNED;
-      }
+    } else if (!f.vectors_kept && !f.by_id.empty()) {
+      pxg::config_error("codes", 0, "the index keeps no vectors to encode: codes and list assignments are required");
+    }
+    f.upload_books(centroids, (int)produced, codebooks);
+    if (codes) {
+      for (size_t s = 0; s < hw; ++s) f.list_of_h[s] = f.live[s] ? list_of[s] : pxg::UNASSIGNED;
       if (hw) {
         PXG_HIP(hipMemcpy(f.codes.p, codes, hw * f.M(), hipMemcpyHostToDevice));
         PXG_HIP(hipMemcpy(f.d_list_of.p, f.list_of_h.data(), hw * 4, hipMemcpyHostToDevice));
@@ -2302,8 +2337,8 @@ int pxg_ivfpq_search(const pxg_ivfpq* index, const float* queries, uint64_t nq, 
     uint32_t* d_oc = (uint32_t*)ctx->get(24, nq * 4);
     PXG_HIP(hipMemcpyAsync(d_q, prep.data(), prep.size() * 4, hipMemcpyHostToDevice, s));
     f.search_device(d_q, false, nq, kq, nprobe ? nprobe : f.cfg.nprobe, d_acc, d_oid, d_od, d_oc, sc, s, kq);
-    PXG_HIP(hipMemcpy2DAsync(out_ids, k * 8, d_oid, kq * 8, kq * 8, nq, hipMemcpyDeviceToHost, s));
-    PXG_HIP(hipMemcpy2DAsync(out_dist, k * 4, d_od, kq * 4, kq * 4, nq, hipMemcpyDeviceToHost, s));
+    pxg::rows_to_host(out_ids, k * 8, d_oid, kq * 8, kq * 8, nq, s);
+    pxg::rows_to_host(out_dist, k * 4, d_od, kq * 4, kq * 4, nq, s);
     PXG_HIP(hipMemcpyAsync(out_count, d_oc, nq * 4, hipMemcpyDeviceToHost, s));
     PXG_HIP(hipStreamSynchronize(s));
   });

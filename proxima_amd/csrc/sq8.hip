@@ -1480,8 +1480,8 @@ static int sq8_search_host(const pxg_sq8* index, const float* queries, const int
     uint64_t fb = 0;
     f.search_device(d_q, d_qc, nq, kq, rescore, d_acc, d_oid, d_od, d_oc, sc, s, &fb, kk);
     if (kq) {
-      PXG_HIP(hipMemcpy2DAsync(out_ids, k * 8, d_oid, kk * 8, kq * 8, nq, hipMemcpyDeviceToHost, s));
-      PXG_HIP(hipMemcpy2DAsync(out_dist, k * 4, d_od, kk * 4, kq * 4, nq, hipMemcpyDeviceToHost, s));
+      pxg::rows_to_host(out_ids, k * 8, d_oid, kk * 8, kq * 8, nq, s);
+      pxg::rows_to_host(out_dist, k * 4, d_od, kk * 4, kq * 4, nq, s);
     }
     PXG_HIP(hipMemcpyAsync(out_count, d_oc, nq * 4, hipMemcpyDeviceToHost, s));
     PXG_HIP(hipStreamSynchronize(s));

@@ -460,3 +460,51 @@ def test_scan_of_a_list_over_65536_entries(gpu):
     q = data[rng.integers(0, n, 800)] + np.float32(0.01)
     want = orc.ivf_search(0, cents, books, codes, list_of, np.arange(n), q, 10, nlist, m, threads=8)
     assert_same(idx.search_batch(q, 10, nprobe=nlist), want)
+
+
+def test_training_rejects_non_finite_residuals(gpu):
+    """ProductQuantizer::train validates every residual (product.rs:221-223):
+    x - c overflows here although every vector is finite, and both the oracle
+    and the GPU report NonFinite for the first such residual component."""
+    px = gpu
+    data = np.zeros((10, 4), np.float32)
+    data[0, 0] = 3e38
+    data[1:, 0] = -3e38
+    data[1:, 1:] = np.arange(1, 4, dtype=np.float32)
+    with pytest.raises(ValueError) as e:
+        orc.ivf_train(data, 1, 2, max_iter=3, seed=1)
+    comp, row = e.value.args[1], e.value.args[2]
+    assert (comp, row) == (0, 0) and e.value.args[3] == float("inf")
+    cfg = px.IvfPqConfig(1, 2).with_train_threshold(1 << 62).with_max_iterations(3).with_seed(1)
+    idx = px.IvfPqIndex(px.VectorSpace(4, px.Metric.EUCLIDEAN), cfg)
+    idx.insert_batch(np.arange(10, dtype=np.uint64), data)
+    with pytest.raises(px.NonFinite) as g:
+        idx.train()
+    assert g.value.index == comp and g.value.value == float("inf")
+    assert not idx.is_trained()
+
+
+def test_corrupt_load_changes_nothing(gpu):
+    """from_parts builds nothing when it fails (ivfpq.rs:624-717): a load with
+    a list assignment beyond the centroids, or codes without assignments,
+    leaves the index as it was, and it still searches the same."""
+    px = gpu
+    rng = np.random.default_rng(3)
+    n, dim, nlist, m = 800, 16, 8, 4
+    data = rng.standard_normal((n, dim)).astype(np.float32)
+    cents, books, _ = orc.ivf_train(data, nlist, m, max_iter=4, seed=2)
+    codes, list_of = orc.ivf_encode(data, cents, books, m)
+    idx = build(px, data, px.IvfPqConfig(nlist, m).with_train_threshold(1 << 62))
+    idx.load_trained(cents, books, codes, list_of)
+    q = data[::80] + 0.01
+    before = idx.search_batch(q, 10, nprobe=4)
+    bad = list_of.copy()
+    bad[5] = nlist + 3
+    with pytest.raises(px.Corruption):
+        idx.load_trained(cents[:4] * 2, books * 2, codes, bad)
+    with pytest.raises(px.Corruption):
+        idx.load_trained(cents, books, codes, None)
+    after = idx.search_batch(q, 10, nprobe=4)
+    for a, b in zip(before, after):
+        assert np.array_equal(a, b)
+    assert np.array_equal(idx.parts()[0], cents)
