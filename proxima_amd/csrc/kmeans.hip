@@ -34,6 +34,9 @@
 #include <cstdio>
 #include <cstdlib>
 #include <string>
+#include <thread>
+#include <exception>
+#include <vector>
 
 #include "common.hpp"
 #include "device.hpp"
@@ -942,13 +945,134 @@ __global__ __launch_bounds__(256) void km_pp_round(const float* __restrict__ P, 
   }
 }
 
+// ---------------------------------------------------------------------------
+// k-means++ rounds over an int8 copy of the points, certified
+// ---------------------------------------------------------------------------
+// A round only lowers ns[i] when the new centre c is strictly nearer than the
+// current one. Each point also has an int8 copy q_i (scale s_i = max|p_i| /
+// 127, q = rint(p / s_i)) and the exact distance delta_i = |p_i - s_i q_i|.
+// The centre is itself a point (kmeans.rs:169-186 picks rows), so it has q_c,
+// s_c and delta_c. With e = |s_i q_i - s_c q_c| from the exact integer dot
+// product, the triangle inequality gives |p_i - c| >= e - delta_i - delta_c
+// = L. The reference's sequential f32 sum (kmeans.rs:234-241) of dim
+// squares is >= |p_i - c|^2 (1 - (dim + 2) 2^-24) for non-negative terms, so
+// when L^2 (1 - gamma) >= ns[i] (with margins for the f64 rounding of e and
+// for subnormal terms) the exact distance cannot be below ns[i] and the
+// point keeps its value without its f32 row being read. The other points
+// (those the centre may capture) are scored exactly as km_pp_round does.
+// Per point the round then reads 4 + 16 bytes plus dim bytes, not 4 dim.
+constexpr int Q8_ROWS = 256;  // points per km_pp_round_q8 block
+
+// int8 copy, scale, delta and squared norm of the copy: one wave per point.
+__global__ __launch_bounds__(256) void km_q8_prep(const float* __restrict__ P, int ldp, int n, int dim, int kq,
+                                                  int8_t* __restrict__ Q, float* __restrict__ scale,
+                                                  float* __restrict__ delta, int* __restrict__ qnorm) {
+  const int lane = threadIdx.x & 63;
+  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (i >= n) return;
+  const float* p = P + (size_t)i * ldp;
+  float mx = 0.0f;
+  for (int j = lane; j < dim; j += 64) mx = fmaxf(mx, fabsf(p[j]));
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  const float sc = mx / 127.0f;
+  double d2 = 0.0;
+  int qn = 0;
+  for (int j = lane; j < kq; j += 64) {
+    int q = 0;
+    if (j < dim && sc > 0.0f) q = max(-127, min(127, (int)rintf(p[j] / sc)));
+    if (j < dim) {
+      const double r = (double)p[j] - (double)q * (double)sc;
+      d2 += r * r;
+    }
+    qn += q * q;
+    Q[(size_t)i * kq + j] = (int8_t)q;
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    d2 += __shfl_xor(d2, o, 64);
+    qn += __shfl_xor(qn, o, 64);
+  }
+  if (lane == 0) {
+    scale[i] = sc;
+    // an upper bound in f32 (the f64 sum's own rounding is far below one ulp)
+    const double d = sqrt(d2) * (1.0 + 1e-12);
+    float df = (float)d;
+    if ((double)df < d) df = nextafterf(df, INFINITY);
+    delta[i] = isfinite(mx) ? df : INFINITY;
+    qnorm[i] = qn;
+  }
+}
+
+__global__ __launch_bounds__(256) void km_pp_round_q8(const float* __restrict__ P, int ldp, int n, int dim,
+                                                      const int8_t* __restrict__ Q, int kq,
+                                                      const float* __restrict__ scale,
+                                                      const float* __restrict__ delta, const int* __restrict__ qnorm,
+                                                      const int* __restrict__ picked, float* __restrict__ ns,
+                                                      double* __restrict__ ps, int* __restrict__ pe,
+                                                      double gamma) {
+  __shared__ int qc[KW_DMAX / 4];
+  __shared__ float cs[KW_DMAX];
+  __shared__ int list[Q8_ROWS];
+  __shared__ int nlist;
+  __shared__ SumCert sh[4];
+  const int t = threadIdx.x;
+  const int c = *picked;
+  const int words = kq / 4;
+  for (int j = t; j < words; j += 256) qc[j] = reinterpret_cast<const int*>(Q + (size_t)c * kq)[j];
+  for (int j = t; j < dim; j += 256) cs[j] = P[(size_t)c * ldp + j];
+  if (t == 0) nlist = 0;
+  __syncthreads();
+  const double sc = scale[c], dc = delta[c], qnc = (double)qnorm[c];
+  const int i = blockIdx.x * Q8_ROWS + t;
+  float cur = 0.0f;
+  bool exact = false;
+  if (i < n) {
+    cur = ns[i];
+    const int* qv = reinterpret_cast<const int*>(Q + (size_t)i * kq);
+    int dot = 0;
+    for (int j = 0; j < words; ++j) dot = __builtin_amdgcn_sdot4(qv[j], qc[j], dot, false);
+    const double sp = scale[i];
+    const double A = sp * sp * (double)qnorm[i], B = sc * sc * qnc, C = sp * sc * (double)dot;
+    const double e2 = A + B - 2.0 * C;
+    const double err = 1e-13 * (A + B + 2.0 * fabs(C));
+    const double e = sqrt(fmax(e2 - err, 0.0)) * (1.0 - 1e-13);
+    const double L = e - (double)delta[i] - dc;
+    const bool keep = isfinite(cur) && L > 0.0 && L * L * (1.0 - gamma) >= (double)cur + 1e-35;
+    exact = !keep;
+  }
+  if (exact) list[atomicAdd(&nlist, 1)] = t;
+  __syncthreads();
+  __shared__ float nv_s[Q8_ROWS];
+  nv_s[t] = cur;
+  __syncthreads();
+  const int m = nlist;
+  for (int u = t; u < m; u += 256) {
+    const int tt = list[u];
+    const int ii = blockIdx.x * Q8_ROWS + tt;
+    const float* row = P + (size_t)ii * ldp;
+    float sum = 0.0f;
+    for (int j = 0; j < dim; ++j) {
+      const float d = row[j] - cs[j];
+      sum += d * d;
+    }
+    if (sum < nv_s[tt]) nv_s[tt] = sum;
+  }
+  __syncthreads();
+  const float nv = i < n ? nv_s[t] : 0.0f;
+  if (i < n && nv != cur) ns[i] = nv;
+  const SumCert r = block_cert_256(cert_of(nv), sh);
+  if (t == 0) {
+    ps[blockIdx.x] = r.s;
+    pe[blockIdx.x] = r.e;
+  }
+}
+
 // One 1024-thread block: the pick of one round and the copy of its row.
 // status: 0 ok, 1 non-finite total (the round and all later ones stop).
 __global__ __launch_bounds__(1024) void km_pp_pick(const float* __restrict__ P, int ldp, int n, int dim,
                                                    const float* __restrict__ ns, const double* __restrict__ ps,
                                                    const int* __restrict__ pe, int nb, ChaCha8* __restrict__ grng,
                                                    float* __restrict__ row_out, int* __restrict__ status,
-                                                   int* __restrict__ inexact) {
+                                                   int* __restrict__ inexact, int* __restrict__ picked_out) {
   __shared__ double ex[1024];
   __shared__ int se[1024];
   __shared__ float stage[4096];
@@ -1064,7 +1188,10 @@ __global__ __launch_bounds__(1024) void km_pp_pick(const float* __restrict__ P, 
   __syncthreads();
   const int picked = s_pick;
   for (int j = t; j < dim; j += 1024) row_out[j] = P[(size_t)picked * ldp + j];
-  if (t == 0) *grng = rng;
+  if (t == 0) {
+    *grng = rng;
+    if (picked_out) *picked_out = picked;
+  }
 }
 
 __global__ void copy_row(const float* __restrict__ src, int ld_src, size_t row, int dim, float* __restrict__ dst) {
@@ -1111,12 +1238,32 @@ size_t kmeans_pp_device(const float* P, size_t n, int dim, int ldp, size_t k, Ch
   const int vec4 = (ldp % 4 == 0 && dim % 4 == 0 && ((uintptr_t)P & 15) == 0) ? 1 : 0;
   hipLaunchKernelGGL(km_pp_round, dim3(nb), dim3(256), 0, s, P, ldp, (int)n, dim, cents, ns.p, 1, ps.p, pe.p, vec4);
   PXG_HIP(hipGetLastError());
+  // rounds after the first over the certified int8 copy (dim >= 32; for
+  // narrower points the copy saves little of each row's bytes)
+  const bool q8 = dim >= 32 && dim <= KW_DMAX && k > 1 && Q8_ROWS == PP_ROWS;
+  const int kq = (dim + 3) / 4 * 4;
+  DevBuf<int8_t> Q(q8 ? n * kq : 0);
+  DevBuf<float> qscale(q8 ? n : 0), qdelta(q8 ? n : 0);
+  DevBuf<int> qnorm(q8 ? n : 0), picked(1);
+  if (q8) {
+    hipLaunchKernelGGL(km_q8_prep, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, P, ldp, (int)n, dim, kq, Q.p,
+                       qscale.p, qdelta.p, qnorm.p);
+    PXG_HIP(hipGetLastError());
+  }
+  const double gamma = (double)(dim + 4) * 0x1p-24 * 1.01;
   for (size_t chosen = 1; chosen < k; ++chosen) {
     float* c = cents + chosen * dim;
     hipLaunchKernelGGL(km_pp_pick, dim3(1), dim3(1024), 0, s, P, ldp, (int)n, dim, ns.p, ps.p, pe.p, nb, drng.p, c,
-                       flags.p, flags.p + 1);
-    if (chosen + 1 < k)
-      hipLaunchKernelGGL(km_pp_round, dim3(nb), dim3(256), 0, s, P, ldp, (int)n, dim, c, ns.p, 0, ps.p, pe.p, vec4);
+                       flags.p, flags.p + 1, picked.p);
+    if (chosen + 1 < k) {
+      if (q8)
+        hipLaunchKernelGGL(km_pp_round_q8, dim3(nb), dim3(256), 0, s, P, ldp, (int)n, dim, (const int8_t*)Q.p, kq,
+                           (const float*)qscale.p, (const float*)qdelta.p, (const int*)qnorm.p, (const int*)picked.p,
+                           ns.p, ps.p, pe.p, gamma);
+      else
+        hipLaunchKernelGGL(km_pp_round, dim3(nb), dim3(256), 0, s, P, ldp, (int)n, dim, c, ns.p, 0, ps.p, pe.p,
+                           vec4);
+    }
     PXG_HIP(hipGetLastError());
   }
   int h[2] = {0, 0};
@@ -1481,21 +1628,69 @@ __global__ void pad_book(float* __restrict__ book, int produced, int w) {
 
 void pq_train_device(const float* R, size_t n, int dim, int ldr, const PqLayout& L, size_t max_iter, uint64_t seed,
                      float* d_books, double* inertia, size_t* iterations, hipStream_t s) {
-  ChaCha8 rng(seed);  // one generator advanced across subspaces (product.rs:244-247)
+  // One generator advanced across the subspaces (product.rs:244-247), but
+  // only k-means++ draws from it (kmeans.rs:146-194; Lloyd and the farthest
+  // point reseeds draw nothing). So the seeds are drawn subspace by subspace
+  // on `s`, and each subspace's Lloyd loop starts on its own stream and host
+  // thread as soon as its seeds exist, overlapping the later seedings and the
+  // other subspaces' loops. Each loop is the same kmeans_device, so every
+  // codebook is the sequential run's.
+  (void)dim;
+  ChaCha8 rng(seed);
+  const int M = L.M;
+  const size_t k = std::max<size_t>(std::min<size_t>(256, n), 1);
+  std::vector<DevBuf<float>> proj(M), seeds(M), cents(M);
+  std::vector<KmeansOut> res(M);
+  std::vector<std::exception_ptr> err(M);
+  std::vector<std::thread> workers;
+  auto join_all = [&]() {
+    for (auto& w : workers)
+      if (w.joinable()) w.join();
+  };
+  try {
+    for (int sidx = 0; sidx < M; ++sidx) {
+      const int w = L.width[sidx], off = L.off[sidx];
+      const size_t tot = n * (size_t)w;
+      proj[sidx].reserve(std::max<size_t>(tot, 1));
+      seeds[sidx].reserve(k * w);
+      if (tot)
+        hipLaunchKernelGGL(gather_cols, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, R, ldr, (int)n, off, w,
+                           proj[sidx].p);
+      PXG_HIP(hipGetLastError());
+      size_t inexact = 0;
+      if (n) inexact = kmeans_pp_device(proj[sidx].p, n, w, w, k, rng, seeds[sidx].p, s);  // synchronises s
+      workers.emplace_back([&, sidx, w, inexact]() {
+        try {
+          hipStream_t ws;
+          PXG_HIP(hipStreamCreateWithFlags(&ws, hipStreamNonBlocking));
+          struct SG {
+            hipStream_t s;
+            ~SG() { (void)hipStreamDestroy(s); }
+          } sg{ws};
+          res[sidx] = kmeans_device(proj[sidx].p, n, w, w, 256, max_iter, nullptr, n ? seeds[sidx].p : nullptr,
+                                    cents[sidx], nullptr, ws);
+          res[sidx].inexact_sums += inexact;
+        } catch (...) {
+          err[sidx] = std::current_exception();
+        }
+      });
+    }
+  } catch (...) {
+    join_all();
+    throw;
+  }
+  join_all();
+  for (auto& e : err)
+    if (e) std::rethrow_exception(e);
   double in = 0.0;
   size_t its = 0;
-  DevBuf<float> proj(std::max<size_t>(n * (size_t)(L.width.empty() ? 1 : *std::max_element(L.width.begin(), L.width.end())), 1));
-  DevBuf<float> cents;
-  for (int sidx = 0; sidx < L.M; ++sidx) {
-    const int w = L.width[sidx], off = L.off[sidx];
-    const size_t tot = n * (size_t)w;
-    if (tot) hipLaunchKernelGGL(gather_cols, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, R, ldr, (int)n, off, w, proj.p);
-    PXG_HIP(hipGetLastError());
-    KmeansOut r = kmeans_device(proj.p, n, w, w, 256, max_iter, &rng, nullptr, cents, nullptr, s);
+  for (int sidx = 0; sidx < M; ++sidx) {
+    const int w = L.width[sidx];
+    const KmeansOut& r = res[sidx];
     in += r.inertia;
     its += r.iterations;
     float* book = d_books + L.book_off[sidx];
-    PXG_HIP(hipMemcpyAsync(book, cents.p, r.k * w * 4, hipMemcpyDeviceToDevice, s));
+    PXG_HIP(hipMemcpyAsync(book, cents[sidx].p, r.k * w * 4, hipMemcpyDeviceToDevice, s));
     if (r.k < 256) {
       const int t = (int)(256 - r.k) * w;
       hipLaunchKernelGGL(pad_book, dim3((t + 255) / 256), dim3(256), 0, s, book, (int)r.k, w);

@@ -239,3 +239,33 @@ def test_pq_validation(gpu):  # product.rs:775-809
             px.ProductQuantizer.train(space, t, bad)
     with pytest.raises(px.Configuration):
         px.ProductQuantizer.train(space, np.array([1.0, 2.0], np.float32), px.PqConfig(2))
+
+
+@pytest.mark.parametrize("case", ["wide_range", "duplicates", "far_outliers"])
+def test_kmeans_pp_certified_int8_rounds(gpu, case):
+    """k-means++ rounds after the first skip a point only when an int8 copy
+    proves its exact distance cannot drop (kmeans.rs:180-186): data where
+    that copy is coarse (coordinates spanning 10 orders of magnitude), exact
+    ties and zero distances (duplicate points), and outliers far from
+    everything. Seeds, then full runs, equal the oracle's bit for bit."""
+    px = gpu
+    rng = np.random.default_rng(5)
+    n, dim, k = 6000, 64, 48
+    if case == "wide_range":
+        pts = (rng.standard_normal((n, dim)) * 1e-3).astype(np.float32)
+        pts[:, 0] += rng.integers(0, 5, n).astype(np.float32) * np.float32(1e4)
+        pts[::7, 5] += np.float32(1e-30)
+    elif case == "duplicates":
+        base = rng.standard_normal((30, dim)).astype(np.float32)
+        pts = base[rng.integers(0, 30, n)].copy()
+        pts[::11, 3] += np.float32(1e-7)
+    else:
+        pts = rng.standard_normal((n, dim)).astype(np.float32)
+        pts[::500] *= np.float32(1e5)
+    got = px.kmeans_pp(pts, k, 3)
+    want = orc.kmeans_pp(pts, k, 3)
+    assert np.array_equal(bits(got), bits(want))
+    g = px.kmeans(pts, dim, k, 4, 3)
+    w = orc.kmeans(pts, k, 4, 3)
+    assert np.array_equal(bits(g.centroids.reshape(-1)), bits(w[0].reshape(-1)))
+    assert g.inertia == w[1] and g.iterations == w[2]
