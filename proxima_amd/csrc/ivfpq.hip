@@ -424,6 +424,182 @@ __global__ __launch_bounds__(256) void ivf_coarse_pick(const uint64_t* __restric
   }
 }
 
+// ---------------------------------------------------------------------------
+// Coarse stage on matrix cores, certified
+// ---------------------------------------------------------------------------
+// The probe set is the np smallest (squared_euclidean_unrolled, list) keys
+// (ivfpq.rs:1019-1026), so it must come from the exact arithmetic. Phase one
+// computes a[q][l] = |q|^2 + |c_l|^2 - 2 q.c_l with FP32 MFMA; the exact
+// D = squared_euclidean_unrolled(q, c_l) satisfies |a - D| <= eps_ql =
+// 4 dim 2^-24 (|q| + |c_l|)^2 (the f32 errors of both computations, each at
+// most about dim ulps of (|q| + |c_l|)^2). Phase two per query: T = the np-th
+// smallest of the 64 group minima of a + eps bounds the np-th smallest D
+// from above, so every list with D below it has a - eps <= T; those lists
+// are rescored exactly and sorted by (D, list). More than IVF_PICK_CAP of
+// them falls back to exact keys over every list.
+typedef float fv16 __attribute__((ext_vector_type(16)));
+
+// 64 queries x 64 lists per 256-thread block, a 32 x 32 block per wave. The
+// k index is permuted alike for both operands (lane half h feeds k-block
+// [8j + 4h, 8j + 4h + 4) of step group j), so each lane loads float4 rows
+// and the dot product covers every k once.
+__global__ __launch_bounds__(256) void ivf_coarse_mfma(const float* __restrict__ Qp, int ld, int nq,
+                                                       const float* __restrict__ qn,
+                                                       const float* __restrict__ C, int produced,
+                                                       const float* __restrict__ cn, int cst,
+                                                       float* __restrict__ A) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int r = lane & 31, h = lane >> 5;
+  const int qrow = blockIdx.x * 64 + (w & 1) * 32 + r;
+  const int crow = blockIdx.y * 64 + (w >> 1) * 32 + r;
+  const float* qp = Qp + (size_t)min(qrow, nq - 1) * ld + 4 * h;
+  const float* cp = C + (size_t)min(crow, produced - 1) * ld + 4 * h;
+  fv16 acc;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+  for (int k = 0; k < ld; k += 8) {
+    const float4 a4 = *reinterpret_cast<const float4*>(qp + k);
+    const float4 b4 = *reinterpret_cast<const float4*>(cp + k);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.x, b4.x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.y, b4.y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.z, b4.z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.w, b4.w, acc, 0, 0, 0);
+  }
+  // lane holds rows 8 (v/4) + 4 h + v%4 (queries) of column r (list)
+  const int l = blockIdx.y * 64 + (w >> 1) * 32 + r;
+  if (l >= produced) return;
+  const float c2 = cn[l] * cn[l];
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const int q = blockIdx.x * 64 + (w & 1) * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+    if (q < nq) {
+      const float q2 = qn[q] * qn[q];
+      A[(size_t)q * cst + l] = (q2 + c2) - 2.0f * acc[v];
+    }
+  }
+}
+
+// Phase two, one workgroup per query (see above); writes the probes in (D,
+// list) order and adds their list lengths to *scanned.
+__global__ __launch_bounds__(256) void ivf_coarse_pick_approx(const float* __restrict__ A, int cst, int produced,
+                                                              int np, const float* __restrict__ Qp, int ld, int dim,
+                                                              const float* __restrict__ qn,
+                                                              const float* __restrict__ C,
+                                                              const float* __restrict__ cn,
+                                                              int* __restrict__ probes,
+                                                              const uint32_t* __restrict__ list_off,
+                                                              unsigned long long* __restrict__ scanned) {
+  const int q = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  __shared__ uint64_t cand[IVF_PICK_CAP];
+  __shared__ int cl[IVF_PICK_CAP];
+  __shared__ float gmin[64];
+  __shared__ int hist[256];
+  __shared__ uint64_t sh[4];
+  __shared__ int ncand;
+  __shared__ float s_t;
+  const float* a = A + (size_t)q * cst;
+  const float qv = qn[q];
+  const float ef = 4.0f * (float)dim * 5.9604645e-08f;
+  const float* qrow = Qp + (size_t)q * ld;
+  auto eps = [&](int l) {
+    const float s = qv + cn[l];
+    return ef * s * s * 1.0001f + 1e-30f;
+  };
+  const int ng = min(64, produced), gs = (produced + ng - 1) / ng;
+  if (tid == 0) ncand = 0;
+  for (int g = w; g < 64; g += 4) {
+    float m = INFINITY;
+    if (g < ng) {
+      const int b = g * gs, e = min(produced, b + gs);
+      for (int i = b + lane; i < e; i += 64) m = fminf(m, a[i] + eps(i));
+    }
+#pragma unroll
+    for (int st = 32; st > 0; st >>= 1) m = fminf(m, __shfl_xor(m, st, 64));
+    if (lane == 0) gmin[g] = m;
+  }
+  __syncthreads();
+  if (w == 0) {
+    // the np-th smallest group minimum (np <= ng <= 64); NaN (from overflow)
+    // sorts last under the ordered key
+    uint64_t v[1] = {lane < ng ? (uint64_t)ord_key(gmin[lane]) : KEY_MAX};
+    wave_bitonic_sort<1>(v, lane);
+    const uint64_t t = readlane64(v[0], np - 1);
+    if (lane == 0) s_t = key_float((uint32_t)t);
+  }
+  __syncthreads();
+  const float t = s_t;
+  const bool finite_t = t == t && t < INFINITY;
+  for (int i = tid; i < produced && finite_t; i += 256) {
+    const float av = a[i];
+    if (!(av - eps(i) > t)) {  // NaN a (overflow) is kept and rescored
+      const int at = atomicAdd(&ncand, 1);
+      if (at < IVF_PICK_CAP) cl[at] = i;
+    }
+  }
+  __syncthreads();
+  const int nc = finite_t ? ncand : IVF_PICK_CAP + 1;
+  if (nc <= IVF_PICK_CAP) {
+    // exact keys of the candidates: 8 threads per list (dist_group8)
+    const int g8 = tid & 7;
+    for (int c = tid >> 3; c < nc; c += 32) {
+      const int l = cl[c];
+      const float d = dist_group8<0>(qrow, C + (size_t)l * ld, dim, g8);
+      if (g8 == 0) cand[c] = ((uint64_t)ord_key(d) << 32) | (uint32_t)l;
+    }
+    __syncthreads();
+    if (nc <= 64) {
+      if (w == 0) {
+        uint64_t v[1] = {lane < nc ? cand[lane] : KEY_MAX};
+        wave_bitonic_sort<1>(v, lane);
+        cand[lane] = v[0];
+      }
+      __syncthreads();
+    } else {
+      int P = 128;
+      while (P < nc) P <<= 1;
+      for (int i = nc + tid; i < P; i += 256) cand[i] = KEY_MAX;
+      __syncthreads();
+      block_bitonic_sort(cand, P);
+    }
+  } else {
+    // exact keys of every list, radix select of the np-th, then sort
+    auto key = [&](int i) -> uint64_t {
+      return ((uint64_t)ord_key(dist_thread<0>(qrow, C + (size_t)i * ld, dim)) << 32) | (uint32_t)i;
+    };
+    const uint64_t pivot = block_radix_select(key, produced, np, hist, sh);
+    if (tid == 0) ncand = 0;
+    __syncthreads();
+    for (int i = tid; i < produced; i += 256) {
+      const uint64_t x = key(i);
+      if (x <= pivot) cand[atomicAdd(&ncand, 1)] = x;  // np <= 64 of them
+    }
+    __syncthreads();
+    if (w == 0) {
+      uint64_t v[1] = {lane < np ? cand[lane] : KEY_MAX};
+      wave_bitonic_sort<1>(v, lane);
+      cand[lane] = v[0];
+    }
+    __syncthreads();
+  }
+  if (w == 0) {
+    const int l = (int)(uint32_t)cand[lane];
+    if (lane < np) probes[(size_t)q * np + lane] = l;
+    uint32_t len = lane < np ? list_off[l + 1] - list_off[l] : 0u;
+#pragma unroll
+    for (int st = 32; st > 0; st >>= 1) len += xor_lane_rt(len, st);
+    if (lane == 0) atomicAdd(scanned, (unsigned long long)len);
+  }
+}
+
+// |c_l| rounded to f32 (the bound above only needs it within a few ulps)
+__global__ void ivf_cent_norms(const float* __restrict__ C, int ld, int dim, int produced, float* __restrict__ cn) {
+  const int l = blockIdx.x * blockDim.x + threadIdx.x;
+  if (l >= produced) return;
+  double s = 0.0;
+  for (int j = 0; j < dim; ++j) s += (double)C[(size_t)l * ld + j] * (double)C[(size_t)l * ld + j];
+  cn[l] = (float)sqrt(s);
+}
+
 __global__ void ivf_transpose_cents(const float* __restrict__ C, int ld, int dim, int produced, int cst,
                                     float* __restrict__ cT) {
   const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1315,6 +1491,7 @@ struct IvfPqIndex {
   DevBuf<uint32_t> d_list_of;
   DevBuf<float> cents, books;
   DevBuf<float> cents_t;  // [dim][cst] transposed centroids for the coarse scan
+  DevBuf<float> cent_norm;  // |c_l| (slightly rounded up), for the certified MFMA coarse stage
   int cst = 0;
   DevBuf<int> d_sub_off, d_book_off;
   RankTable ranks;  // id ranks of the live slots, current after every mutation
@@ -1416,6 +1593,9 @@ struct IvfPqIndex {
     for (int l = 0; l < produced; ++l) lid[l] = (uint64_t)l;
     c.insert_device(lid.data(), dense.p, (uint64_t)produced, nullptr);
     cst = (produced + 63) / 64 * 64;
+    cent_norm.alloc(std::max(produced, 1));
+    hipLaunchKernelGGL(ivf_cent_norms, dim3((unsigned)((produced + 255) / 256)), dim3(256), 0, stream, cents.p,
+                       (int)ld, (int)dim, produced, cent_norm.p);
     cents_t.alloc((size_t)dim * cst);
     const size_t tot = (size_t)dim * cst;
     hipLaunchKernelGGL(ivf_transpose_cents, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, stream, cents.p,
@@ -1875,7 +2055,18 @@ struct IvfPqIndex {
       scanned_dev = (unsigned long long*)(flag_count + 2);
       hipLaunchKernelGGL(fill_u32, dim3(1), dim3(64), 0, s, (uint32_t*)scanned_dev, (size_t)2, 0u);
       const bool fused_count = np <= 64 && dim <= 2048;
-      if (fused_count) {
+      // matrix-core distances with exact rescoring near the cut, for widths
+      // where the GEMM outweighs the rescoring
+      const bool coarse_mfma = fused_count && dim >= 32 && ld % 8 == 0 && np <= produced;
+      if (coarse_mfma) {
+        float* A = (float*)sc.get(13, (size_t)nq * cst * 4);
+        const dim3 gd((unsigned)((nq + 63) / 64), (unsigned)((produced + 63) / 64));
+        hipLaunchKernelGGL(ivf_coarse_mfma, gd, dim3(256), 0, s, Qp, (int)ld, (int)nq, qn, cents.p, produced,
+                           cent_norm.p, cst, A);
+        hipLaunchKernelGGL(ivf_coarse_pick_approx, dim3((unsigned)nq), dim3(256), 0, s, (const float*)A, cst,
+                           produced, np, Qp, (int)ld, (int)dim, qn, cents.p, cent_norm.p, probes, list_off.p,
+                           scanned_dev);
+      } else if (fused_count) {
         uint64_t* keys = (uint64_t*)sc.get(13, (size_t)nq * cst * 8);
         const dim3 gd((unsigned)((nq + IVF_CQ - 1) / IVF_CQ), (unsigned)((produced + IVF_CW * 64 - 1) / (IVF_CW * 64)));
         hipLaunchKernelGGL(ivf_coarse_dist, gd, dim3(IVF_CW * 64), (size_t)dim * IVF_CQ * 4, s, Qp, (int)ld, (int)dim,
