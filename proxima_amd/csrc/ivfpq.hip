@@ -11,25 +11,31 @@
 //   CSR view rebuilt lazily after mutations, one entry per live slot, lists
 //   in order and slots ascending inside each list (ivfpq.rs:891-896):
 //     list_off [produced+1] u32, list_rank [entries] u32 (id rank),
-//     list_codes [entries][M] u8 -> M + 4 bytes per scanned vector.
+//     list_codes [entries][M] u8 -> M bytes per scanned vector streamed by
+//     ivf_scan16 (ranks read only for entries that pass its screen), M + 4
+//     by the other scans.
 //   X          [cap][ld] f32 prepared vectors when retained (rerank, training,
 //              the untrained exhaustive path).
 //
 // Search (ivfpq.rs:998-1110), per batch:
-//   coarse      exact squared_euclidean_unrolled to every centroid (bit-exact,
-//               so the probed list set is the reference's) and the nprobe
-//               smallest (distance, list): ivf_coarse_dist (all keys, over
-//               the transposed centroids) + ivf_coarse_pick for nprobe <= 64,
-//               else the exact flat index over the centroids, else
-//               ivf_coarse_keys + ivf_coarse_select.
+//   coarse      the nprobe smallest (exact squared_euclidean_unrolled, list)
+//               over every centroid (bit-exact, so the probed list set is the
+//               reference's): for nprobe <= 64, ivf_coarse_mfma (FP32 matrix
+//               core distances with a stated error bound) + ivf_coarse_pick_approx
+//               (exact rescoring of every list the bound cannot exclude) when
+//               dim >= 32, else ivf_coarse_dist (all exact keys, over the
+//               transposed centroids) + ivf_coarse_pick; beyond 64 the exact
+//               flat index over the centroids, else ivf_coarse_keys +
+//               ivf_coarse_select.
 //   scan        build each probe's distance table exactly as distance_table
 //               does (per subspace, per centroid, sequential d = q - c;
-//               l2 += d*d; ip += q*c), stream the list's codes coalesced (M
-//               bytes + a 4-byte id rank per entry), ADC-sum the table in
-//               subspace order (bit-exact), keep a per-wave top-kk by (score,
-//               id): ivf_scan16 (16 subspaces, dim <= 128, kk <= 64: codebook
-//               rows in VGPRs, one workgroup per query and up to 32 probes,
-//               list stream staged through LDS by asynchronous copies),
+//               l2 += d*d; ip += q*c), stream the list's codes coalesced,
+//               ADC-sum the table in subspace order (bit-exact), keep a
+//               per-wave top-kk by (score, id): ivf_scan16 (16 subspaces,
+//               dim <= 128, kk <= 64: codebook rows in VGPRs, one workgroup
+//               per query and up to 32 probes, codes staged through LDS by
+//               asynchronous copies, id ranks fetched only for entries whose
+//               score passes the wave's current k-th distance),
 //               ivf_scan_reg (other equal-width layouts, same work split),
 //               else ivf_scan (table in LDS, one workgroup per query and
 //               probe).
@@ -767,8 +773,8 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan_reg(const float* __restr
 // by the waves' own asynchronous loads so that HBM latency is hidden without
 // holding the data in VGPRs.
 //
-// Each wave owns a ring of IVF_NS chunk slots (64 entries: 1 KiB of codes +
-// 256 B of id ranks) and walks the group's (probe, 64-entry chunk) sequence
+// Each wave owns a ring of IVF_NS chunk slots (64 entries: 1 KiB of codes)
+// and walks the group's (probe, 64-entry chunk) sequence
 // twice: a producer cursor issues global->LDS copies (global_load_lds,
 // vmcnt-tracked) up to IVF_NS chunks ahead, refilling each slot as soon as it
 // has been read, and the consumer cursor waits for its chunk with s_waitcnt
@@ -779,7 +785,7 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan_reg(const float* __restr
 // ds_read_b32 with an immediate offset.
 // ---------------------------------------------------------------------------
 constexpr int IVF_NS = 3;                       // staged chunks per wave (all in flight)
-constexpr int IVF_CHUNK = 64 * 16 + 64 * 4;     // codes + ranks of 64 entries
+constexpr int IVF_CHUNK = 64 * 16;              // codes of 64 entries
 
 typedef __attribute__((address_space(3))) uint8_t lds_byte;
 
@@ -787,8 +793,8 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const lds_byte*)p;
 }
 
-// Global -> LDS copies; lane i's data lands at m0 + 16*i (dwordx4) or m0 + 4*i
-// (dword); lanes off in exec copy nothing. Written as inline asm so that the
+// Global -> LDS copy; lane i's 16 bytes land at m0 + 16*i; lanes off in exec
+// copy nothing. Written as inline asm so that the
 // compiler neither sees LDS writes pending behind vmcnt (it would drain them
 // with vmcnt(0) at every barrier) nor schedules around them: the consumer
 // waits with an explicit vmcnt. The asm sets m0 itself; the kernels that use
@@ -800,14 +806,12 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 __device__ __forceinline__ void lds_copy16(const void* g, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g) : "memory", "m0");
 }
-__device__ __forceinline__ void lds_copy4(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(g) : "memory", "m0");
-}
 #pragma clang diagnostic pop
 template <int N>
 __device__ __forceinline__ void vm_wait() {
   static_assert(N >= 0 && N <= 15, "immediate vmcnt");
   if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else if constexpr (N == 1) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
   else if constexpr (N == 2) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
   else if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
   else if constexpr (N == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
@@ -884,6 +888,7 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan16(const float* __restric
   __shared__ float s_qdc[IVF_PGMAX];
   __shared__ uint32_t s_lb[IVF_PGMAX], s_le[IVF_PGMAX];  // the group's list ranges
   __shared__ __align__(16) uint8_t ring[IVF_SW][IVF_NS][IVF_CHUNK];
+  __shared__ uint2 cbuf[IVF_SW][64];  // each wave's pending candidates: (distance key, list entry)
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   // thread t builds subspace ts = t/32 of every table, centroid rows
@@ -990,10 +995,7 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan16(const float* __restric
     uint8_t* slot = myring + (issued % IVF_NS) * IVF_CHUNK;
     const uint32_t e = pe + lane;
     const uint32_t a = __builtin_amdgcn_readfirstlane(lds_addr(slot));
-    if (e < pend) {
-      lds_copy16(list_codes + (size_t)e * 16, a);
-      lds_copy4(list_rank + e, a + 1024);
-    }
+    if (e < pend) lds_copy16(list_codes + (size_t)e * 16, a);
     ++issued;
     pe += IVF_SW * 64;
     seek(pp, pe, pend);
@@ -1006,34 +1008,72 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan16(const float* __restric
   }
   __syncthreads();
   uint64_t kept = KEY_MAX, thr = KEY_MAX;
+  // Candidates are screened on the distance key alone: an entry whose key
+  // exceeds the distance of the wave's kk-th kept key cannot enter the wave's
+  // top kk, whatever its id rank. The rest (ties included) wait in cbuf as
+  // (distance key, list entry); a flush fetches their id ranks (and applies
+  // the filter), sorts the full keys and merges them into `kept`. The list
+  // stream therefore carries codes only: ranks are read for the few entries
+  // that pass, and the screen threshold only tightens, at flushes.
+  uint32_t thr_d = 0xFFFFFFFFu;  // distance part of thr
+  int ncand = 0;                 // pending candidates (wave-uniform)
+  auto flush = [&]() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    uint64_t b[1] = {KEY_MAX};
+    if (lane < ncand) {
+      const uint2 c = cbuf[w][lane];
+      const uint32_t rk = list_rank[c.y];
+      if (accept == nullptr || accept[rank_slot[rk]]) b[0] = ((uint64_t)c.x << 32) | rk;
+    }
+    wave_bitonic_sort<1>(b, lane);
+    wave_merge_sorted(kept, b[0], lane);
+    thr = readlane64(kept, kk - 1);
+    thr_d = (uint32_t)(thr >> 32);
+    ncand = 0;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
   // One consumer iteration: refill the slot read in the previous iteration
   // (its reads are done), wait for this chunk (the chunks issued after it
-  // stay in flight), score it and keep the wave's best.
+  // stay in flight), score it and queue the entries that pass the screen.
   auto chunk = [&](const float* tab, float one_minus_qdc) {
     if (pp < np) issue();
+    static_assert(IVF_NS <= 3, "the waits below cover up to two later chunks");
     const int later = issued - consumed - 1;
-    if (later >= 2) vm_wait<4>();
-    else if (later == 1) vm_wait<2>();
+    if (later >= 2) vm_wait<2>();
+    else if (later == 1) vm_wait<1>();
     else vm_wait<0>();
     const uint8_t* slot = myring + (consumed % IVF_NS) * IVF_CHUNK;
     const uint4 cw = *reinterpret_cast<const uint4*>(slot + lane * 16);
-    const uint32_t rk = *reinterpret_cast<const uint32_t*>(slot + 1024 + lane * 4);
-    const bool valid = ce + lane < cend;
+    const uint32_t e = ce + lane;
+    const bool valid = e < cend;
     ++consumed;
     ce += IVF_SW * 64;
     seek(cp, ce, cend);
-    uint64_t key = KEY_MAX;
-    if (valid && (accept == nullptr || accept[rank_slot[rk]])) {
+    uint32_t dk = 0xFFFFFFFFu;
+    if (valid) {
       const float sum = adc16(tab, cw);
-      if constexpr (METRIC == 0) {
-        // sums of squares are in [+0, +inf]: the order key is the bits with
-        // the sign bit set
-        key = ((uint64_t)(__float_as_uint(sum) | 0x80000000u) << 32) | rk;
-      } else {
-        key = ((uint64_t)ord_key(ivf_cos_score(one_minus_qdc, sum)) << 32) | rk;
-      }
+      // L2: sums of squares are in [+0, +inf], so the order key is the bits
+      // with the sign bit set
+      dk = METRIC == 0 ? (__float_as_uint(sum) | 0x80000000u) : ord_key(ivf_cos_score(one_minus_qdc, sum));
     }
-    wave_topk_add(key, kept, thr, kk, lane);
+    bool pass = valid && dk <= thr_d;
+    uint64_t m = __ballot(pass);
+    if (m == 0) return;
+    if (ncand + __popcll(m) > 64) {
+      flush();
+      pass = pass && dk <= thr_d;
+      m = __ballot(pass);
+    }
+    if (pass) {
+      const int pos = ncand + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                            __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+      cbuf[w][pos] = make_uint2(dk, e);
+    }
+    ncand += __popcll(m);
   };
   // Probe pi scans table B while building table B^1 for probe pi+1 (L2),
   // two entries per thread between the first chunks so that the build's VALU
@@ -1061,6 +1101,7 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan16(const float* __restric
     probe_step(std::integral_constant<int, 0>{}, pi);
     if (pi + 1 < np) probe_step(std::integral_constant<int, 1>{}, pi + 1);
   }
+  if (ncand) flush();
   if (out_ids == nullptr) {
     uint64_t* o = out + (((size_t)q * groups + grp) * IVF_SW + w) * kk;
     if (lane < kk) o[lane] = kept;
