@@ -236,14 +236,12 @@ __global__ __launch_bounds__((SQ_NW + 1) * 64) void sq8_mfma_scan(
     int* __restrict__ ccount, uint64_t* __restrict__ cand, int cap) {
   constexpr int KP = KB * 32, SR = KP + 16, R = sq_rows(KB), RT = R / 32, QT = sq_qt(KB);
   constexpr int PPR = KP / 16;         // 16-byte pieces per row
-  constexpr int D = 2;                // LDS tile buffers: the next tile loads during the current one
+  constexpr int D = 3;                // LDS tile buffers: the next two tiles load during the current one
   __shared__ __align__(16) int8_t tile[D][R * SR];
-  __shared__ __align__(4) uint8_t vb[STAGE1 ? 2 : 1][R];
-  // stage 2: the 16 scores per lane of a recomputed tile with a passing
-  // score, scanned by a rolled loop (each lane reads back only its own
-  // values, so no barrier is needed); passing scores go to a workgroup list
-  // in LDS, filtered and published after the scan.
-  __shared__ int stash[STAGE1 ? 1 : SQ_NW * 16 * 64];
+  __shared__ __align__(4) uint8_t vb[STAGE1 ? D : 1][R];
+  // stage 2: passing scores of recomputed tiles go to a workgroup list in
+  // LDS, filtered and published after the scan. The tiles and the list fit
+  // two workgroups per CU (four compute waves per SIMD).
   __shared__ int lc_score[STAGE1 ? 1 : SQ_LCAP];
   __shared__ int lc_row[STAGE1 ? 1 : SQ_LCAP];
   __shared__ int lc_q[STAGE1 ? 1 : SQ_LCAP];
@@ -417,15 +415,12 @@ __global__ __launch_bounds__((SQ_NW + 1) * 64) void sq8_mfma_scan(
               for (int v = 0; v < 16; ++v) x[v] = 0;
 #pragma unroll
               for (int kb = 0; kb < KB; ++kb) x = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[kb], qa[qt][kb], x, 0, 0, 0);
-              int* sx = stash + w * 16 * 64 + lane;
-#pragma unroll
-              for (int v = 0; v < 16; ++v) sx[v * 64] = x[v];
               const int q = q0 + qt * 32 + r;
               const int tq = thr[qt];
               const int rowb = t * R + rt * 32 + 4 * h;
-#pragma unroll 1
+#pragma unroll
               for (int v = 0; v < 16; ++v) {
-                const int val = sx[v * 64];
+                const int val = x[v];
                 const int row = rowb + 8 * (v >> 2) + (v & 3);
                 if (val >= tq && row < N && q < nq) {
                   const int pos = atomicAdd(&lc_n, 1);
@@ -444,7 +439,12 @@ __global__ __launch_bounds__((SQ_NW + 1) * 64) void sq8_mfma_scan(
         }
       }
     }
-    __syncthreads();
+    // Tile barrier without the workgroup fence of __syncthreads: that fence
+    // would make the loader drain every LDS DMA in flight (vmcnt(0)), tile
+    // it+2's included. The loader has already waited for tile it+1 above;
+    // the compute waves' LDS appends complete before the barrier
+    // (lgkmcnt(0)); tile reads were consumed by their MFMAs.
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   }
   if constexpr (STAGE1) {
     if (active) {
