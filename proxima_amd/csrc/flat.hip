@@ -92,8 +92,8 @@ __device__ __forceinline__ uint32_t lds_u32(const float* p) {
 __device__ __forceinline__ void vm_wait0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 template <int CAP>
-__device__ inline void compact_row(uint64_t* __restrict__ base, int c, int Kp, int lane, uint64_t* thr_row,
-                                   float* thrf_row, int* cnt_row, unsigned long long* gthr_row, bool final_pass) {
+__device__ inline void compact_row_w(uint64_t* __restrict__ base, int c, int Kp, int lane, uint64_t* thr_row,
+                                     float* thrf_row, int* cnt_row, unsigned long long* gthr_row, bool final_pass) {
   constexpr int E = CAP / WAVE;
   uint64_t kk[E];
 #pragma unroll
@@ -117,12 +117,29 @@ __device__ inline void compact_row(uint64_t* __restrict__ base, int c, int Kp, i
   if (lane == 0 && !final_pass) *cnt_row = Kp;
 }
 
+// Keep the Kp smallest of a row's c buffered keys, sorted, KEY_MAX padded to
+// Kp: sorted over the narrowest width (64 keys per lane-slot step) that
+// holds max(c, Kp), up to the buffer's CAP.
+template <int CAP>
+__device__ inline void compact_row(uint64_t* __restrict__ base, int c, int Kp, int lane, uint64_t* thr_row,
+                                   float* thrf_row, int* cnt_row, unsigned long long* gthr_row, bool final_pass) {
+  const int need = c > Kp ? c : Kp;
+  if (need <= 64)
+    compact_row_w<64>(base, c, Kp, lane, thr_row, thrf_row, cnt_row, gthr_row, final_pass);
+  else if (need <= 128 && CAP >= 128)
+    compact_row_w<(CAP >= 128 ? 128 : CAP)>(base, c, Kp, lane, thr_row, thrf_row, cnt_row, gthr_row, final_pass);
+  else if (need <= 256 && CAP >= 256)
+    compact_row_w<(CAP >= 256 ? 256 : CAP)>(base, c, Kp, lane, thr_row, thrf_row, cnt_row, gthr_row, final_pass);
+  else
+    compact_row_w<CAP>(base, c, Kp, lane, thr_row, thrf_row, cnt_row, gthr_row, final_pass);
+}
+
 template <int CAP>
 __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
     const float* __restrict__ Q, int nq, const float* __restrict__ X, int N, int ld,
     const float* __restrict__ qb, const float* __restrict__ xb, float scale, const uint8_t* __restrict__ live,
-    const uint8_t* __restrict__ accept, int S, int QB, int per_split, int Kp, uint64_t* __restrict__ cand,
-    unsigned long long* __restrict__ gthr) {
+    const uint8_t* __restrict__ accept, int S, int QB, int per_split, int max_tiles, int Kp,
+    uint64_t* __restrict__ cand, unsigned long long* __restrict__ gthr) {
   __shared__ __align__(16) float sQ[2][FB_M * FB_K];
   __shared__ __align__(16) float sX[2][FB_N * FB_K];
   __shared__ uint64_t thr[FB_M];
@@ -142,7 +159,8 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
   const int qblk = g % QB, split = g / QB;
   const int q0 = qblk * FB_M;
   const int s_begin = split * per_split;
-  const int s_end = min(N, s_begin + per_split);
+  // a seeding pass visits only the first max_tiles tiles of each split
+  const int s_end = min(N, s_begin + (int)min((long long)per_split, (long long)max_tiles * FB_N));
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int h = lane >> 5, r = lane & 31;
@@ -337,6 +355,22 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
 // ---------------------------------------------------------------------------
 // 3. merge + exact rescore (approximate candidates)
 // ---------------------------------------------------------------------------
+// Per query: the Kp-th smallest key over every split's list from a pass that
+// visited only the first tile of each split (each list holds that split's Kp
+// best keys, sorted, KEY_MAX padded). The full pass meets all of those rows
+// again, so a threshold just above that key (every key at or below it
+// passes the strict test) leaves the query's Kp best rows in its lists.
+__global__ __launch_bounds__(256) void flat_seed_threshold(const uint64_t* __restrict__ cand, int S, int CAP, int Kp,
+                                                           unsigned long long* __restrict__ gthr) {
+  __shared__ int hist[256];
+  __shared__ uint64_t sh[4];
+  const int q = blockIdx.x;
+  const uint64_t* c = cand + (size_t)q * S * CAP;
+  auto get = [&](int i) { return c[(size_t)(i / Kp) * CAP + i % Kp]; };
+  const uint64_t pivot = block_radix_select(get, S * Kp, Kp, hist, sh);
+  if (threadIdx.x == 0 && pivot != KEY_MAX) atomicMin(gthr + q, (unsigned long long)(pivot + 1));
+}
+
 constexpr int MERGE_MAXP = 512;
 
 __global__ __launch_bounds__(256) void flat_merge_rescore(
@@ -605,13 +639,26 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
     tm.mark(1);
     const int grid = ((total + 7) / 8) * 8;
     const float scale = metric == PXG_EUCLIDEAN ? 2.0f : 1.0f;
-    if (CAP == 256)
-      hipLaunchKernelGGL(flat_mfma_candidates<256>, dim3(grid), dim3(256), 0, s, Qp, (int)nq, X.p, (int)N, (int)ld,
-                         qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, Kp, cand, gthr);
-    else
-      hipLaunchKernelGGL(flat_mfma_candidates<512>, dim3(grid), dim3(256), 0, s, Qp, (int)nq, X.p, (int)N, (int)ld,
-                         qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, Kp, cand, gthr);
-    PXG_HIP(hipGetLastError());
+    auto candidates = [&](int max_tiles) {
+      if (CAP == 256)
+        hipLaunchKernelGGL(flat_mfma_candidates<256>, dim3(grid), dim3(256), 0, s, Qp, (int)nq, X.p, (int)N, (int)ld,
+                           qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, max_tiles, Kp, cand, gthr);
+      else
+        hipLaunchKernelGGL(flat_mfma_candidates<512>, dim3(grid), dim3(256), 0, s, Qp, (int)nq, X.p, (int)N, (int)ld,
+                           qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, max_tiles, Kp, cand, gthr);
+      PXG_HIP(hipGetLastError());
+    };
+    // With several tiles per split, a first pass over the first tile of each
+    // split (spread over the whole store) seeds each query's threshold with
+    // the Kp-th best of those rows, so the full pass appends and compacts
+    // little from its first tile on.
+    if (tiles_per >= 8) {
+      candidates(1);
+      hipLaunchKernelGGL(flat_seed_threshold, dim3((unsigned)nq), dim3(256), 0, s, (const uint64_t*)cand, S, CAP, Kp,
+                         gthr);
+      PXG_HIP(hipGetLastError());
+    }
+    candidates(tiles_per);
     tm.mark(2);
     hipLaunchKernelGGL(flat_merge_rescore, dim3((unsigned)nq), dim3(256), 0, s, cand, S, CAP, Kp, (int)kq, Qp,
                        (int)ld, (int)dim, metric, X.p, ranks.rank.p, ranks.rank_slot.p, d_ids.p, qn, maxnorm, 4.0f,
