@@ -213,18 +213,19 @@ __device__ inline void wave_bitonic_sort(uint64_t (&k)[E], int lane) {
 }
 
 // ----------------------------------------------------------------------------
-// Block radix select: the K-th smallest (1-based) of n unique 64-bit keys
-// read through `get(i)`. All threads of the block call it; returns the pivot
-// in every thread. `hist` is 256 ints of shared memory, `sh` 4 u64 of shared.
-// Keys equal to KEY_MAX are padding and never selected; the caller clamps K
-// to the number of real keys.
+// Block radix select: the K-th smallest (1-based, counting repeats) of n
+// BITS-bit keys read through `get(i)`. All threads of the block call it;
+// returns the pivot in every thread. `hist` is 256 ints of shared memory,
+// `sh` 4 u64 of shared. Keys equal to KEY_MAX are padding and never
+// selected; the caller clamps K to the number of real keys.
 // ----------------------------------------------------------------------------
-template <class Get>
+template <class Get, int BITS = 64>
 __device__ inline uint64_t block_radix_select(Get get, int n, int K, int* hist, uint64_t* sh) {
+  static_assert(BITS % 8 == 0 && BITS <= 64, "whole-byte digits");
   uint64_t prefix = 0, mask = 0;
   int remaining = K;
-  for (int pass = 0; pass < 8; ++pass) {
-    const int shift = 56 - 8 * pass;
+  for (int pass = 0; pass < BITS / 8; ++pass) {
+    const int shift = BITS - 8 - 8 * pass;
     for (int i = threadIdx.x; i < 256; i += blockDim.x) hist[i] = 0;
     __syncthreads();
     for (int i = threadIdx.x; i < n; i += blockDim.x) {

@@ -138,7 +138,7 @@ template <int CAP>
 __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
     const float* __restrict__ Q, int nq, const float* __restrict__ X, int N, int ld,
     const float* __restrict__ qb, const float* __restrict__ xb, float scale, const uint8_t* __restrict__ live,
-    const uint8_t* __restrict__ accept, int S, int QB, int per_split, int max_tiles, int Kp,
+    const uint8_t* __restrict__ accept, int S, int QB, int per_split, int seed, int Kp,
     uint64_t* __restrict__ cand, unsigned long long* __restrict__ gthr) {
   __shared__ __align__(16) float sQ[2][FB_M * FB_K];
   __shared__ __align__(16) float sX[2][FB_N * FB_K];
@@ -159,8 +159,8 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
   const int qblk = g % QB, split = g / QB;
   const int q0 = qblk * FB_M;
   const int s_begin = split * per_split;
-  // a seeding pass visits only the first max_tiles tiles of each split
-  const int s_end = min(N, s_begin + (int)min((long long)per_split, (long long)max_tiles * FB_N));
+  // a seeding pass visits only the first tile of each split
+  const int s_end = min(N, s_begin + (seed ? FB_N : per_split));
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int h = lane >> 5, r = lane & 31;
@@ -344,6 +344,16 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
     }
     __syncthreads();
   }
+  if (seed) {
+    // Seeding pass: each row leaves its one tile's keys unsorted, KEY_MAX
+    // padded to FB_N.
+    for (int row = wid; row < FB_M; row += 4) {
+      if (q0 + row >= nq) continue;
+      uint64_t* base = cand + ((size_t)(q0 + row) * S + split) * CAP;
+      for (int i = cnt[row] + lane; i < FB_N; i += WAVE) base[i] = KEY_MAX;
+    }
+    return;
+  }
   // Final: every row leaves exactly Kp sorted keys (KEY_MAX padded).
   for (int row = wid; row < FB_M; row += 4) {
     if (q0 + row >= nq) continue;
@@ -355,20 +365,20 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
 // ---------------------------------------------------------------------------
 // 3. merge + exact rescore (approximate candidates)
 // ---------------------------------------------------------------------------
-// Per query: the Kp-th smallest key over every split's list from a pass that
-// visited only the first tile of each split (each list holds that split's Kp
-// best keys, sorted, KEY_MAX padded). The full pass meets all of those rows
-// again, so a threshold just above that key (every key at or below it
-// passes the strict test) leaves the query's Kp best rows in its lists.
-__global__ __launch_bounds__(256) void flat_seed_threshold(const uint64_t* __restrict__ cand, int S, int CAP, int Kp,
+// Per query: the Kp-th smallest distance part over the keys a seeding pass
+// left (the first tile of every split, FB_N keys per split, KEY_MAX padded).
+// The full pass meets all of those rows again, so a threshold above every
+// key with that distance part (the strict key test passes them all) leaves
+// at least Kp rows, the query's Kp best among them, in its lists.
+__global__ __launch_bounds__(512) void flat_seed_threshold(const uint64_t* __restrict__ cand, int S, int CAP, int Kp,
                                                            unsigned long long* __restrict__ gthr) {
   __shared__ int hist[256];
   __shared__ uint64_t sh[4];
   const int q = blockIdx.x;
   const uint64_t* c = cand + (size_t)q * S * CAP;
-  auto get = [&](int i) { return c[(size_t)(i / Kp) * CAP + i % Kp]; };
-  const uint64_t pivot = block_radix_select(get, S * Kp, Kp, hist, sh);
-  if (threadIdx.x == 0 && pivot != KEY_MAX) atomicMin(gthr + q, (unsigned long long)(pivot + 1));
+  auto get = [&](int i) { return c[(size_t)(i / FB_N) * CAP + i % FB_N] >> 32; };
+  const uint64_t hi = block_radix_select<decltype(get), 32>(get, S * FB_N, Kp, hist, sh);
+  if (threadIdx.x == 0 && hi != 0xFFFFFFFFull) atomicMin(gthr + q, (unsigned long long)((hi << 32) | 0xFFFFFFFFull));
 }
 
 constexpr int MERGE_MAXP = 512;
@@ -639,13 +649,13 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
     tm.mark(1);
     const int grid = ((total + 7) / 8) * 8;
     const float scale = metric == PXG_EUCLIDEAN ? 2.0f : 1.0f;
-    auto candidates = [&](int max_tiles) {
+    auto candidates = [&](int seed) {
       if (CAP == 256)
         hipLaunchKernelGGL(flat_mfma_candidates<256>, dim3(grid), dim3(256), 0, s, Qp, (int)nq, X.p, (int)N, (int)ld,
-                           qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, max_tiles, Kp, cand, gthr);
+                           qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, seed, Kp, cand, gthr);
       else
         hipLaunchKernelGGL(flat_mfma_candidates<512>, dim3(grid), dim3(256), 0, s, Qp, (int)nq, X.p, (int)N, (int)ld,
-                           qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, max_tiles, Kp, cand, gthr);
+                           qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, seed, Kp, cand, gthr);
       PXG_HIP(hipGetLastError());
     };
     // With several tiles per split, a first pass over the first tile of each
@@ -654,11 +664,11 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
     // little from its first tile on.
     if (tiles_per >= 8) {
       candidates(1);
-      hipLaunchKernelGGL(flat_seed_threshold, dim3((unsigned)nq), dim3(256), 0, s, (const uint64_t*)cand, S, CAP, Kp,
+      hipLaunchKernelGGL(flat_seed_threshold, dim3((unsigned)nq), dim3(512), 0, s, (const uint64_t*)cand, S, CAP, Kp,
                          gthr);
       PXG_HIP(hipGetLastError());
     }
-    candidates(tiles_per);
+    candidates(0);
     tm.mark(2);
     hipLaunchKernelGGL(flat_merge_rescore, dim3((unsigned)nq), dim3(256), 0, s, cand, S, CAP, Kp, (int)kq, Qp,
                        (int)ld, (int)dim, metric, X.p, ranks.rank.p, ranks.rank_slot.p, d_ids.p, qn, maxnorm, 4.0f,

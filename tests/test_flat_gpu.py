@@ -340,6 +340,36 @@ def test_thresholds_shared_across_splits(gpu, metric):
     assert_same(got, oracle_search(px, data, ids, metric, q, 10, accept=acc))
 
 
+@pytest.mark.parametrize("metric", [0, 1])
+def test_seeded_thresholds(gpu, metric):
+    """With many tiles per split, a first pass over one tile of every split
+    seeds each query's threshold before the full pass. Integer data (exact
+    distance ties at the seed), removed rows, a filter, queries whose
+    neighbours all sit past the sampled tiles, and k from 1 to 100: ids and
+    distances match the oracle bit for bit."""
+    px = gpu
+    rng = np.random.default_rng(5 + metric)
+    n, dim, nq = 140_000, 16, 1024  # 8 query blocks x 61 splits of 18 tiles (2304 rows)
+    data = rng.integers(-2, 3, (n, dim)).astype(np.float32)
+    ids = rng.permutation(n).astype(np.uint64)
+    idx = make_index(px, data, metric, ids, mode=1)
+    gone = rng.choice(n, 3000, replace=False)
+    for i in gone:
+        idx.remove(int(ids[i]))
+    live = np.ones(n, np.uint8)
+    live[gone] = 0
+    # rows 128..255 of every split are never sampled: aim half the queries
+    # there, with a shift that no sampled row shares
+    far = np.concatenate([np.arange(s + 128, s + 256) for s in range(0, n - 256, 2304)])
+    q = np.concatenate([data[rng.choice(far, nq // 2)] + np.float32(0.25),
+                        rng.integers(-2, 3, (nq // 2, dim)).astype(np.float32)])
+    for k in (1, 10, 100):
+        assert_same(idx.search_batch(q, k), oracle_search(px, data, ids, metric, q, k, live=live))
+    acc = np.array([int(i) % 4 == 1 for i in ids], np.uint8)
+    got = idx.search_batch(q, 10, lambda i, _m: i % 4 == 1)
+    assert_same(got, oracle_search(px, data, ids, metric, q, 10, live=live, accept=acc))
+
+
 # --- k beyond the block selections (check_k allows up to 2^24, index.rs:212-224) ----------
 @pytest.mark.parametrize("metric", [0, 2, 3])
 def test_large_k_matches_oracle(gpu, metric):
