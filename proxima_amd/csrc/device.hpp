@@ -228,10 +228,23 @@ __device__ inline uint64_t block_radix_select(Get get, int n, int K, int* hist, 
     const int shift = BITS - 8 - 8 * pass;
     for (int i = threadIdx.x; i < 256; i += blockDim.x) hist[i] = 0;
     __syncthreads();
+    // runs of one digit in a thread's keys go in as one add (the leading
+    // digits are often shared by most keys, which would otherwise serialise
+    // every add on one bin)
+    int run_d = -1, run_n = 0;
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
-      uint64_t x = get(i);
-      if ((x & mask) == prefix) atomicAdd(&hist[(x >> shift) & 255], 1);
+      const uint64_t x = get(i);
+      if ((x & mask) == prefix) {
+        const int dg = (int)((x >> shift) & 255);
+        if (dg != run_d) {
+          if (run_n) atomicAdd(&hist[run_d], run_n);
+          run_d = dg;
+          run_n = 0;
+        }
+        ++run_n;
+      }
     }
+    if (run_n) atomicAdd(&hist[run_d], run_n);
     __syncthreads();
     if (threadIdx.x < WAVE) {
       // exclusive scan over 256 bins by one wave: 4 bins per lane

@@ -180,6 +180,11 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
   [[maybe_unused]] const int crow = 32 * wid + (lane >> 3), cchunk = (lane & 7) ^ ((lane >> 3) & 7);
   [[maybe_unused]] const int wid_s = __builtin_amdgcn_readfirstlane(wid);
   const int nK = (ld + FB_K - 1) / FB_K;
+  // The two slice buffers alternate over the whole run of tiles (gs counts
+  // the slices consumed so far): the last slice of a tile prefetches the
+  // first slice of the next, so only the first tile waits for its first
+  // slice.
+  int gs = 0;
 
   for (int n0 = s_begin; n0 < s_end; n0 += FB_N) {
     // the other splits' published thresholds for this tile's rows, read now
@@ -212,16 +217,18 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
         for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
 #if defined(__HIP_DEVICE_COMPILE__)
-    // Buffer loads over this tile's query and slot rows, straight to LDS:
-    // rows past the valid ones, and the chunks past a row's end in the last
-    // slice of a stride that is not a multiple of FB_K, are given an offset
-    // outside the resource and land as zeros.
+    // Buffer loads over a tile's query and slot rows, straight to LDS: rows
+    // past the valid ones, and the chunks past a row's end in the last slice
+    // of a stride that is not a multiple of FB_K, are given an offset outside
+    // the resource and land as zeros.
     const float* q_rows = Q + (size_t)q0 * ld;
-    const float* x_rows = X + (size_t)n0 * ld;
-    const int q_bytes = max(min(nq - q0, FB_M), 0) * ld * 4, x_bytes = max(min(s_end - n0, FB_N), 0) * ld * 4;
+    const int q_bytes = max(min(nq - q0, FB_M), 0) * ld * 4;
 #endif
-    auto gload = [&](int k0, int buf) {
+    // slice k0 of the tile starting at slot t0, into buffer buf
+    auto gload = [&](int t0, int k0, int buf) {
 #if defined(__HIP_DEVICE_COMPILE__)
+      const float* x_rows = X + (size_t)t0 * ld;
+      const int x_bytes = max(min(s_end - t0, FB_N), 0) * ld * 4;
       // the resources are rebuilt per call from readfirstlane'd scalars (a
       // hoisted resource kept in VGPRs is not known to be uniform)
       const __amdgpu_buffer_rsrc_t rs_q = uniform_rsrc(q_rows, q_bytes);
@@ -240,12 +247,15 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
 #endif
     };
 
-    gload(0, 0);
-    vm_wait0();
-    __syncthreads();
+    if (n0 == s_begin) {
+      gload(n0, 0, gs & 1);
+      vm_wait0();
+      __syncthreads();
+    }
     for (int kt = 0; kt < nK; ++kt) {
-      const int cur = kt & 1;
-      if (kt + 1 < nK) gload((kt + 1) * FB_K, cur ^ 1);
+      const int cur = (gs + kt) & 1;
+      if (kt + 1 < nK) gload(n0, (kt + 1) * FB_K, cur ^ 1);
+      else if (n0 + FB_N < s_end) gload(n0 + FB_N, 0, cur ^ 1);
       // Lane (h, r) feeds k = h*16 + kk of row r: the MFMA pairs A and B by
       // lane half, so any fixed permutation of k within the slice is a
       // valid dot product; this one lets each lane read 16 contiguous floats
@@ -276,6 +286,7 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
       vm_wait0();  // this wave's copies of the next slice have landed
       __syncthreads();
     }
+    gs += nK;
     if (tid < FB_M && g_thr < thr[tid]) {
       thr[tid] = g_thr;
       thr_f[tid] = key_float((uint32_t)(g_thr >> 32));
