@@ -51,7 +51,7 @@ typedef int i4v __attribute__((ext_vector_type(4)));
 typedef int i16v __attribute__((ext_vector_type(16)));
 
 constexpr int SQ_NW = 8;              // waves per scan workgroup
-constexpr int SQ_SAMPLE = 8;          // stage 1 visits at most one row tile in 8
+constexpr int SQ_SAMPLE = 16;         // stage 1 visits at most one row tile in 16
 constexpr int SQ_MAX_CHUNKS = 1024;   // stage-1 entries per query <= 2 * this
 constexpr int SQ_MAX_KB = 8;          // MFMA path: code rows up to 256 bytes
 constexpr uint32_t SQ_MAX_DIM = 65536;  // |S| < 2^31
