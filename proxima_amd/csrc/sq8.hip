@@ -471,15 +471,18 @@ __global__ __launch_bounds__((SQ_NW + 1) * 64) void sq8_mfma_scan(
 // Per query: the k-th largest of its E stage-1 maxima (INT_MIN when E < k).
 __global__ __launch_bounds__(256) void sq8_thresholds(const int* __restrict__ tmax, int E, int k,
                                                       int* __restrict__ thr) {
-  __shared__ uint64_t keys[2 * SQ_MAX_CHUNKS];
+  __shared__ int hist[256];
+  __shared__ uint64_t sh[4];
   const int q = blockIdx.x;
-  int P = 1;
-  while (P < E) P <<= 1;
-  for (int i = threadIdx.x; i < P; i += blockDim.x)
-    keys[i] = i < E ? (uint64_t)((int64_t)INT_MAX - (int64_t)tmax[(size_t)q * E + i]) : KEY_MAX;
-  __syncthreads();
-  block_bitonic_sort(keys, P);
-  if (threadIdx.x == 0) thr[q] = k <= E ? (int)((int64_t)INT_MAX - (int64_t)keys[k - 1]) : INT_MIN;
+  if (k > E) {
+    if (threadIdx.x == 0) thr[q] = INT_MIN;
+    return;
+  }
+  // the k-th largest maximum: the k-th smallest of INT_MAX - v (in [0, 2^32))
+  const int* t = tmax + (size_t)q * E;
+  auto get = [&](int i) { return (uint64_t)((int64_t)INT_MAX - (int64_t)t[i]); };
+  const uint64_t v = block_radix_select<decltype(get), 32>(get, E, k, hist, sh);
+  if (threadIdx.x == 0) thr[q] = (int)((int64_t)INT_MAX - (int64_t)v);
 }
 
 // Per query: sort the appended candidates and keep the first kk; a query
