@@ -51,7 +51,7 @@ typedef int i4v __attribute__((ext_vector_type(4)));
 typedef int i16v __attribute__((ext_vector_type(16)));
 
 constexpr int SQ_NW = 8;              // waves per scan workgroup
-constexpr int SQ_SAMPLE = 16;         // stage 1 visits at most one row tile in 16
+constexpr int SQ_SAMPLE = 12;         // stage 1 visits at most one row tile in 12
 constexpr int SQ_MAX_CHUNKS = 1024;   // stage-1 entries per query <= 2 * this
 constexpr int SQ_MAX_KB = 8;          // MFMA path: code rows up to 256 bytes
 constexpr uint32_t SQ_MAX_DIM = 65536;  // |S| < 2^31
@@ -368,14 +368,32 @@ __global__ __launch_bounds__((SQ_NW + 1) * 64) void sq8_mfma_scan(
           for (int qt = 0; qt < QT; ++qt)
             acc[qt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[kb], qa[qt][kb], acc[qt], 0, 0, 0);
         if constexpr (STAGE1) {
+          uint32_t vw[4];
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const uint32_t vw = *reinterpret_cast<const uint32_t*>(&vb[buf][rt * 32 + 8 * g + 4 * h]);
+          for (int g = 0; g < 4; ++g) vw[g] = *reinterpret_cast<const uint32_t*>(&vb[buf][rt * 32 + 8 * g + 4 * h]);
+          if (__all((vw[0] & vw[1] & vw[2] & vw[3]) == 0x01010101u)) {
+            // every row of the 32 x 32 tile is usable: a v_max3 chain
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const bool ok = (vw >> (8 * j)) & 1u;
+            for (int qt = 0; qt < QT; ++qt) {
+              const i16v x = acc[qt];
+              int m = max(max(run[qt], x[0]), x[1]);
+              m = max(max(m, x[2]), x[3]);
+              m = max(max(m, x[4]), x[5]);
+              m = max(max(m, x[6]), x[7]);
+              m = max(max(m, x[8]), x[9]);
+              m = max(max(m, x[10]), x[11]);
+              m = max(max(m, x[12]), x[13]);
+              run[qt] = max(max(m, x[14]), x[15]);
+            }
+          } else {
 #pragma unroll
-              for (int qt = 0; qt < QT; ++qt) run[qt] = ok ? max(run[qt], acc[qt][4 * g + j]) : run[qt];
+            for (int g = 0; g < 4; ++g) {
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                const bool ok = (vw[g] >> (8 * j)) & 1u;
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) run[qt] = ok ? max(run[qt], acc[qt][4 * g + j]) : run[qt];
+              }
             }
           }
         } else {
