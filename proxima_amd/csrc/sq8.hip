@@ -513,7 +513,11 @@ __global__ __launch_bounds__(256) void sq8_finish(const int* __restrict__ ccount
   const int q = blockIdx.x;
   const int c = ccount[q];
   if (c > cap) {
-    if (threadIdx.x == 0) flag_list[atomicAdd(flag_count, 1)] = q;
+    // listed for the exact scan; no result until then
+    if (threadIdx.x == 0) {
+      flag_list[atomicAdd(flag_count, 1)] = q;
+      ocount[q] = 0;
+    }
     return;
   }
   int P = 1;
@@ -1087,6 +1091,21 @@ struct Sq8Index {
     const int ntiles_all = KB <= SQ_MAX_KB ? (N + sq_rows(KB) - 1) / sq_rows(KB) : 0;
     const bool mfma = mode != 2 && KB <= SQ_MAX_KB && (mode == 1 || (N >= 4096 && 2 * ntiles_all >= 4 * kk));
     int nflag = 0;
+    // ids and distances (or the f32 rescoring) of each query's kept keys
+    auto emit = [&]() {
+      if (rescore) {
+        int P = 1;
+        while (P < kk) P <<= 1;
+        hipLaunchKernelGGL(sq8_rescore, dim3((unsigned)nq), dim3(256), (size_t)P * 8, s, (const uint64_t*)okeys,
+                           (const uint32_t*)ocount, kk, (int)ldo, (const float*)Qp, (int)ld, (int)dim,
+                           (const int8_t*)codes.p, (int)KP, per_dim, d_mn.p, d_scale.p, ranks.rank_slot.p, d_ids.p,
+                           d_oid, d_od, d_oc);
+      } else {
+        hipLaunchKernelGGL(sq8_emit, dim3((unsigned)nq), dim3(64), 0, s, (const uint64_t*)okeys,
+                           (const uint32_t*)ocount, kk, (int)ldo, ranks.rank_slot.p, d_ids.p, d_oid, d_od, d_oc);
+      }
+      PXG_HIP(hipGetLastError());
+    };
     if (mfma) {
       const int R = sq_rows(KB), QT = sq_qt(KB);
       // Chunks: about 512 (two per CU), and at least 2 * kk so that every
@@ -1147,6 +1166,10 @@ struct Sq8Index {
       hipLaunchKernelGGL(sq8_finish, dim3((unsigned)nq), dim3(256), (size_t)cap_c * 8, s, (const int*)ccount,
                          (const uint64_t*)cand, cap_c, kk, okeys, ocount, flag_list, flag_count);
       PXG_HIP(hipGetLastError());
+      // The results go out before the one host round trip; a query listed
+      // for the exact scan has none yet, and its results are emitted again
+      // after that scan.
+      emit();
       // bad (8 bytes) and flag_count (the int after it) in one copy
       unsigned long long* tail = sc.host_words();
       PXG_HIP(hipMemcpyAsync(tail, bad, 16, hipMemcpyDeviceToHost, s));
@@ -1175,23 +1198,12 @@ struct Sq8Index {
                          (const int*)flag_count, (const uint64_t*)ecand, nchunks, kk, ranks.rank_slot.p, d_ids.p,
                          (uint64_t*)nullptr, (float*)nullptr, ocount, okeys, (size_t)kk);
       PXG_HIP(hipGetLastError());
+      emit();
+      unsigned long long* tail = sc.host_words();
+      if (d_raw && !mfma) PXG_HIP(hipMemcpyAsync(tail, bad, 8, hipMemcpyDeviceToHost, s));
+      PXG_HIP(hipStreamSynchronize(s));
+      if (d_raw && !mfma) check_non_finite(tail[0]);
     }
-    if (rescore) {
-      int P = 1;
-      while (P < kk) P <<= 1;
-      hipLaunchKernelGGL(sq8_rescore, dim3((unsigned)nq), dim3(256), (size_t)P * 8, s, (const uint64_t*)okeys,
-                         (const uint32_t*)ocount, kk, (int)ldo, (const float*)Qp, (int)ld, (int)dim,
-                         (const int8_t*)codes.p, (int)KP, per_dim, d_mn.p, d_scale.p, ranks.rank_slot.p, d_ids.p, d_oid,
-                         d_od, d_oc);
-    } else {
-      hipLaunchKernelGGL(sq8_emit, dim3((unsigned)nq), dim3(64), 0, s, (const uint64_t*)okeys,
-                         (const uint32_t*)ocount, kk, (int)ldo, ranks.rank_slot.p, d_ids.p, d_oid, d_od, d_oc);
-    }
-    PXG_HIP(hipGetLastError());
-    unsigned long long* tail = sc.host_words();
-    if (d_raw && !mfma) PXG_HIP(hipMemcpyAsync(tail, bad, 8, hipMemcpyDeviceToHost, s));
-    PXG_HIP(hipStreamSynchronize(s));
-    if (d_raw && !mfma) check_non_finite(tail[0]);
     tm.finish();
   }
 
