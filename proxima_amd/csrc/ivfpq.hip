@@ -32,7 +32,7 @@
 //               l2 += d*d; ip += q*c), stream the list's codes coalesced,
 //               ADC-sum the table in subspace order (bit-exact), keep a
 //               per-wave top-kk by (score, id): ivf_scan16 (16 subspaces,
-//               dim <= 128, kk <= 64: codebook rows in VGPRs, one workgroup
+//               dim <= 128, kk <= 128: codebook rows in VGPRs, one workgroup
 //               per query and up to 32 probes, codes staged through LDS by
 //               asynchronous copies, id ranks fetched only for entries whose
 //               score passes the wave's current k-th distance),
@@ -252,6 +252,22 @@ __device__ inline void wave_merge_sorted(uint64_t& kept, uint64_t other, int lan
     v = (lane & st) ? (v < p ? p : v) : (v < p ? v : p);
   }
   kept = v;
+}
+
+// The 128 keys of two ascending lists (one key per lane each) as two
+// ascending lists: lo the 64 smallest, hi the other 64. Min and max against
+// the reversed b are the two bitonic halves; a half-cleaner cascade sorts each.
+__device__ inline void wave_merge_split(uint64_t a, uint64_t b, int lane, uint64_t& lo, uint64_t& hi) {
+  const uint64_t r = ((uint64_t)lane_reverse((uint32_t)(b >> 32)) << 32) | lane_reverse((uint32_t)b);
+  uint64_t l = a < r ? a : r, h = a < r ? r : a;
+#pragma unroll
+  for (int st = 32; st > 0; st >>= 1) {
+    const uint64_t pl = shfl_xor64(l, st), ph = shfl_xor64(h, st);
+    l = (lane & st) ? (l < pl ? pl : l) : (l < pl ? l : pl);
+    h = (lane & st) ? (h < ph ? ph : h) : (h < ph ? h : ph);
+  }
+  lo = l;
+  hi = h;
 }
 
 // Add one candidate key per lane to the sorted list: a batch with many
@@ -991,7 +1007,7 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan16(const float* __restric
   cend = pend;
   int issued = 0, consumed = 0;
   uint8_t* myring = &ring[w][0][0];
-  auto issue = [&]() {
+  auto issue = [&]() __attribute__((always_inline)) {
     uint8_t* slot = myring + (issued % IVF_NS) * IVF_CHUNK;
     const uint32_t e = pe + lane;
     const uint32_t a = __builtin_amdgcn_readfirstlane(lds_addr(slot));
@@ -1007,7 +1023,9 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan16(const float* __restric
     build_part(I0{}, I8{}, rv, tabs[0]);
   }
   __syncthreads();
-  uint64_t kept = KEY_MAX, thr = KEY_MAX;
+  // the wave's best keys, ascending, one per lane: kept the first 64 and,
+  // for a shortlist above 64, kept2 the next 64
+  uint64_t kept = KEY_MAX, kept2 = KEY_MAX, thr = KEY_MAX;
   // Candidates are screened on the distance key alone: an entry whose key
   // exceeds the distance of the wave's kk-th kept key cannot enter the wave's
   // top kk, whatever its id rank. The rest (ties included) wait in cbuf as
@@ -1017,7 +1035,7 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan16(const float* __restric
   // that pass, and the screen threshold only tightens, at flushes.
   uint32_t thr_d = 0xFFFFFFFFu;  // distance part of thr
   int ncand = 0;                 // pending candidates (wave-uniform)
-  auto flush = [&]() {
+  auto flush = [&]() __attribute__((always_inline)) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -1028,8 +1046,18 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan16(const float* __restric
       if (accept == nullptr || accept[rank_slot[rk]]) b[0] = ((uint64_t)c.x << 32) | rk;
     }
     wave_bitonic_sort<1>(b, lane);
-    wave_merge_sorted(kept, b[0], lane);
-    thr = readlane64(kept, kk - 1);
+    if (kk > 64) {
+      // the 64 smallest of kept and the batch stay first; the rest competes
+      // with kept2 for the next 64 (no key of kept2 is below any of kept)
+      uint64_t lo, hi;
+      wave_merge_split(kept, b[0], lane, lo, hi);
+      kept = lo;
+      wave_merge_sorted(kept2, hi, lane);
+      thr = readlane64(kept2, kk - 65);
+    } else {
+      wave_merge_sorted(kept, b[0], lane);
+      thr = readlane64(kept, kk - 1);
+    }
     thr_d = (uint32_t)(thr >> 32);
     ncand = 0;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -1039,7 +1067,7 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan16(const float* __restric
   // One consumer iteration: refill the slot read in the previous iteration
   // (its reads are done), wait for this chunk (the chunks issued after it
   // stay in flight), score it and queue the entries that pass the screen.
-  auto chunk = [&](const float* tab, float one_minus_qdc) {
+  auto chunk = [&](const float* tab, float one_minus_qdc) __attribute__((always_inline)) {
     if (pp < np) issue();
     static_assert(IVF_NS <= 3, "the waits below cover up to two later chunks");
     const int later = issued - consumed - 1;
@@ -1078,7 +1106,7 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan16(const float* __restric
   // Probe pi scans table B while building table B^1 for probe pi+1 (L2),
   // two entries per thread between the first chunks so that the build's VALU
   // work overlaps the lookups' LDS latency.
-  auto probe_step = [&](auto bc, int pi) {
+  auto probe_step = [&](auto bc, int pi) __attribute__((always_inline)) {
     constexpr int B = decltype(bc)::value;
     const float* tab = tabs[METRIC == 0 ? B : 0];
     const float one_minus_qdc = METRIC == 1 ? arm_nan(1.0f - s_qdc[pi]) : 0.0f;
@@ -1105,6 +1133,7 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan16(const float* __restric
   if (out_ids == nullptr) {
     uint64_t* o = out + (((size_t)q * groups + grp) * IVF_SW + w) * kk;
     if (lane < kk) o[lane] = kept;
+    if (64 + lane < kk) o[64 + lane] = kept2;
     return;
   }
   // One group per query and no rerank: merge the waves' sorted lists here
@@ -2143,10 +2172,13 @@ struct IvfPqIndex {
       const int W = (int)(dim / M());
       // the register-codebook scans keep two distance tables in LDS (one for
       // cosine): an L2 index with 128 subspaces takes the general scan
-      const bool reg_path = !wide && dim <= 128 && dim % M() == 0 && kk <= 64 &&
-                            (W == 1 || W == 2 || W == 4 || W == 8 || W == 16 || W == 32) &&
-                            (metric == PXG_COSINE || M() <= 64);
-      const bool staged16 = reg_path && M() == 16;
+      // (the 16-subspace scan keeps shortlists up to 128 per wave, the
+      // other register-codebook scan up to 64)
+      const bool reg_shape = !wide && dim <= 128 && dim % M() == 0 &&
+                             (W == 1 || W == 2 || W == 4 || W == 8 || W == 16 || W == 32) &&
+                             (metric == PXG_COSINE || M() <= 64);
+      const bool staged16 = reg_shape && M() == 16 && kk <= 128;
+      const bool reg_path = reg_shape && (kk <= 64 || staged16);
       if (reg_path) {
         const size_t lds = (size_t)(metric == PXG_COSINE ? 1 : 2) * M() * 256 * 4;
         // probes per workgroup: up to IVF_PGMAX, fewer when that would leave
@@ -2157,8 +2189,9 @@ struct IvfPqIndex {
         uint64_t* cand = (uint64_t*)sc.get(10, (size_t)nq * groups * IVF_SW * kk * 8);
         const int grid = (int)(nq * groups);
         tm.mark(1);
-        // one group per query and no rerank: the scan writes the results
-        const bool fused = groups == 1 && !rerank;
+        // one group per query, no rerank and a shortlist within one key per
+        // lane: the scan writes the results
+        const bool fused = groups == 1 && !rerank && kk <= 64;
 #define PXG_SCANR(WW, MET)                                                                                          \
   hipLaunchKernelGGL((ivf_scan_reg<WW, MET>), dim3(grid), dim3(IVF_SW * 64), lds, s, Qp, (int)ld, (int)dim,        \
                      (int)M(), probes, np, pg, groups, cents.p, books.p, list_off.p, list_rank.p, list_codes.p,      \

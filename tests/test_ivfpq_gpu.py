@@ -294,9 +294,12 @@ def test_insert_device_matches_host_insert(gpu):
     assert len(b) == 1500
 
 
-@pytest.mark.parametrize("dim,m,k,rerank", [(20, 8, 10, 0), (32, 16, 100, 0), (32, 8, 10, 120), (24, 24, 70, 0)])
+@pytest.mark.parametrize("dim,m,k,rerank", [(20, 8, 10, 0), (32, 16, 100, 0), (32, 8, 10, 120), (24, 24, 70, 0),
+                                            (32, 16, 200, 0), (64, 16, 10, 100), (128, 16, 128, 0), (64, 16, 65, 0)])
 def test_search_parity_general_path(gpu, dim, m, k, rerank):
-    """Shortlists above 64 and uneven subspace widths take the LDS-table scan."""
+    """Shortlists above 64 (above 128 with 16 subspaces) and uneven subspace
+    widths take the LDS-table scan; 16-subspace shortlists of 65 to 128 keep
+    two keys per lane in the register-codebook scan."""
     px = gpu
     n, nlist = 2000, 16
     data = corpus(n, dim, 20) + np.random.default_rng(3).standard_normal((n, dim)).astype(np.float32) * 0.3
@@ -379,7 +382,8 @@ def test_l2_one_dimension_subspaces_take_the_general_scan(gpu):
     assert_same(idx.search_batch(q, 10, nprobe=2), want)
 
 
-@pytest.mark.parametrize("dim,metric,rerank", [(16, 0, 0), (32, 1, 0), (64, 0, 40), (128, 1, 40), (128, 0, 0)])
+@pytest.mark.parametrize("dim,metric,rerank", [(16, 0, 0), (32, 1, 0), (64, 0, 40), (128, 1, 40), (128, 0, 0),
+                                               (64, 0, 100), (128, 1, 128)])
 def test_large_batch_scan(gpu, dim, metric, rerank):
     """A 700-query batch over 12 lists (4200 and 8400 (query, probe) pairs,
     every list probed by hundreds of queries): ids and ADC distances match the
