@@ -1060,6 +1060,11 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan16(const float* __restric
     }
     thr_d = (uint32_t)(thr >> 32);
     ncand = 0;
+    // The rank and filter loads above were waited with vmcnt(0) before use.
+    // Say so to the compiler with a wait it can see, or its wait bookkeeping
+    // carries them as possibly pending into every chunk and drains the ring
+    // copies (vmcnt(0)) before each chunk's lookups.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt and lgkmcnt unconstrained
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
