@@ -143,7 +143,8 @@ def bench_c1(args, torch, px, dev):
            "config": {"workload": "flat exact search, Euclidean, 100k x 128 f32 (100 Gaussian clusters, sigma 0.15), "
                                   "1,000 queries in one batch, k=10", "n": n, "dim": dim, "batch": nq, "k": k},
            "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
-                        "frac": round(tflops / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": None,
+                        "frac": round(tflops / PEAK_FP32_MFMA_TFLOPS, 4),
+                        "traffic": load_traffic("flat_mfma_candidates_c1"),
                         "kernel": "flat_mfma_candidates", "ms_per_launch": round(cand_ms, 4)},
            "stage_ms": {key: round(float(np.mean([t[key] for t in stages])), 4) for key in stages[0]},
            "host_path": host_path(idx.search_batch, [qh], k),
