@@ -218,10 +218,37 @@ __device__ inline void wave_bitonic_sort(uint64_t (&k)[E], int lane) {
 // returns the pivot in every thread. `hist` is 256 ints of shared memory,
 // `sh` 4 u64 of shared. Keys equal to KEY_MAX are padding and never
 // selected; the caller clamps K to the number of real keys.
+//
+// PER > 0 reads each key once into registers (key i of thread t is
+// i = t + j * blockDim.x, j < PER; requires n <= PER * blockDim.x); PER = 0
+// reads the keys through `get` on every pass. The digit passes stop early
+// once the chosen digit's bin holds exactly the keys still needed: all of
+// them are then among the K smallest, and the K-th smallest is their
+// largest, found by a block maximum.
 // ----------------------------------------------------------------------------
-template <class Get, int BITS = 64>
+template <class Get, int BITS = 64, int PER = 0>
 __device__ inline uint64_t block_radix_select(Get get, int n, int K, int* hist, uint64_t* sh) {
   static_assert(BITS % 8 == 0 && BITS <= 64, "whole-byte digits");
+  constexpr int C = PER > 0 ? PER : 1;
+  uint64_t v[C];
+  if constexpr (PER > 0) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int i = threadIdx.x + j * blockDim.x;
+      v[j] = i < n ? (uint64_t)get(i) : 0;
+    }
+  }
+  // every key of this thread, in order: f(x)
+  auto each = [&](auto f) {
+    if constexpr (PER > 0) {
+#pragma unroll
+      for (int j = 0; j < PER; ++j)
+        if (threadIdx.x + j * blockDim.x < n) f(v[j]);
+    } else {
+      for (int i = threadIdx.x; i < n; i += blockDim.x) f((uint64_t)get(i));
+    }
+  };
+  if (threadIdx.x == 0) sh[3] = 0;
   uint64_t prefix = 0, mask = 0;
   int remaining = K;
   for (int pass = 0; pass < BITS / 8; ++pass) {
@@ -232,8 +259,7 @@ __device__ inline uint64_t block_radix_select(Get get, int n, int K, int* hist, 
     // digits are often shared by most keys, which would otherwise serialise
     // every add on one bin)
     int run_d = -1, run_n = 0;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-      const uint64_t x = get(i);
+    each([&](uint64_t x) {
       if ((x & mask) == prefix) {
         const int dg = (int)((x >> shift) & 255);
         if (dg != run_d) {
@@ -243,7 +269,7 @@ __device__ inline uint64_t block_radix_select(Get get, int n, int K, int* hist, 
         }
         ++run_n;
       }
-    }
+    });
     if (run_n) atomicAdd(&hist[run_d], run_n);
     __syncthreads();
     if (threadIdx.x < WAVE) {
@@ -259,22 +285,35 @@ __device__ inline uint64_t block_radix_select(Get get, int n, int K, int* hist, 
       int excl = incl - s;
       // the digit d with excl(d) < remaining <= excl(d) + count(d)
       int e0 = excl, e1 = e0 + c0, e2 = e1 + c1, e3 = e2 + c2;
-      int d = -1, before = 0;
-      if (remaining > e0 && remaining <= e1) { d = lane * 4; before = e0; }
-      else if (remaining > e1 && remaining <= e2) { d = lane * 4 + 1; before = e1; }
-      else if (remaining > e2 && remaining <= e3) { d = lane * 4 + 2; before = e2; }
-      else if (remaining > e3 && remaining <= e3 + c3) { d = lane * 4 + 3; before = e3; }
+      int d = -1, before = 0, cnt = 0;
+      if (remaining > e0 && remaining <= e1) { d = lane * 4; before = e0; cnt = c0; }
+      else if (remaining > e1 && remaining <= e2) { d = lane * 4 + 1; before = e1; cnt = c1; }
+      else if (remaining > e2 && remaining <= e3) { d = lane * 4 + 2; before = e2; cnt = c2; }
+      else if (remaining > e3 && remaining <= e3 + c3) { d = lane * 4 + 3; before = e3; cnt = c3; }
       if (d >= 0) {
         sh[0] = (uint64_t)d;
         sh[1] = (uint64_t)before;
+        sh[2] = (uint64_t)cnt;
       }
     }
     __syncthreads();
     const uint64_t d = sh[0];
     remaining -= (int)sh[1];
+    const int cnt = (int)sh[2];
     prefix |= d << shift;
     mask |= 255ull << shift;
     __syncthreads();
+    if (cnt == remaining && pass + 1 < BITS / 8) {
+      uint64_t m = 0;
+      each([&](uint64_t x) {
+        if ((x & mask) == prefix && x > m) m = x;
+      });
+      if (m) atomicMax((unsigned long long*)&sh[3], (unsigned long long)m);
+      __syncthreads();
+      const uint64_t r = sh[3];
+      __syncthreads();  // sh may be reused by the caller's next select
+      return r;
+    }
   }
   return prefix;
 }

@@ -388,7 +388,9 @@ __global__ __launch_bounds__(512) void flat_seed_threshold(const uint64_t* __res
   const int q = blockIdx.x;
   const uint64_t* c = cand + (size_t)q * S * CAP;
   auto get = [&](int i) { return c[(size_t)(i / FB_N) * CAP + i % FB_N] >> 32; };
-  const uint64_t hi = block_radix_select<decltype(get), 32>(get, S * FB_N, Kp, hist, sh);
+  const int n = S * FB_N;
+  const uint64_t hi = n <= 16 * (int)blockDim.x ? block_radix_select<decltype(get), 32, 16>(get, n, Kp, hist, sh)
+                                    : block_radix_select<decltype(get), 32>(get, n, Kp, hist, sh);
   if (threadIdx.x == 0 && hi != 0xFFFFFFFFull) atomicMin(gthr + q, (unsigned long long)((hi << 32) | 0xFFFFFFFFull));
 }
 
@@ -425,7 +427,9 @@ __global__ __launch_bounds__(256) void flat_merge_rescore(
     if (threadIdx.x == 0) out_count[q] = 0;
     return;
   }
-  const uint64_t pivot = block_radix_select(get, n, ksel, hist, sh);
+  const uint64_t pivot = n <= 16 * (int)blockDim.x ? block_radix_select<decltype(get), 64, 16>(get, n, ksel, hist, sh)
+                         : n <= 40 * (int)blockDim.x ? block_radix_select<decltype(get), 64, 40>(get, n, ksel, hist, sh)
+                                         : block_radix_select(get, n, ksel, hist, sh);
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
     const uint64_t x = get(i);
     if (x <= pivot && x != KEY_MAX) {

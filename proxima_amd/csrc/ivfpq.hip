@@ -1191,7 +1191,9 @@ __global__ __launch_bounds__(256) void ivf_merge(const uint64_t* __restrict__ ca
     if (threadIdx.x == 0) out_count[q] = 0;
     return;
   }
-  const uint64_t pivot = block_radix_select(get, n_per_q, ksel, hist, sh);
+  const uint64_t pivot = n_per_q <= 16 * (int)blockDim.x
+                             ? block_radix_select<decltype(get), 64, 16>(get, n_per_q, ksel, hist, sh)
+                             : block_radix_select(get, n_per_q, ksel, hist, sh);
   for (int i = threadIdx.x; i < n_per_q; i += blockDim.x) {
     const uint64_t x = base[i];
     if (x <= pivot && x != KEY_MAX) sel[atomicAdd(&n_sel, 1)] = x;

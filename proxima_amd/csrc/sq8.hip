@@ -214,38 +214,101 @@ __global__ void sq8_mark(const uint32_t* __restrict__ slots, const uint64_t* __r
   ids[slots[i]] = sid[i];
 }
 
+#if defined(__HIP_DEVICE_COMPILE__)
+// A raw buffer resource over [p, p + bytes), from wave-uniform values.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t sq_rsrc(const void* p, int bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)(((uint64_t)hi << 32) | lo), 0,
+                                           __builtin_amdgcn_readfirstlane(bytes), SQ_RSRC_WORD3);
+}
+
+// Buffer loads straight into LDS: lane i's 16 (4) bytes land at m0 + 16 i
+// (m0 + 4 i); an offset outside the resource lands as zeros. Inline asm, so
+// that the compiler does not count these loads under vmcnt (it would wait
+// for every one in flight before each LDS read of the tile); the scan waits
+// for them itself (wait_vm_upto) before the tile barrier. The scan kernel
+// has no other use of m0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void sq_dma16(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff), "s"(rs)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void sq_dma4(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(m0), "v"(voff), "s"(rs)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+#endif
+
+// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 15].
+__device__ __forceinline__ void wait_vm_upto(int n) {
+  switch (n) {
+    case 0: wait_vm<0>(); break;
+    case 1: wait_vm<1>(); break;
+    case 2: wait_vm<2>(); break;
+    case 3: wait_vm<3>(); break;
+    case 4: wait_vm<4>(); break;
+    case 5: wait_vm<5>(); break;
+    case 6: wait_vm<6>(); break;
+    case 7: wait_vm<7>(); break;
+    case 8: wait_vm<8>(); break;
+    case 9: wait_vm<9>(); break;
+    case 10: wait_vm<10>(); break;
+    case 11: wait_vm<11>(); break;
+    case 12: wait_vm<12>(); break;
+    case 13: wait_vm<13>(); break;
+    case 14: wait_vm<14>(); break;
+    default: wait_vm<15>(); break;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ uint32_t lds_addr(const T* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) T*)p;
+}
+
 // ---------------------------------------------------------------------------
-// Integer MFMA scan. Workgroup = SQ_NW compute waves + one loader wave.
-// Compute wave w holds QT tiles of 32 query codes in VGPRs (the MFMA B
-// operand: lane l gives query l%32, bytes [kb*32 + 16*(l/32), +16) of K
-// block kb); database rows stream through a double-buffered LDS tile of R
-// rows (row stride KP+16 bytes: 16-byte reads of 16 consecutive rows hit
-// distinct banks) and feed the A operand the same way. Output lane l,
-// register v = row 8*(v/4) + 4*(l/32) + v%4 of the tile against query l%32,
-// so every lane filters scores of one query.
+// Integer MFMA scan. Workgroup = SQ_NW waves, two per SIMD, each with up to
+// 256 registers. Wave w holds QT tiles of 32 query codes in VGPRs (the MFMA
+// B operand: lane l gives query l%32, bytes [kb*32 + 16*(l/32), +16) of K
+// block kb); database rows stream through D LDS tiles of R rows (row stride
+// KP+16 bytes: 16-byte reads of 16 consecutive rows hit distinct banks) and
+// feed the A operand the same way. Output lane l, register v = row
+// 8*(v/4) + 4*(l/32) + v%4 of the tile against query l%32, so every lane
+// filters scores of one query.
 //
-// The loader wave fetches the next tile into the idle LDS buffer while the
-// compute waves work on the current one, so the compute waves never wait on
-// HBM and never hold outstanding vector-memory loads.
+// Every wave issues its share of the tile DMAs (buffer loads into LDS, D - 1
+// tiles ahead) and waits only for its own share before the tile barrier, so
+// no wave stalls on HBM inside a tile. Within a tile the row blocks are
+// software-pipelined: the MFMAs of row block rt+1 are issued before the
+// scores of block rt are filtered, from a second accumulator set and a
+// second A operand, so the matrix core runs while the filter's VALU work and
+// the next block's LDS reads proceed.
 // ---------------------------------------------------------------------------
 template <int KB, bool STAGE1>
-__global__ __launch_bounds__((SQ_NW + 1) * 64) void sq8_mfma_scan(
+__global__ __launch_bounds__(SQ_NW * 64) void sq8_mfma_scan(
     const int8_t* __restrict__ Qc, int nq, const int8_t* __restrict__ C, int N, const uint8_t* __restrict__ live,
     const uint8_t* __restrict__ accept, const uint32_t* __restrict__ rank, int nchunks, int qgroups,
     int tiles_per_chunk, int sample, const int* __restrict__ thr_in, int* __restrict__ tmax,
     int* __restrict__ ccount, uint64_t* __restrict__ cand, int cap) {
   constexpr int KP = KB * 32, SR = KP + 16, R = sq_rows(KB), RT = R / 32, QT = sq_qt(KB);
   constexpr int PPR = KP / 16;         // 16-byte pieces per row
-  constexpr int D = 3;                // LDS tile buffers: the next two tiles load during the current one
+  constexpr int D = 3;                // LDS tiles: the next two tiles load during the current one
   __shared__ __align__(16) int8_t tile[D][R * SR];
-  __shared__ __align__(4) uint8_t vb[STAGE1 ? D : 1][R];
+  // stage 1: the tile's live and accept bytes (256 per tile; rows past the
+  // tile or past N read zero)
+  __shared__ __align__(16) uint8_t vlive[STAGE1 ? D : 1][256];
+  __shared__ __align__(16) uint8_t vacc[STAGE1 ? D : 1][256];
   // stage 2: passing scores of recomputed tiles go to a workgroup list in
-  // LDS, filtered and published after the scan. The tiles and the list fit
-  // two workgroups per CU (four compute waves per SIMD).
+  // LDS, filtered and published after the scan
   __shared__ int lc_score[STAGE1 ? 1 : SQ_LCAP];
   __shared__ int lc_row[STAGE1 ? 1 : SQ_LCAP];
   __shared__ int lc_q[STAGE1 ? 1 : SQ_LCAP];
   __shared__ int lc_n;
+  static_assert(R <= 256, "one 4-byte DMA per lane covers a tile's live bytes");
 
   // XCD-aware mapping: workgroup ids are dealt round-robin over the 8 XCDs;
   // consecutive logical ids (the query groups of one chunk) go to the same
@@ -256,10 +319,10 @@ __global__ __launch_bounds__((SQ_NW + 1) * 64) void sq8_mfma_scan(
   if (lid >= total) return;  // uniform over the workgroup, before any barrier
   const int chunk = lid / qgroups, qgroup = lid % qgroups;
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, r = lane & 31;
-  const bool loader = w == SQ_NW;
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, r = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q0 = qgroup * (SQ_NW * QT * 32) + w * (QT * 32);
-  const bool active = !loader && q0 < nq;
+  const bool active = q0 < nq;
 
   i4v qa[QT][KB];
   int thr[QT], run[QT];
@@ -273,6 +336,9 @@ __global__ __launch_bounds__((SQ_NW + 1) * 64) void sq8_mfma_scan(
     thr[qt] = STAGE1 ? INT_MIN : (ok ? thr_in[q] : INT_MAX);
     run[qt] = INT_MIN;
   }
+  // The query loads land here, before any tile DMA: a compiler wait for them
+  // inside the loop would also drain the DMAs in flight.
+  wait_vm<0>();
 
   const int ntiles = (N + R - 1) / R;
   const int tb = chunk * tiles_per_chunk;
@@ -281,138 +347,142 @@ __global__ __launch_bounds__((SQ_NW + 1) * 64) void sq8_mfma_scan(
   const int t0 = STAGE1 ? (tb + sample - 1) / sample * sample : tb;
   const int niter = t0 < te ? (te - t0 + step - 1) / step : 0;
 
-  // The loader fills a tile with buffer_load_dwordx4 ... lds: instruction
-  // i writes 64 x 16 bytes at LDS offset 1024*i, lane l to byte 16*l, i.e.
-  // the 16-byte slot 64*i + l of the padded tile (PPR data slots + 1 padding
-  // slot per row). The buffer resource is rebased on each tile and covers
-  // its rows only, so rows past N and padding slots (given an offset beyond
-  // the range) read zeros. The per-lane offsets are the same for every tile:
-  // the loader steps slot 64*i + l -> (row, part) from one instruction to
-  // the next (64 slots = 64/SPR rows + 64%SPR parts).
-  constexpr int SPR = PPR + 1, NI = R * SPR / 64;
+  // Tile DMA: instruction i writes 64 x 16 bytes at LDS offset 1024*i,
+  // lane l to byte 16*l, i.e. the 16-byte slot 64*i + l of the padded tile
+  // (PPR data slots + 1 padding slot per row). Wave w issues the
+  // instructions i = w, w + SQ_NW, ...; the buffer resource is rebased on
+  // each tile and covers its rows only, so rows past N and padding slots
+  // (given an offset beyond the range) read zeros. Stage 1 adds one 4-byte
+  // DMA each for the tile's live and accept bytes, on the last two waves
+  // (the ones with the fewest tile instructions).
+  constexpr int SPR = PPR + 1, NI = R * SPR / 64, NJ = (NI + SQ_NW - 1) / SQ_NW;
   static_assert(R * SPR % 64 == 0 && NI < 64, "tile must split into whole DMA instructions");
-  static_assert(64 % SPR != 0 || SPR == 64, "slot stepping assumes 64 / SPR rows plus a part step");
-  auto issue = [&](int t, int buf) {
-    if (STAGE1) {
-      // usable-row bytes first; their wait leaves only the tile DMA in flight
-      uint8_t pv[(R + 63) / 64];
+  const int nmine = w < NI % SQ_NW || NI % SQ_NW == 0 ? NJ : NJ - 1;
+  const bool vdma = STAGE1 && w >= SQ_NW - 2;
+  const int ndma = nmine + (vdma ? 1 : 0);  // vmcnt entries per issued tile
+  uint32_t voff[NJ];
 #pragma unroll
-      for (int i = 0; i < (R + 63) / 64; ++i) {
-        const int row = lane + i * 64;
-        const long g = (long)t * R + row;
-        pv[i] = (row < R && g < N && live[g] && (accept == nullptr || accept[g])) ? 1 : 0;
-      }
-#pragma unroll
-      for (int i = 0; i < (R + 63) / 64; ++i)
-        if (lane + i * 64 < R) vb[buf][lane + i * 64] = pv[i];
-    }
+  for (int j = 0; j < NJ; ++j) {
+    const int sl = 64 * (w + j * SQ_NW) + lane, row = sl / SPR, part = sl % SPR;
+    voff[j] = part < PPR ? row * KP + part * 16 : 0x7FFFFFF0u;  // padding: beyond the range, reads zeros
+  }
+  const uint8_t* vsrc = w == SQ_NW - 1 ? live : (accept ? accept : live);
+  auto issue = [&](int t, int buf) __attribute__((always_inline)) {
 #if defined(__HIP_DEVICE_COMPILE__)
     const int rows = min(R, N - t * R);
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(C + (size_t)t * R * KP), 0, rows * KP, SQ_RSRC_WORD3);
-    int row = lane / SPR, part = lane % SPR;
-#pragma unroll 1
-    for (int i = 0; i < NI; ++i) {
-      const int off = part < PPR ? row * KP + part * 16 : 0x7FFFFFF0;  // padding: beyond the range, reads zeros
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)&tile[buf][i * 1024], 16,
-                                               off, 0, 0, 0);
-      row += 64 / SPR;
-      part += 64 % SPR;
-      if (part >= SPR) {
-        part -= SPR;
-        ++row;
-      }
+    const __amdgpu_buffer_rsrc_t rs = sq_rsrc(C + (size_t)t * R * KP, rows * KP);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      if (j < nmine) sq_dma16(rs, voff[j], lds_addr(&tile[buf][(w + j * SQ_NW) * 1024]));
+    if (vdma) {
+      const __amdgpu_buffer_rsrc_t vs = sq_rsrc(vsrc + (size_t)t * R, rows);
+      sq_dma4(vs, 4u * lane, lds_addr(w == SQ_NW - 1 ? &vlive[buf][0] : &vacc[buf][0]));
     }
 #endif
   };
 
-  // Loader pipeline: tile j goes to buffer j % D, issued D - 1 iterations
-  // before it is used (its buffer was last read in the iteration before the
-  // issue). Before each barrier the loader waits until only the DMAs of the
-  // tiles after the next one are outstanding.
-  if (tid == 0) lc_n = 0;
-  if (loader) {
-    for (int j = 0; j < D - 1 && j < niter; ++j) issue(t0 + j * step, j);
-    const int later = min(D - 2, niter - 1);  // tiles issued after tile 0
-    if (later >= 1) wait_vm<NI>();
-    else wait_vm<0>();
-  }
-  __syncthreads();
-  for (int it = 0; it < niter; ++it) {
-    const int buf = it % D;
-    const int t = t0 + it * step;
-    if (loader) {
-      if (it + D - 1 < niter) issue(t0 + (it + D - 1) * step, (it + D - 1) % D);
-      // tiles it+2 .. min(it+D-1, niter-1) may stay in flight; tile it+1 must land
-      const int later = max(0, min(it + D - 1, niter - 1) - (it + 1));
-      static_assert(D <= 3, "the waits below cover at most one later tile");
-      if (later >= 1) wait_vm<NI>();
-      else wait_vm<0>();
-    } else if (active) {
-      static_assert(RT * QT <= 32, "one pass bit per 32 x 32 tile");
-      uint32_t passmask = 0;  // bit rt*QT+qt: that 32 x 32 tile has a score >= the threshold
+  // A operand of row block rt: lane l reads row rt*32 + l%32, bytes
+  // kb*32 + 16*(l/32) .. +16 of every K block.
+  auto load_a = [&](i4v(&a)[KB], const int8_t* tl, int rt) __attribute__((always_inline)) {
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        i4v a[KB];
+    for (int kb = 0; kb < KB; ++kb) a[kb] = *reinterpret_cast<const i4v*>(&tl[(rt * 32 + r) * SR + kb * 32 + h * 16]);
+  };
+  auto mfmas = [&](i16v(&acc)[QT], const i4v(&a)[KB]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
-          a[kb] = *reinterpret_cast<const i4v*>(&tile[buf][(rt * 32 + r) * SR + kb * 32 + h * 16]);
-        i16v acc[QT];
+    for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt)
+      for (int v = 0; v < 16; ++v) acc[qt][v] = 0;
 #pragma unroll
-          for (int v = 0; v < 16; ++v) acc[qt][v] = 0;
+    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
+      for (int qt = 0; qt < QT; ++qt) acc[qt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[kb], qa[qt][kb], acc[qt], 0, 0, 0);
+  };
+  uint32_t passmask = 0;  // stage 2, bit rt*QT+qt: that 32 x 32 block has a score >= the threshold
+  auto reduce = [&](const i16v(&acc)[QT], int rt, int buf) __attribute__((always_inline)) {
+    if constexpr (STAGE1) {
+      uint32_t vw[4];
 #pragma unroll
-          for (int qt = 0; qt < QT; ++qt)
-            acc[qt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[kb], qa[qt][kb], acc[qt], 0, 0, 0);
-        if constexpr (STAGE1) {
-          uint32_t vw[4];
+      for (int g = 0; g < 4; ++g)
+        vw[g] = *reinterpret_cast<const uint32_t*>(&vlive[buf][rt * 32 + 8 * g + 4 * h]) &
+                *reinterpret_cast<const uint32_t*>(&vacc[buf][rt * 32 + 8 * g + 4 * h]);
+      if (__all((vw[0] & vw[1] & vw[2] & vw[3]) == 0x01010101u)) {
+        // every row of the 32 x 32 block is usable: a v_max3 chain
 #pragma unroll
-          for (int g = 0; g < 4; ++g) vw[g] = *reinterpret_cast<const uint32_t*>(&vb[buf][rt * 32 + 8 * g + 4 * h]);
-          if (__all((vw[0] & vw[1] & vw[2] & vw[3]) == 0x01010101u)) {
-            // every row of the 32 x 32 tile is usable: a v_max3 chain
+        for (int qt = 0; qt < QT; ++qt) {
+          const i16v x = acc[qt];
+          int m = max(max(run[qt], x[0]), x[1]);
+          m = max(max(m, x[2]), x[3]);
+          m = max(max(m, x[4]), x[5]);
+          m = max(max(m, x[6]), x[7]);
+          m = max(max(m, x[8]), x[9]);
+          m = max(max(m, x[10]), x[11]);
+          m = max(max(m, x[12]), x[13]);
+          run[qt] = max(max(m, x[14]), x[15]);
+        }
+      } else {
 #pragma unroll
-            for (int qt = 0; qt < QT; ++qt) {
-              const i16v x = acc[qt];
-              int m = max(max(run[qt], x[0]), x[1]);
-              m = max(max(m, x[2]), x[3]);
-              m = max(max(m, x[4]), x[5]);
-              m = max(max(m, x[6]), x[7]);
-              m = max(max(m, x[8]), x[9]);
-              m = max(max(m, x[10]), x[11]);
-              m = max(max(m, x[12]), x[13]);
-              run[qt] = max(max(m, x[14]), x[15]);
-            }
-          } else {
+        for (int g = 0; g < 4; ++g) {
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
+          for (int j = 0; j < 4; ++j) {
+            const bool ok = (vw[g] >> (8 * j)) & 1u;
 #pragma unroll
-              for (int j = 0; j < 4; ++j) {
-                const bool ok = (vw[g] >> (8 * j)) & 1u;
-#pragma unroll
-                for (int qt = 0; qt < QT; ++qt) run[qt] = ok ? max(run[qt], acc[qt][4 * g + j]) : run[qt];
-              }
-            }
-          }
-        } else {
-#pragma unroll
-          for (int qt = 0; qt < QT; ++qt) {
-            const i16v x = acc[qt];
-            int m = max(max(x[0], x[1]), x[2]);  // a chain of v_max3
-            m = max(max(m, x[3]), x[4]);
-            m = max(max(m, x[5]), x[6]);
-            m = max(max(m, x[7]), x[8]);
-            m = max(max(m, x[9]), x[10]);
-            m = max(max(m, x[11]), x[12]);
-            m = max(max(m, x[13]), x[14]);
-            m = max(m, x[15]);
-            passmask |= (__ballot(m >= thr[qt]) != 0 ? 1u : 0u) << (rt * QT + qt);
+            for (int qt = 0; qt < QT; ++qt) run[qt] = ok ? max(run[qt], acc[qt][4 * g + j]) : run[qt];
           }
         }
       }
-      // Rare: some 32 x 32 tiles hold a score >= the threshold. Recompute
+    } else {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        const i16v x = acc[qt];
+        int m = max(max(x[0], x[1]), x[2]);  // a chain of v_max3
+        m = max(max(m, x[3]), x[4]);
+        m = max(max(m, x[5]), x[6]);
+        m = max(max(m, x[7]), x[8]);
+        m = max(max(m, x[9]), x[10]);
+        m = max(max(m, x[11]), x[12]);
+        m = max(max(m, x[13]), x[14]);
+        m = max(m, x[15]);
+        passmask |= (__ballot(m >= thr[qt]) != 0 ? 1u : 0u) << (rt * QT + qt);
+      }
+    }
+  };
+
+  // Tile j goes to buffer j % D, issued D - 1 iterations before it is used
+  // (its buffer was last read in the iteration before the issue). Before
+  // each barrier a wave waits until only its DMAs of the tile issued in
+  // that iteration are outstanding, i.e. its share of the next tile landed.
+  static_assert(D == 3, "the waits below keep exactly one later tile in flight");
+  if (tid == 0) lc_n = 0;
+  if (niter > 0) issue(t0, 0);
+  if (niter > 1) issue(t0 + step, 1);
+  wait_vm_upto(niter > 1 ? ndma : 0);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  for (int it = 0; it < niter; ++it) {
+    const int buf = it % D;
+    const int t = t0 + it * step;
+    const bool more = it + D - 1 < niter;
+    if (more) issue(t0 + (it + D - 1) * step, (it + D - 1) % D);
+    if (active) {
+      const int8_t* tl = &tile[buf][0];
+      passmask = 0;
+      i4v a0[KB], a1[KB];
+      i16v c0[QT], c1[QT];
+      load_a(a0, tl, 0);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        if (rt % 2 == 0) {
+          mfmas(c0, a0);
+          if (rt + 1 < RT) load_a(a1, tl, rt + 1);
+          if (rt > 0) reduce(c1, rt - 1, buf);
+        } else {
+          mfmas(c1, a1);
+          if (rt + 1 < RT) load_a(a0, tl, rt + 1);
+          reduce(c0, rt - 1, buf);
+        }
+      }
+      if ((RT - 1) % 2 == 0) reduce(c0, RT - 1, buf);
+      else reduce(c1, RT - 1, buf);
+      // Rare: some 32 x 32 blocks hold a score >= the threshold. Recompute
       // exactly those from the LDS tile (still valid until the barrier) and
       // append their passing scores to the workgroup list.
       if constexpr (!STAGE1) {
@@ -422,9 +492,7 @@ __global__ __launch_bounds__((SQ_NW + 1) * 64) void sq8_mfma_scan(
             const uint32_t bits = (passmask >> (rt * QT)) & ((1u << QT) - 1u);
             if (!bits) continue;
             i4v a[KB];
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb)
-              a[kb] = *reinterpret_cast<const i4v*>(&tile[buf][(rt * 32 + r) * SR + kb * 32 + h * 16]);
+            load_a(a, tl, rt);
 #pragma unroll
             for (int qt = 0; qt < QT; ++qt) {
               if (!((bits >> qt) & 1u)) continue;
@@ -457,11 +525,12 @@ __global__ __launch_bounds__((SQ_NW + 1) * 64) void sq8_mfma_scan(
         }
       }
     }
-    // Tile barrier without the workgroup fence of __syncthreads: that fence
-    // would make the loader drain every LDS DMA in flight (vmcnt(0)), tile
-    // it+2's included. The loader has already waited for tile it+1 above;
-    // the compute waves' LDS appends complete before the barrier
+    // This wave's share of the next tile has landed once only the DMAs
+    // issued in this iteration remain. Tile barrier without the workgroup
+    // fence of __syncthreads (that fence would drain every DMA in flight,
+    // the later tile's included); the waves' LDS appends complete before it
     // (lgkmcnt(0)); tile reads were consumed by their MFMAs.
+    wait_vm_upto(more ? ndma : 0);
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   }
   if constexpr (STAGE1) {
@@ -476,7 +545,7 @@ __global__ __launch_bounds__((SQ_NW + 1) * 64) void sq8_mfma_scan(
     // publish the workgroup's candidates (the loop's last barrier ordered
     // every append before this read)
     const int n = min(lc_n, SQ_LCAP);
-    for (int i = tid; i < n; i += (SQ_NW + 1) * 64) {
+    for (int i = tid; i < n; i += SQ_NW * 64) {
       const int row = lc_row[i], q = lc_q[i];
       if (live[row] && (accept == nullptr || accept[row])) {
         const int gp = atomicAdd(&ccount[q], 1);
@@ -499,7 +568,8 @@ __global__ __launch_bounds__(256) void sq8_thresholds(const int* __restrict__ tm
   // the k-th largest maximum: the k-th smallest of INT_MAX - v (in [0, 2^32))
   const int* t = tmax + (size_t)q * E;
   auto get = [&](int i) { return (uint64_t)((int64_t)INT_MAX - (int64_t)t[i]); };
-  const uint64_t v = block_radix_select<decltype(get), 32>(get, E, k, hist, sh);
+  const uint64_t v = E <= 8 * (int)blockDim.x ? block_radix_select<decltype(get), 32, 8>(get, E, k, hist, sh)
+                                  : block_radix_select<decltype(get), 32>(get, E, k, hist, sh);
   if (threadIdx.x == 0) thr[q] = (int)((int64_t)INT_MAX - (int64_t)v);
 }
 
@@ -1135,7 +1205,7 @@ struct Sq8Index {
       uint64_t* cand = (uint64_t*)sc.get(12, nq * cap_c * 8);
       const dim3 grid((unsigned)((nchunks * qgroups + 7) / 8 * 8));
 #define PXG_SQ_SCAN(KBV, ST)                                                                                        \
-  hipLaunchKernelGGL((sq8_mfma_scan<KBV, ST>), grid, dim3((SQ_NW + 1) * 64), 0, s, (const int8_t*)Qc, (int)nq,           \
+  hipLaunchKernelGGL((sq8_mfma_scan<KBV, ST>), grid, dim3(SQ_NW * 64), 0, s, (const int8_t*)Qc, (int)nq,           \
                      (const int8_t*)codes.p, N, d_live.p, d_accept, ranks.rank.p, nchunks, qgroups, tpc, sample,       \
                      (const int*)thr, tmax,                                                                        \
                      ccount, cand, cap_c)
