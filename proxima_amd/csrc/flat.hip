@@ -300,16 +300,24 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
     // key below thr[row] (key_float inverts ord_key; NaN and the sign of zero
     // pass), so only the marked values take the exact key test and append.
     {
-      bool okj[2];
+      // Validity as bit masks applied once per row group (usable slots: the
+      // j halves; rows below nq: both halves), so that the per-value work is
+      // straight-line code: one compare and one select into the mask.
+      uint32_t okbits = 0u;
       float xbj[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        okj[j] = slotj[j] < s_end && (lvj[j] & acj[j]) != 0u;
-        xbj[j] = okj[j] ? xbr[j] : 0.0f;
+        const bool ok = (slotj[j] < s_end) & ((lvj[j] & acj[j]) != 0u);
+        okbits |= ok ? 0xFFFFu << (16 * j) : 0u;
+        xbj[j] = ok ? xbr[j] : 0.0f;
       }
       uint32_t pass[2] = {0u, 0u};  // pass[i], bit j * 16 + v
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < 2; ++i) {
+        uint32_t rokbits = 0u;
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          rokbits |= q0 + wm + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3) < nq ? 0x10001u << v : 0u;
 #pragma unroll
         for (int vb = 0; vb < 4; ++vb) {
           const int row0 = wm + i * 32 + 8 * vb + 4 * h;
@@ -318,15 +326,16 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
           const float sqv[4] = {sq.x, sq.y, sq.z, sq.w}, tfv[4] = {tf.x, tf.y, tf.z, tf.w};
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const bool rok = q0 + row0 + e < nq;
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
               const float a = (sqv[e] + xbj[j]) - scale * acc[i][j][vb * 4 + e];
-              pass[i] |= (okj[j] && rok && !(a > tfv[e])) ? 1u << (j * 16 + vb * 4 + e) : 0u;
+              pass[i] |= !(a > tfv[e]) ? 1u << (j * 16 + vb * 4 + e) : 0u;
             }
           }
           __builtin_amdgcn_sched_barrier(0);  // bounds the live rows (no spills)
         }
+        pass[i] &= okbits & rokbits;
+      }
       if (__ballot((pass[0] | pass[1]) != 0)) {
 #pragma unroll
         for (int i = 0; i < 2; ++i)
