@@ -1630,58 +1630,91 @@ void pq_train_device(const float* R, size_t n, int dim, int ldr, const PqLayout&
                      float* d_books, double* inertia, size_t* iterations, hipStream_t s) {
   // One generator advanced across the subspaces (product.rs:244-247), but
   // only k-means++ draws from it (kmeans.rs:146-194; Lloyd and the farthest
-  // point reseeds draw nothing). So the seeds are drawn subspace by subspace
-  // on `s`, and each subspace's Lloyd loop starts on its own stream and host
-  // thread as soon as its seeds exist, overlapping the later seedings and the
-  // other subspaces' loops. Each loop is the same kmeans_device, so every
-  // codebook is the sequential run's.
+  // point reseeds draw nothing). In the common case a seeding's draws do not
+  // depend on the data: one gen_range over the points, then one 64-bit word
+  // per further centroid (gen_range_f64 accepts its first word unless the
+  // product rounds up to the total, and only a zero total takes a gen_range
+  // instead). So each subspace's starting state is predicted on the host,
+  // every subspace seeds and runs its Lloyd loop at once on its own stream
+  // and host thread, and each seeding's final state is checked against the
+  // next subspace's predicted start. From the first subspace whose draws
+  // differed, the later subspaces are redone in order from the true state,
+  // so every codebook is the sequential run's.
   (void)dim;
-  ChaCha8 rng(seed);
   const int M = L.M;
   const size_t k = std::max<size_t>(std::min<size_t>(256, n), 1);
   std::vector<DevBuf<float>> proj(M), seeds(M), cents(M);
   std::vector<KmeansOut> res(M);
   std::vector<std::exception_ptr> err(M);
-  std::vector<std::thread> workers;
-  auto join_all = [&]() {
-    for (auto& w : workers)
-      if (w.joinable()) w.join();
-  };
-  try {
+  std::vector<ChaCha8> start(M), end(M);
+  {
+    ChaCha8 r(seed);
     for (int sidx = 0; sidx < M; ++sidx) {
-      const int w = L.width[sidx], off = L.off[sidx];
-      const size_t tot = n * (size_t)w;
-      proj[sidx].reserve(std::max<size_t>(tot, 1));
-      seeds[sidx].reserve(k * w);
-      if (tot)
-        hipLaunchKernelGGL(gather_cols, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, R, ldr, (int)n, off, w,
-                           proj[sidx].p);
-      PXG_HIP(hipGetLastError());
-      size_t inexact = 0;
-      if (n) inexact = kmeans_pp_device(proj[sidx].p, n, w, w, k, rng, seeds[sidx].p, s);  // synchronises s
-      workers.emplace_back([&, sidx, w, inexact]() {
-        try {
-          hipStream_t ws;
-          PXG_HIP(hipStreamCreateWithFlags(&ws, hipStreamNonBlocking));
-          struct SG {
-            hipStream_t s;
-            ~SG() { (void)hipStreamDestroy(s); }
-          } sg{ws};
-          res[sidx] = kmeans_device(proj[sidx].p, n, w, w, 256, max_iter, nullptr, n ? seeds[sidx].p : nullptr,
-                                    cents[sidx], nullptr, ws);
-          res[sidx].inexact_sums += inexact;
-        } catch (...) {
-          err[sidx] = std::current_exception();
-        }
-      });
+      start[sidx] = r;
+      if (n) {
+        (void)r.gen_range_usize(n);
+        for (size_t c = 1; c < k; ++c) (void)r.next_u64();
+      }
     }
-  } catch (...) {
-    join_all();
-    throw;
   }
-  join_all();
+  for (int sidx = 0; sidx < M; ++sidx) {
+    const int w = L.width[sidx], off = L.off[sidx];
+    const size_t tot = n * (size_t)w;
+    proj[sidx].reserve(std::max<size_t>(tot, 1));
+    seeds[sidx].reserve(k * w);
+    if (tot)
+      hipLaunchKernelGGL(gather_cols, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, R, ldr, (int)n, off, w,
+                         proj[sidx].p);
+    PXG_HIP(hipGetLastError());
+  }
+  PXG_HIP(hipStreamSynchronize(s));
+  // seeding from `rng` (advanced by it) and the Lloyd loop of one subspace
+  auto train_one = [&](int sidx, ChaCha8& rng, hipStream_t ws) {
+    const int w = L.width[sidx];
+    size_t inexact = 0;
+    if (n) inexact = kmeans_pp_device(proj[sidx].p, n, w, w, k, rng, seeds[sidx].p, ws);  // synchronises ws
+    res[sidx] = kmeans_device(proj[sidx].p, n, w, w, 256, max_iter, nullptr, n ? seeds[sidx].p : nullptr, cents[sidx],
+                              nullptr, ws);
+    res[sidx].inexact_sums += inexact;
+  };
+  {
+    std::vector<std::thread> workers;
+    try {
+      for (int sidx = 0; sidx < M; ++sidx)
+        workers.emplace_back([&, sidx]() {
+          try {
+            hipStream_t ws;
+            PXG_HIP(hipStreamCreateWithFlags(&ws, hipStreamNonBlocking));
+            struct SG {
+              hipStream_t s;
+              ~SG() { (void)hipStreamDestroy(s); }
+            } sg{ws};
+            end[sidx] = start[sidx];
+            train_one(sidx, end[sidx], ws);
+          } catch (...) {
+            err[sidx] = std::current_exception();
+          }
+        });
+    } catch (...) {
+      for (auto& w : workers) w.join();
+      throw;
+    }
+    for (auto& w : workers) w.join();
+  }
   for (auto& e : err)
     if (e) std::rethrow_exception(e);
+  // the stream position (32-bit words drawn) of a generator state
+  auto pos = [](const ChaCha8& r) { return r.counter * 16 - (uint64_t)(64 - r.index); };
+  // PXG_PQ_REDO_AFTER=i takes the in-order path after subspace i as if its
+  // draws had differed (a test of that path; the results are the same)
+  const char* force = std::getenv("PXG_PQ_REDO_AFTER");
+  const int forced = force ? std::atoi(force) : -1;
+  for (int sidx = 0; sidx + 1 < M; ++sidx) {
+    if (sidx != forced && pos(end[sidx]) == pos(start[sidx + 1])) continue;
+    ChaCha8 rng = end[sidx];
+    for (int t = sidx + 1; t < M; ++t) train_one(t, rng, s);
+    break;
+  }
   double in = 0.0;
   size_t its = 0;
   for (int sidx = 0; sidx < M; ++sidx) {

@@ -230,6 +230,20 @@ def test_pq_train_and_encode_bit_exact(gpu, dim, m, count, seed):
     assert np.array_equal(pq.encode(t), orc.pq_encode(books, dim, m, t))
 
 
+@pytest.mark.parametrize("after", [0, 5])
+def test_pq_train_in_order_path(gpu, monkeypatch, after):
+    """The subspaces seed at once from predicted generator states; the
+    in-order path that redoes the later subspaces (taken when a seeding's
+    draws differ from the prediction, forced here) gives the same codebooks."""
+    px = gpu
+    t = _lcg_clustered(32, 512, 3)
+    monkeypatch.setenv("PXG_PQ_REDO_AFTER", str(after))
+    pq = px.ProductQuantizer.train(px.VectorSpace(32, px.Metric.EUCLIDEAN), t, px.PqConfig(8).with_seed(7))
+    books, inertia, iters = orc.pq_train(t, 8, 25, 7)
+    assert np.array_equal(bits(pq.codebooks), bits(books))
+    assert pq.training_inertia == inertia and pq.training_iterations == iters
+
+
 def test_pq_validation(gpu):  # product.rs:775-809
     px = gpu
     space = px.VectorSpace(8, px.Metric.EUCLIDEAN)
