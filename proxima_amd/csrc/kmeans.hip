@@ -1027,9 +1027,21 @@ __global__ __launch_bounds__(256) void km_pp_round_q8(const float* __restrict__ 
   bool exact = false;
   if (i < n) {
     cur = ns[i];
-    const int* qv = reinterpret_cast<const int*>(Q + (size_t)i * kq);
-    int dot = 0;
-    for (int j = 0; j < words; ++j) dot = __builtin_amdgcn_sdot4(qv[j], qc[j], dot, false);
+    int dot = 0;  // exact in any order: |dot| < 2^31 for kq <= KW_DMAX
+    if ((kq & 15) == 0) {
+      // 16-byte loads: the row's bytes in kq/16 loads instead of kq/4
+      const int4* qv = reinterpret_cast<const int4*>(Q + (size_t)i * kq);
+      for (int j = 0; j < words / 4; ++j) {
+        const int4 v = qv[j];
+        dot = __builtin_amdgcn_sdot4(v.x, qc[4 * j], dot, false);
+        dot = __builtin_amdgcn_sdot4(v.y, qc[4 * j + 1], dot, false);
+        dot = __builtin_amdgcn_sdot4(v.z, qc[4 * j + 2], dot, false);
+        dot = __builtin_amdgcn_sdot4(v.w, qc[4 * j + 3], dot, false);
+      }
+    } else {
+      const int* qv = reinterpret_cast<const int*>(Q + (size_t)i * kq);
+      for (int j = 0; j < words; ++j) dot = __builtin_amdgcn_sdot4(qv[j], qc[j], dot, false);
+    }
     const double sp = scale[i];
     const double A = sp * sp * (double)qnorm[i], B = sc * sc * qnc, C = sp * sc * (double)dot;
     const double e2 = A + B - 2.0 * C;
