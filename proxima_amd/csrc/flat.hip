@@ -427,7 +427,14 @@ __global__ __launch_bounds__(256) void flat_merge_rescore(
   }
   __syncthreads();
   int local = 0;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) local += get(i) != KEY_MAX;
+  // eight keys per thread per step, loaded together before any is used
+  for (int i0 = threadIdx.x; i0 < n; i0 += 8 * blockDim.x) {
+    uint64_t x[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) x[u] = get(min(i0 + u * (int)blockDim.x, n - 1));  // unconditional loads
+#pragma unroll
+    for (int u = 0; u < 8; ++u) local += (i0 + u * (int)blockDim.x < n && x[u] != KEY_MAX) ? 1 : 0;
+  }
   atomicAdd(&n_valid, local);
   __syncthreads();
   const int valid = n_valid;
@@ -439,12 +446,16 @@ __global__ __launch_bounds__(256) void flat_merge_rescore(
   const uint64_t pivot = n <= 16 * (int)blockDim.x ? block_radix_select<decltype(get), 64, 16>(get, n, ksel, hist, sh)
                          : n <= 40 * (int)blockDim.x ? block_radix_select<decltype(get), 64, 40>(get, n, ksel, hist, sh)
                                          : block_radix_select(get, n, ksel, hist, sh);
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const uint64_t x = get(i);
-    if (x <= pivot && x != KEY_MAX) {
-      const int p = atomicAdd(&n_sel, 1);
-      sel[p] = x;
-    }
+  for (int i0 = threadIdx.x; i0 < n; i0 += 8 * blockDim.x) {
+    uint64_t x[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) x[u] = get(min(i0 + u * (int)blockDim.x, n - 1));  // unconditional loads
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (i0 + u * (int)blockDim.x < n && x[u] <= pivot && x[u] != KEY_MAX) {
+        const int p = atomicAdd(&n_sel, 1);
+        sel[p] = x[u];
+      }
   }
   __syncthreads();
   // rescore: 8 threads per candidate

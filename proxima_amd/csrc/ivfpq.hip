@@ -1183,7 +1183,14 @@ __global__ __launch_bounds__(256) void ivf_merge(const uint64_t* __restrict__ ca
   }
   __syncthreads();
   int local = 0;
-  for (int i = threadIdx.x; i < n_per_q; i += blockDim.x) local += base[i] != KEY_MAX;
+  // four keys per thread per step, loaded together before any is used
+  for (int i0 = threadIdx.x; i0 < n_per_q; i0 += 4 * blockDim.x) {
+    uint64_t x[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) x[u] = base[min(i0 + u * (int)blockDim.x, n_per_q - 1)];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) local += (i0 + u * (int)blockDim.x < n_per_q && x[u] != KEY_MAX) ? 1 : 0;
+  }
   atomicAdd(&n_valid, local);
   __syncthreads();
   const int ksel = min(kk, n_valid);
@@ -1194,9 +1201,13 @@ __global__ __launch_bounds__(256) void ivf_merge(const uint64_t* __restrict__ ca
   const uint64_t pivot = n_per_q <= 16 * (int)blockDim.x
                              ? block_radix_select<decltype(get), 64, 16>(get, n_per_q, ksel, hist, sh)
                              : block_radix_select(get, n_per_q, ksel, hist, sh);
-  for (int i = threadIdx.x; i < n_per_q; i += blockDim.x) {
-    const uint64_t x = base[i];
-    if (x <= pivot && x != KEY_MAX) sel[atomicAdd(&n_sel, 1)] = x;
+  for (int i0 = threadIdx.x; i0 < n_per_q; i0 += 4 * blockDim.x) {
+    uint64_t x[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) x[u] = base[min(i0 + u * (int)blockDim.x, n_per_q - 1)];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (i0 + u * (int)blockDim.x < n_per_q && x[u] <= pivot && x[u] != KEY_MAX) sel[atomicAdd(&n_sel, 1)] = x[u];
   }
   __syncthreads();
   int P = 1;
