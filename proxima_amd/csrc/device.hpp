@@ -131,6 +131,9 @@ template <int METRIC>
 __device__ inline float dist_group8(const float* __restrict__ a, const float* __restrict__ b, int dim, int g) {
   float acc = 0.0f;
   const int chunks = dim >> 3;
+  // unrolled so that 16 chunks' loads are in flight together; the adds stay
+  // in chunk order
+#pragma unroll 16
   for (int c = 0; c < chunks; ++c) acc += lane_term<METRIC>(a[c * 8 + g], b[c * 8 + g]);
   // ((0+1)+(2+3))+((4+5)+(6+7)): f32 addition is commutative, so the xor
   // partner order gives the same bits on every lane of the group.
