@@ -148,6 +148,53 @@ __device__ inline float dist_group8(const float* __restrict__ a, const float* __
   return r;
 }
 
+// dist_group8 for two rows b0 and b1 against the same a, in one loop: each
+// row keeps its own accumulator and add order, and both rows' loads (and a's,
+// once) are in flight together.
+template <int METRIC>
+__device__ inline void dist_group8_x2(const float* __restrict__ a, const float* __restrict__ b0,
+                                      const float* __restrict__ b1, int dim, int g, float& r0, float& r1) {
+  float acc0 = 0.0f, acc1 = 0.0f;
+  const int chunks = dim >> 3;
+#pragma unroll 16
+  for (int c = 0; c < chunks; ++c) {
+    const float x = a[c * 8 + g];
+    acc0 += lane_term<METRIC>(x, b0[c * 8 + g]);
+    acc1 += lane_term<METRIC>(x, b1[c * 8 + g]);
+  }
+  acc0 = acc0 + __shfl_xor(acc0, 1, WAVE);
+  acc1 = acc1 + __shfl_xor(acc1, 1, WAVE);
+  acc0 = acc0 + __shfl_xor(acc0, 2, WAVE);
+  acc1 = acc1 + __shfl_xor(acc1, 2, WAVE);
+  acc0 = acc0 + __shfl_xor(acc0, 4, WAVE);
+  acc1 = acc1 + __shfl_xor(acc1, 4, WAVE);
+  float t0 = 0.0f, t1 = 0.0f;
+  for (int i = chunks * 8; i < dim; ++i) {
+    t0 += lane_term<METRIC>(a[i], b0[i]);
+    t1 += lane_term<METRIC>(a[i], b1[i]);
+  }
+  r0 = acc0 + t0;
+  r1 = acc1 + t1;
+  if constexpr (METRIC == 1) {
+    r0 = arm_nan(1.0f - arm_nan(r0));
+    r1 = arm_nan(1.0f - arm_nan(r1));
+  }
+  if constexpr (METRIC == 2) {
+    r0 = -arm_nan(r0);
+    r1 = -arm_nan(r1);
+  }
+}
+
+__device__ inline void dist_group8_x2_rt(int metric, const float* a, const float* b0, const float* b1, int dim, int g,
+                                         float& r0, float& r1) {
+  switch (metric) {
+    case 0: dist_group8_x2<0>(a, b0, b1, dim, g, r0, r1); break;
+    case 1: dist_group8_x2<1>(a, b0, b1, dim, g, r0, r1); break;
+    case 2: dist_group8_x2<2>(a, b0, b1, dim, g, r0, r1); break;
+    default: dist_group8_x2<3>(a, b0, b1, dim, g, r0, r1); break;
+  }
+}
+
 // One thread computes the whole distance (same arithmetic as dist_group8).
 template <int METRIC>
 __device__ inline float dist_thread(const float* __restrict__ a, const float* __restrict__ b, int dim) {

@@ -11,6 +11,13 @@ namespace pxg {
 
 constexpr int EXACT_CH = 1024;
 
+// Rows per chunk of the exact scan: EXACT_CH, or 256 when EXACT_CH-row
+// chunks would give the launch fewer workgroups than there are CUs (a single
+// query over a small store), so that more of the GPU scans at once.
+inline int exact_chunk_rows(size_t nq, size_t N) {
+  return nq * ((N + EXACT_CH - 1) / EXACT_CH) < 256 ? 256 : EXACT_CH;
+}
+
 // Small fills done by kernels rather than memsets (so that a caller's stream
 // holds only kernel work): the query flag word ~0, the flagged-query count 0.
 static __global__ void init_search_flags(unsigned long long* bad, int* flag_count) {
@@ -97,30 +104,56 @@ __device__ inline void block_bitonic_sort(uint64_t* keys, int n) {
 // ---------------------------------------------------------------------------
 // 4. exact VALU scan for a list of queries
 // ---------------------------------------------------------------------------
+template <int CH>
 static __global__ __launch_bounds__(256) void flat_exact_candidates(
     const int* __restrict__ qlist, const int* __restrict__ qcount, int nchunks, const float* __restrict__ Qp, int ld,
     int dim, int metric, const float* __restrict__ X, int N, const uint8_t* __restrict__ live,
     const uint8_t* __restrict__ accept, const uint32_t* __restrict__ rank, int k, uint64_t* __restrict__ ecand) {
-  __shared__ uint64_t keys[EXACT_CH];
+  __shared__ uint64_t keys[CH];
   const int total = (*qcount) * nchunks;
   const int g = threadIdx.x & 7, grp = threadIdx.x >> 3;
-  const int kk = min(k, EXACT_CH);
+  const int kk = min(k, CH);
   for (int w = blockIdx.x; w < total; w += gridDim.x) {
     const int f = w / nchunks, c = w % nchunks;
     const int q = qlist[f];
     const float* qv = Qp + (size_t)q * ld;
-    const int base = c * EXACT_CH;
-    for (int s = grp; s < EXACT_CH; s += 32) {
-      const int slot = base + s;
-      uint64_t key = KEY_MAX;
-      if (slot < N && live[slot] && (accept == nullptr || accept[slot])) {
-        const float d = dist_group8_rt(metric, qv, X + (size_t)slot * ld, dim, g);
-        key = ((uint64_t)ord_key(d) << 32) | rank[slot];
+    const int base = c * CH;
+    if (dim < 256) {
+      // a row's chunks fit one batch of loads (dist_group8 unrolls 16)
+      for (int s = grp; s < CH; s += 32) {
+        const int slot = base + s;
+        uint64_t key = KEY_MAX;
+        if (slot < N && live[slot] && (accept == nullptr || accept[slot])) {
+          const float d = dist_group8_rt(metric, qv, X + (size_t)slot * ld, dim, g);
+          key = ((uint64_t)ord_key(d) << 32) | rank[slot];
+        }
+        if (g == 0) keys[s] = key;
       }
-      if (g == 0) keys[s] = key;
+    } else {
+      // two rows per group at a time (s and s + 32), both rows' loads in
+      // flight together; rows past N or not usable are scored from a clamped
+      // row and keep KEY_MAX
+      static_assert(CH % 64 == 0, "row pairs");
+      for (int s = grp; s < CH; s += 64) {
+        const int s0 = base + s, s1 = base + s + 32;
+        const bool u0 = s0 < N && live[s0] && (accept == nullptr || accept[s0]);
+        const bool u1 = s1 < N && live[s1] && (accept == nullptr || accept[s1]);
+        uint64_t k0 = KEY_MAX, k1 = KEY_MAX;
+        if (__any(u0 || u1)) {
+          float d0, d1;
+          dist_group8_x2_rt(metric, qv, X + (size_t)max(min(s0, N - 1), 0) * ld, X + (size_t)max(min(s1, N - 1), 0) * ld,
+                            dim, g, d0, d1);
+          if (u0) k0 = ((uint64_t)ord_key(d0) << 32) | rank[s0];
+          if (u1) k1 = ((uint64_t)ord_key(d1) << 32) | rank[s1];
+        }
+        if (g == 0) {
+          keys[s] = k0;
+          keys[s + 32] = k1;
+        }
+      }
     }
     __syncthreads();
-    block_bitonic_sort(keys, EXACT_CH);
+    block_bitonic_sort(keys, CH);
     uint64_t* out = ecand + ((size_t)f * nchunks + c) * kk;
     for (int i = threadIdx.x; i < kk; i += blockDim.x) out[i] = keys[i];
     __syncthreads();
@@ -129,6 +162,7 @@ static __global__ __launch_bounds__(256) void flat_exact_candidates(
 
 constexpr int EXACT_MERGE_MAXK = 1024;
 
+template <int CH>
 static __global__ __launch_bounds__(256) void flat_merge_exact(const int* __restrict__ qlist, const int* __restrict__ qcount,
                                                         const uint64_t* __restrict__ ecand, int nchunks, int k,
                                                         const uint32_t* __restrict__ rank_slot,
@@ -143,7 +177,7 @@ static __global__ __launch_bounds__(256) void flat_merge_exact(const int* __rest
   __shared__ uint64_t sh[4];
   __shared__ uint64_t sel[EXACT_MERGE_MAXK];
   __shared__ int n_sel, n_valid;
-  const int kk = min(k, EXACT_CH);
+  const int kk = min(k, CH);
   const uint64_t* base = ecand + (size_t)f * nchunks * kk;
   const int n = nchunks * kk;
   auto get = [&](int i) -> uint64_t { return base[i]; };

@@ -719,8 +719,9 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
   read_flags(&nflag);
   if (nflag > 0) {
     sc.release_from(6);  // the candidate buffers are dead
-    const int nchunks = (int)((N + EXACT_CH - 1) / EXACT_CH);
-    const int kk = (int)std::min<uint64_t>(kq, EXACT_CH);
+    const int CH = exact_chunk_rows((size_t)nflag, N);
+    const int nchunks = (int)((N + CH - 1) / CH);
+    const int kk = (int)std::min<uint64_t>(kq, (uint64_t)CH);
     const size_t per_query = (size_t)nchunks * kk * 8;
     size_t fit = sc.room() / per_query;
     if (fit == 0) (void)sc.get(7, per_query);  // raises the capacity error
@@ -734,13 +735,19 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
         hipLaunchKernelGGL(set_int, dim3(1), dim3(64), 0, s, grp_count, gn);
         count = grp_count;
       }
-      hipLaunchKernelGGL(flat_exact_candidates, dim3(std::min(gn * nchunks, 4096)), dim3(256), 0, s,
-                         flag_list + g0, count, nchunks, Qp, (int)ld, (int)dim, metric, X.p, (int)N, d_live.p,
-                         d_accept, ranks.rank.p, (int)kq, ecand);
+#define PXG_EXACT_SCAN(CHV)                                                                                   \
+  hipLaunchKernelGGL(flat_exact_candidates<CHV>, dim3(std::min(gn * nchunks, 4096)), dim3(256), 0, s,          \
+                     flag_list + g0, count, nchunks, Qp, (int)ld, (int)dim, metric, X.p, (int)N, d_live.p,     \
+                     d_accept, ranks.rank.p, (int)kq, ecand)
+#define PXG_EXACT_MERGE(CHV)                                                                                  \
+  hipLaunchKernelGGL(flat_merge_exact<CHV>, dim3((unsigned)gn), dim3(256), 0, s, flag_list + g0, count, ecand, \
+                     nchunks, (int)kq, ranks.rank_slot.p, d_ids.p, d_oid, d_od, d_oc, (uint64_t*)nullptr, ldo)
+      if (CH == 256) PXG_EXACT_SCAN(256); else PXG_EXACT_SCAN(EXACT_CH);
       PXG_HIP(hipGetLastError());
       if (exact_all && g0 == 0) tm.mark(2);
-      hipLaunchKernelGGL(flat_merge_exact, dim3((unsigned)gn), dim3(256), 0, s, flag_list + g0, count, ecand,
-                         nchunks, (int)kq, ranks.rank_slot.p, d_ids.p, d_oid, d_od, d_oc, (uint64_t*)nullptr, ldo);
+      if (CH == 256) PXG_EXACT_MERGE(256); else PXG_EXACT_MERGE(EXACT_CH);
+#undef PXG_EXACT_SCAN
+#undef PXG_EXACT_MERGE
       PXG_HIP(hipGetLastError());
     }
     PXG_HIP(hipStreamSynchronize(s));

@@ -2115,17 +2115,24 @@ struct IvfPqIndex {
       int* qlist = (int*)sc.get(5, nq * 4);
       hipLaunchKernelGGL(iota_kernel, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s, qlist, (int)nq,
                          flag_count);
-      const int nchunks = (int)((N + EXACT_CH - 1) / EXACT_CH);
-      const int kk = (int)std::min<uint64_t>(kq, EXACT_CH);
+      const int CH = exact_chunk_rows((size_t)nq, N);
+      const int nchunks = (int)((N + CH - 1) / CH);
+      const int kk = (int)std::min<uint64_t>(kq, (uint64_t)CH);
       uint64_t* ecand = (uint64_t*)sc.get(7, (size_t)nq * nchunks * kk * 8);
       tm.mark(1);
-      hipLaunchKernelGGL(flat_exact_candidates, dim3(std::min<int>((int)nq * nchunks, 4096)), dim3(256), 0, s, qlist,
-                         flag_count, nchunks, Qp, (int)ld, (int)dim, metric, X.p, (int)N, d_live.p, d_accept,
-                         ranks.rank.p, (int)kq, ecand);
+#define PXG_EXACT_SCAN(CHV)                                                                                       \
+  hipLaunchKernelGGL(flat_exact_candidates<CHV>, dim3(std::min<int>((int)nq * nchunks, 4096)), dim3(256), 0, s,    \
+                     qlist, flag_count, nchunks, Qp, (int)ld, (int)dim, metric, X.p, (int)N, d_live.p, d_accept,  \
+                     ranks.rank.p, (int)kq, ecand)
+#define PXG_EXACT_MERGE(CHV)                                                                                      \
+  hipLaunchKernelGGL(flat_merge_exact<CHV>, dim3((unsigned)nq), dim3(256), 0, s, qlist, flag_count, ecand, nchunks, \
+                     (int)kq, ranks.rank_slot.p, d_ids.p, d_oid, d_od, d_oc, (uint64_t*)nullptr, ldo)
+      if (CH == 256) PXG_EXACT_SCAN(256); else PXG_EXACT_SCAN(EXACT_CH);
       PXG_HIP(hipGetLastError());
       tm.mark(2);
-      hipLaunchKernelGGL(flat_merge_exact, dim3((unsigned)nq), dim3(256), 0, s, qlist, flag_count, ecand, nchunks,
-                         (int)kq, ranks.rank_slot.p, d_ids.p, d_oid, d_od, d_oc, (uint64_t*)nullptr, ldo);
+      if (CH == 256) PXG_EXACT_MERGE(256); else PXG_EXACT_MERGE(EXACT_CH);
+#undef PXG_EXACT_SCAN
+#undef PXG_EXACT_MERGE
       PXG_HIP(hipGetLastError());
     } else {
       const int np = (int)std::min<uint64_t>(std::max<uint64_t>(nprobe_in, 1), (uint64_t)std::max(produced, 1));

@@ -1264,7 +1264,7 @@ struct Sq8Index {
                          (int)KP, (const int8_t*)codes.p, N, d_live.p, d_accept, ranks.rank.p, kk, ecand);
       PXG_HIP(hipGetLastError());
       if (!mfma) tm.mark(2);
-      hipLaunchKernelGGL(flat_merge_exact, dim3((unsigned)nflag), dim3(256), 0, s, (const int*)flag_list,
+      hipLaunchKernelGGL(flat_merge_exact<EXACT_CH>, dim3((unsigned)nflag), dim3(256), 0, s, (const int*)flag_list,
                          (const int*)flag_count, (const uint64_t*)ecand, nchunks, kk, ranks.rank_slot.p, d_ids.p,
                          (uint64_t*)nullptr, (float*)nullptr, ocount, okeys, (size_t)kk);
       PXG_HIP(hipGetLastError());
