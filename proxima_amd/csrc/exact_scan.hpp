@@ -187,7 +187,14 @@ static __global__ __launch_bounds__(256) void flat_merge_exact(const int* __rest
   }
   __syncthreads();
   int local = 0;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) local += base[i] != KEY_MAX;
+  // four keys per thread per step, loaded together before any is used
+  for (int i0 = threadIdx.x; i0 < n; i0 += 4 * blockDim.x) {
+    uint64_t x[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) x[u] = base[min(i0 + u * (int)blockDim.x, n - 1)];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) local += (i0 + u * (int)blockDim.x < n && x[u] != KEY_MAX) ? 1 : 0;
+  }
   atomicAdd(&n_valid, local);
   __syncthreads();
   const int ksel = min(k, n_valid);
@@ -195,10 +202,16 @@ static __global__ __launch_bounds__(256) void flat_merge_exact(const int* __rest
     if (threadIdx.x == 0) out_count[q] = 0;
     return;
   }
-  const uint64_t pivot = block_radix_select(get, n, ksel, hist, sh);
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const uint64_t x = base[i];
-    if (x <= pivot && x != KEY_MAX) sel[atomicAdd(&n_sel, 1)] = x;
+  const uint64_t pivot = n <= 16 * (int)blockDim.x   ? block_radix_select<decltype(get), 64, 16>(get, n, ksel, hist, sh)
+                         : n <= 40 * (int)blockDim.x ? block_radix_select<decltype(get), 64, 40>(get, n, ksel, hist, sh)
+                                                     : block_radix_select(get, n, ksel, hist, sh);
+  for (int i0 = threadIdx.x; i0 < n; i0 += 4 * blockDim.x) {
+    uint64_t x[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) x[u] = base[min(i0 + u * (int)blockDim.x, n - 1)];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (i0 + u * (int)blockDim.x < n && x[u] <= pivot && x[u] != KEY_MAX) sel[atomicAdd(&n_sel, 1)] = x[u];
   }
   __syncthreads();
   int P = 1;
