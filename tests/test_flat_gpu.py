@@ -168,6 +168,30 @@ def test_parity_random_shapes(gpu, metric, mode):
         assert_same(idx.search_batch(q, k), oracle_search(px, data, ids, metric, q, k))
 
 
+@pytest.mark.parametrize("metric", [0, 1, 2, 3])
+def test_exact_scan_wide_rows(gpu, metric):
+    """The exact scan's two-rows-per-group form (rows of 256+ dims, a tail
+    past the last multiple of 8) with removed rows, a filter and a store
+    whose size is not a multiple of the row pairs; one query (256-row
+    chunks) and 40 queries over 9000 rows (1024-row chunks)."""
+    px = gpu
+    rng = np.random.default_rng(31 + metric)
+    for (n, dim, nq, k) in [(1500, 260, 1, 7), (9000, 264, 40, 25)]:
+        data = rng.standard_normal((n, dim)).astype(np.float32)
+        q = rng.standard_normal((nq, dim)).astype(np.float32)
+        ids = rng.permutation(n * 2)[:n].astype(np.uint64)
+        idx = make_index(px, data, metric, ids, 2)
+        gone = rng.choice(n, n // 10, replace=False)
+        for i in gone:
+            idx.remove(int(ids[i]))
+        live = np.ones(n, np.uint8)
+        live[gone] = 0
+        assert_same(idx.search_batch(q, k), oracle_search(px, data, ids, metric, q, k, live=live))
+        keep = lambda i, _m: i % 4 != 1  # noqa: E731
+        acc = np.array([int(ids[s]) % 4 != 1 for s in range(n)], np.uint8)
+        assert_same(idx.search_batch(q, k, keep), oracle_search(px, data, ids, metric, q, k, live=live, accept=acc))
+
+
 @pytest.mark.parametrize("mode", MODES)
 def test_parity_with_holes_ties_and_filter(gpu, mode):
     px = gpu
