@@ -216,7 +216,7 @@ static void launch_assign(const float* P, int ldp, const uint32_t* rows, size_t 
 // eps: the fp32 dot product and norms over d terms, the final two roundings
 // and the exact sequential (or 8-lane) sum of squares each stay within
 // (2d + 6) * 2^-24 * (|p| + max|c|)^2; twice that is used.
-constexpr int KA_M = 128, KA_N = 128, KA_K = 32, KA_LDR = KA_K + 4;
+constexpr int KA_M = 128, KA_N = 128, KA_K = 32;
 
 // |row|^2 in fp32 (any order; it only feeds the approximation): eight lanes
 // per row, float4 loads (rows 16-byte aligned, dim a multiple of 4).
@@ -251,20 +251,38 @@ __global__ __launch_bounds__(1024) void km_max_of(const float* __restrict__ v, i
   if (threadIdx.x == 0) out[0] = sh[0];
 }
 
+// 16 zero bytes: the source of slice chunks past the end of a row.
+__device__ const float4 km_zero16 = {0.0f, 0.0f, 0.0f, 0.0f};
+
+// Global -> LDS copy of 16 bytes per lane (lane i's bytes land at m0 + 16 i),
+// 64-bit address per lane. Inline asm, so that the compiler does not count
+// it under vmcnt; km_mfma_top waits for it with km_vm_wait0 before each
+// slice's barrier and uses m0 for nothing else.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void km_lds_copy16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+__device__ __forceinline__ void km_vm_wait0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 __global__ __launch_bounds__(256, 2) void km_mfma_top(const float* __restrict__ P, int ldp,
                                                       const uint32_t* __restrict__ rows, int n, int dim,
                                                       const float* __restrict__ C, int ldc, int k,
                                                       const float* __restrict__ pn, const float* __restrict__ cn,
                                                       uint32_t* __restrict__ best_idx, float* __restrict__ best,
                                                       float* __restrict__ second) {
-  // k slices (sA, sB) and, after each tile's k loop, the tile's dot
-  // products (dt) share one LDS buffer. A dt row holds columns 0-63, a
-  // 4-float gap, then columns 64-127, so that the two threads of a row read
-  // their halves as float4 without bank conflicts.
-  constexpr int SLICE = KA_M * KA_LDR, DT_LD = KA_N + 8;
-  static_assert(KA_M * DT_LD <= 4 * SLICE, "tile of dot products fits the slice buffers");
-  static_assert(KA_N == 128, "two 64-column halves per row");
-  __shared__ __align__(16) float smem[4 * SLICE];
+  // k slices of the points (A) and of the centroids (B), double-buffered,
+  // and after each tile's k loop the tile's dot products (dt), share one LDS
+  // buffer. The slices are unpadded 128 x 32 floats: 16-byte chunk c of row
+  // r sits at position c ^ (r & 7), so the MFMA operand reads are
+  // conflict-free. A dt row holds columns 0-63, a 4-float gap, then columns
+  // 64-127, so that the two threads of a row read their halves as float4
+  // without bank conflicts.
+  constexpr int SLICE = KA_M * KA_K, DT_LD = KA_N + 8;
+  static_assert(KA_M == KA_N && 4 * SLICE <= KA_M * DT_LD, "slices fit the dot-product tile");
+  static_assert(KA_N == 128 && KA_K == 32, "two 64-column halves per row; 8 chunks per slice row");
+  __shared__ __align__(16) float smem[KA_M * DT_LD];
   __shared__ __align__(16) float spn[KA_M];
   __shared__ __align__(16) float scn[KA_N];
   float* dt = smem;
@@ -273,13 +291,34 @@ __global__ __launch_bounds__(256, 2) void km_mfma_top(const float* __restrict__ 
   const int wm = (wid >> 1) * 64, wn = (wid & 1) * 64;
   const int p0 = blockIdx.x * KA_M;
   for (int i = tid; i < KA_M; i += 256) spn[i] = p0 + i < n ? pn[p0 + i] : 0.0f;
-  const int lr = tid >> 3, lc = (tid & 7) * 4;
+  // DMA lanes: instruction u of wave wid fills rows 32 wid + 8 u .. +7 of a
+  // slice, lane l landing at chunk position l & 7 of row 8 u + l / 8, so it
+  // fetches that row's chunk (l & 7) ^ (row & 7). Rows past n (points) or k
+  // (centroids) read a valid row: their products only reach outputs that are
+  // never used.
+  const int crow0 = 32 * wid + (lane >> 3), cchunk = (lane & 7) ^ ((lane >> 3) & 7);
   const float* prow[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    const int p = p0 + lr + 32 * u;
-    prow[u] = p < n ? P + (size_t)(rows ? rows[p] : (uint32_t)p) * ldp : nullptr;
+    const int p = min(p0 + crow0 + 8 * u, n - 1);
+    prow[u] = P + (size_t)(rows ? rows[p] : (uint32_t)p) * ldp;
   }
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float*)smem;
+  const int wid_s = __builtin_amdgcn_readfirstlane(wid);
+  // slice k0 of centroid tile n0 into buffer buf
+  auto gload = [&](int n0, int k0, int buf) __attribute__((always_inline)) {
+    const int kc = k0 + cchunk * 4;
+    const bool kin = kc < dim;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = min(n0 + crow0 + 8 * u, k - 1);
+      const float* pa = kin ? prow[u] + kc : reinterpret_cast<const float*>(&km_zero16);
+      const float* pb = kin ? C + (size_t)c * ldc + kc : reinterpret_cast<const float*>(&km_zero16);
+      const uint32_t grp = (uint32_t)((32 * wid_s + 8 * u) * KA_K * 4);
+      km_lds_copy16(pa, lds0 + (uint32_t)(buf * SLICE * 4) + grp);
+      km_lds_copy16(pb, lds0 + (uint32_t)((2 + buf) * SLICE * 4) + grp);
+    }
+  };
   const int nK = (dim + KA_K - 1) / KA_K;
   // this thread scans row tid/2, columns 64 (tid&1) .. +63 of every tile
   const int my_row = tid >> 1, my_par = tid & 1;
@@ -293,44 +332,28 @@ __global__ __launch_bounds__(256, 2) void km_mfma_top(const float* __restrict__ 
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-    float4 ra[4], rb[4];
-    auto gload = [&](int k0) {
-      const int kc = k0 + lc;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int c = n0 + lr + 32 * u;
-        ra[u] = (prow[u] && kc < dim) ? *reinterpret_cast<const float4*>(prow[u] + kc) : make_float4(0.f, 0.f, 0.f, 0.f);
-        rb[u] = (c < k && kc < dim) ? *reinterpret_cast<const float4*>(C + (size_t)c * ldc + kc)
-                                    : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-    };
-    auto lstore = [&](int buf) {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int row = lr + 32 * u;
-        *reinterpret_cast<float4*>(&smem[buf * SLICE + row * KA_LDR + lc]) = ra[u];
-        *reinterpret_cast<float4*>(&smem[(2 + buf) * SLICE + row * KA_LDR + lc]) = rb[u];
-      }
-    };
-    gload(0);
     __syncthreads();  // the previous tile's scan of dt is done
-    lstore(0);
     if (tid < KA_N) scn[tid] = n0 + tid < k ? cn[n0 + tid] : 0.0f;
+    gload(n0, 0, 0);
+    km_vm_wait0();
     __syncthreads();
     for (int kt = 0; kt < nK; ++kt) {
       const int cur = kt & 1;
-      if (kt + 1 < nK) gload((kt + 1) * KA_K);
-      // lane (h, r) feeds k = h*16 + kk of row r; A and B agree on that map
-      const float* a0p = &smem[cur * SLICE + (wm + r) * KA_LDR + h * 16];
-      const float* a1p = &smem[cur * SLICE + (wm + 32 + r) * KA_LDR + h * 16];
-      const float* b0p = &smem[(2 + cur) * SLICE + (wn + r) * KA_LDR + h * 16];
-      const float* b1p = &smem[(2 + cur) * SLICE + (wn + 32 + r) * KA_LDR + h * 16];
+      if (kt + 1 < nK) gload(n0, (kt + 1) * KA_K, cur ^ 1);
+      // lane (h, r) feeds k = h*16 + 4 k4 + t of row r: chunk 4h + k4,
+      // stored at position (4h + k4) ^ (r & 7); A and B agree on that map
+      const float* a0p = &smem[cur * SLICE + (wm + r) * KA_K];
+      const float* a1p = &smem[cur * SLICE + (wm + 32 + r) * KA_K];
+      const float* b0p = &smem[(2 + cur) * SLICE + (wn + r) * KA_K];
+      const float* b1p = &smem[(2 + cur) * SLICE + (wn + 32 + r) * KA_K];
+      const int r7 = r & 7;
 #pragma unroll
       for (int k4 = 0; k4 < 4; ++k4) {
-        const float4 a0 = *reinterpret_cast<const float4*>(a0p + k4 * 4);
-        const float4 a1 = *reinterpret_cast<const float4*>(a1p + k4 * 4);
-        const float4 q0 = *reinterpret_cast<const float4*>(b0p + k4 * 4);
-        const float4 q1 = *reinterpret_cast<const float4*>(b1p + k4 * 4);
+        const int co = ((4 * h + k4) ^ r7) * 4;
+        const float4 a0 = *reinterpret_cast<const float4*>(a0p + co);
+        const float4 a1 = *reinterpret_cast<const float4*>(a1p + co);
+        const float4 q0 = *reinterpret_cast<const float4*>(b0p + co);
+        const float4 q1 = *reinterpret_cast<const float4*>(b1p + co);
         const float av0[4] = {a0.x, a0.y, a0.z, a0.w}, av1[4] = {a1.x, a1.y, a1.z, a1.w};
         const float bv0[4] = {q0.x, q0.y, q0.z, q0.w}, bv1[4] = {q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
@@ -341,7 +364,7 @@ __global__ __launch_bounds__(256, 2) void km_mfma_top(const float* __restrict__ 
           acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(av1[t], bv1[t], acc[1][1], 0, 0, 0);
         }
       }
-      if (kt + 1 < nK) lstore(cur ^ 1);
+      km_vm_wait0();  // this wave's copies of the next slice have landed
       __syncthreads();
     }
     // the tile's dot products to LDS, then each thread scans its row's
