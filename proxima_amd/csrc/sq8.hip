@@ -14,7 +14,7 @@
 //
 // Kernels
 //   sq_minmax / sq_encode_rows          range training and encoding
-//   sq8_mfma_scan<KB,QT,STAGE1>         i8 x i8 -> i32 on v_mfma_i32_32x32x32_i8
+//   sq8_mfma_scan<KB,STAGE1>            i8 x i8 -> i32 on v_mfma_i32_32x32x32_i8
 //       stage 1: every SQ_SAMPLE-th row tile, per-lane maxima over usable rows
 //       stage 2: every tile; a v_max3 chain and one compare per 16 scores,
 //                rows scoring >= the query's threshold are appended
