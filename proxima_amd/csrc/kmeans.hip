@@ -324,6 +324,7 @@ __global__ __launch_bounds__(256, 2) void km_mfma_top(const float* __restrict__ 
   const int my_row = tid >> 1, my_par = tid & 1;
   float b1 = INFINITY, b2 = INFINITY;
   int i1 = 0;
+  bool nan_seen = false;
   for (int n0 = 0; n0 < k; n0 += KA_N) {
     f16v acc[2][2];
 #pragma unroll
@@ -380,15 +381,16 @@ __global__ __launch_bounds__(256, 2) void km_mfma_top(const float* __restrict__ 
     const float prn = spn[my_row];
     const float* drow = dt + my_row * DT_LD + my_par * 68;
     const int c0 = my_par * 64, cols = min(KA_N, k - n0);
-    // branch-free form of: x < b1 -> (b2 = min(b1, b2), b1 = x, i1 = m);
-    // else x < b2 -> b2 = x; else NaN -> b2 = -inf (the point takes the exact
-    // scan; fminf keeps that mark)
+    // Smallest, its first column (strict <) and second-smallest, in column
+    // order. With b1 <= b2 the new second-smallest is the median of (b1, b2,
+    // x) and the new smallest min(b1, x): one med3 and one min per value. A
+    // NaN (overflow) is only noted here; it sets b2 = -inf after the last
+    // tile, which sends the point to the exact scan.
     auto take = [&](float x, int m) {
-      const bool lt1 = x < b1, lt2 = x < b2, nan = !(x == x);
-      const float nb2 = lt1 ? fminf(b1, b2) : lt2 ? x : nan ? -INFINITY : b2;
-      i1 = lt1 ? n0 + m : i1;
-      b1 = lt1 ? x : b1;
-      b2 = nb2;
+      i1 = x < b1 ? n0 + m : i1;
+      b2 = __builtin_amdgcn_fmed3f(b1, b2, x);
+      b1 = fminf(b1, x);
+      nan_seen |= !(x == x);
     };
     if (cols == KA_N) {
 #pragma unroll
@@ -404,6 +406,7 @@ __global__ __launch_bounds__(256, 2) void km_mfma_top(const float* __restrict__ 
       for (int m = c0; m < min(cols, c0 + 64); ++m) take((prn + scn[m]) - 2.0f * drow[m - c0], m);
     }
   }
+  if (nan_seen) b2 = -INFINITY;
   // merge the two threads of each row
   const float y1 = __shfl_xor(b1, 1, WAVE), y2 = __shfl_xor(b2, 1, WAVE);
   const int yi = __shfl_xor(i1, 1, WAVE);
