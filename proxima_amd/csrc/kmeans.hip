@@ -199,11 +199,11 @@ static void launch_assign(const float* P, int ldp, const uint32_t* rows, size_t 
 // assignment on FP32 MFMA with exact verification
 // ---------------------------------------------------------------------------
 // km_mfma_top: for a block of 128 points, approximate squared distances to
-// every centroid, (|p|^2 + |c|^2) - 2 p.c with the dot product on
-// v_mfma_f32_32x32x2f32 (128x128 tiles, 32-wide k slices double-buffered in
-// LDS). Each lane keeps, per row it owns, the smallest and second-smallest
-// approximate distance (and the smallest's centroid) over the columns it
-// sees; the lanes and waves are merged at the end.
+// every centroid less the point's own |p|^2, a = |c|^2 - 2 p.c (one fma),
+// with the dot product on v_mfma_f32_32x32x2f32 (128x128 tiles, 32-wide k
+// slices double-buffered in LDS). Each lane keeps, per row it owns, the
+// smallest and second-smallest approximation (and the smallest's centroid)
+// over the columns it sees; the lanes and waves are merged at the end.
 //
 // km_mfma_verify: with eps a bound on |approx - exact| for every centroid of
 // the point, every centroid whose exact distance could tie or beat the
@@ -213,9 +213,20 @@ static void launch_assign(const float* P, int ldp, const uint32_t* rows, size_t 
 // 2 eps too); its exact distance is recomputed with the reference's own
 // arithmetic. Other points are listed and take the exact VALU scan.
 //
-// eps: the fp32 dot product and norms over d terms, the final two roundings
-// and the exact sequential (or 8-lane) sum of squares each stay within
+// A point's approximations all omit the same |p|^2, so their differences are
+// those of the exact distances up to the errors below, and the certificate
+// only compares differences.
+//
+// eps: the fp32 dot product and norms over d terms, the final rounding and
+// the exact sequential (or 8-lane) sum of squares each stay within
 // (2d + 6) * 2^-24 * (|p| + max|c|)^2; twice that is used.
+//
+// Non-finite values: with finite coordinates every partial sum of the
+// approximation is at most (|p| + |c|)^2 in magnitude, which is below s^2 in
+// km_mfma_verify's bound, so the approximations are finite whenever eps is.
+// A NaN or infinite coordinate makes that row's norm non-finite (km_max_of
+// propagates a centroid's), eps is then not finite, and the point takes the
+// exact scan.
 constexpr int KA_M = 128, KA_N = 128, KA_K = 32;
 
 // |row|^2 in fp32 (any order; it only feeds the approximation): eight lanes
@@ -238,14 +249,21 @@ __global__ __launch_bounds__(256) void km_row_norms(const float* __restrict__ P,
   if (i < n && sub == 0) out[i] = s;
 }
 
+// The largest of v[0..n), or NaN if any is NaN.
 __global__ __launch_bounds__(1024) void km_max_of(const float* __restrict__ v, int n, float* __restrict__ out) {
   __shared__ float sh[1024];
   float m = 0.0f;
-  for (int i = threadIdx.x; i < n; i += 1024) m = fmaxf(m, v[i]);
+  for (int i = threadIdx.x; i < n; i += 1024) {
+    const float x = v[i];
+    m = x > m || x != x ? x : m;  // a NaN, once taken, stays
+  }
   sh[threadIdx.x] = m;
   __syncthreads();
   for (int o = 512; o > 0; o >>= 1) {
-    if (threadIdx.x < o) sh[threadIdx.x] = fmaxf(sh[threadIdx.x], sh[threadIdx.x + o]);
+    if (threadIdx.x < o) {
+      const float x = sh[threadIdx.x + o];
+      if (x > sh[threadIdx.x] || x != x) sh[threadIdx.x] = x;
+    }
     __syncthreads();
   }
   if (threadIdx.x == 0) out[0] = sh[0];
@@ -269,7 +287,7 @@ __device__ __forceinline__ void km_vm_wait0() { asm volatile("s_waitcnt vmcnt(0)
 __global__ __launch_bounds__(256, 2) void km_mfma_top(const float* __restrict__ P, int ldp,
                                                       const uint32_t* __restrict__ rows, int n, int dim,
                                                       const float* __restrict__ C, int ldc, int k,
-                                                      const float* __restrict__ pn, const float* __restrict__ cn,
+                                                      const float* __restrict__ cn,
                                                       uint32_t* __restrict__ best_idx, float* __restrict__ best,
                                                       float* __restrict__ second) {
   // k slices of the points (A) and of the centroids (B), double-buffered,
@@ -283,14 +301,12 @@ __global__ __launch_bounds__(256, 2) void km_mfma_top(const float* __restrict__ 
   static_assert(KA_M == KA_N && 4 * SLICE <= KA_M * DT_LD, "slices fit the dot-product tile");
   static_assert(KA_N == 128 && KA_K == 32, "two 64-column halves per row; 8 chunks per slice row");
   __shared__ __align__(16) float smem[KA_M * DT_LD];
-  __shared__ __align__(16) float spn[KA_M];
   __shared__ __align__(16) float scn[KA_N];
   float* dt = smem;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int h = lane >> 5, r = lane & 31;
   const int wm = (wid >> 1) * 64, wn = (wid & 1) * 64;
   const int p0 = blockIdx.x * KA_M;
-  for (int i = tid; i < KA_M; i += 256) spn[i] = p0 + i < n ? pn[p0 + i] : 0.0f;
   // DMA lanes: instruction u of wave wid fills rows 32 wid + 8 u .. +7 of a
   // slice, lane l landing at chunk position l & 7 of row 8 u + l / 8, so it
   // fetches that row's chunk (l & 7) ^ (row & 7). Rows past n (points) or k
@@ -323,8 +339,7 @@ __global__ __launch_bounds__(256, 2) void km_mfma_top(const float* __restrict__ 
   // this thread scans row tid/2, columns 64 (tid&1) .. +63 of every tile
   const int my_row = tid >> 1, my_par = tid & 1;
   float b1 = INFINITY, b2 = INFINITY;
-  int i1 = 0;
-  bool nan_seen = false;
+  int i1 = 0, t1 = 0;  // the smallest's column in its tile, and that tile
   for (int n0 = 0; n0 < k; n0 += KA_N) {
     f16v acc[2][2];
 #pragma unroll
@@ -378,35 +393,35 @@ __global__ __launch_bounds__(256, 2) void km_mfma_top(const float* __restrict__ 
         for (int v = 0; v < 16; ++v)
           dt[(wm + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3)) * DT_LD + wn + (wn >> 4) + j * 32 + r] = acc[i][j][v];
     __syncthreads();
-    const float prn = spn[my_row];
     const float* drow = dt + my_row * DT_LD + my_par * 68;
     const int c0 = my_par * 64, cols = min(KA_N, k - n0);
     // Smallest, its first column (strict <) and second-smallest, in column
     // order. With b1 <= b2 the new second-smallest is the median of (b1, b2,
-    // x) and the new smallest min(b1, x): one med3 and one min per value. A
-    // NaN (overflow) is only noted here; it sets b2 = -inf after the last
-    // tile, which sends the point to the exact scan.
+    // x) and the new smallest min(b1, x): one med3 and one min per value.
+    // The column is kept within this thread's half-tile (a constant per
+    // value); the tile is recorded once, after the tile, if b1 went down.
+    const float b1_in = b1;
     auto take = [&](float x, int m) {
-      i1 = x < b1 ? n0 + m : i1;
+      i1 = x < b1 ? m : i1;
       b2 = __builtin_amdgcn_fmed3f(b1, b2, x);
       b1 = fminf(b1, x);
-      nan_seen |= !(x == x);
     };
     if (cols == KA_N) {
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
         const float4 d4 = *reinterpret_cast<const float4*>(drow + 4 * q);
         const float4 s4 = *reinterpret_cast<const float4*>(scn + c0 + 4 * q);
-        take((prn + s4.x) - 2.0f * d4.x, c0 + 4 * q);
-        take((prn + s4.y) - 2.0f * d4.y, c0 + 4 * q + 1);
-        take((prn + s4.z) - 2.0f * d4.z, c0 + 4 * q + 2);
-        take((prn + s4.w) - 2.0f * d4.w, c0 + 4 * q + 3);
+        take(__builtin_fmaf(-2.0f, d4.x, s4.x), 4 * q);
+        take(__builtin_fmaf(-2.0f, d4.y, s4.y), 4 * q + 1);
+        take(__builtin_fmaf(-2.0f, d4.z, s4.z), 4 * q + 2);
+        take(__builtin_fmaf(-2.0f, d4.w, s4.w), 4 * q + 3);
       }
     } else {
-      for (int m = c0; m < min(cols, c0 + 64); ++m) take((prn + scn[m]) - 2.0f * drow[m - c0], m);
+      for (int m = c0; m < min(cols, c0 + 64); ++m) take(__builtin_fmaf(-2.0f, drow[m - c0], scn[m]), m - c0);
     }
+    t1 = b1 < b1_in ? n0 : t1;
   }
-  if (nan_seen) b2 = -INFINITY;
+  i1 += t1 + my_par * 64;
   // merge the two threads of each row
   const float y1 = __shfl_xor(b1, 1, WAVE), y2 = __shfl_xor(b2, 1, WAVE);
   const int yi = __shfl_xor(i1, 1, WAVE);
@@ -688,7 +703,7 @@ void nearest_device(const float* P, int ldp, const uint32_t* rows, size_t n, int
   PXG_HIP(hipEventCreate(&e1));
   PXG_HIP(hipEventRecord(e0, s));
   hipLaunchKernelGGL(km_mfma_top, dim3((unsigned)((n + KA_M - 1) / KA_M)), dim3(256), 0, s, P, ldp, rows, (int)n,
-                     dim, C, ldc, (int)k, (const float*)pn, (const float*)cn, bidx, best, second);
+                     dim, C, ldc, (int)k, (const float*)cn, bidx, best, second);
   PXG_HIP(hipEventRecord(e1, s));
   PXG_HIP(hipMemsetAsync(nredo, 0, 4, s));
   const dim3 g((unsigned)((n + KV_PB - 1) / KV_PB));

@@ -188,6 +188,34 @@ def test_assign_matrix_core_path_matches_oracle(gpu):
         assert np.array_equal(bits(d), bits(wd)), dim
 
 
+@pytest.mark.parametrize("case", ["centroid_nan", "centroid_inf", "centroid_norm_overflow", "points"])
+def test_assign_matrix_core_nonfinite(gpu, case):
+    """Non-finite values on the MFMA path: a NaN or infinite centroid
+    coordinate, or a centroid whose squared norm overflows, makes every
+    point's bound non-finite (all take the exact scan); NaN and infinite
+    point coordinates send only those points there. The assignments and
+    distances are the reference's (a NaN distance never wins: strict <)."""
+    px = gpu
+    rng = np.random.default_rng(21)
+    p = clustered(rng, 6000, 64, 30, 0.3)
+    c = p[rng.choice(6000, 200, replace=False)] + rng.standard_normal((200, 64)).astype(np.float32) * 0.05
+    if case == "centroid_nan":
+        c[7, 3] = np.nan
+    elif case == "centroid_inf":
+        c[150, 0] = np.inf
+    elif case == "centroid_norm_overflow":
+        c[33, :2] = np.float32(2e19)
+    else:
+        p[10, 5] = np.nan
+        p[11, 0] = np.inf
+        p[12, :] = -np.inf
+        p[13, 63] = np.float32(-3e38)
+    a, d = px.kmeans_assign(p, c)
+    wa, wd = orc.kmeans_assign(p, c)
+    assert np.array_equal(a, wa), case
+    assert np.array_equal(bits(d), bits(wd)), case
+
+
 def test_reference_kmeans_properties(gpu):  # kmeans.rs:271-336
     px = gpu
     r = px.kmeans(blobs(), 2, 3, 25, 0x00C0FFEE)
