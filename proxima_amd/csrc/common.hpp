@@ -157,6 +157,9 @@ struct SlotAllocator {
   void clear() { next = 0; free.clear(); }
 };
 
+// Pinned host words a search reads its device flags and counts back into.
+constexpr int TAIL_WORDS = 128;
+
 // Per-call execution context: a stream plus scratch memory. Searches on one
 // handle may run concurrently from many host threads; each takes its own
 // context from the pool, so no two calls share a stream or scratch.
@@ -170,11 +173,11 @@ struct Ctx {
     if (b.n < bytes) b.alloc(bytes + bytes / 8 + 256);
     return b.p;
   }
-  // Eight pinned host words: a search copies its device flags and counts
-  // here, so the copy is one direct DMA rather than a staged copy into
-  // pageable memory.
+  // TAIL_WORDS pinned host words: a search copies its device flags and
+  // counts here, so the copy is one direct DMA rather than a staged copy
+  // into pageable memory.
   unsigned long long* tail_host() {
-    if (!pinned) PXG_HIP(hipHostMalloc((void**)&pinned, 64, hipHostMallocDefault));
+    if (!pinned) PXG_HIP(hipHostMalloc((void**)&pinned, TAIL_WORDS * 8, hipHostMallocDefault));
     return pinned;
   }
   ~Ctx() {
@@ -194,7 +197,7 @@ struct Scratch {
   virtual size_t room() const { return SIZE_MAX; }
   // an arena takes back the region of `key` and everything carved after it
   virtual void release_from(int key) { (void)key; }
-  virtual unsigned long long* host_words() = 0;  // at least 8 words
+  virtual unsigned long long* host_words() = 0;  // TAIL_WORDS words
   virtual bool timing() const { return true; }   // stage timers may create events
 };
 
@@ -210,7 +213,7 @@ struct Arena : Scratch {
   unsigned char* base;
   size_t cap, off = 0;
   size_t start[KEYS];
-  unsigned long long words[8] = {};
+  unsigned long long words[TAIL_WORDS] = {};
   Arena(void* p, size_t bytes) : base((unsigned char*)p), cap(bytes) {
     for (size_t& x : start) x = SIZE_MAX;
   }

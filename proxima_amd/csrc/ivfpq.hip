@@ -362,6 +362,10 @@ __global__ __launch_bounds__(IVF_CW * 64) void ivf_coarse_dist(const float* __re
 // they are gathered in LDS and sorted. Should they exceed IVF_PICK_CAP, a
 // radix select of the np-th key takes over.
 constexpr int IVF_PICK_CAP = 1024;
+// The scanned-entry count is spread over this many counters (query q adds to
+// counter q % IVF_SCAN_SLOTS), so that a batch's workgroups do not all
+// update one address; the host adds them up.
+constexpr int IVF_SCAN_SLOTS = 64;
 __global__ __launch_bounds__(256) void ivf_coarse_pick(const uint64_t* __restrict__ ck, int cst, int produced, int np,
                                                        int* __restrict__ probes, const uint32_t* __restrict__ list_off,
                                                        unsigned long long* __restrict__ scanned) {
@@ -442,7 +446,7 @@ __global__ __launch_bounds__(256) void ivf_coarse_pick(const uint64_t* __restric
     uint32_t len = lane < np ? list_off[l + 1] - list_off[l] : 0u;
 #pragma unroll
     for (int st = 32; st > 0; st >>= 1) len += xor_lane_rt(len, st);
-    if (lane == 0) atomicAdd(scanned, (unsigned long long)len);
+    if (lane == 0) atomicAdd(scanned + (q & (IVF_SCAN_SLOTS - 1)), (unsigned long long)len);
   }
 }
 
@@ -529,15 +533,44 @@ __global__ __launch_bounds__(256) void ivf_coarse_pick_approx(const float* __res
   };
   const int ng = min(64, produced), gs = (produced + ng - 1) / ng;
   if (tid == 0) ncand = 0;
-  for (int g = w; g < 64; g += 4) {
-    float m = INFINITY;
-    if (g < ng) {
-      const int b = g * gs, e = min(produced, b + gs);
-      for (int i = b + lane; i < e; i += 64) m = fminf(m, a[i] + eps(i));
-    }
+  // Groups of up to 64 lists (up to 4096 lists): thread 4 g + u holds lists
+  // g gs + u + 4 j of group g, all loaded at once, and keeps a - eps of each
+  // for the candidate test, so the lists are read once.
+  const bool held = gs <= 64;
+  float lo[16];
+  if (held) {
+    const int g = tid >> 2, u = tid & 3;
+    const int b = g * gs, e = g < ng ? min(produced, b + gs) : b;
+    float av[16], cv[16];
 #pragma unroll
-    for (int st = 32; st > 0; st >>= 1) m = fminf(m, __shfl_xor(m, st, 64));
-    if (lane == 0) gmin[g] = m;
+    for (int j = 0; j < 16; ++j) {
+      const int i = min(b + u + 4 * j, produced - 1);
+      av[j] = a[i];
+      cv[j] = cn[i];
+    }
+    float m = INFINITY;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float sv = qv + cv[j];
+      const float ev = ef * sv * sv * 1.0001f + 1e-30f;
+      const bool in = b + u + 4 * j < e;
+      m = in ? fminf(m, av[j] + ev) : m;
+      lo[j] = in ? av[j] - ev : INFINITY;
+    }
+    m = fminf(m, __shfl_xor(m, 1, 64));
+    m = fminf(m, __shfl_xor(m, 2, 64));
+    if (u == 0) gmin[g] = m;
+  } else {
+    for (int g = w; g < 64; g += 4) {
+      float m = INFINITY;
+      if (g < ng) {
+        const int b = g * gs, e = min(produced, b + gs);
+        for (int i = b + lane; i < e; i += 64) m = fminf(m, a[i] + eps(i));
+      }
+#pragma unroll
+      for (int st = 32; st > 0; st >>= 1) m = fminf(m, __shfl_xor(m, st, 64));
+      if (lane == 0) gmin[g] = m;
+    }
   }
   __syncthreads();
   if (w == 0) {
@@ -551,11 +584,22 @@ __global__ __launch_bounds__(256) void ivf_coarse_pick_approx(const float* __res
   __syncthreads();
   const float t = s_t;
   const bool finite_t = t == t && t < INFINITY;
-  for (int i = tid; i < produced && finite_t; i += 256) {
-    const float av = a[i];
-    if (!(av - eps(i) > t)) {  // NaN a (overflow) is kept and rescored
-      const int at = atomicAdd(&ncand, 1);
-      if (at < IVF_PICK_CAP) cl[at] = i;
+  if (held && finite_t) {
+    const int g = tid >> 2, u = tid & 3, b = g * gs;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      if (!(lo[j] > t)) {  // NaN a (overflow) is kept and rescored
+        const int at = atomicAdd(&ncand, 1);
+        if (at < IVF_PICK_CAP) cl[at] = b + u + 4 * j;
+      }
+    }
+  } else {
+    for (int i = tid; i < produced && finite_t; i += 256) {
+      const float av = a[i];
+      if (!(av - eps(i) > t)) {  // NaN a (overflow) is kept and rescored
+        const int at = atomicAdd(&ncand, 1);
+        if (at < IVF_PICK_CAP) cl[at] = i;
+      }
     }
   }
   __syncthreads();
@@ -609,7 +653,7 @@ __global__ __launch_bounds__(256) void ivf_coarse_pick_approx(const float* __res
     uint32_t len = lane < np ? list_off[l + 1] - list_off[l] : 0u;
 #pragma unroll
     for (int st = 32; st > 0; st >>= 1) len += xor_lane_rt(len, st);
-    if (lane == 0) atomicAdd(scanned, (unsigned long long)len);
+    if (lane == 0) atomicAdd(scanned + (q & (IVF_SCAN_SLOTS - 1)), (unsigned long long)len);
   }
 }
 
@@ -1246,7 +1290,7 @@ __global__ void ivf_count_scanned(const int* __restrict__ probes, int n, const u
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const int l = probes[i];
-  atomicAdd(total, (unsigned long long)(list_off[l + 1] - list_off[l]));
+  atomicAdd(total + (i & (IVF_SCAN_SLOTS - 1)), (unsigned long long)(list_off[l + 1] - list_off[l]));
 }
 
 __global__ void ivf_gather_rows(const float* __restrict__ X, int ld, const uint32_t* __restrict__ rows, int n,
@@ -2095,7 +2139,9 @@ struct IvfPqIndex {
     float* Qp = (float*)sc.get(1, nq * ld * 4);
     float* qb = (float*)sc.get(2, nq * 4);
     float* qn = (float*)sc.get(3, nq * 4);
-    unsigned long long* bad = (unsigned long long*)sc.get(4, 32);
+    // flag word, flag count, then the IVF_SCAN_SLOTS scanned-entry counters
+    static_assert(2 + IVF_SCAN_SLOTS <= TAIL_WORDS, "one readback holds the flags and the counters");
+    unsigned long long* bad = (unsigned long long*)sc.get(4, 8 * (2 + IVF_SCAN_SLOTS));
     int* flag_count = (int*)(bad + 1);
     unsigned long long* scanned_dev = nullptr;
     uint64_t scanned_host = 0;
@@ -2148,7 +2194,8 @@ struct IvfPqIndex {
       int* probes = (int*)sc.get(9, (size_t)nq * np * 4);
       tm.mark(0);
       scanned_dev = (unsigned long long*)(flag_count + 2);
-      hipLaunchKernelGGL(fill_u32, dim3(1), dim3(64), 0, s, (uint32_t*)scanned_dev, (size_t)2, 0u);
+      hipLaunchKernelGGL(fill_u32, dim3(1), dim3(2 * IVF_SCAN_SLOTS), 0, s, (uint32_t*)scanned_dev,
+                         (size_t)(2 * IVF_SCAN_SLOTS), 0u);
       const bool fused_count = np <= 64 && dim <= 2048;
       // matrix-core distances with exact rescoring near the cut, for widths
       // where the GEMM outweighs the rescoring
@@ -2294,14 +2341,19 @@ struct IvfPqIndex {
       PXG_HIP(hipGetLastError());
       }
     }
-    // one copy brings back the validation flag and the scanned-entry count
-    // (bytes 0-7 and 16-23 of the same scratch block)
+    // one copy brings back the validation flag (word 0) and the scanned-entry
+    // counters (words 2 ..) of the same scratch block
     unsigned long long* tail = sc.host_words();
-    tail[0] = tail[1] = tail[2] = 0;
-    PXG_HIP(hipMemcpyAsync(tail, bad, scanned_dev ? 24 : 8, hipMemcpyDeviceToHost, s));
+    tail[0] = 0;
+    PXG_HIP(hipMemcpyAsync(tail, bad, scanned_dev ? 8 * (2 + IVF_SCAN_SLOTS) : 8, hipMemcpyDeviceToHost, s));
     PXG_HIP(hipStreamSynchronize(s));
     tm.finish();
-    const unsigned long long badv = tail[0], scanned = scanned_dev ? tail[2] : scanned_host;
+    uint64_t scanned = scanned_host;
+    if (scanned_dev) {
+      scanned = 0;
+      for (int i = 0; i < IVF_SCAN_SLOTS; ++i) scanned += tail[2 + i];
+    }
+    const unsigned long long badv = tail[0];
     g_last_scanned = scanned;
     if (badv != ~0ull) {
       const uint32_t qi = (uint32_t)(badv >> 32), comp = (uint32_t)badv;
