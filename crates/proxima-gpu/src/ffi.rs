@@ -149,6 +149,8 @@ extern "C" {
         assign_out: *mut u32, dist_out: *mut f32) -> c_int;
     pub(crate) fn pxg_kmeans_last_stats(mfma_ms: *mut f64, mfma_flops: *mut f64, mfma_passes: *mut u64,
         rescanned: *mut u64, inexact_sums: *mut u64) -> c_int;
+    pub(crate) fn pxg_kmeans_last_reseeds(reseeds: *mut u64, pool_reseeds: *mut u64,
+        pool_fallbacks: *mut u64) -> c_int;
     pub(crate) fn pxg_pq_train(training: *const f32, n: u64, dim: u32, subspaces: u64, max_iterations: u64,
         seed: u64, codebooks_out: *mut f32, inertia: *mut f64, iterations: *mut u64) -> c_int;
     pub(crate) fn pxg_pq_train_device(d_training: *const f32, n: u64, dim: u32, subspaces: u64,

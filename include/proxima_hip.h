@@ -271,6 +271,13 @@ int pxg_kmeans_assign(const float* points, uint64_t n, uint32_t dim, const float
  * be NULL. */
 int pxg_kmeans_last_stats(double* mfma_ms, double* mfma_flops, uint64_t* mfma_passes, uint64_t* rescanned,
                           uint64_t* inexact_sums);
+/* Empty-cluster reseeds (kmeans.rs:115-124) of the calling thread's last
+ * k-means run. No counterpart in the reference; it is for measurement and
+ * tests: the reseeds in all, those found in the candidate pool of the points
+ * with the largest distance bounds, and the iterations whose pool test
+ * failed (their reseeds went through the segment passes). Any pointer may be
+ * NULL. */
+int pxg_kmeans_last_reseeds(uint64_t* reseeds, uint64_t* pool_reseeds, uint64_t* pool_fallbacks);
 /* ProductQuantizer::train (product.rs:198-296): codebooks_out holds, per
  * subspace, 256 rows of its width (dim floats x 256 in total). */
 int pxg_pq_train(const float* training, uint64_t n, uint32_t dim, uint64_t subspaces, uint64_t max_iterations,

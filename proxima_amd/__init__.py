@@ -689,6 +689,14 @@ def kmeans_last_stats():
             "inexact_sums": inex.value}
 
 
+def kmeans_last_reseeds():
+    """Empty-cluster reseeds of this thread's last k-means run: in all, found
+    in the candidate pool, and iterations whose pool test failed."""
+    r, p, f = C.c_uint64(), C.c_uint64(), C.c_uint64()
+    _check(_lib.pxg_kmeans_last_reseeds(C.byref(r), C.byref(p), C.byref(f)))
+    return {"reseeds": r.value, "pool": p.value, "pool_fallbacks": f.value}
+
+
 def kmeans_pp(points, k, seed):
     p = np.ascontiguousarray(points, dtype=np.float32)
     n, dim = p.shape
@@ -766,7 +774,7 @@ class ProductQuantizer:
         return out
 
 
-__all__ += ["IvfPqConfig", "IvfPqIndex", "TrainingReport", "Clustering", "kmeans", "kmeans_device", "kmeans_lloyd", "kmeans_pp", "kmeans_last_stats",
+__all__ += ["IvfPqConfig", "IvfPqIndex", "TrainingReport", "Clustering", "kmeans", "kmeans_device", "kmeans_lloyd", "kmeans_pp", "kmeans_last_stats", "kmeans_last_reseeds",
             "kmeans_assign", "PqConfig", "ProductQuantizer"]
 
 

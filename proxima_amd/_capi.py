@@ -121,6 +121,7 @@ SIGNATURES = {
     "pxg_kmeans_device": (_i32, [_vp, _u64, _u32, _u64, _u64, _u64, _vp, _vp, _vp, _P(_f64), _P(_u64)]),
     "pxg_kmeans_pp": (_i32, [_vp, _u64, _u32, _u64, _u64, _vp]),
     "pxg_kmeans_last_stats": (_i32, [_P(_f64), _P(_f64), _P(_u64), _P(_u64), _P(_u64)]),
+    "pxg_kmeans_last_reseeds": (_i32, [_P(_u64), _P(_u64), _P(_u64)]),
     "pxg_kmeans_assign": (_i32, [_vp, _u64, _u32, _vp, _u64, _vp, _vp]),
     "pxg_pq_train": (_i32, [_vp, _u64, _u32, _u64, _u64, _u64, _vp, _P(_f64), _P(_u64)]),
     "pxg_pq_encode": (_i32, [_vp, _u32, _u64, _vp, _u64, _vp]),

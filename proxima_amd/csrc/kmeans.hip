@@ -52,6 +52,7 @@ thread_local size_t g_last_redo = 0;
 struct KmStats {
   double mfma_ms = 0.0, mfma_flops = 0.0;
   uint64_t passes = 0, rescanned = 0, inexact_sums = 0;
+  uint64_t reseeds = 0, pool_reseeds = 0, pool_fallbacks = 0;
 };
 thread_local KmStats g_km;
 constexpr size_t SEQ_SUM_LIMIT = 1u << 17;
@@ -1494,6 +1495,100 @@ static void launch_farthest(const float* dist, size_t n, unsigned long long* par
   hipLaunchKernelGGL(km_farthest_pick, dim3(1), dim3(256), 0, s, (const unsigned long long*)part, out);
 }
 
+// ---------------------------------------------------------------------------
+// Empty-cluster reseeds from a candidate pool
+// ---------------------------------------------------------------------------
+// At empty cluster E[i] the reference takes farthest_point over the array
+// holding the new means (and the victims so far) below E[i] and the old rows
+// from E[i] on (kmeans.rs:115-124). A point's own cluster w is not empty (the
+// point is in it), so that array's row w is its old centroid if w > E[i] and
+// its new mean if w < E[i], and the point's nearest distance there is at
+// most ub_i = d_old or squared(p, new_w) accordingly; a NaN distance
+// (overflow) counts as +inf, and a nearest distance is never NaN. Take as
+// the pool the points of the largest ub_i and let theta be the largest ub_i
+// outside it: every point outside has distance <= theta. So if the largest
+// exact distance over the pool is above theta, the farthest point (the
+// first index among equal distances) is in the pool, and is the pool's. Each
+// empty cluster then costs a sort of the bounds and an exact scan of the
+// pool instead of passes over every point; if the test fails at any empty
+// cluster, the segment passes redo them all.
+constexpr size_t RESEED_POOL = 8192;
+
+// squared(p, new_w) per point (NaN as +inf): the reference's sequential sum,
+// staged through LDS as in km_mfma_verify (rows 16-byte aligned, dim a
+// multiple of 4).
+__global__ __launch_bounds__(256) void km_reseed_bound(const float* __restrict__ P, int ldp, int n, int dim,
+                                                       const float* __restrict__ newc,
+                                                       const uint32_t* __restrict__ assign,
+                                                       float* __restrict__ dnew) {
+  __shared__ float tp[KV_PB * 33], tc[KV_PB * 33];
+  __shared__ uint32_t sc[KV_PB];
+  const int t = threadIdx.x, i0 = blockIdx.x * KV_PB, i = i0 + t;
+  if (t < KV_PB) sc[t] = i < n ? assign[i] : 0u;
+  float sum = 0.0f;
+  for (int j0 = 0; j0 < dim; j0 += 32) {
+    const int w = min(32, dim - j0);
+    __syncthreads();
+    for (int f = t; f < KV_PB * 8; f += 256) {
+      const int r = f >> 3, c4 = (f & 7) * 4;
+      if (c4 < w && i0 + r < n) {
+        const float4 x = *reinterpret_cast<const float4*>(P + (size_t)(i0 + r) * ldp + j0 + c4);
+        const float4 y = *reinterpret_cast<const float4*>(newc + (size_t)sc[r] * dim + j0 + c4);
+        float* dp = tp + r * 33 + c4;
+        float* dc = tc + r * 33 + c4;
+        dp[0] = x.x; dp[1] = x.y; dp[2] = x.z; dp[3] = x.w;
+        dc[0] = y.x; dc[1] = y.y; dc[2] = y.z; dc[3] = y.w;
+      }
+    }
+    __syncthreads();
+    if (t < KV_PB && i < n) {
+      const float* a = tp + t * 33;
+      const float* b = tc + t * 33;
+      for (int jj = 0; jj < w; ++jj) {
+        const float d = a[jj] - b[jj];
+        sum += d * d;  // squared(), kmeans.rs:234-241
+      }
+    }
+  }
+  if (t < KV_PB && i < n) dnew[i] = sum == sum ? sum : INFINITY;
+}
+
+// ub_i per point as a descending sort key (~ its bits; ub_i >= 0), with the
+// point's index as the value, for the empty cluster e.
+__global__ __launch_bounds__(256) void km_reseed_keys(const uint32_t* __restrict__ assign,
+                                                      const float* __restrict__ dold, const float* __restrict__ dnew,
+                                                      int n, uint32_t e, uint32_t* __restrict__ key,
+                                                      uint32_t* __restrict__ idx) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float ub = assign[i] > e ? dold[i] : dnew[i];
+  key[i] = ~__float_as_uint(ub + 0.0f);
+  idx[i] = (uint32_t)i;
+}
+
+// The pool's farthest point: the largest distance, then the smallest index
+// (the largest key, as in km_farthest_part). *fail is set unless that
+// distance is above theta = the largest ub outside the pool (theta_key holds
+// its sort key; none when the pool holds every point).
+__global__ __launch_bounds__(256) void km_pool_farthest(const uint32_t* __restrict__ rows,
+                                                        const float* __restrict__ d, int m,
+                                                        const uint32_t* __restrict__ theta_key, int force_fail,
+                                                        long long* __restrict__ out, int* __restrict__ fail) {
+  __shared__ unsigned long long sh[4];
+  unsigned long long best = 0;
+  for (int j = threadIdx.x; j < m; j += 256) {
+    const unsigned long long key =
+        ((unsigned long long)__float_as_uint(d[j] + 0.0f) << 32) | (0xFFFFFFFFu - rows[j]);
+    best = key > best ? key : best;
+  }
+  best = block_max_u64_256(best, sh);
+  if (threadIdx.x == 0) {
+    *out = (long long)(0xFFFFFFFFu - (uint32_t)best);
+    const float dmax = __uint_as_float((uint32_t)(best >> 32));
+    if (force_fail || (theta_key && !(dmax > __uint_as_float(~*theta_key)))) *fail = 1;
+  }
+}
+
 // Optional phase timings on stderr (PXG_TRAIN_VERBOSE=1), for tuning.
 static bool train_verbose() {
   static const bool v = [] {
@@ -1530,8 +1625,22 @@ KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req
 
   DevBuf<uint32_t> assign(n), prev(n), counts(k), offsets(k), idx(n), keys_sorted(n), members(n);
   DevBuf<float> dist(n), newc(k * dim), work(k * dim);
-  DevBuf<int> changed(1);
+  DevBuf<int> changed(1), pool_fail(1);
   DevBuf<long long> far(1);
+  // the reseed pool's bounds, their sorted order, and the pool's exact scan
+  DevBuf<uint32_t> rs_key, rs_skey, rs_idx, rs_rows, pool_a;
+  DevBuf<float> rs_dnew, pool_d;
+  size_t pool_reseeds = 0, pool_fallbacks = 0;
+  // PXG_RESEED_POOL=size sets the pool size (0: no pool), so that small
+  // inputs can take the pool path; PXG_RESEED_FAIL_AT=i fails the pool's test
+  // at empty cluster i, so that the fallback runs after victims were placed
+  // (test hooks; the results are the same either way)
+  size_t pool = RESEED_POOL;
+  if (const char* e = std::getenv("PXG_RESEED_POOL")) pool = (size_t)std::strtoull(e, nullptr, 10);
+  const char* fail_env = std::getenv("PXG_RESEED_FAIL_AT");
+  const long long fail_at = fail_env ? std::atoll(fail_env) : -1;
+  const bool pool_fits = pool > 0 && n > 4 * pool && dim % 4 == 0 && dim <= KW_DMAX && ldp % 4 == 0 &&
+                         ((uintptr_t)P & 15) == 0;
   DevBuf<unsigned long long> far_part(KF_BLOCKS);
   NearestWork nw;  // the points do not change during the run
   PXG_HIP(hipMemsetAsync(prev.p, 0, n * 4, s));
@@ -1593,7 +1702,47 @@ KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req
     for (size_t c = 0; c < k; ++c)
       if (h_counts[c] == 0) E.push_back(c);
     const size_t m = E.size();
-    if (m >= 2 && m * n <= ((size_t)1 << 29)) {
+    if (m >= 1 && pool_fits) {
+      rs_key.reserve(n);
+      rs_skey.reserve(n);
+      rs_idx.reserve(n);
+      rs_rows.reserve(n);
+      rs_dnew.reserve(n);
+      pool_a.reserve(pool);
+      pool_d.reserve(pool);
+      hipLaunchKernelGGL(km_reseed_bound, dim3((unsigned)((n + KV_PB - 1) / KV_PB)), dim3(256), 0, s, P, ldp, (int)n,
+                         dim, (const float*)newc.p, (const uint32_t*)assign.p, rs_dnew.p);
+      PXG_HIP(hipMemsetAsync(pool_fail.p, 0, 4, s));
+      for (size_t ii = 0; ii < m; ++ii) {
+        const size_t c = E[ii];
+        hipLaunchKernelGGL(km_reseed_keys, gn, dim3(256), 0, s, (const uint32_t*)assign.p, (const float*)dist.p,
+                           (const float*)rs_dnew.p, (int)n, (uint32_t)c, rs_key.p, rs_idx.p);
+        PXG_HIP(hipcub::DeviceRadixSort::SortPairs(tmp.p, tmp_bytes, rs_key.p, rs_skey.p, rs_idx.p, rs_rows.p, (int)n,
+                                                   0, 32, s));
+        PXG_HIP(hipMemcpyAsync(work.p, newc.p, c * dim * 4, hipMemcpyDeviceToDevice, s));
+        PXG_HIP(hipMemcpyAsync(work.p + c * dim, cents.p + c * dim, (k - c) * dim * 4, hipMemcpyDeviceToDevice, s));
+        hipLaunchKernelGGL(km_exact_multi<false>, dim3((unsigned)((pool + KX_PB - 1) / KX_PB)), dim3(256),
+                           (size_t)KX_PB * dim * 4, s, P, ldp, (const uint32_t*)rs_rows.p, (int)pool, dim,
+                           (const float*)work.p, dim, (int)k, pool_a.p, pool_d.p);
+        hipLaunchKernelGGL(km_pool_farthest, dim3(1), dim3(256), 0, s, (const uint32_t*)rs_rows.p,
+                           (const float*)pool_d.p, (int)pool, (const uint32_t*)(rs_skey.p + pool),
+                           (int)((long long)ii == fail_at), far.p, pool_fail.p);
+        hipLaunchKernelGGL(copy_row_at, dim3(1), dim3(256), 0, s, P, ldp, (const long long*)far.p, dim,
+                           newc.p + c * dim);
+        PXG_HIP(hipGetLastError());
+      }
+      int h_fail = 0;
+      PXG_HIP(hipMemcpyAsync(&h_fail, pool_fail.p, 4, hipMemcpyDeviceToHost, s));
+      PXG_HIP(hipStreamSynchronize(s));
+      if (h_fail) {
+        ++pool_fallbacks;  // the passes below redo every empty cluster, victims included
+      } else {
+        empties += m;
+        pool_reseeds += m;
+        E.clear();
+      }
+    }
+    if (E.size() >= 2 && m * n <= ((size_t)1 << 29)) {
       // Several empty clusters: the nearest distance of a point against the
       // array seen at empty cluster E[i] is min(L_i, R_i), L_i over the rows
       // below E[i] (new means and the victims chosen so far), R_i over the
@@ -1653,11 +1802,16 @@ KmeansOut kmeans_device(const float* P, size_t n, int dim, int ldp, size_t k_req
   }
   PXG_HIP(hipStreamSynchronize(s));
   g_km.inexact_sums = out.inexact_sums;
+  g_km.reseeds = empties;
+  g_km.pool_reseeds = pool_reseeds;
+  g_km.pool_fallbacks = pool_fallbacks;
   if (train_verbose())
     std::fprintf(stderr,
-                 "[pxg kmeans] n=%zu dim=%d k=%zu: seeding %.3fs, lloyd %zu it %.3fs, %zu empty reseeds, %zu points "
-                 "rescanned exactly in the last assignment; empties per iteration:%s\n",
-                 n, dim, k, t_seeded - t_start, out.iterations, now_s() - t_seeded, empties, g_last_redo,
+                 "[pxg kmeans] n=%zu dim=%d k=%zu: seeding %.3fs, lloyd %zu it %.3fs, %zu empty reseeds (%zu from the "
+                 "pool, %zu pool fallbacks), %zu points rescanned exactly in the last assignment; empties per "
+                 "iteration:%s\n",
+                 n, dim, k, t_seeded - t_start, out.iterations, now_s() - t_seeded, empties, pool_reseeds,
+                 pool_fallbacks, g_last_redo,
                  empties_per_it.c_str());
   return out;
 }
@@ -1933,6 +2087,14 @@ int pxg_kmeans_last_stats(double* mfma_ms, double* mfma_flops, uint64_t* mfma_pa
     if (mfma_passes) *mfma_passes = pxg::g_km.passes;
     if (rescanned) *rescanned = pxg::g_km.rescanned;
     if (inexact_sums) *inexact_sums = pxg::g_km.inexact_sums;
+  });
+}
+
+int pxg_kmeans_last_reseeds(uint64_t* reseeds, uint64_t* pool_reseeds, uint64_t* pool_fallbacks) {
+  return pxg::guard([&] {
+    if (reseeds) *reseeds = pxg::g_km.reseeds;
+    if (pool_reseeds) *pool_reseeds = pxg::g_km.pool_reseeds;
+    if (pool_fallbacks) *pool_fallbacks = pxg::g_km.pool_fallbacks;
   });
 }
 

@@ -44,46 +44,80 @@ def test_kmeans_bit_exact_vs_oracle(gpu, n, dim, k, iters, seed):
     assert got.inertia == want_in
 
 
-def test_lloyd_from_init_with_empty_clusters(gpu):
+# How the empty-cluster reseeds of a run are searched: the segment passes
+# (inputs below four pool sizes), the candidate pool (a small pool size set
+# for these inputs), or the pool with its test failed at the second empty
+# cluster of an iteration (victims already placed), so that the segment passes
+# redo them all. Each must give the reference's results.
+RESEED_PATHS = ["segments", "pool", "pool_fallback"]
+
+
+def reseed_path(monkeypatch, path, pool):
+    if path != "segments":
+        monkeypatch.setenv("PXG_RESEED_POOL", str(pool))
+    if path == "pool_fallback":
+        monkeypatch.setenv("PXG_RESEED_FAIL_AT", "1")
+
+
+def check_reseed_path(px, path, several):
+    st = px.kmeans_last_reseeds()
+    assert st["reseeds"] > 0
+    if path == "segments":
+        assert st["pool"] == 0 and st["pool_fallbacks"] == 0
+    elif path == "pool" or not several:
+        assert st["pool"] == st["reseeds"] and st["pool_fallbacks"] == 0
+    else:
+        assert st["pool_fallbacks"] >= 1
+
+
+@pytest.mark.parametrize("path", RESEED_PATHS)
+def test_lloyd_from_init_with_empty_clusters(gpu, monkeypatch, path):
     px = gpu
+    reseed_path(monkeypatch, path, 900)
     rng = np.random.default_rng(5)
     pts = clustered(rng, 4000, 16, 8, 0.3)
     init = pts[:12].copy()
     init[3] += 1000.0  # attracts nothing -> farthest-point reseed
     init[7] -= 1000.0
     got = px.kmeans_lloyd(pts, init, 20)
+    check_reseed_path(px, path, True)
     want = orc.kmeans_lloyd(pts, init, 20)
     assert np.array_equal(bits(got[0]), bits(want[0]))
     assert np.array_equal(got[1], want[1])
     assert got[2] == want[2] and got[3] == want[3]
 
 
-def test_lloyd_several_empty_clusters_in_one_iteration(gpu):
+@pytest.mark.parametrize("path", RESEED_PATHS)
+def test_lloyd_several_empty_clusters_in_one_iteration(gpu, monkeypatch, path):
     """Five centroids that attract nothing, spread over 512: the reseeds of
     one iteration go through the segmented farthest-point search (exact
-    segment minima over old and new rows, MFMA-sized segments) and must
-    pick the reference's points in order."""
+    segment minima over old and new rows, MFMA-sized segments) or the pool
+    and must pick the reference's points in order."""
     px = gpu
+    reseed_path(monkeypatch, path, 2000)
     rng = np.random.default_rng(15)
     pts = clustered(rng, 9000, 32, 300, 0.4)
     init = pts[rng.choice(9000, 512, replace=False)].copy()
     for c, off in ((40, 900.0), (170, -800.0), (171, 700.0), (333, 650.0), (500, -950.0)):
         init[c] += np.float32(off)
     got = px.kmeans_lloyd(pts, init, 6)
+    check_reseed_path(px, path, True)
     want = orc.kmeans_lloyd(pts, init, 6)
     assert np.array_equal(bits(got[0]), bits(want[0]))
     assert np.array_equal(got[1], want[1])
     assert got[2] == want[2] and got[3] == want[3]
 
 
+@pytest.mark.parametrize("path", RESEED_PATHS)
 @pytest.mark.parametrize("empties", [(7,), (7, 60)])
-def test_farthest_point_ties_take_the_first_index(gpu, empties):
+def test_farthest_point_ties_take_the_first_index(gpu, monkeypatch, empties, path):
     """Two distinct outliers, m - 20 e0 (index 1000) and m + 20 e0 (index
     4000), are the farthest points at exactly equal distance 400 from their
     centroid m, whose 8-point group keeps the mean m exactly: the reseed takes
     index 1000 (strict > from -1.0), through the one-empty and the segmented
-    several-empty searches."""
+    several-empty searches, and through the pool."""
     px = gpu
+    reseed_path(monkeypatch, path, 1400)
     rng = np.random.default_rng(21)
     dim = 32
     pts = clustered(rng, 6000, dim, 40, 0.3)
@@ -103,6 +137,7 @@ def test_farthest_point_ties_take_the_first_index(gpu, empties):
     for c in empties:
         init[c] += np.float32(5000.0)  # attracts nothing
     got = px.kmeans_lloyd(pts, init, 3)
+    check_reseed_path(px, path, len(empties) > 1)
     want = orc.kmeans_lloyd(pts, init, 3)
     assert np.array_equal(bits(got[0]), bits(want[0]))
     assert np.array_equal(got[1], want[1])
