@@ -36,6 +36,7 @@
 #include <string>
 #include <thread>
 #include <exception>
+#include <type_traits>
 #include <vector>
 
 #include "common.hpp"
@@ -434,6 +435,105 @@ __global__ __launch_bounds__(256, 2) void km_mfma_top(const float* __restrict__ 
   }
 }
 
+// km_mfma_small: the same certified approximation for narrow rows (dim 8,
+// 16 or 24: product-quantizer subspaces), with the centroids (k * dim <=
+// KS_MAXF floats) and their norms staged in LDS once per workgroup. One wave
+// takes 32 points at a time. With the centroids as the MFMA's A operand and
+// the points as B, lane (h, r) ends each 32-centroid block holding point r's
+// values for centroids 8 (v / 4) + 4 h + v % 4 of the block (v < 16), so the
+// running top-2 stays in registers, as in km_mfma_top's scan (one fma, one
+// compare and select, one med3, one min per value, the index as the value's
+// position v with the block recorded once per block); the two half-waves
+// merge at the end. Lane half h supplies dims [h dim/2, (h+1) dim/2) of both
+// operands over the dim/2 MFMA steps: any order of the dot product's terms
+// that both operands share is a valid one, and this one makes every operand
+// load a float4. Rows 16-byte aligned.
+constexpr int KS_MAXF = 8192;  // centroid floats staged in LDS (32 KB)
+constexpr int KS_PW = 4;       // 32-point groups per wave
+template <int DS>  // dim = 8 DS
+__global__ __launch_bounds__(256, 2) void km_mfma_small(const float* __restrict__ P, int ldp,
+                                                     const uint32_t* __restrict__ rows, int n,
+                                                     const float* __restrict__ C, int ldc, int k,
+                                                     const float* __restrict__ cn, uint32_t* __restrict__ best_idx,
+                                                     float* __restrict__ best, float* __restrict__ second) {
+  constexpr int D = 8 * DS, HD = D / 2;
+  extern __shared__ float4 ks_sm[];
+  float* sc = reinterpret_cast<float*>(ks_sm);  // [k][D]
+  float* scn = sc + k * D;                      // [k rounded up to 32]
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, r = lane & 31;
+  for (int f = tid; f < k * 2 * DS; f += 256) {
+    const int row = f / (2 * DS), c4 = (f - row * 2 * DS) * 4;
+    *reinterpret_cast<float4*>(&sc[row * D + c4]) = *reinterpret_cast<const float4*>(C + (size_t)row * ldc + c4);
+  }
+  const int kr = (k + 31) & ~31;
+  for (int i = tid; i < kr; i += 256) scn[i] = i < k ? cn[i] : 0.0f;
+  __syncthreads();
+  const int nblk = kr / 32;
+  for (int g = 0; g < KS_PW; ++g) {
+    const int p0 = ((blockIdx.x * 4 + w) * KS_PW + g) * 32;
+    if (p0 >= n) break;  // wave-uniform
+    const int pi = min(p0 + r, n - 1);
+    const float* prow = P + (size_t)(rows ? rows[pi] : (uint32_t)pi) * ldp + h * HD;
+    float bq[HD];
+#pragma unroll
+    for (int q = 0; q < HD / 4; ++q) {
+      const float4 x = *reinterpret_cast<const float4*>(prow + 4 * q);
+      bq[4 * q] = x.x;
+      bq[4 * q + 1] = x.y;
+      bq[4 * q + 2] = x.z;
+      bq[4 * q + 3] = x.w;
+    }
+    float b1 = INFINITY, b2 = INFINITY;
+    int i1 = 0, t1 = 0;
+    auto take = [&](float x, int v) {
+      i1 = x < b1 ? v : i1;
+      b2 = __builtin_amdgcn_fmed3f(b1, b2, x);
+      b1 = fminf(b1, x);
+    };
+    // one 32-centroid block; PART masks the centroids past k (last block)
+    auto block = [&](int blk, auto part) __attribute__((always_inline)) {
+      const float* ca = &sc[min(blk * 32 + r, k - 1) * D + h * HD];
+      f16v acc;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+#pragma unroll
+      for (int q = 0; q < HD / 4; ++q) {
+        const float4 a = *reinterpret_cast<const float4*>(ca + 4 * q);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, bq[4 * q], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, bq[4 * q + 1], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, bq[4 * q + 2], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, bq[4 * q + 3], acc, 0, 0, 0);
+      }
+      const float b1_in = b1;
+#pragma unroll
+      for (int vb = 0; vb < 4; ++vb) {
+        const float4 c4 = *reinterpret_cast<const float4*>(&scn[blk * 32 + 8 * vb + 4 * h]);
+        const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float x = __builtin_fmaf(-2.0f, acc[4 * vb + e], cv[e]);
+          if constexpr (decltype(part)::value) x = blk * 32 + 8 * vb + 4 * h + e < k ? x : INFINITY;
+          take(x, 4 * vb + e);
+        }
+      }
+      t1 = b1 < b1_in ? blk : t1;
+    };
+    const int nfull = k / 32;
+    for (int blk = 0; blk < nfull; ++blk) block(blk, std::false_type{});
+    if (nfull < nblk) block(nfull, std::true_type{});
+    int ix = t1 * 32 + 8 * (i1 >> 2) + 4 * h + (i1 & 3);
+    // merge the two halves of the wave (lanes r and r + 32 hold point r)
+    const float y1 = __shfl_xor(b1, 32, WAVE), y2 = __shfl_xor(b2, 32, WAVE);
+    const int yi = __shfl_xor(ix, 32, WAVE);
+    if (h == 0 && p0 + r < n) {
+      const bool tk = y1 < b1 || (y1 == b1 && yi < ix);
+      best[p0 + r] = tk ? y1 : b1;
+      best_idx[p0 + r] = (uint32_t)(tk ? yi : ix);
+      second[p0 + r] = fminf(tk ? b1 : y1, fminf(b2, y2));
+    }
+  }
+}
+
 constexpr int KV_PB = 128;  // points per km_mfma_verify block (256 threads)
 template <bool UNR>
 __global__ __launch_bounds__(256) void km_mfma_verify(const float* __restrict__ P, int ldp,
@@ -666,7 +766,9 @@ void nearest_device(const float* P, int ldp, const uint32_t* rows, size_t n, int
   if (n == 0) return;
   const bool aligned = ldp % 4 == 0 && ldc % 4 == 0 && dim % 4 == 0 && ((uintptr_t)P & 15) == 0 &&
                        ((uintptr_t)C & 15) == 0;
-  if (!(aligned && dim >= 32 && dim <= KW_DMAX && k >= 64 && n >= 4096)) {
+  // narrow rows (product-quantizer subspaces) with their centroids in LDS
+  const bool small = aligned && (dim == 8 || dim == 16 || dim == 24) && k >= 64 && k * dim <= KS_MAXF && n >= 4096;
+  if (!small && !(aligned && dim >= 32 && dim <= KW_DMAX && k >= 64 && n >= 4096)) {
     if (unrolled)
       launch_assign<true>(P, ldp, rows, n, dim, C, ldc, k, assign, dist, s);
     else
@@ -699,13 +801,27 @@ void nearest_device(const float* P, int ldp, const uint32_t* rows, size_t n, int
   hipLaunchKernelGGL(km_row_norms, dim3((unsigned)((k + 31) / 32)), dim3(256), 0, s, C, ldc,
                      (const uint32_t*)nullptr, (int)k, dim, cn);
   hipLaunchKernelGGL(km_max_of, dim3(1), dim3(1024), 0, s, cn, (int)k, cmax);
-  hipEvent_t e0, e1;
-  PXG_HIP(hipEventCreate(&e0));
-  PXG_HIP(hipEventCreate(&e1));
-  PXG_HIP(hipEventRecord(e0, s));
-  hipLaunchKernelGGL(km_mfma_top, dim3((unsigned)((n + KA_M - 1) / KA_M)), dim3(256), 0, s, P, ldp, rows, (int)n,
-                     dim, C, ldc, (int)k, (const float*)cn, bidx, best, second);
-  PXG_HIP(hipEventRecord(e1, s));
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (small) {
+    const dim3 gs((unsigned)((n + 4 * KS_PW * 32 - 1) / (4 * KS_PW * 32)));
+    const size_t lds = (k * dim + ((k + 31) & ~(size_t)31)) * 4;
+    if (dim == 8)
+      hipLaunchKernelGGL(km_mfma_small<1>, gs, dim3(256), lds, s, P, ldp, rows, (int)n, C, ldc, (int)k,
+                         (const float*)cn, bidx, best, second);
+    else if (dim == 16)
+      hipLaunchKernelGGL(km_mfma_small<2>, gs, dim3(256), lds, s, P, ldp, rows, (int)n, C, ldc, (int)k,
+                         (const float*)cn, bidx, best, second);
+    else
+      hipLaunchKernelGGL(km_mfma_small<3>, gs, dim3(256), lds, s, P, ldp, rows, (int)n, C, ldc, (int)k,
+                         (const float*)cn, bidx, best, second);
+  } else {
+    PXG_HIP(hipEventCreate(&e0));
+    PXG_HIP(hipEventCreate(&e1));
+    PXG_HIP(hipEventRecord(e0, s));
+    hipLaunchKernelGGL(km_mfma_top, dim3((unsigned)((n + KA_M - 1) / KA_M)), dim3(256), 0, s, P, ldp, rows, (int)n,
+                       dim, C, ldc, (int)k, (const float*)cn, bidx, best, second);
+    PXG_HIP(hipEventRecord(e1, s));
+  }
   PXG_HIP(hipMemsetAsync(nredo, 0, 4, s));
   const dim3 g((unsigned)((n + KV_PB - 1) / KV_PB));
   if (unrolled)
@@ -720,13 +836,15 @@ void nearest_device(const float* P, int ldp, const uint32_t* rows, size_t n, int
   int m = 0;
   PXG_HIP(hipMemcpyAsync(&m, nredo, 4, hipMemcpyDeviceToHost, s));
   PXG_HIP(hipStreamSynchronize(s));
-  float ms = 0.0f;
-  PXG_HIP(hipEventElapsedTime(&ms, e0, e1));
-  PXG_HIP(hipEventDestroy(e0));
-  PXG_HIP(hipEventDestroy(e1));
-  g_km.mfma_ms += ms;
-  g_km.mfma_flops += 2.0 * (double)n * (double)k * (double)dim;
-  g_km.passes += 1;
+  if (!small) {  // the counters cover km_mfma_top
+    float ms = 0.0f;
+    PXG_HIP(hipEventElapsedTime(&ms, e0, e1));
+    PXG_HIP(hipEventDestroy(e0));
+    PXG_HIP(hipEventDestroy(e1));
+    g_km.mfma_ms += ms;
+    g_km.mfma_flops += 2.0 * (double)n * (double)k * (double)dim;
+    g_km.passes += 1;
+  }
   g_km.rescanned += (uint64_t)m;
   g_last_redo = (size_t)m;
   if (m == 0) return;

@@ -206,10 +206,11 @@ def test_assign_matrix_core_path_matches_oracle(gpu):
     """Enough points and centroids for the MFMA pass: approximate winners are
     certified against the runner-up and rescored exactly; duplicated
     centroids (exact ties, lower index wins), points equidistant from two
-    centroids and rows whose norms overflow take the exact scan."""
+    centroids and rows whose norms overflow take the exact scan. Widths 8, 16
+    and 24 take the narrow-row kernel (centroids in LDS, top-2 per lane)."""
     px = gpu
     rng = np.random.default_rng(9)
-    for dim in (32, 96, 128):
+    for dim in (8, 16, 24, 32, 96, 128):
         p = clustered(rng, 9000, dim, 40, 0.3)
         c = p[rng.choice(9000, 300, replace=False)] + rng.standard_normal((300, dim)).astype(np.float32) * 0.05
         c[5] = c[9]
@@ -223,8 +224,9 @@ def test_assign_matrix_core_path_matches_oracle(gpu):
         assert np.array_equal(bits(d), bits(wd)), dim
 
 
+@pytest.mark.parametrize("dim", [64, 8])
 @pytest.mark.parametrize("case", ["centroid_nan", "centroid_inf", "centroid_norm_overflow", "points"])
-def test_assign_matrix_core_nonfinite(gpu, case):
+def test_assign_matrix_core_nonfinite(gpu, case, dim):
     """Non-finite values on the MFMA path: a NaN or infinite centroid
     coordinate, or a centroid whose squared norm overflows, makes every
     point's bound non-finite (all take the exact scan); NaN and infinite
@@ -232,8 +234,8 @@ def test_assign_matrix_core_nonfinite(gpu, case):
     distances are the reference's (a NaN distance never wins: strict <)."""
     px = gpu
     rng = np.random.default_rng(21)
-    p = clustered(rng, 6000, 64, 30, 0.3)
-    c = p[rng.choice(6000, 200, replace=False)] + rng.standard_normal((200, 64)).astype(np.float32) * 0.05
+    p = clustered(rng, 6000, dim, 30, 0.3)
+    c = p[rng.choice(6000, 200, replace=False)] + rng.standard_normal((200, dim)).astype(np.float32) * 0.05
     if case == "centroid_nan":
         c[7, 3] = np.nan
     elif case == "centroid_inf":
@@ -244,7 +246,7 @@ def test_assign_matrix_core_nonfinite(gpu, case):
         p[10, 5] = np.nan
         p[11, 0] = np.inf
         p[12, :] = -np.inf
-        p[13, 63] = np.float32(-3e38)
+        p[13, dim - 1] = np.float32(-3e38)
     a, d = px.kmeans_assign(p, c)
     wa, wd = orc.kmeans_assign(p, c)
     assert np.array_equal(a, wa), case
@@ -281,7 +283,10 @@ def _lcg_clustered(dim, count, seed):  # product.rs:635-654
     return out
 
 
-@pytest.mark.parametrize("dim,m,count,seed", [(32, 8, 512, 3), (10, 4, 300, 2), (8, 2, 3, 6), (64, 16, 400, 1)])
+# the last two train 8- and 24-wide subspaces on enough vectors for the
+# narrow-row matrix-core assignment
+@pytest.mark.parametrize("dim,m,count,seed", [(32, 8, 512, 3), (10, 4, 300, 2), (8, 2, 3, 6), (64, 16, 400, 1),
+                                              (16, 2, 6000, 4), (48, 2, 5000, 5)])
 def test_pq_train_and_encode_bit_exact(gpu, dim, m, count, seed):
     px = gpu
     t = _lcg_clustered(dim, count, seed)
