@@ -295,6 +295,8 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
 
     // Epilogue: approximate score, threshold filter, append. Lane (h, r)
     // holds rows wm + 32i + 8vb + 4h + e (e < 4) of slots n0 + wn + 32j + r.
+    // The score (qb + xb) - scale * dot is one fma: scale is 2 or 1, so the
+    // product is exact and the fma rounds once, as the subtraction would.
     // A branch-free pass marks the values a with !(a > thr_f[row]), reading
     // four rows' norms and thresholds per LDS read. That test passes every
     // key below thr[row] (key_float inverts ord_key; NaN and the sign of zero
@@ -328,7 +330,7 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
           for (int e = 0; e < 4; ++e) {
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-              const float a = (sqv[e] + xbj[j]) - scale * acc[i][j][vb * 4 + e];
+              const float a = __builtin_fmaf(-scale, acc[i][j][vb * 4 + e], sqv[e] + xbj[j]);
               pass[i] |= !(a > tfv[e]) ? 1u << (j * 16 + vb * 4 + e) : 0u;
             }
           }
@@ -345,7 +347,7 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
             for (int v = 0; v < 16; ++v) {
               if (pass[i] & (1u << (j * 16 + v))) {
                 const int row = wm + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-                const float a = (sqb[row] + xbj[j]) - scale * acc[i][j][v];
+                const float a = __builtin_fmaf(-scale, acc[i][j][v], sqb[row] + xbj[j]);
                 const uint64_t key = ((uint64_t)ord_key(a) << 32) | (uint32_t)slotj[j];
                 if (key < thr[row]) {
                   const int pos = atomicAdd(&cnt[row], 1);
