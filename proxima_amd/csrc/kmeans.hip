@@ -1238,15 +1238,29 @@ __global__ __launch_bounds__(256) void km_pp_round_q8(const float* __restrict__ 
   }
 }
 
+// Inclusive prefix sum over a wave (shuffles, no LDS).
+__device__ inline double wave_incl_scan_f64(double v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const double u = __shfl_up(v, o, 64);
+    if (lane >= o) v += u;
+  }
+  return v;
+}
+
 // One 1024-thread block: the pick of one round and the copy of its row.
 // status: 0 ok, 1 non-finite total (the round and all later ones stop).
+// The prefix sums are wave scans joined through the 16 (or 4) wave totals:
+// under the certificate every order gives the exact sums, and otherwise this
+// is the fixed parallel order.
 __global__ __launch_bounds__(1024) void km_pp_pick(const float* __restrict__ P, int ldp, int n, int dim,
                                                    const float* __restrict__ ns, const double* __restrict__ ps,
                                                    const int* __restrict__ pe, int nb, ChaCha8* __restrict__ grng,
                                                    float* __restrict__ row_out, int* __restrict__ status,
                                                    int* __restrict__ inexact, int* __restrict__ picked_out) {
-  __shared__ double ex[1024];
-  __shared__ int se[1024];
+  __shared__ double wtot[16];
+  __shared__ int wemin[16];
+  __shared__ double s_pre;
   __shared__ float stage[4096];
   __shared__ __align__(8) unsigned char rng_mem[sizeof(ChaCha8)];
   ChaCha8& rng = *reinterpret_cast<ChaCha8*>(rng_mem);
@@ -1264,21 +1278,25 @@ __global__ __launch_bounds__(1024) void km_pp_pick(const float* __restrict__ P, 
     ls += ps[b];
     le = min(le, pe[b]);
   }
-  // inclusive scan over the threads in a fixed order (Hillis-Steele)
-  ex[t] = ls;
-  se[t] = le;
+  // inclusive scan over the threads: wave scans, then the earlier waves'
+  // totals in wave order
+  const int lane = t & 63, wv = t >> 6;
+  double incl = wave_incl_scan_f64(ls, lane);
+  int wm = le;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) wm = min(wm, __shfl_xor(wm, o, 64));
+  if (lane == 63) wtot[wv] = incl;
+  if (lane == 0) wemin[wv] = wm;
   __syncthreads();
-  for (int o = 1; o < 1024; o <<= 1) {
-    const double add = t >= o ? ex[t - o] : 0.0;
-    const int me = t >= o ? se[t - o] : NO_TERMS;
-    __syncthreads();
-    ex[t] += add;
-    se[t] = min(se[t], me);
-    __syncthreads();
+  double total = 0.0, wpre = 0.0;
+  int emin = NO_TERMS;
+  for (int q = 0; q < 16; ++q) {
+    if (q == wv) wpre = total;
+    total += wtot[q];
+    emin = min(emin, wemin[q]);
   }
-  double total = ex[1023];
-  const int emin = se[1023];
-  const double before = ex[t] - ls;  // exact when the certificate holds
+  incl += wpre;
+  const double before = incl - ls;  // exact when the certificate holds
   // distances are >= 0, so the sum of |x| is the total itself
   const bool exact = sums_exact(total, emin);
   const bool sequential = !exact && n <= (int)SEQ_SUM_LIMIT;
@@ -1336,25 +1354,22 @@ __global__ __launch_bounds__(1024) void km_pp_pick(const float* __restrict__ P, 
     const int bb = s_block;
     if (bb < nb) {
       // prefix before block bb: recomputed by the owning thread's run
-      __syncthreads();
       if (b0 <= bb && bb < b1) {
         double pre = before;
         for (int b = b0; b < bb; ++b) pre += ps[b];
-        ex[0] = pre;  // ex is free after the scan
+        s_pre = pre;
       }
-      __syncthreads();
-      const double pre = ex[0];
-      __syncthreads();
+      // the block's PP_ROWS points (the first PP_ROWS / 64 waves): wave
+      // scans, then the earlier waves' totals; wtot is free after the scan
+      // above (every thread read it before s_block was settled)
+      static_assert(PP_ROWS % 64 == 0 && PP_ROWS <= 1024, "whole waves of points");
       const int i = bb * PP_ROWS + t;
-      ex[t] = (t < PP_ROWS && i < n) ? (double)ns[i] : 0.0;
+      double inc2 = wave_incl_scan_f64((t < PP_ROWS && i < n) ? (double)ns[i] : 0.0, lane);
+      if (lane == 63 && t < PP_ROWS) wtot[wv] = inc2;
       __syncthreads();
-      for (int o = 1; o < PP_ROWS; o <<= 1) {
-        const double add = (t < PP_ROWS && t >= o) ? ex[t - o] : 0.0;
-        __syncthreads();
-        if (t < PP_ROWS) ex[t] += add;
-        __syncthreads();
-      }
-      if (t < PP_ROWS && i < n && pre + ex[t] >= target) atomicMin(&s_pick, i);
+      const double pre = s_pre;
+      for (int q = 0; q < wv && t < PP_ROWS; ++q) inc2 += wtot[q];
+      if (t < PP_ROWS && i < n && pre + inc2 >= target) atomicMin(&s_pick, i);
     }
   }
   __syncthreads();
