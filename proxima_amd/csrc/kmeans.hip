@@ -1162,13 +1162,40 @@ __global__ __launch_bounds__(256) void km_q8_prep(const float* __restrict__ P, i
   }
 }
 
+// Lower bounds on the distances from the chosen centres 0 .. chosen-1 to
+// centre `chosen` (all rows of the points): f64 sums of the f32 coordinates'
+// squared differences, four lanes per centre, rounded down to f32 after a
+// relative margin far above the f64 rounding.
+__global__ __launch_bounds__(256) void km_pp_cdist(const float* __restrict__ cents, int dim, int chosen,
+                                                   float* __restrict__ dcc) {
+  const int j = blockIdx.x * 64 + (threadIdx.x >> 2), part = threadIdx.x & 3;
+  const bool on = j < chosen;
+  const float* a = cents + (size_t)(on ? j : 0) * dim;
+  const float* b = cents + (size_t)chosen * dim;
+  double d = 0.0;
+  for (int u = part; u < dim; u += 4) {
+    const double x = (double)a[u] - (double)b[u];
+    d += x * x;
+  }
+  d += __shfl_xor(d, 1, 64);
+  d += __shfl_xor(d, 2, 64);
+  if (on && part == 0) dcc[j] = __double2float_rd(sqrt(d) * (1.0 - 1e-12));
+}
+
+// near[i] is the chosen centre whose distance ns[i] holds. Before the
+// int8 test, a point whose nearest centre a lies far from the new centre c
+// keeps its distance without reading its codes: |p - c| >= |a - c| - |p - a|,
+// with |p - a|^2 <= (ns + 1e-35) / (1 - gamma) from ns being the reference's
+// sequential sum for a, and dcc[a] a lower bound on |a - c|; the same
+// L^2 (1 - gamma) >= ns + 1e-35 test as the int8 bound then follows.
 __global__ __launch_bounds__(256) void km_pp_round_q8(const float* __restrict__ P, int ldp, int n, int dim,
                                                       const int8_t* __restrict__ Q, int kq,
                                                       const float* __restrict__ scale,
                                                       const float* __restrict__ delta, const int* __restrict__ qnorm,
                                                       const int* __restrict__ picked, float* __restrict__ ns,
                                                       double* __restrict__ ps, int* __restrict__ pe,
-                                                      double gamma) {
+                                                      double gamma, uint32_t* __restrict__ near,
+                                                      const float* __restrict__ dcc, int chosen) {
   __shared__ int qc[KW_DMAX / 4];
   __shared__ float cs[KW_DMAX];
   __shared__ int list[Q8_ROWS];
@@ -1185,8 +1212,14 @@ __global__ __launch_bounds__(256) void km_pp_round_q8(const float* __restrict__ 
   const int i = blockIdx.x * Q8_ROWS + t;
   float cur = 0.0f;
   bool exact = false;
+  bool far = false;
   if (i < n) {
     cur = ns[i];
+    const double r = sqrt(((double)cur + 1e-35) / (1.0 - gamma)) * (1.0 + 1e-12);
+    const double L0 = (double)dcc[near[i]] - r;
+    far = isfinite(cur) && L0 > 0.0 && L0 * L0 * (1.0 - gamma) >= (double)cur + 1e-35;
+  }
+  if (i < n && !far) {
     int dot = 0;  // exact in any order: |dot| < 2^31 for kq <= KW_DMAX
     if ((kq & 15) == 0) {
       // 16-byte loads: the row's bytes in kq/16 loads instead of kq/4
@@ -1230,7 +1263,10 @@ __global__ __launch_bounds__(256) void km_pp_round_q8(const float* __restrict__ 
   }
   __syncthreads();
   const float nv = i < n ? nv_s[t] : 0.0f;
-  if (i < n && nv != cur) ns[i] = nv;
+  if (i < n && nv != cur) {
+    ns[i] = nv;
+    near[i] = (uint32_t)chosen;
+  }
   const SumCert r = block_cert_256(cert_of(nv), sh);
   if (t == 0) {
     ps[blockIdx.x] = r.s;
@@ -1432,7 +1468,10 @@ size_t kmeans_pp_device(const float* P, size_t n, int dim, int ldp, size_t k, Ch
   DevBuf<int8_t> Q(q8 ? n * kq : 0);
   DevBuf<float> qscale(q8 ? n : 0), qdelta(q8 ? n : 0);
   DevBuf<int> qnorm(q8 ? n : 0), picked(1);
+  DevBuf<uint32_t> near(q8 ? n : 0);  // every distance is to centre 0 so far
+  DevBuf<float> dcc(q8 ? k : 0);
   if (q8) {
+    PXG_HIP(hipMemsetAsync(near.p, 0, n * 4, s));
     hipLaunchKernelGGL(km_q8_prep, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, P, ldp, (int)n, dim, kq, Q.p,
                        qscale.p, qdelta.p, qnorm.p);
     PXG_HIP(hipGetLastError());
@@ -1443,11 +1482,13 @@ size_t kmeans_pp_device(const float* P, size_t n, int dim, int ldp, size_t k, Ch
     hipLaunchKernelGGL(km_pp_pick, dim3(1), dim3(1024), 0, s, P, ldp, (int)n, dim, ns.p, ps.p, pe.p, nb, drng.p, c,
                        flags.p, flags.p + 1, picked.p);
     if (chosen + 1 < k) {
-      if (q8)
+      if (q8) {
+        hipLaunchKernelGGL(km_pp_cdist, dim3((unsigned)((chosen + 63) / 64)), dim3(256), 0, s, (const float*)cents,
+                           dim, (int)chosen, dcc.p);
         hipLaunchKernelGGL(km_pp_round_q8, dim3(nb), dim3(256), 0, s, P, ldp, (int)n, dim, (const int8_t*)Q.p, kq,
                            (const float*)qscale.p, (const float*)qdelta.p, (const int*)qnorm.p, (const int*)picked.p,
-                           ns.p, ps.p, pe.p, gamma);
-      else
+                           ns.p, ps.p, pe.p, gamma, near.p, (const float*)dcc.p, (int)chosen);
+      } else
         hipLaunchKernelGGL(km_pp_round, dim3(nb), dim3(256), 0, s, P, ldp, (int)n, dim, c, ns.p, 0, ps.p, pe.p,
                            vec4);
     }
