@@ -436,12 +436,15 @@ def bench_kmeans(args, torch, px, dev):
     inertia, its = px.kmeans_device(x, K, iters, args.seed, cents, assign, init=seeds)
     t_lloyd = time.perf_counter() - t0
     st = px.kmeans_last_stats()
-    resid = (x - cents[assign.long()]).contiguous()
-    books = torch.empty(dim * 256, device=dev)
-    t0 = time.perf_counter()
-    pq = px.ProductQuantizer.train_device(px.VectorSpace(dim, px.Metric.EUCLIDEAN), resid,
-                                          px.PqConfig(16).with_seed(args.seed), books)
-    t_pq = time.perf_counter() - t0
+    t_pq, pq_its = float("nan"), 0
+    if not args.km_skip_pq:
+        resid = (x - cents[assign.long()]).contiguous()
+        books = torch.empty(dim * 256, device=dev)
+        t0 = time.perf_counter()
+        pq = px.ProductQuantizer.train_device(px.VectorSpace(dim, px.Metric.EUCLIDEAN), resid,
+                                              px.PqConfig(16).with_seed(args.seed), books)
+        t_pq = time.perf_counter() - t0
+        pq_its = pq.training_iterations
     per_iter = t_lloyd / max(its, 1)
     flops = 2.0 * n * K * dim  # per assignment pass
     tflops = flops / per_iter / 1e12
@@ -453,20 +456,20 @@ def bench_kmeans(args, torch, px, dev):
         f"{tflops:.1f} TFLOP/s by 2nKd per iteration), inertia {inertia:.1f}; MFMA distance pass "
         f"{mfma_ms:.2f} ms = {mfma_tflops:.1f} TFLOP/s over {st['mfma_passes']} passes, "
         f"{st['rescanned']} points rescanned exactly; PQ 16x256 on residuals {t_pq:.2f}s "
-        f"({pq.training_iterations} iterations)")
+        f"({pq_its} iterations)")
     out = {"value": round(1.0 / per_iter, 3), "unit": "Lloyd iterations/s", "ms_per_iteration": round(per_iter * 1e3, 2),
            "config": {"workload": "k-means 2M x 128 f32 -> 4096, k-means++ then 10 Lloyd iterations; PQ 16x256 on "
                                   "the residuals", "n": n, "dim": dim, "k": K, "iterations": its},
            "roofline": {"bound": "mfma", "achieved": round(mfma_tflops, 2), "peak": PEAK_FP32_MFMA_TFLOPS,
                         "unit": "TFLOP/s", "frac": round(mfma_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
-                        "traffic": load_traffic("km_mfma_top"),
-                        "kernel": "km_mfma_top", "ms_per_launch": round(mfma_ms, 3),
+                        "traffic": load_traffic("km_mfma_reg"),
+                        "kernel": "km_mfma_reg", "ms_per_launch": round(mfma_ms, 3),
                         "note": "2nKd per assignment pass over the FP32-MFMA approximate distances; winners are "
                                 "certified and rescored with the reference's sequential f32 arithmetic"},
            "effective_tflops_per_iteration": round(tflops, 2),
            "mfma_passes": st["mfma_passes"], "rescanned_points": st["rescanned"],
            "inexact_sums": {"seeding": inexact_seed, "lloyd": st["inexact_sums"]},
-           "seeding_s": round(t_seed, 3), "lloyd_s": round(t_lloyd, 3), "pq_train_s": round(t_pq, 3),
+           "seeding_s": round(t_seed, 3), "lloyd_s": round(t_lloyd, 3), "pq_train_s": None if args.km_skip_pq else round(t_pq, 3),
            "inertia": inertia}
     if not args.no_cpu:
         from oracle import oracle as orc
@@ -583,6 +586,8 @@ def main():
     ap.add_argument("--skip-kmeans", action="store_true")
     ap.add_argument("--kmeans-only", action="store_true", help="run only the k-means leg (prints its JSON object)")
     ap.add_argument("--km-n", type=int, default=2_000_000)
+    ap.add_argument("--km-skip-pq", action="store_true",
+                    help="k-means leg without the PQ training (one host thread; for counter profiling)")
     ap.add_argument("--km-cpu-sample", type=int, default=131072)
     ap.add_argument("--skip-fixture", action="store_true")
     ap.add_argument("--fixture-only", action="store_true", help="run only the fixture leg (prints its JSON object)")

@@ -534,6 +534,111 @@ __global__ __launch_bounds__(256, 2) void km_mfma_small(const float* __restrict_
   }
 }
 
+// km_mfma_reg: km_mfma_small's form for rows of 32 to 128 floats (dim a
+// multiple of 32): each wave holds its 32 points' rows in VGPRs (lane half h
+// the dims [h dim/2, (h+1) dim/2)) for the whole pass, and the centroids
+// stream through LDS 32 rows at a time (a block of the MFMA), copied
+// straight from memory (km_lds_copy16), double-buffered, one barrier per
+// block. Rows are stored unpadded with 16-byte chunk c of row r at position
+// c ^ (r & 7), so the lanes' float4 operand reads of 32 rows spread over the
+// banks. The top-2 scan is km_mfma_small's; no dot-product tile goes
+// through LDS. 128 points per 256-thread workgroup.
+template <int HD>  // dim / 2
+__global__ __launch_bounds__(256, 3) void km_mfma_reg(const float* __restrict__ P, int ldp,
+                                                   const uint32_t* __restrict__ rows, int n,
+                                                   const float* __restrict__ C, int ldc, int k,
+                                                   const float* __restrict__ cn, uint32_t* __restrict__ best_idx,
+                                                   float* __restrict__ best, float* __restrict__ second) {
+  constexpr int D = 2 * HD, CPR = D / 4;  // 16-byte chunks per row
+  static_assert(D % 32 == 0 && D <= 128, "whole groups of eight chunks per row");
+  constexpr int TILE = 32 * D;             // floats per centroid block
+  constexpr int NI = CPR / 8;              // copy instructions per wave per block (4 waves, 64 lanes)
+  __shared__ __align__(16) float sc[2 * TILE];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, r = lane & 31;
+  const int wid_s = __builtin_amdgcn_readfirstlane(w);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float*)sc;
+  // the copy of block b into buffer buf: instruction u of wave w covers
+  // chunk positions 64 (w NI + u) + lane of the block
+  auto gload = [&](int b, int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < NI; ++u) {
+      const int g = wid_s * NI + u;
+      const int idx = 64 * g + lane, row = idx / CPR, pos = idx - row * CPR;
+      const int c = pos ^ (row & 7);
+      const int crow = min(b * 32 + row, k - 1);
+      km_lds_copy16(C + (size_t)crow * ldc + 4 * c, lds0 + (uint32_t)((buf * TILE + 64 * 4 * g) * 4));
+    }
+  };
+  const int p0 = (blockIdx.x * 4 + w) * 32;
+  const int pi = min(p0 + r, n - 1);
+  const float* prow = P + (size_t)(rows ? rows[pi] : (uint32_t)pi) * ldp + h * HD;
+  float bq[HD];
+#pragma unroll
+  for (int q = 0; q < HD / 4; ++q) {
+    const float4 x = *reinterpret_cast<const float4*>(prow + 4 * q);
+    bq[4 * q] = x.x;
+    bq[4 * q + 1] = x.y;
+    bq[4 * q + 2] = x.z;
+    bq[4 * q + 3] = x.w;
+  }
+  const int nblk = (k + 31) / 32;
+  gload(0, 0);
+  float b1 = INFINITY, b2 = INFINITY;
+  int i1 = 0, t1 = 0;
+  auto take = [&](float x, int v) {
+    i1 = x < b1 ? v : i1;
+    b2 = __builtin_amdgcn_fmed3f(b1, b2, x);
+    b1 = fminf(b1, x);
+  };
+  const int r7 = r & 7;
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int cur = blk & 1;
+    // this block's norms (rows 8 (v/4) + 4 h + v%4), loaded before the wait
+    float cv[16];
+#pragma unroll
+    for (int vb = 0; vb < 4; ++vb) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) cv[4 * vb + e] = cn[min(blk * 32 + 8 * vb + 4 * h + e, k - 1)];
+    }
+    km_vm_wait0();  // this wave's copies of block blk (and the norms) have landed
+    __syncthreads();  // everyone's copies of blk are in; everyone is done with blk - 1
+    if (blk + 1 < nblk) gload(blk + 1, cur ^ 1);
+    const float* ca = &sc[cur * TILE + r * D];
+    f16v acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+#pragma unroll
+    for (int q = 0; q < HD / 4; ++q) {
+      const float4 a = *reinterpret_cast<const float4*>(ca + 4 * ((h * (HD / 4) + q) ^ r7));
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, bq[4 * q], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, bq[4 * q + 1], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, bq[4 * q + 2], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, bq[4 * q + 3], acc, 0, 0, 0);
+    }
+    const float b1_in = b1;
+    if (blk * 32 + 32 <= k) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) take(__builtin_fmaf(-2.0f, acc[v], cv[v]), v);
+    } else {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float x = __builtin_fmaf(-2.0f, acc[v], cv[v]);
+        take(blk * 32 + 8 * (v >> 2) + 4 * h + (v & 3) < k ? x : INFINITY, v);
+      }
+    }
+    t1 = b1 < b1_in ? blk : t1;
+  }
+  const int ix = t1 * 32 + 8 * (i1 >> 2) + 4 * h + (i1 & 3);
+  const float y1 = __shfl_xor(b1, 32, WAVE), y2 = __shfl_xor(b2, 32, WAVE);
+  const int yi = __shfl_xor(ix, 32, WAVE);
+  if (h == 0 && p0 + r < n) {
+    const bool tk = y1 < b1 || (y1 == b1 && yi < ix);
+    best[p0 + r] = tk ? y1 : b1;
+    best_idx[p0 + r] = (uint32_t)(tk ? yi : ix);
+    second[p0 + r] = fminf(tk ? b1 : y1, fminf(b2, y2));
+  }
+}
+
 constexpr int KV_PB = 128;  // points per km_mfma_verify block (256 threads)
 template <bool UNR>
 __global__ __launch_bounds__(256) void km_mfma_verify(const float* __restrict__ P, int ldp,
@@ -818,8 +923,22 @@ void nearest_device(const float* P, int ldp, const uint32_t* rows, size_t n, int
     PXG_HIP(hipEventCreate(&e0));
     PXG_HIP(hipEventCreate(&e1));
     PXG_HIP(hipEventRecord(e0, s));
-    hipLaunchKernelGGL(km_mfma_top, dim3((unsigned)((n + KA_M - 1) / KA_M)), dim3(256), 0, s, P, ldp, rows, (int)n,
-                       dim, C, ldc, (int)k, (const float*)cn, bidx, best, second);
+    const dim3 g128((unsigned)((n + 127) / 128));
+    if (dim == 128)
+      hipLaunchKernelGGL(km_mfma_reg<64>, g128, dim3(256), 0, s, P, ldp, rows, (int)n, C, ldc, (int)k,
+                         (const float*)cn, bidx, best, second);
+    else if (dim == 96)
+      hipLaunchKernelGGL(km_mfma_reg<48>, g128, dim3(256), 0, s, P, ldp, rows, (int)n, C, ldc, (int)k,
+                         (const float*)cn, bidx, best, second);
+    else if (dim == 64)
+      hipLaunchKernelGGL(km_mfma_reg<32>, g128, dim3(256), 0, s, P, ldp, rows, (int)n, C, ldc, (int)k,
+                         (const float*)cn, bidx, best, second);
+    else if (dim == 32)
+      hipLaunchKernelGGL(km_mfma_reg<16>, g128, dim3(256), 0, s, P, ldp, rows, (int)n, C, ldc, (int)k,
+                         (const float*)cn, bidx, best, second);
+    else
+      hipLaunchKernelGGL(km_mfma_top, dim3((unsigned)((n + KA_M - 1) / KA_M)), dim3(256), 0, s, P, ldp, rows,
+                         (int)n, dim, C, ldc, (int)k, (const float*)cn, bidx, best, second);
     PXG_HIP(hipEventRecord(e1, s));
   }
   PXG_HIP(hipMemsetAsync(nredo, 0, 4, s));
