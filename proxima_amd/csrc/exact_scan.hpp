@@ -20,24 +20,24 @@ inline int exact_chunk_rows(size_t nq, size_t N) {
 
 // Small fills done by kernels rather than memsets (so that a caller's stream
 // holds only kernel work): the query flag word ~0, the flagged-query count 0.
-static __global__ void init_search_flags(unsigned long long* bad, int* flag_count) {
+[[maybe_unused]] static __global__ void init_search_flags(unsigned long long* bad, int* flag_count) {
   if (threadIdx.x == 0) {
     *bad = ~0ull;
     *flag_count = 0;
   }
 }
-static __global__ void fill_u32(uint32_t* p, size_t n, uint32_t v) {
+[[maybe_unused]] static __global__ void fill_u32(uint32_t* p, size_t n, uint32_t v) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;
 }
-static __global__ void set_int(int* p, int v) {
+[[maybe_unused]] static __global__ void set_int(int* p, int v) {
   if (threadIdx.x == 0) *p = v;
 }
 
 // ---------------------------------------------------------------------------
 // 1. query preparation
 // ---------------------------------------------------------------------------
-static __global__ __launch_bounds__(64) void flat_prep_queries(const float* __restrict__ raw, int dim, int ld, int metric,
+[[maybe_unused]] static __global__ __launch_bounds__(64) void flat_prep_queries(const float* __restrict__ raw, int dim, int ld, int metric,
                                                         int do_prepare, float* __restrict__ Qp,
                                                         float* __restrict__ qb, float* __restrict__ qn,
                                                         unsigned long long* __restrict__ bad) {
@@ -105,7 +105,7 @@ __device__ inline void block_bitonic_sort(uint64_t* keys, int n) {
 // 4. exact VALU scan for a list of queries
 // ---------------------------------------------------------------------------
 template <int CH>
-static __global__ __launch_bounds__(256) void flat_exact_candidates(
+[[maybe_unused]] static __global__ __launch_bounds__(256) void flat_exact_candidates(
     const int* __restrict__ qlist, const int* __restrict__ qcount, int nchunks, const float* __restrict__ Qp, int ld,
     int dim, int metric, const float* __restrict__ X, int N, const uint8_t* __restrict__ live,
     const uint8_t* __restrict__ accept, const uint32_t* __restrict__ rank, int k, uint64_t* __restrict__ ecand) {
@@ -163,7 +163,7 @@ static __global__ __launch_bounds__(256) void flat_exact_candidates(
 constexpr int EXACT_MERGE_MAXK = 1024;
 
 template <int CH>
-static __global__ __launch_bounds__(256) void flat_merge_exact(const int* __restrict__ qlist, const int* __restrict__ qcount,
+[[maybe_unused]] static __global__ __launch_bounds__(256) void flat_merge_exact(const int* __restrict__ qlist, const int* __restrict__ qcount,
                                                         const uint64_t* __restrict__ ecand, int nchunks, int k,
                                                         const uint32_t* __restrict__ rank_slot,
                                                         const uint64_t* __restrict__ ids,
@@ -231,7 +231,7 @@ static __global__ __launch_bounds__(256) void flat_merge_exact(const int* __rest
   if (threadIdx.x == 0) out_count[q] = ksel;
 }
 
-static __global__ void iota_kernel(int* a, int n, int* count) {
+[[maybe_unused]] static __global__ void iota_kernel(int* a, int n, int* count) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) a[i] = i;
   if (i == 0) *count = n;
@@ -239,7 +239,7 @@ static __global__ void iota_kernel(int* a, int n, int* count) {
 
 // Scatter staged rows into their slots (insert path); X and xb may be null
 // (an index that keeps no full-precision rows).
-static __global__ void flat_scatter_rows(const float* __restrict__ staged, const uint32_t* __restrict__ slots,
+[[maybe_unused]] static __global__ void flat_scatter_rows(const float* __restrict__ staged, const uint32_t* __restrict__ slots,
                                   const float* __restrict__ bias, const uint64_t* __restrict__ sid, int n, int ld,
                                   float* __restrict__ X, float* __restrict__ xb, uint8_t* __restrict__ live,
                                   uint64_t* __restrict__ ids) {

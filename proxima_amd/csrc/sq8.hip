@@ -56,7 +56,7 @@ constexpr int SQ_MAX_CHUNKS = 1024;   // stage-1 entries per query <= 2 * this
 constexpr int SQ_MAX_KB = 8;          // MFMA path: code rows up to 256 bytes
 constexpr uint32_t SQ_MAX_DIM = 65536;  // |S| < 2^31
 // Buffer resource word 3 for raw (untyped, stride 0) gfx9 buffer accesses.
-constexpr int SQ_RSRC_WORD3 = 0x00020000;
+[[maybe_unused]] constexpr int SQ_RSRC_WORD3 = 0x00020000;
 constexpr int SQ_LCAP = 1024;         // per-workgroup candidate list in LDS
 
 __host__ __device__ constexpr int sq_rows(int kb) { return kb <= 4 ? 256 : 128; }
@@ -366,7 +366,7 @@ __global__ __launch_bounds__(SQ_NW * 64) void sq8_mfma_scan(
     const int sl = 64 * (w + j * SQ_NW) + lane, row = sl / SPR, part = sl % SPR;
     voff[j] = part < PPR ? row * KP + part * 16 : 0x7FFFFFF0u;  // padding: beyond the range, reads zeros
   }
-  const uint8_t* vsrc = w == SQ_NW - 1 ? live : (accept ? accept : live);
+  [[maybe_unused]] const uint8_t* vsrc = w == SQ_NW - 1 ? live : (accept ? accept : live);
   auto issue = [&](int t, int buf) __attribute__((always_inline)) {
 #if defined(__HIP_DEVICE_COMPILE__)
     const int rows = min(R, N - t * R);

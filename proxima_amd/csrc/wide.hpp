@@ -32,13 +32,13 @@ void exact_wide_search(const float* Qp, int ld, int dim, int metric, uint64_t nq
                        size_t ldo, Scratch& sc, hipStream_t s);
 
 // offsets[i] = i * seg for i <= n
-static __global__ void wide_offsets(uint32_t* offsets, int n, uint32_t seg) {
+[[maybe_unused]] static __global__ void wide_offsets(uint32_t* offsets, int n, uint32_t seg) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i <= n) offsets[i] = (uint32_t)i * seg;
 }
 
 // ends[g] = begins[g] + min(t, ends_in[g] - begins[g])
-static __global__ void wide_truncate(const uint32_t* __restrict__ begins, const uint32_t* __restrict__ ends_in,
+[[maybe_unused]] static __global__ void wide_truncate(const uint32_t* __restrict__ begins, const uint32_t* __restrict__ ends_in,
                                      int n, uint64_t t, uint32_t* __restrict__ ends) {
   const int g = blockIdx.x * blockDim.x + threadIdx.x;
   if (g >= n) return;
@@ -49,7 +49,7 @@ static __global__ void wide_truncate(const uint32_t* __restrict__ begins, const 
 // Results of queries q0 .. q0 + G - 1 from their sorted segments: the first
 // min(kq, valid) keys (KEY_MAX marks no candidate; valid keys sort first).
 // Grid (ceil(kq / 256), G).
-static __global__ void wide_emit(const uint64_t* __restrict__ sorted, const uint32_t* __restrict__ begins,
+[[maybe_unused]] static __global__ void wide_emit(const uint64_t* __restrict__ sorted, const uint32_t* __restrict__ begins,
                                  const uint32_t* __restrict__ ends, int q0, uint64_t kq,
                                  const uint32_t* __restrict__ rank_slot, const uint64_t* __restrict__ ids,
                                  uint64_t* __restrict__ out_ids, float* __restrict__ out_d,
@@ -79,7 +79,7 @@ static __global__ void wide_emit(const uint64_t* __restrict__ sorted, const uint
 // Exact (distance, id rank) keys of every slot for queries q0 .. q0 + G - 1
 // (grid (ceil(N / 32), G), 8 threads per slot), KEY_MAX for free or
 // filtered slots; segment g starts at g * seg.
-static __global__ __launch_bounds__(256) void wide_exact_keys(const float* __restrict__ Qp, int ld, int dim,
+[[maybe_unused]] static __global__ __launch_bounds__(256) void wide_exact_keys(const float* __restrict__ Qp, int ld, int dim,
                                                               int metric, const float* __restrict__ X, int N,
                                                               const uint8_t* __restrict__ live,
                                                               const uint8_t* __restrict__ accept,
