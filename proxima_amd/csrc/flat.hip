@@ -376,11 +376,18 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
     }
     return;
   }
-  // Final: every row leaves exactly Kp sorted keys (KEY_MAX padded).
+  // Final: every row leaves Kp keys, its Kp smallest (KEY_MAX padded). The
+  // merge reads them as a set, so a row with at most Kp keys is only padded;
+  // a fuller one is sorted down to Kp.
   for (int row = wid; row < FB_M; row += 4) {
     if (q0 + row >= nq) continue;
-    compact_row<CAP>(cand + ((size_t)(q0 + row) * S + split) * CAP, cnt[row], Kp, lane, &thr[row], &thr_f[row],
-                     &cnt[row], gthr + q0 + row, true);
+    uint64_t* base = cand + ((size_t)(q0 + row) * S + split) * CAP;
+    const int c = cnt[row];
+    if (c <= Kp) {
+      for (int i = c + lane; i < Kp; i += WAVE) base[i] = KEY_MAX;
+    } else {
+      compact_row<CAP>(base, c, Kp, lane, &thr[row], &thr_f[row], &cnt[row], gthr + q0 + row, true);
+    }
   }
 }
 
