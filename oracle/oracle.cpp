@@ -385,6 +385,22 @@ size_t km_farthest(const float* pts, size_t n, size_t dim, const float* cents, s
   return best;
 }
 
+// The D^2 pick of one k-means++ round (kmeans.rs:167-178): the first index
+// whose f64 cumulative sum of the nearest-squared distances reaches `target`,
+// n-1 if none does.
+size_t pp_pick(const float* ns, size_t n, double target) {
+  double cum = 0.0;
+  size_t index = n - 1;
+  for (size_t i = 0; i < n; ++i) {
+    cum += (double)ns[i];
+    if (cum >= target) {
+      index = i;
+      break;
+    }
+  }
+  return index;
+}
+
 // kmeans_plus_plus: kmeans.rs:146-194.
 void kmeans_pp(const float* pts, size_t n, size_t dim, size_t k, Rng& rng, float* cents) {
   size_t first = rng.gen_range_usize(n);
@@ -399,16 +415,7 @@ void kmeans_pp(const float* pts, size_t n, size_t dim, size_t k, Rng& rng, float
       picked = rng.gen_range_usize(n);
     } else {
       double target = rng.gen_range_f64(0.0, total);
-      double cum = 0.0;
-      size_t index = n - 1;
-      for (size_t i = 0; i < n; ++i) {
-        cum += (double)ns[i];
-        if (cum >= target) {
-          index = i;
-          break;
-        }
-      }
-      picked = index;
+      picked = pp_pick(ns.data(), n, target);
     }
     float* c = cents + chosen * dim;
     std::memcpy(c, pts + picked * dim, dim * sizeof(float));
@@ -877,6 +884,16 @@ void orc_kmeans_pp(const float* pts, size_t n, size_t dim, size_t k, uint64_t se
   kmeans_pp(pts, n, dim, k, rng, cents);
 }
 // kmeans() with a fresh ChaCha8Rng::seed_from_u64(seed). Returns clamped k.
+size_t orc_kmeans_pp_pick(const float* ns, size_t n, double target) { return pp_pick(ns, n, target); }
+// kmeans() driven by a caller's generator (left advanced, as the reference's
+// `&mut rng` is): the composition product.rs:247-270 repeats per subspace.
+size_t orc_kmeans_rng(const float* pts, size_t n, size_t dim, size_t k, size_t max_iter, void* rng, float* cents_out,
+                      double* inertia, size_t* iters) {
+  std::vector<float> cents;
+  size_t kk = kmeans_full(pts, n, dim, k, max_iter, *(Rng*)rng, cents, inertia, iters);
+  std::memcpy(cents_out, cents.data(), cents.size() * sizeof(float));
+  return kk;
+}
 size_t orc_kmeans(const float* pts, size_t n, size_t dim, size_t k, size_t max_iter, uint64_t seed, float* cents_out,
                   double* inertia, size_t* iters) {
   Rng rng;

@@ -73,6 +73,9 @@ def _load():
         "orc_kmeans_pp": (None, [_f32p, _sz, _sz, _sz, C.c_uint64, _f32p]),
         "orc_kmeans": (_sz, [_f32p, _sz, _sz, _sz, _sz, C.c_uint64, _f32p, C.POINTER(C.c_double),
                              C.POINTER(C.c_size_t)]),
+        "orc_kmeans_pp_pick": (_sz, [_f32p, _sz, C.c_double]),
+        "orc_kmeans_rng": (_sz, [_f32p, _sz, _sz, _sz, _sz, C.c_void_p, _f32p, C.POINTER(C.c_double),
+                                 C.POINTER(C.c_size_t)]),
         "orc_kmeans_assign": (None, [_f32p, _sz, _sz, _f32p, _sz, _u32p, _f32p]),
         "orc_kmeans_assign_mt": (None, [_f32p, _sz, _sz, _f32p, _sz, _u32p, _f32p, C.c_int]),
         "orc_rng_new": (C.c_void_p, [C.c_uint64, C.c_int]),
@@ -352,6 +355,23 @@ def kmeans(points, k, max_iter, seed):
     inertia = C.c_double()
     iters = C.c_size_t()
     got = lib.orc_kmeans(points.reshape(-1), n, dim, k, max_iter, seed, cents, C.byref(inertia), C.byref(iters))
+    return cents.reshape(got, dim), inertia.value, iters.value
+
+
+def kmeans_pp_pick(ns, target):
+    ns = f32(ns)
+    return int(lib.orc_kmeans_pp_pick(ns, ns.size, float(target)))
+
+
+def kmeans_with_rng(points, k, max_iter, rng):
+    """kmeans() over `rng` (an Rng), which is left advanced."""
+    points = f32(points)
+    n, dim = points.shape
+    kk = max(min(k, n), 1)
+    cents = np.zeros(kk * dim, np.float32)
+    inertia = C.c_double()
+    iters = C.c_size_t()
+    got = lib.orc_kmeans_rng(points.reshape(-1), n, dim, k, max_iter, rng.h, cents, C.byref(inertia), C.byref(iters))
     return cents.reshape(got, dim), inertia.value, iters.value
 
 

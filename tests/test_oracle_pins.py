@@ -18,7 +18,8 @@ vector, chosen so that a plausible restatement slip gives a different answer:
   generator, and the ChaCha core at 8 and 12 rounds against published vectors.
 
 test_planted_mistakes_are_caught compiles mutated copies of oracle.cpp and
-checks that these tests fail on each.
+checks that these tests, and the composition pins of
+test_oracle_compositions.py, fail on each.
 """
 import os
 import re
@@ -309,6 +310,67 @@ MUTANTS = [
      "    state = state * MUL + INC;\n    uint32_t xorshifted = (uint32_t)(((state >> 18) ^ state) >> 27);\n    uint32_t rot = (uint32_t)(state >> 59);",
      "    uint64_t old = state;\n    state = state * MUL + INC;\n    uint32_t xorshifted = (uint32_t)(((old >> 18) ^ old) >> 27);\n    uint32_t rot = (uint32_t)(old >> 59);",
      ["test_kat_seed_from_u64_is_pcg32"]),
+    # compositions (test_oracle_compositions.py)
+    ("PQ generator reseeded per subspace",
+     "    size_t w = L.widths[s], off = L.offsets[s];",
+     "    seed_from_u64(rng, seed);\n    size_t w = L.widths[s], off = L.offsets[s];",
+     ["test_pq_train_one_generator_across_subspaces", "test_pq_twin_subspaces_get_different_codebooks"]),
+    ("PQ padding repeats the first centroid",
+     "cents.data() + (produced - 1) * w",
+     "cents.data()",
+     ["test_pq_padding_repeats_the_last_centroid", "test_pq_train_one_generator_across_subspaces"]),
+    ("Box-Muller draws swapped",
+     "  float u1 = std::fmax(rng.gen_f32(), 1.17549435e-38f);\n  float u2 = rng.gen_f32();",
+     "  float u2 = rng.gen_f32();\n  float u1 = std::fmax(rng.gen_f32(), 1.17549435e-38f);",
+     ["test_fixture_draw_order_and_box_muller"]),
+    ("fixture query noise scale",
+     "fixture_gaussian(rng) * 0.25f",
+     "fixture_gaussian(rng) * 0.5f",
+     ["test_fixture_draw_order_and_box_muller"]),
+    ("fixture query source without the stride",
+     "    size_t src = (q * stride) % count;",
+     "    size_t src = q % count;",
+     ["test_fixture_draw_order_and_box_muller"]),
+    ("k-means++ cumulative sum in f32",
+     "  double cum = 0.0;\n  size_t index = n - 1;",
+     "  float cum = 0.0f;\n  size_t index = n - 1;",
+     ["test_pp_pick_accumulates_in_f64", "test_kmeans_pp_composition"]),
+    ("k-means++ pick with > for >=",
+     "    if (cum >= target) {",
+     "    if (cum > target) {",
+     ["test_pp_pick_first_index_reaching_target"]),
+    ("IVF PQ seeded apart from the coarse stage",
+     "  pq_train(resid.data(), sampled, dim, m, max_iter, seed, books_out, &rin, &rit);",
+     "  pq_train(resid.data(), sampled, dim, m, max_iter, seed + 1, books_out, &rin, &rit);",
+     ["test_ivf_train_composition"]),
+    ("IVF PQ trained on the sample, not its residuals",
+     "  pq_train(resid.data(), sampled, dim, m, max_iter, seed, books_out, &rin, &rit);",
+     "  pq_train(sample.data(), sampled, dim, m, max_iter, seed, books_out, &rin, &rit);",
+     ["test_ivf_train_composition"]),
+    ("IVF stride sample floored",
+     "  size_t stride = std::max<size_t>((L + training_sample - 1) / training_sample, 1);",
+     "  size_t stride = std::max<size_t>(L / training_sample, 1);",
+     ["test_ivf_train_composition"]),
+    ("IVF coarse ties by descending list",
+     "        return a.second < b.second;",
+     "        return a.second > b.second;",
+     ["test_ivf_search_composition_l2"]),
+    ("IVF shortlist ignores k",
+     "      size_t shortlist = rerank > 0 ? std::max(rerank, k) : k;",
+     "      size_t shortlist = rerank > 0 ? rerank : k;",
+     ["test_ivf_search_composition_l2", "test_ivf_search_composition_cosine_filter_and_untrained_shape"]),
+    ("IVF nprobe not clamped below",
+     "  size_t np = std::min(std::max<size_t>(nprobe, 1), std::max<size_t>(produced, 1));",
+     "  size_t np = std::min(nprobe, produced);",
+     ["test_ivf_search_composition_l2"]),
+    ("IVF cosine score without the centroid term",
+     "arm_nan(1.0f - qdc)",
+     "arm_nan(1.0f)",
+     ["test_ivf_search_composition_cosine_filter_and_untrained_shape"]),
+    ("IVF rerank keeps the ADC score",
+     "        exact.push(h.id, space_distance(metric, qv, vectors + s * dim, dim));",
+     "        exact.push(h.id, h.d);",
+     ["test_ivf_search_composition_l2", "test_ivf_search_composition_cosine_filter_and_untrained_shape"]),
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -327,7 +389,8 @@ def _run_mutant(tmp, i, src, old, new):
                     "-shared", "-o", so, cpp], check=True)
     env = dict(os.environ, PXG_ORACLE_LIB=so)
     res = subprocess.run([sys.executable, "-m", "pytest", "-q", "-p", "no:cacheprovider", "-rf",
-                          os.path.join(_HERE, "test_oracle_pins.py"), "-k", "not planted"],
+                          os.path.join(_HERE, "test_oracle_pins.py"), os.path.join(_HERE, "test_oracle_compositions.py"),
+                          "-k", "not planted"],
                          capture_output=True, text=True, cwd=_ROOT, env=env)
     return set(re.findall(r"FAILED \S*::(\w+)", res.stdout))
 
