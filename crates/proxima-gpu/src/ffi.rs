@@ -77,6 +77,8 @@ pub(crate) struct PxgTrainingReport {
 extern "C" {
     pub(crate) fn pxg_last_error_message() -> *const c_char;
     pub(crate) fn pxg_last_error_detail(a: *mut u64, b: *mut u64, value: *mut f32) -> c_int;
+    pub(crate) fn pxg_last_error_parameter() -> *const c_char;
+    pub(crate) fn pxg_last_error_reason() -> *const c_char;
     pub(crate) fn pxg_version() -> *const c_char;
     pub(crate) fn pxg_device_count() -> c_int;
     pub(crate) fn pxg_set_profiling(enabled: c_int);

@@ -38,16 +38,39 @@ fn check(status: c_int) -> Result<()> {
     unsafe { ffi::pxg_last_error_detail(&mut a, &mut b, &mut value) };
     // SAFETY: the message is a NUL-terminated thread-local string that lives until the next call.
     let detail = unsafe { CStr::from_ptr(ffi::pxg_last_error_message()) }.to_string_lossy().into_owned();
+    // SAFETY: both accessors return pointers to string literals inside the
+    // library (static storage; the library is linked, never unloaded), so the
+    // borrow may be 'static.
+    let parameter = unsafe { static_str(ffi::pxg_last_error_parameter()) };
+    let reason = unsafe { static_str(ffi::pxg_last_error_reason()) };
     Err(match status {
         1 => ProximaError::DimensionMismatch { expected: a as usize, actual: b as usize },
         2 => ProximaError::UnknownId { id: VectorId::new(a) },
         3 => ProximaError::DuplicateId { id: VectorId::new(a) },
-        4 => ProximaError::Capacity { what: "device memory", limit: a as usize },
+        4 => ProximaError::Capacity { what: parameter.unwrap_or("device memory"), limit: a as usize },
         5 => ProximaError::NonFinite { index: a as usize, value },
         6 => ProximaError::Corruption { structure: "device index", detail },
-        7 => ProximaError::Configuration { parameter: "proxima-gpu", value: a.to_string(), reason: "rejected by libproxima_hip" },
+        7 => ProximaError::Configuration {
+            parameter: parameter.unwrap_or("proxima-gpu"),
+            value: a.to_string(),
+            reason: reason.unwrap_or("rejected by libproxima_hip"),
+        },
         _ => ProximaError::Internal { location: "proxima-gpu", detail },
     })
+}
+
+/// A NUL-terminated string of static storage from the library, or `None`
+/// when it is empty or not UTF-8.
+///
+/// # Safety
+/// `p` is NULL or points to a NUL-terminated string that lives for the rest
+/// of the process.
+unsafe fn static_str(p: *const std::os::raw::c_char) -> Option<&'static str> {
+    if p.is_null() {
+        return None;
+    }
+    let s: &'static CStr = CStr::from_ptr(p);
+    s.to_str().ok().filter(|s| !s.is_empty())
 }
 
 /// `Metric` in declaration order (distance.rs:90-118), as the C ABI numbers it.
@@ -231,6 +254,7 @@ impl GpuFlatIndex {
     }
 
     fn search_one(&self, query: &[f32], k: usize, filter: Option<&dyn Filter>) -> Result<Vec<SearchResult>> {
+        check_k(k)?;  // first, as flat.rs:153-155 and ivfpq.rs:988
         self.space.validate(query)?;
         Ok(self.search_batch(query, k, filter)?.pop().unwrap_or_default())
     }
@@ -380,6 +404,7 @@ impl GpuIvfPqIndex {
 
     /// `IvfPqIndex::search_with_nprobe` (ivfpq.rs:981-996).
     pub fn search_with_nprobe(&self, query: &[f32], k: usize, nprobe: usize, filter: &dyn Filter) -> Result<Vec<SearchResult>> {
+        check_k(k)?;  // first, as flat.rs:153-155 and ivfpq.rs:988
         self.space.validate(query)?;
         Ok(self.search_batch(query, k, nprobe, Some(filter))?.pop().unwrap_or_default())
     }
@@ -407,6 +432,7 @@ impl VectorIndex for GpuIvfPqIndex {
     }
 
     fn search_all(&self, query: &[f32], k: usize) -> Result<Vec<SearchResult>> {
+        check_k(k)?;  // first, as flat.rs:153-155 and ivfpq.rs:988
         self.space.validate(query)?;
         Ok(self.search_batch(query, k, self.config.nprobe(), None)?.pop().unwrap_or_default())
     }
@@ -509,11 +535,13 @@ impl VectorIndex for GpuSq8Index {
     }
 
     fn search(&self, query: &[f32], k: usize, filter: &dyn Filter) -> Result<Vec<SearchResult>> {
+        check_k(k)?;  // first, as flat.rs:153-155 and ivfpq.rs:988
         self.space.validate(query)?;
         Ok(self.search_batch(query, k, Some(filter))?.pop().unwrap_or_default())
     }
 
     fn search_all(&self, query: &[f32], k: usize) -> Result<Vec<SearchResult>> {
+        check_k(k)?;  // first, as flat.rs:153-155 and ivfpq.rs:988
         self.space.validate(query)?;
         Ok(self.search_batch(query, k, None)?.pop().unwrap_or_default())
     }

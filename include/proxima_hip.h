@@ -73,6 +73,15 @@ typedef struct pxg_index_stats {
 const char* pxg_last_error_message(void);
 /* Structured fields of the last error; returns its status. Any pointer may be NULL. */
 int pxg_last_error_detail(uint64_t* a, uint64_t* b, float* value);
+/* PXG_ERR_CONFIGURATION: the parameter's name, as the reference's
+ * Configuration{parameter} spells it ("k", "nprobe", "subspaces", ...);
+ * PXG_ERR_CAPACITY: the structure that ran out of room, as Capacity{what}
+ * ("slot allocator", "device memory", ...). "" for other errors. The pointer
+ * is to static storage and stays valid for the life of the process. */
+const char* pxg_last_error_parameter(void);
+/* PXG_ERR_CONFIGURATION: the constraint that was broken, as the reference's
+ * Configuration{reason}; "" otherwise. Static storage, as above. */
+const char* pxg_last_error_reason(void);
 /* Library version string. */
 const char* pxg_version(void);
 /* Number of visible devices (0 when none); never fails. */
@@ -136,9 +145,14 @@ int pxg_flat_search_device(const pxg_flat* index, const float* d_queries, uint64
  * pinned host memory, stream or event. No counterpart in the reference; it is
  * for callers that cannot allocate (serving loops with a fixed memory budget,
  * code that must not touch the allocator). Its scratch is one static device
- * array of 128 MiB per GPU, held until the process ends; a call that needs
- * more (prepared queries, candidate buffers, exact-scan keys) fails with
- * PXG_ERR_CAPACITY before any work is queued, detail a = bytes it would need.
+ * array of 128 MiB per GPU, held until the process ends. A call that needs
+ * more fails with PXG_ERR_CAPACITY (parameter "no-allocation scratch",
+ * detail a = the array's size) at the first scratch region that does not fit:
+ * prepared queries (nq x round_up(dim, 4) x 4 bytes), candidate buffers
+ * (nq x CAP x 8 bytes per split, CAP = 256 for k <= 96, else 512, at least
+ * one split), exact-scan keys, or the wide path's keys. Stages queued before
+ * that point are waited for before the call returns, so no kernel still uses
+ * the array or writes the outputs afterwards (the outputs are then undefined).
  * Calls on one GPU share that array: a per-GPU lock inside the library
  * serializes them, and each call has finished on the GPU when it returns.
  * stream: the caller's (NULL = the null stream). Results equal
@@ -186,7 +200,9 @@ typedef struct pxg_training_report {
  * iterations, 100000-vector sample, threshold nlist*100, vectors retained. */
 int pxg_ivfpq_config_default(uint64_t nlist, uint64_t subspaces, pxg_ivfpq_config* out);
 /* IvfPqIndex::new (ivfpq.rs:481-509): Euclidean or Cosine only; config validated
- * (ivfpq.rs:259-304). The GPU distance table holds at most 128 subspaces. */
+ * (ivfpq.rs:259-304): 1 to dim subspaces. Above 128 subspaces the per-probe
+ * tables do not fit in LDS and the search takes the wide path (tables and
+ * keys in device memory, sorted). */
 int pxg_ivfpq_create(uint32_t dim, int metric, const pxg_ivfpq_config* config, pxg_ivfpq** out);
 void pxg_ivfpq_destroy(pxg_ivfpq* index);
 /* VectorIndex::insert (ivfpq.rs:1129-1158), batched and all-or-nothing per
@@ -344,7 +360,8 @@ int pxg_sq8_slots(const pxg_sq8* index, uint64_t* ids, uint8_t* live);
 /* Search nq f32 queries (encoded with the index's ranges). rescore > 0:
  * the best max(rescore, k) by integer score are rescored with
  * asymmetric_inner_product and the best k by (distance, id) returned.
- * accept as pxg_flat_search. max(k, rescore) <= 1024. */
+ * accept as pxg_flat_search. k up to 2^24 (check_k); max(k, rescore) above
+ * 1024 takes the sorted path. */
 int pxg_sq8_search(const pxg_sq8* index, const float* queries, uint64_t nq, uint64_t k, uint64_t rescore,
                    const uint8_t* accept, uint64_t* out_ids, float* out_dist, uint32_t* out_count);
 /* Search with queries given as I8 codes (nq x dim bytes); no rescoring. */

@@ -104,6 +104,14 @@ class DuplicateId(ProximaError):
 class Capacity(ProximaError):
     status = 4
 
+    def __init__(self, message, a=0, b=0, value=0.0, what=None):
+        super().__init__(message, a, b, value)
+        self.what = what  # Capacity{what}: the structure that ran out of room
+
+    @property
+    def limit(self):
+        return self.a
+
 
 class NonFinite(ProximaError):
     status = 5
@@ -120,9 +128,10 @@ class Corruption(ProximaError):
 class Configuration(ProximaError):
     status = 7
 
-    def __init__(self, message, a=0, b=0, value=0.0, parameter=None):
+    def __init__(self, message, a=0, b=0, value=0.0, parameter=None, reason=None):
         super().__init__(message, a, b, value)
-        self.parameter = parameter
+        self.parameter = parameter  # Configuration{parameter}, e.g. "k", "nprobe"
+        self.reason = reason        # Configuration{reason}: the constraint that was broken
 
 
 class Internal(ProximaError):
@@ -142,13 +151,16 @@ def _check(status):
     cls = _BY_STATUS.get(status, Internal)
     err = cls(msg, a.value, b.value, v.value)
     if cls is Configuration:
-        err.parameter = msg.split("invalid configuration: ")[-1].split(" =")[0] if "=" in msg else None
+        err.parameter = _lib.pxg_last_error_parameter().decode() or None
+        err.reason = _lib.pxg_last_error_reason().decode() or None
+    elif cls is Capacity:
+        err.what = _lib.pxg_last_error_parameter().decode() or None
     raise err
 
 
 def _config(parameter, value, reason):
     e = Configuration(f"invalid configuration: {parameter} = {value} ({reason})", value if isinstance(value, int)
-                      else 0, parameter=parameter)
+                      else 0, parameter=parameter, reason=reason)
     return e
 
 

@@ -70,6 +70,8 @@ class TrainingReportC(C.Structure):
 SIGNATURES = {
     "pxg_last_error_message": (C.c_char_p, []),
     "pxg_last_error_detail": (_i32, [_P(_u64), _P(_u64), _P(_f32)]),
+    "pxg_last_error_parameter": (C.c_char_p, []),
+    "pxg_last_error_reason": (C.c_char_p, []),
     "pxg_version": (C.c_char_p, []),
     "pxg_device_count": (_i32, []),
     "pxg_set_profiling": (None, [_i32]),

@@ -63,6 +63,10 @@ int pxg_last_error_detail(uint64_t* a, uint64_t* b, float* value) {
   return pxg::g_last.status;
 }
 
+const char* pxg_last_error_parameter(void) { return pxg::g_last.parameter; }
+
+const char* pxg_last_error_reason(void) { return pxg::g_last.reason; }
+
 const char* pxg_version(void) { return "proxima-hip 0.1.0 (gfx950)"; }
 
 void pxg_set_profiling(int enabled) { pxg::g_profiling.store(enabled ? 1 : 0); }

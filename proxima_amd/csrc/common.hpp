@@ -8,6 +8,7 @@
 
 #include <cstdint>
 #include <cstring>
+#include <exception>
 #include <mutex>
 #include <stdexcept>
 #include <string>
@@ -25,6 +26,11 @@ struct Error {
   std::string message;
   uint64_t a = 0, b = 0;  // expected/actual, index, id or limit, per variant
   float value = 0.0f;
+  // Configuration: the parameter's name and the constraint it broke;
+  // Capacity: the structure that ran out of room. Always string literals
+  // (static storage), so the C ABI can hand the pointers out as they are.
+  const char* parameter = "";
+  const char* reason = "";
 };
 
 struct Raise {
@@ -37,9 +43,20 @@ void clear_last_error();
 [[noreturn]] inline void raise(int status, std::string msg, uint64_t a = 0, uint64_t b = 0, float v = 0.0f) {
   throw Raise{Error{status, std::move(msg), a, b, v}};
 }
+// `parameter` and `reason` must be string literals.
 [[noreturn]] inline void config_error(const char* parameter, uint64_t value, const char* reason) {
-  raise(PXG_ERR_CONFIGURATION,
-        std::string("invalid configuration: ") + parameter + " = " + std::to_string(value) + " (" + reason + ")", value);
+  Error e{PXG_ERR_CONFIGURATION,
+          std::string("invalid configuration: ") + parameter + " = " + std::to_string(value) + " (" + reason + ")",
+          value};
+  e.parameter = parameter;
+  e.reason = reason;
+  throw Raise{std::move(e)};
+}
+// Capacity{what, limit} (error.rs:80-85); `what` must be a string literal.
+[[noreturn]] inline void capacity_error(const char* what, uint64_t limit, std::string msg) {
+  Error e{PXG_ERR_CAPACITY, std::move(msg), limit};
+  e.parameter = what;
+  throw Raise{std::move(e)};
 }
 [[noreturn]] inline void internal_error(const char* location, const std::string& detail) {
   raise(PXG_ERR_INTERNAL, std::string("internal invariant violated in ") + location + ": " + detail);
@@ -50,8 +67,9 @@ void clear_last_error();
     hipError_t e_ = (call);                                                                   \
     if (e_ != hipSuccess) {                                                                   \
       if (e_ == hipErrorOutOfMemory || e_ == hipErrorMemoryAllocation)                        \
-        ::pxg::raise(PXG_ERR_CAPACITY, std::string("capacity exceeded: device memory limit (") + \
-                                           hipGetErrorString(e_) + ")");                       \
+        ::pxg::capacity_error("device memory", 0,                                              \
+                              std::string("capacity exceeded: device memory limit (") +        \
+                                  hipGetErrorString(e_) + ")");                                \
       ::pxg::internal_error(#call, hipGetErrorString(e_));                                    \
     }                                                                                         \
   } while (0)
@@ -66,7 +84,9 @@ int guard(F&& f) {
     set_last_error(r.e);
     return r.e.status;
   } catch (const std::bad_alloc&) {
-    set_last_error(Error{PXG_ERR_CAPACITY, "capacity exceeded: host memory"});
+    Error e{PXG_ERR_CAPACITY, "capacity exceeded: host memory"};
+    e.parameter = "host memory";
+    set_last_error(e);
     return PXG_ERR_CAPACITY;
   } catch (const std::exception& ex) {
     set_last_error(Error{PXG_ERR_INTERNAL, std::string("internal invariant violated: ") + ex.what()});
@@ -149,7 +169,7 @@ struct SlotAllocator {
       return s;
     }
     if (next == UINT32_MAX)
-      raise(PXG_ERR_CAPACITY, "capacity exceeded: slot allocator limit is 4294967295", UINT32_MAX);
+      capacity_error("slot allocator", UINT32_MAX, "capacity exceeded: slot allocator limit is 4294967295");
     return next++;
   }
   void release(uint32_t s) { free.push_back(s); }
@@ -220,11 +240,10 @@ struct Arena : Scratch {
   unsigned char* get(int key, size_t bytes) override {
     const size_t at = (off + 255) & ~(size_t)255;
     if (key < 0 || key >= KEYS || at > cap || bytes > cap - at)
-      raise(PXG_ERR_CAPACITY,
-            "this search needs more than the " + std::to_string(cap >> 20) +
-                " MiB of the no-allocation scratch (region " + std::to_string(key) + " of " + std::to_string(bytes) +
-                " bytes at offset " + std::to_string(at) + ")",
-            at + bytes);
+      capacity_error("no-allocation scratch", cap,
+                     "this search needs more than the " + std::to_string(cap >> 20) +
+                         " MiB of the no-allocation scratch (region " + std::to_string(key) + " of " +
+                         std::to_string(bytes) + " bytes at offset " + std::to_string(at) + ")");
     start[key] = at;
     off = at + bytes;
     return base + at;
@@ -271,6 +290,20 @@ struct CtxLease {
   explicit CtxLease(CtxPool& p) : pool(p), c(p.acquire()) {}
   ~CtxLease() { pool.release(c); }
   Ctx* operator->() { return c; }
+};
+
+// A search that fails part-way (a capacity error in a later scratch region,
+// a non-finite query found at the flag readback) may already have kernels
+// queued that read its scratch and write the caller's outputs. Declared after
+// the scratch's owner (a CtxLease, or the lock of the fixed no-allocation
+// block), this waits for that work as the error unwinds, so no kernel still
+// touches the scratch once another call may take it, and none writes the
+// outputs after the call has returned.
+struct DrainOnUnwind {
+  hipStream_t s;
+  ~DrainOnUnwind() {
+    if (std::uncaught_exceptions() > 0) (void)hipStreamSynchronize(s);
+  }
 };
 
 // VectorSpace::validate / prepare on the host (space.rs:104-138). Returns -1

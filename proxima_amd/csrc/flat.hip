@@ -562,7 +562,7 @@ void FlatIndex::insert(const uint64_t* in_ids, const float* vecs, uint64_t n, ui
     }
   }
   if (by_id.size() + n > (size_t)UINT32_MAX - 1)
-    raise(PXG_ERR_CAPACITY, "capacity exceeded: slot allocator limit is 4294967295", UINT32_MAX);
+    capacity_error("slot allocator", UINT32_MAX, "capacity exceeded: slot allocator limit is 4294967295");
   std::vector<uint32_t> sl(n);
   const size_t old_hw = slots.high_water();
   // Allocate in order, exactly as repeated VectorStore::insert would.
@@ -783,7 +783,7 @@ void FlatIndex::insert_device(const uint64_t* in_ids, const float* d_vecs, uint6
         raise(PXG_ERR_DUPLICATE_ID, "duplicate vector id " + std::to_string(in_ids[i]), in_ids[i]);
   }
   if (by_id.size() + n > (size_t)UINT32_MAX - 1)
-    raise(PXG_ERR_CAPACITY, "capacity exceeded: slot allocator limit is 4294967295", UINT32_MAX);
+    capacity_error("slot allocator", UINT32_MAX, "capacity exceeded: slot allocator limit is 4294967295");
   const size_t rows_per = std::max<size_t>(1, (256u << 20) / ((size_t)ld * 4));
   const size_t chunk = std::min<size_t>(rows_per, n);
   DevBuf<float> st_rows(chunk * ld);
@@ -1013,11 +1013,13 @@ int pxg_flat_search_device(const pxg_flat* index, const float* d_queries, uint64
                            const uint8_t* d_accept, uint64_t* d_out_ids, float* d_out_dist, uint32_t* d_out_count,
                            void* stream) {
   return pxg::guard([&] {
+    pxg::check_k(k);  // first, as flat.rs:153-155
     FlatIndex& f = const_cast<FlatIndex&>(index->impl);
     std::shared_lock<std::shared_mutex> lk(f.mu);
     pxg::CtxLease ctx(f.pool);
     pxg::CtxScratch sc(ctx.c);
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    pxg::DrainOnUnwind drain{s};
     uint64_t fb = 0;
     f.search_device(d_queries, true, nq, k, d_accept, d_out_ids, d_out_dist, d_out_count, sc, s, &fb, k);
     PXG_HIP(hipStreamSynchronize(s));

@@ -2690,11 +2690,13 @@ int pxg_ivfpq_search_device(const pxg_ivfpq* index, const float* d_queries, uint
                             const uint8_t* d_accept, uint64_t* d_out_ids, float* d_out_dist, uint32_t* d_out_count,
                             void* stream) {
   return pxg::guard([&] {
+    pxg::check_k(k);  // first, as ivfpq.rs:988
     IvfPqIndex& f = const_cast<IvfPqIndex&>(index->impl);
     std::shared_lock<std::shared_mutex> lk(f.mu);
     pxg::CtxLease ctx(f.pool);
     pxg::CtxScratch sc(ctx.c);
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    pxg::DrainOnUnwind drain{s};
     f.search_device(d_queries, true, nq, k, nprobe ? nprobe : f.cfg.nprobe, d_accept, d_out_ids, d_out_dist,
                     d_out_count, sc, s, k);
     PXG_HIP(hipStreamSynchronize(s));

@@ -33,11 +33,15 @@ extern "C" {
 // hipGetSymbolAddress gives once per device with that device current; host
 // code uses only that address). Calls on one GPU share the array, so a
 // per-GPU lock serializes them, and each call has finished on the GPU when it
-// returns.
+// returns, also when it fails: a request too large for the array fails with
+// Capacity when it reaches the first region that does not fit, possibly after
+// earlier stages were queued, and those are waited for before the lock is
+// released.
 int pxg_flat_search_device_noalloc(const pxg_flat* index, const float* d_queries, uint64_t nq, uint64_t k,
                                    const uint8_t* d_accept, uint64_t* d_out_ids, float* d_out_dist,
                                    uint32_t* d_out_count, void* stream) {
   return pxg::guard([&] {
+    pxg::check_k(k);
     int dev = 0;
     PXG_HIP(hipGetDevice(&dev));
     if (dev < 0 || dev >= pxg::NOALLOC_MAX_DEVICES)
@@ -55,6 +59,7 @@ int pxg_flat_search_device_noalloc(const pxg_flat* index, const float* d_queries
     std::shared_lock<std::shared_mutex> lk(f.mu);
     pxg::Arena arena(pxg::g_noalloc_ptr[dev], pxg::NOALLOC_SCRATCH_BYTES);
     hipStream_t s = (hipStream_t)stream;
+    pxg::DrainOnUnwind drain{s};  // after the lock: an error waits for queued work before the lock is released
     uint64_t fb = 0;
     f.search_device(d_queries, true, nq, k, d_accept, d_out_ids, d_out_dist, d_out_count, arena, s, &fb, k);
     PXG_HIP(hipStreamSynchronize(s));

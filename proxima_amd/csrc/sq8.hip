@@ -932,7 +932,7 @@ struct Sq8Index {
       if (by_id.count(in_ids[i]) || !seen.emplace(in_ids[i], 1).second)
         raise(PXG_ERR_DUPLICATE_ID, "duplicate vector id " + std::to_string(in_ids[i]), in_ids[i]);
     if (by_id.size() + n > (size_t)UINT32_MAX - 1)
-      raise(PXG_ERR_CAPACITY, "capacity exceeded: slot allocator limit is 4294967295", UINT32_MAX);
+      capacity_error("slot allocator", UINT32_MAX, "capacity exceeded: slot allocator limit is 4294967295");
   }
 
   std::vector<uint32_t> claim_slots(const uint64_t* in_ids, uint64_t n, uint32_t* out_slots) {
@@ -1606,11 +1606,13 @@ int pxg_sq8_search_device(const pxg_sq8* index, const float* d_queries, uint64_t
                           const uint8_t* d_accept, uint64_t* d_out_ids, float* d_out_dist, uint32_t* d_out_count,
                           void* stream) {
   return pxg::guard([&] {
+    pxg::check_k(k);
     Sq8Index& f = const_cast<Sq8Index&>(index->impl);
     std::shared_lock<std::shared_mutex> lk(f.mu);
     pxg::CtxLease ctx(f.pool);
     pxg::CtxScratch sc(ctx.c);
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    pxg::DrainOnUnwind drain{s};
     uint64_t fb = 0;
     f.search_device(d_queries, nullptr, nq, k, rescore, d_accept, d_out_ids, d_out_dist, d_out_count, sc, s, &fb, k);
     PXG_HIP(hipStreamSynchronize(s));

@@ -6,6 +6,7 @@ import glob
 import os
 import re
 
+import numpy as np
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -101,3 +102,62 @@ def test_fixture_configuration_errors_without_gpu(lib):
     assert lib.pxg_fixture_generate(ctypes.c_uint64(0), ctypes.c_uint32(4), ctypes.c_uint64(1), ctypes.c_uint64(2),
                                     ctypes.c_uint64(1), buf, buf) == 7
     assert b"count" in lib.pxg_last_error_message()
+
+
+def test_configuration_errors_carry_parameter_and_reason(lib):
+    # Configuration{parameter, value, reason} (error.rs:110-128) crosses the
+    # ABI as static strings, with the reference's parameter names
+    lib.pxg_last_error_parameter.restype = ctypes.c_char_p
+    lib.pxg_last_error_reason.restype = ctypes.c_char_p
+    a = ctypes.c_uint64()
+    null = ctypes.c_void_p()
+    big_k = (1 << 24) + 1
+    # k is checked before anything else, as flat.rs:153-155 and ivfpq.rs:988 do,
+    # so a search fails on it without an index or a device
+    for fn in ("pxg_flat_search", "pxg_flat_search_device", "pxg_flat_search_device_noalloc",
+               "pxg_ivfpq_search", "pxg_ivfpq_search_device", "pxg_sq8_search", "pxg_sq8_search_codes",
+               "pxg_sq8_search_device"):
+        f = getattr(lib, fn)
+        nargs = len(__import__("proxima_amd._capi", fromlist=["SIGNATURES"]).SIGNATURES[fn][1])
+        args = [null] * nargs
+        args[3] = ctypes.c_uint64(big_k)  # (index, queries, nq, k, ...)
+        args[2] = ctypes.c_uint64(1)
+        assert f(*args) == 7, fn
+        assert lib.pxg_last_error_parameter() == b"k", fn
+        assert lib.pxg_last_error_reason() == b"exceeds the 16777216 result ceiling"
+        assert lib.pxg_last_error_detail(ctypes.byref(a), None, None) == 7 and a.value == big_k
+    # subspaces outside 1..=dim (product.rs:200-206, ivfpq.rs:268-274)
+    books = (ctypes.c_float * 64)()
+    pts = (ctypes.c_float * 64)()
+    inertia, iters = ctypes.c_double(), ctypes.c_uint64()
+    st = lib.pxg_pq_train(pts, ctypes.c_uint64(8), ctypes.c_uint32(8), ctypes.c_uint64(9), ctypes.c_uint64(5),
+                          ctypes.c_uint64(1), books, ctypes.byref(inertia), ctypes.byref(iters))
+    assert st == 7 and lib.pxg_last_error_parameter() == b"subspaces"
+    assert lib.pxg_last_error_reason() == b"must be between 1 and the space dimension"
+    from proxima_amd import _capi
+    cfg = _capi.IvfPqConfigC()
+    assert lib.pxg_ivfpq_config_default(ctypes.c_uint64(16), ctypes.c_uint64(9), ctypes.byref(cfg)) == 0
+    h = ctypes.c_void_p()
+    assert lib.pxg_ivfpq_create(ctypes.c_uint32(8), 0, ctypes.byref(cfg), ctypes.byref(h)) == 7
+    assert lib.pxg_last_error_parameter() == b"subspaces"
+    cfg.subspaces, cfg.nprobe = 4, 17
+    assert lib.pxg_ivfpq_create(ctypes.c_uint32(8), 0, ctypes.byref(cfg), ctypes.byref(h)) == 7
+    assert lib.pxg_last_error_parameter() == b"nprobe"
+    # a later success clears the record
+    assert lib.pxg_ivfpq_config_default(ctypes.c_uint64(16), ctypes.c_uint64(4), ctypes.byref(cfg)) == 0
+    assert lib.pxg_last_error_parameter() == b"" and lib.pxg_last_error_reason() == b""
+
+
+def test_python_mirror_reads_parameter_names():
+    import proxima_amd as px
+    with pytest.raises(px.Configuration) as e:
+        px.ProductQuantizer.train(px.VectorSpace(8, px.Metric.EUCLIDEAN), np.zeros((4, 8), np.float32), px.PqConfig(9))
+    assert e.value.parameter == "subspaces" and e.value.reason == "must be between 1 and the space dimension"
+
+
+def test_rust_ffi_declares_the_header():
+    # crates/proxima-gpu/src/ffi.rs binds exactly the entry points of the header
+    text = open(os.path.join(ROOT, "crates", "proxima-gpu", "src", "ffi.rs")).read()
+    bound = set(re.findall(r"pub\(crate\) fn (pxg_[a-z0-9_]+)\s*\(", text))
+    declared = set(declared_functions())
+    assert bound == declared, (sorted(declared - bound), sorted(bound - declared))
