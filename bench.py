@@ -35,13 +35,22 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def gen_corpus(torch, n, dim, clusters, seed, device):
-    g = torch.Generator(device=device)
-    g.manual_seed(seed)
-    offs = torch.randn((clusters, dim), generator=g, device=device, dtype=torch.float32)
-    x = torch.randn((n, dim), generator=g, device=device, dtype=torch.float32)
-    x += offs[torch.arange(n, device=device) % clusters]
-    return x, offs
+GENERATOR = ("ChaCha8Rng::seed_from_u64(seed) counter-mode stream on the GPU, fixture.rs's Box-Muller "
+             "(pxg_mixture_generate_device / pxg_uniform_generate_device)")
+
+
+def mixture(torch, px, dev, n, dim, clusters, sigma, nq, drawn, seed):
+    """Centres N(0,1), point i = centre[cluster(i)] + sigma * N(0,1), queries the
+    same, from one seeded ChaCha8 stream (cluster(i) = i % clusters, or drawn
+    from the stream)."""
+    x = torch.empty((n, dim), dtype=torch.float32, device=dev)
+    q = torch.empty((nq, dim), dtype=torch.float32, device=dev)
+    px.mixture_generate_device(n, dim, clusters, 1.0, sigma, nq, drawn, seed, x, q)
+    return x, q
+
+
+def inputs_info(seed, recipe):
+    return {"seed": seed, "generator": GENERATOR, "recipe": recipe}
 
 
 def load_traffic(name):
@@ -106,12 +115,8 @@ def bench_c1(args, torch, px, dev):
     100 Gaussian clusters (centres N(0,1), sigma 0.15); 1,000 queries drawn
     fresh from the same mixture, searched as one batch of 1,000."""
     n, dim, nq, k = 100_000, 128, 1000, 10
-    g = torch.Generator(device=dev)
-    g.manual_seed(args.seed + 3)
-    centres = torch.randn((100, dim), generator=g, device=dev)
-    x = (centres[torch.arange(n, device=dev) % 100] + 0.15 * torch.randn((n, dim), generator=g, device=dev)).contiguous()
-    qc = torch.randint(0, 100, (nq,), generator=g, device=dev)
-    q = (centres[qc] + 0.15 * torch.randn((nq, dim), generator=g, device=dev)).contiguous()
+    seed = args.seed + 3
+    x, q = mixture(torch, px, dev, n, dim, 100, 0.15, nq, False, seed)
     ids = np.arange(n, dtype=np.uint64)
     idx = px.FlatIndex(px.VectorSpace(dim, px.Metric.EUCLIDEAN), n)
     idx.insert_device(ids, x)
@@ -141,7 +146,9 @@ def bench_c1(args, torch, px, dev):
         f"{tflops:.1f} TFLOP/s")
     out = {"value": round(nq / step_s, 2), "unit": "queries/s", "ms_per_step": round(step_s * 1e3, 4), "steps": steps,
            "config": {"workload": "flat exact search, Euclidean, 100k x 128 f32 (100 Gaussian clusters, sigma 0.15), "
-                                  "1,000 queries in one batch, k=10", "n": n, "dim": dim, "batch": nq, "k": k},
+                                  "1,000 queries in one batch, k=10", "n": n, "dim": dim, "batch": nq, "k": k,
+                      "inputs": inputs_info(seed, "100 centres N(0,1)^128; x_i = centre[i % 100] + 0.15 N(0,1); "
+                                                  "query q = centre[q % 100] + 0.15 N(0,1)")},
            "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
                         "frac": round(tflops / PEAK_FP32_MFMA_TFLOPS, 4),
                         "traffic": load_traffic("flat_mfma_candidates_c1"),
@@ -179,20 +186,11 @@ def bench_ivfpq(args, torch, px, dev):
     queries from the same mixture in batches of 1,024. Trained on the GPU from
     the default 100,000-vector stride sample (seed 0x1FF9C0D, 25 iterations)."""
     n, dim, B, k, nprobe = args.ivf_n, 128, args.batch, 10, 32
-    g = torch.Generator(device=dev)
-    g.manual_seed(args.seed + 7)
-    centres = torch.randn((1000, dim), generator=g, device=dev)
-    x = torch.empty((n, dim), device=dev)
-    # cluster ids drawn at random: an `i % clusters` layout would alias with
-    # the trainer's deterministic stride sample (stride 100 at 10M) and show it
-    # only 10 of the 1,000 clusters
-    step = 1 << 22
-    for a in range(0, n, step):
-        b = min(n, a + step)
-        cid = torch.randint(0, 1000, (b - a,), generator=g, device=dev)
-        x[a:b] = centres[cid] + 0.15 * torch.randn((b - a, dim), generator=g, device=dev)
-    qc = torch.randint(0, 1000, (args.queries,), generator=g, device=dev)
-    queries = (centres[qc] + 0.15 * torch.randn((args.queries, dim), generator=g, device=dev)).contiguous()
+    seed = args.seed + 7
+    # cluster ids drawn from the stream: an `i % clusters` layout would alias
+    # with the trainer's deterministic stride sample (stride 100 at 10M) and
+    # show it only 10 of the 1,000 clusters
+    x, queries = mixture(torch, px, dev, n, dim, 1000, 0.15, args.queries, True, seed)
     ids = np.arange(n, dtype=np.uint64)
     cfg = px.IvfPqConfig(4096, 16).with_nprobe(nprobe).with_train_threshold(1 << 63)
     idx = px.IvfPqIndex(px.VectorSpace(dim, px.Metric.EUCLIDEAN), cfg)
@@ -232,14 +230,35 @@ def bench_ivfpq(args, torch, px, dev):
     log(f"[bench] ivfpq: {step_s * 1e3:.3f} ms/step = {B / step_s:.0f} QPS; scan {scan_ms:.3f} ms, "
         f"{bytes_per_launch / 1e9:.3f} GB/launch = {gbs:.0f} GB/s")
     # recall@10 against the exact GPU flat index over the same vectors
-    m = 200
+    m = 1024
     flat = px.FlatIndex(px.VectorSpace(dim, px.Metric.EUCLIDEAN), n)
     flat.insert_device(ids, x)
     qh = queries.cpu().numpy()
     ti, _, _ = flat.search_batch(qh[:m], k)
-    gi, gd, gc = idx.search_batch(qh[:m], k)
-    recall = float(np.mean([len(set(ti[i].tolist()) & set(gi[i, :gc[i]].tolist())) / k for i in range(m)]))
     del flat
+
+    def recall_of(gi, gc):
+        return float(np.mean([len(set(ti[i].tolist()) & set(gi[i, :gc[i]].tolist())) / k for i in range(m)]))
+
+    gi, gd, gc = idx.search_batch(qh[:m], k)
+    recall = recall_of(gi, gc)
+    # the reference harness's dial (bench.rs:267-300): recall@10 and throughput
+    # against nprobe, on the same index and batches
+    sweep = []
+    for npb in (1, 4, 16, 32, 64, 256):
+        for s_ in range(2):
+            idx.search_device(batches[s_ % nb], k, oi, od, oc, nprobe=npb, stream=stream)
+        torch.cuda.synchronize()
+        reps = max(3, min(args.ivf_steps, 10))
+        t0 = time.perf_counter()
+        for s_ in range(reps):
+            idx.search_device(batches[s_ % nb], k, oi, od, oc, nprobe=npb, stream=stream)
+        torch.cuda.synchronize()
+        t = (time.perf_counter() - t0) / reps
+        si, _, sc = idx.search_batch(qh[:m], k, nprobe=npb)
+        sweep.append({"nprobe": npb, "queries_per_s": round(B / t, 2), "ms_per_step": round(t * 1e3, 4),
+                      "recall_at_10_vs_exact": round(recall_of(si, sc), 4)})
+        log(f"[bench] ivfpq nprobe {npb}: {t * 1e3:.3f} ms/step = {B / t:.0f} QPS, recall@10 {sweep[-1]['recall_at_10_vs_exact']:.4f}")
     # the same trained parts with an exact rerank of the best 100 ADC
     # candidates (IvfPqConfig::with_rerank, ivfpq.rs:1094-1109)
     rr = 100
@@ -259,7 +278,7 @@ def bench_ivfpq(args, torch, px, dev):
     torch.cuda.synchronize()
     rr_step = (time.perf_counter() - t0) / args.ivf_steps
     ri, _, rc = idx_rr.search_batch(qh[:m], k)
-    recall_rr = float(np.mean([len(set(ti[i].tolist()) & set(ri[i, :rc[i]].tolist())) / k for i in range(m)]))
+    recall_rr = recall_of(ri, rc)
     del idx_rr
     torch.cuda.empty_cache()
     log(f"[bench] ivfpq rerank {rr}: {rr_step * 1e3:.3f} ms/step = {B / rr_step:.0f} QPS, recall@10 {recall_rr:.4f}")
@@ -269,12 +288,16 @@ def bench_ivfpq(args, torch, px, dev):
            "steps": args.ivf_steps,
            "config": {"workload": "IVF-PQ search, Euclidean, 10M x 128 f32, nlist 4096, PQ 16x256, nprobe 32, "
                                   "batch 1024, k=10", "n": n, "dim": dim, "nlist": 4096, "subspaces": 16,
-                      "nprobe": nprobe, "batch": B, "k": k},
+                      "nprobe": nprobe, "batch": B, "k": k,
+                      "inputs": inputs_info(seed, "1000 centres N(0,1)^128; each point and query takes a cluster "
+                                                  "drawn from the stream, + 0.15 N(0,1)")},
            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                         "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": load_traffic("ivf_scan")},
            "kernel": "ivf_scan", "scanned_entries_per_launch": float(np.mean(scanned)),
            "stage_ms": {key: round(float(np.mean([t[key] for t in stages])), 4) for key in stages[0]},
            "train_s": round(train_s, 2), "training_report": rep._asdict(), "recall_at_10_vs_exact": round(recall, 4),
+           "recall_queries": m,
+           "nprobe_sweep": sweep,
            "rerank100": {"value": round(B / rr_step, 2), "unit": "queries/s", "ms_per_step": round(rr_step * 1e3, 4),
                          "recall_at_10_vs_exact": round(recall_rr, 4),
                          "note": "same trained parts, exact rerank of the best 100 ADC candidates per query"},
@@ -317,10 +340,10 @@ def bench_sq8(args, torch, px, dev):
     ~U(-1,1) quantised the same way, batches of 1,024. Score = -(float) of the
     exact int32 code dot product (integer MFMA)."""
     n, dim, B, k = args.sq8_n, 96, args.batch, 10
-    g = torch.Generator(device=dev)
-    g.manual_seed(args.seed + 11)
-    x = torch.rand((n, dim), generator=g, device=dev) * 2.0 - 1.0
-    queries = (torch.rand((args.queries, dim), generator=g, device=dev) * 2.0 - 1.0).contiguous()
+    seed = args.seed + 11
+    xq = torch.empty((n + args.queries, dim), dtype=torch.float32, device=dev)
+    px.uniform_generate_device(n + args.queries, dim, -1.0, 1.0, seed, xq)  # corpus rows, then the queries
+    x, queries = xq[:n], xq[n:]
     ids = np.arange(n, dtype=np.uint64)
     idx = px.Sq8Index(px.VectorSpace(dim, px.Metric.INNER_PRODUCT), capacity=n)
     t0 = time.time()
@@ -373,7 +396,8 @@ def bench_sq8(args, torch, px, dev):
     out = {"value": round(B / step_s, 2), "unit": "queries/s", "ms_per_step": round(step_s * 1e3, 4),
            "steps": args.sq8_steps,
            "config": {"workload": "SQ8 flat search, inner product, 10M x 96 f32 ~U(-1,1) as I8 codes, batch 1024, "
-                                  "k=10", "n": n, "dim": dim, "batch": B, "k": k, "calibration": 100_000},
+                                  "k=10", "n": n, "dim": dim, "batch": B, "k": k, "calibration": 100_000,
+                      "inputs": inputs_info(seed, "U(-1,1) = -1 + 2 gen::<f32>(), corpus rows then the queries")},
            "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": PEAK_INT8_MFMA_TOPS, "unit": "TOP/s",
                         "frac": round(tops / PEAK_INT8_MFMA_TOPS, 4), "traffic": load_traffic("sq8_mfma_scan")},
            "kernel": "sq8_mfma_scan (stage 2)", "fallback_queries": fallbacks,
@@ -419,11 +443,8 @@ def bench_kmeans(args, torch, px, dev):
     the seed, 10 Lloyd iterations; then PQ 16 x 256 trained on the residuals
     (25 iterations per subspace)."""
     n, dim, K, iters = args.km_n, 128, 4096, 10
-    g = torch.Generator(device=dev)
-    g.manual_seed(args.seed + 13)
-    centres = torch.randn((K, dim), generator=g, device=dev)
-    cid = torch.randint(0, K, (n,), generator=g, device=dev)
-    x = (centres[cid] + 0.2 * torch.randn((n, dim), generator=g, device=dev)).contiguous()
+    seed = args.seed + 13
+    x, _ = mixture(torch, px, dev, n, dim, K, 0.2, 0, True, seed)
     seeds = torch.empty((K, dim), device=dev)
     cents = torch.empty((K, dim), device=dev)
     assign = torch.empty(n, dtype=torch.int32, device=dev)
@@ -459,7 +480,10 @@ def bench_kmeans(args, torch, px, dev):
         f"({pq_its} iterations)")
     out = {"value": round(1.0 / per_iter, 3), "unit": "Lloyd iterations/s", "ms_per_iteration": round(per_iter * 1e3, 2),
            "config": {"workload": "k-means 2M x 128 f32 -> 4096, k-means++ then 10 Lloyd iterations; PQ 16x256 on "
-                                  "the residuals", "n": n, "dim": dim, "k": K, "iterations": its},
+                                  "the residuals", "n": n, "dim": dim, "k": K, "iterations": its,
+                      "inputs": inputs_info(seed, "4096 centres N(0,1)^128; each point takes a cluster drawn from "
+                                                  "the stream, + 0.2 N(0,1)"),
+                      "kmeans_seed": args.seed, "pq_seed": args.seed},
            "roofline": {"bound": "mfma", "achieved": round(mfma_tflops, 2), "peak": PEAK_FP32_MFMA_TFLOPS,
                         "unit": "TFLOP/s", "frac": round(mfma_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
                         "traffic": load_traffic("km_mfma_reg"),
@@ -527,7 +551,7 @@ def bench_fixture(args, torch, px, dev):
     gbs = written / t / 1e9
     out = {"value": round(written / t / 2**20, 1), "unit": "MiB/s of f32 generated", "ms_per_run": round(t * 1e3, 3),
            "config": {"workload": "fixture::generate 10M x 128 f32, 1000 clusters, 10,000 queries", "count": n,
-                      "dim": dim, "clusters": clusters, "queries": nq},
+                      "dim": dim, "clusters": clusters, "queries": nq, "seed": args.seed},
            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                         "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
                         "note": "bytes written per run over the host-timed run (3 launches + one host sync); "
@@ -624,12 +648,7 @@ def main():
         return
     n, dim, B = args.n, args.dim, args.batch
     log(f"[bench] generating {n}x{dim} corpus + {args.queries} queries on the GPU")
-    x, offs = gen_corpus(torch, n, dim, 256, args.seed, dev)
-    gq = torch.Generator(device=dev)
-    gq.manual_seed(args.seed + 1)
-    qc = torch.randint(0, 256, (args.queries,), generator=gq, device=dev)
-    queries = torch.randn((args.queries, dim), generator=gq, device=dev) + offs[qc]
-    queries = queries.contiguous()
+    x, queries = mixture(torch, px, dev, n, dim, 256, 1.0, args.queries, False, args.seed)
 
     idx = px.FlatIndex(px.VectorSpace(dim, px.Metric.COSINE), n)
     t0 = time.time()
@@ -784,9 +803,12 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic: N(0,1) + one of 256 N(0,1) cluster offsets, L2-normalised; seeded torch RNG on device",
+        "data": "synthetic: N(0,1) + one of 256 N(0,1) cluster offsets (i % 256), L2-normalised by the index's "
+                "prepare step; ChaCha8 stream from the recorded seed, generated on the GPU",
         "config": {"workload": "flat exact search, cosine, 1M x 768 f32, batch 1024, k=10", "n": n, "dim": dim,
-                   "batch": B, "k": args.k, "metric": "cosine", "queries": args.queries},
+                   "batch": B, "k": args.k, "metric": "cosine", "queries": args.queries,
+                   "inputs": inputs_info(args.seed, "256 centres N(0,1)^768; x_i = centre[i % 256] + N(0,1); "
+                                                    "query q = centre[q % 256] + N(0,1)")},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
                      "traffic": load_traffic("flat_mfma_candidates")},

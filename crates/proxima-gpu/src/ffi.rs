@@ -205,4 +205,7 @@ extern "C" {
         vectors: *mut f32, query_vectors: *mut f32) -> c_int;
     pub(crate) fn pxg_fixture_generate_device(count: u64, dim: u32, clusters: u64, queries: u64, seed: u64,
         d_vectors: *mut f32, d_queries: *mut f32) -> c_int;
+    pub(crate) fn pxg_mixture_generate_device(count: u64, dim: u32, clusters: u64, centre_scale: f32, sigma: f32,
+        queries: u64, drawn_clusters: c_int, seed: u64, d_vectors: *mut f32, d_queries: *mut f32) -> c_int;
+    pub(crate) fn pxg_uniform_generate_device(count: u64, dim: u32, lo: f32, hi: f32, seed: u64, d_out: *mut f32) -> c_int;
 }

@@ -393,6 +393,23 @@ int pxg_fixture_generate(uint64_t count, uint32_t dim, uint64_t clusters, uint64
 int pxg_fixture_generate_device(uint64_t count, uint32_t dim, uint64_t clusters, uint64_t queries, uint64_t seed,
                                 float* d_vectors, float* d_queries);
 
+/* Synthetic inputs of the benchmark configurations. No reference counterpart
+ * (the reference's generator is fixture::generate above): the same
+ * ChaCha8Rng::seed_from_u64(seed) stream and Box-Muller step, drawn in this
+ * order of Gaussian slots (slot g = stream words 2g and 2g+1): clusters x dim
+ * centres = centre_scale * gaussian; when drawn_clusters, one cluster choice
+ * per point then per query, item t from word 2*clusters*dim + t as
+ * (word * clusters) >> 32, the region rounded up to whole slots; count x dim
+ * points = centre[cluster(i)] + sigma * gaussian; queries x dim queries the
+ * same, cluster(q). Without drawn_clusters, cluster(i) = i % clusters and
+ * cluster(q) = q % clusters. Device pointers; returns when written. */
+int pxg_mixture_generate_device(uint64_t count, uint32_t dim, uint64_t clusters, float centre_scale, float sigma,
+                                uint64_t queries, int drawn_clusters, uint64_t seed, float* d_vectors,
+                                float* d_queries);
+/* count x dim values lo + (hi - lo) * gen::<f32>() of stream word t (no
+ * reference counterpart; the uniform configuration's inputs). */
+int pxg_uniform_generate_device(uint64_t count, uint32_t dim, float lo, float hi, uint64_t seed, float* d_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1158,4 +1158,33 @@ def fixture_generate_device(count, dim, clusters, queries, seed, vectors_out, qu
                                             None if queries_out is None else _device_ptr(queries_out)))
 
 
-__all__ += ["fixture_generate", "fixture_generate_device"]
+def _gen_outputs(outs, dim):
+    for t, rows, name in outs:
+        if rows == 0 and t is None:
+            continue
+        if (t is None or not t.is_cuda or str(t.dtype) != "torch.float32" or not t.is_contiguous()
+                or t.numel() < rows * dim):
+            raise ValueError(f"{name} must be a contiguous float32 GPU tensor of at least {rows} x {dim} elements")
+
+
+def mixture_generate_device(count, dim, clusters, centre_scale, sigma, queries, drawn_clusters, seed, vectors_out,
+                            queries_out=None):
+    """The benchmark configurations' Gaussian mixtures (no reference
+    counterpart): centres centre_scale * N(0,1), each point and query its
+    cluster's centre plus sigma * N(0,1), clusters i % C or drawn, all from one
+    seeded ChaCha8 stream with fixture.rs's Box-Muller step. Writes contiguous
+    f32 GPU tensors [count, dim] and [queries, dim]."""
+    _gen_outputs(((vectors_out, count, "vectors_out"), (queries_out, queries, "queries_out")), dim)
+    _check(_lib.pxg_mixture_generate_device(count, dim, clusters, float(centre_scale), float(sigma), queries,
+                                            1 if drawn_clusters else 0, seed, _device_ptr(vectors_out),
+                                            _device_ptr(queries_out) if queries else None))
+
+
+def uniform_generate_device(count, dim, lo, hi, seed, out):
+    """count x dim values lo + (hi - lo) * gen::<f32>() from a seeded ChaCha8
+    stream, into a contiguous f32 GPU tensor (no reference counterpart)."""
+    _gen_outputs(((out, count, "out"),), dim)
+    _check(_lib.pxg_uniform_generate_device(count, dim, float(lo), float(hi), seed, _device_ptr(out)))
+
+
+__all__ += ["fixture_generate", "fixture_generate_device", "mixture_generate_device", "uniform_generate_device"]

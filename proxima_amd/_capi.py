@@ -130,6 +130,8 @@ SIGNATURES = {
     "pxg_pq_train_device": (_i32, [_vp, _u64, _u32, _u64, _u64, _u64, _vp, _P(_f64), _P(_u64)]),
     "pxg_fixture_generate": (_i32, [_u64, _u32, _u64, _u64, _u64, _vp, _vp]),
     "pxg_fixture_generate_device": (_i32, [_u64, _u32, _u64, _u64, _u64, _vp, _vp]),
+    "pxg_mixture_generate_device": (_i32, [_u64, _u32, _u64, _f32, _f32, _u64, _i32, _u64, _vp, _vp]),
+    "pxg_uniform_generate_device": (_i32, [_u64, _u32, _f32, _f32, _u64, _vp]),
     # scalar quantizer / SQ8 index
     "pxg_sq_train": (_i32, [_vp, _u64, _u32, _i32, _vp, _vp, _vp]),
     "pxg_sq_encode": (_i32, [_vp, _u64, _u32, _i32, _i32, _vp, _vp, _vp]),

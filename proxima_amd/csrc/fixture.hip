@@ -141,6 +141,136 @@ void fixture_generate_device(uint64_t count, uint32_t dim, uint64_t clusters, ui
   PXG_HIP(hipStreamSynchronize(s));
 }
 
+// ---------------------------------------------------------------------------
+// Synthetic inputs of the benchmark configurations (no reference
+// counterpart; the reference's own generator is fixture::generate above).
+// The same counter-mode ChaCha8Rng::seed_from_u64(seed) stream and the same
+// Box-Muller step, in this order of Gaussian slots (slot g = words 2g, 2g+1):
+//   [0, C*dim)                  centres, centre_scale * gaussian
+//   [gB, gB + ceil(items / 2))  cluster choices, when drawn: item t (points
+//                               first, then queries) takes word 2 gB + t as
+//                               c = (word * C) >> 32
+//   [gC, gC + count*dim)        points:  centre[cluster(i)] + sigma * gaussian
+//   [gD, gD + queries*dim)      queries: centre[cluster(q)] + sigma * gaussian
+// with cluster(i) = i % C (points) and q % C (queries) when not drawn.
+// ---------------------------------------------------------------------------
+__global__ void mx_centres(const uint32_t* __restrict__ key, uint64_t total, float scale, float* __restrict__ centres) {
+  uint64_t first;
+  float v[8];
+  if (!fx_values(key, 0, total, first, v)) return;
+#pragma unroll
+  for (int u = 0; u < 8; ++u)
+    if (first + u < total) centres[first + u] = v[u] * scale;
+}
+
+// cluster choices of `items` items from word 2 gB on: one 16-word block per thread
+__global__ void mx_choices(const uint32_t* __restrict__ key, uint64_t w0, uint64_t items, uint64_t clusters,
+                           uint32_t* __restrict__ cl) {
+  const uint64_t blk = w0 / 16 + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (blk * 16 >= w0 + items) return;
+  uint32_t k[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) k[i] = key[i];
+  uint32_t w[16];
+  ChaCha8::block(k, blk, w);
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const uint64_t pos = blk * 16 + u;
+    if (pos >= w0 && pos < w0 + items) cl[pos - w0] = (uint32_t)(((uint64_t)w[u] * clusters) >> 32);
+  }
+}
+
+// Item t = i * dim + d of a region at Gaussian slot `base`: centre row of
+// cluster(i) plus sigma times the Gaussian; cl (cluster per item) or i % C.
+__global__ void mx_rows(const uint32_t* __restrict__ key, uint64_t base, uint64_t total, uint32_t dim,
+                        uint64_t clusters, const uint32_t* __restrict__ cl, float sigma,
+                        const float* __restrict__ centres, float* __restrict__ out) {
+  uint64_t first;
+  float v[8];
+  if (!fx_values(key, base, base + total, first, v)) return;
+  const uint64_t t0 = (first > base ? first : base) - base;
+  uint64_t i = t0 / dim;
+  uint32_t d = (uint32_t)(t0 - i * dim);
+  const float* crow = centres + (cl ? (uint64_t)cl[i] : i % clusters) * dim;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const uint64_t g = first + u;
+    if (g >= base && g < base + total) {
+      out[g - base] = crow[d] + sigma * v[u];
+      if (++d == dim) {
+        d = 0;
+        ++i;
+        if (g + 1 < base + total) crow = centres + (cl ? (uint64_t)cl[i] : i % clusters) * dim;
+      }
+    }
+  }
+}
+
+// value t = lo + (hi - lo) * gen::<f32>() of word t: one 16-word block per thread
+__global__ void mx_uniform(const uint32_t* __restrict__ key, uint64_t total, float lo, float hi,
+                           float* __restrict__ out) {
+  const uint64_t blk = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (blk * 16 >= total) return;
+  uint32_t k[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) k[i] = key[i];
+  uint32_t w[16];
+  ChaCha8::block(k, blk, w);
+  const float span = hi - lo;
+#pragma unroll
+  for (int u = 0; u < 16; ++u)
+    if (blk * 16 + u < total) out[blk * 16 + u] = lo + span * fx_u01(w[u]);
+}
+
+void mixture_generate_device(uint64_t count, uint32_t dim, uint64_t clusters, float centre_scale, float sigma,
+                             uint64_t queries, int drawn, uint64_t seed, float* d_vectors, float* d_queries,
+                             hipStream_t s) {
+  const ChaCha8 rng(seed);
+  DevBuf<uint32_t> key(8);
+  const uint64_t cd = clusters * dim, nd = count * dim, qd = queries * dim, items = count + queries;
+  DevBuf<float> centres(std::max<uint64_t>(cd, 1));
+  DevBuf<uint32_t> cl(drawn ? std::max<uint64_t>(items, 1) : 0);
+  PXG_HIP(hipMemcpyAsync(key.p, rng.key, 32, hipMemcpyHostToDevice, s));
+  const uint64_t gB = cd, gC = gB + (drawn ? (items + 1) / 2 : 0), gD = gC + nd;
+  dim3 g;
+  if (cd) {
+    launch_blocks(0, cd, g);
+    hipLaunchKernelGGL(mx_centres, g, dim3(256), 0, s, key.p, cd, centre_scale, centres.p);
+  }
+  if (drawn && items) {
+    const uint64_t blocks = (2 * gB + items + 15) / 16 - (2 * gB) / 16;
+    hipLaunchKernelGGL(mx_choices, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0, s, key.p, 2 * gB, items,
+                       clusters, cl.p);
+  }
+  if (nd) {
+    launch_blocks(gC, gC + nd, g);
+    hipLaunchKernelGGL(mx_rows, g, dim3(256), 0, s, key.p, gC, nd, dim, clusters, drawn ? cl.p : nullptr, sigma,
+                       centres.p, d_vectors);
+  }
+  if (qd) {
+    launch_blocks(gD, gD + qd, g);
+    hipLaunchKernelGGL(mx_rows, g, dim3(256), 0, s, key.p, gD, qd, dim, clusters,
+                       drawn ? cl.p + count : nullptr, sigma, centres.p, d_queries);
+  }
+  PXG_HIP(hipGetLastError());
+  PXG_HIP(hipStreamSynchronize(s));
+}
+
+void uniform_generate_device(uint64_t count, uint32_t dim, float lo, float hi, uint64_t seed, float* d_out,
+                             hipStream_t s) {
+  const ChaCha8 rng(seed);
+  DevBuf<uint32_t> key(8);
+  const uint64_t total = count * dim;
+  PXG_HIP(hipMemcpyAsync(key.p, rng.key, 32, hipMemcpyHostToDevice, s));
+  if (total) {
+    const uint64_t blocks = (total + 15) / 16;
+    hipLaunchKernelGGL(mx_uniform, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0, s, key.p, total, lo, hi,
+                       d_out);
+  }
+  PXG_HIP(hipGetLastError());
+  PXG_HIP(hipStreamSynchronize(s));
+}
+
 }  // namespace pxg
 
 extern "C" {
@@ -164,6 +294,29 @@ int pxg_fixture_generate_device(uint64_t count, uint32_t dim, uint64_t clusters,
     fixture_check(count, clusters, queries);
     FxStream st;
     pxg::fixture_generate_device(count, dim, clusters, queries, seed, d_vectors, d_queries, st.s);
+  });
+}
+
+int pxg_mixture_generate_device(uint64_t count, uint32_t dim, uint64_t clusters, float centre_scale, float sigma,
+                                uint64_t queries, int drawn_clusters, uint64_t seed, float* d_vectors,
+                                float* d_queries) {
+  return pxg::guard([&] {
+    if (count + queries > 0 && clusters == 0)
+      pxg::config_error("clusters", 0, "every point and query belongs to a cluster");
+    if (clusters > 0xFFFFFFFFull) pxg::config_error("clusters", clusters, "at most 2^32 - 1 clusters");
+    if (!std::isfinite(centre_scale) || !std::isfinite(sigma))
+      pxg::config_error("sigma", 0, "centre_scale and sigma must be finite");
+    FxStream st;
+    pxg::mixture_generate_device(count, dim, clusters, centre_scale, sigma, queries, drawn_clusters ? 1 : 0, seed,
+                                 d_vectors, d_queries, st.s);
+  });
+}
+
+int pxg_uniform_generate_device(uint64_t count, uint32_t dim, float lo, float hi, uint64_t seed, float* d_out) {
+  return pxg::guard([&] {
+    if (!std::isfinite(lo) || !std::isfinite(hi) || !(lo < hi)) pxg::config_error("hi", 0, "need finite lo < hi");
+    FxStream st;
+    pxg::uniform_generate_device(count, dim, lo, hi, seed, d_out, st.s);
   });
 }
 

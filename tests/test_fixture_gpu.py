@@ -73,3 +73,73 @@ def test_device_entry_point_matches_host(gpu):
     assert np.array_equal(dv.cpu().numpy(), v) and np.array_equal(dq.cpu().numpy(), q)
     with pytest.raises(ValueError):
         px.fixture_generate_device(4096, 24, 30, 100, 9, dv[:10], dq)
+
+
+# --- the benchmark configurations' inputs (no reference counterpart) ---------------
+def _stream_words(seed, n):
+    r = orc.Rng(seed)
+    return np.array([r.next_u32() for _ in range(n)], np.uint64)
+
+
+def _u01(w):
+    return ((w >> 8).astype(np.float64) * 2.0 ** -24).astype(np.float32)
+
+
+def _gaussians(words):
+    u1 = np.maximum(_u01(words[0::2]), np.float32(1.17549435e-38))
+    u2 = _u01(words[1::2])
+    ln = np.log(u1.astype(np.float64)).astype(np.float32)
+    a = (np.float32(6.2831855) * u2).astype(np.float32)
+    c = np.cos(a.astype(np.float64)).astype(np.float32)
+    return (np.sqrt((np.float32(-2.0) * ln).astype(np.float32)) * c).astype(np.float32)
+
+
+@pytest.mark.parametrize("drawn", [False, True])
+def test_mixture_matches_its_stated_stream(gpu, drawn):
+    import torch
+    px = gpu
+    count, dim, clusters, queries, seed, scale, sigma = 301, 12, 7, 33, 0x9E3779B9, 1.0, 0.15
+    cd, items = clusters * dim, count + queries
+    gB = cd
+    gC = gB + ((items + 1) // 2 if drawn else 0)
+    gD = gC + count * dim
+    words = _stream_words(seed, 2 * (gD + queries * dim))
+    g = _gaussians(words)
+    centres = (g[:cd] * np.float32(scale)).reshape(clusters, dim)
+    if drawn:
+        cw = words[2 * gB:2 * gB + items]
+        cl = ((cw * np.uint64(clusters)) >> np.uint64(32)).astype(np.int64)
+    else:
+        cl = np.concatenate([np.arange(count) % clusters, np.arange(queries) % clusters])
+    want_v = centres[cl[:count]] + np.float32(sigma) * g[gC:gD].reshape(count, dim)
+    want_q = centres[cl[count:]] + np.float32(sigma) * g[gD:].reshape(queries, dim)
+    v = torch.empty((count, dim), dtype=torch.float32, device="cuda")
+    q = torch.empty((queries, dim), dtype=torch.float32, device="cuda")
+    px.mixture_generate_device(count, dim, clusters, scale, sigma, queries, drawn, seed, v, q)
+    for got, want in ((v.cpu().numpy(), want_v), (q.cpu().numpy(), want_q)):
+        same, ok, worst = close(got, want)
+        assert ok and same > 0.8, (same, worst)
+    if drawn:
+        assert len(set(cl.tolist())) == clusters  # drawn choices reach every cluster
+    # the same seed gives the same bytes; another seed other bytes
+    v2 = torch.empty_like(v)
+    q2 = torch.empty_like(q)
+    px.mixture_generate_device(count, dim, clusters, scale, sigma, queries, drawn, seed, v2, q2)
+    assert torch.equal(v, v2) and torch.equal(q, q2)
+    px.mixture_generate_device(count, dim, clusters, scale, sigma, queries, drawn, seed + 1, v2, q2)
+    assert not torch.equal(v, v2)
+
+
+def test_uniform_matches_its_stated_stream(gpu):
+    import torch
+    px = gpu
+    count, dim, seed = 1000, 96, 0x9E3779B9 + 11
+    w = _stream_words(seed, count * dim)
+    want = (np.float32(-1.0) + np.float32(2.0) * _u01(w)).astype(np.float32).reshape(count, dim)
+    out = torch.empty((count, dim), dtype=torch.float32, device="cuda")
+    px.uniform_generate_device(count, dim, -1.0, 1.0, seed, out)
+    got = out.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert got.min() >= -1.0 and got.max() < 1.0
+    with pytest.raises(ValueError):
+        px.uniform_generate_device(count, dim, -1.0, 1.0, seed, out[:10])

@@ -86,3 +86,28 @@ def test_noalloc_wide_k_and_capacity(gpu):
     assert "no-allocation scratch" in px._lib.pxg_last_error_message().decode()
     # still serves afterwards
     _same(_run(px, na, idx, q, 10), _run(px, ref, idx, q, 10))
+
+
+def test_noalloc_capacity_after_queued_stages(gpu):
+    # the prepared queries (50000 x 128 x 4 bytes) and the per-query regions fit
+    # the 128 MiB, but one split of candidate buffers (50000 x 512 x 8 bytes at
+    # k = 100) does not: the call fails with Capacity after its first stages
+    # were queued, waits for them, and the next calls are served correctly
+    import torch
+    px = gpu
+    na = _noalloc(px)
+    rng = np.random.default_rng(9)
+    n, dim = 8192, 128
+    data = rng.standard_normal((n, dim)).astype(np.float32)
+    idx = px.FlatIndex(px.VectorSpace(dim, 0), n)
+    idx.insert_batch(np.arange(n, dtype=np.uint64), data)
+    idx.set_search_mode(1)
+    big = torch.from_numpy(rng.standard_normal((50_000, dim)).astype(np.float32)).cuda()
+    st = _run(px, na, idx, big, 100)[0]
+    assert st == 4  # PXG_ERR_CAPACITY
+    px._lib.pxg_last_error_parameter.restype = C.c_char_p
+    assert px._lib.pxg_last_error_parameter() == b"no-allocation scratch"
+    ref = px._lib.pxg_flat_search_device
+    q = big[:3000].contiguous()
+    _same(_run(px, na, idx, q, 100), _run(px, ref, idx, q, 100))
+    _same(_run(px, na, idx, q[:64], 10), _run(px, ref, idx, q[:64], 10))
