@@ -34,7 +34,6 @@
 #include <cstdio>
 #include <cstdlib>
 #include <string>
-#include <thread>
 #include <exception>
 #include <type_traits>
 #include <vector>
@@ -111,11 +110,11 @@ __device__ inline float point_dist(const float* x, const float* __restrict__ c, 
 }
 
 template <int D, bool UNR>
-__global__ __launch_bounds__(256) void km_assign(const float* __restrict__ P, int ldp, const uint32_t* __restrict__ rows,
+__device__ __forceinline__ void km_assign_body(const float* __restrict__ P, int ldp, const uint32_t* __restrict__ rows,
                                                  int n, int dim, const float* __restrict__ C, int ldc, int k,
-                                                 uint32_t* __restrict__ assign, float* __restrict__ dist, int vec4) {
+                                                 uint32_t* __restrict__ assign, float* __restrict__ dist, int vec4, int bx) {
   __shared__ float cs[KM_LDS_FLOATS];
-  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int i = bx * 256 + threadIdx.x;
   const bool valid = i < n;
   const size_t row = valid ? (rows ? rows[i] : (uint32_t)i) : 0;
   const float* pr = P + row * ldp;
@@ -171,6 +170,13 @@ __global__ __launch_bounds__(256) void km_assign(const float* __restrict__ P, in
     assign[i] = (uint32_t)bi;
     if (dist) dist[i] = bd;
   }
+}
+
+template <int D, bool UNR>
+__global__ __launch_bounds__(256) void km_assign(const float* __restrict__ P, int ldp, const uint32_t* __restrict__ rows,
+                                                 int n, int dim, const float* __restrict__ C, int ldc, int k,
+                                                 uint32_t* __restrict__ assign, float* __restrict__ dist, int vec4) {
+  km_assign_body<D, UNR>(P, ldp, rows, n, dim, C, ldc, k, assign, dist, vec4, blockIdx.x);
 }
 
 template <bool UNR>
@@ -1051,16 +1057,21 @@ __device__ inline SumCert cert_of(float x) {
 }
 
 // per-256-value block certificates of v[0..n)
-__global__ __launch_bounds__(256) void f64_partials(const float* __restrict__ v, int n, double* __restrict__ ps,
-                                                    double* __restrict__ pa, int* __restrict__ pe) {
+__device__ __forceinline__ void f64_partials_body(const float* __restrict__ v, int n, double* __restrict__ ps,
+                                                    double* __restrict__ pa, int* __restrict__ pe, int bx) {
   __shared__ SumCert sh[4];
-  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int i = bx * 256 + threadIdx.x;
   const SumCert r = block_cert_256(cert_of(i < n ? v[i] : 0.0f), sh);
   if (threadIdx.x == 0) {
-    ps[blockIdx.x] = r.s;
-    pa[blockIdx.x] = r.a;
-    pe[blockIdx.x] = r.e;
+    ps[bx] = r.s;
+    pa[bx] = r.a;
+    pe[bx] = r.e;
   }
+}
+
+__global__ __launch_bounds__(256) void f64_partials(const float* __restrict__ v, int n, double* __restrict__ ps,
+                                                    double* __restrict__ pa, int* __restrict__ pe) {
+  f64_partials_body(v, n, ps, pa, pe, blockIdx.x);
 }
 
 // Sequential sum of v[0..n) by one block: all threads stage 4096 values in
@@ -1081,7 +1092,7 @@ __device__ inline double seq_sum_block(const float* __restrict__ v, int n, float
 // Total of v from its block certificates (one 1024-thread block): exact when
 // the certificate holds, else sequential (n <= SEQ_SUM_LIMIT) or the fixed
 // order. out[0] = total, out[1] = 1.0 if it equals the sequential sum.
-__global__ __launch_bounds__(1024) void f64_total(const float* __restrict__ v, int n, const double* __restrict__ ps,
+__device__ __forceinline__ void f64_total_body(const float* __restrict__ v, int n, const double* __restrict__ ps,
                                                   const double* __restrict__ pa, const int* __restrict__ pe, int nb,
                                                   double* __restrict__ out) {
   __shared__ double ss[1024], sa[1024];
@@ -1114,6 +1125,12 @@ __global__ __launch_bounds__(1024) void f64_total(const float* __restrict__ v, i
     out[0] = total;
     out[1] = (exact || n <= (int)SEQ_SUM_LIMIT) ? 1.0 : 0.0;
   }
+}
+
+__global__ __launch_bounds__(1024) void f64_total(const float* __restrict__ v, int n, const double* __restrict__ ps,
+                                                  const double* __restrict__ pa, const int* __restrict__ pe, int nb,
+                                                  double* __restrict__ out) {
+  f64_total_body(v, n, ps, pa, pe, nb, out);
 }
 
 struct F64Sum {
@@ -1151,15 +1168,15 @@ constexpr int PP_ROWS = 256;  // points per km_pp_round block
 // Sequential squared (kmeans.rs:234-241) of each of the block's 256 points to
 // centre c: the block's rows are staged through LDS 32 coordinates at a time
 // (coalesced loads), each thread then runs its point's chain.
-__global__ __launch_bounds__(256) void km_pp_round(const float* __restrict__ P, int ldp, int n, int dim,
+__device__ __forceinline__ void km_pp_round_body(const float* __restrict__ P, int ldp, int n, int dim,
                                                    const float* __restrict__ c, float* __restrict__ ns, int init,
-                                                   double* __restrict__ ps, int* __restrict__ pe, int vec4) {
+                                                   double* __restrict__ ps, int* __restrict__ pe, int vec4, int bx) {
   constexpr int CS = 2048;  // centre coordinates staged in LDS
   __shared__ float tile[PP_ROWS * 33];
   __shared__ float cs[CS];
   __shared__ SumCert sh[4];
   const int t = threadIdx.x;
-  const int r0 = blockIdx.x * PP_ROWS;
+  const int r0 = bx * PP_ROWS;
   const bool staged_c = dim <= CS;
   if (staged_c)
     for (int j = t; j < dim; j += 256) cs[j] = c[j];
@@ -1219,9 +1236,15 @@ __global__ __launch_bounds__(256) void km_pp_round(const float* __restrict__ P, 
   }
   const SumCert r = block_cert_256(cert_of(nv), sh);
   if (t == 0) {
-    ps[blockIdx.x] = r.s;
-    pe[blockIdx.x] = r.e;
+    ps[bx] = r.s;
+    pe[bx] = r.e;
   }
+}
+
+__global__ __launch_bounds__(256) void km_pp_round(const float* __restrict__ P, int ldp, int n, int dim,
+                                                   const float* __restrict__ c, float* __restrict__ ns, int init,
+                                                   double* __restrict__ ps, int* __restrict__ pe, int vec4) {
+  km_pp_round_body(P, ldp, n, dim, c, ns, init, ps, pe, vec4, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -1408,7 +1431,7 @@ __device__ inline double wave_incl_scan_f64(double v, int lane) {
 // The prefix sums are wave scans joined through the 16 (or 4) wave totals:
 // under the certificate every order gives the exact sums, and otherwise this
 // is the fixed parallel order.
-__global__ __launch_bounds__(1024) void km_pp_pick(const float* __restrict__ P, int ldp, int n, int dim,
+__device__ __forceinline__ void km_pp_pick_body(const float* __restrict__ P, int ldp, int n, int dim,
                                                    const float* __restrict__ ns, const double* __restrict__ ps,
                                                    const int* __restrict__ pe, int nb, ChaCha8* __restrict__ grng,
                                                    float* __restrict__ row_out, int* __restrict__ status,
@@ -1534,6 +1557,14 @@ __global__ __launch_bounds__(1024) void km_pp_pick(const float* __restrict__ P, 
     *grng = rng;
     if (picked_out) *picked_out = picked;
   }
+}
+
+__global__ __launch_bounds__(1024) void km_pp_pick(const float* __restrict__ P, int ldp, int n, int dim,
+                                                   const float* __restrict__ ns, const double* __restrict__ ps,
+                                                   const int* __restrict__ pe, int nb, ChaCha8* __restrict__ grng,
+                                                   float* __restrict__ row_out, int* __restrict__ status,
+                                                   int* __restrict__ inexact, int* __restrict__ picked_out) {
+  km_pp_pick_body(P, ldp, n, dim, ns, ps, pe, nb, grng, row_out, status, inexact, picked_out);
 }
 
 __global__ void copy_row(const float* __restrict__ src, int ld_src, size_t row, int dim, float* __restrict__ dst) {
@@ -1666,18 +1697,18 @@ __global__ __launch_bounds__(256) void km_changed_counts(const uint32_t* __restr
 // thread per coordinate redoes the sum sequentially. The mean is
 // (float)(sum * (1.0 / count)).
 template <int JW, int NT>
-__global__ __launch_bounds__(NT) void km_sums(const float* __restrict__ P, int ldp, int dim,
+__device__ __forceinline__ void km_sums_body(const float* __restrict__ P, int ldp, int dim,
                                                const uint32_t* __restrict__ members,
                                                const uint32_t* __restrict__ offsets,
-                                               const uint32_t* __restrict__ counts, int k, float* __restrict__ newc) {
+                                               const uint32_t* __restrict__ counts, int k, float* __restrict__ newc, int bx, int by) {
   constexpr int G = NT / JW, ROWS = 2048 / JW;  // 8 KiB of staged values (the sequential redo)
   __shared__ double ss[G][JW], sa[G][JW];
   __shared__ int se[G][JW];
   __shared__ float stage[ROWS][JW];
   __shared__ int redo;
-  const int c = blockIdx.x;
+  const int c = bx;
   const int jl = threadIdx.x % JW, g = threadIdx.x / JW;
-  const int j = blockIdx.y * JW + jl;
+  const int j = by * JW + jl;
   const uint32_t cnt = counts[c];
   if (cnt == 0) return;
   const uint32_t off = offsets[c];
@@ -1736,6 +1767,14 @@ __global__ __launch_bounds__(NT) void km_sums(const float* __restrict__ P, int l
     const double inv = 1.0 / (double)cnt;
     newc[(size_t)c * dim + j] = (float)(s * inv);
   }
+}
+
+template <int JW, int NT>
+__global__ __launch_bounds__(NT) void km_sums(const float* __restrict__ P, int ldp, int dim,
+                                               const uint32_t* __restrict__ members,
+                                               const uint32_t* __restrict__ offsets,
+                                               const uint32_t* __restrict__ counts, int k, float* __restrict__ newc) {
+  km_sums_body<JW, NT>(P, ldp, dim, members, offsets, counts, k, newc, blockIdx.x, blockIdx.y);
 }
 
 // farthest_point (kmeans.rs:215-226): the first point with the largest
@@ -2126,27 +2165,416 @@ __global__ void pad_book(float* __restrict__ book, int produced, int w) {
   book[r * w + (t % w)] = book[(produced - 1) * w + (t % w)];
 }
 
+// ---------------------------------------------------------------------------
+// Product-quantizer training, every subspace in one launch per step
+// ---------------------------------------------------------------------------
+// ProductQuantizer::train (product.rs:198-296) runs kmeans on each subspace
+// in turn with one generator advanced across them. Only the k-means++
+// seedings draw from it (kmeans.rs:146-194; Lloyd and the farthest-point
+// reseeds draw nothing), and in the common case a seeding's draws do not
+// depend on the data: one gen_range over the points, then one 64-bit word
+// per further centroid (gen_range_f64 accepts its first word unless the
+// product rounds up to the total; only a zero total takes a gen_range
+// instead). So the host predicts each subspace's starting state, and every
+// step below covers all subspaces in one launch from one host thread:
+// blockIdx.y (blockIdx.x for the one-block kernels) names the subspace, and
+// each subspace's kernels are the single-run kernels' bodies over its own
+// arrays. After the seedings each subspace's final generator state is
+// compared with the next one's predicted start; from the first that differs,
+// the later subspaces are trained again in order from the true state by the
+// single-run path, so every codebook is the sequential run's. Empty clusters
+// (rare) are reseeded per subspace with the single-run farthest-point pass.
+
+// One subspace of a batched training: its projected points (n x w, row
+// stride w) and its working arrays.
+struct PqSub {
+  const float* P;
+  float* cents;       // k x w, the centroid array (updated in place per iteration)
+  float* newc;        // k x w, the next iteration's array while it is built
+  float* ns;          // n: k-means++ nearest squared distances
+  double* ps;         // k-means++ per-block sums and exponents
+  int* pe;
+  ChaCha8* rng;       // the subspace's generator
+  uint32_t* assign;   // n
+  uint32_t* prev;     // n: the previous assignment (kmeans.rs:93-96)
+  float* dist;        // n: the assignment's distances
+  uint32_t* counts;   // k
+  uint32_t* offsets;  // k: each cluster's first member in the shared member array
+  double* fps;        // per-256-point certificates of dist (the inertia)
+  double* fpa;
+  int* fpe;
+  double* total;      // [2]: inertia, 1.0 when it equals the sequential sum
+  int* flags;         // [0] non-finite k-means++ total, [1] inexact picks, [2] assignment changed
+  int w;
+  int active;         // still iterating
+};
+
+__global__ void pqb_first(const PqSub* __restrict__ S, const uint64_t* __restrict__ first) {
+  const PqSub& q = S[blockIdx.x];
+  for (int j = threadIdx.x; j < q.w; j += blockDim.x) q.cents[j] = q.P[first[blockIdx.x] * q.w + j];
+}
+
+__global__ __launch_bounds__(256) void pqb_pp_round(const PqSub* __restrict__ S, int n, int chosen, int init,
+                                                    int vec4) {
+  const PqSub& q = S[blockIdx.y];
+  km_pp_round_body(q.P, q.w, n, q.w, q.cents + (size_t)chosen * q.w, q.ns, init, q.ps, q.pe, vec4, blockIdx.x);
+}
+
+// The same round for narrow equal-width subspaces (W a multiple of 4, rows
+// 16-byte aligned): one thread per point reads its row straight into
+// registers (the centre row is uniform over the block), so a wave's loads
+// cover 64 consecutive rows.
+template <int W>
+__global__ __launch_bounds__(256) void pqb_pp_round_w(const PqSub* __restrict__ S, int n, int chosen, int init) {
+  __shared__ SumCert sh[4];
+  const PqSub& q = S[blockIdx.y];
+  const int i = blockIdx.x * PP_ROWS + threadIdx.x;
+  const float* c = q.cents + (size_t)chosen * W;
+  float nv = 0.0f;
+  if (i < n) {
+    const float4* pr = reinterpret_cast<const float4*>(q.P + (size_t)i * W);
+    float x[W];
+#pragma unroll
+    for (int u = 0; u < W / 4; ++u) {
+      const float4 v = pr[u];
+      x[4 * u] = v.x;
+      x[4 * u + 1] = v.y;
+      x[4 * u + 2] = v.z;
+      x[4 * u + 3] = v.w;
+    }
+    float sum = 0.0f;  // squared(), kmeans.rs:234-241
+#pragma unroll
+    for (int j = 0; j < W; ++j) {
+      const float d = x[j] - c[j];
+      sum += d * d;
+    }
+    nv = sum;
+    if (!init) {
+      const float cur = q.ns[i];
+      if (!(sum < cur)) nv = cur;
+    }
+    q.ns[i] = nv;
+  }
+  const SumCert r = block_cert_256(cert_of(nv), sh);
+  if (threadIdx.x == 0) {
+    q.ps[blockIdx.x] = r.s;
+    q.pe[blockIdx.x] = r.e;
+  }
+}
+
+__global__ __launch_bounds__(1024) void pqb_pp_pick(const PqSub* __restrict__ S, int n, int nb, int chosen) {
+  const PqSub& q = S[blockIdx.x];
+  km_pp_pick_body(q.P, q.w, n, q.w, q.ns, q.ps, q.pe, nb, q.rng, q.cents + (size_t)chosen * q.w, q.flags,
+                  q.flags + 1, nullptr);
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void pqb_assign(const PqSub* __restrict__ S, int n, int k, int vec4) {
+  const PqSub& q = S[blockIdx.y];
+  if (!q.active) return;  // uniform over the block
+  km_assign_body<D, false>(q.P, q.w, nullptr, n, q.w, q.cents, q.w, k, q.assign, q.dist, vec4, blockIdx.x);
+}
+
+__global__ __launch_bounds__(256) void pqb_partials(const PqSub* __restrict__ S, int n) {
+  const PqSub& q = S[blockIdx.y];
+  if (!q.active) return;
+  f64_partials_body(q.dist, n, q.fps, q.fpa, q.fpe, blockIdx.x);
+}
+
+__global__ __launch_bounds__(1024) void pqb_total(const PqSub* __restrict__ S, int n, int nb) {
+  const PqSub& q = S[blockIdx.x];
+  if (!q.active) return;
+  f64_total_body(q.dist, n, q.fps, q.fpa, q.fpe, nb, q.total);
+}
+
+// km_changed_counts per subspace, plus the sort keys (subspace, cluster) and
+// point indices of the shared member sort: 2048 points per block.
+__global__ __launch_bounds__(256) void pqb_changed_counts(const PqSub* __restrict__ S, int n, int k,
+                                                          uint32_t* __restrict__ keys, uint32_t* __restrict__ vals) {
+  __shared__ uint32_t hist[256];
+  __shared__ int any;
+  const int sub = blockIdx.y;
+  const PqSub& q = S[sub];
+  const size_t base = (size_t)sub * n;
+  const bool active = q.active;
+  for (int c = threadIdx.x; c < k; c += 256) hist[c] = 0;
+  if (threadIdx.x == 0) any = 0;
+  __syncthreads();
+  const int end = min(n, (int)(blockIdx.x + 1) * 2048);
+  for (int i = blockIdx.x * 2048 + threadIdx.x; i < end; i += 256) {
+    const uint32_t c = active ? q.assign[i] : 0u;
+    if (active) {
+      if (q.prev[i] != c) {
+        any = 1;
+        q.prev[i] = c;
+      }
+      atomicAdd(&hist[c], 1u);
+    }
+    keys[base + i] = (uint32_t)sub * (uint32_t)k + c;
+    vals[base + i] = (uint32_t)i;
+  }
+  __syncthreads();
+  if (!active) return;
+  for (int c = threadIdx.x; c < k; c += 256)
+    if (hist[c]) atomicAdd(&q.counts[c], hist[c]);
+  if (threadIdx.x == 0 && any) q.flags[2] = 1;
+}
+
+template <int JW, int NT>
+__global__ __launch_bounds__(NT) void pqb_sums(const PqSub* __restrict__ S, int k,
+                                               const uint32_t* __restrict__ members) {
+  const PqSub& q = S[blockIdx.y];
+  if (!q.active) return;
+  km_sums_body<JW, NT>(q.P, q.w, q.w, members, q.offsets, q.counts, k, q.newc, blockIdx.x, 0);
+}
+
+__global__ void pqb_reset_changed(const PqSub* __restrict__ S, int M) {
+  for (int q = threadIdx.x; q < M; q += blockDim.x) S[q].flags[2] = 0;
+}
+
+// newc = cents before the means are written: the rows of empty clusters are
+// replaced by the reseeds
+__global__ void pqb_stage(const PqSub* __restrict__ S, int k) {
+  const PqSub& q = S[blockIdx.x];
+  if (!q.active) return;
+  for (int t = threadIdx.x; t < k * q.w; t += blockDim.x) q.newc[t] = q.cents[t];
+}
+
+__global__ void pqb_commit(const PqSub* __restrict__ S, int k) {
+  const PqSub& q = S[blockIdx.x];
+  if (!q.active) return;
+  for (int t = threadIdx.x; t < k * q.w; t += blockDim.x) q.cents[t] = q.newc[t];
+}
+
+// Every subspace at once; widths up to 32. Writes each subspace's k x w
+// centroids to cents[sidx] and its result to res[sidx]; returns the index of
+// the first subspace whose seeding's draws differed from the prediction (M
+// when none did): that subspace's results stand, the later ones must be
+// trained again from `next` (its final generator state).
+static int pq_train_batched(const std::vector<DevBuf<float>>& proj, size_t n, const PqLayout& L, size_t k,
+                            size_t max_iter, const std::vector<ChaCha8>& start, std::vector<DevBuf<float>>& cents,
+                            std::vector<KmeansOut>& res, ChaCha8* next, hipStream_t s) {
+  const int M = L.M;
+  const int nb = (int)((n + PP_ROWS - 1) / PP_ROWS), nb256 = (int)((n + 255) / 256);
+  std::vector<PqSub> h(M);
+  DevBuf<float> ns((size_t)M * n), dist((size_t)M * n), newc_all;
+  DevBuf<uint32_t> assign((size_t)M * n), prev((size_t)M * n), counts((size_t)M * k), offsets((size_t)M * k);
+  DevBuf<uint32_t> keys((size_t)M * n), keys_sorted((size_t)M * n), vals((size_t)M * n), members((size_t)M * n);
+  DevBuf<double> ps((size_t)M * nb), fps((size_t)M * nb256), fpa((size_t)M * nb256), total((size_t)M * 2);
+  DevBuf<int> pe((size_t)M * nb), fpe((size_t)M * nb256), flags((size_t)M * 4);
+  DevBuf<ChaCha8> drng(M);
+  DevBuf<uint64_t> dfirst(M);
+  DevBuf<PqSub> dS(M);
+  size_t cofs_total = 0;
+  std::vector<size_t> cofs(M);
+  for (int q = 0; q < M; ++q) {
+    cofs[q] = cofs_total;
+    cofs_total += k * L.width[q];
+  }
+  newc_all.reserve(cofs_total);
+  std::vector<ChaCha8> rng(start);
+  std::vector<uint64_t> first(M);
+  bool vec4 = true, equal = true;
+  for (int q = 0; q < M; ++q) {
+    const int w = L.width[q];
+    cents[q].reserve(k * w);
+    first[q] = rng[q].gen_range_usize(n);  // kmeans.rs:150
+    PqSub& t = h[q];
+    t.P = proj[q].p;
+    t.cents = cents[q].p;
+    t.newc = newc_all.p + cofs[q];
+    t.ns = ns.p + (size_t)q * n;
+    t.ps = ps.p + (size_t)q * nb;
+    t.pe = pe.p + (size_t)q * nb;
+    t.rng = drng.p + q;
+    t.assign = assign.p + (size_t)q * n;
+    t.prev = prev.p + (size_t)q * n;
+    t.dist = dist.p + (size_t)q * n;
+    t.counts = counts.p + (size_t)q * k;
+    t.offsets = offsets.p + (size_t)q * k;
+    t.fps = fps.p + (size_t)q * nb256;
+    t.fpa = fpa.p + (size_t)q * nb256;
+    t.fpe = fpe.p + (size_t)q * nb256;
+    t.total = total.p + (size_t)q * 2;
+    t.flags = flags.p + (size_t)q * 4;
+    t.w = w;
+    t.active = 1;
+    vec4 = vec4 && w % 4 == 0 && ((uintptr_t)proj[q].p & 15) == 0;
+    equal = equal && w == L.width[0];
+  }
+  PXG_HIP(hipMemcpyAsync(dS.p, h.data(), M * sizeof(PqSub), hipMemcpyHostToDevice, s));
+  PXG_HIP(hipMemcpyAsync(drng.p, rng.data(), M * sizeof(ChaCha8), hipMemcpyHostToDevice, s));
+  PXG_HIP(hipMemcpyAsync(dfirst.p, first.data(), M * 8, hipMemcpyHostToDevice, s));
+  PXG_HIP(hipMemsetAsync(flags.p, 0, (size_t)M * 16, s));
+  PXG_HIP(hipMemsetAsync(prev.p, 0, (size_t)M * n * 4, s));  // kmeans.rs:88: every point starts in cluster 0
+  // k-means++, all subspaces a round at a time
+  const int w0 = L.width[0];
+  auto round = [&](int chosen, int init) {
+    const dim3 g(nb, M);
+    if (vec4 && equal && w0 == 8)
+      hipLaunchKernelGGL(pqb_pp_round_w<8>, g, dim3(256), 0, s, (const PqSub*)dS.p, (int)n, chosen, init);
+    else if (vec4 && equal && w0 == 4)
+      hipLaunchKernelGGL(pqb_pp_round_w<4>, g, dim3(256), 0, s, (const PqSub*)dS.p, (int)n, chosen, init);
+    else if (vec4 && equal && w0 == 16)
+      hipLaunchKernelGGL(pqb_pp_round_w<16>, g, dim3(256), 0, s, (const PqSub*)dS.p, (int)n, chosen, init);
+    else
+      hipLaunchKernelGGL(pqb_pp_round, g, dim3(256), 0, s, (const PqSub*)dS.p, (int)n, chosen, init, vec4 ? 1 : 0);
+  };
+  hipLaunchKernelGGL(pqb_first, dim3(M), dim3(64), 0, s, (const PqSub*)dS.p, (const uint64_t*)dfirst.p);
+  round(0, 1);
+  for (size_t chosen = 1; chosen < k; ++chosen) {
+    hipLaunchKernelGGL(pqb_pp_pick, dim3(M), dim3(1024), 0, s, (const PqSub*)dS.p, (int)n, nb, (int)chosen);
+    if (chosen + 1 < k) round((int)chosen, 0);
+  }
+  PXG_HIP(hipGetLastError());
+  std::vector<int> hf((size_t)M * 4);
+  PXG_HIP(hipMemcpyAsync(rng.data(), drng.p, M * sizeof(ChaCha8), hipMemcpyDeviceToHost, s));
+  PXG_HIP(hipMemcpyAsync(hf.data(), flags.p, (size_t)M * 16, hipMemcpyDeviceToHost, s));
+  PXG_HIP(hipStreamSynchronize(s));
+  for (int q = 0; q < M; ++q)
+    if (hf[(size_t)q * 4] != 0)
+      internal_error("kmeans++", "the sum of squared distances is not finite; coordinates are too large to square");
+  // the stream position (32-bit words drawn) of a generator state
+  auto pos = [](const ChaCha8& r) { return r.counter * 16 - (uint64_t)(64 - r.index); };
+  // PXG_PQ_REDO_AFTER=i takes the in-order path after subspace i as if its
+  // draws had differed (a test of that path; the results are the same)
+  const char* force = std::getenv("PXG_PQ_REDO_AFTER");
+  const int forced = force ? std::atoi(force) : -1;
+  int redo_from = M;
+  for (int q = 0; q + 1 < M; ++q)
+    if (q == forced || pos(rng[q]) != pos(start[q + 1])) {
+      redo_from = q + 1;
+      *next = rng[q];
+      break;
+    }
+  const int Mb = redo_from;  // subspaces whose seeding stands
+  for (int q = Mb; q < M; ++q) h[q].active = 0;
+  for (int q = 0; q < Mb; ++q) {
+    res[q] = KmeansOut();
+    res[q].k = k;
+    res[q].inexact_sums = (size_t)hf[(size_t)q * 4 + 1];
+  }
+  // Lloyd (kmeans.rs:85-136), the active subspaces a step at a time
+  int bits = 1;
+  while ((1ull << bits) < (uint64_t)M * k) ++bits;
+  size_t tmp_bytes = 0;
+  PXG_HIP(hipcub::DeviceRadixSort::SortPairs(nullptr, tmp_bytes, keys.p, keys_sorted.p, vals.p, members.p,
+                                             (int)((size_t)M * n), 0, bits, s));
+  DevBuf<unsigned char> tmp(tmp_bytes + 16);
+  std::vector<uint32_t> hc((size_t)M * k), ho((size_t)M * k);
+  std::vector<double> ht((size_t)M * 2);
+  // the single-run reseed pass's buffers (empty clusters)
+  DevBuf<float> work, rdist;
+  DevBuf<uint32_t> rassign;
+  DevBuf<unsigned long long> far_part(KF_BLOCKS);
+  DevBuf<long long> far(1);
+  const dim3 gn((unsigned)((n + 255) / 256), (unsigned)M);
+  for (size_t it = 0; it < max_iter; ++it) {
+    int live = 0;
+    for (int q = 0; q < Mb; ++q) live += h[q].active;
+    if (!live) break;
+    PXG_HIP(hipMemcpyAsync(dS.p, h.data(), M * sizeof(PqSub), hipMemcpyHostToDevice, s));
+    for (int q = 0; q < Mb; ++q)
+      if (h[q].active) res[q].iterations = it + 1;
+    // assignment: the sequential squared, strict < (kmeans.rs:200-212)
+    const int v4 = vec4 ? 1 : 0;
+    if (equal && L.width[0] == 8)
+      hipLaunchKernelGGL(pqb_assign<8>, gn, dim3(256), 0, s, (const PqSub*)dS.p, (int)n, (int)k, v4);
+    else if (equal && L.width[0] == 16)
+      hipLaunchKernelGGL(pqb_assign<16>, gn, dim3(256), 0, s, (const PqSub*)dS.p, (int)n, (int)k, v4);
+    else if (equal && L.width[0] == 4)
+      hipLaunchKernelGGL(pqb_assign<4>, gn, dim3(256), 0, s, (const PqSub*)dS.p, (int)n, (int)k, v4);
+    else if (equal && L.width[0] == 2)
+      hipLaunchKernelGGL(pqb_assign<2>, gn, dim3(256), 0, s, (const PqSub*)dS.p, (int)n, (int)k, v4);
+    else if (equal && L.width[0] == 1)
+      hipLaunchKernelGGL(pqb_assign<1>, gn, dim3(256), 0, s, (const PqSub*)dS.p, (int)n, (int)k, v4);
+    else if (equal && L.width[0] == 32)
+      hipLaunchKernelGGL(pqb_assign<32>, gn, dim3(256), 0, s, (const PqSub*)dS.p, (int)n, (int)k, v4);
+    else
+      hipLaunchKernelGGL(pqb_assign<0>, gn, dim3(256), 0, s, (const PqSub*)dS.p, (int)n, (int)k, 0);
+    // inertia: the f64 sum of the distances in point order (certified)
+    hipLaunchKernelGGL(pqb_partials, dim3(nb256, M), dim3(256), 0, s, (const PqSub*)dS.p, (int)n);
+    hipLaunchKernelGGL(pqb_total, dim3(M), dim3(1024), 0, s, (const PqSub*)dS.p, (int)n, nb256);
+    PXG_HIP(hipMemsetAsync(counts.p, 0, (size_t)M * k * 4, s));
+    hipLaunchKernelGGL(pqb_reset_changed, dim3(1), dim3(256), 0, s, (const PqSub*)dS.p, M);
+    hipLaunchKernelGGL(pqb_changed_counts, dim3((unsigned)((n + 2047) / 2048), M), dim3(256), 0, s,
+                       (const PqSub*)dS.p, (int)n, (int)k, keys.p, vals.p);
+    PXG_HIP(hipGetLastError());
+    PXG_HIP(hipMemcpyAsync(hc.data(), counts.p, (size_t)M * k * 4, hipMemcpyDeviceToHost, s));
+    PXG_HIP(hipMemcpyAsync(ht.data(), total.p, (size_t)M * 16, hipMemcpyDeviceToHost, s));
+    PXG_HIP(hipMemcpyAsync(hf.data(), flags.p, (size_t)M * 16, hipMemcpyDeviceToHost, s));
+    PXG_HIP(hipStreamSynchronize(s));
+    for (int q = 0; q < Mb; ++q) {
+      if (!h[q].active) continue;
+      res[q].inertia = ht[(size_t)q * 2];
+      if (ht[(size_t)q * 2 + 1] == 0.0) ++res[q].inexact_sums;
+      if (hf[(size_t)q * 4 + 2] == 0 && it > 0) h[q].active = 0;  // kmeans.rs:99-102
+    }
+    live = 0;
+    for (int q = 0; q < Mb; ++q) live += h[q].active;
+    if (!live) break;
+    PXG_HIP(hipMemcpyAsync(dS.p, h.data(), M * sizeof(PqSub), hipMemcpyHostToDevice, s));
+    // members of each (subspace, cluster) in point order: a stable sort
+    PXG_HIP(hipcub::DeviceRadixSort::SortPairs(tmp.p, tmp_bytes, keys.p, keys_sorted.p, vals.p, members.p,
+                                               (int)((size_t)M * n), 0, bits, s));
+    for (int q = 0; q < M; ++q) {
+      uint32_t acc = (uint32_t)((size_t)q * n);
+      for (size_t c = 0; c < k; ++c) {
+        ho[(size_t)q * k + c] = acc;
+        acc += hc[(size_t)q * k + c];
+      }
+    }
+    PXG_HIP(hipMemcpyAsync(offsets.p, ho.data(), (size_t)M * k * 4, hipMemcpyHostToDevice, s));
+    hipLaunchKernelGGL(pqb_stage, dim3(M), dim3(256), 0, s, (const PqSub*)dS.p, (int)k);
+    const int wmax = *std::max_element(L.width.begin(), L.width.end());
+    const bool wide = n >= 64 * k;
+    if (wmax <= 8 && wide)
+      hipLaunchKernelGGL((pqb_sums<8, 1024>), dim3((unsigned)k, M), dim3(1024), 0, s, (const PqSub*)dS.p, (int)k,
+                         (const uint32_t*)members.p);
+    else if (wmax <= 8)
+      hipLaunchKernelGGL((pqb_sums<8, 256>), dim3((unsigned)k, M), dim3(256), 0, s, (const PqSub*)dS.p, (int)k,
+                         (const uint32_t*)members.p);
+    else if (wmax <= 16)
+      hipLaunchKernelGGL((pqb_sums<16, 256>), dim3((unsigned)k, M), dim3(256), 0, s, (const PqSub*)dS.p, (int)k,
+                         (const uint32_t*)members.p);
+    else
+      hipLaunchKernelGGL((pqb_sums<32, 256>), dim3((unsigned)k, M), dim3(256), 0, s, (const PqSub*)dS.p, (int)k,
+                         (const uint32_t*)members.p);
+    PXG_HIP(hipGetLastError());
+    // empty clusters, ascending, against the partially updated array
+    // (kmeans.rs:119-123): the farthest point of [new rows < c, old rows >= c]
+    for (int q = 0; q < Mb; ++q) {
+      if (!h[q].active) continue;
+      const int w = h[q].w;
+      for (size_t c = 0; c < k; ++c) {
+        if (hc[(size_t)q * k + c] != 0) continue;
+        work.reserve(k * w);
+        rdist.reserve(n);
+        rassign.reserve(n);
+        PXG_HIP(hipMemcpyAsync(work.p, h[q].newc, c * w * 4, hipMemcpyDeviceToDevice, s));
+        PXG_HIP(hipMemcpyAsync(work.p + c * w, h[q].cents + c * w, (k - c) * w * 4, hipMemcpyDeviceToDevice, s));
+        nearest_device(h[q].P, w, nullptr, n, w, work.p, w, k, false, rassign.p, rdist.p, s);
+        launch_farthest(rdist.p, n, far_part.p, far.p, s);
+        hipLaunchKernelGGL(copy_row_at, dim3(1), dim3(256), 0, s, h[q].P, w, (const long long*)far.p, w,
+                           h[q].newc + c * w);
+        PXG_HIP(hipGetLastError());
+      }
+    }
+    hipLaunchKernelGGL(pqb_commit, dim3(M), dim3(256), 0, s, (const PqSub*)dS.p, (int)k);
+    PXG_HIP(hipGetLastError());
+  }
+  PXG_HIP(hipStreamSynchronize(s));
+  return redo_from;
+}
+
 void pq_train_device(const float* R, size_t n, int dim, int ldr, const PqLayout& L, size_t max_iter, uint64_t seed,
                      float* d_books, double* inertia, size_t* iterations, hipStream_t s) {
-  // One generator advanced across the subspaces (product.rs:244-247), but
-  // only k-means++ draws from it (kmeans.rs:146-194; Lloyd and the farthest
-  // point reseeds draw nothing). In the common case a seeding's draws do not
-  // depend on the data: one gen_range over the points, then one 64-bit word
-  // per further centroid (gen_range_f64 accepts its first word unless the
-  // product rounds up to the total, and only a zero total takes a gen_range
-  // instead). So each subspace's starting state is predicted on the host,
-  // every subspace seeds and runs its Lloyd loop at once on its own stream
-  // and host thread, and each seeding's final state is checked against the
-  // next subspace's predicted start. From the first subspace whose draws
-  // differed, the later subspaces are redone in order from the true state,
-  // so every codebook is the sequential run's.
   (void)dim;
   const int M = L.M;
   const size_t k = std::max<size_t>(std::min<size_t>(256, n), 1);
   std::vector<DevBuf<float>> proj(M), seeds(M), cents(M);
   std::vector<KmeansOut> res(M);
-  std::vector<std::exception_ptr> err(M);
-  std::vector<ChaCha8> start(M), end(M);
+  std::vector<ChaCha8> start(M);
   {
     ChaCha8 r(seed);
     for (int sidx = 0; sidx < M; ++sidx) {
@@ -2161,60 +2589,32 @@ void pq_train_device(const float* R, size_t n, int dim, int ldr, const PqLayout&
     const int w = L.width[sidx], off = L.off[sidx];
     const size_t tot = n * (size_t)w;
     proj[sidx].reserve(std::max<size_t>(tot, 1));
-    seeds[sidx].reserve(k * w);
     if (tot)
       hipLaunchKernelGGL(gather_cols, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, R, ldr, (int)n, off, w,
                          proj[sidx].p);
     PXG_HIP(hipGetLastError());
   }
-  PXG_HIP(hipStreamSynchronize(s));
-  // seeding from `rng` (advanced by it) and the Lloyd loop of one subspace
-  auto train_one = [&](int sidx, ChaCha8& rng, hipStream_t ws) {
+  // seeding from `rng` (advanced by it) and the Lloyd loop of one subspace:
+  // the single-run path
+  auto train_one = [&](int sidx, ChaCha8& rng) {
     const int w = L.width[sidx];
+    seeds[sidx].reserve(k * w);
     size_t inexact = 0;
-    if (n) inexact = kmeans_pp_device(proj[sidx].p, n, w, w, k, rng, seeds[sidx].p, ws);  // synchronises ws
+    if (n) inexact = kmeans_pp_device(proj[sidx].p, n, w, w, k, rng, seeds[sidx].p, s);
     res[sidx] = kmeans_device(proj[sidx].p, n, w, w, 256, max_iter, nullptr, n ? seeds[sidx].p : nullptr, cents[sidx],
-                              nullptr, ws);
+                              nullptr, s);
     res[sidx].inexact_sums += inexact;
   };
-  {
-    std::vector<std::thread> workers;
-    try {
-      for (int sidx = 0; sidx < M; ++sidx)
-        workers.emplace_back([&, sidx]() {
-          try {
-            hipStream_t ws;
-            PXG_HIP(hipStreamCreateWithFlags(&ws, hipStreamNonBlocking));
-            struct SG {
-              hipStream_t s;
-              ~SG() { (void)hipStreamDestroy(s); }
-            } sg{ws};
-            end[sidx] = start[sidx];
-            train_one(sidx, end[sidx], ws);
-          } catch (...) {
-            err[sidx] = std::current_exception();
-          }
-        });
-    } catch (...) {
-      for (auto& w : workers) w.join();
-      throw;
-    }
-    for (auto& w : workers) w.join();
+  const int wmax = *std::max_element(L.width.begin(), L.width.end());
+  int done = 0;
+  ChaCha8 next(seed);
+  // the shared member sort indexes M * n entries with an int
+  if (n && wmax <= 32 && (uint64_t)M * n < (1ull << 31)) {
+    done = pq_train_batched(proj, n, L, k, max_iter, start, cents, res, &next, s);
+  } else {
+    next = start[0];
   }
-  for (auto& e : err)
-    if (e) std::rethrow_exception(e);
-  // the stream position (32-bit words drawn) of a generator state
-  auto pos = [](const ChaCha8& r) { return r.counter * 16 - (uint64_t)(64 - r.index); };
-  // PXG_PQ_REDO_AFTER=i takes the in-order path after subspace i as if its
-  // draws had differed (a test of that path; the results are the same)
-  const char* force = std::getenv("PXG_PQ_REDO_AFTER");
-  const int forced = force ? std::atoi(force) : -1;
-  for (int sidx = 0; sidx + 1 < M; ++sidx) {
-    if (sidx != forced && pos(end[sidx]) == pos(start[sidx + 1])) continue;
-    ChaCha8 rng = end[sidx];
-    for (int t = sidx + 1; t < M; ++t) train_one(t, rng, s);
-    break;
-  }
+  for (int t = done; t < M; ++t) train_one(t, next);
   double in = 0.0;
   size_t its = 0;
   for (int sidx = 0; sidx < M; ++sidx) {

@@ -312,6 +312,40 @@ def test_pq_train_in_order_path(gpu, monkeypatch, after):
     assert pq.training_inertia == inertia and pq.training_iterations == iters
 
 
+@pytest.mark.parametrize("dim,m,count,distinct", [(16, 2, 300, 40), (12, 3, 2000, 150)])
+def test_pq_train_duplicates_reseed_empty_clusters(gpu, dim, m, count, distinct):
+    """Few distinct rows: k-means++ falls back to uniform picks once the total
+    is zero (kmeans.rs:162-166), duplicate seeds leave clusters empty, and the
+    batched trainer reseeds them per subspace with the farthest point of the
+    partially updated array (kmeans.rs:119-123)."""
+    px = gpu
+    rng = np.random.default_rng(count)
+    rows = rng.standard_normal((distinct, dim)).astype(np.float32)
+    t = rows[rng.integers(0, distinct, count)]
+    pq = px.ProductQuantizer.train(px.VectorSpace(dim, px.Metric.EUCLIDEAN), t, px.PqConfig(m).with_seed(11))
+    books, inertia, iters = orc.pq_train(t, m, 25, 11)
+    assert np.array_equal(bits(pq.codebooks), bits(books))
+    assert pq.training_inertia == inertia and pq.training_iterations == iters
+
+
+def test_pq_train_many_points_uneven_convergence(gpu):
+    """Enough points for the wide cluster sums (n >= 64 k) and subspaces that
+    stop at different iterations: one subspace's columns are a few exact
+    clusters (converges early), the other's noisy."""
+    px = gpu
+    rng = np.random.default_rng(17)
+    n, dim = 20000, 16
+    t = np.empty((n, dim), np.float32)
+    t[:, :8] = rng.standard_normal((300, 8)).astype(np.float32)[rng.integers(0, 300, n)]
+    t[:, 8:] = rng.standard_normal((n, 8)).astype(np.float32)
+    pq = px.ProductQuantizer.train(px.VectorSpace(dim, px.Metric.EUCLIDEAN), t,
+                                   px.PqConfig(2).with_seed(5).with_max_iterations(12))
+    books, inertia, iters = orc.pq_train(t, 2, 12, 5)
+    assert np.array_equal(bits(pq.codebooks), bits(books))
+    assert pq.training_inertia == inertia and pq.training_iterations == iters
+    assert iters < 24  # the clustered subspace stopped early
+
+
 def test_pq_validation(gpu):  # product.rs:775-809
     px = gpu
     space = px.VectorSpace(8, px.Metric.EUCLIDEAN)
