@@ -328,7 +328,68 @@ def bench_ivfpq(args, torch, px, dev):
         out["parity_sample"] = {"queries": mq, "bit_exact": same}
         log(f"[bench] ivfpq CPU {mq / cpu_s:.1f} QPS ({args.cpu_threads} threads), {m1 / cpu_1:.1f} QPS (1 thread); "
             f"GPU/oracle bit-exact on {same}/{mq}")
+    out["mutate_cycle"] = ivf_mutate_cycles(args, torch, px, dev, idx, batches, stream, k, cents_h, books_h)
     return out
+
+
+def ivf_mutate_cycles(args, torch, px, dev, idx, batches, stream, k, cents, books):
+    """IvfPqIndex insert/remove (ivfpq.rs:1129-1180) between searches at the
+    full 10M size: each cycle removes 100 ids, inserts 100 new vectors from the
+    same mixture and searches one 1,024-query batch. The list view is updated
+    in place (appends, holes filled, regions moved when full), so a cycle
+    costs its mutations plus one search, not a rebuild of the lists."""
+    B, dim = batches[0].shape
+    nb = len(batches)
+    cycles, per = 20, 100
+    oi = torch.empty((B, k), dtype=torch.int64, device=dev)
+    od = torch.empty((B, k), dtype=torch.float32, device=dev)
+    oc = torch.empty((B,), dtype=torch.int32, device=dev)
+    new, _ = mixture(torch, px, dev, cycles * per, dim, 1000, 0.15, 0, True, args.seed + 8)
+    ids, live = idx.slots()
+    present = ids[live.astype(bool)]
+    rng = np.random.default_rng(args.seed)
+    victims = rng.choice(present, size=cycles * per, replace=False)
+    next_id = int(ids.max()) + 1
+    r0, m0 = idx.view_stats()
+    t_rm = t_ins = t_srch = 0.0
+    torch.cuda.synchronize()
+    t_all = time.perf_counter()
+    for c in range(cycles):
+        t0 = time.perf_counter()
+        for i in victims[c * per:(c + 1) * per]:
+            idx.remove(int(i))
+        t1 = time.perf_counter()
+        idx.insert_device(np.arange(next_id, next_id + per, dtype=np.uint64), new[c * per:(c + 1) * per])
+        next_id += per
+        t2 = time.perf_counter()
+        idx.search_device(batches[c % nb], k, oi, od, oc, stream=stream)
+        torch.cuda.synchronize()
+        t3 = time.perf_counter()
+        t_rm += t1 - t0
+        t_ins += t2 - t1
+        t_srch += t3 - t2
+    t_all = time.perf_counter() - t_all
+    r1, m1 = idx.view_stats()
+    res = {"cycles": cycles, "removed_per_cycle": per, "inserted_per_cycle": per,
+           "ms_per_cycle": round(t_all / cycles * 1e3, 3), "remove_ms_per_id": round(t_rm / (cycles * per) * 1e3, 4),
+           "insert_ms_per_batch": round(t_ins / cycles * 1e3, 3), "search_ms": round(t_srch / cycles * 1e3, 3),
+           "view_rebuilds": r1 - r0, "view_region_moves": m1 - m0,
+           "note": "remove 100 ids, insert 100 vectors (insert_device), search one batch of 1024, per cycle"}
+    if not args.no_cpu:
+        from oracle import oracle as orc
+        ids, live = idx.slots()
+        _, _, codes, list_of = idx.parts()
+        qh = batches[0][:256].cpu().numpy()
+        gi, gd, gc = idx.search_batch(qh, k)
+        wi, wd, wc = orc.ivf_search(0, cents, books, codes, list_of, ids, qh, k, 32, 16, live=live,
+                                    threads=args.cpu_threads)
+        same = int(sum(np.array_equal(gi[i], wi[i]) and np.array_equal(gd[i].view(np.uint32), wd[i].view(np.uint32))
+                       for i in range(qh.shape[0])))
+        res["parity_after_mutations"] = {"queries": qh.shape[0], "bit_exact": same}
+    log(f"[bench] ivfpq mutate cycle: {res['ms_per_cycle']} ms (remove {res['remove_ms_per_id']} ms/id, insert "
+        f"{res['insert_ms_per_batch']} ms/100, search {res['search_ms']} ms); view rebuilds {r1 - r0}, "
+        f"region moves {m1 - m0}; parity {res.get('parity_after_mutations')}")
+    return res
 
 
 PEAK_INT8_MFMA_TOPS = 5000.0

@@ -137,6 +137,7 @@ extern "C" {
         nprobe: u64, d_accept: *const u8, d_out_ids: *mut u64, d_out_dist: *mut f32, d_out_count: *mut u32,
         stream: *mut c_void) -> c_int;
     pub(crate) fn pxg_ivfpq_last_scanned() -> u64;
+    pub(crate) fn pxg_ivfpq_view_stats(index: *const PxgIvfPq, rebuilds: *mut u64, moves: *mut u64) -> c_int;
     pub(crate) fn pxg_kmeans(points: *const f32, n: u64, dim: u32, k: u64, max_iterations: u64, seed: u64,
         centroids_out: *mut f32, inertia: *mut f64, iterations: *mut u64, k_out: *mut u64) -> c_int;
     pub(crate) fn pxg_kmeans_lloyd(points: *const f32, n: u64, dim: u32, k: u64, max_iterations: u64,

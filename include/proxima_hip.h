@@ -255,6 +255,10 @@ int pxg_ivfpq_search_device(const pxg_ivfpq* index, const float* d_queries, uint
 /* Code entries (M bytes + a 4-byte id rank each) the last search on this
  * thread streamed: the scan's algorithmic traffic. No reference counterpart. */
 uint64_t pxg_ivfpq_last_scanned(void);
+/* Maintenance counters of the index's list view (no reference counterpart):
+ * full rebuilds (after train, load, compact, or a full pool) and list regions
+ * moved by appends. Inserts and removals otherwise update the view in place. */
+int pxg_ivfpq_view_stats(const pxg_ivfpq* index, uint64_t* rebuilds, uint64_t* moves);
 
 /* ------------------------------------------------------------------------ */
 /* k-means and the product quantizer (crates/proxima-quantize).              */

@@ -578,6 +578,12 @@ class IvfPqIndex(_IndexBase):
         _check(_lib.pxg_ivfpq_slots(self._h, _ptr(ids), _ptr(live)))
         return ids[:n], live[:n]
 
+    def view_stats(self):
+        """(full rebuilds, regions moved) of the list view so far (no reference counterpart)."""
+        r, m = C.c_uint64(), C.c_uint64()
+        _check(_lib.pxg_ivfpq_view_stats(self._h, C.byref(r), C.byref(m)))
+        return int(r.value), int(m.value)
+
     def list_lengths(self):
         n = int(_lib.pxg_ivfpq_list_count(self._h))
         out = np.zeros(max(n, 1), np.uint64)

@@ -117,6 +117,7 @@ SIGNATURES = {
     "pxg_ivfpq_search": (_i32, [_vp, _vp, _u64, _u64, _u64, _vp, _vp, _vp, _vp]),
     "pxg_ivfpq_search_device": (_i32, [_vp, _vp, _u64, _u64, _u64, _vp, _vp, _vp, _vp, _vp]),
     "pxg_ivfpq_last_scanned": (_u64, []),
+    "pxg_ivfpq_view_stats": (_i32, [_vp, _P(_u64), _P(_u64)]),
     # k-means / PQ
     "pxg_kmeans": (_i32, [_vp, _u64, _u32, _u64, _u64, _u64, _vp, _P(_f64), _P(_u64), _P(_u64)]),
     "pxg_kmeans_lloyd": (_i32, [_vp, _u64, _u32, _u64, _u64, _vp, _vp, _vp, _P(_f64), _P(_u64)]),

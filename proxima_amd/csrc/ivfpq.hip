@@ -8,12 +8,15 @@
 //              width_s floats (product.rs:226-238 layout)
 //   codes      [cap][M] u8           slot-major PQ codes (product.rs:361-380)
 //   list_of    [cap] u32             coarse list per slot, UINT32_MAX if none
-//   CSR view rebuilt lazily after mutations, one entry per live slot, lists
-//   in order and slots ascending inside each list (ivfpq.rs:891-896):
-//     list_off [produced+1] u32, list_rank [entries] u32 (id rank),
-//     list_codes [entries][M] u8 -> M bytes per scanned vector streamed by
-//     ivf_scan16 (ranks read only for entries that pass its screen), M + 4
-//     by the other scans.
+//   list view, one entry per live slot (ivfpq.rs:891-896): list l's entries
+//   at positions [list_beg[l], list_end[l]) of a pool with slack per list,
+//   kept current by every insert (append) and removal (the list's last entry
+//   fills the hole), laid out again only after train, load, compact or when
+//   the pool fills:
+//     list_beg, list_end [produced] u32, list_slot [pool] u32 (slot),
+//     list_codes [pool][M] u8 -> M bytes per scanned vector streamed by
+//     ivf_scan16 (slots, and through them id ranks and filters, read only
+//     for entries that pass its screen), M + 4 by the other scans.
 //   X          [cap][ld] f32 prepared vectors when retained (rerank, training,
 //              the untrained exhaustive path).
 //
@@ -123,10 +126,12 @@ __global__ __launch_bounds__(256) void ivf_scan(const float* __restrict__ Qp, in
                                                 const int* __restrict__ probes, int nprobe,
                                                 const float* __restrict__ cents, const float* __restrict__ books,
                                                 const int* __restrict__ sub_off, const int* __restrict__ book_off,
-                                                const uint32_t* __restrict__ list_off,
-                                                const uint32_t* __restrict__ list_rank,
+                                                const uint32_t* __restrict__ list_beg,
+                                                const uint32_t* __restrict__ list_end,
+                                                const uint32_t* __restrict__ list_slot,
                                                 const uint8_t* __restrict__ list_codes,
                                                 const uint32_t* __restrict__ rank_slot,
+                                                const uint32_t* __restrict__ slot_rank,
                                                 const uint8_t* __restrict__ accept, int kk,
                                                 uint64_t* __restrict__ out) {
   extern __shared__ float lut[];  // M * 256 floats
@@ -170,13 +175,14 @@ __global__ __launch_bounds__(256) void ivf_scan(const float* __restrict__ Qp, in
   uint64_t* wb = wbuf[w];
   uint64_t thr = KEY_MAX;
   int cnt = 0;
-  const uint32_t begin = list_off[l], end = list_off[l + 1];
+  const uint32_t begin = list_beg[l], end = list_end[l];
   for (uint32_t e0 = begin + w * 64; e0 < end; e0 += 256) {
     const uint32_t e = e0 + lane;
     uint64_t key = KEY_MAX;
     if (e < end) {
-      const uint32_t rk = list_rank[e];
-      if (accept == nullptr || accept[rank_slot[rk]]) {
+      const uint32_t sl = list_slot[e];
+      if (accept == nullptr || accept[sl]) {
+        const uint32_t rk = slot_rank[sl];
         const uint8_t* code = list_codes + (size_t)e * M;
         float sum = 0.0f;  // DistanceTable::squared_l2 / inner_product, product.rs:580-603
         if (M == 16) {
@@ -367,7 +373,8 @@ constexpr int IVF_PICK_CAP = 1024;
 // update one address; the host adds them up.
 constexpr int IVF_SCAN_SLOTS = 64;
 __global__ __launch_bounds__(256) void ivf_coarse_pick(const uint64_t* __restrict__ ck, int cst, int produced, int np,
-                                                       int* __restrict__ probes, const uint32_t* __restrict__ list_off,
+                                                       int* __restrict__ probes, const uint32_t* __restrict__ list_beg,
+                                                       const uint32_t* __restrict__ list_end,
                                                        unsigned long long* __restrict__ scanned) {
   const int q = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   __shared__ uint64_t cand[IVF_PICK_CAP];
@@ -443,7 +450,7 @@ __global__ __launch_bounds__(256) void ivf_coarse_pick(const uint64_t* __restric
   if (w == 0) {
     const int l = (int)(uint32_t)cand[lane];
     if (lane < np) probes[(size_t)q * np + lane] = l;
-    uint32_t len = lane < np ? list_off[l + 1] - list_off[l] : 0u;
+    uint32_t len = lane < np ? list_end[l] - list_beg[l] : 0u;
 #pragma unroll
     for (int st = 32; st > 0; st >>= 1) len += xor_lane_rt(len, st);
     if (lane == 0) atomicAdd(scanned + (q & (IVF_SCAN_SLOTS - 1)), (unsigned long long)len);
@@ -513,7 +520,8 @@ __global__ __launch_bounds__(256) void ivf_coarse_pick_approx(const float* __res
                                                               const float* __restrict__ C,
                                                               const float* __restrict__ cn,
                                                               int* __restrict__ probes,
-                                                              const uint32_t* __restrict__ list_off,
+                                                              const uint32_t* __restrict__ list_beg,
+                                                              const uint32_t* __restrict__ list_end,
                                                               unsigned long long* __restrict__ scanned) {
   const int q = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   __shared__ uint64_t cand[IVF_PICK_CAP];
@@ -650,7 +658,7 @@ __global__ __launch_bounds__(256) void ivf_coarse_pick_approx(const float* __res
   if (w == 0) {
     const int l = (int)(uint32_t)cand[lane];
     if (lane < np) probes[(size_t)q * np + lane] = l;
-    uint32_t len = lane < np ? list_off[l + 1] - list_off[l] : 0u;
+    uint32_t len = lane < np ? list_end[l] - list_beg[l] : 0u;
 #pragma unroll
     for (int st = 32; st > 0; st >>= 1) len += xor_lane_rt(len, st);
     if (lane == 0) atomicAdd(scanned + (q & (IVF_SCAN_SLOTS - 1)), (unsigned long long)len);
@@ -691,10 +699,12 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan_reg(const float* __restr
                                                          const int* __restrict__ probes, int nprobe, int pg,
                                                          int groups, const float* __restrict__ cents,
                                                          const float* __restrict__ books,
-                                                         const uint32_t* __restrict__ list_off,
-                                                         const uint32_t* __restrict__ list_rank,
+                                                         const uint32_t* __restrict__ list_beg,
+                                                         const uint32_t* __restrict__ list_end,
+                                                         const uint32_t* __restrict__ list_slot,
                                                          const uint8_t* __restrict__ list_codes,
                                                          const uint32_t* __restrict__ rank_slot,
+                                                         const uint32_t* __restrict__ slot_rank,
                                                          const uint8_t* __restrict__ accept, int kk,
                                                          uint64_t* __restrict__ out, int k,
                                                          const uint64_t* __restrict__ ids,
@@ -781,13 +791,14 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan_reg(const float* __restr
     if (METRIC == 0 && pi + 1 < np) build(srs[pi + 1], lut + ((pi + 1) & 1) * tsz);
     const float* tab = lut + (METRIC == 0 ? (pi & 1) * tsz : 0);
     const float one_minus_qdc = METRIC == 1 ? arm_nan(1.0f - s_qdc[pi]) : 0.0f;
-    const uint32_t begin = list_off[l], end = list_off[l + 1];
+    const uint32_t begin = list_beg[l], end = list_end[l];
     for (uint32_t e0 = begin + w * 64; e0 < end; e0 += IVF_SW * 64) {
       const uint32_t e = e0 + lane;
       uint64_t key = KEY_MAX;
       if (e < end) {
-        const uint32_t rk = list_rank[e];
-        if (accept == nullptr || accept[rank_slot[rk]]) {
+        const uint32_t sl = list_slot[e];
+        if (accept == nullptr || accept[sl]) {
+          const uint32_t rk = slot_rank[sl];
           float sum = 0.0f;  // DistanceTable::squared_l2 / inner_product, product.rs:580-603
           if (M == 16) {
             const uint4 cw = *reinterpret_cast<const uint4*>(list_codes + (size_t)e * 16);
@@ -933,10 +944,12 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan16(const float* __restric
                                                           const int* __restrict__ probes, int nprobe, int pg,
                                                           int groups, const float* __restrict__ cents,
                                                           const float* __restrict__ books,
-                                                          const uint32_t* __restrict__ list_off,
-                                                          const uint32_t* __restrict__ list_rank,
+                                                          const uint32_t* __restrict__ list_beg,
+                                                          const uint32_t* __restrict__ list_end,
+                                                          const uint32_t* __restrict__ list_slot,
                                                           const uint8_t* __restrict__ list_codes,
                                                           const uint32_t* __restrict__ rank_slot,
+                                                          const uint32_t* __restrict__ slot_rank,
                                                           const uint8_t* __restrict__ accept, int kk,
                                                           uint64_t* __restrict__ out, int k,
                                                           const uint64_t* __restrict__ ids,
@@ -972,8 +985,8 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan16(const float* __restric
     srs[pi][j] = METRIC == 0 ? qv[j] - cents[(size_t)pq[pi] * ld + j] : qv[j];
   }
   if (tid < np) {
-    s_lb[tid] = list_off[pq[tid]];
-    s_le[tid] = list_off[pq[tid] + 1];
+    s_lb[tid] = list_beg[pq[tid]];
+    s_le[tid] = list_end[pq[tid]];
   }
   if (METRIC == 1) {
     for (int pi = w; pi < np; pi += IVF_SW) {
@@ -1086,8 +1099,8 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan16(const float* __restric
     uint64_t b[1] = {KEY_MAX};
     if (lane < ncand) {
       const uint2 c = cbuf[w][lane];
-      const uint32_t rk = list_rank[c.y];
-      if (accept == nullptr || accept[rank_slot[rk]]) b[0] = ((uint64_t)c.x << 32) | rk;
+      const uint32_t sl = list_slot[c.y];
+      if (accept == nullptr || accept[sl]) b[0] = ((uint64_t)c.x << 32) | slot_rank[sl];
     }
     wave_bitonic_sort<1>(b, lane);
     if (kk > 64) {
@@ -1285,12 +1298,13 @@ __global__ void ivf_probes_from_ids(const uint64_t* __restrict__ ids, int n, int
   if (i < n) probes[i] = (int)ids[i];
 }
 
-__global__ void ivf_count_scanned(const int* __restrict__ probes, int n, const uint32_t* __restrict__ list_off,
+__global__ void ivf_count_scanned(const int* __restrict__ probes, int n, const uint32_t* __restrict__ list_beg,
+                                  const uint32_t* __restrict__ list_end,
                                   unsigned long long* __restrict__ total) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const int l = probes[i];
-  atomicAdd(total + (i & (IVF_SCAN_SLOTS - 1)), (unsigned long long)(list_off[l + 1] - list_off[l]));
+  atomicAdd(total + (i & (IVF_SCAN_SLOTS - 1)), (unsigned long long)(list_end[l] - list_beg[l]));
 }
 
 __global__ void ivf_gather_rows(const float* __restrict__ X, int ld, const uint32_t* __restrict__ rows, int n,
@@ -1383,22 +1397,25 @@ __global__ __launch_bounds__(256) void ivf_wide_tables(const float* __restrict__
 __global__ __launch_bounds__(256) void ivf_wide_keys(const int* __restrict__ probes, int np, int q0, int M,
                                                      int metric, const float* __restrict__ tables,
                                                      const float* __restrict__ omq,
-                                                     const uint32_t* __restrict__ list_off,
-                                                     const uint32_t* __restrict__ list_rank,
+                                                     const uint32_t* __restrict__ list_beg,
+                                                     const uint32_t* __restrict__ list_end,
+                                                     const uint32_t* __restrict__ list_slot,
                                                      const uint8_t* __restrict__ list_codes,
                                                      const uint32_t* __restrict__ rank_slot,
+                                                     const uint32_t* __restrict__ slot_rank,
                                                      const uint8_t* __restrict__ accept,
                                                      const uint32_t* __restrict__ pofs, uint64_t* __restrict__ keys) {
   const int item = blockIdx.x;
   const int l = probes[(size_t)q0 * np + item];
   const float* tab = tables + (size_t)item * M * 256;
-  const uint32_t begin = list_off[l], end = list_off[l + 1];
+  const uint32_t begin = list_beg[l], end = list_end[l];
   uint64_t* out = keys + pofs[item];
   const float om = metric == 1 ? omq[item] : 0.0f;
   for (uint32_t e = begin + threadIdx.x; e < end; e += blockDim.x) {
-    const uint32_t rk = list_rank[e];
+    const uint32_t sl = list_slot[e];
     uint64_t key = KEY_MAX;
-    if (accept == nullptr || accept[rank_slot[rk]]) {
+    if (accept == nullptr || accept[sl]) {
+      const uint32_t rk = slot_rank[sl];
       const uint8_t* code = list_codes + (size_t)e * M;
       float sum = 0.0f;
       for (int sidx = 0; sidx < M; ++sidx) sum += tab[sidx * 256 + code[sidx]];
@@ -1463,13 +1480,20 @@ __global__ void ivf_remap_slots(uint32_t* __restrict__ rank_slot, uint32_t len,
   if (r < len) rank_slot[r] = new_of_old[rank_slot[r]];
 }
 
-__global__ void ivf_gather_csr(const uint32_t* __restrict__ entry_slot, int n, const uint32_t* __restrict__ rank,
-                               const uint8_t* __restrict__ codes, int M, uint32_t* __restrict__ list_rank,
+// The list view's entry at `from` moves to `to` (a removal's hole).
+__global__ void ivf_move_entry(uint32_t* __restrict__ list_slot, uint8_t* __restrict__ list_codes, int M,
+                               uint32_t from, uint32_t to) {
+  if (threadIdx.x == 0) list_slot[to] = list_slot[from];
+  for (int j = threadIdx.x; j < M; j += blockDim.x) list_codes[(size_t)to * M + j] = list_codes[(size_t)from * M + j];
+}
+
+__global__ void ivf_gather_csr(const uint32_t* __restrict__ entry_slot, int n, const uint32_t* __restrict__ pos,
+                               const uint8_t* __restrict__ codes, int M, uint32_t* __restrict__ list_slot,
                                uint8_t* __restrict__ list_codes) {
-  const int e = blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= n) return;
-  const uint32_t s = entry_slot[e];
-  list_rank[e] = rank[s];
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint32_t s = entry_slot[i], e = pos[i];
+  list_slot[e] = s;
   for (int j = 0; j < M; ++j) list_codes[(size_t)e * M + j] = codes[(size_t)s * M + j];
 }
 
@@ -1627,9 +1651,23 @@ struct IvfPqIndex {
   int cst = 0;
   DevBuf<int> d_sub_off, d_book_off;
   RankTable ranks;  // id ranks of the live slots, current after every mutation
-  DevBuf<uint32_t> list_off, list_rank;
+  // The scan view (ivfpq.rs:891-896): list l's entries, each a slot and its
+  // M code bytes, at pool positions [lbeg[l], lend[l]) of a region of
+  // lcap[l] positions. An insert appends to its list (a full region moves to
+  // the pool's end with twice the room, O(|list|)); a removal moves the
+  // list's last entry into its hole; so a mutation costs O(1) amortised, as
+  // the reference's Vec pushes and retains do (ivfpq.rs:893-896, 1172). Scan
+  // keys are (distance, id rank), so the order within a list changes no
+  // result. A full rebuild (train, load, compact, or a pool half made of
+  // regions left behind by moves) lays the lists out again with slack.
+  DevBuf<uint32_t> list_beg, list_end, list_slot;
   DevBuf<uint8_t> list_codes;
-  std::vector<uint32_t> list_len_h;
+  std::vector<uint32_t> list_len_h, lbeg_h, lend_h, lcap_h;
+  std::vector<uint32_t> ent_slot_h;  // pool position -> slot
+  std::vector<uint32_t> pos_h;       // slot -> pool position (NO_POS when not in the view)
+  size_t pool_cap = 0, pool_used = 0, pool_abandoned = 0;
+  uint64_t view_rebuilds = 0, view_moves = 0;  // full rebuilds; regions moved by appends
+  static constexpr uint32_t NO_POS = 0xFFFFFFFFu;
   // the coarse quantizer as an exact flat index over the centroids (ids =
   // list numbers): MFMA candidates + exact unrolled rescoring give the
   // reference's (distance, list) order for the probe selection
@@ -1664,35 +1702,62 @@ struct IvfPqIndex {
     cap = nc;
   }
 
-  // the CSR list view (it caches id ranks); rebuilt on first use after a change
+  // room of a list region holding `len` entries: slack for appends, whole
+  // 32-entry groups (the bank order's unit)
+  static uint32_t region_for(uint64_t len) {
+    const uint64_t c = len + std::max<uint64_t>(32, len / 16);
+    return (uint32_t)((c + 31) & ~(uint64_t)31);
+  }
+
+  // The full rebuild of the scan view, on first use after train, load,
+  // compact or too many abandoned regions.
   void refresh(hipStream_t s) {
     std::lock_guard<std::mutex> lk(lazy_mu);
     const size_t hw = slots.high_water();
     if (trained && csr_dirty) {
-      std::vector<uint32_t> count(produced + 1, 0);
+      std::vector<uint64_t> count(produced + 1, 0);
       for (size_t i = 0; i < hw; ++i)
         if (live[i] && list_of_h[i] != UNASSIGNED) count[list_of_h[i] + 1]++;
       for (int l = 0; l < produced; ++l) count[l + 1] += count[l];
-      const uint32_t total = count[produced];
-      std::vector<uint32_t> entry(std::max<uint32_t>(total, 1)), cur(count.begin(), count.end() - 1);
+      const uint64_t total = count[produced];
+      std::vector<uint32_t> entry(std::max<uint64_t>(total, 1));
+      std::vector<uint64_t> cur(count.begin(), count.end() - 1);
       for (size_t i = 0; i < hw; ++i)
         if (live[i] && list_of_h[i] != UNASSIGNED) entry[cur[list_of_h[i]]++] = (uint32_t)i;
       list_len_h.assign(produced, 0);
-      for (int l = 0; l < produced; ++l) list_len_h[l] = count[l + 1] - count[l];
-      list_off.reserve(produced + 1);
-      list_rank.reserve(std::max<uint32_t>(total, 1));
-      list_codes.reserve(std::max<size_t>((size_t)total * M() + 16, 16));
-      DevBuf<uint32_t> d_entry(std::max<uint32_t>(total, 1)), d_banked;
-      DevBuf<uint2> d_segs;
-      std::vector<uint2> segs;  // read by an async copy: lives to the sync below
-      PXG_HIP(hipMemcpyAsync(list_off.p, count.data(), (produced + 1) * 4, hipMemcpyHostToDevice, s));
+      lbeg_h.assign(produced, 0);
+      lend_h.assign(produced, 0);
+      lcap_h.assign(produced, 0);
+      uint64_t at = 0;
+      for (int l = 0; l < produced; ++l) {
+        list_len_h[l] = (uint32_t)(count[l + 1] - count[l]);
+        lcap_h[l] = region_for(list_len_h[l]);
+        lbeg_h[l] = (uint32_t)at;
+        lend_h[l] = (uint32_t)(at + list_len_h[l]);
+        at += lcap_h[l];
+      }
+      pool_used = at;
+      pool_cap = at + at / 8 + 1024;  // room for moved regions
+      if (pool_cap >= NO_POS) capacity_error("ivf-pq list view", NO_POS, "capacity exceeded: the IVF-PQ list view holds fewer than 2^32 entries");
+      pool_abandoned = 0;
+      list_beg.reserve(std::max(produced, 1));
+      list_end.reserve(std::max(produced, 1));
+      list_slot.alloc(pool_cap);
+      list_codes.alloc(pool_cap * M() + 16);
+      PXG_HIP(hipMemcpyAsync(list_beg.p, lbeg_h.data(), produced * 4, hipMemcpyHostToDevice, s));
+      PXG_HIP(hipMemcpyAsync(list_end.p, lend_h.data(), produced * 4, hipMemcpyHostToDevice, s));
+      ent_slot_h.assign(pool_cap, NO_POS);
+      pos_h.assign(std::max<size_t>(cap, hw), NO_POS);
       if (total) {
+        DevBuf<uint32_t> d_entry(total), d_banked, d_pos(total);
+        DevBuf<uint2> d_segs;
+        std::vector<uint2> segs;  // read by an async copy: lives to the sync below
         PXG_HIP(hipMemcpyAsync(d_entry.p, entry.data(), total * 4, hipMemcpyHostToDevice, s));
         const uint32_t* order = d_entry.p;
         if (M() == 16) {  // the staged 16-subspace scan gathers by half-wave
           for (int l = 0; l < produced; ++l)
             for (uint32_t s0 = 0; s0 < list_len_h[l]; s0 += BO_SEG)
-              segs.push_back(make_uint2(count[l] + s0, std::min(BO_SEG, list_len_h[l] - s0)));
+              segs.push_back(make_uint2((uint32_t)count[l] + s0, std::min(BO_SEG, list_len_h[l] - s0)));
           d_banked.reserve(total);
           d_segs.reserve(segs.size());
           PXG_HIP(hipMemcpyAsync(d_segs.p, segs.data(), segs.size() * sizeof(uint2), hipMemcpyHostToDevice, s));
@@ -1700,14 +1765,117 @@ struct IvfPqIndex {
                              codes.p, d_banked.p);
           PXG_HIP(hipGetLastError());
           order = d_banked.p;
+          PXG_HIP(hipMemcpyAsync(entry.data(), d_banked.p, total * 4, hipMemcpyDeviceToHost, s));
         }
-        hipLaunchKernelGGL(ivf_gather_csr, dim3((total + 255) / 256), dim3(256), 0, s, order, (int)total,
-                           ranks.rank.p, codes.p, (int)M(), list_rank.p, list_codes.p);
+        // dense entry i of list l goes to position lbeg[l] + (i - count[l])
+        std::vector<uint32_t> pos(total);
+        for (int l = 0; l < produced; ++l)
+          for (uint64_t i = count[l]; i < count[l + 1]; ++i) pos[i] = lbeg_h[l] + (uint32_t)(i - count[l]);
+        PXG_HIP(hipMemcpyAsync(d_pos.p, pos.data(), total * 4, hipMemcpyHostToDevice, s));
+        hipLaunchKernelGGL(ivf_gather_csr, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, order, (int)total,
+                           (const uint32_t*)d_pos.p, codes.p, (int)M(), list_slot.p, list_codes.p);
         PXG_HIP(hipGetLastError());
+        PXG_HIP(hipStreamSynchronize(s));  // entry holds the banked order now
+        for (uint64_t i = 0; i < total; ++i) {
+          ent_slot_h[pos[i]] = entry[i];
+          pos_h[entry[i]] = pos[i];
+        }
       }
       PXG_HIP(hipStreamSynchronize(s));
       csr_dirty = false;
+      ++view_rebuilds;
     }
+  }
+
+  // Move list l's region to the pool's end with room for `room` entries; a
+  // full pool doubles first (one copy of the used part, amortised over the
+  // appends that filled it). False when the pool would pass 2^32 entries
+  // (the caller lays the view out again instead).
+  bool view_move(int l, uint64_t room) {
+    const uint32_t nc = region_for(room);
+    if (pool_used + nc > pool_cap) {
+      const size_t grown = std::max<size_t>(2 * pool_cap, pool_used + nc);
+      if (grown >= NO_POS) return false;
+      list_slot.grow(grown, pool_used, stream);
+      list_codes.grow(grown * M() + 16, pool_used * M(), stream);
+      ent_slot_h.resize(grown, NO_POS);
+      pool_cap = grown;
+    }
+    const uint32_t nb = (uint32_t)pool_used, len = lend_h[l] - lbeg_h[l];
+    if (len) {
+      PXG_HIP(hipMemcpyAsync(list_slot.p + nb, list_slot.p + lbeg_h[l], (size_t)len * 4, hipMemcpyDeviceToDevice,
+                             stream));
+      PXG_HIP(hipMemcpyAsync(list_codes.p + (size_t)nb * M(), list_codes.p + (size_t)lbeg_h[l] * M(),
+                             (size_t)len * M(), hipMemcpyDeviceToDevice, stream));
+    }
+    for (uint32_t i = 0; i < len; ++i) {
+      const uint32_t sl = ent_slot_h[lbeg_h[l] + i];
+      ent_slot_h[nb + i] = sl;
+      ent_slot_h[lbeg_h[l] + i] = NO_POS;
+      pos_h[sl] = nb + i;
+    }
+    pool_abandoned += lcap_h[l];
+    pool_used += nc;
+    lbeg_h[l] = nb;
+    lend_h[l] = nb + len;
+    lcap_h[l] = nc;
+    ++view_moves;
+    return true;
+  }
+
+  // Append newly encoded slots (list_of_h and codes set) to their lists.
+  void view_append(const std::vector<uint32_t>& sl) {
+    if (!trained || csr_dirty || sl.empty()) return;
+    if (pos_h.size() < cap) pos_h.resize(cap, NO_POS);
+    // room first, so that no region moves after an entry was placed in it
+    std::unordered_map<uint32_t, uint64_t> add;
+    for (uint32_t s0 : sl) add[list_of_h[s0]]++;
+    for (auto& kv : add) {
+      const int l = (int)kv.first;
+      const uint64_t need = (uint64_t)(lend_h[l] - lbeg_h[l]) + kv.second;
+      if (need > lcap_h[l] && !view_move(l, std::max<uint64_t>(need, 2ull * lcap_h[l]))) {
+        csr_dirty = true;  // the next search lays the lists out again
+        return;
+      }
+    }
+    std::vector<uint32_t> pos(sl.size());
+    for (size_t i = 0; i < sl.size(); ++i) {
+      const uint32_t l = list_of_h[sl[i]], p = lend_h[l]++;
+      ++list_len_h[l];
+      ent_slot_h[p] = sl[i];
+      pos_h[sl[i]] = p;
+      pos[i] = p;
+    }
+    DevBuf<uint32_t> d_sl(sl.size()), d_pos(sl.size());
+    PXG_HIP(hipMemcpyAsync(d_sl.p, sl.data(), sl.size() * 4, hipMemcpyHostToDevice, stream));
+    PXG_HIP(hipMemcpyAsync(d_pos.p, pos.data(), pos.size() * 4, hipMemcpyHostToDevice, stream));
+    hipLaunchKernelGGL(ivf_gather_csr, dim3((unsigned)((sl.size() + 255) / 256)), dim3(256), 0, stream,
+                       (const uint32_t*)d_sl.p, (int)sl.size(), (const uint32_t*)d_pos.p, codes.p, (int)M(),
+                       list_slot.p, list_codes.p);
+    PXG_HIP(hipGetLastError());
+    PXG_HIP(hipMemcpyAsync(list_beg.p, lbeg_h.data(), produced * 4, hipMemcpyHostToDevice, stream));
+    PXG_HIP(hipMemcpyAsync(list_end.p, lend_h.data(), produced * 4, hipMemcpyHostToDevice, stream));
+    PXG_HIP(hipStreamSynchronize(stream));
+    // regions left behind by moves: lay the view out again once they are half the pool
+    if (pool_abandoned > pool_used / 2) csr_dirty = true;
+  }
+
+  // Drop slot s (in list l) from the view: the list's last entry fills its place.
+  void view_remove(uint32_t s0, uint32_t l) {
+    if (!trained || csr_dirty || l == UNASSIGNED || s0 >= pos_h.size() || pos_h[s0] == NO_POS) return;
+    const uint32_t p = pos_h[s0], last = lend_h[l] - 1;
+    if (p != last) {
+      const uint32_t t = ent_slot_h[last];
+      hipLaunchKernelGGL(ivf_move_entry, dim3(1), dim3(64), 0, stream, list_slot.p, list_codes.p, (int)M(), last, p);
+      PXG_HIP(hipGetLastError());
+      ent_slot_h[p] = t;
+      pos_h[t] = p;
+    }
+    ent_slot_h[last] = NO_POS;
+    pos_h[s0] = NO_POS;
+    lend_h[l] = last;
+    --list_len_h[l];
+    PXG_HIP(hipMemcpyAsync(list_end.p + l, &lend_h[l], 4, hipMemcpyHostToDevice, stream));
   }
 
   void build_coarse() {
@@ -1769,7 +1937,7 @@ struct IvfPqIndex {
                        d_as.p, (int)sl.size(), d_list_of.p);
     PXG_HIP(hipGetLastError());
     PXG_HIP(hipStreamSynchronize(stream));
-    csr_dirty = true;
+    view_append(sl);
   }
 
   // Encode n prepared rows staged compactly on the device (st[n][ld]) into
@@ -1790,7 +1958,7 @@ struct IvfPqIndex {
     PXG_HIP(hipMemcpyAsync(as.data(), d_as.p, n * 4, hipMemcpyDeviceToHost, stream));
     PXG_HIP(hipStreamSynchronize(stream));
     for (size_t i = 0; i < n; ++i) list_of_h[sl[i]] = as[i];
-    csr_dirty = true;
+    view_append(sl);
   }
 
   // IvfPqIndex::train (ivfpq.rs:735-825)
@@ -1857,6 +2025,7 @@ struct IvfPqIndex {
     books = std::move(B);
     PXG_HIP(hipStreamSynchronize(stream));
     trained = true;
+    csr_dirty = true;  // new lists: the view is laid out again
     build_coarse();
     const double t_enc = std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
     encode_slots(live_slots);
@@ -1953,7 +2122,6 @@ struct IvfPqIndex {
       if (out_slots) out_slots[i] = sl[i];
     }
     ranks.insert(in_ids, sl.data(), n, d_ids.p, stream);
-    csr_dirty = true;  // the list view caches ranks
     if (trained) encode_staged(st.p, sl);
   }
 
@@ -2021,6 +2189,7 @@ struct IvfPqIndex {
     const uint32_t s = it->second;
     by_id.erase(it);
     live[s] = 0;
+    view_remove(s, list_of_h[s]);
     list_of_h[s] = UNASSIGNED;
     slots.release(s);
     const uint32_t un = UNASSIGNED;
@@ -2028,7 +2197,6 @@ struct IvfPqIndex {
     PXG_HIP(hipMemcpyAsync(d_list_of.p + s, &un, 4, hipMemcpyHostToDevice, stream));
     ranks.remove(s, stream);
     PXG_HIP(hipStreamSynchronize(stream));
-    csr_dirty = true;
   }
 
   // The wide search of a trained index over the probes already chosen: all
@@ -2100,7 +2268,7 @@ struct IvfPqIndex {
       hipLaunchKernelGGL(ivf_wide_tables, dim3((unsigned)items), dim3(256), 0, s, Qp, (int)ld, (int)dim, (int)M(),
                          metric, probes, np, (int)g.first, cents.p, books.p, d_sub_off.p, d_book_off.p, tables, omq);
       hipLaunchKernelGGL(ivf_wide_keys, dim3((unsigned)items), dim3(256), 0, s, probes, np, (int)g.first, (int)M(),
-                         metric, tables, omq, list_off.p, list_rank.p, list_codes.p, ranks.rank_slot.p, d_accept,
+                         metric, tables, omq, list_beg.p, list_end.p, list_slot.p, list_codes.p, ranks.rank_slot.p, ranks.rank.p, d_accept,
                          dpofs, keys);
       PXG_HIP(hipGetLastError());
       wide_sort(temp, temp_bytes, keys, sorted, at, (uint32_t)gn, dbeg, dend, s);
@@ -2206,15 +2374,15 @@ struct IvfPqIndex {
         hipLaunchKernelGGL(ivf_coarse_mfma, gd, dim3(256), 0, s, Qp, (int)ld, (int)nq, qn, cents.p, produced,
                            cent_norm.p, cst, A);
         hipLaunchKernelGGL(ivf_coarse_pick_approx, dim3((unsigned)nq), dim3(256), 0, s, (const float*)A, cst,
-                           produced, np, Qp, (int)ld, (int)dim, qn, cents.p, cent_norm.p, probes, list_off.p,
-                           scanned_dev);
+                           produced, np, Qp, (int)ld, (int)dim, qn, cents.p, cent_norm.p, probes, list_beg.p,
+                           list_end.p, scanned_dev);
       } else if (fused_count) {
         uint64_t* keys = (uint64_t*)sc.get(13, (size_t)nq * cst * 8);
         const dim3 gd((unsigned)((nq + IVF_CQ - 1) / IVF_CQ), (unsigned)((produced + IVF_CW * 64 - 1) / (IVF_CW * 64)));
         hipLaunchKernelGGL(ivf_coarse_dist, gd, dim3(IVF_CW * 64), (size_t)dim * IVF_CQ * 4, s, Qp, (int)ld, (int)dim,
                            (int)nq, cents_t.p, cst, produced, keys);
         hipLaunchKernelGGL(ivf_coarse_pick, dim3((unsigned)nq), dim3(256), 0, s, (const uint64_t*)keys, cst, produced,
-                           np, probes, list_off.p, scanned_dev);
+                           np, probes, list_beg.p, list_end.p, scanned_dev);
       } else if (np <= 1024 && coarse) {
         // exact top-nprobe by (squared_l2, list) through the flat pipeline
         const float* Qd = Qp;
@@ -2240,7 +2408,7 @@ struct IvfPqIndex {
       PXG_HIP(hipGetLastError());
       if (!fused_count)
         hipLaunchKernelGGL(ivf_count_scanned, dim3((unsigned)((nq * np + 255) / 256)), dim3(256), 0, s, probes,
-                           (int)(nq * np), list_off.p, scanned_dev);
+                           (int)(nq * np), list_beg.p, list_end.p, scanned_dev);
       const int W = (int)(dim / M());
       // the register-codebook scans keep two distance tables in LDS (one for
       // cosine): an L2 index with 128 subspaces takes the general scan
@@ -2266,8 +2434,8 @@ struct IvfPqIndex {
         const bool fused = groups == 1 && !rerank && kk <= 64;
 #define PXG_SCANR(WW, MET)                                                                                          \
   hipLaunchKernelGGL((ivf_scan_reg<WW, MET>), dim3(grid), dim3(IVF_SW * 64), lds, s, Qp, (int)ld, (int)dim,        \
-                     (int)M(), probes, np, pg, groups, cents.p, books.p, list_off.p, list_rank.p, list_codes.p,      \
-                     ranks.rank_slot.p, d_accept, kk, cand, (int)ldo, d_ids.p, fused ? d_oid : nullptr, d_od, d_oc)
+                     (int)M(), probes, np, pg, groups, cents.p, books.p, list_beg.p, list_end.p, list_slot.p, list_codes.p,      \
+                     ranks.rank_slot.p, ranks.rank.p, d_accept, kk, cand, (int)ldo, d_ids.p, fused ? d_oid : nullptr, d_od, d_oc)
 #define PXG_SCANR_W(MET)                  \
   switch (W) {                            \
     case 1: PXG_SCANR(1, MET); break;     \
@@ -2279,7 +2447,7 @@ struct IvfPqIndex {
   }
 #define PXG_SCAN16(WW, MET)                                                                                         \
   hipLaunchKernelGGL((ivf_scan16<WW, MET>), dim3(grid), dim3(IVF_SW * 64), 0, s, Qp, (int)ld, probes, np, pg, groups, \
-                     cents.p, books.p, list_off.p, list_rank.p, list_codes.p, ranks.rank_slot.p, d_accept, kk, cand,     \
+                     cents.p, books.p, list_beg.p, list_end.p, list_slot.p, list_codes.p, ranks.rank_slot.p, ranks.rank.p, d_accept, kk, cand,     \
                      (int)ldo, d_ids.p, fused ? d_oid : nullptr, d_od, d_oc)
 #define PXG_SCAN16_W(MET)                 \
   switch (W) {                            \
@@ -2323,8 +2491,8 @@ struct IvfPqIndex {
       tm.mark(1);
 #define PXG_SCAN(CAPW, MET)                                                                                       \
   hipLaunchKernelGGL((ivf_scan<CAPW, MET>), dim3(grid), dim3(256), lds, s, Qp, (int)ld, (int)dim, (int)M(), probes, \
-                     np, cents.p, books.p, d_sub_off.p, d_book_off.p, list_off.p, list_rank.p, list_codes.p,       \
-                     ranks.rank_slot.p, d_accept, kk, cand)
+                     np, cents.p, books.p, d_sub_off.p, d_book_off.p, list_beg.p, list_end.p, list_slot.p, list_codes.p,       \
+                     ranks.rank_slot.p, ranks.rank.p, d_accept, kk, cand)
       if (kk <= 192) {
         if (metric == PXG_COSINE) PXG_SCAN(256, 1); else PXG_SCAN(256, 0);
       } else if (kk <= 448) {
@@ -2536,7 +2704,8 @@ int pxg_ivfpq_stats(const pxg_ivfpq* index, pxg_index_stats* out) {
     out->edges = 0;
     out->vector_bytes = f.vectors_kept ? f.X.bytes() : 0;
     // codes, lists and codebooks (ivfpq.rs:575-588, 1207-1212)
-    out->graph_bytes = f.codes.bytes() + f.d_list_of.bytes() + f.list_rank.bytes() + f.list_off.bytes() +
+    out->graph_bytes = f.codes.bytes() + f.d_list_of.bytes() + f.list_slot.bytes() + f.list_beg.bytes() +
+                       f.list_end.bytes() +
                        f.list_codes.bytes() + f.cents.bytes() + f.cents_t.bytes() + f.books.bytes();
   });
 }
@@ -2704,5 +2873,13 @@ int pxg_ivfpq_search_device(const pxg_ivfpq* index, const float* d_queries, uint
 }
 
 uint64_t pxg_ivfpq_last_scanned(void) { return pxg::g_last_scanned; }
+
+int pxg_ivfpq_view_stats(const pxg_ivfpq* index, uint64_t* rebuilds, uint64_t* moves) {
+  return pxg::guard([&] {
+    std::shared_lock<std::shared_mutex> lk(index->impl.mu);
+    if (rebuilds) *rebuilds = index->impl.view_rebuilds;
+    if (moves) *moves = index->impl.view_moves;
+  });
+}
 
 }  // extern "C"

@@ -512,3 +512,103 @@ def test_corrupt_load_changes_nothing(gpu):
     for a, b in zip(before, after):
         assert np.array_equal(a, b)
     assert np.array_equal(idx.parts()[0], cents)
+
+
+def _oracle_state(idx, vectors_by_slot, cents, books, m):
+    """The index's current slots (ids, live) and the oracle's own encoding of
+    their vectors (ivfpq.rs:828-898)."""
+    ids, live = idx.slots()
+    codes, list_of = orc.ivf_encode(vectors_by_slot[: ids.size], cents, books, m, live=live)
+    return ids, live, codes, list_of
+
+
+@pytest.mark.parametrize("dim,m,rerank", [(32, 16, 0), (32, 16, 40), (16, 8, 0)])
+def test_interleaved_mutations_and_searches(gpu, dim, m, rerank):
+    """Removals and inserts between searches update the list view in place
+    (appends, holes filled by each list's last entry, regions moved when
+    full); every search equals the oracle's on the state at that moment
+    (ivfpq.rs:1129-1180 then 998-1110)."""
+    px = gpu
+    rng = np.random.default_rng(dim + m + rerank)
+    n, nlist = 6000, 24
+    data = corpus(n, dim, 20) + rng.standard_normal((n, dim)).astype(np.float32) * 0.2
+    cents, books, _ = orc.ivf_train(data, nlist, m, max_iter=8, seed=4)
+    codes, list_of = orc.ivf_encode(data, cents, books, m)
+    cfg = px.IvfPqConfig(nlist, m).with_train_threshold(1 << 62).with_rerank(rerank)
+    idx = build(px, data, cfg)
+    idx.load_trained(cents, books, codes, list_of)
+    vec = np.zeros((4 * n, dim), np.float32)  # vectors by slot
+    vec[:n] = data
+    q = data[5::211] + 0.07
+    next_id = 10 ** 6
+    idx.search_batch(q, 10, nprobe=4)  # lays the view out
+    rebuilds0, _ = idx.view_stats()
+    for cycle in range(6):
+        ids, live = idx.slots()
+        present = ids[live.astype(bool)]
+        for i in rng.choice(present, size=150, replace=False):
+            idx.remove(int(i))
+        # new vectors: half near one centroid (its region fills and moves), half spread
+        near = cents[cycle % nlist] + rng.standard_normal((200, dim)).astype(np.float32) * 0.05
+        spread = data[rng.integers(0, n, 200)] * np.float32(1.02)
+        new = np.concatenate([near, spread]).astype(np.float32)
+        new_ids = np.arange(next_id, next_id + new.shape[0], dtype=np.uint64)
+        next_id += new.shape[0]
+        slots = idx.insert_batch(new_ids, new)
+        vec[slots] = new
+        ids, live, codes2, list_of2 = _oracle_state(idx, vec, cents, books, m)
+        _, _, gc, glo = idx.parts()
+        lv = live.astype(bool)
+        assert np.array_equal(glo[lv], list_of2[lv]) and np.array_equal(gc[lv], codes2[lv])
+        for nprobe, k in ((4, 10), (24, 7)):
+            got = idx.search_batch(q, k, nprobe=nprobe)
+            want = orc.ivf_search(0, cents, books, codes2, list_of2, ids, q, k, nprobe, m,
+                                  vectors=vec[: ids.size] if rerank else None, rerank=rerank, live=live, threads=8)
+            assert_same(got, want)
+        acc = (ids % 3 != 0).astype(np.uint8)
+        got = idx.search_batch(q, 10, lambda i, _m: i % 3 != 0, nprobe=6)
+        want = orc.ivf_search(0, cents, books, codes2, list_of2, ids, q, 10, 6, m,
+                              vectors=vec[: ids.size] if rerank else None, rerank=rerank, live=live, accept=acc,
+                              threads=8)
+        assert_same(got, want)
+    rebuilds, moves = idx.view_stats()
+    assert rebuilds == rebuilds0  # every mutation was applied in place
+    assert moves > 0  # the filled regions moved
+
+
+def test_list_view_growth_and_compaction(gpu):
+    """A batch far beyond the slack of one list: its region moves and the pool
+    grows in place; a compaction then lays the view out again. Results equal
+    the oracle's throughout."""
+    px = gpu
+    rng = np.random.default_rng(3)
+    n, dim, m, nlist = 3000, 16, 8, 8
+    data = corpus(n, dim, 10)
+    cents, books, _ = orc.ivf_train(data, nlist, m, max_iter=6, seed=2)
+    codes, list_of = orc.ivf_encode(data, cents, books, m)
+    idx = build(px, data, px.IvfPqConfig(nlist, m).with_train_threshold(1 << 62))
+    idx.load_trained(cents, books, codes, list_of)
+    q = data[::301] + 0.1
+    idx.search_batch(q, 5, nprobe=2)
+    r0, m0 = idx.view_stats()
+    new = (cents[0] + rng.standard_normal((4 * n, dim)) * 0.01).astype(np.float32)
+    slots = idx.insert_batch(np.arange(n, 5 * n, dtype=np.uint64), new)
+    vec = np.zeros((5 * n, dim), np.float32)
+    vec[:n] = data
+    vec[slots] = new
+    ids, live, codes2, list_of2 = _oracle_state(idx, vec, cents, books, m)
+    assert_same(idx.search_batch(q, 5, nprobe=2),
+                orc.ivf_search(0, cents, books, codes2, list_of2, ids, q, 5, 2, m, live=live, threads=8))
+    r1, m1 = idx.view_stats()
+    assert r1 == r0 and m1 > m0
+    for i in range(0, n, 2):
+        idx.remove(i)
+    assert idx.compact() > 0
+    ids, live = idx.slots()
+    vec2 = np.zeros_like(vec)
+    for s_, i in enumerate(ids):
+        vec2[s_] = data[int(i)] if i < n else new[int(i) - n]
+    ids, live, codes3, list_of3 = _oracle_state(idx, vec2, cents, books, m)
+    assert_same(idx.search_batch(q, 5, nprobe=2),
+                orc.ivf_search(0, cents, books, codes3, list_of3, ids, q, 5, 2, m, live=live, threads=8))
+    assert idx.view_stats()[0] == r1 + 1
