@@ -375,7 +375,8 @@ constexpr int IVF_SCAN_SLOTS = 64;
 __global__ __launch_bounds__(256) void ivf_coarse_pick(const uint64_t* __restrict__ ck, int cst, int produced, int np,
                                                        int* __restrict__ probes, const uint32_t* __restrict__ list_beg,
                                                        const uint32_t* __restrict__ list_end,
-                                                       unsigned long long* __restrict__ scanned) {
+                                                       unsigned long long* __restrict__ scanned,
+                                                       uint32_t* __restrict__ qwork) {
   const int q = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   __shared__ uint64_t cand[IVF_PICK_CAP];
   __shared__ uint64_t gmin[64];
@@ -454,6 +455,7 @@ __global__ __launch_bounds__(256) void ivf_coarse_pick(const uint64_t* __restric
 #pragma unroll
     for (int st = 32; st > 0; st >>= 1) len += xor_lane_rt(len, st);
     if (lane == 0) atomicAdd(scanned + (q & (IVF_SCAN_SLOTS - 1)), (unsigned long long)len);
+    if (lane == 0 && qwork) qwork[q] = len;
   }
 }
 
@@ -522,7 +524,8 @@ __global__ __launch_bounds__(256) void ivf_coarse_pick_approx(const float* __res
                                                               int* __restrict__ probes,
                                                               const uint32_t* __restrict__ list_beg,
                                                               const uint32_t* __restrict__ list_end,
-                                                              unsigned long long* __restrict__ scanned) {
+                                                              unsigned long long* __restrict__ scanned,
+                                                              uint32_t* __restrict__ qwork) {
   const int q = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   __shared__ uint64_t cand[IVF_PICK_CAP];
   __shared__ int cl[IVF_PICK_CAP];
@@ -662,6 +665,7 @@ __global__ __launch_bounds__(256) void ivf_coarse_pick_approx(const float* __res
 #pragma unroll
     for (int st = 32; st > 0; st >>= 1) len += xor_lane_rt(len, st);
     if (lane == 0) atomicAdd(scanned + (q & (IVF_SCAN_SLOTS - 1)), (unsigned long long)len);
+    if (lane == 0 && qwork) qwork[q] = len;
   }
 }
 
@@ -709,7 +713,8 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan_reg(const float* __restr
                                                          uint64_t* __restrict__ out, int k,
                                                          const uint64_t* __restrict__ ids,
                                                          uint64_t* __restrict__ out_ids, float* __restrict__ out_d,
-                                                         uint32_t* __restrict__ out_count) {
+                                                         uint32_t* __restrict__ out_count,
+                                                         const int* __restrict__ qorder) {
   constexpr int MMAX = 128 / W, MH = (MMAX + 1) / 2;
   extern __shared__ float lut[];  // 2 x M * 256 floats (cosine: one table)
   __shared__ uint64_t s_kept[IVF_SW][64];
@@ -717,7 +722,8 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan_reg(const float* __restr
   __shared__ float s_qdc[IVF_PGMAX];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int c = tid & 255, half = tid >> 8;
-  const int q = blockIdx.x / groups, grp = blockIdx.x % groups;
+  const int qi = blockIdx.x / groups, grp = blockIdx.x % groups;
+  const int q = qorder ? qorder[qi] : qi;
   const int p0 = grp * pg, np = min(nprobe, p0 + pg) - p0;
   const int mh = (M + 1) / 2;           // subspaces per half
   const int sb = half * mh;             // this thread's first subspace
@@ -954,7 +960,8 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan16(const float* __restric
                                                           uint64_t* __restrict__ out, int k,
                                                           const uint64_t* __restrict__ ids,
                                                           uint64_t* __restrict__ out_ids, float* __restrict__ out_d,
-                                                          uint32_t* __restrict__ out_count) {
+                                                          uint32_t* __restrict__ out_count,
+                                                          const int* __restrict__ qorder) {
   constexpr int M = 16, DIM = 16 * W, MH = 8, NT = METRIC == 0 ? 2 : 1;
   __shared__ __align__(16) float tabs[NT][M * 256];
   __shared__ __align__(16) float srs[IVF_PGMAX][DIM];
@@ -968,7 +975,8 @@ __global__ __launch_bounds__(IVF_SW * 64) void ivf_scan16(const float* __restric
   // t%32 + 32*(i ^ (ts&1)), i < 8: one residual slice per table, and the two
   // half-waves (even and odd subspace) write distinct banks at every store
   const int ts = tid >> 5, g = tid & 31, flip = ts & 1;
-  const int q = blockIdx.x / groups, grp = blockIdx.x % groups;
+  const int qi = blockIdx.x / groups, grp = blockIdx.x % groups;
+  const int q = qorder ? qorder[qi] : qi;
   const int p0 = grp * pg, np = min(nprobe, p0 + pg) - p0;
   const int* pq = probes + (size_t)q * nprobe + p0;
   float breg[MH][W];
@@ -1296,6 +1304,43 @@ __global__ __launch_bounds__(256) void ivf_merge(const uint64_t* __restrict__ ca
 __global__ void ivf_probes_from_ids(const uint64_t* __restrict__ ids, int n, int* __restrict__ probes) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) probes[i] = (int)ids[i];
+}
+
+// Longest first: the scan's workgroups take queries in descending order of
+// the entries their probes hold (buckets of 256 entries), so the last
+// workgroups of a batch are short ones and the tail of the launch is short.
+// Each query's results come from its own workgroup whatever the order.
+constexpr int LPT_BUCKETS = 1024, LPT_MAXQ = 8192;
+__global__ __launch_bounds__(1024) void ivf_lpt_order(const uint32_t* __restrict__ qwork, int nq,
+                                                      int* __restrict__ qorder) {
+  __shared__ uint32_t cnt[LPT_BUCKETS];
+  __shared__ uint16_t key[LPT_MAXQ];
+  __shared__ uint32_t wsum[16];
+  const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
+  cnt[t] = 0;
+  __syncthreads();
+  for (int q = t; q < nq; q += 1024) {
+    const uint32_t b = (uint32_t)(LPT_BUCKETS - 1) - min(qwork[q] >> 8, (uint32_t)(LPT_BUCKETS - 1));
+    key[q] = (uint16_t)b;
+    atomicAdd(&cnt[b], 1u);
+  }
+  __syncthreads();
+  // exclusive prefix over the buckets: wave scans joined through the wave totals
+  const uint32_t v = cnt[t];
+  uint32_t x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wsum[wid] = x;
+  __syncthreads();
+  uint32_t before = 0;
+  for (int i = 0; i < wid; ++i) before += wsum[i];
+  __syncthreads();
+  cnt[t] = before + x - v;
+  __syncthreads();
+  for (int q = t; q < nq; q += 1024) qorder[atomicAdd(&cnt[key[q]], 1u)] = q;
 }
 
 __global__ void ivf_count_scanned(const int* __restrict__ probes, int n, const uint32_t* __restrict__ list_beg,
@@ -2365,6 +2410,8 @@ struct IvfPqIndex {
       hipLaunchKernelGGL(fill_u32, dim3(1), dim3(2 * IVF_SCAN_SLOTS), 0, s, (uint32_t*)scanned_dev,
                          (size_t)(2 * IVF_SCAN_SLOTS), 0u);
       const bool fused_count = np <= 64 && dim <= 2048;
+      // entries per query (written by the fused pick), for the longest-first order
+      uint32_t* qwork = fused_count && nq <= (uint64_t)LPT_MAXQ ? (uint32_t*)sc.get(16, nq * 4) : nullptr;
       // matrix-core distances with exact rescoring near the cut, for widths
       // where the GEMM outweighs the rescoring
       const bool coarse_mfma = fused_count && dim >= 32 && ld % 8 == 0 && np <= produced;
@@ -2375,14 +2422,14 @@ struct IvfPqIndex {
                            cent_norm.p, cst, A);
         hipLaunchKernelGGL(ivf_coarse_pick_approx, dim3((unsigned)nq), dim3(256), 0, s, (const float*)A, cst,
                            produced, np, Qp, (int)ld, (int)dim, qn, cents.p, cent_norm.p, probes, list_beg.p,
-                           list_end.p, scanned_dev);
+                           list_end.p, scanned_dev, qwork);
       } else if (fused_count) {
         uint64_t* keys = (uint64_t*)sc.get(13, (size_t)nq * cst * 8);
         const dim3 gd((unsigned)((nq + IVF_CQ - 1) / IVF_CQ), (unsigned)((produced + IVF_CW * 64 - 1) / (IVF_CW * 64)));
         hipLaunchKernelGGL(ivf_coarse_dist, gd, dim3(IVF_CW * 64), (size_t)dim * IVF_CQ * 4, s, Qp, (int)ld, (int)dim,
                            (int)nq, cents_t.p, cst, produced, keys);
         hipLaunchKernelGGL(ivf_coarse_pick, dim3((unsigned)nq), dim3(256), 0, s, (const uint64_t*)keys, cst, produced,
-                           np, probes, list_beg.p, list_end.p, scanned_dev);
+                           np, probes, list_beg.p, list_end.p, scanned_dev, qwork);
       } else if (np <= 1024 && coarse) {
         // exact top-nprobe by (squared_l2, list) through the flat pipeline
         const float* Qd = Qp;
@@ -2428,6 +2475,13 @@ struct IvfPqIndex {
         const int groups = (np + pg - 1) / pg;
         uint64_t* cand = (uint64_t*)sc.get(10, (size_t)nq * groups * IVF_SW * kk * 8);
         const int grid = (int)(nq * groups);
+        // queries longest first (two or more rounds of workgroups)
+        int* qorder = nullptr;
+        if (qwork && grid > 512) {
+          qorder = (int*)sc.get(15, nq * 4);
+          hipLaunchKernelGGL(ivf_lpt_order, dim3(1), dim3(1024), 0, s, (const uint32_t*)qwork, (int)nq, qorder);
+          PXG_HIP(hipGetLastError());
+        }
         tm.mark(1);
         // one group per query, no rerank and a shortlist within one key per
         // lane: the scan writes the results
@@ -2435,7 +2489,8 @@ struct IvfPqIndex {
 #define PXG_SCANR(WW, MET)                                                                                          \
   hipLaunchKernelGGL((ivf_scan_reg<WW, MET>), dim3(grid), dim3(IVF_SW * 64), lds, s, Qp, (int)ld, (int)dim,        \
                      (int)M(), probes, np, pg, groups, cents.p, books.p, list_beg.p, list_end.p, list_slot.p, list_codes.p,      \
-                     ranks.rank_slot.p, ranks.rank.p, d_accept, kk, cand, (int)ldo, d_ids.p, fused ? d_oid : nullptr, d_od, d_oc)
+                     ranks.rank_slot.p, ranks.rank.p, d_accept, kk, cand, (int)ldo, d_ids.p, fused ? d_oid : nullptr, d_od, d_oc, \
+                     (const int*)qorder)
 #define PXG_SCANR_W(MET)                  \
   switch (W) {                            \
     case 1: PXG_SCANR(1, MET); break;     \
@@ -2448,7 +2503,7 @@ struct IvfPqIndex {
 #define PXG_SCAN16(WW, MET)                                                                                         \
   hipLaunchKernelGGL((ivf_scan16<WW, MET>), dim3(grid), dim3(IVF_SW * 64), 0, s, Qp, (int)ld, probes, np, pg, groups, \
                      cents.p, books.p, list_beg.p, list_end.p, list_slot.p, list_codes.p, ranks.rank_slot.p, ranks.rank.p, d_accept, kk, cand,     \
-                     (int)ldo, d_ids.p, fused ? d_oid : nullptr, d_od, d_oc)
+                     (int)ldo, d_ids.p, fused ? d_oid : nullptr, d_od, d_oc, (const int*)qorder)
 #define PXG_SCAN16_W(MET)                 \
   switch (W) {                            \
     case 1: PXG_SCAN16(1, MET); break;    \
