@@ -134,11 +134,13 @@ __device__ inline void compact_row(uint64_t* __restrict__ base, int c, int Kp, i
     compact_row_w<CAP>(base, c, Kp, lane, thr_row, thrf_row, cnt_row, gthr_row, final_pass);
 }
 
-template <int CAP>
+// SEED: the seeding pass (a separate instantiation, so that the full pass's
+// code is not shaped by the seeding epilogue).
+template <int CAP, bool SEED>
 __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
     const float* __restrict__ Q, int nq, const float* __restrict__ X, int N, int ld,
     const float* __restrict__ qb, const float* __restrict__ xb, float scale, const uint8_t* __restrict__ live,
-    const uint8_t* __restrict__ accept, int S, int QB, int per_split, int seed, int Kp,
+    const uint8_t* __restrict__ accept, int S, int QB, int per_split, int Kp,
     uint64_t* __restrict__ cand, unsigned long long* __restrict__ gthr) {
   __shared__ __align__(16) float sQ[2][FB_M * FB_K];
   __shared__ __align__(16) float sX[2][FB_N * FB_K];
@@ -160,7 +162,7 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
   const int q0 = qblk * FB_M;
   const int s_begin = split * per_split;
   // a seeding pass visits only the first tile of each split
-  const int s_end = min(N, s_begin + (seed ? FB_N : per_split));
+  const int s_end = min(N, s_begin + (SEED ? FB_N : per_split));
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int h = lane >> 5, r = lane & 31;
@@ -301,7 +303,29 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
     // four rows' norms and thresholds per LDS read. That test passes every
     // key below thr[row] (key_float inverts ord_key; NaN and the sign of zero
     // pass), so only the marked values take the exact key test and append.
-    {
+    if constexpr (SEED) {
+      // Seeding pass: every usable value of its one tile is kept, so each
+      // lane writes its distance part straight to its column of the row's
+      // buffer, read as 32-bit words (no counters, no atomics; the seed
+      // threshold needs only the distance parts); unusable slots hold
+      // 0xFFFFFFFF.
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const bool ok = (slotj[j] < s_end) & ((lvj[j] & acj[j]) != 0u);
+        const float xo = ok ? xbr[j] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int row = wm + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+            if (q0 + row < nq) {
+              const float a = __builtin_fmaf(-scale, acc[i][j][v], sqb[row] + xo);
+              reinterpret_cast<uint32_t*>(cand + ((size_t)(q0 + row) * S + split) * CAP)[wn + j * 32 + r] =
+                  ok ? ord_key(a) : 0xFFFFFFFFu;
+            }
+          }
+      }
+    } else {
       // Validity as bit masks applied once per row group (usable slots: the
       // j halves; rows below nq: both halves), so that the per-value work is
       // straight-line code: one compare and one select into the mask.
@@ -366,16 +390,8 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
     }
     __syncthreads();
   }
-  if (seed) {
-    // Seeding pass: each row leaves its one tile's keys unsorted, KEY_MAX
-    // padded to FB_N.
-    for (int row = wid; row < FB_M; row += 4) {
-      if (q0 + row >= nq) continue;
-      uint64_t* base = cand + ((size_t)(q0 + row) * S + split) * CAP;
-      for (int i = cnt[row] + lane; i < FB_N; i += WAVE) base[i] = KEY_MAX;
-    }
-    return;
-  }
+  // Seeding pass: each row has left its one tile's FB_N distance parts.
+  if constexpr (SEED) return;
   // Final: every row leaves Kp keys, its Kp smallest (KEY_MAX padded). The
   // merge reads them as a set, so a row with at most Kp keys is only padded;
   // a fuller one is sorted down to Kp.
@@ -394,8 +410,9 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
 // ---------------------------------------------------------------------------
 // 3. merge + exact rescore (approximate candidates)
 // ---------------------------------------------------------------------------
-// Per query: the Kp-th smallest distance part over the keys a seeding pass
-// left (the first tile of every split, FB_N keys per split, KEY_MAX padded).
+// Per query: the Kp-th smallest distance part over the words a seeding pass
+// left (the first tile of every split, FB_N 32-bit distance parts per split
+// at the start of its buffer, 0xFFFFFFFF for unusable slots).
 // The full pass meets all of those rows again, so a threshold above every
 // key with that distance part (the strict key test passes them all) leaves
 // at least Kp rows, the query's Kp best among them, in its lists.
@@ -405,7 +422,8 @@ __global__ __launch_bounds__(512) void flat_seed_threshold(const uint64_t* __res
   __shared__ uint64_t sh[4];
   const int q = blockIdx.x;
   const uint64_t* c = cand + (size_t)q * S * CAP;
-  auto get = [&](int i) { return c[(size_t)(i / FB_N) * CAP + i % FB_N] >> 32; };
+  const uint32_t* c32 = reinterpret_cast<const uint32_t*>(c);
+  auto get = [&](int i) { return (uint64_t)c32[(size_t)(i / FB_N) * (2 * CAP) + i % FB_N]; };
   const int n = S * FB_N;
   const uint64_t hi = n <= 16 * (int)blockDim.x ? block_radix_select<decltype(get), 32, 16>(get, n, Kp, hist, sh)
                                     : block_radix_select<decltype(get), 32>(get, n, Kp, hist, sh);
@@ -693,13 +711,14 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
     tm.mark(1);
     const int grid = ((total + 7) / 8) * 8;
     const float scale = metric == PXG_EUCLIDEAN ? 2.0f : 1.0f;
-    auto candidates = [&](int seed) {
+    auto candidates = [&](auto seed) {
+      constexpr bool SD = decltype(seed)::value;
       if (CAP == 256)
-        hipLaunchKernelGGL(flat_mfma_candidates<256>, dim3(grid), dim3(256), 0, s, Qp, (int)nq, X.p, (int)N, (int)ld,
-                           qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, seed, Kp, cand, gthr);
+        hipLaunchKernelGGL((flat_mfma_candidates<256, SD>), dim3(grid), dim3(256), 0, s, Qp, (int)nq, X.p, (int)N,
+                           (int)ld, qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, Kp, cand, gthr);
       else
-        hipLaunchKernelGGL(flat_mfma_candidates<512>, dim3(grid), dim3(256), 0, s, Qp, (int)nq, X.p, (int)N, (int)ld,
-                           qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, seed, Kp, cand, gthr);
+        hipLaunchKernelGGL((flat_mfma_candidates<512, SD>), dim3(grid), dim3(256), 0, s, Qp, (int)nq, X.p, (int)N,
+                           (int)ld, qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, Kp, cand, gthr);
       PXG_HIP(hipGetLastError());
     };
     // With several tiles per split, a first pass over the first tile of each
@@ -707,12 +726,12 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
     // the Kp-th best of those rows, so the full pass appends and compacts
     // little from its first tile on.
     if (tiles_per >= 8) {
-      candidates(1);
+      candidates(std::true_type{});
       hipLaunchKernelGGL(flat_seed_threshold, dim3((unsigned)nq), dim3(512), 0, s, (const uint64_t*)cand, S, CAP, Kp,
                          gthr);
       PXG_HIP(hipGetLastError());
     }
-    candidates(0);
+    candidates(std::false_type{});
     tm.mark(2);
     hipLaunchKernelGGL(flat_merge_rescore, dim3((unsigned)nq), dim3(256), 0, s, cand, S, CAP, Kp, (int)kq, Qp,
                        (int)ld, (int)dim, metric, X.p, ranks.rank.p, ranks.rank_slot.p, d_ids.p, qn, maxnorm, 4.0f,
