@@ -1994,7 +1994,32 @@ struct IvfPqIndex {
     DevBuf<uint32_t> d_sl(n), d_as(n);
     DevBuf<uint8_t> tmp(n * M());
     PXG_HIP(hipMemcpyAsync(d_sl.p, sl.data(), n * 4, hipMemcpyHostToDevice, stream));
-    nearest_device(st, (int)ld, nullptr, n, (int)dim, cents.p, (int)ld, produced, true, d_as.p, nullptr, stream);
+    if (n < 4096 && coarse) {
+      // Few rows (inserts into a trained index): nearest_centroid
+      // (ivfpq.rs:1231-1243, unrolled kernel, first minimum) as the exact
+      // flat search of k = 1 over the centroids, whose (distance, list)
+      // order gives the same list; it spreads the centroids over the GPU
+      // instead of one thread per row scanning them all.
+      const float* q = st;
+      DevBuf<float> dense;
+      if (ld != dim) {
+        dense.alloc(n * dim);
+        PXG_HIP(hipMemcpy2DAsync(dense.p, dim * 4, st, ld * 4, dim * 4, n, hipMemcpyDeviceToDevice, stream));
+        q = dense.p;
+      }
+      DevBuf<uint64_t> cid(n);
+      DevBuf<float> cd(n);
+      DevBuf<uint32_t> cc(n);
+      CtxLease cl(coarse->pool);
+      CtxScratch csc(cl.c);
+      uint64_t fb = 0;
+      coarse->search_device(q, false, n, 1, nullptr, cid.p, cd.p, cc.p, csc, stream, &fb, 1);
+      hipLaunchKernelGGL(ivf_probes_from_ids, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                         (const uint64_t*)cid.p, (int)n, (int*)d_as.p);
+      PXG_HIP(hipGetLastError());
+    } else {
+      nearest_device(st, (int)ld, nullptr, n, (int)dim, cents.p, (int)ld, produced, true, d_as.p, nullptr, stream);
+    }
     pq_encode_device(st, (int)ld, nullptr, n, (int)dim, cents.p, (int)ld, d_as.p, books.p, pq, tmp.p, stream);
     hipLaunchKernelGGL(ivf_scatter_codes, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, tmp.p, d_sl.p,
                        d_as.p, (int)n, (int)M(), codes.p, d_list_of.p);
