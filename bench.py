@@ -144,6 +144,8 @@ def bench_c1(args, torch, px, dev):
     qh = q.cpu().numpy()
     log(f"[bench] c1: {step_s * 1e3:.3f} ms/batch = {nq / step_s:.0f} QPS; candidate GEMM {cand_ms:.3f} ms = "
         f"{tflops:.1f} TFLOP/s")
+    if args.profile_core:
+        return {"ms_per_step": round(step_s * 1e3, 4), "candidates_ms": round(cand_ms, 4)}
     out = {"value": round(nq / step_s, 2), "unit": "queries/s", "ms_per_step": round(step_s * 1e3, 4), "steps": steps,
            "config": {"workload": "flat exact search, Euclidean, 100k x 128 f32 (100 Gaussian clusters, sigma 0.15), "
                                   "1,000 queries in one batch, k=10", "n": n, "dim": dim, "batch": nq, "k": k,
@@ -152,7 +154,9 @@ def bench_c1(args, torch, px, dev):
            "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
                         "frac": round(tflops / PEAK_FP32_MFMA_TFLOPS, 4),
                         "traffic": load_traffic("flat_mfma_candidates_c1"),
-                        "kernel": "flat_mfma_candidates", "ms_per_launch": round(cand_ms, 4)},
+                        "kernel": "flat_mfma_candidates",
+                        "timed": "the candidate stage: seeding pass, flat_seed_threshold and full pass",
+                        "ms_per_launch": round(cand_ms, 4)},
            "stage_ms": {key: round(float(np.mean([t[key] for t in stages])), 4) for key in stages[0]},
            "host_path": host_path(idx.search_batch, [qh], k),
            "latency_batch1": latency_batch1(idx.search_all, qh, k)}
@@ -229,6 +233,9 @@ def bench_ivfpq(args, torch, px, dev):
     gbs = bytes_per_launch / (scan_ms * 1e-3) / 1e9
     log(f"[bench] ivfpq: {step_s * 1e3:.3f} ms/step = {B / step_s:.0f} QPS; scan {scan_ms:.3f} ms, "
         f"{bytes_per_launch / 1e9:.3f} GB/launch = {gbs:.0f} GB/s")
+    if args.profile_core:
+        return {"ms_per_step": round(step_s * 1e3, 4), "scan_ms": round(scan_ms, 4),
+                "scanned_entries": float(np.mean(scanned))}
     # recall@10 against the exact GPU flat index over the same vectors
     m = 1024
     flat = px.FlatIndex(px.VectorSpace(dim, px.Metric.EUCLIDEAN), n)
@@ -438,6 +445,8 @@ def bench_sq8(args, torch, px, dev):
     tops = 2.0 * n * dim * B / (scan_ms * 1e-3) / 1e12
     log(f"[bench] sq8: {step_s * 1e3:.3f} ms/step = {B / step_s:.0f} QPS; stage-2 scan {scan_ms:.3f} ms = "
         f"{tops:.0f} TOP/s; fallback queries {fallbacks}")
+    if args.profile_core:
+        return {"ms_per_step": round(step_s * 1e3, 4), "scan_ms": round(scan_ms, 4)}
     # recall@10 against exact f32 inner product over the same vectors
     m = 200
     qh = queries.cpu().numpy()
@@ -675,6 +684,9 @@ def main():
                     help="k-means leg without the PQ training (one host thread; for counter profiling)")
     ap.add_argument("--km-cpu-sample", type=int, default=131072)
     ap.add_argument("--skip-fixture", action="store_true")
+    ap.add_argument("--profile-core", action="store_true",
+                    help="only the timed and stage-timed batches of the leg that runs (the flat cosine leg, or "
+                         "the one --c1-only, --ivf-only or --sq8-only picks; for profiler runs)")
     ap.add_argument("--fixture-only", action="store_true", help="run only the fixture leg (prints its JSON object)")
     ap.add_argument("--fx-n", type=int, default=10_000_000)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -692,6 +704,15 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_probe_mib:
+        src = torch.empty(args.copy_probe_mib << 18, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] copy probe: {args.copy_probe_mib} MiB device-to-device copy")
+        del src, dst
+        torch.cuda.empty_cache()
     if args.c1_only:
         print(json.dumps(bench_c1(args, torch, px, dev)), flush=True)
         return
@@ -721,15 +742,6 @@ def main():
         x_host = x.cpu().numpy()
     del x
     torch.cuda.empty_cache()
-
-    if args.copy_probe_mib:
-        src = torch.empty(args.copy_probe_mib << 18, dtype=torch.float32, device=dev).fill_(1.0)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        log(f"[bench] copy probe: {args.copy_probe_mib} MiB device-to-device copy")
-        del src, dst
 
     nb = args.queries // B
     batches = [queries[i * B:(i + 1) * B] for i in range(nb)]
@@ -765,6 +777,9 @@ def main():
     flops = 2.0 * n * dim * B
     achieved = flops / (cand_ms * 1e-3) / 1e12
     log(f"[bench] k={args.k}: {step_s * 1e3:.3f} ms/step, candidate GEMM {cand_ms:.3f} ms = {achieved:.1f} TFLOP/s")
+    if args.profile_core:
+        print(json.dumps({"ms_per_step": round(step_s * 1e3, 4), "candidates_ms": round(cand_ms, 4)}), flush=True)
+        return
 
     k2 = 100
     step100, stages100, fb100 = run(k2, max(5, args.steps // 2), 1, prof=True)
