@@ -239,10 +239,10 @@ constexpr int KA_M = 128, KA_N = 128, KA_K = 32;
 
 // |row|^2 in fp32 (any order; it only feeds the approximation): eight lanes
 // per row, float4 loads (rows 16-byte aligned, dim a multiple of 4).
-__global__ __launch_bounds__(256) void km_row_norms(const float* __restrict__ P, int ldp,
-                                                    const uint32_t* __restrict__ rows, int n, int dim,
-                                                    float* __restrict__ out) {
-  const int i = blockIdx.x * 32 + (threadIdx.x >> 3), sub = threadIdx.x & 7;
+__device__ __forceinline__ void km_row_norms_body(const float* __restrict__ P, int ldp,
+                                                  const uint32_t* __restrict__ rows, int n, int dim,
+                                                  float* __restrict__ out, int bx) {
+  const int i = bx * 32 + (threadIdx.x >> 3), sub = threadIdx.x & 7;
   float s = 0.0f;
   if (i < n) {
     const float* pr = P + (size_t)(rows ? rows[i] : (uint32_t)i) * ldp;
@@ -255,6 +255,11 @@ __global__ __launch_bounds__(256) void km_row_norms(const float* __restrict__ P,
   s += __shfl_xor(s, 2, WAVE);
   s += __shfl_xor(s, 1, WAVE);
   if (i < n && sub == 0) out[i] = s;
+}
+__global__ __launch_bounds__(256) void km_row_norms(const float* __restrict__ P, int ldp,
+                                                    const uint32_t* __restrict__ rows, int n, int dim,
+                                                    float* __restrict__ out) {
+  km_row_norms_body(P, ldp, rows, n, dim, out, blockIdx.x);
 }
 
 // The largest of v[0..n), or NaN if any is NaN.
@@ -457,15 +462,15 @@ __global__ __launch_bounds__(256, 2) void km_mfma_top(const float* __restrict__ 
 constexpr int KS_MAXF = 8192;  // centroid floats staged in LDS (32 KB)
 constexpr int KS_PW = 4;       // 32-point groups per wave
 template <int DS>  // dim = 8 DS
-__global__ __launch_bounds__(256, 2) void km_mfma_small(const float* __restrict__ P, int ldp,
-                                                     const uint32_t* __restrict__ rows, int n,
-                                                     const float* __restrict__ C, int ldc, int k,
-                                                     const float* __restrict__ cn, uint32_t* __restrict__ best_idx,
-                                                     float* __restrict__ best, float* __restrict__ second) {
+__device__ __forceinline__ void km_mfma_small_body(const float* __restrict__ P, int ldp,
+                                                   const uint32_t* __restrict__ rows, int n,
+                                                   const float* __restrict__ C, int ldc, int k,
+                                                   const float* __restrict__ cn, uint32_t* __restrict__ best_idx,
+                                                   float* __restrict__ best, float* __restrict__ second,
+                                                   float* __restrict__ sc, int bx) {
   constexpr int D = 8 * DS, HD = D / 2;
-  extern __shared__ float4 ks_sm[];
-  float* sc = reinterpret_cast<float*>(ks_sm);  // [k][D]
-  float* scn = sc + k * D;                      // [k rounded up to 32]
+  // sc: [k][D] centroids, then their norms [k rounded up to 32]
+  float* scn = sc + k * D;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, r = lane & 31;
   for (int f = tid; f < k * 2 * DS; f += 256) {
     const int row = f / (2 * DS), c4 = (f - row * 2 * DS) * 4;
@@ -476,7 +481,7 @@ __global__ __launch_bounds__(256, 2) void km_mfma_small(const float* __restrict_
   __syncthreads();
   const int nblk = kr / 32;
   for (int g = 0; g < KS_PW; ++g) {
-    const int p0 = ((blockIdx.x * 4 + w) * KS_PW + g) * 32;
+    const int p0 = ((bx * 4 + w) * KS_PW + g) * 32;
     if (p0 >= n) break;  // wave-uniform
     const int pi = min(p0 + r, n - 1);
     const float* prow = P + (size_t)(rows ? rows[pi] : (uint32_t)pi) * ldp + h * HD;
@@ -538,6 +543,16 @@ __global__ __launch_bounds__(256, 2) void km_mfma_small(const float* __restrict_
       second[p0 + r] = fminf(tk ? b1 : y1, fminf(b2, y2));
     }
   }
+}
+template <int DS>
+__global__ __launch_bounds__(256, 2) void km_mfma_small(const float* __restrict__ P, int ldp,
+                                                     const uint32_t* __restrict__ rows, int n,
+                                                     const float* __restrict__ C, int ldc, int k,
+                                                     const float* __restrict__ cn, uint32_t* __restrict__ best_idx,
+                                                     float* __restrict__ best, float* __restrict__ second) {
+  extern __shared__ float4 ks_sm[];
+  km_mfma_small_body<DS>(P, ldp, rows, n, C, ldc, k, cn, best_idx, best, second, reinterpret_cast<float*>(ks_sm),
+                         blockIdx.x);
 }
 
 // km_mfma_reg: km_mfma_small's form for rows of 32 to 128 floats (dim a
@@ -647,20 +662,20 @@ __global__ __launch_bounds__(256, 3) void km_mfma_reg(const float* __restrict__ 
 
 constexpr int KV_PB = 128;  // points per km_mfma_verify block (256 threads)
 template <bool UNR>
-__global__ __launch_bounds__(256) void km_mfma_verify(const float* __restrict__ P, int ldp,
-                                                      const uint32_t* __restrict__ rows, int n, int dim,
-                                                      const float* __restrict__ C, int ldc,
-                                                      const float* __restrict__ pn, const float* __restrict__ cmax,
-                                                      const uint32_t* __restrict__ best_idx,
-                                                      const float* __restrict__ best, const float* __restrict__ second,
-                                                      uint32_t* __restrict__ assign, float* __restrict__ dist,
-                                                      uint32_t* __restrict__ redo, int* __restrict__ nredo) {
+__device__ __forceinline__ void km_mfma_verify_body(const float* __restrict__ P, int ldp,
+                                                    const uint32_t* __restrict__ rows, int n, int dim,
+                                                    const float* __restrict__ C, int ldc,
+                                                    const float* __restrict__ pn, const float* __restrict__ cmax,
+                                                    const uint32_t* __restrict__ best_idx,
+                                                    const float* __restrict__ best, const float* __restrict__ second,
+                                                    uint32_t* __restrict__ assign, float* __restrict__ dist,
+                                                    uint32_t* __restrict__ redo, int* __restrict__ nredo, int bx) {
   // the block's KV_PB points and their winning centroids, staged through LDS
   // 32 coordinates at a time (eight lanes per 128-byte row slice); 34 KB of
   // LDS, so four blocks per CU keep the row loads in flight
   __shared__ float tp[KV_PB * 33], tc[KV_PB * 33];
   __shared__ uint32_t sr[KV_PB], sc[KV_PB];
-  const int t = threadIdx.x, i0 = blockIdx.x * KV_PB, i = i0 + t;
+  const int t = threadIdx.x, i0 = bx * KV_PB, i = i0 + t;
   bool ok = false;
   if (t < KV_PB) {  // threads KV_PB.. only help with the loads
     if (i < n) {
@@ -721,6 +736,18 @@ __global__ __launch_bounds__(256) void km_mfma_verify(const float* __restrict__ 
         dist[i] = sum;
     }
   }
+}
+template <bool UNR>
+__global__ __launch_bounds__(256) void km_mfma_verify(const float* __restrict__ P, int ldp,
+                                                      const uint32_t* __restrict__ rows, int n, int dim,
+                                                      const float* __restrict__ C, int ldc,
+                                                      const float* __restrict__ pn, const float* __restrict__ cmax,
+                                                      const uint32_t* __restrict__ best_idx,
+                                                      const float* __restrict__ best, const float* __restrict__ second,
+                                                      uint32_t* __restrict__ assign, float* __restrict__ dist,
+                                                      uint32_t* __restrict__ redo, int* __restrict__ nredo) {
+  km_mfma_verify_body<UNR>(P, ldp, rows, n, dim, C, ldc, pn, cmax, best_idx, best, second, assign, dist, redo, nredo,
+                           blockIdx.x);
 }
 
 constexpr int KW_DMAX = 2048;  // largest dim of the MFMA assignment path
@@ -2205,6 +2232,15 @@ struct PqSub {
   int* fpe;
   double* total;      // [2]: inertia, 1.0 when it equals the sequential sum
   int* flags;         // [0] non-finite k-means++ total, [1] inexact picks, [2] assignment changed
+  // the certified matrix-core assignment (narrow equal widths)
+  float* pn;          // n: the points' squared norms
+  float* cn;          // k: the centroids' squared norms
+  float* cmax;        // [1]: the largest of them
+  uint32_t* bidx;     // n: the approximate pass's best centroid
+  float* best;        // n: its approximate score
+  float* second;      // n: the second-best approximate score
+  uint32_t* redo;     // n: the points the certificate leaves to the exact scan
+  int* nredo;         // [1]
   int w;
   int active;         // still iterating
 };
@@ -2266,6 +2302,56 @@ __global__ __launch_bounds__(1024) void pqb_pp_pick(const PqSub* __restrict__ S,
   const PqSub& q = S[blockIdx.x];
   km_pp_pick_body(q.P, q.w, n, q.w, q.ns, q.ps, q.pe, nb, q.rng, q.cents + (size_t)chosen * q.w, q.flags,
                   q.flags + 1, nullptr);
+}
+
+// The certified matrix-core assignment of every subspace at once: the
+// single-run pass's kernels (km_row_norms, the centroid norms and their
+// largest, km_mfma_small, km_mfma_verify) over each subspace's arrays. The
+// points the certificate leaves go to the exact scan per subspace.
+__global__ __launch_bounds__(256) void pqb_point_norms(const PqSub* __restrict__ S, int n) {
+  const PqSub& q = S[blockIdx.y];
+  km_row_norms_body(q.P, q.w, nullptr, n, q.w, q.pn, blockIdx.x);
+}
+
+// cn[c] = |c|^2 and cmax = the largest (NaN if any is NaN), per active subspace
+__global__ __launch_bounds__(256) void pqb_cent_norms(const PqSub* __restrict__ S, int k) {
+  __shared__ float sh[256];
+  const PqSub& q = S[blockIdx.x];
+  if (!q.active) return;  // uniform over the block
+  float m = 0.0f;
+  for (int c = threadIdx.x; c < k; c += 256) {
+    const float* cr = q.cents + (size_t)c * q.w;
+    float v = 0.0f;
+    for (int j = 0; j < q.w; ++j) v += cr[j] * cr[j];
+    q.cn[c] = v;
+    m = v > m || v != v ? v : m;  // a NaN, once taken, stays
+  }
+  sh[threadIdx.x] = m;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (threadIdx.x < o) {
+      const float x = sh[threadIdx.x + o];
+      if (x > sh[threadIdx.x] || x != x) sh[threadIdx.x] = x;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) q.cmax[0] = sh[0];
+}
+
+template <int DS>
+__global__ __launch_bounds__(256, 2) void pqb_mfma_small(const PqSub* __restrict__ S, int n, int k) {
+  extern __shared__ float4 ks_sm[];
+  const PqSub& q = S[blockIdx.y];
+  if (!q.active) return;
+  km_mfma_small_body<DS>(q.P, q.w, nullptr, n, q.cents, q.w, k, q.cn, q.bidx, q.best, q.second,
+                         reinterpret_cast<float*>(ks_sm), blockIdx.x);
+}
+
+__global__ __launch_bounds__(256) void pqb_verify(const PqSub* __restrict__ S, int n) {
+  const PqSub& q = S[blockIdx.y];
+  if (!q.active) return;
+  km_mfma_verify_body<false>(q.P, q.w, nullptr, n, q.w, q.cents, q.w, q.pn, q.cmax, q.bidx, q.best, q.second,
+                             q.assign, q.dist, q.redo, q.nredo, blockIdx.x);
 }
 
 template <int D>
@@ -2365,6 +2451,8 @@ static int pq_train_batched(const std::vector<DevBuf<float>>& proj, size_t n, co
   DevBuf<ChaCha8> drng(M);
   DevBuf<uint64_t> dfirst(M);
   DevBuf<PqSub> dS(M);
+  // the matrix-core assignment: narrow equal widths with enough points
+  const int w0 = L.width[0];
   size_t cofs_total = 0;
   std::vector<size_t> cofs(M);
   for (int q = 0; q < M; ++q) {
@@ -2402,13 +2490,39 @@ static int pq_train_batched(const std::vector<DevBuf<float>>& proj, size_t n, co
     vec4 = vec4 && w % 4 == 0 && ((uintptr_t)proj[q].p & 15) == 0;
     equal = equal && w == L.width[0];
   }
+  const bool mfma = vec4 && equal && (w0 == 8 || w0 == 16 || w0 == 24) && k >= 64 && k * (size_t)w0 <= KS_MAXF &&
+                    n >= 4096;
+  DevBuf<float> pn, cn, cmax, best, second;
+  DevBuf<uint32_t> bidx, redo, ra;
+  DevBuf<float> rd;
+  DevBuf<int> nredo;
+  if (mfma) {
+    pn.reserve((size_t)M * n);
+    cn.reserve((size_t)M * k);
+    cmax.reserve(M);
+    bidx.reserve((size_t)M * n);
+    best.reserve((size_t)M * n);
+    second.reserve((size_t)M * n);
+    redo.reserve((size_t)M * n);
+    nredo.reserve(M);
+    for (int q = 0; q < M; ++q) {
+      PqSub& t = h[q];
+      t.pn = pn.p + (size_t)q * n;
+      t.cn = cn.p + (size_t)q * k;
+      t.cmax = cmax.p + q;
+      t.bidx = bidx.p + (size_t)q * n;
+      t.best = best.p + (size_t)q * n;
+      t.second = second.p + (size_t)q * n;
+      t.redo = redo.p + (size_t)q * n;
+      t.nredo = nredo.p + q;
+    }
+  }
   PXG_HIP(hipMemcpyAsync(dS.p, h.data(), M * sizeof(PqSub), hipMemcpyHostToDevice, s));
   PXG_HIP(hipMemcpyAsync(drng.p, rng.data(), M * sizeof(ChaCha8), hipMemcpyHostToDevice, s));
   PXG_HIP(hipMemcpyAsync(dfirst.p, first.data(), M * 8, hipMemcpyHostToDevice, s));
   PXG_HIP(hipMemsetAsync(flags.p, 0, (size_t)M * 16, s));
   PXG_HIP(hipMemsetAsync(prev.p, 0, (size_t)M * n * 4, s));  // kmeans.rs:88: every point starts in cluster 0
   // k-means++, all subspaces a round at a time
-  const int w0 = L.width[0];
   auto round = [&](int chosen, int init) {
     const dim3 g(nb, M);
     if (vec4 && equal && w0 == 8)
@@ -2469,6 +2583,10 @@ static int pq_train_batched(const std::vector<DevBuf<float>>& proj, size_t n, co
   DevBuf<unsigned long long> far_part(KF_BLOCKS);
   DevBuf<long long> far(1);
   const dim3 gn((unsigned)((n + 255) / 256), (unsigned)M);
+  if (mfma)
+    hipLaunchKernelGGL(pqb_point_norms, dim3((unsigned)((n + 31) / 32), (unsigned)M), dim3(256), 0, s,
+                       (const PqSub*)dS.p, (int)n);
+  std::vector<int> hredo(M);
   for (size_t it = 0; it < max_iter; ++it) {
     int live = 0;
     for (int q = 0; q < Mb; ++q) live += h[q].active;
@@ -2478,7 +2596,41 @@ static int pq_train_batched(const std::vector<DevBuf<float>>& proj, size_t n, co
       if (h[q].active) res[q].iterations = it + 1;
     // assignment: the sequential squared, strict < (kmeans.rs:200-212)
     const int v4 = vec4 ? 1 : 0;
-    if (equal && L.width[0] == 8)
+    if (mfma) {
+      // the certified approximation, then the exact scan of the points it
+      // leaves (nearest_device's steps, every subspace at once)
+      hipLaunchKernelGGL(pqb_cent_norms, dim3(M), dim3(256), 0, s, (const PqSub*)dS.p, (int)k);
+      PXG_HIP(hipMemsetAsync(nredo.p, 0, (size_t)M * 4, s));
+      const dim3 gs((unsigned)((n + 4 * KS_PW * 32 - 1) / (4 * KS_PW * 32)), (unsigned)M);
+      const size_t lds = (k * w0 + ((k + 31) & ~(size_t)31)) * 4;
+      if (w0 == 8)
+        hipLaunchKernelGGL(pqb_mfma_small<1>, gs, dim3(256), lds, s, (const PqSub*)dS.p, (int)n, (int)k);
+      else if (w0 == 16)
+        hipLaunchKernelGGL(pqb_mfma_small<2>, gs, dim3(256), lds, s, (const PqSub*)dS.p, (int)n, (int)k);
+      else
+        hipLaunchKernelGGL(pqb_mfma_small<3>, gs, dim3(256), lds, s, (const PqSub*)dS.p, (int)n, (int)k);
+      hipLaunchKernelGGL(pqb_verify, dim3((unsigned)((n + KV_PB - 1) / KV_PB), (unsigned)M), dim3(256), 0, s,
+                         (const PqSub*)dS.p, (int)n);
+      PXG_HIP(hipGetLastError());
+      PXG_HIP(hipMemcpyAsync(hredo.data(), nredo.p, (size_t)M * 4, hipMemcpyDeviceToHost, s));
+      PXG_HIP(hipStreamSynchronize(s));
+      int mmax = 0;
+      for (int q = 0; q < Mb; ++q)
+        if (h[q].active) mmax = std::max(mmax, hredo[q]);
+      ra.reserve(mmax);  // the stream is idle here (synchronized above)
+      rd.reserve(mmax);
+      for (int q = 0; q < Mb; ++q) {
+        const int m = hredo[q];
+        if (!h[q].active || m == 0) continue;
+        const dim3 gx((unsigned)((m + KX_PB - 1) / KX_PB));
+        hipLaunchKernelGGL(km_exact_multi<false>, gx, dim3(256), (size_t)KX_PB * w0 * 4, s, h[q].P, w0,
+                           (const uint32_t*)h[q].redo, m, w0, (const float*)h[q].cents, w0, (int)k, ra.p, rd.p);
+        hipLaunchKernelGGL(km_scatter_redo, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, s,
+                           (const uint32_t*)h[q].redo, m, (const uint32_t*)ra.p, (const float*)rd.p, h[q].assign,
+                           h[q].dist);
+        PXG_HIP(hipGetLastError());
+      }
+    } else if (equal && L.width[0] == 8)
       hipLaunchKernelGGL(pqb_assign<8>, gn, dim3(256), 0, s, (const PqSub*)dS.p, (int)n, (int)k, v4);
     else if (equal && L.width[0] == 16)
       hipLaunchKernelGGL(pqb_assign<16>, gn, dim3(256), 0, s, (const PqSub*)dS.p, (int)n, (int)k, v4);

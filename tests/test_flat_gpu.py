@@ -365,15 +365,16 @@ def test_thresholds_shared_across_splits(gpu, metric):
 
 
 @pytest.mark.parametrize("metric", [0, 1])
-def test_seeded_thresholds(gpu, metric):
+@pytest.mark.parametrize("dim", [16, 32])
+def test_seeded_thresholds(gpu, metric, dim):
     """With many tiles per split, a first pass over one tile of every split
     seeds each query's threshold before the full pass. Integer data (exact
     distance ties at the seed), removed rows, a filter, queries whose
     neighbours all sit past the sampled tiles, and k from 1 to 100: ids and
-    distances match the oracle bit for bit."""
+    distances match the oracle bit for bit, for rows of 16 and 32 floats."""
     px = gpu
-    rng = np.random.default_rng(5 + metric)
-    n, dim, nq = 140_000, 16, 1024  # 8 query blocks x 61 splits of 18 tiles (2304 rows)
+    rng = np.random.default_rng(5 + metric + dim)
+    n, nq = 140_000, 1024  # 8 query blocks x 61 splits of 18 tiles (2304 rows)
     data = rng.integers(-2, 3, (n, dim)).astype(np.float32)
     ids = rng.permutation(n).astype(np.uint64)
     idx = make_index(px, data, metric, ids, mode=1)

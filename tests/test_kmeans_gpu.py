@@ -283,10 +283,10 @@ def _lcg_clustered(dim, count, seed):  # product.rs:635-654
     return out
 
 
-# the last two train 8- and 24-wide subspaces on enough vectors for the
-# narrow-row matrix-core assignment
+# the last three train 8-, 24- and 16-wide subspaces on enough vectors for
+# the narrow-row matrix-core assignment (all subspaces in each launch)
 @pytest.mark.parametrize("dim,m,count,seed", [(32, 8, 512, 3), (10, 4, 300, 2), (8, 2, 3, 6), (64, 16, 400, 1),
-                                              (16, 2, 6000, 4), (48, 2, 5000, 5)])
+                                              (16, 2, 6000, 4), (48, 2, 5000, 5), (32, 2, 4500, 8)])
 def test_pq_train_and_encode_bit_exact(gpu, dim, m, count, seed):
     px = gpu
     t = _lcg_clustered(dim, count, seed)
@@ -312,12 +312,15 @@ def test_pq_train_in_order_path(gpu, monkeypatch, after):
     assert pq.training_inertia == inertia and pq.training_iterations == iters
 
 
-@pytest.mark.parametrize("dim,m,count,distinct", [(16, 2, 300, 40), (12, 3, 2000, 150)])
+@pytest.mark.parametrize("dim,m,count,distinct", [(16, 2, 300, 40), (12, 3, 2000, 150), (16, 2, 6000, 60)])
 def test_pq_train_duplicates_reseed_empty_clusters(gpu, dim, m, count, distinct):
     """Few distinct rows: k-means++ falls back to uniform picks once the total
     is zero (kmeans.rs:162-166), duplicate seeds leave clusters empty, and the
     batched trainer reseeds them per subspace with the farthest point of the
-    partially updated array (kmeans.rs:119-123)."""
+    partially updated array (kmeans.rs:119-123). With 6000 rows the
+    assignment takes the matrix-core pass, whose certificate fails on the
+    duplicate centroids' exact ties: those points go to the exact scan, which
+    keeps the lower index."""
     px = gpu
     rng = np.random.default_rng(count)
     rows = rng.standard_normal((distinct, dim)).astype(np.float32)
