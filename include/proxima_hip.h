@@ -149,7 +149,7 @@ int pxg_flat_search_device(const pxg_flat* index, const float* d_queries, uint64
  * more fails with PXG_ERR_CAPACITY (parameter "no-allocation scratch",
  * detail a = the array's size) at the first scratch region that does not fit:
  * prepared queries (nq x round_up(dim, 4) x 4 bytes), candidate buffers
- * (nq x CAP x 8 bytes per split, CAP = 256 for k <= 96, else 512, at least
+ * (nq x CAP x 8 bytes per split, CAP = 256 for k <= 48, else 512, at least
  * one split), exact-scan keys, or the wide path's keys. Stages queued before
  * that point are waited for before the call returns, so no kernel still uses
  * the array or writes the outputs afterwards (the outputs are then undefined).

@@ -53,7 +53,7 @@ constexpr int FB_K = 32;    // k-slice staged in LDS
 // A staged slice is [rows][FB_K] floats without padding; 16-byte chunk c of
 // row r sits at chunk position c ^ (r & 7), so 8 lanes reading chunk c of 8
 // consecutive rows touch 8 different groups of banks.
-constexpr int MARGIN = 32;  // k' = k + MARGIN
+constexpr int MARGIN = 16;  // k' = k + MARGIN
 constexpr int FAST_KMAX = 256;
 
 // ---------------------------------------------------------------------------
@@ -690,7 +690,9 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
                          (mode == 0 && (N < 4096 || (double)N * (double)nq < 4.0e6));
   if (!exact_all) {
     const int Kp = (int)std::min<uint64_t>(kq + MARGIN, (uint64_t)FAST_KMAX + MARGIN);
-    const int CAP = (Kp + FB_N) <= 256 ? 256 : 512;
+    // a row's buffer holds its Kp keys, one tile's appends (FB_N) and at
+    // least 64 more before it must be compacted
+    const int CAP = (Kp + FB_N + 64) <= 256 ? 256 : 512;
     const int QB = (int)((nq + FB_M - 1) / FB_M);
     const int tiles = (int)((N + FB_N - 1) / FB_N);
     // per query, the least threshold any split has published

@@ -91,8 +91,9 @@ def test_noalloc_wide_k_and_capacity(gpu):
 def test_noalloc_capacity_after_queued_stages(gpu):
     # the prepared queries (50000 x 128 x 4 bytes) and the per-query regions fit
     # the 128 MiB, but one split of candidate buffers (50000 x 512 x 8 bytes at
-    # k = 100) does not: the call fails with Capacity after its first stages
-    # were queued, waits for them, and the next calls are served correctly
+    # k = 100, whose k' = 116 takes the 512-key buffers) does not: the call
+    # fails with Capacity after its first stages were queued, waits for them,
+    # and the next calls are served correctly
     import torch
     px = gpu
     na = _noalloc(px)
