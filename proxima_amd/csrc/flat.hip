@@ -121,7 +121,7 @@ __device__ inline void compact_row_w(uint64_t* __restrict__ base, int c, int Kp,
 // Kp: sorted over the narrowest width (64 keys per lane-slot step) that
 // holds max(c, Kp), up to the buffer's CAP.
 template <int CAP>
-__device__ inline void compact_row(uint64_t* __restrict__ base, int c, int Kp, int lane, uint64_t* thr_row,
+__device__ __attribute__((noinline)) void compact_row(uint64_t* __restrict__ base, int c, int Kp, int lane, uint64_t* thr_row,
                                    float* thrf_row, int* cnt_row, unsigned long long* gthr_row, bool final_pass) {
   const int need = c > Kp ? c : Kp;
   if (need <= 64)
@@ -382,13 +382,20 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
       }
     }
     __syncthreads();
-    for (int row = wid; row < FB_M; row += 4) {
-      const int c = cnt[row];
-      if (c > CAP - FB_N)
-        compact_row<CAP>(cand + ((size_t)(q0 + row) * S + split) * CAP, c, Kp, lane, &thr[row], &thr_f[row],
-                         &cnt[row], gthr + q0 + row, false);
+    if constexpr (!SEED) {
+      // this wave's rows wid, wid + 4, ...: one count per lane, then a
+      // compaction for each row that might not take another tile's appends
+      const int c_l = lane < FB_M / 4 ? cnt[wid + 4 * lane] : 0;
+      uint64_t full = __ballot(c_l > CAP - FB_N);
+      while (full) {
+        const int l = __builtin_ctzll(full);
+        full &= full - 1;
+        const int row = wid + 4 * l;
+        compact_row<CAP>(cand + ((size_t)(q0 + row) * S + split) * CAP, __builtin_amdgcn_readlane(c_l, l), Kp,
+                         lane, &thr[row], &thr_f[row], &cnt[row], gthr + q0 + row, false);
+      }
+      __syncthreads();
     }
-    __syncthreads();
   }
   // Seeding pass: each row has left its one tile's FB_N distance parts.
   if constexpr (SEED) return;
