@@ -479,6 +479,18 @@ __global__ __launch_bounds__(SQ_NW * 64) void sq8_mfma_scan(
           if (rt + 1 < RT) load_a(a0, tl, rt + 1);
           reduce(c0, rt - 1, buf);
         }
+        if constexpr (!STAGE1) {
+          // the next A operand's reads first, then each MFMA followed by
+          // four of the previous block's filter instructions; nothing of
+          // this block's filter moves up
+          __builtin_amdgcn_sched_group_barrier(0x100, KB, 0);
+#pragma unroll
+          for (int g = 0; g < KB * QT; ++g) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
       if ((RT - 1) % 2 == 0) reduce(c0, RT - 1, buf);
       else reduce(c1, RT - 1, buf);
