@@ -546,8 +546,8 @@ def bench_kmeans(args, torch, px, dev):
     log(f"[bench] kmeans: seeding {t_seed:.2f}s, {its} Lloyd iterations {t_lloyd:.2f}s ({per_iter * 1e3:.1f} ms each, "
         f"{tflops:.1f} TFLOP/s by 2nKd per iteration), inertia {inertia:.1f}; MFMA distance pass "
         f"{mfma_ms:.2f} ms = {mfma_tflops:.1f} TFLOP/s over {st['mfma_passes']} passes, "
-        f"{st['rescanned']} points rescanned exactly; PQ 16x256 on residuals {t_pq:.2f}s "
-        f"({pq_its} iterations)")
+        f"{st['rescanned']} points rescanned exactly; PQ 16x256 on residuals "
+        + ("skipped" if args.km_skip_pq else f"{t_pq:.2f}s ({pq_its} iterations)"))
     out = {"value": round(1.0 / per_iter, 3), "unit": "Lloyd iterations/s", "ms_per_iteration": round(per_iter * 1e3, 2),
            "config": {"workload": "k-means 2M x 128 f32 -> 4096, k-means++ then 10 Lloyd iterations; PQ 16x256 on "
                                   "the residuals", "n": n, "dim": dim, "k": K, "iterations": its,

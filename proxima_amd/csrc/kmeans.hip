@@ -580,14 +580,18 @@ __global__ __launch_bounds__(256, 3) void km_mfma_reg(const float* __restrict__ 
   const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float*)sc;
   // the copy of block b into buffer buf: instruction u of wave w covers
   // chunk positions 64 (w NI + u) + lane of the block
+  // (a full block's rows are the lane's fixed offsets plus the block's
+  // uniform first row; the last block clamps its rows to k - 1)
   auto gload = [&](int b, int buf) __attribute__((always_inline)) {
+    const bool full = b * 32 + 32 <= k;
+    const float* cb = C + (size_t)(b * 32) * ldc;
 #pragma unroll
     for (int u = 0; u < NI; ++u) {
       const int g = wid_s * NI + u;
       const int idx = 64 * g + lane, row = idx / CPR, pos = idx - row * CPR;
       const int c = pos ^ (row & 7);
-      const int crow = min(b * 32 + row, k - 1);
-      km_lds_copy16(C + (size_t)crow * ldc + 4 * c, lds0 + (uint32_t)((buf * TILE + 64 * 4 * g) * 4));
+      const float* src = full ? cb + (row * ldc + 4 * c) : C + (size_t)min(b * 32 + row, k - 1) * ldc + 4 * c;
+      km_lds_copy16(src, lds0 + (uint32_t)((buf * TILE + 64 * 4 * g) * 4));
     }
   };
   const int p0 = (blockIdx.x * 4 + w) * 32;
@@ -614,12 +618,25 @@ __global__ __launch_bounds__(256, 3) void km_mfma_reg(const float* __restrict__ 
   const int r7 = r & 7;
   for (int blk = 0; blk < nblk; ++blk) {
     const int cur = blk & 1;
-    // this block's norms (rows 8 (v/4) + 4 h + v%4), loaded before the wait
+    // this block's norms (rows 8 (v/4) + 4 h + v%4), loaded before the wait:
+    // four rows at a time in a full block (cn is 16-byte aligned)
     float cv[16];
+    if (blk * 32 + 32 <= k) {
+      const float* cr = cn + blk * 32 + 4 * h;
 #pragma unroll
-    for (int vb = 0; vb < 4; ++vb) {
+      for (int vb = 0; vb < 4; ++vb) {
+        const float4 c4 = *reinterpret_cast<const float4*>(cr + 8 * vb);
+        cv[4 * vb] = c4.x;
+        cv[4 * vb + 1] = c4.y;
+        cv[4 * vb + 2] = c4.z;
+        cv[4 * vb + 3] = c4.w;
+      }
+    } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) cv[4 * vb + e] = cn[min(blk * 32 + 8 * vb + 4 * h + e, k - 1)];
+      for (int vb = 0; vb < 4; ++vb) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) cv[4 * vb + e] = cn[min(blk * 32 + 8 * vb + 4 * h + e, k - 1)];
+      }
     }
     km_vm_wait0();  // this wave's copies of block blk (and the norms) have landed
     __syncthreads();  // everyone's copies of blk are in; everyone is done with blk - 1
