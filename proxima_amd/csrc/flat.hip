@@ -11,7 +11,12 @@
 //                         below the running threshold are appended to a
 //                         per-(query, split) buffer that a wave-level bitonic
 //                         sort compacts back to k' whenever it fills. The
-//                         N x nq score matrix never reaches HBM.
+//                         N x nq score matrix never reaches HBM. With many
+//                         tiles per split, a seeding pass scores the first
+//                         tile of every split first: flat_seed_threshold
+//                         turns those keys into each query's starting
+//                         threshold, and the full pass filters them instead
+//                         of recomputing that tile.
 //  3. flat_merge_rescore  per query: radix-select the k' best approximate
 //                         keys over all splits, rescore those k' exactly with
 //                         the reference's 8-lane arithmetic, sort by
@@ -134,6 +139,46 @@ __device__ __attribute__((noinline)) void compact_row(uint64_t* __restrict__ bas
     compact_row_w<CAP>(base, c, Kp, lane, thr_row, thrf_row, cnt_row, gthr_row, final_pass);
 }
 
+// The first tile of a seeded split in the full pass: the keys the seeding
+// pass left in the last FB_N / 2 entries of each row's buffer (FB_N 32-bit
+// distance parts, slot n0 + c at word c), rebuilt as (distance part, slot)
+// and tested against the row's threshold like computed ones. Thread t takes
+// row t / 2, words (t & 1) * FB_N / 2 onwards. The appends (at most FB_N
+// per row, the row's first) stay below the stored words. Out of line, so
+// that the main loop's registers are not shaped by it.
+template <int CAP>
+__device__ __attribute__((noinline)) void flat_stored_tile(uint64_t* __restrict__ cand, int S, int split, int q0,
+                                                           int nq, int n0, int s_end, const uint8_t* __restrict__ live,
+                                                           const uint8_t* __restrict__ acc_src, const uint64_t* thr,
+                                                           int* cnt, int tid) {
+  const int row = tid >> 1, c0 = (tid & 1) * (FB_N / 2);
+  if (row >= FB_M || q0 + row >= nq) return;
+  uint64_t* buf = cand + ((size_t)(q0 + row) * S + split) * CAP;
+  const uint32_t* kw = reinterpret_cast<const uint32_t*>(buf + (CAP - FB_N / 2)) + c0;
+  const uint64_t t = thr[row];
+  // four words per load, four loads in flight (few registers: this runs
+  // inside the main loop's register budget)
+#pragma nounroll
+  for (int u0 = 0; u0 < FB_N / 8; u0 += 4) {
+    uint4 w[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) w[u] = reinterpret_cast<const uint4*>(kw)[u0 + u];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t kk[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int slot = n0 + c0 + 4 * (u0 + u) + e;
+        const uint64_t key = ((uint64_t)kk[e] << 32) | (uint32_t)slot;
+        if (key < t && slot < s_end && (live[slot] & acc_src[slot]) != 0) {
+          const int pos = atomicAdd(&cnt[row], 1);
+          buf[pos] = key;
+        }
+      }
+    }
+  }
+}
+
 // SEED: the seeding pass (a separate instantiation, so that the full pass's
 // code is not shaped by the seeding epilogue).
 template <int CAP, bool SEED>
@@ -141,7 +186,7 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
     const float* __restrict__ Q, int nq, const float* __restrict__ X, int N, int ld,
     const float* __restrict__ qb, const float* __restrict__ xb, float scale, const uint8_t* __restrict__ live,
     const uint8_t* __restrict__ accept, int S, int QB, int per_split, int Kp,
-    uint64_t* __restrict__ cand, unsigned long long* __restrict__ gthr) {
+    uint64_t* __restrict__ cand, unsigned long long* __restrict__ gthr, int seeded) {
   __shared__ __align__(16) float sQ[2][FB_M * FB_K];
   __shared__ __align__(16) float sX[2][FB_N * FB_K];
   __shared__ uint64_t thr[FB_M];
@@ -210,6 +255,11 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
       acj[j] = acc_src[sl];
       xbr[j] = xb[sl];
     }
+    // A seeded full pass takes the first tile of its split from the keys
+    // the seeding pass left at the tail of each row's buffer (the same
+    // instructions on the same operands, so the same keys) instead of
+    // computing it again.
+    const bool stored = !SEED && seeded != 0 && n0 == s_begin;
     f16v acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -249,46 +299,53 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
 #endif
     };
 
-    if (n0 == s_begin) {
-      gload(n0, 0, gs & 1);
-      vm_wait0();
-      __syncthreads();
-    }
-    for (int kt = 0; kt < nK; ++kt) {
-      const int cur = (gs + kt) & 1;
-      if (kt + 1 < nK) gload(n0, (kt + 1) * FB_K, cur ^ 1);
-      else if (n0 + FB_N < s_end) gload(n0 + FB_N, 0, cur ^ 1);
-      // Lane (h, r) feeds k = h*16 + kk of row r: the MFMA pairs A and B by
-      // lane half, so any fixed permutation of k within the slice is a
-      // valid dot product; this one lets each lane read 16 contiguous floats
-      // (chunks 4h .. 4h+3 of its row, swizzled by r & 7; wm, wn and 32 are
-      // multiples of 8).
-      const float* a0p = &sQ[cur][(wm + r) * FB_K];
-      const float* a1p = &sQ[cur][(wm + 32 + r) * FB_K];
-      const float* b0p = &sX[cur][(wn + r) * FB_K];
-      const float* b1p = &sX[cur][(wn + 32 + r) * FB_K];
-      const int r7 = r & 7;
-#pragma unroll
-      for (int k4 = 0; k4 < 4; ++k4) {
-        const int co = ((4 * h + k4) ^ r7) * 4;
-        const float4 a0 = *reinterpret_cast<const float4*>(a0p + co);
-        const float4 a1 = *reinterpret_cast<const float4*>(a1p + co);
-        const float4 b0 = *reinterpret_cast<const float4*>(b0p + co);
-        const float4 b1 = *reinterpret_cast<const float4*>(b1p + co);
-        const float av0[4] = {a0.x, a0.y, a0.z, a0.w}, av1[4] = {a1.x, a1.y, a1.z, a1.w};
-        const float bv0[4] = {b0.x, b0.y, b0.z, b0.w}, bv1[4] = {b1.x, b1.y, b1.z, b1.w};
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(av0[t], bv0[t], acc[0][0], 0, 0, 0);
-          acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(av0[t], bv1[t], acc[0][1], 0, 0, 0);
-          acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(av1[t], bv0[t], acc[1][0], 0, 0, 0);
-          acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(av1[t], bv1[t], acc[1][1], 0, 0, 0);
-        }
+    if (stored) {
+      // the next tile's first slice, which the k loop below would have
+      // prefetched (no slice is consumed here, so gs is unchanged); waited
+      // for after the stored keys' epilogue
+      if (n0 + FB_N < s_end) gload(n0 + FB_N, 0, gs & 1);
+    } else {
+      if (n0 == s_begin) {
+        gload(n0, 0, gs & 1);
+        vm_wait0();
+        __syncthreads();
       }
-      vm_wait0();  // this wave's copies of the next slice have landed
-      __syncthreads();
+      for (int kt = 0; kt < nK; ++kt) {
+        const int cur = (gs + kt) & 1;
+        if (kt + 1 < nK) gload(n0, (kt + 1) * FB_K, cur ^ 1);
+        else if (n0 + FB_N < s_end) gload(n0 + FB_N, 0, cur ^ 1);
+        // Lane (h, r) feeds k = h*16 + kk of row r: the MFMA pairs A and B by
+        // lane half, so any fixed permutation of k within the slice is a
+        // valid dot product; this one lets each lane read 16 contiguous floats
+        // (chunks 4h .. 4h+3 of its row, swizzled by r & 7; wm, wn and 32 are
+        // multiples of 8).
+        const float* a0p = &sQ[cur][(wm + r) * FB_K];
+        const float* a1p = &sQ[cur][(wm + 32 + r) * FB_K];
+        const float* b0p = &sX[cur][(wn + r) * FB_K];
+        const float* b1p = &sX[cur][(wn + 32 + r) * FB_K];
+        const int r7 = r & 7;
+#pragma unroll
+        for (int k4 = 0; k4 < 4; ++k4) {
+          const int co = ((4 * h + k4) ^ r7) * 4;
+          const float4 a0 = *reinterpret_cast<const float4*>(a0p + co);
+          const float4 a1 = *reinterpret_cast<const float4*>(a1p + co);
+          const float4 b0 = *reinterpret_cast<const float4*>(b0p + co);
+          const float4 b1 = *reinterpret_cast<const float4*>(b1p + co);
+          const float av0[4] = {a0.x, a0.y, a0.z, a0.w}, av1[4] = {a1.x, a1.y, a1.z, a1.w};
+          const float bv0[4] = {b0.x, b0.y, b0.z, b0.w}, bv1[4] = {b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(av0[t], bv0[t], acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(av0[t], bv1[t], acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(av1[t], bv0[t], acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(av1[t], bv1[t], acc[1][1], 0, 0, 0);
+          }
+        }
+        vm_wait0();  // this wave's copies of the next slice have landed
+        __syncthreads();
+      }
+      gs += nK;
     }
-    gs += nK;
     if (tid < FB_M && g_thr < thr[tid]) {
       thr[tid] = g_thr;
       thr_f[tid] = key_float((uint32_t)(g_thr >> 32));
@@ -305,10 +362,12 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
     // pass), so only the marked values take the exact key test and append.
     if constexpr (SEED) {
       // Seeding pass: every usable value of its one tile is kept, so each
-      // lane writes its distance part straight to its column of the row's
-      // buffer, read as 32-bit words (no counters, no atomics; the seed
-      // threshold needs only the distance parts); unusable slots hold
-      // 0xFFFFFFFF.
+      // lane writes its distance part straight to its column of the last
+      // FB_N / 2 words of the row's buffer, read as FB_N 32-bit words (no
+      // counters, no atomics; the seed threshold needs only the distance
+      // parts, and the full pass rebuilds each key from its slot);
+      // unusable slots hold 0xFFFFFFFF. The full pass's appends from this
+      // tile (at most FB_N) stay below that region.
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const bool ok = (slotj[j] < s_end) & ((lvj[j] & acj[j]) != 0u);
@@ -320,11 +379,14 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
             const int row = wm + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
             if (q0 + row < nq) {
               const float a = __builtin_fmaf(-scale, acc[i][j][v], sqb[row] + xo);
-              reinterpret_cast<uint32_t*>(cand + ((size_t)(q0 + row) * S + split) * CAP)[wn + j * 32 + r] =
-                  ok ? ord_key(a) : 0xFFFFFFFFu;
+              reinterpret_cast<uint32_t*>(cand + ((size_t)(q0 + row) * S + split) * CAP +
+                                          (CAP - FB_N / 2))[wn + j * 32 + r] = ok ? ord_key(a) : 0xFFFFFFFFu;
             }
           }
       }
+    } else if (stored) {
+      flat_stored_tile<CAP>(cand, S, split, q0, nq, n0, s_end, live, acc_src, thr, cnt, tid);
+      vm_wait0();  // the prefetched slice
     } else {
       // Validity as bit masks applied once per row group (usable slots: the
       // j halves; rows below nq: both halves), so that the per-value work is
@@ -418,8 +480,9 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
 // 3. merge + exact rescore (approximate candidates)
 // ---------------------------------------------------------------------------
 // Per query: the Kp-th smallest distance part over the words a seeding pass
-// left (the first tile of every split, FB_N 32-bit distance parts per split
-// at the start of its buffer, 0xFFFFFFFF for unusable slots).
+// left (the first tile of every split, FB_N 32-bit distance parts in the
+// last FB_N / 2 entries of each split's buffer, 0xFFFFFFFF for unusable
+// slots).
 // The full pass meets all of those rows again, so a threshold above every
 // key with that distance part (the strict key test passes them all) leaves
 // at least Kp rows, the query's Kp best among them, in its lists.
@@ -430,7 +493,7 @@ __global__ __launch_bounds__(512) void flat_seed_threshold(const uint64_t* __res
   const int q = blockIdx.x;
   const uint64_t* c = cand + (size_t)q * S * CAP;
   const uint32_t* c32 = reinterpret_cast<const uint32_t*>(c);
-  auto get = [&](int i) { return (uint64_t)c32[(size_t)(i / FB_N) * (2 * CAP) + i % FB_N]; };
+  auto get = [&](int i) { return (uint64_t)c32[(size_t)(i / FB_N) * (2 * CAP) + 2 * (CAP - FB_N / 2) + i % FB_N]; };
   const int n = S * FB_N;
   const uint64_t hi = n <= 16 * (int)blockDim.x ? block_radix_select<decltype(get), 32, 16>(get, n, Kp, hist, sh)
                                     : block_radix_select<decltype(get), 32>(get, n, Kp, hist, sh);
@@ -720,21 +783,23 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
     tm.mark(1);
     const int grid = ((total + 7) / 8) * 8;
     const float scale = metric == PXG_EUCLIDEAN ? 2.0f : 1.0f;
+    // With several tiles per split, a first pass over the first tile of each
+    // split (spread over the whole store) seeds each query's threshold with
+    // the Kp-th best of those rows, so the full pass appends and compacts
+    // little from its first tile on; the full pass then filters that tile's
+    // stored keys instead of computing it again.
+    const int seeded = tiles_per >= 8 ? 1 : 0;
     auto candidates = [&](auto seed) {
       constexpr bool SD = decltype(seed)::value;
       if (CAP == 256)
         hipLaunchKernelGGL((flat_mfma_candidates<256, SD>), dim3(grid), dim3(256), 0, s, Qp, (int)nq, X.p, (int)N,
-                           (int)ld, qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, Kp, cand, gthr);
+                           (int)ld, qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, Kp, cand, gthr, seeded);
       else
         hipLaunchKernelGGL((flat_mfma_candidates<512, SD>), dim3(grid), dim3(256), 0, s, Qp, (int)nq, X.p, (int)N,
-                           (int)ld, qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, Kp, cand, gthr);
+                           (int)ld, qb, xb.p, scale, d_live.p, d_accept, S, QB, per_split, Kp, cand, gthr, seeded);
       PXG_HIP(hipGetLastError());
     };
-    // With several tiles per split, a first pass over the first tile of each
-    // split (spread over the whole store) seeds each query's threshold with
-    // the Kp-th best of those rows, so the full pass appends and compacts
-    // little from its first tile on.
-    if (tiles_per >= 8) {
+    if (seeded) {
       candidates(std::true_type{});
       hipLaunchKernelGGL(flat_seed_threshold, dim3((unsigned)nq), dim3(512), 0, s, (const uint64_t*)cand, S, CAP, Kp,
                          gthr);
