@@ -384,6 +384,32 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
             }
           }
       }
+      // Each row's two smallest words of the tile, as two 32-bit words in the
+      // entry just below them (smallest first): two threads per row read
+      // the words back (the barrier makes the other waves' stores visible),
+      // keep a sorted pair, and merge with the neighbour lane's pair.
+      __syncthreads();
+      {
+        const int row = tid >> 1, c0 = (tid & 1) * (FB_N / 2);
+        uint64_t* buf = cand + ((size_t)(q0 + row) * S + split) * CAP;
+        uint32_t m1 = 0xFFFFFFFFu, m2 = 0xFFFFFFFFu;
+        if (q0 + row < nq) {
+          const uint4* kw = reinterpret_cast<const uint4*>(reinterpret_cast<const uint32_t*>(buf + (CAP - FB_N / 2)) + c0);
+#pragma unroll
+          for (int u = 0; u < FB_N / 8; ++u) {
+            const uint4 w = kw[u];
+            const uint32_t x4[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              m2 = min(m2, max(m1, x4[e]));
+              m1 = min(m1, x4[e]);
+            }
+          }
+        }
+        const uint32_t p1 = __shfl_xor(m1, 1), p2 = __shfl_xor(m2, 1);
+        const uint32_t n1 = min(m1, p1), n2 = min(max(m1, p1), min(m2, p2));
+        if ((tid & 1) == 0 && q0 + row < nq) buf[CAP - FB_N / 2 - 1] = ((uint64_t)n2 << 32) | n1;
+      }
     } else if (stored) {
       flat_stored_tile<CAP>(cand, S, split, q0, nq, n0, s_end, live, acc_src, thr, cnt, tid);
       vm_wait0();  // the prefetched slice
@@ -497,6 +523,23 @@ __global__ __launch_bounds__(512) void flat_seed_threshold(const uint64_t* __res
   const int n = S * FB_N;
   const uint64_t hi = n <= 16 * (int)blockDim.x ? block_radix_select<decltype(get), 32, 16>(get, n, Kp, hist, sh)
                                     : block_radix_select<decltype(get), 32>(get, n, Kp, hist, sh);
+  if (threadIdx.x == 0 && hi != 0xFFFFFFFFull) atomicMin(gthr + q, (unsigned long long)((hi << 32) | 0xFFFFFFFFull));
+}
+
+// Per query: the Kp-th smallest of the splits' pairs of smallest distance
+// parts (2 S >= Kp words, one entry below each split's stored words). The
+// pairs come from distinct rows, so at least Kp rows have a distance part at
+// or below it: the same kind of bound as flat_seed_threshold's, from 2 words
+// per split instead of FB_N, and as tight unless a split holds three or more
+// of the Kp best seeding rows.
+__global__ __launch_bounds__(64) void flat_seed_threshold2(const uint64_t* __restrict__ cand, int S, int CAP, int Kp,
+                                                           unsigned long long* __restrict__ gthr) {
+  __shared__ int hist[256];
+  __shared__ uint64_t sh[4];
+  const int q = blockIdx.x;
+  const uint32_t* c32 = reinterpret_cast<const uint32_t*>(cand + (size_t)q * S * CAP + (CAP - FB_N / 2 - 1));
+  auto get = [&](int i) { return (uint64_t)c32[(size_t)(i >> 1) * (2 * CAP) + (i & 1)]; };
+  const uint64_t hi = block_radix_select<decltype(get), 32, 16>(get, 2 * S, Kp, hist, sh);
   if (threadIdx.x == 0 && hi != 0xFFFFFFFFull) atomicMin(gthr + q, (unsigned long long)((hi << 32) | 0xFFFFFFFFull));
 }
 
@@ -801,8 +844,14 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
     };
     if (seeded) {
       candidates(std::true_type{});
-      hipLaunchKernelGGL(flat_seed_threshold, dim3((unsigned)nq), dim3(512), 0, s, (const uint64_t*)cand, S, CAP, Kp,
-                         gthr);
+      // the splits' pairs when they are many against Kp (and fit the
+      // select's 16 words per thread), else every seeding word
+      if (2 * S >= 4 * Kp && 2 * S <= 16 * 64)
+        hipLaunchKernelGGL(flat_seed_threshold2, dim3((unsigned)nq), dim3(64), 0, s, (const uint64_t*)cand, S, CAP,
+                           Kp, gthr);
+      else
+        hipLaunchKernelGGL(flat_seed_threshold, dim3((unsigned)nq), dim3(512), 0, s, (const uint64_t*)cand, S, CAP,
+                           Kp, gthr);
       PXG_HIP(hipGetLastError());
     }
     candidates(std::false_type{});
