@@ -368,10 +368,13 @@ def test_thresholds_shared_across_splits(gpu, metric):
 @pytest.mark.parametrize("dim", [16, 32])
 def test_seeded_thresholds(gpu, metric, dim):
     """With many tiles per split, a first pass over one tile of every split
-    seeds each query's threshold before the full pass. Integer data (exact
-    distance ties at the seed), removed rows, a filter, queries whose
-    neighbours all sit past the sampled tiles, and k from 1 to 100: ids and
-    distances match the oracle bit for bit, for rows of 16 and 32 floats."""
+    seeds each query's threshold before the full pass, which filters that
+    tile's stored keys instead of computing them again (k = 1 and 10 select
+    the seed from each split's two smallest keys, k = 100 from every key).
+    Integer data (exact distance ties at the seed), removed rows, a filter,
+    queries whose neighbours all sit past the sampled tiles, and k from 1 to
+    100: ids and distances match the oracle bit for bit, for rows of 16 and
+    32 floats."""
     px = gpu
     rng = np.random.default_rng(5 + metric + dim)
     n, nq = 140_000, 1024  # 8 query blocks x 61 splits of 18 tiles (2304 rows)
