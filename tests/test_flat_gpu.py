@@ -364,7 +364,7 @@ def test_thresholds_shared_across_splits(gpu, metric):
     assert_same(got, oracle_search(px, data, ids, metric, q, 10, accept=acc))
 
 
-@pytest.mark.parametrize("metric", [0, 1])
+@pytest.mark.parametrize("metric", [0, 1, 2])
 @pytest.mark.parametrize("dim", [16, 32])
 def test_seeded_thresholds(gpu, metric, dim):
     """With many tiles per split, a first pass over one tile of every split
