@@ -673,7 +673,7 @@ def main():
     ap.add_argument("--sq8-cpu-sample", type=int, default=2048)
     ap.add_argument("--sq8-cpu1-sample", type=int, default=32)
     ap.add_argument("--ivf-cpu1-sample", type=int, default=1000)
-    ap.add_argument("--cpu1-sample", type=int, default=32, help="queries of the one-thread C2 CPU baseline")
+    ap.add_argument("--cpu1-sample", type=int, default=32, help="queries of the one-thread CPU baseline of the 1M x 768 cosine search")
     ap.add_argument("--skip-c1", action="store_true")
     ap.add_argument("--c1-only", action="store_true", help="run only the 100k x 128 flat leg (prints its JSON object)")
     ap.add_argument("--c1-steps", type=int, default=50)

@@ -1,6 +1,6 @@
 """GPU FlatIndex: the reference's flat.rs tests, parity with the oracle (ids and
 distances bit-exact) on both device paths (MFMA candidates + exact rescoring,
-and the exact VALU scan), the BASELINE configs at parity-test sizes, the
+and the exact VALU scan), the benchmark workloads at parity-test sizes, the
 device-pointer entry point, and concurrent searches on one handle."""
 import threading
 

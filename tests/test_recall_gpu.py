@@ -59,7 +59,7 @@ def test_recall_of_approximate_indexes_and_filtered(gpu):
     x = (centres[rng.integers(0, 50, n)] + 0.3 * rng.standard_normal((n, dim))).astype(np.float32)
     q = (centres[rng.integers(0, 50, 64)] + 0.3 * rng.standard_normal((64, dim))).astype(np.float32)
     ids = np.arange(n, dtype=np.uint64)
-    # SQ8 on the C3-style uniform workload (inner product)
+    # SQ8 on a uniform U(-1,1) workload like the 10M x 96 benchmark (inner product)
     xu = rng.uniform(-1, 1, (n, 64)).astype(np.float32)
     qu = rng.uniform(-1, 1, (64, 64)).astype(np.float32)
     truth = px.FlatIndex(px.VectorSpace(64, px.Metric.INNER_PRODUCT))
