@@ -398,6 +398,34 @@ def test_seeded_thresholds(gpu, metric, dim):
     assert_same(got, oracle_search(px, data, ids, metric, q, 10, live=live, accept=acc))
 
 
+@pytest.mark.parametrize("metric", [0, 2])
+def test_seeded_short_last_split(gpu, metric):
+    """A seeded search whose last split is shorter than a tile: 57,346 rows
+    and 1024 queries split into 57 splits of 8 tiles (1024 rows), the last
+    holding 2 rows, so its seeding tile is mostly unusable slots and the full
+    pass's stored first tile is partial. Removed rows (two of them in the last
+    split), a filter, and k of 1, 10 and 30."""
+    px = gpu
+    rng = np.random.default_rng(91 + metric)
+    n, nq, dim = 57_346, 1024, 24
+    data = rng.standard_normal((n, dim)).astype(np.float32)
+    data[n - 2:] = data[7]  # the last split's rows tie with an early row
+    ids = rng.permutation(n).astype(np.uint64)
+    idx = make_index(px, data, metric, ids, mode=1)
+    gone = np.concatenate([rng.choice(n - 2, 400, replace=False), [n - 1]])
+    for i in gone:
+        idx.remove(int(ids[i]))
+    live = np.ones(n, np.uint8)
+    live[gone] = 0
+    q = np.concatenate([data[rng.choice(n, nq // 2)] + np.float32(0.01), rng.standard_normal((nq // 2, dim))])
+    q = q.astype(np.float32)
+    for k in (1, 10, 30):
+        assert_same(idx.search_batch(q, k), oracle_search(px, data, ids, metric, q, k, live=live, threads=16))
+    acc = np.array([int(i) % 3 != 0 for i in ids], np.uint8)
+    got = idx.search_batch(q, 10, lambda i, _m: i % 3 != 0)
+    assert_same(got, oracle_search(px, data, ids, metric, q, 10, live=live, accept=acc, threads=16))
+
+
 # --- k beyond the block selections (check_k allows up to 2^24, index.rs:212-224) ----------
 @pytest.mark.parametrize("metric", [0, 2, 3])
 def test_large_k_matches_oracle(gpu, metric):
