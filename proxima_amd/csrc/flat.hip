@@ -13,10 +13,12 @@
 //                         sort compacts back to k' whenever it fills. The
 //                         N x nq score matrix never reaches HBM. With many
 //                         tiles per split, a seeding pass scores the first
-//                         tile of every split first: flat_seed_threshold
-//                         turns those keys into each query's starting
-//                         threshold, and the full pass filters them instead
-//                         of recomputing that tile.
+//                         tile of every split first: flat_seed_threshold2
+//                         (from each split's two smallest keys per row) or
+//                         flat_seed_threshold (from all of them) turns those
+//                         keys into each query's starting threshold, and the
+//                         full pass filters them instead of recomputing
+//                         that tile.
 //  3. flat_merge_rescore  per query: radix-select the k' best approximate
 //                         keys over all splits, rescore those k' exactly with
 //                         the reference's 8-lane arithmetic, sort by
