@@ -867,9 +867,13 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
                        flag_count);
     PXG_HIP(hipGetLastError());
   }
-  // exact scan for flagged queries (all of them on the exact path)
+  // exact scan for flagged queries (all of them on the exact path, where the
+  // count is known here and the flags are read once, with the results)
   int nflag = 0;
-  read_flags(&nflag);
+  if (exact_all)
+    nflag = (int)nq;
+  else
+    read_flags(&nflag);
   if (nflag > 0) {
     sc.release_from(6);  // the candidate buffers are dead
     const int CH = exact_chunk_rows((size_t)nflag, N);
@@ -877,7 +881,10 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
     const int kk = (int)std::min<uint64_t>(kq, (uint64_t)CH);
     const size_t per_query = (size_t)nchunks * kk * 8;
     size_t fit = sc.room() / per_query;
-    if (fit == 0) (void)sc.get(7, per_query);  // raises the capacity error
+    if (fit == 0) {
+      if (exact_all) read_flags(nullptr);  // a non-finite query is reported first
+      (void)sc.get(7, per_query);          // raises the capacity error
+    }
     const int G = (int)std::min<size_t>((size_t)nflag, fit);
     uint64_t* ecand = (uint64_t*)sc.get(7, (size_t)G * per_query);
     tm.mark(exact_all ? 1 : 3);
@@ -903,7 +910,10 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
 #undef PXG_EXACT_MERGE
       PXG_HIP(hipGetLastError());
     }
-    PXG_HIP(hipStreamSynchronize(s));
+    if (exact_all)
+      read_flags(nullptr);  // waits for the results; a non-finite query fails the call
+    else
+      PXG_HIP(hipStreamSynchronize(s));
     *fallbacks = exact_all ? 0 : (uint64_t)nflag;
   }
   tm.finish();
