@@ -188,6 +188,8 @@ struct Ctx {
   std::unordered_map<int, DevBuf<unsigned char>> scratch;  // keyed by purpose
   std::vector<unsigned char> host;                         // pinned-free host staging
   unsigned long long* pinned = nullptr;                    // 64 pinned host bytes for a search's flags
+  unsigned char* stage = nullptr;                          // pinned host staging for a search's results
+  size_t stage_n = 0;
   unsigned char* get(int key, size_t bytes) {
     auto& b = scratch[key];
     if (b.n < bytes) b.alloc(bytes + bytes / 8 + 256);
@@ -200,9 +202,24 @@ struct Ctx {
     if (!pinned) PXG_HIP(hipHostMalloc((void**)&pinned, TAIL_WORDS * 8, hipHostMallocDefault));
     return pinned;
   }
+  // Pinned host bytes a host-pointer search copies its results into (one
+  // direct DMA per array instead of staged copies into pageable memory);
+  // grown on demand, only between calls (no copy is in flight then).
+  unsigned char* host_stage(size_t bytes) {
+    if (stage_n < bytes) {
+      if (stage) PXG_HIP(hipHostFree(stage));
+      stage = nullptr;
+      stage_n = 0;
+      const size_t n = bytes + bytes / 8 + 256;
+      PXG_HIP(hipHostMalloc((void**)&stage, n, hipHostMallocDefault));
+      stage_n = n;
+    }
+    return stage;
+  }
   ~Ctx() {
     scratch.clear();
     if (pinned) (void)hipHostFree(pinned);
+    if (stage) (void)hipHostFree(stage);
     if (stream) (void)hipStreamDestroy(stream);
   }
 };

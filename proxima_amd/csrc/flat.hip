@@ -746,9 +746,20 @@ void FlatIndex::remove(uint64_t id) {
 }
 
 // Run the search pipeline on prepared-or-raw device queries.
+void check_query_flags(const unsigned long long* words) {
+  const unsigned long long badv = words[0];
+  if (badv != ~0ull) {
+    const uint32_t qi = (uint32_t)(badv >> 32), comp = (uint32_t)badv;
+    raise(PXG_ERR_NON_FINITE,
+          "vector component " + std::to_string(comp) + " is not finite (query " + std::to_string(qi) + ")", comp,
+          qi, NAN);
+  }
+}
+
 void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, uint64_t k, const uint8_t* d_accept,
                               uint64_t* d_oid, float* d_od, uint32_t* d_oc, Scratch& sc, hipStream_t s,
-                              uint64_t* fallbacks, size_t ldo) {
+                              uint64_t* fallbacks, size_t ldo, bool* deferred) {
+  if (deferred) *deferred = false;
   check_k(k);
   *fallbacks = 0;
   if (nq == 0) return;
@@ -776,14 +787,8 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
   auto read_flags = [&](int* nflag) {
     PXG_HIP(hipMemcpyAsync(tail, bad, 16, hipMemcpyDeviceToHost, s));
     PXG_HIP(hipStreamSynchronize(s));
-    const unsigned long long badv = tail[0];
     if (nflag) std::memcpy(nflag, &tail[1], sizeof(int));
-    if (badv != ~0ull) {
-      const uint32_t qi = (uint32_t)(badv >> 32), comp = (uint32_t)badv;
-      raise(PXG_ERR_NON_FINITE, "vector component " + std::to_string(comp) + " is not finite (query " +
-                                    std::to_string(qi) + ")",
-            comp, qi, NAN);
-    }
+    check_query_flags(tail);
   };
   if (kq == 0) {
     hipLaunchKernelGGL(fill_u32, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s, d_oc, (size_t)nq, 0u);
@@ -910,10 +915,15 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
 #undef PXG_EXACT_MERGE
       PXG_HIP(hipGetLastError());
     }
-    if (exact_all)
+    if (exact_all && deferred) {
+      // the caller waits once, for this copy and its own result copies
+      PXG_HIP(hipMemcpyAsync(tail, bad, 16, hipMemcpyDeviceToHost, s));
+      *deferred = true;
+    } else if (exact_all) {
       read_flags(nullptr);  // waits for the results; a non-finite query fails the call
-    else
+    } else {
       PXG_HIP(hipStreamSynchronize(s));
+    }
     *fallbacks = exact_all ? 0 : (uint64_t)nflag;
   }
   tm.finish();
@@ -1154,11 +1164,33 @@ int pxg_flat_search(const pxg_flat* index, const float* queries, uint64_t nq, ui
     uint32_t* d_oc = (uint32_t*)ctx->get(24, nq * 4);
     PXG_HIP(hipMemcpyAsync(d_q, prep.data(), prep.size() * 4, hipMemcpyHostToDevice, s));
     uint64_t fb = 0;
-    f.search_device(d_q, false, nq, kq, d_acc, d_oid, d_od, d_oc, sc, s, &fb, kq);
-    pxg::rows_to_host(out_ids, k * 8, d_oid, kq * 8, kq * 8, nq, s);
-    pxg::rows_to_host(out_dist, k * 4, d_od, kq * 4, kq * 4, nq, s);
-    PXG_HIP(hipMemcpyAsync(out_count, d_oc, nq * 4, hipMemcpyDeviceToHost, s));
-    PXG_HIP(hipStreamSynchronize(s));
+    bool deferred = false;
+    f.search_device(d_q, false, nq, kq, d_acc, d_oid, d_od, d_oc, sc, s, &fb, kq, &deferred);
+    const size_t bi = (size_t)nq * kq * 8, bd = (size_t)nq * kq * 4, bc = (size_t)nq * 4;
+    if (bi + bd + bc <= (64u << 20)) {
+      // the three arrays into pinned staging (direct DMA), one wait, then
+      // into the caller's rows of k
+      unsigned char* st = ctx->host_stage(bi + bd + bc);
+      PXG_HIP(hipMemcpyAsync(st, d_oid, bi, hipMemcpyDeviceToHost, s));
+      PXG_HIP(hipMemcpyAsync(st + bi, d_od, bd, hipMemcpyDeviceToHost, s));
+      PXG_HIP(hipMemcpyAsync(st + bi + bd, d_oc, bc, hipMemcpyDeviceToHost, s));
+      PXG_HIP(hipStreamSynchronize(s));
+      if (deferred) pxg::check_query_flags(sc.host_words());
+      for (uint64_t i = 0; i < nq; ++i) {
+        std::memcpy(out_ids + i * k, st + i * kq * 8, kq * 8);
+        std::memcpy(out_dist + i * k, st + bi + i * kq * 4, kq * 4);
+      }
+      std::memcpy(out_count, st + bi + bd, bc);
+    } else {
+      if (deferred) {
+        PXG_HIP(hipStreamSynchronize(s));
+        pxg::check_query_flags(sc.host_words());
+      }
+      pxg::rows_to_host(out_ids, k * 8, d_oid, kq * 8, kq * 8, nq, s);
+      pxg::rows_to_host(out_dist, k * 4, d_od, kq * 4, kq * 4, nq, s);
+      PXG_HIP(hipMemcpyAsync(out_count, d_oc, nq * 4, hipMemcpyDeviceToHost, s));
+      PXG_HIP(hipStreamSynchronize(s));
+    }
     pxg::g_last_fallbacks = fb;
   });
 }

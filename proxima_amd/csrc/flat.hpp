@@ -42,14 +42,23 @@ struct FlatIndex {
   void remove(uint64_t id);
   // Search nq device queries (raw when do_prepare, else already prepared
   // rows of ld floats); results go to rows of ldo entries. Scratch comes from
-  // `sc`; the call returns after the results are complete.
+  // `sc`; the call returns after the results are complete. With `deferred`
+  // given, a search that ends on the exact scan may instead return with its
+  // work queued on `s` and the copy of its flag words into sc.host_words()
+  // queued after it (*deferred = true): the caller then waits on `s` and
+  // calls check_query_flags(sc.host_words()) before using the results.
   void search_device(const float* d_raw, bool do_prepare, uint64_t nq, uint64_t k, const uint8_t* d_accept,
                      uint64_t* d_oid, float* d_od, uint32_t* d_oc, Scratch& sc, hipStream_t s, uint64_t* fallbacks,
-                     size_t ldo);
+                     size_t ldo, bool* deferred = nullptr);
   void search_wide(const float* Qp, uint64_t nq, uint64_t kq, const uint8_t* d_accept, uint64_t* d_oid, float* d_od,
                    uint32_t* d_oc, Scratch& sc, hipStream_t s, size_t ldo);
   void insert_device(const uint64_t* in_ids, const float* d_vecs, uint64_t n, uint32_t* out_slots);
 };
+
+// Raises NonFinite when a search's flag words, read back from the device,
+// name a non-finite query (word 0: query << 32 | component, all ones when
+// every query is finite).
+void check_query_flags(const unsigned long long* words);
 
 }  // namespace pxg
 
