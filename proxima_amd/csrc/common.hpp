@@ -224,6 +224,43 @@ struct Ctx {
   }
 };
 
+// A search's results, from device rows of `sp` entries (the first `n` used)
+// to the caller's host rows of `k`: nq rows of ids and of distances, and nq
+// counts. They come through the context's pinned staging with one wait when
+// they fit in 64 MiB, else through staged copies. `check` runs after the
+// wait and before anything reaches the caller's arrays (it may raise).
+template <class F>
+inline void results_to_host(Ctx& c, hipStream_t s, uint64_t nq, uint64_t k, uint64_t n, uint64_t sp,
+                            const uint64_t* d_oid, const float* d_od, const uint32_t* d_oc, uint64_t* out_ids,
+                            float* out_dist, uint32_t* out_count, F check) {
+  const size_t bi = (size_t)nq * sp * 8, bd = (size_t)nq * sp * 4, bc = (size_t)nq * 4;
+  if (bi + bd + bc <= ((size_t)64 << 20)) {
+    unsigned char* st = c.host_stage(bi + bd + bc);
+    if (n) {
+      PXG_HIP(hipMemcpyAsync(st, d_oid, bi, hipMemcpyDeviceToHost, s));
+      PXG_HIP(hipMemcpyAsync(st + bi, d_od, bd, hipMemcpyDeviceToHost, s));
+    }
+    PXG_HIP(hipMemcpyAsync(st + bi + bd, d_oc, bc, hipMemcpyDeviceToHost, s));
+    PXG_HIP(hipStreamSynchronize(s));
+    check();
+    if (n)
+      for (uint64_t i = 0; i < nq; ++i) {
+        std::memcpy(out_ids + i * k, st + i * sp * 8, n * 8);
+        std::memcpy(out_dist + i * k, st + bi + i * sp * 4, n * 4);
+      }
+    std::memcpy(out_count, st + bi + bd, bc);
+  } else {
+    PXG_HIP(hipStreamSynchronize(s));
+    check();
+    if (n) {
+      rows_to_host(out_ids, k * 8, d_oid, sp * 8, n * 8, nq, s);
+      rows_to_host(out_dist, k * 4, d_od, sp * 4, n * 4, nq, s);
+    }
+    PXG_HIP(hipMemcpyAsync(out_count, d_oc, bc, hipMemcpyDeviceToHost, s));
+    PXG_HIP(hipStreamSynchronize(s));
+  }
+}
+
 // Device scratch of one search, by purpose, plus host words for the flag
 // readback at its end. A Ctx allocates on demand; an Arena hands out regions
 // of a fixed block and never allocates.

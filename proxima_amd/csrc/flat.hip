@@ -1166,31 +1166,9 @@ int pxg_flat_search(const pxg_flat* index, const float* queries, uint64_t nq, ui
     uint64_t fb = 0;
     bool deferred = false;
     f.search_device(d_q, false, nq, kq, d_acc, d_oid, d_od, d_oc, sc, s, &fb, kq, &deferred);
-    const size_t bi = (size_t)nq * kq * 8, bd = (size_t)nq * kq * 4, bc = (size_t)nq * 4;
-    if (bi + bd + bc <= (64u << 20)) {
-      // the three arrays into pinned staging (direct DMA), one wait, then
-      // into the caller's rows of k
-      unsigned char* st = ctx->host_stage(bi + bd + bc);
-      PXG_HIP(hipMemcpyAsync(st, d_oid, bi, hipMemcpyDeviceToHost, s));
-      PXG_HIP(hipMemcpyAsync(st + bi, d_od, bd, hipMemcpyDeviceToHost, s));
-      PXG_HIP(hipMemcpyAsync(st + bi + bd, d_oc, bc, hipMemcpyDeviceToHost, s));
-      PXG_HIP(hipStreamSynchronize(s));
+    pxg::results_to_host(*ctx.c, s, nq, k, kq, kq, d_oid, d_od, d_oc, out_ids, out_dist, out_count, [&] {
       if (deferred) pxg::check_query_flags(sc.host_words());
-      for (uint64_t i = 0; i < nq; ++i) {
-        std::memcpy(out_ids + i * k, st + i * kq * 8, kq * 8);
-        std::memcpy(out_dist + i * k, st + bi + i * kq * 4, kq * 4);
-      }
-      std::memcpy(out_count, st + bi + bd, bc);
-    } else {
-      if (deferred) {
-        PXG_HIP(hipStreamSynchronize(s));
-        pxg::check_query_flags(sc.host_words());
-      }
-      pxg::rows_to_host(out_ids, k * 8, d_oid, kq * 8, kq * 8, nq, s);
-      pxg::rows_to_host(out_dist, k * 4, d_od, kq * 4, kq * 4, nq, s);
-      PXG_HIP(hipMemcpyAsync(out_count, d_oc, nq * 4, hipMemcpyDeviceToHost, s));
-      PXG_HIP(hipStreamSynchronize(s));
-    }
+    });
     pxg::g_last_fallbacks = fb;
   });
 }

@@ -2928,10 +2928,7 @@ int pxg_ivfpq_search(const pxg_ivfpq* index, const float* queries, uint64_t nq, 
     uint32_t* d_oc = (uint32_t*)ctx->get(24, nq * 4);
     PXG_HIP(hipMemcpyAsync(d_q, prep.data(), prep.size() * 4, hipMemcpyHostToDevice, s));
     f.search_device(d_q, false, nq, kq, nprobe ? nprobe : f.cfg.nprobe, d_acc, d_oid, d_od, d_oc, sc, s, kq);
-    pxg::rows_to_host(out_ids, k * 8, d_oid, kq * 8, kq * 8, nq, s);
-    pxg::rows_to_host(out_dist, k * 4, d_od, kq * 4, kq * 4, nq, s);
-    PXG_HIP(hipMemcpyAsync(out_count, d_oc, nq * 4, hipMemcpyDeviceToHost, s));
-    PXG_HIP(hipStreamSynchronize(s));
+    pxg::results_to_host(*ctx.c, s, nq, k, kq, kq, d_oid, d_od, d_oc, out_ids, out_dist, out_count, [] {});
   });
 }
 

@@ -1594,12 +1594,7 @@ static int sq8_search_host(const pxg_sq8* index, const float* queries, const int
     }
     uint64_t fb = 0;
     f.search_device(d_q, d_qc, nq, kq, rescore, d_acc, d_oid, d_od, d_oc, sc, s, &fb, kk);
-    if (kq) {
-      pxg::rows_to_host(out_ids, k * 8, d_oid, kk * 8, kq * 8, nq, s);
-      pxg::rows_to_host(out_dist, k * 4, d_od, kk * 4, kq * 4, nq, s);
-    }
-    PXG_HIP(hipMemcpyAsync(out_count, d_oc, nq * 4, hipMemcpyDeviceToHost, s));
-    PXG_HIP(hipStreamSynchronize(s));
+    pxg::results_to_host(*ctx.c, s, nq, k, kq, kk, d_oid, d_od, d_oc, out_ids, out_dist, out_count, [] {});
     pxg::g_sq8_fallbacks = fb;
   });
 }
