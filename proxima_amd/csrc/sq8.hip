@@ -288,13 +288,16 @@ __device__ __forceinline__ uint32_t lds_addr(const T* p) {
 // second A operand, so the matrix core runs while the filter's VALU work and
 // the next block's LDS reads proceed.
 // ---------------------------------------------------------------------------
-template <int KB, bool STAGE1>
+// QTT: query tiles per wave (0 = sq_qt(KB)). A smaller batch takes fewer,
+// so that its queries spread over all the waves (and SIMDs) of a workgroup
+// rather than a few waves multiplying code tiles of absent queries.
+template <int KB, bool STAGE1, int QTT = 0>
 __global__ __launch_bounds__(SQ_NW * 64) void sq8_mfma_scan(
     const int8_t* __restrict__ Qc, int nq, const int8_t* __restrict__ C, int N, const uint8_t* __restrict__ live,
     const uint8_t* __restrict__ accept, const uint32_t* __restrict__ rank, int nchunks, int qgroups,
     int tiles_per_chunk, int sample, const int* __restrict__ thr_in, int* __restrict__ tmax,
     int* __restrict__ ccount, uint64_t* __restrict__ cand, int cap) {
-  constexpr int KP = KB * 32, SR = KP + 16, R = sq_rows(KB), RT = R / 32, QT = sq_qt(KB);
+  constexpr int KP = KB * 32, SR = KP + 16, R = sq_rows(KB), RT = R / 32, QT = QTT > 0 ? QTT : sq_qt(KB);
   constexpr int PPR = KP / 16;         // 16-byte pieces per row
   constexpr int D = 3;                // LDS tiles: the next two tiles load during the current one
   __shared__ __align__(16) int8_t tile[D][R * SR];
@@ -1189,7 +1192,11 @@ struct Sq8Index {
       PXG_HIP(hipGetLastError());
     };
     if (mfma) {
-      const int R = sq_rows(KB), QT = sq_qt(KB);
+      // query tiles per wave: the fewest that hold the batch in one
+      // workgroup's SQ_NW waves (1 up to 256 queries, 2 up to 512), at most
+      // sq_qt(KB); qtt names the kernel variant (0 = sq_qt(KB))
+      const int R = sq_rows(KB), QT = nq <= 256 ? 1 : (nq <= 512 ? std::min(2, sq_qt(KB)) : sq_qt(KB));
+      const int qtt = QT == sq_qt(KB) ? 0 : QT;
       // Chunks: about 512 (two per CU), and at least 2 * kk so that every
       // query gets >= 4 * kk stage-1 maxima when the index has the tiles.
       // Stage 1 samples every `sample`-th tile (a divisor of the chunk
@@ -1216,11 +1223,18 @@ struct Sq8Index {
       int* ccount = (int*)sc.get(11, nq * 4);
       uint64_t* cand = (uint64_t*)sc.get(12, nq * cap_c * 8);
       const dim3 grid((unsigned)((nchunks * qgroups + 7) / 8 * 8));
-#define PXG_SQ_SCAN(KBV, ST)                                                                                        \
-  hipLaunchKernelGGL((sq8_mfma_scan<KBV, ST>), grid, dim3(SQ_NW * 64), 0, s, (const int8_t*)Qc, (int)nq,           \
+#define PXG_SQ_SCAN_Q(KBV, ST, QTV)                                                                                 \
+  hipLaunchKernelGGL((sq8_mfma_scan<KBV, ST, QTV>), grid, dim3(SQ_NW * 64), 0, s, (const int8_t*)Qc, (int)nq,      \
                      (const int8_t*)codes.p, N, d_live.p, d_accept, ranks.rank.p, nchunks, qgroups, tpc, sample,       \
                      (const int*)thr, tmax,                                                                        \
                      ccount, cand, cap_c)
+#define PXG_SQ_SCAN(KBV, ST)             \
+  if (qtt == 1)                          \
+    PXG_SQ_SCAN_Q(KBV, ST, 1);           \
+  else if (qtt == 2)                     \
+    PXG_SQ_SCAN_Q(KBV, ST, 2);           \
+  else                                   \
+    PXG_SQ_SCAN_Q(KBV, ST, 0)
 #define PXG_SQ_SWITCH(ST)                  \
   switch (KB) {                            \
     case 1: PXG_SQ_SCAN(1, ST); break;     \
@@ -1243,6 +1257,7 @@ struct Sq8Index {
       PXG_SQ_SWITCH(false)
 #undef PXG_SQ_SWITCH
 #undef PXG_SQ_SCAN
+#undef PXG_SQ_SCAN_Q
       PXG_HIP(hipGetLastError());
       tm.mark(2);
       hipLaunchKernelGGL(sq8_finish, dim3((unsigned)nq), dim3(256), (size_t)cap_c * 8, s, (const int*)ccount,

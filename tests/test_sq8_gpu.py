@@ -128,11 +128,17 @@ def test_search_parity_all_paths(gpu, dim, mode):
     idx.insert_batch(np.arange(n, dtype=np.uint64), x)
     idx.set_search_mode(mode)
     codes, ranges = oracle_index(x, x[:5000])
-    q = uniform(rng, nq, dim)
+    qa = uniform(rng, 300, dim)
+    q = qa[:nq]
     for k in (1, 10, 100):
         assert_same(idx.search_batch(q, k), oracle_search(codes, np.arange(n), q, ranges, k))
     if mode == 0:  # automatic mode picks a path that needs no rescans
         assert px.Sq8Index.last_fallbacks() == 0
+    # other batch sizes: the MFMA scan holds 1 query tile per wave up to 256
+    # queries, 2 up to 512, then the full count
+    for m in (1, 17, 32, 300):
+        for k in (1, 10):
+            assert_same(idx.search_batch(qa[:m], k), oracle_search(codes, np.arange(n), qa[:m], ranges, k))
 
 
 def test_ranges_and_codes_match_oracle(gpu):
