@@ -148,50 +148,43 @@ __device__ inline float dist_group8(const float* __restrict__ a, const float* __
   return r;
 }
 
-// dist_group8 for two rows b0 and b1 against the same a, in one loop: each
-// row keeps its own accumulator and add order, and both rows' loads (and a's,
-// once) are in flight together.
+// dist_group8's arithmetic with two lanes per row: lane h (of an adjacent
+// pair) owns the reference's accumulators 4h .. 4h+3, i.e. elements 8c + 4h
+// .. 8c + 4h + 3 of every chunk c, loaded as one float4 per chunk and added
+// in chunk order; its half (a0 + a1) + (a2 + a3) and the partner's combine
+// as ((0+1)+(2+3)) + ((4+5)+(6+7)), dist_group8's reduce (the last add is
+// commutative, so both lanes get the same bits). Rows start 16-byte aligned.
 template <int METRIC>
-__device__ inline void dist_group8_x2(const float* __restrict__ a, const float* __restrict__ b0,
-                                      const float* __restrict__ b1, int dim, int g, float& r0, float& r1) {
-  float acc0 = 0.0f, acc1 = 0.0f;
+__device__ inline float dist_pair4(const float* __restrict__ a, const float* __restrict__ b, int dim, int h) {
+  float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
   const int chunks = dim >> 3;
-#pragma unroll 16
+  const float* ap = a + 4 * h;
+  const float* bp = b + 4 * h;
+#pragma unroll 8
   for (int c = 0; c < chunks; ++c) {
-    const float x = a[c * 8 + g];
-    acc0 += lane_term<METRIC>(x, b0[c * 8 + g]);
-    acc1 += lane_term<METRIC>(x, b1[c * 8 + g]);
+    const float4 x = *reinterpret_cast<const float4*>(ap + 8 * c);
+    const float4 y = *reinterpret_cast<const float4*>(bp + 8 * c);
+    s0 += lane_term<METRIC>(x.x, y.x);
+    s1 += lane_term<METRIC>(x.y, y.y);
+    s2 += lane_term<METRIC>(x.z, y.z);
+    s3 += lane_term<METRIC>(x.w, y.w);
   }
-  acc0 = acc0 + __shfl_xor(acc0, 1, WAVE);
-  acc1 = acc1 + __shfl_xor(acc1, 1, WAVE);
-  acc0 = acc0 + __shfl_xor(acc0, 2, WAVE);
-  acc1 = acc1 + __shfl_xor(acc1, 2, WAVE);
-  acc0 = acc0 + __shfl_xor(acc0, 4, WAVE);
-  acc1 = acc1 + __shfl_xor(acc1, 4, WAVE);
-  float t0 = 0.0f, t1 = 0.0f;
-  for (int i = chunks * 8; i < dim; ++i) {
-    t0 += lane_term<METRIC>(a[i], b0[i]);
-    t1 += lane_term<METRIC>(a[i], b1[i]);
-  }
-  r0 = acc0 + t0;
-  r1 = acc1 + t1;
-  if constexpr (METRIC == 1) {
-    r0 = arm_nan(1.0f - arm_nan(r0));
-    r1 = arm_nan(1.0f - arm_nan(r1));
-  }
-  if constexpr (METRIC == 2) {
-    r0 = -arm_nan(r0);
-    r1 = -arm_nan(r1);
-  }
+  const float half = (s0 + s1) + (s2 + s3);
+  const float acc = half + __shfl_xor(half, 1, WAVE);
+  float tail = 0.0f;
+  for (int i = chunks * 8; i < dim; ++i) tail += lane_term<METRIC>(a[i], b[i]);
+  const float r = acc + tail;
+  if constexpr (METRIC == 1) return arm_nan(1.0f - arm_nan(r));
+  if constexpr (METRIC == 2) return -arm_nan(r);
+  return r;
 }
 
-__device__ inline void dist_group8_x2_rt(int metric, const float* a, const float* b0, const float* b1, int dim, int g,
-                                         float& r0, float& r1) {
+__device__ inline float dist_pair4_rt(int metric, const float* a, const float* b, int dim, int h) {
   switch (metric) {
-    case 0: dist_group8_x2<0>(a, b0, b1, dim, g, r0, r1); break;
-    case 1: dist_group8_x2<1>(a, b0, b1, dim, g, r0, r1); break;
-    case 2: dist_group8_x2<2>(a, b0, b1, dim, g, r0, r1); break;
-    default: dist_group8_x2<3>(a, b0, b1, dim, g, r0, r1); break;
+    case 0: return dist_pair4<0>(a, b, dim, h);
+    case 1: return dist_pair4<1>(a, b, dim, h);
+    case 2: return dist_pair4<2>(a, b, dim, h);
+    default: return dist_pair4<3>(a, b, dim, h);
   }
 }
 

@@ -118,8 +118,24 @@ template <int CH>
     const int q = qlist[f];
     const float* qv = Qp + (size_t)q * ld;
     const int base = c * CH;
-    if (dim < 256) {
-      // a row's chunks fit one batch of loads (dist_group8 unrolls 16)
+    if (dim >= 8) {
+      // two lanes per row (dist_pair4): 128 rows per pass of the workgroup,
+      // one float4 per lane per 8-wide chunk; rows past N or not usable are
+      // scored from a clamped row (both lanes of a pair take part in its
+      // shuffle) and keep KEY_MAX
+      const int h = threadIdx.x & 1;
+      for (int s = threadIdx.x >> 1; s < CH; s += 128) {
+        const int slot = base + s;
+        const bool u = slot < N && live[slot] && (accept == nullptr || accept[slot]);
+        uint64_t key = KEY_MAX;
+        if (__any(u)) {
+          const float d = dist_pair4_rt(metric, qv, X + (size_t)max(min(slot, N - 1), 0) * ld, dim, h);
+          if (u) key = ((uint64_t)ord_key(d) << 32) | rank[slot];
+        }
+        if (h == 0) keys[s] = key;
+      }
+    } else {
+      // rows narrower than one 8-wide chunk: eight lanes per row
       for (int s = grp; s < CH; s += 32) {
         const int slot = base + s;
         uint64_t key = KEY_MAX;
@@ -128,28 +144,6 @@ template <int CH>
           key = ((uint64_t)ord_key(d) << 32) | rank[slot];
         }
         if (g == 0) keys[s] = key;
-      }
-    } else {
-      // two rows per group at a time (s and s + 32), both rows' loads in
-      // flight together; rows past N or not usable are scored from a clamped
-      // row and keep KEY_MAX
-      static_assert(CH % 64 == 0, "row pairs");
-      for (int s = grp; s < CH; s += 64) {
-        const int s0 = base + s, s1 = base + s + 32;
-        const bool u0 = s0 < N && live[s0] && (accept == nullptr || accept[s0]);
-        const bool u1 = s1 < N && live[s1] && (accept == nullptr || accept[s1]);
-        uint64_t k0 = KEY_MAX, k1 = KEY_MAX;
-        if (__any(u0 || u1)) {
-          float d0, d1;
-          dist_group8_x2_rt(metric, qv, X + (size_t)max(min(s0, N - 1), 0) * ld, X + (size_t)max(min(s1, N - 1), 0) * ld,
-                            dim, g, d0, d1);
-          if (u0) k0 = ((uint64_t)ord_key(d0) << 32) | rank[s0];
-          if (u1) k1 = ((uint64_t)ord_key(d1) << 32) | rank[s1];
-        }
-        if (g == 0) {
-          keys[s] = k0;
-          keys[s + 32] = k1;
-        }
       }
     }
     __syncthreads();
