@@ -1282,13 +1282,24 @@ __global__ __launch_bounds__(256) void ivf_merge(const uint64_t* __restrict__ ca
   block_bitonic_sort(sel, P);
   int kout = min(k, ksel);
   if (rerank) {
-    // exact rescoring of the shortlist (ivfpq.rs:1098-1109)
-    const int g = threadIdx.x & 7, grp = threadIdx.x >> 3;
+    // exact rescoring of the shortlist (ivfpq.rs:1098-1109): two lanes per
+    // candidate (dist_pair4, the same bits as dist_group8), eight for rows
+    // narrower than one 8-wide chunk
     const float* qv = Qp + (size_t)q * ld;
-    for (int c = grp; c < ksel; c += 32) {
-      const uint32_t rk = (uint32_t)sel[c];
-      const float d = dist_group8_rt(metric, qv, X + (size_t)rank_slot[rk] * ld, dim, g);
-      if (g == 0) sel[c] = ((uint64_t)ord_key(d) << 32) | rk;
+    if (dim >= 8) {
+      const int h = threadIdx.x & 1;
+      for (int c = threadIdx.x >> 1; c < ksel; c += (int)blockDim.x / 2) {
+        const uint32_t rk = (uint32_t)sel[c];
+        const float d = dist_pair4_rt(metric, qv, X + (size_t)rank_slot[rk] * ld, dim, h);
+        if (h == 0) sel[c] = ((uint64_t)ord_key(d) << 32) | rk;
+      }
+    } else {
+      const int g = threadIdx.x & 7, grp = threadIdx.x >> 3;
+      for (int c = grp; c < ksel; c += 32) {
+        const uint32_t rk = (uint32_t)sel[c];
+        const float d = dist_group8_rt(metric, qv, X + (size_t)rank_slot[rk] * ld, dim, g);
+        if (g == 0) sel[c] = ((uint64_t)ord_key(d) << 32) | rk;
+      }
     }
     __syncthreads();
     block_bitonic_sort(sel, P);
