@@ -809,7 +809,7 @@ def main():
         log(f"[bench] tail batch of {nt}: {tail_s * 1e3:.3f} ms; all {args.queries} queries at "
             f"{args.queries / all_s:.0f} QPS")
     qhost = queries.cpu().numpy()
-    host = host_path(idx.search_batch, [qhost[i * B:(i + 1) * B] for i in range(2)], args.k, reps=2)
+    host = host_path(idx.search_batch, [qhost[i * B:(i + 1) * B] for i in range(2)], args.k, reps=5)
     lat = latency_batch1(idx.search_all, qhost, args.k, repeats=100)
     log(f"[bench] host path {host['ms_per_batch']} ms/batch; batch-1 latency mean {lat['mean_us']} us, "
         f"p95 {lat['p95_us']} us")
