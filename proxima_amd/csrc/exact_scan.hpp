@@ -110,11 +110,20 @@ template <int CH>
     int dim, int metric, const float* __restrict__ X, int N, const uint8_t* __restrict__ live,
     const uint8_t* __restrict__ accept, const uint32_t* __restrict__ rank, int k, uint64_t* __restrict__ ecand) {
   __shared__ uint64_t keys[CH];
-  const int total = (*qcount) * nchunks;
+  const int nf = *qcount;
+  const int total = nf * nchunks;
   const int g = threadIdx.x & 7, grp = threadIdx.x >> 3;
   const int kk = min(k, CH);
-  for (int w = blockIdx.x; w < total; w += gridDim.x) {
-    const int f = w / nchunks, c = w % nchunks;
+  // Chunk-major work order, dealt to the XCDs in contiguous ranges: the
+  // queries of one chunk run on one XCD at about the same time and share its
+  // L2 copy of the chunk's rows. Workgroup ids go round-robin over the 8
+  // XCDs and the grid is a multiple of 8, so w & 7 keeps naming the same XCD
+  // on every pass of the grid-stride loop.
+  const int per_xcd = (total + 7) / 8;
+  for (int w = blockIdx.x; w < 8 * per_xcd; w += gridDim.x) {
+    const int item = (w & 7) * per_xcd + (w >> 3);
+    if (item >= total) continue;  // uniform over the workgroup
+    const int c = item / nf, f = item % nf;
     const int q = qlist[f];
     const float* qv = Qp + (size_t)q * ld;
     const int base = c * CH;

@@ -901,7 +901,7 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
         count = grp_count;
       }
 #define PXG_EXACT_SCAN(CHV)                                                                                   \
-  hipLaunchKernelGGL(flat_exact_candidates<CHV>, dim3(std::min(gn * nchunks, 4096)), dim3(256), 0, s,          \
+  hipLaunchKernelGGL(flat_exact_candidates<CHV>, dim3((std::min(gn * nchunks, 4096) + 7) / 8 * 8), dim3(256), 0, s,          \
                      flag_list + g0, count, nchunks, Qp, (int)ld, (int)dim, metric, X.p, (int)N, d_live.p,     \
                      d_accept, ranks.rank.p, (int)kq, ecand)
 #define PXG_EXACT_MERGE(CHV)                                                                                  \

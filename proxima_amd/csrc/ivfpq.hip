@@ -2416,7 +2416,7 @@ struct IvfPqIndex {
       uint64_t* ecand = (uint64_t*)sc.get(7, (size_t)nq * nchunks * kk * 8);
       tm.mark(1);
 #define PXG_EXACT_SCAN(CHV)                                                                                       \
-  hipLaunchKernelGGL(flat_exact_candidates<CHV>, dim3(std::min<int>((int)nq * nchunks, 4096)), dim3(256), 0, s,    \
+  hipLaunchKernelGGL(flat_exact_candidates<CHV>, dim3((std::min<int>((int)nq * nchunks, 4096) + 7) / 8 * 8), dim3(256), 0, s,    \
                      qlist, flag_count, nchunks, Qp, (int)ld, (int)dim, metric, X.p, (int)N, d_live.p, d_accept,  \
                      ranks.rank.p, (int)kq, ecand)
 #define PXG_EXACT_MERGE(CHV)                                                                                      \
