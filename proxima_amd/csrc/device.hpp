@@ -255,6 +255,24 @@ __device__ inline void wave_bitonic_sort(uint64_t (&k)[E], int lane) {
   }
 }
 
+// Ascending bitonic sort of 64 (key, value) pairs across one wavefront, one
+// pair per lane: afterwards lane L holds the L-th smallest key and its value.
+__device__ inline void wave_sort_kv64(uint64_t& key, uint32_t& val, int lane) {
+#pragma unroll
+  for (int size = 2; size <= WAVE; size <<= 1) {
+#pragma unroll
+    for (int j = size >> 1; j > 0; j >>= 1) {
+      const uint64_t pk = shfl_xor64(key, j);
+      const uint32_t pv = xor_lane_rt(val, j);
+      // the lower lane of a pair keeps the smaller key in an ascending run
+      const bool take_min = ((lane & j) == 0) == ((lane & size) == 0);
+      const bool take = take_min ? pk < key : key < pk;
+      key = take ? pk : key;
+      val = take ? pv : val;
+    }
+  }
+}
+
 // ----------------------------------------------------------------------------
 // Block radix select: the K-th smallest (1-based, counting repeats) of n
 // BITS-bit keys read through `get(i)`. All threads of the block call it;
@@ -269,28 +287,12 @@ __device__ inline void wave_bitonic_sort(uint64_t (&k)[E], int lane) {
 // them are then among the K smallest, and the K-th smallest is their
 // largest, found by a block maximum.
 // ----------------------------------------------------------------------------
-template <class Get, int BITS = 64, int PER = 0>
-__device__ inline uint64_t block_radix_select(Get get, int n, int K, int* hist, uint64_t* sh) {
+// block_radix_select over keys the calling threads already hold: each(f)
+// calls f(x) once for every key of the calling thread, in a fixed order (the
+// keys of all threads together are the n keys).
+template <int BITS, class Each>
+__device__ inline uint64_t block_radix_select_each(Each each, int K, int* hist, uint64_t* sh) {
   static_assert(BITS % 8 == 0 && BITS <= 64, "whole-byte digits");
-  constexpr int C = PER > 0 ? PER : 1;
-  uint64_t v[C];
-  if constexpr (PER > 0) {
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int i = threadIdx.x + j * blockDim.x;
-      v[j] = i < n ? (uint64_t)get(i) : 0;
-    }
-  }
-  // every key of this thread, in order: f(x)
-  auto each = [&](auto f) {
-    if constexpr (PER > 0) {
-#pragma unroll
-      for (int j = 0; j < PER; ++j)
-        if (threadIdx.x + j * blockDim.x < n) f(v[j]);
-    } else {
-      for (int i = threadIdx.x; i < n; i += blockDim.x) f((uint64_t)get(i));
-    }
-  };
   if (threadIdx.x == 0) sh[3] = 0;
   uint64_t prefix = 0, mask = 0;
   int remaining = K;
@@ -359,6 +361,31 @@ __device__ inline uint64_t block_radix_select(Get get, int n, int K, int* hist, 
     }
   }
   return prefix;
+}
+
+template <class Get, int BITS = 64, int PER = 0>
+__device__ inline uint64_t block_radix_select(Get get, int n, int K, int* hist, uint64_t* sh) {
+  static_assert(BITS % 8 == 0 && BITS <= 64, "whole-byte digits");
+  constexpr int C = PER > 0 ? PER : 1;
+  uint64_t v[C];
+  if constexpr (PER > 0) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int i = threadIdx.x + j * blockDim.x;
+      v[j] = i < n ? (uint64_t)get(i) : 0;
+    }
+  }
+  // every key of this thread, in order: f(x)
+  auto each = [&](auto f) {
+    if constexpr (PER > 0) {
+#pragma unroll
+      for (int j = 0; j < PER; ++j)
+        if (threadIdx.x + j * blockDim.x < n) f(v[j]);
+    } else {
+      for (int i = threadIdx.x; i < n; i += blockDim.x) f((uint64_t)get(i));
+    }
+  };
+  return block_radix_select_each<BITS>(each, K, hist, sh);
 }
 
 }  // namespace pxg

@@ -25,7 +25,11 @@
 //                         (total_cmp(distance), id) and keep k. A query whose
 //                         k-th exact distance is not below the k'-th
 //                         approximate one minus the MFMA error bound is
-//                         flagged.
+//                         flagged. flat_merge_rescore_reg does the same
+//                         when a query's keys fit eight per thread and k'
+//                         one wavefront: its keys are read once into
+//                         registers and one wavefront sorts the rescored
+//                         ones.
 //  4. flat_exact_candidates + flat_merge_exact   exact VALU scan for flagged
 //                         queries (and the whole batch for Manhattan, small
 //                         problems, or when forced). Distances are the
@@ -547,6 +551,25 @@ __global__ __launch_bounds__(64) void flat_seed_threshold2(const uint64_t* __res
 
 constexpr int MERGE_MAXP = 512;
 
+// The certificate of one query's merge. Every candidate outside the
+// selection has approx >= approx(pivot), hence exact >= approx(pivot) - eps;
+// the k-th exact distance (the high word of `kth`) must be strictly below
+// that for the selection to contain the exact top-k.
+__device__ inline bool merge_certified(uint64_t pivot, uint64_t kth, int metric, float qnv, float maxnorm, float eps_c,
+                                       int dim) {
+  const float ak = key_float((uint32_t)(pivot >> 32));
+  const float dk = key_float((uint32_t)(kth >> 32));
+  float eps;
+  if (metric == 0) {
+    const float s = qnv + maxnorm;
+    eps = eps_c * (float)dim * 5.9604645e-08f * s * s;
+  } else {
+    eps = eps_c * (float)dim * 5.9604645e-08f * qnv * maxnorm + 2.4e-7f;
+  }
+  eps += 1e-30f;
+  return dk < ak - eps;
+}
+
 __global__ __launch_bounds__(256) void flat_merge_rescore(
     const uint64_t* __restrict__ cand, int S, int CAP, int Kp, int k, const float* __restrict__ Qp, int ld, int dim,
     int metric, const float* __restrict__ X, const uint32_t* __restrict__ rank, const uint32_t* __restrict__ rank_slot,
@@ -623,25 +646,99 @@ __global__ __launch_bounds__(256) void flat_merge_rescore(
   }
   if (threadIdx.x == 0) {
     out_count[q] = kout;
-    if (valid >= Kp) {
-      // Every candidate outside the selection has approx >= approx(pivot),
-      // hence exact >= approx(pivot) - eps. The k-th exact distance must be
-      // strictly below that for the selection to contain the exact top-k.
-      const float ak = key_float((uint32_t)(pivot >> 32));
-      const float dk = key_float((uint32_t)(sel[kout - 1] >> 32));
-      const float qnv = qn[q];
-      float eps;
-      if (metric == 0) {
-        const float s = qnv + maxnorm;
-        eps = eps_c * (float)dim * 5.9604645e-08f * s * s;
-      } else {
-        eps = eps_c * (float)dim * 5.9604645e-08f * qnv * maxnorm + 2.4e-7f;
-      }
-      eps += 1e-30f;
-      if (!(dk < ak - eps)) {
-        const int p = atomicAdd(flag_count, 1);
-        flag_list[p] = q;
-      }
+    if (valid >= Kp && !merge_certified(pivot, sel[kout - 1], metric, qn[q], maxnorm, eps_c, dim)) {
+      const int p = atomicAdd(flag_count, 1);
+      flag_list[p] = q;
+    }
+  }
+}
+
+// flat_merge_rescore for a query whose S * Kp keys fit eight per thread and
+// whose Kp fits one wavefront. Each key is read once into registers, and the
+// count, the select and the gather use that copy; one wavefront sorts the
+// rescored keys with their slots in registers. Same results as the general
+// kernel: the same selection, rescore arithmetic and (distance, rank) order.
+__global__ __launch_bounds__(256) void flat_merge_rescore_reg(
+    const uint64_t* __restrict__ cand, int S, int CAP, int Kp, int k, const float* __restrict__ Qp, int ld, int dim,
+    int metric, const float* __restrict__ X, const uint32_t* __restrict__ rank, const uint64_t* __restrict__ ids,
+    const float* __restrict__ qn, float maxnorm, float eps_c, uint64_t* __restrict__ out_ids,
+    float* __restrict__ out_d, uint32_t* __restrict__ out_count, int* __restrict__ flag_list,
+    int* __restrict__ flag_count, size_t ldo) {
+  constexpr int PER = 8;
+  const int q = blockIdx.x;
+  const int lane = threadIdx.x & (WAVE - 1);
+  __shared__ int hist[256];
+  __shared__ uint64_t sh[4];
+  __shared__ uint64_t sel[WAVE];
+  __shared__ uint64_t rkey[WAVE];
+  __shared__ uint32_t rslot[WAVE];
+  __shared__ int n_sel;
+  __shared__ int n_valid;
+  const uint64_t* base = cand + (size_t)q * S * CAP;
+  const int n = S * Kp;
+  if (threadIdx.x == 0) {
+    n_valid = 0;
+    n_sel = 0;
+  }
+  uint64_t x[PER];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int i = min((int)threadIdx.x + u * (int)blockDim.x, n - 1);  // unconditional loads
+    x[u] = base[(size_t)(i / Kp) * CAP + i % Kp];
+  }
+  int wcount = 0;
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    if ((int)threadIdx.x + u * (int)blockDim.x >= n) x[u] = KEY_MAX;
+    wcount += __popcll(__ballot(x[u] != KEY_MAX));
+  }
+  __syncthreads();  // the counters are set
+  if (lane == 0) atomicAdd(&n_valid, wcount);
+  __syncthreads();
+  const int valid = n_valid;
+  const int ksel = min(Kp, valid);
+  if (ksel == 0) {
+    if (threadIdx.x == 0) out_count[q] = 0;
+    return;
+  }
+  auto each = [&](auto f) {
+#pragma unroll
+    for (int u = 0; u < PER; ++u)
+      if (x[u] != KEY_MAX) f(x[u]);
+  };
+  const uint64_t pivot = block_radix_select_each<64>(each, ksel, hist, sh);
+  // keys are distinct (one per row), so exactly ksel of them are <= pivot
+#pragma unroll
+  for (int u = 0; u < PER; ++u)
+    if (x[u] <= pivot && x[u] != KEY_MAX) sel[atomicAdd(&n_sel, 1)] = x[u];
+  __syncthreads();
+  // rescore: 8 threads per candidate
+  const int g = threadIdx.x & 7, grp = threadIdx.x >> 3;
+  const float* qv = Qp + (size_t)q * ld;
+  for (int c = grp; c < ksel; c += (int)blockDim.x / 8) {
+    const uint32_t slot = (uint32_t)sel[c];
+    const float d = dist_group8_rt(metric, qv, X + (size_t)slot * ld, dim, g);
+    if (g == 0) {
+      rkey[c] = ((uint64_t)ord_key(d) << 32) | rank[slot];
+      rslot[c] = slot;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x >= WAVE) return;
+  uint64_t key = lane < ksel ? rkey[lane] : KEY_MAX;
+  uint32_t slot = lane < ksel ? rslot[lane] : 0;
+  wave_sort_kv64(key, slot, lane);
+  const int kout = min(k, ksel);
+  if (lane < kout) {
+    out_ids[(size_t)q * ldo + lane] = ids[slot];
+    out_d[(size_t)q * ldo + lane] = key_float((uint32_t)(key >> 32));
+  }
+  const uint32_t kth_hi = (uint32_t)__shfl((int)(uint32_t)(key >> 32), kout - 1, WAVE);
+  if (lane == 0) {
+    out_count[q] = kout;
+    if (valid >= Kp && !merge_certified(pivot, (uint64_t)kth_hi << 32, metric, qn[q], maxnorm, eps_c, dim)) {
+      const int p = atomicAdd(flag_count, 1);
+      flag_list[p] = q;
     }
   }
 }
@@ -863,9 +960,14 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
     }
     candidates(std::false_type{});
     tm.mark(2);
-    hipLaunchKernelGGL(flat_merge_rescore, dim3((unsigned)nq), dim3(256), 0, s, cand, S, CAP, Kp, (int)kq, Qp,
-                       (int)ld, (int)dim, metric, X.p, ranks.rank.p, ranks.rank_slot.p, d_ids.p, qn, maxnorm, 4.0f,
-                       d_oid, d_od, d_oc, flag_list, flag_count, ldo);
+    if ((size_t)S * Kp <= 8 * 256 && Kp <= WAVE)
+      hipLaunchKernelGGL(flat_merge_rescore_reg, dim3((unsigned)nq), dim3(256), 0, s, cand, S, CAP, Kp, (int)kq, Qp,
+                         (int)ld, (int)dim, metric, X.p, ranks.rank.p, d_ids.p, qn, maxnorm, 4.0f, d_oid, d_od, d_oc,
+                         flag_list, flag_count, ldo);
+    else
+      hipLaunchKernelGGL(flat_merge_rescore, dim3((unsigned)nq), dim3(256), 0, s, cand, S, CAP, Kp, (int)kq, Qp,
+                         (int)ld, (int)dim, metric, X.p, ranks.rank.p, ranks.rank_slot.p, d_ids.p, qn, maxnorm, 4.0f,
+                         d_oid, d_od, d_oc, flag_list, flag_count, ldo);
     PXG_HIP(hipGetLastError());
   } else {
     hipLaunchKernelGGL(iota_kernel, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s, flag_list, (int)nq,

@@ -341,6 +341,29 @@ def test_growth_preserves_contents(gpu):
     assert_same(idx.search_batch(q, 15), oracle_search(px, data, np.arange(5000), 0, q, 15))
 
 
+@pytest.mark.parametrize("metric", [0, 1])
+def test_merge_register_boundary(gpu, metric):
+    """1000 queries over 16,384 rows make 32 splits. k = 48 (k' = 64) puts
+    exactly 2048 keys per query into the merge that holds them in registers
+    and sorts one wavefront; k = 49 (k' = 65) takes the general merge; k = 1
+    is the smallest selection. Every vector is stored twice under unrelated
+    ids, so equal distances are ordered by id, and a filter that accepts 33
+    rows leaves every query fewer than k' candidates."""
+    px = gpu
+    rng = np.random.default_rng(901 + metric)
+    n, dim, nq = 16384, 40, 1000
+    half = rng.standard_normal((n // 2, dim)).astype(np.float32)
+    data = np.concatenate([half, half])
+    ids = rng.permutation(n).astype(np.uint64)
+    idx = make_index(px, data, metric, ids, 1)
+    q = rng.standard_normal((nq, dim)).astype(np.float32)
+    for k in (1, 48, 49):
+        assert_same(idx.search_batch(q, k), oracle_search(px, data, ids, metric, q, k))
+    keep = lambda i, _m: i % 500 == 0  # noqa: E731
+    acc = (ids % 500 == 0).astype(np.uint8)
+    assert_same(idx.search_batch(q, 48, keep), oracle_search(px, data, ids, metric, q, 48, accept=acc))
+
+
 @pytest.mark.parametrize("metric", [0, 2])
 def test_thresholds_shared_across_splits(gpu, metric):
     """The MFMA path splits the store over many workgroups per query block,
