@@ -653,18 +653,19 @@ __global__ __launch_bounds__(256) void flat_merge_rescore(
   }
 }
 
-// flat_merge_rescore for a query whose S * Kp keys fit eight per thread and
-// whose Kp fits one wavefront. Each key is read once into registers, and the
-// count, the select and the gather use that copy; one wavefront sorts the
-// rescored keys with their slots in registers. Same results as the general
-// kernel: the same selection, rescore arithmetic and (distance, rank) order.
-__global__ __launch_bounds__(256) void flat_merge_rescore_reg(
+// flat_merge_rescore for a query whose S * Kp keys fit PER per thread of an
+// NT-thread block and whose Kp fits one wavefront. Each key is read once into
+// registers, and the count, the select and the gather use that copy; one
+// wavefront sorts the rescored keys with their slots in registers. Same
+// results as the general kernel: the same selection, rescore arithmetic and
+// (distance, rank) order.
+template <int NT, int PER>
+__global__ __launch_bounds__(NT) void flat_merge_rescore_reg(
     const uint64_t* __restrict__ cand, int S, int CAP, int Kp, int k, const float* __restrict__ Qp, int ld, int dim,
     int metric, const float* __restrict__ X, const uint32_t* __restrict__ rank, const uint64_t* __restrict__ ids,
     const float* __restrict__ qn, float maxnorm, float eps_c, uint64_t* __restrict__ out_ids,
     float* __restrict__ out_d, uint32_t* __restrict__ out_count, int* __restrict__ flag_list,
     int* __restrict__ flag_count, size_t ldo) {
-  constexpr int PER = 8;
   const int q = blockIdx.x;
   const int lane = threadIdx.x & (WAVE - 1);
   __shared__ int hist[256];
@@ -683,13 +684,13 @@ __global__ __launch_bounds__(256) void flat_merge_rescore_reg(
   uint64_t x[PER];
 #pragma unroll
   for (int u = 0; u < PER; ++u) {
-    const int i = min((int)threadIdx.x + u * (int)blockDim.x, n - 1);  // unconditional loads
+    const int i = min((int)threadIdx.x + u * NT, n - 1);  // unconditional loads
     x[u] = base[(size_t)(i / Kp) * CAP + i % Kp];
   }
   int wcount = 0;
 #pragma unroll
   for (int u = 0; u < PER; ++u) {
-    if ((int)threadIdx.x + u * (int)blockDim.x >= n) x[u] = KEY_MAX;
+    if ((int)threadIdx.x + u * NT >= n) x[u] = KEY_MAX;
     wcount += __popcll(__ballot(x[u] != KEY_MAX));
   }
   __syncthreads();  // the counters are set
@@ -715,7 +716,7 @@ __global__ __launch_bounds__(256) void flat_merge_rescore_reg(
   // rescore: 8 threads per candidate
   const int g = threadIdx.x & 7, grp = threadIdx.x >> 3;
   const float* qv = Qp + (size_t)q * ld;
-  for (int c = grp; c < ksel; c += (int)blockDim.x / 8) {
+  for (int c = grp; c < ksel; c += NT / 8) {
     const uint32_t slot = (uint32_t)sel[c];
     const float d = dist_group8_rt(metric, qv, X + (size_t)slot * ld, dim, g);
     if (g == 0) {
@@ -960,10 +961,15 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
     }
     candidates(std::false_type{});
     tm.mark(2);
-    if ((size_t)S * Kp <= 8 * 256 && Kp <= WAVE)
-      hipLaunchKernelGGL(flat_merge_rescore_reg, dim3((unsigned)nq), dim3(256), 0, s, cand, S, CAP, Kp, (int)kq, Qp,
-                         (int)ld, (int)dim, metric, X.p, ranks.rank.p, d_ids.p, qn, maxnorm, 4.0f, d_oid, d_od, d_oc,
-                         flag_list, flag_count, ldo);
+    const size_t nkeys = (size_t)S * Kp;
+    if (nkeys <= 8 * 256 && Kp <= WAVE)
+      hipLaunchKernelGGL((flat_merge_rescore_reg<256, 8>), dim3((unsigned)nq), dim3(256), 0, s, cand, S, CAP, Kp,
+                         (int)kq, Qp, (int)ld, (int)dim, metric, X.p, ranks.rank.p, d_ids.p, qn, maxnorm, 4.0f, d_oid,
+                         d_od, d_oc, flag_list, flag_count, ldo);
+    else if (nkeys <= 16 * 1024 && Kp <= WAVE)
+      hipLaunchKernelGGL((flat_merge_rescore_reg<1024, 16>), dim3((unsigned)nq), dim3(1024), 0, s, cand, S, CAP, Kp,
+                         (int)kq, Qp, (int)ld, (int)dim, metric, X.p, ranks.rank.p, d_ids.p, qn, maxnorm, 4.0f, d_oid,
+                         d_od, d_oc, flag_list, flag_count, ldo);
     else
       hipLaunchKernelGGL(flat_merge_rescore, dim3((unsigned)nq), dim3(256), 0, s, cand, S, CAP, Kp, (int)kq, Qp,
                          (int)ld, (int)dim, metric, X.p, ranks.rank.p, ranks.rank_slot.p, d_ids.p, qn, maxnorm, 4.0f,

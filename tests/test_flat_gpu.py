@@ -342,16 +342,19 @@ def test_growth_preserves_contents(gpu):
 
 
 @pytest.mark.parametrize("metric", [0, 1])
-def test_merge_register_boundary(gpu, metric):
-    """1000 queries over 16,384 rows make 32 splits. k = 48 (k' = 64) puts
-    exactly 2048 keys per query into the merge that holds them in registers
-    and sorts one wavefront; k = 49 (k' = 65) takes the general merge; k = 1
-    is the smallest selection. Every vector is stored twice under unrelated
-    ids, so equal distances are ordered by id, and a filter that accepts 33
-    rows leaves every query fewer than k' candidates."""
+@pytest.mark.parametrize("n,nq", [(16384, 1000), (131072, 40)])
+def test_merge_register_boundary(gpu, metric, n, nq):
+    """The merges that hold a query's keys in registers, at their limits.
+    1000 queries over 16,384 rows make 32 splits: k = 48 (k' = 64) puts
+    exactly 2048 keys per query into the 256-thread merge. 40 queries over
+    131,072 rows make 256 splits: k = 48 puts exactly 16,384 keys into the
+    1024-thread merge. k = 49 (k' = 65) takes the general merge, and k = 1 is
+    the smallest selection. Every vector is stored twice under unrelated ids,
+    so equal distances are ordered by id, and a filter that accepts n / 500
+    rows leaves every query fewer than k' candidates at the first shape."""
     px = gpu
-    rng = np.random.default_rng(901 + metric)
-    n, dim, nq = 16384, 40, 1000
+    rng = np.random.default_rng(901 + metric + n)
+    dim = 40 if n <= 16384 else 16
     half = rng.standard_normal((n // 2, dim)).astype(np.float32)
     data = np.concatenate([half, half])
     ids = rng.permutation(n).astype(np.uint64)
