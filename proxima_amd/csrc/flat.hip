@@ -527,6 +527,7 @@ __global__ __launch_bounds__(512) void flat_seed_threshold(const uint64_t* __res
   const uint32_t* c32 = reinterpret_cast<const uint32_t*>(c);
   auto get = [&](int i) { return (uint64_t)c32[(size_t)(i / FB_N) * (2 * CAP) + 2 * (CAP - FB_N / 2) + i % FB_N]; };
   const int n = S * FB_N;
+  if (n < Kp) return;  // fewer words than Kp bound nothing (the host does not seed then)
   const uint64_t hi = n <= 16 * (int)blockDim.x ? block_radix_select<decltype(get), 32, 16>(get, n, Kp, hist, sh)
                                     : block_radix_select<decltype(get), 32>(get, n, Kp, hist, sh);
   if (threadIdx.x == 0 && hi != 0xFFFFFFFFull) atomicMin(gthr + q, (unsigned long long)((hi << 32) | 0xFFFFFFFFull));
@@ -545,6 +546,7 @@ __global__ __launch_bounds__(64) void flat_seed_threshold2(const uint64_t* __res
   const int q = blockIdx.x;
   const uint32_t* c32 = reinterpret_cast<const uint32_t*>(cand + (size_t)q * S * CAP + (CAP - FB_N / 2 - 1));
   auto get = [&](int i) { return (uint64_t)c32[(size_t)(i >> 1) * (2 * CAP) + (i & 1)]; };
+  if (2 * S < Kp) return;  // the host launches this with 2 S >= 4 Kp
   const uint64_t hi = block_radix_select<decltype(get), 32, 16>(get, 2 * S, Kp, hist, sh);
   if (threadIdx.x == 0 && hi != 0xFFFFFFFFull) atomicMin(gthr + q, (unsigned long long)((hi << 32) | 0xFFFFFFFFull));
 }
@@ -931,12 +933,14 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
     tm.mark(1);
     const int grid = ((total + 7) / 8) * 8;
     const float scale = metric == PXG_EUCLIDEAN ? 2.0f : 1.0f;
-    // With several tiles per split, a first pass over the first tile of each
-    // split (spread over the whole store) seeds each query's threshold with
-    // the Kp-th best of those rows, so the full pass appends and compacts
-    // little from its first tile on; the full pass then filters that tile's
-    // stored keys instead of computing it again.
-    const int seeded = tiles_per >= 8 ? 1 : 0;
+    // A first pass over the first tile of each split (spread over the whole
+    // store) seeds each query's threshold with the Kp-th best of those rows,
+    // so the full pass appends and compacts little from its first tile on
+    // (unseeded, every row would append its split's first two tiles whole
+    // and compact them); the full pass then filters that tile's stored keys
+    // instead of computing it again. The seed needs at least Kp words per
+    // query: S tiles of FB_N.
+    const int seeded = (size_t)S * FB_N >= (size_t)Kp ? 1 : 0;
     auto candidates = [&](auto seed) {
       constexpr bool SD = decltype(seed)::value;
       if (CAP == 256)

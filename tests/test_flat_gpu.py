@@ -367,6 +367,27 @@ def test_merge_register_boundary(gpu, metric, n, nq):
     assert_same(idx.search_batch(q, 48, keep), oracle_search(px, data, ids, metric, q, 48, accept=acc))
 
 
+@pytest.mark.parametrize("metric", [0, 1])
+def test_seed_word_count_boundary(gpu, metric):
+    """A store of 300 rows is one split of 3 tiles on the MFMA path. The
+    seeding pass bounds k' = k + 16 only from at least k' words, one tile's
+    128 here: k = 112 (k' = 128) is seeded, k = 113 and k = 200 take the
+    unseeded full pass, and a filter leaves some tiles partly usable."""
+    px = gpu
+    rng = np.random.default_rng(313 + metric)
+    n, dim, nq = 300, 24, 50
+    data = rng.standard_normal((n, dim)).astype(np.float32)
+    ids = rng.permutation(10 * n)[:n].astype(np.uint64)
+    idx = make_index(px, data, metric, ids, 1)
+    q = rng.standard_normal((nq, dim)).astype(np.float32)
+    for k in (5, 112, 113, 200):
+        assert_same(idx.search_batch(q, k), oracle_search(px, data, ids, metric, q, k))
+    keep = lambda i, _m: i % 3 != 0  # noqa: E731
+    acc = (ids % 3 != 0).astype(np.uint8)
+    for k in (112, 113):
+        assert_same(idx.search_batch(q, k, keep), oracle_search(px, data, ids, metric, q, k, accept=acc))
+
+
 @pytest.mark.parametrize("metric", [0, 2])
 def test_thresholds_shared_across_splits(gpu, metric):
     """The MFMA path splits the store over many workgroups per query block,
