@@ -316,7 +316,9 @@ class FlatIndex(_IndexBase):
 
     def __del__(self):
         h = getattr(self, "_h", None)
-        if h:
+        # at interpreter exit the module's globals may already be cleared;
+        # the process is ending and its device memory goes with it
+        if h and _lib is not None:
             _lib.pxg_flat_destroy(h)
             self._h = None
 
@@ -493,7 +495,9 @@ class IvfPqIndex(_IndexBase):
 
     def __del__(self):
         h = getattr(self, "_h", None)
-        if h:
+        # at interpreter exit the module's globals may already be cleared;
+        # the process is ending and its device memory goes with it
+        if h and _lib is not None:
             _lib.pxg_ivfpq_destroy(h)
             self._h = None
 
@@ -910,7 +914,9 @@ class Sq8Index(_IndexBase):
 
     def __del__(self):
         h = getattr(self, "_h", None)
-        if h:
+        # at interpreter exit the module's globals may already be cleared;
+        # the process is ending and its device memory goes with it
+        if h and _lib is not None:
             _lib.pxg_sq8_destroy(h)
             self._h = None
 
