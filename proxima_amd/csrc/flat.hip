@@ -431,9 +431,19 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
         okbits |= ok ? 0xFFFFu << (16 * j) : 0u;
         xbj[j] = ok ? xbr[j] : 0.0f;
       }
-      uint32_t pass[2] = {0u, 0u};  // pass[i], bit j * 16 + v
+      // Appends go through this wave's 8 KB of the slice buffer the k loop
+      // has finished with (all waves are past its last read, and the next
+      // tile's first write to it follows the epilogue's closing barrier):
+      // each row group's eight approximate scores are stored there, and a
+      // lane then visits only its own marked values, lowest bit first, so
+      // the wave loops as often as its busiest lane has marks instead of
+      // once per value with two LDS round trips each.
+      const int fb = (gs - 1) & 1;
+      float* slab = (wid < 2 ? &sQ[fb][0] : &sX[fb][0]) + (wid & 1) * (2 * 4 * WAVE * 4);
+      // value (j, v) of this lane at slab[((j * 4 + (v >> 2)) * WAVE + lane) * 4 + (v & 3)]
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
+        uint32_t pass = 0u;  // bit j * 16 + v
         uint32_t rokbits = 0u;
 #pragma unroll
         for (int v = 0; v < 16; ++v)
@@ -444,35 +454,37 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
           const float4 sq = *reinterpret_cast<const float4*>(&sqb[row0]);
           const float4 tf = *reinterpret_cast<const float4*>(&thr_f[row0]);
           const float sqv[4] = {sq.x, sq.y, sq.z, sq.w}, tfv[4] = {tf.x, tf.y, tf.z, tf.w};
+          float av[2][4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
               const float a = __builtin_fmaf(-scale, acc[i][j][vb * 4 + e], sqv[e] + xbj[j]);
-              pass[i] |= !(a > tfv[e]) ? 1u << (j * 16 + vb * 4 + e) : 0u;
+              av[j][e] = a;
+              pass |= !(a > tfv[e]) ? 1u << (j * 16 + vb * 4 + e) : 0u;
             }
           }
-          __builtin_amdgcn_sched_barrier(0);  // bounds the live rows (no spills)
-        }
-        pass[i] &= okbits & rokbits;
-      }
-      if (__ballot((pass[0] | pass[1]) != 0)) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
 #pragma unroll
           for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-              if (pass[i] & (1u << (j * 16 + v))) {
-                const int row = wm + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-                const float a = __builtin_fmaf(-scale, acc[i][j][v], sqb[row] + xbj[j]);
-                const uint64_t key = ((uint64_t)ord_key(a) << 32) | (uint32_t)slotj[j];
-                if (key < thr[row]) {
-                  const int pos = atomicAdd(&cnt[row], 1);
-                  cand[((size_t)(q0 + row) * S + split) * CAP + pos] = key;
-                }
-              }
+            *reinterpret_cast<float4*>(&slab[((j * 4 + vb) * WAVE + lane) * 4]) =
+                make_float4(av[j][0], av[j][1], av[j][2], av[j][3]);
+          __builtin_amdgcn_sched_barrier(0);  // bounds the live rows (no spills)
+        }
+        pass &= okbits & rokbits;
+        while (__ballot(pass != 0u)) {
+          if (pass != 0u) {
+            const int b = __builtin_ctz(pass);
+            pass &= pass - 1u;
+            const int j = b >> 4, v = b & 15;
+            const int row = wm + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+            const float a = slab[((j * 4 + (v >> 2)) * WAVE + lane) * 4 + (v & 3)];
+            const uint64_t key = ((uint64_t)ord_key(a) << 32) | (uint32_t)(n0 + wn + j * 32 + r);
+            if (key < thr[row]) {
+              const int pos = atomicAdd(&cnt[row], 1);
+              cand[((size_t)(q0 + row) * S + split) * CAP + pos] = key;
             }
+          }
+        }
       }
     }
     __syncthreads();
