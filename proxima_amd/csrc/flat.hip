@@ -367,13 +367,18 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
     // key below thr[row] (key_float inverts ord_key; NaN and the sign of zero
     // pass), so only the marked values take the exact key test and append.
     if constexpr (SEED) {
-      // Seeding pass: every usable value of its one tile is kept, so each
-      // lane writes its distance part straight to its column of the last
-      // FB_N / 2 words of the row's buffer, read as FB_N 32-bit words (no
-      // counters, no atomics; the seed threshold needs only the distance
-      // parts, and the full pass rebuilds each key from its slot);
-      // unusable slots hold 0xFFFFFFFF. The full pass's appends from this
-      // tile (at most FB_N) stay below that region.
+      // Seeding pass: every usable value of its one tile is kept, as its
+      // distance part (unusable slots: 0xFFFFFFFF), in the last FB_N / 2
+      // entries of the row's buffer read as FB_N 32-bit words (no counters,
+      // no atomics; the seed threshold needs only the distance parts, and
+      // the full pass rebuilds each key from its slot). The full pass's
+      // appends from this tile (at most FB_N) stay below that region.
+      // The tile's words go through LDS first: both slice buffers are free
+      // after a one-tile k loop, and hold the 128 x 128 words exactly (rows
+      // 0..63 in sQ, 64..127 in sX, the wave's rows wm..wm+63 in one of
+      // them). Row R's word c sits at c ^ (32 * bit 2 of R), so that the
+      // two lane halves of a store (rows 4 apart) use different banks.
+      uint32_t* wbase = reinterpret_cast<uint32_t*>(wm == 0 ? &sQ[0][0] : &sX[0][0]);
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const bool ok = (slotj[j] < s_end) & ((lvj[j] & acj[j]) != 0u);
@@ -382,39 +387,47 @@ __global__ __launch_bounds__(256, 2) void flat_mfma_candidates(
         for (int i = 0; i < 2; ++i)
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
-            const int row = wm + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-            if (q0 + row < nq) {
-              const float a = __builtin_fmaf(-scale, acc[i][j][v], sqb[row] + xo);
-              reinterpret_cast<uint32_t*>(cand + ((size_t)(q0 + row) * S + split) * CAP +
-                                          (CAP - FB_N / 2))[wn + j * 32 + r] = ok ? ord_key(a) : 0xFFFFFFFFu;
-            }
+            const int lrow = i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);  // row - wm
+            const float a = __builtin_fmaf(-scale, acc[i][j][v], sqb[wm + lrow] + xo);
+            wbase[lrow * FB_N + ((wn + j * 32 + r) ^ (32 * h))] = ok ? ord_key(a) : 0xFFFFFFFFu;
           }
       }
-      // Each row's two smallest words of the tile, as two 32-bit words in the
-      // entry just below them (smallest first): two threads per row read
-      // the words back (the barrier makes the other waves' stores visible),
-      // keep a sorted pair, and merge with the neighbour lane's pair.
       __syncthreads();
-      {
-        const int row = tid >> 1, c0 = (tid & 1) * (FB_N / 2);
-        uint64_t* buf = cand + ((size_t)(q0 + row) * S + split) * CAP;
-        uint32_t m1 = 0xFFFFFFFFu, m2 = 0xFFFFFFFFu;
+      const uint32_t* words = reinterpret_cast<const uint32_t*>(&sQ[0][0]);
+      const uint32_t* words_hi = reinterpret_cast<const uint32_t*>(&sX[0][0]);
+      // copy out: 32 threads per row, 16 bytes each (the row's 512 bytes)
+#pragma unroll 4
+      for (int u = 0; u < FB_M / 8; ++u) {
+        const int row = (tid >> 5) + 8 * u, c = tid & 31;
         if (q0 + row < nq) {
-          const uint4* kw = reinterpret_cast<const uint4*>(reinterpret_cast<const uint32_t*>(buf + (CAP - FB_N / 2)) + c0);
+          const uint32_t* rw = (row < 64 ? words + row * FB_N : words_hi + (row - 64) * FB_N);
+          const uint4 w4 = *reinterpret_cast<const uint4*>(rw + ((4 * c) ^ (32 * ((row >> 2) & 1))));
+          reinterpret_cast<uint4*>(cand + ((size_t)(q0 + row) * S + split) * CAP + (CAP - FB_N / 2))[c] = w4;
+        }
+      }
+      // Each row's two smallest words, as two 32-bit words in the entry just
+      // below them (smallest first): two threads per row, each over one half
+      // of the row's positions (any order: it starts at chunk row & 15, so
+      // that the rows of one read use different banks), keep a sorted pair
+      // and merge with the neighbour lane's pair.
+      {
+        const int row = tid >> 1, half = tid & 1;
+        const uint32_t* rw = (row < 64 ? words + row * FB_N : words_hi + (row - 64) * FB_N) + half * (FB_N / 2);
+        uint32_t m1 = 0xFFFFFFFFu, m2 = 0xFFFFFFFFu;
 #pragma unroll
-          for (int u = 0; u < FB_N / 8; ++u) {
-            const uint4 w = kw[u];
-            const uint32_t x4[4] = {w.x, w.y, w.z, w.w};
+        for (int u = 0; u < FB_N / 8; ++u) {
+          const uint4 w = reinterpret_cast<const uint4*>(rw)[(u + row) & (FB_N / 8 - 1)];
+          const uint32_t x4[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              m2 = min(m2, max(m1, x4[e]));
-              m1 = min(m1, x4[e]);
-            }
+          for (int e = 0; e < 4; ++e) {
+            m2 = min(m2, max(m1, x4[e]));
+            m1 = min(m1, x4[e]);
           }
         }
         const uint32_t p1 = __shfl_xor(m1, 1), p2 = __shfl_xor(m2, 1);
         const uint32_t n1 = min(m1, p1), n2 = min(max(m1, p1), min(m2, p2));
-        if ((tid & 1) == 0 && q0 + row < nq) buf[CAP - FB_N / 2 - 1] = ((uint64_t)n2 << 32) | n1;
+        if (half == 0 && q0 + row < nq)
+          cand[((size_t)(q0 + row) * S + split) * CAP + (CAP - FB_N / 2 - 1)] = ((uint64_t)n2 << 32) | n1;
       }
     } else if (stored) {
       flat_stored_tile<CAP>(cand, S, split, q0, nq, n0, s_end, live, acc_src, thr, cnt, tid);
