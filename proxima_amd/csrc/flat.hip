@@ -148,37 +148,48 @@ __device__ __attribute__((noinline)) void compact_row(uint64_t* __restrict__ bas
 // The first tile of a seeded split in the full pass: the keys the seeding
 // pass left in the last FB_N / 2 entries of each row's buffer (FB_N 32-bit
 // distance parts, slot n0 + c at word c), rebuilt as (distance part, slot)
-// and tested against the row's threshold like computed ones. Thread t takes
-// row t / 2, words (t & 1) * FB_N / 2 onwards. The appends (at most FB_N
-// per row, the row's first) stay below the stored words. Out of line, so
-// that the main loop's registers are not shaped by it.
+// and tested against the row's threshold like computed ones. 32 threads per
+// row, 16 bytes each (thread t takes chunk t & 31 of rows t / 32 + 8 u, the
+// same four slots in every row), all loads in flight together, the slots'
+// liveness and acceptance read once beside them; a word above the
+// threshold's distance part is skipped before the exact key test. The
+// appends (at most FB_N per row, the row's first) stay below the stored
+// words. Out of line, so that the main loop's registers are not shaped by it.
 template <int CAP>
 __device__ __attribute__((noinline)) void flat_stored_tile(uint64_t* __restrict__ cand, int S, int split, int q0,
                                                            int nq, int n0, int s_end, const uint8_t* __restrict__ live,
                                                            const uint8_t* __restrict__ acc_src, const uint64_t* thr,
                                                            int* cnt, int tid) {
-  const int row = tid >> 1, c0 = (tid & 1) * (FB_N / 2);
-  if (row >= FB_M || q0 + row >= nq) return;
-  uint64_t* buf = cand + ((size_t)(q0 + row) * S + split) * CAP;
-  const uint32_t* kw = reinterpret_cast<const uint32_t*>(buf + (CAP - FB_N / 2)) + c0;
-  const uint64_t t = thr[row];
-  // four words per load, four loads in flight (few registers: this runs
-  // inside the main loop's register budget)
-#pragma nounroll
-  for (int u0 = 0; u0 < FB_N / 8; u0 += 4) {
-    uint4 w[4];
+  constexpr int U = FB_M / 8;
+  const int c = tid & 31;
+  uint4 w[U];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) w[u] = reinterpret_cast<const uint4*>(kw)[u0 + u];
+  for (int u = 0; u < U; ++u) {
+    const int qr = min(q0 + (tid >> 5) + 8 * u, nq - 1);  // unconditional loads
+    w[u] = reinterpret_cast<const uint4*>(cand + ((size_t)qr * S + split) * CAP + (CAP - FB_N / 2))[c];
+  }
+  bool usable[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const uint32_t kk[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+  for (int e = 0; e < 4; ++e) {
+    const int slot = n0 + 4 * c + e;
+    const int sl = min(slot, s_end - 1);  // unconditional loads
+    usable[e] = slot < s_end && (live[sl] & acc_src[sl]) != 0;
+  }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int slot = n0 + c0 + 4 * (u0 + u) + e;
+  for (int u = 0; u < U; ++u) {
+    const int row = (tid >> 5) + 8 * u;
+    if (q0 + row >= nq) continue;
+    const uint64_t t = thr[row];
+    const uint32_t th = (uint32_t)(t >> 32);
+    const uint32_t kk[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (kk[e] <= th) {
+        const int slot = n0 + 4 * c + e;
         const uint64_t key = ((uint64_t)kk[e] << 32) | (uint32_t)slot;
-        if (key < t && slot < s_end && (live[slot] & acc_src[slot]) != 0) {
+        if (key < t && usable[e]) {
           const int pos = atomicAdd(&cnt[row], 1);
-          buf[pos] = key;
+          cand[((size_t)(q0 + row) * S + split) * CAP + pos] = key;
         }
       }
     }
