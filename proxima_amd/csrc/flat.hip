@@ -785,6 +785,22 @@ __global__ __launch_bounds__(NT) void flat_merge_rescore_reg(
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
+// Whether the exact scan is expected to finish nq queries over N rows of dim
+// floats sooner than the MFMA candidate path. Both estimates are fitted to
+// timings of the two paths at 20k x 128, 100k x 128, 300k x 256, 1M x 96 and
+// 1M x 768 with 1 to 128 queries (the crossover, 4 to 50 queries over those
+// stores, lands within one measured batch size): the MFMA path costs about
+// 0.1 ms of fixed work plus its GEMM, whole 128-query blocks at about 80% of
+// the FP32 MFMA peak; the exact scan reads the store from HBM once (about
+// 5 TB/s) and streams it through L2 again for every further query (about
+// 0.4 ns per 1000 floats).
+static bool exact_scan_cheaper(size_t N, size_t dim, size_t nq) {
+  const double nd = (double)N * (double)dim;
+  const double t_mfma = 1.0e-4 + (double)((nq + 127) / 128) * nd * 256.0 / 1.25e14;
+  const double t_exact = 5.0e-5 + nd * 4.0 / 5.0e12 + (double)(nq - 1) * nd * 4.0e-13;
+  return t_exact < t_mfma;
+}
+
 FlatIndex::~FlatIndex() {
   if (stream) (void)hipStreamDestroy(stream);
 }
@@ -941,9 +957,10 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
 
   int* flag_list = (int*)sc.get(5, nq * 4);
   // Manhattan has no inner-product form and k beyond FAST_KMAX exceeds the
-  // candidate buffers: both take the exact scan, as do small problems.
+  // candidate buffers: both take the exact scan, as do stores under 4096
+  // rows and batches the exact scan finishes sooner.
   const bool exact_all = mode == 2 || metric == PXG_MANHATTAN || kq > FAST_KMAX ||
-                         (mode == 0 && (N < 4096 || (double)N * (double)nq < 4.0e6));
+                         (mode == 0 && (N < 4096 || exact_scan_cheaper(N, dim, nq)));
   if (!exact_all) {
     const int Kp = (int)std::min<uint64_t>(kq + MARGIN, (uint64_t)FAST_KMAX + MARGIN);
     // a row's buffer holds its Kp keys, one tile's appends (FB_N) and at
