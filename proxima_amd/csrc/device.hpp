@@ -179,6 +179,55 @@ __device__ inline float dist_pair4(const float* __restrict__ a, const float* __r
   return r;
 }
 
+// dist_pair4 for QG queries a[0..QG) against one row b: the row's float4 of
+// each chunk is loaded once and used by every query, and each query keeps its
+// own four accumulators and operand order, so out[j] has the bits of
+// dist_pair4(a[j], b, dim, h).
+template <int METRIC, int QG>
+__device__ inline void dist_pair4_multi(const float* const (&a)[QG], const float* __restrict__ b, int dim, int h,
+                                        float (&out)[QG], int nv = QG) {
+  float s[QG][4];
+#pragma unroll
+  for (int j = 0; j < QG; ++j) s[j][0] = s[j][1] = s[j][2] = s[j][3] = 0.0f;
+  const int chunks = dim >> 3;
+  const float* bp = b + 4 * h;
+#pragma unroll 4
+  for (int c = 0; c < chunks; ++c) {
+    const float4 y = *reinterpret_cast<const float4*>(bp + 8 * c);
+#pragma unroll
+    for (int j = 0; j < QG; ++j) {
+      if (j >= nv) break;  // uniform: queries past the group's end
+      const float4 x = *reinterpret_cast<const float4*>(a[j] + 4 * h + 8 * c);
+      s[j][0] += lane_term<METRIC>(x.x, y.x);
+      s[j][1] += lane_term<METRIC>(x.y, y.y);
+      s[j][2] += lane_term<METRIC>(x.z, y.z);
+      s[j][3] += lane_term<METRIC>(x.w, y.w);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < QG; ++j) {
+    const float half = (s[j][0] + s[j][1]) + (s[j][2] + s[j][3]);
+    const float acc = half + __shfl_xor(half, 1, WAVE);
+    float tail = 0.0f;
+    for (int i = chunks * 8; i < dim; ++i) tail += lane_term<METRIC>(a[j][i], b[i]);
+    const float r = acc + tail;
+    if constexpr (METRIC == 1) out[j] = arm_nan(1.0f - arm_nan(r));
+    else if constexpr (METRIC == 2) out[j] = -arm_nan(r);
+    else out[j] = r;
+  }
+}
+
+template <int QG>
+__device__ inline void dist_pair4_multi_rt(int metric, const float* const (&a)[QG], const float* b, int dim, int h,
+                                           float (&out)[QG], int nv = QG) {
+  switch (metric) {
+    case 0: dist_pair4_multi<0, QG>(a, b, dim, h, out, nv); break;
+    case 1: dist_pair4_multi<1, QG>(a, b, dim, h, out, nv); break;
+    case 2: dist_pair4_multi<2, QG>(a, b, dim, h, out, nv); break;
+    default: dist_pair4_multi<3, QG>(a, b, dim, h, out, nv); break;
+  }
+}
+
 __device__ inline float dist_pair4_rt(int metric, const float* a, const float* b, int dim, int h) {
   switch (metric) {
     case 0: return dist_pair4<0>(a, b, dim, h);

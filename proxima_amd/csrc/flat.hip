@@ -1046,7 +1046,8 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
     read_flags(&nflag);
   if (nflag > 0) {
     sc.release_from(6);  // the candidate buffers are dead
-    const int CH = exact_chunk_rows((size_t)nflag, N);
+    const int QG = exact_query_group((size_t)nflag, dim, N);
+    const int CH = exact_chunk_rows(((size_t)nflag + QG - 1) / QG, N);
     const int nchunks = (int)((N + CH - 1) / CH);
     const int kk = (int)std::min<uint64_t>(kq, (uint64_t)CH);
     const size_t per_query = (size_t)nchunks * kk * 8;
@@ -1065,14 +1066,18 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
         hipLaunchKernelGGL(set_int, dim3(1), dim3(64), 0, s, grp_count, gn);
         count = grp_count;
       }
-#define PXG_EXACT_SCAN(CHV)                                                                                   \
-  hipLaunchKernelGGL(flat_exact_candidates<CHV>, dim3((std::min(gn * nchunks, 4096) + 7) / 8 * 8), dim3(256), 0, s,          \
-                     flag_list + g0, count, nchunks, Qp, (int)ld, (int)dim, metric, X.p, (int)N, d_live.p,     \
-                     d_accept, ranks.rank.p, (int)kq, ecand)
+#define PXG_EXACT_SCAN(CHV, QGV)                                                                              \
+  hipLaunchKernelGGL((flat_exact_candidates<CHV, QGV>), dim3((std::min((gn + QGV - 1) / QGV * nchunks, 4096) + 7) / 8 * 8), \
+                     dim3(256), 0, s, flag_list + g0, count, nchunks, Qp, (int)ld, (int)dim, metric, X.p, (int)N,       \
+                     d_live.p, d_accept, ranks.rank.p, (int)kq, ecand)
 #define PXG_EXACT_MERGE(CHV)                                                                                  \
   hipLaunchKernelGGL(flat_merge_exact<CHV>, dim3((unsigned)gn), dim3(256), 0, s, flag_list + g0, count, ecand, \
                      nchunks, (int)kq, ranks.rank_slot.p, d_ids.p, d_oid, d_od, d_oc, (uint64_t*)nullptr, ldo)
-      if (CH == 256) PXG_EXACT_SCAN(256); else PXG_EXACT_SCAN(EXACT_CH);
+      if (CH == 256) {
+        if (QG == 4) PXG_EXACT_SCAN(256, 4); else PXG_EXACT_SCAN(256, 1);
+      } else {
+        if (QG == 4) PXG_EXACT_SCAN(EXACT_CH, 4); else PXG_EXACT_SCAN(EXACT_CH, 1);
+      }
       PXG_HIP(hipGetLastError());
       if (exact_all && g0 == 0) tm.mark(2);
       if (CH == 256) PXG_EXACT_MERGE(256); else PXG_EXACT_MERGE(EXACT_CH);

@@ -2410,19 +2410,25 @@ struct IvfPqIndex {
       int* qlist = (int*)sc.get(5, nq * 4);
       hipLaunchKernelGGL(iota_kernel, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s, qlist, (int)nq,
                          flag_count);
-      const int CH = exact_chunk_rows((size_t)nq, N);
+      const int QG = exact_query_group((size_t)nq, dim, N);
+      const int CH = exact_chunk_rows(((size_t)nq + QG - 1) / QG, N);
       const int nchunks = (int)((N + CH - 1) / CH);
       const int kk = (int)std::min<uint64_t>(kq, (uint64_t)CH);
       uint64_t* ecand = (uint64_t*)sc.get(7, (size_t)nq * nchunks * kk * 8);
       tm.mark(1);
-#define PXG_EXACT_SCAN(CHV)                                                                                       \
-  hipLaunchKernelGGL(flat_exact_candidates<CHV>, dim3((std::min<int>((int)nq * nchunks, 4096) + 7) / 8 * 8), dim3(256), 0, s,    \
+#define PXG_EXACT_SCAN(CHV, QGV)                                                                                  \
+  hipLaunchKernelGGL((flat_exact_candidates<CHV, QGV>),                                                           \
+                     dim3((std::min<int>(((int)nq + QGV - 1) / QGV * nchunks, 4096) + 7) / 8 * 8), dim3(256), 0, s, \
                      qlist, flag_count, nchunks, Qp, (int)ld, (int)dim, metric, X.p, (int)N, d_live.p, d_accept,  \
                      ranks.rank.p, (int)kq, ecand)
 #define PXG_EXACT_MERGE(CHV)                                                                                      \
   hipLaunchKernelGGL(flat_merge_exact<CHV>, dim3((unsigned)nq), dim3(256), 0, s, qlist, flag_count, ecand, nchunks, \
                      (int)kq, ranks.rank_slot.p, d_ids.p, d_oid, d_od, d_oc, (uint64_t*)nullptr, ldo)
-      if (CH == 256) PXG_EXACT_SCAN(256); else PXG_EXACT_SCAN(EXACT_CH);
+      if (CH == 256) {
+        if (QG == 4) PXG_EXACT_SCAN(256, 4); else PXG_EXACT_SCAN(256, 1);
+      } else {
+        if (QG == 4) PXG_EXACT_SCAN(EXACT_CH, 4); else PXG_EXACT_SCAN(EXACT_CH, 1);
+      }
       PXG_HIP(hipGetLastError());
       tm.mark(2);
       if (CH == 256) PXG_EXACT_MERGE(256); else PXG_EXACT_MERGE(EXACT_CH);

@@ -388,6 +388,27 @@ def test_seed_word_count_boundary(gpu, metric):
         assert_same(idx.search_batch(q, k, keep), oracle_search(px, data, ids, metric, q, k, accept=acc))
 
 
+@pytest.mark.parametrize("metric", [0, 1, 2, 3])
+def test_exact_scan_query_groups(gpu, metric):
+    """The exact scan takes four queries per work item (rows loaded once for
+    the group, queries staged in LDS) for rows of 256 floats or more and four
+    queries or more: 300-float rows (a 4-float tail after 37 chunks), 7 and
+    13 queries (groups of 4 + 3 and 4 + 4 + 4 + 1), a filter, and 3 queries
+    (one per item). Ids and distances match the oracle bit for bit."""
+    px = gpu
+    rng = np.random.default_rng(4242 + metric)
+    n, dim = 3000, 300
+    data = rng.standard_normal((n, dim)).astype(np.float32)
+    ids = rng.permutation(3 * n)[:n].astype(np.uint64)
+    idx = make_index(px, data, metric, ids, 2)
+    q = rng.standard_normal((13, dim)).astype(np.float32)
+    for nq in (3, 7, 13):
+        assert_same(idx.search_batch(q[:nq], 10), oracle_search(px, data, ids, metric, q[:nq], 10))
+    keep = lambda i, _m: i % 5 != 2  # noqa: E731
+    acc = (ids % 5 != 2).astype(np.uint8)
+    assert_same(idx.search_batch(q[:7], 25, keep), oracle_search(px, data, ids, metric, q[:7], 25, accept=acc))
+
+
 @pytest.mark.parametrize("metric", [0, 2])
 def test_thresholds_shared_across_splits(gpu, metric):
     """The MFMA path splits the store over many workgroups per query block,
