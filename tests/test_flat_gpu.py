@@ -391,22 +391,25 @@ def test_seed_word_count_boundary(gpu, metric):
 @pytest.mark.parametrize("metric", [0, 1, 2, 3])
 def test_exact_scan_query_groups(gpu, metric):
     """The exact scan takes four queries per work item (rows loaded once for
-    the group, queries staged in LDS) for rows of 256 floats or more and four
-    queries or more: 300-float rows (a 4-float tail after 37 chunks), 7 and
-    13 queries (groups of 4 + 3 and 4 + 4 + 4 + 1), a filter, and 3 queries
-    (one per item). Ids and distances match the oracle bit for bit."""
+    the group, queries staged in LDS) for rows of 256 to 1024 floats, four
+    queries or more and at least 512 grouped items of 1024 rows: 300-float
+    rows (a 4-float tail after 37 chunks) over 131,149 rows (129 chunks, the
+    last partial), 13 and 18 queries (groups of 4 + 4 + 4 + 1 and
+    4 + 4 + 4 + 4 + 2), a filter, and 5 queries (one per item: too few
+    groups). Ids and distances match the oracle bit for bit."""
     px = gpu
     rng = np.random.default_rng(4242 + metric)
-    n, dim = 3000, 300
+    n, dim = 131_149, 300
     data = rng.standard_normal((n, dim)).astype(np.float32)
     ids = rng.permutation(3 * n)[:n].astype(np.uint64)
     idx = make_index(px, data, metric, ids, 2)
-    q = rng.standard_normal((13, dim)).astype(np.float32)
-    for nq in (3, 7, 13):
-        assert_same(idx.search_batch(q[:nq], 10), oracle_search(px, data, ids, metric, q[:nq], 10))
+    q = rng.standard_normal((18, dim)).astype(np.float32)
+    for nq in (5, 13, 18):
+        assert_same(idx.search_batch(q[:nq], 10), oracle_search(px, data, ids, metric, q[:nq], 10, threads=16))
     keep = lambda i, _m: i % 5 != 2  # noqa: E731
     acc = (ids % 5 != 2).astype(np.uint8)
-    assert_same(idx.search_batch(q[:7], 25, keep), oracle_search(px, data, ids, metric, q[:7], 25, accept=acc))
+    assert_same(idx.search_batch(q[:13], 25, keep),
+                oracle_search(px, data, ids, metric, q[:13], 25, accept=acc, threads=16))
 
 
 @pytest.mark.parametrize("metric", [0, 2])
