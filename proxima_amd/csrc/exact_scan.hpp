@@ -37,10 +37,10 @@ inline int exact_chunk_rows(size_t nq, size_t N) {
 // ---------------------------------------------------------------------------
 // 1. query preparation
 // ---------------------------------------------------------------------------
-[[maybe_unused]] static __global__ __launch_bounds__(64) void flat_prep_queries(const float* __restrict__ raw, int dim, int ld, int metric,
-                                                        int do_prepare, float* __restrict__ Qp,
-                                                        float* __restrict__ qb, float* __restrict__ qn,
-                                                        unsigned long long* __restrict__ bad) {
+// One 64-thread workgroup per row: validate, (cosine) normalise, pad to ld.
+__device__ inline void prep_query_row(const float* __restrict__ raw, int dim, int ld, int metric, int do_prepare,
+                                      float* __restrict__ Qp, float* __restrict__ qb, float* __restrict__ qn,
+                                      unsigned long long* __restrict__ bad) {
   const int q = blockIdx.x;
   const int lane = threadIdx.x;
   const float* v = raw + (size_t)q * dim;
@@ -79,6 +79,26 @@ inline int exact_chunk_rows(size_t nq, size_t N) {
       qb[q] = metric == 0 ? d : (metric == 1 ? 1.0f : 0.0f);
     }
   }
+}
+
+[[maybe_unused]] static __global__ __launch_bounds__(64) void flat_prep_queries(const float* __restrict__ raw, int dim,
+                                                                                int ld, int metric, int do_prepare,
+                                                                                float* __restrict__ Qp,
+                                                                                float* __restrict__ qb,
+                                                                                float* __restrict__ qn,
+                                                                                unsigned long long* __restrict__ bad) {
+  prep_query_row(raw, dim, ld, metric, do_prepare, Qp, qb, qn, bad);
+}
+
+// flat_prep_queries for a flat search, which also sets each query's shared
+// candidate threshold to its initial "none" (~0), saving the search a fill
+// launch ahead of its candidate passes.
+[[maybe_unused]] static __global__ __launch_bounds__(64) void flat_prep_search_queries(
+    const float* __restrict__ raw, int dim, int ld, int metric, int do_prepare, float* __restrict__ Qp,
+    float* __restrict__ qb, float* __restrict__ qn, unsigned long long* __restrict__ bad,
+    unsigned long long* __restrict__ gthr) {
+  if (threadIdx.x == 0) gthr[blockIdx.x] = ~0ull;
+  prep_query_row(raw, dim, ld, metric, do_prepare, Qp, qb, qn, bad);
 }
 
 // ---------------------------------------------------------------------------

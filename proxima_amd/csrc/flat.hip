@@ -931,9 +931,12 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
   unsigned long long* bad = (unsigned long long*)sc.get(4, 8 + 8);
   int* flag_count = (int*)(bad + 1);
   int* grp_count = flag_count + 1;
+  // per query, the least threshold any split has published (MFMA path),
+  // cleared by the preparation kernel
+  unsigned long long* gthr = (unsigned long long*)sc.get(25, nq * 8);
   hipLaunchKernelGGL(init_search_flags, dim3(1), dim3(64), 0, s, bad, flag_count);
-  hipLaunchKernelGGL(flat_prep_queries, dim3((unsigned)nq), dim3(64), 0, s, d_raw, (int)dim, (int)ld, metric,
-                     do_prepare ? 1 : 0, Qp, qb, qn, bad);
+  hipLaunchKernelGGL(flat_prep_search_queries, dim3((unsigned)nq), dim3(64), 0, s, d_raw, (int)dim, (int)ld, metric,
+                     do_prepare ? 1 : 0, Qp, qb, qn, bad, gthr);
   PXG_HIP(hipGetLastError());
   unsigned long long* tail = sc.host_words();
   auto read_flags = [&](int* nflag) {
@@ -968,8 +971,6 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
     const int CAP = (Kp + FB_N + 64) <= 256 ? 256 : 512;
     const int QB = (int)((nq + FB_M - 1) / FB_M);
     const int tiles = (int)((N + FB_N - 1) / FB_N);
-    // per query, the least threshold any split has published
-    unsigned long long* gthr = (unsigned long long*)sc.get(25, nq * 8);
     int S = std::max(1, std::min(512 / QB, std::max(1, tiles / 4)));
     // a fixed scratch may hold fewer splits (the results do not depend on S)
     const size_t per_split_bytes = (size_t)nq * CAP * 8;
@@ -980,8 +981,6 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
     const int per_split = tiles_per * FB_N;
     S = (int)((N + per_split - 1) / per_split);
     uint64_t* cand = (uint64_t*)sc.get(6, (size_t)nq * S * CAP * 8);
-    hipLaunchKernelGGL(fill_u32, dim3((unsigned)((nq * 2 + 255) / 256)), dim3(256), 0, s, (uint32_t*)gthr,
-                       (size_t)nq * 2, ~0u);
     const int total = QB * S;
     tm.mark(1);
     const int grid = ((total + 7) / 8) * 8;
