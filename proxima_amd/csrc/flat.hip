@@ -11,10 +11,11 @@
 //                         below the running threshold are appended to a
 //                         per-(query, split) buffer that a wave-level bitonic
 //                         sort compacts back to k' whenever it fills. The
-//                         N x nq score matrix never reaches HBM. With many
-//                         tiles per split, a seeding pass scores the first
-//                         tile of every split first: flat_seed_threshold2
-//                         (from each split's two smallest keys per row) or
+//                         N x nq score matrix never reaches HBM. A seeding
+//                         pass scores the first tile of every split first:
+//                         flat_seed_threshold2 (from each split's two
+//                         smallest keys per row; _wave sorts them in one
+//                         wavefront for up to 64 splits) or
 //                         flat_seed_threshold (from all of them) turns those
 //                         keys into each query's starting threshold, and the
 //                         full pass filters them instead of recomputing
@@ -587,6 +588,28 @@ __global__ __launch_bounds__(64) void flat_seed_threshold2(const uint64_t* __res
   if (threadIdx.x == 0 && hi != 0xFFFFFFFFull) atomicMin(gthr + q, (unsigned long long)((hi << 32) | 0xFFFFFFFFull));
 }
 
+// flat_seed_threshold2 for S <= 64 splits: lane L loads split L's pair of
+// smallest words (0xFFFFFFFF past S) and one wavefront sorts the 128 words
+// in registers; the Kp-th smallest (1-based) is sorted element Kp - 1. Same
+// value as the radix select over the 2 S words (the padding words are the
+// largest possible, and Kp <= 2 S).
+__global__ __launch_bounds__(64) void flat_seed_threshold2_wave(const uint64_t* __restrict__ cand, int S, int CAP,
+                                                                int Kp, unsigned long long* __restrict__ gthr) {
+  const int q = blockIdx.x, lane = threadIdx.x;
+  if (2 * S < Kp) return;  // the host launches this with 2 S >= 4 Kp
+  uint64_t w[2] = {0xFFFFFFFFull, 0xFFFFFFFFull};
+  if (lane < S) {
+    const uint64_t pr = cand[((size_t)q * S + lane) * CAP + (CAP - FB_N / 2 - 1)];
+    w[0] = pr & 0xFFFFFFFFull;
+    w[1] = pr >> 32;
+  }
+  wave_bitonic_sort<2>(w, lane);
+  const int src = (Kp - 1) >> 1;
+  const uint64_t mine = ((Kp - 1) & 1) ? w[1] : w[0];
+  const uint64_t hi = (uint64_t)(uint32_t)__shfl((int)(uint32_t)mine, src, WAVE);
+  if (lane == 0 && hi != 0xFFFFFFFFull) atomicMin(gthr + q, (unsigned long long)((hi << 32) | 0xFFFFFFFFull));
+}
+
 constexpr int MERGE_MAXP = 512;
 
 // The certificate of one query's merge. Every candidate outside the
@@ -1007,7 +1030,10 @@ void FlatIndex::search_device(const float* d_raw, bool do_prepare, uint64_t nq, 
       candidates(std::true_type{});
       // the splits' pairs when they are many against Kp (and fit the
       // select's 16 words per thread), else every seeding word
-      if (2 * S >= 4 * Kp && 2 * S <= 16 * 64)
+      if (2 * S >= 4 * Kp && S <= WAVE)
+        hipLaunchKernelGGL(flat_seed_threshold2_wave, dim3((unsigned)nq), dim3(64), 0, s, (const uint64_t*)cand, S,
+                           CAP, Kp, gthr);
+      else if (2 * S >= 4 * Kp && 2 * S <= 16 * 64)
         hipLaunchKernelGGL(flat_seed_threshold2, dim3((unsigned)nq), dim3(64), 0, s, (const uint64_t*)cand, S, CAP,
                            Kp, gthr);
       else
