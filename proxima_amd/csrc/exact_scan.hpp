@@ -26,6 +26,16 @@ inline int exact_chunk_rows(size_t nq, size_t N) {
     *flag_count = 0;
   }
 }
+// init_search_flags that also clears the n 64-bit words at `words` (a
+// search's counters beside its flags), saving a fill launch.
+[[maybe_unused]] static __global__ void init_search_flags_zero(unsigned long long* bad, int* flag_count,
+                                                               unsigned long long* words, int n) {
+  if (threadIdx.x == 0) {
+    *bad = ~0ull;
+    *flag_count = 0;
+  }
+  for (int i = threadIdx.x; i < n; i += blockDim.x) words[i] = 0;
+}
 [[maybe_unused]] static __global__ void fill_u32(uint32_t* p, size_t n, uint32_t v) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;

@@ -2394,7 +2394,10 @@ struct IvfPqIndex {
     int* flag_count = (int*)(bad + 1);
     unsigned long long* scanned_dev = nullptr;
     uint64_t scanned_host = 0;
-    hipLaunchKernelGGL(init_search_flags, dim3(1), dim3(64), 0, s, bad, flag_count);
+    // the flags, and the scanned-entry counters after them (used by the
+    // trained path's scan)
+    hipLaunchKernelGGL(init_search_flags_zero, dim3(1), dim3(64), 0, s, bad, flag_count,
+                       (unsigned long long*)(flag_count + 2), IVF_SCAN_SLOTS);
     hipLaunchKernelGGL(flat_prep_queries, dim3((unsigned)nq), dim3(64), 0, s, d_raw, (int)dim, (int)ld, metric,
                        do_prepare ? 1 : 0, Qp, qb, qn, bad);
     PXG_HIP(hipGetLastError());
@@ -2448,9 +2451,7 @@ struct IvfPqIndex {
       uint64_t* ck = (uint64_t*)sc.get(8, (size_t)nq * produced * 8);
       int* probes = (int*)sc.get(9, (size_t)nq * np * 4);
       tm.mark(0);
-      scanned_dev = (unsigned long long*)(flag_count + 2);
-      hipLaunchKernelGGL(fill_u32, dim3(1), dim3(2 * IVF_SCAN_SLOTS), 0, s, (uint32_t*)scanned_dev,
-                         (size_t)(2 * IVF_SCAN_SLOTS), 0u);
+      scanned_dev = (unsigned long long*)(flag_count + 2);  // cleared by init_search_flags_zero
       const bool fused_count = np <= 64 && dim <= 2048;
       // entries per query (written by the fused pick), for the longest-first order
       uint32_t* qwork = fused_count && nq <= (uint64_t)LPT_MAXQ ? (uint32_t*)sc.get(16, nq * 4) : nullptr;
