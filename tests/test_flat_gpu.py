@@ -367,6 +367,30 @@ def test_merge_register_boundary(gpu, metric, n, nq):
     assert_same(idx.search_batch(q, 48, keep), oracle_search(px, data, ids, metric, q, 48, accept=acc))
 
 
+@pytest.mark.parametrize("n,nq", [(16384, 1000), (131072, 40)])
+def test_merge_register_no_or_one_candidate(gpu, n, nq):
+    """Filters that accept no row and exactly one row on the MFMA path: the
+    merges that hold a query's keys in registers (256 threads at 1000
+    queries over 16,384 rows, 1024 threads at 40 queries over 131,072 rows)
+    see zero or one usable key per query, and the seeding pass bounds
+    nothing. Counts 0 and 1, the one id and its exact distance match the
+    oracle."""
+    px = gpu
+    rng = np.random.default_rng(77 + n)
+    dim = 32
+    data = rng.standard_normal((n, dim)).astype(np.float32)
+    ids = rng.permutation(2 * n)[:n].astype(np.uint64)
+    idx = make_index(px, data, 0, ids, 1)
+    q = rng.standard_normal((nq, dim)).astype(np.float32)
+    none = idx.search_batch(q, 10, lambda i, _m: False)
+    assert_same(none, oracle_search(px, data, ids, 0, q, 10, accept=np.zeros(n, np.uint8)))
+    assert not none[2].any()
+    one_id = int(ids[n // 3])
+    got = idx.search_batch(q, 10, lambda i, _m: i == one_id)
+    assert_same(got, oracle_search(px, data, ids, 0, q, 10, accept=(ids == one_id).astype(np.uint8)))
+    assert (got[2] == 1).all() and (got[0][:, 0] == one_id).all()
+
+
 @pytest.mark.parametrize("metric", [0, 1])
 def test_seed_word_count_boundary(gpu, metric):
     """A store of 300 rows is one split of 3 tiles on the MFMA path. The
