@@ -769,10 +769,14 @@ __global__ __launch_bounds__(NT) void flat_merge_rescore_reg(
       if (x[u] != KEY_MAX) f(x[u]);
   };
   const uint64_t pivot = block_radix_select_each<64>(each, ksel, hist, sh);
-  // keys are distinct (one per row), so exactly ksel of them are <= pivot
+  // keys are distinct (one per row), so exactly ksel <= WAVE of them are
+  // <= pivot (the bound on the write only guards the array)
 #pragma unroll
   for (int u = 0; u < PER; ++u)
-    if (x[u] <= pivot && x[u] != KEY_MAX) sel[atomicAdd(&n_sel, 1)] = x[u];
+    if (x[u] <= pivot && x[u] != KEY_MAX) {
+      const int p = atomicAdd(&n_sel, 1);
+      if (p < WAVE) sel[p] = x[u];
+    }
   __syncthreads();
   // rescore: 8 threads per candidate
   const int g = threadIdx.x & 7, grp = threadIdx.x >> 3;
