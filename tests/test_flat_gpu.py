@@ -392,48 +392,28 @@ def test_merge_register_no_or_one_candidate(gpu, n, nq):
 
 
 @pytest.mark.parametrize("metric", [0, 1])
-def test_seed_word_count_boundary(gpu, metric):
-    """A store of 300 rows is one split of 3 tiles on the MFMA path. The
-    seeding pass bounds k' = k + 16 only from at least k' words, one tile's
-    128 here: k = 112 (k' = 128) is seeded, k = 113 and k = 200 take the
-    unseeded full pass, and a filter leaves some tiles partly usable."""
+@pytest.mark.parametrize("n,ks", [(300, (5, 112, 113, 200)), (1024, (240, 241, 250))])
+def test_seed_word_count_boundary(gpu, metric, n, ks):
+    """The seeding pass bounds k' = k + 16 only from at least k' words, one
+    tile's 128 per split. 300 rows are one split of 3 tiles on the MFMA
+    path: k = 112 (k' = 128) is seeded, k = 113 and 200 take the unseeded
+    full pass. 1024 rows are two splits of 4 tiles: k = 240 (k' = 256) is
+    seeded, k = 241 and 250 are not, and their rows append whole tiles and
+    compact them (512-key buffers). A filter leaves some tiles partly
+    usable."""
     px = gpu
-    rng = np.random.default_rng(313 + metric)
-    n, dim, nq = 300, 24, 50
+    rng = np.random.default_rng(313 + metric + n)
+    dim, nq = 24, 50
     data = rng.standard_normal((n, dim)).astype(np.float32)
     ids = rng.permutation(10 * n)[:n].astype(np.uint64)
     idx = make_index(px, data, metric, ids, 1)
     q = rng.standard_normal((nq, dim)).astype(np.float32)
-    for k in (5, 112, 113, 200):
+    for k in ks:
         assert_same(idx.search_batch(q, k), oracle_search(px, data, ids, metric, q, k))
     keep = lambda i, _m: i % 3 != 0  # noqa: E731
     acc = (ids % 3 != 0).astype(np.uint8)
-    for k in (112, 113):
+    for k in ks[1:3]:
         assert_same(idx.search_batch(q, k, keep), oracle_search(px, data, ids, metric, q, k, accept=acc))
-
-
-@pytest.mark.parametrize("metric", [0, 1, 2, 3])
-def test_exact_scan_query_groups(gpu, metric):
-    """The exact scan takes four queries per work item (rows loaded once for
-    the group, queries staged in LDS) for rows of 256 to 1024 floats, four
-    queries or more and at least 512 grouped items of 1024 rows: 300-float
-    rows (a 4-float tail after 37 chunks) over 131,149 rows (129 chunks, the
-    last partial), 13 and 18 queries (groups of 4 + 4 + 4 + 1 and
-    4 + 4 + 4 + 4 + 2), a filter, and 5 queries (one per item: too few
-    groups). Ids and distances match the oracle bit for bit."""
-    px = gpu
-    rng = np.random.default_rng(4242 + metric)
-    n, dim = 131_149, 300
-    data = rng.standard_normal((n, dim)).astype(np.float32)
-    ids = rng.permutation(3 * n)[:n].astype(np.uint64)
-    idx = make_index(px, data, metric, ids, 2)
-    q = rng.standard_normal((18, dim)).astype(np.float32)
-    for nq in (5, 13, 18):
-        assert_same(idx.search_batch(q[:nq], 10), oracle_search(px, data, ids, metric, q[:nq], 10, threads=16))
-    keep = lambda i, _m: i % 5 != 2  # noqa: E731
-    acc = (ids % 5 != 2).astype(np.uint8)
-    assert_same(idx.search_batch(q[:13], 25, keep),
-                oracle_search(px, data, ids, metric, q[:13], 25, accept=acc, threads=16))
 
 
 @pytest.mark.parametrize("metric", [0, 2])
