@@ -416,6 +416,22 @@ def test_seed_word_count_boundary(gpu, metric, n, ks):
         assert_same(idx.search_batch(q, k, keep), oracle_search(px, data, ids, metric, q, k, accept=acc))
 
 
+@pytest.mark.parametrize("n,dim,nqs", [(100_000, 128, (13, 14)), (300_000, 256, (5, 6)), (20_000, 128, (52, 53))])
+def test_default_mode_path_crossover(gpu, n, dim, nqs):
+    """The default mode picks the exact scan or the MFMA path by estimated
+    cost; batch sizes on either side of each store's crossover (100k x 128 at
+    13/14 queries, 300k x 256 at 5/6, 20k x 128 at 52/53) take different
+    paths and match the oracle bit for bit."""
+    px = gpu
+    rng = np.random.default_rng(n + dim)
+    data = rng.standard_normal((n, dim)).astype(np.float32)
+    ids = np.arange(n, dtype=np.uint64)
+    idx = make_index(px, data, 0, ids, 0)
+    q = rng.standard_normal((max(nqs), dim)).astype(np.float32)
+    for nq in nqs:
+        assert_same(idx.search_batch(q[:nq], 10), oracle_search(px, data, ids, 0, q[:nq], 10, threads=16))
+
+
 @pytest.mark.parametrize("metric", [0, 2])
 def test_thresholds_shared_across_splits(gpu, metric):
     """The MFMA path splits the store over many workgroups per query block,
