@@ -162,6 +162,27 @@ def test_untrained_index_is_exact(gpu):
         assert idx.search_all(q, 5) == flat.search_all(q, 5)
 
 
+@pytest.mark.parametrize("metric", [0, 1])
+def test_untrained_exact_scan_query_groups(gpu, metric):
+    """An untrained index searches by the exact scan (ivfpq.rs:1008-1012), the
+    flat index's kernel: 300-float rows over 131,149 rows (129 chunks of 1024,
+    the last partial) take four queries per work item at 13 and 18 queries
+    and one per item at 5. Ids and distances match the oracle's flat search
+    bit for bit."""
+    px = gpu
+    rng = np.random.default_rng(1301 + metric)
+    n, dim = 131_149, 300
+    data = rng.standard_normal((n, dim)).astype(np.float32)
+    idx = build(px, data, px.IvfPqConfig(64, 4).with_train_threshold(1 << 62), metric)
+    assert not idx.is_trained()
+    q = rng.standard_normal((18, dim)).astype(np.float32)
+    ids = np.arange(n, dtype=np.uint64)
+    pd = orc.prepare_rows(metric, data)
+    for nq in (5, 13, 18):
+        want = orc.flat_search(pd, ids, metric, orc.prepare_rows(metric, q[:nq]), 10, threads=16)
+        assert_same(idx.search_batch(q[:nq], 10), want)
+
+
 def test_training_populates_lists_and_auto_training(gpu):
     px = gpu
     idx = build(px, corpus(1000, 16, 24), px.IvfPqConfig(16, 8).with_seed(3).with_train_threshold(1 << 62))
