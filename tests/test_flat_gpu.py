@@ -432,6 +432,22 @@ def test_default_mode_path_crossover(gpu, n, dim, nqs):
         assert_same(idx.search_batch(q[:nq], 10), oracle_search(px, data, ids, 0, q[:nq], 10, threads=16))
 
 
+def test_search_mode_range(gpu):
+    """Search modes are 0 (automatic), 1 (MFMA path) and 2 (exact scan);
+    others are refused as a configuration error naming the parameter, and
+    the index keeps its mode."""
+    px = gpu
+    rng = np.random.default_rng(5)
+    data = rng.standard_normal((5000, 16)).astype(np.float32)
+    idx = make_index(px, data, 0, mode=1)
+    for bad in (3, -1):
+        with pytest.raises(px.ProximaError) as e:
+            idx.set_search_mode(bad)
+        assert "mode" in str(e.value)
+    q = rng.standard_normal((40, 16)).astype(np.float32)
+    assert_same(idx.search_batch(q, 7), oracle_search(px, data, np.arange(5000, dtype=np.uint64), 0, q, 7))
+
+
 @pytest.mark.parametrize("metric", [0, 2])
 def test_thresholds_shared_across_splits(gpu, metric):
     """The MFMA path splits the store over many workgroups per query block,
